@@ -1,0 +1,203 @@
+"""Benchmark of the hot path: na2d forward+backward, DiNAT scale
+(B=16, 56x56, 4 heads, head dim 32, kernel 7, bf16), on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--dilation 1] [--no-cpu]
+
+A step is one forward + backward pass through the public API
+(``natten_mps_amd.na2d`` then ``torch.autograd.grad``) on synthetic seeded
+inputs already resident in HBM.  Prints one JSON line (rank 0):
+
+* value / unit: effective TFLOP/s = (fwd 4*P*D + bwd 10*P*D) / step time,
+  with P = B * Hq * (valid query-key pairs of the neighbourhood map);
+* roofline: for the kernel with the largest share of GPU time, its
+  algorithmic HBM bytes per launch / its mean launch time (HIP events
+  bracketing each launch on its stream, recorded during the timed steps),
+  against 8 TB/s;
+* cpu_baseline: the CPU oracle (the reference's pure algorithm) timed on the
+  host for a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "natten-mps_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "na2d fwd+bwd ms & effective TFLOP/s (56×56,K=7,bf16); % of roofline"
+
+CFG = dict(B=16, H=56, W=56, heads=4, dim=32, kernel=7)
+
+
+def _log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _valid_pairs(spatial, kernel, dilation, stride, causal, device):
+    from natten_mps_amd._core import hip
+
+    _, valid = hip.neighborhood_map(len(spatial), spatial, kernel, dilation, stride, causal, device)
+    return int(valid.sum().item())
+
+
+def kernel_bytes(name, B, N, Hq, Hkv, D, esz):
+    """Algorithmic HBM bytes of one launch (compulsory traffic: every operand
+    read once, every result written once; K/V at Hkv heads; fp32 LSE/delta)."""
+    tq, tkv, lse = B * N * Hq * D * esz, B * N * Hkv * D * esz, B * N * Hq * 4
+    return {
+        "na_forward": tq + 2 * tkv + tq + lse,                 # q, k, v -> out, lse
+        "na_bwd_dq": tq + 2 * tkv + 2 * tq + lse + tq + lse,   # q, k, v, out, dout, lse -> dq, delta
+        "na_bwd_dkdv": tq + 2 * tkv + tq + 2 * lse + 2 * tkv,  # q, k, v, dout, lse, delta -> dk, dv
+    }.get(name)
+
+
+def cpu_baseline(dilation, budget_s=20.0):
+    """The oracle (reference pure algorithm, torch on the host CPU) on a
+    bounded sample: the same problem at batch 1 (1/16 of the workload), bf16,
+    forward + backward, median of the timed repeats."""
+    import torch
+
+    import oracle.pure as P
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(1003)
+    shape = (1, CFG["H"], CFG["W"], CFG["heads"], CFG["dim"])
+    q, k, v, do = (torch.randn(shape, generator=g).to(torch.bfloat16) for _ in range(4))
+    ks, dil = (CFG["kernel"],) * 2, (dilation,) * 2
+
+    def step():
+        leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
+        out = P.na2d_forward(*leaves, ks, (1, 1), dil, (False, False), None)
+        torch.autograd.grad(out, leaves, do)
+
+    step()
+    times, t_end = [], time.perf_counter() + budget_s
+    while time.perf_counter() < t_end and len(times) < 20:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    pairs = CFG["H"] * CFG["W"] * CFG["kernel"] ** 2 * CFG["heads"]  # non-causal: windows always full
+    flops = 14.0 * pairs * CFG["dim"]
+    med = statistics.median(times)
+    return {
+        "value": flops / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"na2d bf16 fwd+bwd at batch 1 of 16 (1/16 of the workload), oracle/pure.py on the host CPU, "
+                  f"median of {len(times)} runs = {med * 1e3:.1f} ms (x16 = {med * 16e3:.0f} ms per full step); "
+                  f"os.cpu_count()={os.cpu_count()}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--dilation", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "neighbourhood attention shards over batch x heads with no communication, "
+              "so the N-GPU figure is N x the 1-GPU value.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import natten_mps_amd
+    from natten_mps_amd import functional as F
+    from natten_mps_amd._core import _lib
+
+    natten_mps_amd.set_backend("hip")
+    dev = torch.device("cuda:0")
+    B, H, W, Hq, D, K = CFG["B"], CFG["H"], CFG["W"], CFG["heads"], CFG["dim"], CFG["kernel"]
+    dil = args.dilation
+    g = torch.Generator().manual_seed(1003)
+    q, k, v, do = (torch.randn((B, H, W, Hq, D), generator=g).to(torch.bfloat16).to(dev) for _ in range(4))
+    q.requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+
+    def step():
+        out = F.na2d(q, k, v, kernel_size=K, dilation=dil)
+        return torch.autograd.grad(out, (q, k, v), do)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_read(reset=True)
+
+    _lib.profile_enable(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    ms = start.elapsed_time(stop) / args.steps
+    stats = _lib.profile_read(reset=True)
+
+    pairs = B * Hq * _valid_pairs((H, W), (K, K), (dil, dil), (1, 1), (False, False), dev)
+    flops = 14.0 * pairs * D
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    gpu_total = sum(s[1] for s in stats.values())
+    for name, (n, tot, mn, mx) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
+        _log(f"  {name:14s} launches={n:4d} mean={tot / n * 1e3:8.1f} us  min={mn * 1e3:8.1f}  max={mx * 1e3:8.1f}"
+             f"  share={tot / gpu_total:5.1%}")
+    dom = max(stats.items(), key=lambda kv: kv[1][1])
+    dom_name, (dn, dtot, _, _) = dom
+    nbytes = kernel_bytes(dom_name, B, H * W, Hq, Hq, D, 2)
+    mean_s = dtot / dn * 1e-3
+    roof = None
+    if nbytes is not None:
+        gbs = nbytes / mean_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom_name,
+                "mean_us": round(mean_s * 1e6, 2), "alg_bytes": nbytes}
+    fwd_bwd_bytes = (4 * B * H * W * Hq * D * 2 + B * H * W * Hq * 4) + (8 * B * H * W * Hq * D * 2 + 2 * B * H * W * Hq * 4)
+    _log(f"step {ms:.3f} ms  {tflops:.2f} TFLOP/s  fwd+bwd HBM floor {fwd_bwd_bytes / 8e12 * 1e6:.1f} us "
+         f"-> {fwd_bwd_bytes / 8e12 / (ms * 1e-3):.1%} of roofline (step)")
+
+    cpu = None
+    if not args.no_cpu:
+        try:
+            cpu = cpu_baseline(dil)
+        except Exception as e:  # the baseline is reported, never required
+            _log("cpu baseline failed:", repr(e))
+
+    print(json.dumps({
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded randn, resident in HBM)",
+        "config": {"workload": f"na2d fwd+bwd B=16 56x56 heads=4 dim=32 K=7 dilation={dil} bf16 (BASELINE config 3)",
+                   "global_batch": B, "seq_len": H * W, "parallelism": "single GPU",
+                   "hbm_floor_frac_step": round(fwd_bwd_bytes / 8e12 / (ms * 1e-3), 4)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }), flush=True)
+
+
+if __name__ == "__main__":
+    main()

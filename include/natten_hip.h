@@ -1,0 +1,178 @@
+/*
+ * natten_hip.h -- C ABI of the MI355X (gfx950) neighbourhood-attention library
+ * (libnatten_hip.so).
+ *
+ * Plain pointers, sizes and element strides; no torch types.  The caller owns
+ * every buffer (inputs, outputs, workspaces) and the stream; no entry point
+ * allocates device memory.  Every entry point returns 0 on success and a
+ * non-zero natten_status_t otherwise, with a message available from
+ * natten_hip_last_error().  Launches are asynchronous on `stream` (a
+ * hipStream_t; NULL = the default stream).
+ *
+ * Tensor conventions (spatial-first, as the reference's public API):
+ *   q      [B, *sp,     Hq,  Dqk]      k  [B, *sp, Hkv, Dqk]    v [B, *sp, Hkv, Dv]
+ *   out    [B, *sp_out, Hq,  Dv]       lse / delta [B, *sp_out, Hq]  (fp32)
+ *   attn   [B, *sp_out, H,   KV]       KV = prod(kernel), row-major over the axes
+ * `*sp` always has three axes here, outermost first: a rank-r problem pads the
+ * leading 3-r axes with length 1, kernel 1, dilation 1, stride 1, non-causal.
+ * Each tensor is described by a natten_layout_t of element strides; the
+ * innermost dimension (D, or KV for attn, or nothing for lse) must be
+ * contiguous.
+ *
+ * Reference interfaces these entry points replace (paths under
+ * /root/reference/src/natten_mps):
+ *   natten_hip_forward         _core/metal.py:452-558  na{1,2,3}d_fused_forward
+ *                              (and the forward_with_lse hooks :592-621,
+ *                              :845-874, :1051-1080)
+ *   natten_hip_qk_forward      _core/metal.py:181-224, 273-338, 882-949  na{r}d_qk_forward
+ *   natten_hip_av_forward      _core/metal.py:227-265, 341-401, 952-1012 na{r}d_av_forward
+ *   natten_hip_backward        _core/metal.py:1088-1330 na{r}d_fused_backward
+ *   natten_hip_qk_backward     _core/metal.py:1352-1470 (q/k backward kernels)
+ *   natten_hip_av_backward     _core/metal.py:1473-1611 (a/v backward kernels)
+ *   natten_hip_neighborhood_map _core/pure.py:91-129, 335-387 (index maps; the
+ *                              Metal backend has no equivalent export)
+ */
+#ifndef NATTEN_HIP_H
+#define NATTEN_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NATTEN_HIP_ABI_VERSION 1
+
+typedef enum {
+    NATTEN_OK = 0,
+    NATTEN_ERR_INVALID = 1,     /* bad shape / parameter / alignment */
+    NATTEN_ERR_UNSUPPORTED = 2, /* valid input outside what the kernels cover */
+    NATTEN_ERR_LAUNCH = 3       /* HIP launch error */
+} natten_status_t;
+
+typedef enum { NATTEN_F32 = 0, NATTEN_F16 = 1, NATTEN_BF16 = 2 } natten_dtype_t;
+
+typedef struct {
+    int32_t batch;
+    int32_t heads_q;       /* query heads (= heads of attn/out)                  */
+    int32_t heads_kv;      /* key/value heads; heads_q % heads_kv == 0 (GQA)     */
+    int32_t dim_qk;        /* head dim of q and k                                */
+    int32_t dim_v;         /* head dim of v and out                              */
+    int32_t dtype;         /* natten_dtype_t of q, k, v, out, attn and gradients */
+    int32_t has_scale;     /* split QK / its backward: 0 = logits left unscaled  */
+    float scale;           /* softmax scale (fused ops), logit scale (split QK)  */
+    int32_t length[3];     /* key/value spatial extent per axis                  */
+    int32_t out_length[3]; /* query positions per axis (ceil(len/stride), or the
+                              attn extent for the split ops at stride 1)         */
+    int32_t kernel[3];
+    int32_t dilation[3];
+    int32_t stride[3];
+    int32_t causal[3];
+} natten_problem_t;
+
+typedef struct {
+    int64_t batch;
+    int64_t axis[3];
+    int64_t head;
+} natten_layout_t;
+
+/* Library / ABI introspection. */
+int natten_hip_abi_version(void);
+const char *natten_hip_last_error(void);
+
+/* Fused forward: out = softmax(scale * q k^T over each neighbourhood) v, and
+ * lse = log-sum-exp of the scaled logits (natural log).  Native GQA: query
+ * head h reads key/value head h / (Hq/Hkv). */
+int natten_hip_forward(const natten_problem_t *p,
+                       const void *q, const natten_layout_t *lq,
+                       const void *k, const natten_layout_t *lk,
+                       const void *v, const natten_layout_t *lv,
+                       void *out, const natten_layout_t *lo,
+                       float *lse, const natten_layout_t *llse,
+                       void *stream);
+
+/* Fused backward.  Inputs: q, k, v, the forward's out and lse, dout, and an
+ * optional upstream gradient of lse (dlse, NULL if none).  Outputs: dq (zeroed
+ * by the caller at off-stride positions when any stride > 1), dk, dv, at the
+ * shapes of q, k, v (dk/dv summed over each GQA group).  delta is an fp32
+ * workspace shaped like lse. */
+int natten_hip_backward(const natten_problem_t *p,
+                        const void *q, const natten_layout_t *lq,
+                        const void *k, const natten_layout_t *lk,
+                        const void *v, const natten_layout_t *lv,
+                        const void *out, const natten_layout_t *lo,
+                        const void *dout, const natten_layout_t *ldo,
+                        const float *lse, const natten_layout_t *llse,
+                        const float *dlse, const natten_layout_t *ldlse,
+                        void *dq, const natten_layout_t *ldq,
+                        void *dk, const natten_layout_t *ldk,
+                        void *dv, const natten_layout_t *ldv,
+                        float *delta, const natten_layout_t *ldelta,
+                        void *stream);
+
+/* Split QK: attn[.., kv] = q . k_neighbour (times scale if has_scale); entries
+ * of causally invalid neighbours are -inf (times scale).  heads_q == heads_kv. */
+int natten_hip_qk_forward(const natten_problem_t *p,
+                          const void *q, const natten_layout_t *lq,
+                          const void *k, const natten_layout_t *lk,
+                          void *attn, const natten_layout_t *la,
+                          void *stream);
+
+/* Split AV: out = sum over valid neighbours of attn * v_neighbour. */
+int natten_hip_av_forward(const natten_problem_t *p,
+                          const void *attn, const natten_layout_t *la,
+                          const void *v, const natten_layout_t *lv,
+                          void *out, const natten_layout_t *lo,
+                          void *stream);
+
+/* Split QK backward: dq = sum dattn * k, dk = sum dattn * q over valid pairs,
+ * each times scale when has_scale.  dq must be zeroed by the caller at
+ * off-stride positions when any stride > 1. */
+int natten_hip_qk_backward(const natten_problem_t *p,
+                           const void *dattn, const natten_layout_t *lda,
+                           const void *q, const natten_layout_t *lq,
+                           const void *k, const natten_layout_t *lk,
+                           void *dq, const natten_layout_t *ldq,
+                           void *dk, const natten_layout_t *ldk,
+                           void *stream);
+
+/* Split AV backward: dattn = dout . v_neighbour (0 for invalid neighbours),
+ * dv = sum attn * dout over valid pairs. */
+int natten_hip_av_backward(const natten_problem_t *p,
+                           const void *dout, const natten_layout_t *ldo,
+                           const void *attn, const natten_layout_t *la,
+                           const void *v, const natten_layout_t *lv,
+                           void *dattn, const natten_layout_t *lda,
+                           void *dv, const natten_layout_t *ldv,
+                           void *stream);
+
+/* The flattened neighbour index map of the fused op, computed on the device:
+ * flat[o, kv] (int64, row-major over the padded three axes, causal indices
+ * clamped to the axis) and valid[o, kv] (uint8), o over all query positions.
+ * Same values as the reference's _build_2d/_build_3d_neighborhood. */
+int natten_hip_neighborhood_map(const natten_problem_t *p,
+                                int64_t *flat, uint8_t *valid,
+                                void *stream);
+
+/* Per-kernel timing (no counterpart in the reference; for benchmarks and
+ * profiling).  While enabled, every kernel launch of the library is bracketed
+ * by two HIP events on its stream.  natten_hip_profile_read waits for the
+ * recorded events, folds them into per-kernel totals, copies up to
+ * max_entries of them to `out` (may be NULL) and returns the number of
+ * kernels seen; reset != 0 clears the totals afterwards. */
+typedef struct {
+    char name[64];
+    int64_t launches;
+    double total_ms;
+    double min_ms;
+    double max_ms;
+} natten_kernel_stat_t;
+
+int natten_hip_profile_enable(int on);
+int natten_hip_profile_read(natten_kernel_stat_t *out, int max_entries, int reset);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NATTEN_HIP_H */

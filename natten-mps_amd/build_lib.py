@@ -1,0 +1,81 @@
+"""Build libnatten_hip.so (gfx950) in-tree with hipcc.
+
+    python natten-mps_amd/build_lib.py            # build
+    python natten-mps_amd/build_lib.py --check    # print the commands only
+
+Objects go to natten-mps_amd/_build/, the library to
+natten-mps_amd/natten_mps_amd/libnatten_hip.so (git-ignored; it travels to
+the GPU box with the working tree).
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+OBJ = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "natten_mps_amd", "libnatten_hip.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+SOURCES = ["na_generic.hip", "na_mfma.hip", "na_profile.hip", "na_capi.hip"]
+
+FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # keep hipcc from forming packed-fp32 (v_pk_*_f32) instructions
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+    "-I" + os.path.join(ROOT, "include"),
+    "-I" + CSRC,
+]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    return r
+
+
+def commands():
+    objs, cmds = [], []
+    for src in SOURCES:
+        path = os.path.join(CSRC, src)
+        if not os.path.exists(path):
+            continue
+        obj = os.path.join(OBJ, src.replace(".hip", ".o"))
+        objs.append(obj)
+        cmds.append([HIPCC, *FLAGS, "-c", path, "-o", obj])
+    link = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", LIB]
+    return cmds, link
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(OBJ, exist_ok=True)
+    cmds, link = commands()
+    with cf.ThreadPoolExecutor(max_workers=min(len(cmds), 8)) as ex:
+        for cmd, _ in zip(cmds, ex.map(_run, cmds)):
+            if verbose:
+                print(" ".join(cmd))
+    tmp = LIB + ".tmp"
+    link = link[:-1] + [tmp]
+    _run(link)
+    os.replace(tmp, LIB)
+    if verbose:
+        print(" ".join(link[:-1] + [LIB]))
+    return LIB
+
+
+if __name__ == "__main__":
+    if "--check" in sys.argv:
+        c, l = commands()
+        for x in c + [l]:
+            print(" ".join(x))
+    else:
+        print(build(verbose=True))

@@ -1,0 +1,235 @@
+// C ABI of libnatten_hip.so (declared in include/natten_hip.h): argument
+// validation, problem set-up and kernel selection.  No entry point allocates.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "na_launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int launch_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return NATTEN_OK;
+    return fail(NATTEN_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+}
+
+na::Lay to_lay(const natten_layout_t* l) {
+    na::Lay r{};
+    if (l) {
+        r.b = l->batch;
+        r.s0 = l->axis[0];
+        r.s1 = l->axis[1];
+        r.s2 = l->axis[2];
+        r.h = l->head;
+    }
+    return r;
+}
+
+int elem_size(int dtype) { return dtype == NATTEN_F32 ? 4 : 2; }
+
+// Validates the problem and fills the kernel-side descriptor.  `fused` ops use
+// out = ceil(len/stride); split ops may use a shorter query extent at stride 1.
+int make_prob(const natten_problem_t* p, bool fused, na::Prob& P) {
+    if (!p) return fail(NATTEN_ERR_INVALID, "problem is NULL");
+    if (p->dtype < NATTEN_F32 || p->dtype > NATTEN_BF16) return fail(NATTEN_ERR_INVALID, "bad dtype %d", p->dtype);
+    if (p->batch < 1 || p->heads_q < 1 || p->heads_kv < 1)
+        return fail(NATTEN_ERR_INVALID, "batch and heads must be >= 1");
+    if (p->heads_q % p->heads_kv != 0)
+        return fail(NATTEN_ERR_INVALID, "heads_q (%d) must be divisible by heads_kv (%d)", p->heads_q, p->heads_kv);
+    if (p->dim_qk < 1 || p->dim_v < 1) return fail(NATTEN_ERR_INVALID, "head dims must be >= 1");
+    if (p->dim_qk > 256 || p->dim_v > 256)
+        return fail(NATTEN_ERR_UNSUPPORTED, "head dims above 256 are not supported (got %d, %d)", p->dim_qk,
+                    p->dim_v);
+    P.B = p->batch;
+    P.Hq = p->heads_q;
+    P.Hkv = p->heads_kv;
+    P.rep = p->heads_q / p->heads_kv;
+    P.Dqk = p->dim_qk;
+    P.Dv = p->dim_v;
+    P.has_scale = p->has_scale ? 1 : 0;
+    P.scale = p->scale;
+    P.kv = 1;
+    P.nout = 1;
+    P.nkey = 1;
+    for (int a = 0; a < 3; ++a) {
+        na::Axis& A = P.ax[a];
+        A.len = p->length[a];
+        A.out = p->out_length[a];
+        A.k = p->kernel[a];
+        A.dil = p->dilation[a];
+        A.st = p->stride[a];
+        A.causal = p->causal[a] ? 1 : 0;
+        if (A.len < 1 || A.k < 1 || A.dil < 1 || A.st < 1)
+            return fail(NATTEN_ERR_INVALID, "axis %d: length, kernel, dilation and stride must be >= 1", a);
+        if (static_cast<long long>(A.k) * A.dil > A.len)
+            return fail(NATTEN_ERR_INVALID, "axis %d: dilation*kernel (%d*%d) exceeds length %d", a, A.dil, A.k,
+                        A.len);
+        const int full = (A.len + A.st - 1) / A.st;
+        if (fused ? (A.out != full) : (A.out < 1 || A.out > full || (A.st != 1 && A.out != full)))
+            return fail(NATTEN_ERR_INVALID, "axis %d: query extent %d does not match length %d / stride %d", a,
+                        A.out, A.len, A.st);
+        // The reference rule places the window at -1 only in this case (even
+        // kernel equal to the axis, no dilation, non-causal); no defined result.
+        if (!A.causal && A.dil == 1 && (A.k % 2) == 0 && A.k == A.len)
+            return fail(NATTEN_ERR_UNSUPPORTED,
+                        "axis %d: an even kernel (%d) equal to the axis length is not supported", a, A.k);
+        P.kv *= A.k;
+        P.nout *= A.out;
+        P.nkey *= A.len;
+    }
+    return NATTEN_OK;
+}
+
+// Dims per lane used by the generic kernels for head dim D.
+int dpl_for(int D) { return D <= 128 ? 8 : 16; }
+
+struct Run {
+    const void* ptr;
+    const natten_layout_t* lay;
+    int D;
+};
+
+// True when every operand can be read in aligned runs of `dpl` elements:
+// 16-byte aligned base, its head dim and every stride a multiple of dpl.
+bool runs_aligned(int dpl, std::initializer_list<Run> ts) {
+    for (auto& t : ts) {
+        if (!t.ptr) continue;
+        if (t.D % dpl) return false;
+        if (reinterpret_cast<uintptr_t>(t.ptr) % 16) return false;
+        const natten_layout_t* l = t.lay;
+        if (!l) return false;
+        if (l->batch % dpl || l->axis[0] % dpl || l->axis[1] % dpl || l->axis[2] % dpl || l->head % dpl) return false;
+    }
+    return true;
+}
+
+bool any_null(std::initializer_list<const void*> ps) {
+    for (auto p : ps)
+        if (!p) return true;
+    return false;
+}
+
+}  // namespace
+
+extern "C" {
+
+int natten_hip_abi_version(void) { return NATTEN_HIP_ABI_VERSION; }
+
+const char* natten_hip_last_error(void) { return g_err; }
+
+int natten_hip_forward(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
+                       const natten_layout_t* lk, const void* v, const natten_layout_t* lv, void* out,
+                       const natten_layout_t* lo, float* lse, const natten_layout_t* llse, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, true, P);
+    if (rc) return rc;
+    if (any_null({q, k, v, out, lse, lq, lk, lv, lo, llse})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    const int D = P.Dqk > P.Dv ? P.Dqk : P.Dv;
+    const int vec =
+        runs_aligned(dpl_for(D), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {v, lv, P.Dv}, {out, lo, P.Dv}}) ? 1 : 0;
+    return launch_status(na::generic_forward(P, vec, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo),
+                                             lse, to_lay(llse), p->dtype, static_cast<hipStream_t>(stream)),
+                         "forward");
+}
+
+int natten_hip_backward(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
+                        const natten_layout_t* lk, const void* v, const natten_layout_t* lv, const void* out,
+                        const natten_layout_t* lo, const void* dout, const natten_layout_t* ldo, const float* lse,
+                        const natten_layout_t* llse, const float* dlse, const natten_layout_t* ldlse, void* dq,
+                        const natten_layout_t* ldq, void* dk, const natten_layout_t* ldk, void* dv,
+                        const natten_layout_t* ldv, float* delta, const natten_layout_t* ldelta, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, true, P);
+    if (rc) return rc;
+    if (any_null({q, k, v, out, dout, lse, dq, dk, dv, delta, lq, lk, lv, lo, ldo, llse, ldq, ldk, ldv, ldelta}))
+        return fail(NATTEN_ERR_INVALID, "NULL operand");
+    if (dlse && !ldlse) return fail(NATTEN_ERR_INVALID, "dlse given without a layout");
+    const int D = P.Dqk > P.Dv ? P.Dqk : P.Dv;
+    const int vec = runs_aligned(dpl_for(D), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {v, lv, P.Dv}, {out, lo, P.Dv},
+                                              {dout, ldo, P.Dv}, {dq, ldq, P.Dqk}, {dk, ldk, P.Dqk}, {dv, ldv, P.Dv}})
+                        ? 1
+                        : 0;
+    return launch_status(
+        na::generic_backward(P, vec, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout, to_lay(ldo),
+                             lse, to_lay(llse), dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv,
+                             to_lay(ldv), delta, to_lay(ldelta), p->dtype, static_cast<hipStream_t>(stream)),
+        "backward");
+}
+
+int natten_hip_qk_forward(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
+                          const natten_layout_t* lk, void* attn, const natten_layout_t* la, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, false, P);
+    if (rc) return rc;
+    if (P.rep != 1) return fail(NATTEN_ERR_INVALID, "split QK needs heads_q == heads_kv");
+    if (any_null({q, k, attn, lq, lk, la})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    const int vec = runs_aligned(dpl_for(P.Dqk), {{q, lq, P.Dqk}, {k, lk, P.Dqk}}) ? 1 : 0;
+    return launch_status(na::generic_qk(P, vec, q, to_lay(lq), k, to_lay(lk), attn, to_lay(la), p->dtype,
+                                        static_cast<hipStream_t>(stream)),
+                         "qk_forward");
+}
+
+int natten_hip_av_forward(const natten_problem_t* p, const void* attn, const natten_layout_t* la, const void* v,
+                          const natten_layout_t* lv, void* out, const natten_layout_t* lo, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, false, P);
+    if (rc) return rc;
+    if (P.rep != 1) return fail(NATTEN_ERR_INVALID, "split AV needs heads_q == heads_kv");
+    if (any_null({attn, v, out, la, lv, lo})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    const int vec = runs_aligned(dpl_for(P.Dv), {{v, lv, P.Dv}, {out, lo, P.Dv}}) ? 1 : 0;
+    return launch_status(na::generic_av(P, vec, attn, to_lay(la), v, to_lay(lv), out, to_lay(lo), p->dtype,
+                                        static_cast<hipStream_t>(stream)),
+                         "av_forward");
+}
+
+int natten_hip_qk_backward(const natten_problem_t* p, const void* dattn, const natten_layout_t* lda, const void* q,
+                           const natten_layout_t* lq, const void* k, const natten_layout_t* lk, void* dq,
+                           const natten_layout_t* ldq, void* dk, const natten_layout_t* ldk, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, false, P);
+    if (rc) return rc;
+    if (P.rep != 1) return fail(NATTEN_ERR_INVALID, "split QK needs heads_q == heads_kv");
+    if (any_null({dattn, q, k, dq, dk, lda, lq, lk, ldq, ldk})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    const int vec =
+        runs_aligned(dpl_for(P.Dqk), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {dq, ldq, P.Dqk}, {dk, ldk, P.Dqk}}) ? 1 : 0;
+    return launch_status(na::generic_qk_backward(P, vec, dattn, to_lay(lda), q, to_lay(lq), k, to_lay(lk), dq,
+                                                 to_lay(ldq), dk, to_lay(ldk), p->dtype,
+                                                 static_cast<hipStream_t>(stream)),
+                         "qk_backward");
+}
+
+int natten_hip_av_backward(const natten_problem_t* p, const void* dout, const natten_layout_t* ldo,
+                           const void* attn, const natten_layout_t* la, const void* v, const natten_layout_t* lv,
+                           void* dattn, const natten_layout_t* lda, void* dv, const natten_layout_t* ldv,
+                           void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, false, P);
+    if (rc) return rc;
+    if (P.rep != 1) return fail(NATTEN_ERR_INVALID, "split AV needs heads_q == heads_kv");
+    if (any_null({dout, attn, v, dattn, dv, ldo, la, lv, lda, ldv})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    const int vec = runs_aligned(dpl_for(P.Dv), {{dout, ldo, P.Dv}, {v, lv, P.Dv}, {dv, ldv, P.Dv}}) ? 1 : 0;
+    return launch_status(na::generic_av_backward(P, vec, dout, to_lay(ldo), attn, to_lay(la), v, to_lay(lv), dattn,
+                                                 to_lay(lda), dv, to_lay(ldv), p->dtype,
+                                                 static_cast<hipStream_t>(stream)),
+                         "av_backward");
+}
+
+int natten_hip_neighborhood_map(const natten_problem_t* p, int64_t* flat, uint8_t* valid, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, true, P);
+    if (rc) return rc;
+    if (any_null({flat, valid})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    return launch_status(na::neighborhood_map(P, flat, valid, static_cast<hipStream_t>(stream)), "neighborhood_map");
+}
+
+}  // extern "C"

@@ -1,0 +1,243 @@
+// Shared device-side definitions for the neighbourhood-attention kernels:
+// problem descriptors, the window rule, element conversion and vector I/O.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "natten_hip.h"
+
+namespace na {
+
+// ---------------------------------------------------------------------------
+// Problem description passed by value to every kernel.
+// ---------------------------------------------------------------------------
+
+struct Axis {
+    int len;     // key/value extent
+    int out;     // number of query positions
+    int k;       // kernel size
+    int dil;     // dilation
+    int st;      // stride
+    int causal;  // 0 / 1
+};
+
+struct Prob {
+    int B, Hq, Hkv, rep;   // rep = Hq / Hkv
+    int Dqk, Dv;
+    int has_scale;
+    float scale;
+    Axis ax[3];
+    int kv;                // K0*K1*K2
+    int nout;              // out0*out1*out2
+    int nkey;              // len0*len1*len2
+};
+
+struct Lay {
+    long long b, s0, s1, s2, h;
+    __host__ __device__ long long at(int bb, int p0, int p1, int p2, int hh) const {
+        return bb * b + p0 * s0 + p1 * s1 + p2 * s2 + hh * h;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Window rule.  Non-causal start of the window of query position i on an axis
+// of length L, kernel K, dilation d (utils/window.py:91-111 of the
+// reference): centred, shifted inwards at the borders, and for d > 1 kept on
+// the residue class of i.  Causal windows start at i-(K-1)d and are clipped
+// by validity (j >= 0) rather than shifted.
+// ---------------------------------------------------------------------------
+
+__host__ __device__ inline int window_start(int i, int L, int K, int d) {
+    const int half = K / 2;
+    if (d <= 1) {
+        int s = i - half;
+        if (s < 0) s = 0;
+        if (i + half >= L) s += L - i - half - 1;
+        return s;
+    }
+    if (i - half * d < 0) return i % d;
+    if (i + half * d >= L) {
+        const int r = i % d;
+        const int full = (L / d) * d;
+        const int tail = L - full;
+        return (r < tail) ? (L - tail + r - 2 * half * d) : (full + r - K * d);
+    }
+    return i - half * d;
+}
+
+__host__ __device__ inline int axis_first(const Axis& a, int i) {
+    return a.causal ? i - (a.k - 1) * a.dil : window_start(i, a.len, a.k, a.dil);
+}
+
+// Range [t_lo, t_hi] of offsets t such that query position i = m + t*dil has
+// key position m inside its window (and is inside the axis).  Window starts
+// are non-decreasing along a residue class, so the set is contiguous in t.
+// Returns false when empty.  The caller still filters by stride and out.
+// A non-causal window lies within K*dil of its query (an even kernel at the
+// right border does not contain the query itself), hence t in [-K, K].
+__host__ __device__ inline bool axis_query_range(const Axis& a, int m, int& t_lo, int& t_hi) {
+    int lo = a.causal ? 0 : -a.k;
+    int hi = a.causal ? a.k - 1 : a.k;
+    // clip to 0 <= m + t*dil < len
+    while (lo <= hi && m + lo * a.dil < 0) ++lo;
+    while (hi >= lo && m + hi * a.dil >= a.len) --hi;
+    if (a.causal) { t_lo = lo; t_hi = hi; return lo <= hi; }
+    while (lo <= hi) {
+        const int i = m + lo * a.dil;
+        const int f = window_start(i, a.len, a.k, a.dil);
+        if (m <= f + (a.k - 1) * a.dil) break;  // m >= f holds on this side
+        ++lo;
+    }
+    while (hi >= lo) {
+        const int i = m + hi * a.dil;
+        const int f = window_start(i, a.len, a.k, a.dil);
+        if (m >= f) break;
+        --hi;
+    }
+    t_lo = lo; t_hi = hi;
+    return lo <= hi;
+}
+
+// f(j0, j1, j2, e, valid) for each neighbour e (row-major over the kernel) of
+// the query at (i0, i1, i2).  Invalid (causal) neighbours have j < 0 on some
+// axis and must not be dereferenced.
+template <class F>
+__host__ __device__ inline void for_each_neighbor(const Prob& p, int i0, int i1, int i2, F&& f) {
+    const Axis &A0 = p.ax[0], &A1 = p.ax[1], &A2 = p.ax[2];
+    const int f0 = axis_first(A0, i0), f1 = axis_first(A1, i1), f2 = axis_first(A2, i2);
+    int e = 0;
+    for (int x = 0; x < A0.k; ++x) {
+        const int j0 = f0 + x * A0.dil;
+        for (int y = 0; y < A1.k; ++y) {
+            const int j1 = f1 + y * A1.dil;
+            for (int z = 0; z < A2.k; ++z, ++e) {
+                const int j2 = f2 + z * A2.dil;
+                f(j0, j1, j2, e, (j0 >= 0) & (j1 >= 0) & (j2 >= 0));
+            }
+        }
+    }
+}
+
+// f(o0, o1, o2, i0, i1, i2, e) for every query (output index o, position i)
+// whose window holds the key at (m0, m1, m2) as neighbour e (valid pairs only).
+template <class F>
+__host__ __device__ inline void for_each_query(const Prob& p, int m0, int m1, int m2, F&& f) {
+    const Axis &A0 = p.ax[0], &A1 = p.ax[1], &A2 = p.ax[2];
+    int l0, h0, l1, h1, l2, h2;
+    if (!axis_query_range(A0, m0, l0, h0)) return;
+    if (!axis_query_range(A1, m1, l1, h1)) return;
+    if (!axis_query_range(A2, m2, l2, h2)) return;
+    for (int t0 = l0; t0 <= h0; ++t0) {
+        const int i0 = m0 + t0 * A0.dil;
+        if (i0 % A0.st) continue;
+        const int o0 = i0 / A0.st;
+        if (o0 >= A0.out) continue;
+        const int x = (m0 - axis_first(A0, i0)) / A0.dil;
+        for (int t1 = l1; t1 <= h1; ++t1) {
+            const int i1 = m1 + t1 * A1.dil;
+            if (i1 % A1.st) continue;
+            const int o1 = i1 / A1.st;
+            if (o1 >= A1.out) continue;
+            const int y = (m1 - axis_first(A1, i1)) / A1.dil;
+            for (int t2 = l2; t2 <= h2; ++t2) {
+                const int i2 = m2 + t2 * A2.dil;
+                if (i2 % A2.st) continue;
+                const int o2 = i2 / A2.st;
+                if (o2 >= A2.out) continue;
+                const int z = (m2 - axis_first(A2, i2)) / A2.dil;
+                f(o0, o1, o2, i0, i1, i2, (x * A1.k + y) * A2.k + z);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Element types.  bf16 is carried as raw bits; fp32 -> bf16 rounds to nearest
+// even with NaN kept quiet, the same rounding torch uses.
+// ---------------------------------------------------------------------------
+
+struct bf16 { uint16_t x; };
+using f16 = _Float16;
+
+__device__ __forceinline__ float to_f(float v) { return v; }
+__device__ __forceinline__ float to_f(f16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ float to_f(bf16 v) { return __uint_as_float(static_cast<uint32_t>(v.x) << 16); }
+
+template <typename T> __device__ __forceinline__ T from_f(float f);
+template <> __device__ __forceinline__ float from_f<float>(float f) { return f; }
+template <> __device__ __forceinline__ f16 from_f<f16>(float f) { return static_cast<f16>(f); }
+template <> __device__ __forceinline__ bf16 from_f<bf16>(float f) {
+    uint32_t u = __float_as_uint(f);
+    bf16 r;
+    if ((u & 0x7fffffffu) > 0x7f800000u) { r.x = static_cast<uint16_t>((u >> 16) | 0x40u); return r; }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    r.x = static_cast<uint16_t>(u >> 16);
+    return r;
+}
+
+// N consecutive elements starting at p[d0], converted to float.  `vec` means
+// p + d0 is aligned to N*sizeof(T) bytes and D % N == 0 (so d0 < D implies the
+// whole run is in range).  Otherwise a guarded scalar path.
+template <typename T, int N>
+__device__ __forceinline__ void load_run(const T* __restrict__ p, int d0, int D, bool vec, float (&out)[N]) {
+    if (vec) {
+        if (d0 < D) {
+            constexpr int NW = (N * (int)sizeof(T)) / 16;
+            static_assert(NW >= 1, "run must cover at least 16 bytes");
+            uint4 raw[NW];
+            const uint4* src = reinterpret_cast<const uint4*>(p + d0);
+#pragma unroll
+            for (int w = 0; w < NW; ++w) raw[w] = src[w];
+            const T* e = reinterpret_cast<const T*>(raw);
+#pragma unroll
+            for (int j = 0; j < N; ++j) out[j] = to_f(e[j]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; ++j) out[j] = 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < N; ++j) out[j] = (d0 + j < D) ? to_f(p[d0 + j]) : 0.f;
+    }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_run(T* __restrict__ p, int d0, int D, bool vec, const float (&in)[N]) {
+    if (vec) {
+        if (d0 < D) {
+            constexpr int NW = (N * (int)sizeof(T)) / 16;
+            T e[N];
+#pragma unroll
+            for (int j = 0; j < N; ++j) e[j] = from_f<T>(in[j]);
+            const uint4* src = reinterpret_cast<const uint4*>(e);
+            uint4* dst = reinterpret_cast<uint4*>(p + d0);
+#pragma unroll
+            for (int w = 0; w < NW; ++w) dst[w] = src[w];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+            if (d0 + j < D) p[d0 + j] = from_f<T>(in[j]);
+    }
+}
+
+// Sum over the LPQ consecutive lanes that share one query.
+template <int LPQ>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int m = LPQ / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, LPQ);
+    return v;
+}
+
+// Blocks are dealt round-robin to the 8 XCDs; remap so that each XCD works on
+// one contiguous range of logical blocks (neighbouring tiles share K/V lines in
+// that XCD's L2).  Identity on the tail that does not fill all 8.
+__device__ __forceinline__ int xcd_block(int bid, int nb) {
+    const int per = nb >> 3;
+    const int full = per << 3;
+    if (bid >= full) return bid;
+    return (bid & 7) * per + (bid >> 3);
+}
+
+}  // namespace na

@@ -1,0 +1,574 @@
+// Generic neighbourhood-attention kernels: every rank (as three padded axes),
+// dtype (fp32 / fp16 / bf16), kernel size, dilation, stride, causal mask and
+// GQA ratio.  Vector-ALU (FMA) kernels with fp32 accumulation.
+//
+// Work mapping: a "group" of LPQ consecutive lanes owns one query (or one key,
+// for the key-centric gradient kernels); each lane owns DPL consecutive head
+// dims, so a group covers up to DPL*LPQ dims and dot products finish with a
+// log2(LPQ)-step butterfly.  Queries are enumerated (b, o0, o1, o2, h) with the
+// head fastest, so one wave reads whole [H, D] token rows.  K/V neighbours are
+// read straight from global memory; the overlap between neighbouring windows
+// is served by L1/L2 (blocks are remapped so each XCD walks a contiguous
+// range).
+#include "na_launch.h"
+
+namespace na {
+
+namespace {
+
+struct QPos {
+    int b, h, o0, o1, o2, i0, i1, i2;
+};
+
+__device__ __forceinline__ QPos decode_query(const Prob& p, long long qi) {
+    QPos r;
+    r.h = static_cast<int>(qi % p.Hq);
+    long long t = qi / p.Hq;
+    r.o2 = static_cast<int>(t % p.ax[2].out); t /= p.ax[2].out;
+    r.o1 = static_cast<int>(t % p.ax[1].out); t /= p.ax[1].out;
+    r.o0 = static_cast<int>(t % p.ax[0].out);
+    r.b = static_cast<int>(t / p.ax[0].out);
+    r.i0 = r.o0 * p.ax[0].st;
+    r.i1 = r.o1 * p.ax[1].st;
+    r.i2 = r.o2 * p.ax[2].st;
+    return r;
+}
+
+struct KPos {
+    int b, h, m0, m1, m2;
+};
+
+__device__ __forceinline__ KPos decode_key(const Prob& p, long long ki, int heads) {
+    KPos r;
+    r.h = static_cast<int>(ki % heads);
+    long long t = ki / heads;
+    r.m2 = static_cast<int>(t % p.ax[2].len); t /= p.ax[2].len;
+    r.m1 = static_cast<int>(t % p.ax[1].len); t /= p.ax[1].len;
+    r.m0 = static_cast<int>(t % p.ax[0].len);
+    r.b = static_cast<int>(t / p.ax[0].len);
+    return r;
+}
+
+__device__ __forceinline__ long long group_index(int lpq) {
+    const int blk = xcd_block(blockIdx.x, gridDim.x);
+    return (static_cast<long long>(blk) * blockDim.x + threadIdx.x) / lpq;
+}
+
+// ---------------------------------------------------------------------------
+// Fused forward with online softmax.
+// ---------------------------------------------------------------------------
+template <typename T, int DPL, int LPQ>
+__global__ __launch_bounds__(256) void k_forward(Prob p, int vec,
+                                                 const T* __restrict__ q, Lay lq,
+                                                 const T* __restrict__ k, Lay lk,
+                                                 const T* __restrict__ v, Lay lv,
+                                                 T* __restrict__ out, Lay lo,
+                                                 float* __restrict__ lse, Lay ll) {
+    const long long qi = group_index(LPQ);
+    if (qi >= static_cast<long long>(p.B) * p.nout * p.Hq) return;
+    const int d0 = (threadIdx.x % LPQ) * DPL;
+    const QPos Q = decode_query(p, qi);
+    const int hk = Q.h / p.rep;
+
+    float qv[DPL];
+    load_run<T, DPL>(q + lq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, qv);
+    float m = -INFINITY, l = 0.f, acc[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+
+    for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int, bool ok) {
+        if (!ok) return;
+        float kv[DPL], vv[DPL];
+        load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk, vec, kv);
+        load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, hk), d0, p.Dv, vec, vv);
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) s = fmaf(qv[j], kv[j], s);
+        s = group_sum<LPQ>(s) * p.scale;
+        if (s > m) {
+            const float c = expf(m - s);
+            l *= c;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) acc[j] *= c;
+            m = s;
+        }
+        const float e = expf(s - m);
+        l += e;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(e, vv[j], acc[j]);
+    });
+
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] = acc[j] / l;
+    store_run<T, DPL>(out + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, acc);
+    if (d0 == 0) lse[ll.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = m + logf(l);
+}
+
+// ---------------------------------------------------------------------------
+// Split QK: logits per neighbour (unscaled unless has_scale), -inf if invalid.
+// ---------------------------------------------------------------------------
+template <typename T, int DPL, int LPQ>
+__global__ __launch_bounds__(256) void k_qk(Prob p, int vec,
+                                            const T* __restrict__ q, Lay lq,
+                                            const T* __restrict__ k, Lay lk,
+                                            T* __restrict__ attn, Lay la) {
+    const long long qi = group_index(LPQ);
+    if (qi >= static_cast<long long>(p.B) * p.nout * p.Hq) return;
+    const int d0 = (threadIdx.x % LPQ) * DPL;
+    const QPos Q = decode_query(p, qi);
+    float qv[DPL];
+    load_run<T, DPL>(q + lq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, qv);
+    T* row = attn + la.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h);
+    for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
+        float s = -INFINITY;
+        if (ok) {
+            float kv[DPL];
+            load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, Q.h), d0, p.Dqk, vec, kv);
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) acc = fmaf(qv[j], kv[j], acc);
+            s = group_sum<LPQ>(acc);
+        }
+        if (p.has_scale) s *= p.scale;
+        if (d0 == 0) row[e] = from_f<T>(s);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Split AV: out = sum_valid attn * v.
+// ---------------------------------------------------------------------------
+template <typename T, int DPL, int LPQ>
+__global__ __launch_bounds__(256) void k_av(Prob p, int vec,
+                                            const T* __restrict__ attn, Lay la,
+                                            const T* __restrict__ v, Lay lv,
+                                            T* __restrict__ out, Lay lo) {
+    const long long qi = group_index(LPQ);
+    if (qi >= static_cast<long long>(p.B) * p.nout * p.Hq) return;
+    const int d0 = (threadIdx.x % LPQ) * DPL;
+    const QPos Q = decode_query(p, qi);
+    const T* row = attn + la.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h);
+    float acc[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+    for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
+        if (!ok) return;
+        const float a = to_f(row[e]);
+        float vv[DPL];
+        load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, Q.h), d0, p.Dv, vec, vv);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(a, vv[j], acc[j]);
+    });
+    store_run<T, DPL>(out + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Fused backward, query side: delta = dO.O - dlse, and
+// dq = scale * sum_k P (dO.v_k - delta) k_k with P = exp(scale q.k - lse).
+// ---------------------------------------------------------------------------
+template <typename T, int DPL, int LPQ>
+__global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec,
+                                                const T* __restrict__ q, Lay lq,
+                                                const T* __restrict__ k, Lay lk,
+                                                const T* __restrict__ v, Lay lv,
+                                                const T* __restrict__ o, Lay lo,
+                                                const T* __restrict__ dout, Lay ldo,
+                                                const float* __restrict__ lse, Lay ll,
+                                                const float* __restrict__ dlse, Lay ldl,
+                                                T* __restrict__ dq, Lay ldq,
+                                                float* __restrict__ delta, Lay lde) {
+    const long long qi = group_index(LPQ);
+    if (qi >= static_cast<long long>(p.B) * p.nout * p.Hq) return;
+    const int d0 = (threadIdx.x % LPQ) * DPL;
+    const QPos Q = decode_query(p, qi);
+    const int hk = Q.h / p.rep;
+
+    float qv[DPL], dov[DPL], ov[DPL];
+    load_run<T, DPL>(q + lq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, qv);
+    load_run<T, DPL>(dout + ldo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, dov);
+    load_run<T, DPL>(o + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, ov);
+    float di = 0.f;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) di = fmaf(dov[j], ov[j], di);
+    di = group_sum<LPQ>(di);
+    if (dlse) di -= dlse[ldl.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)];
+    if (d0 == 0) delta[lde.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = di;
+    const float L = lse[ll.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)];
+
+    float acc[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+    for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int, bool ok) {
+        if (!ok) return;
+        float kv[DPL], vv[DPL];
+        load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk, vec, kv);
+        load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, hk), d0, p.Dv, vec, vv);
+        float s = 0.f, dp = 0.f;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) { s = fmaf(qv[j], kv[j], s); dp = fmaf(dov[j], vv[j], dp); }
+        s = group_sum<LPQ>(s) * p.scale;
+        dp = group_sum<LPQ>(dp);
+        const float ds = expf(s - L) * (dp - di);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(ds, kv[j], acc[j]);
+    });
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] *= p.scale;
+    store_run<T, DPL>(dq + ldq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Fused backward, key side: for each key/value position and kv head, gather
+// over the queries (of every q head in the GQA group) whose windows hold it:
+// dv = sum P dO,  dk = scale * sum P (dO.v - delta) q.  Deterministic (no
+// atomics); recomputes P from q, k and lse.
+// ---------------------------------------------------------------------------
+template <typename T, int DPL, int LPQ>
+__global__ __launch_bounds__(256) void k_bwd_dkdv(Prob p, int vec,
+                                                  const T* __restrict__ q, Lay lq,
+                                                  const T* __restrict__ k, Lay lk,
+                                                  const T* __restrict__ v, Lay lv,
+                                                  const T* __restrict__ dout, Lay ldo,
+                                                  const float* __restrict__ lse, Lay ll,
+                                                  const float* __restrict__ delta, Lay lde,
+                                                  T* __restrict__ dk, Lay ldk,
+                                                  T* __restrict__ dv, Lay ldv) {
+    const long long ki = group_index(LPQ);
+    if (ki >= static_cast<long long>(p.B) * p.nkey * p.Hkv) return;
+    const int d0 = (threadIdx.x % LPQ) * DPL;
+    const KPos K = decode_key(p, ki, p.Hkv);
+
+    float kv[DPL], vv[DPL], gk[DPL], gv[DPL];
+    load_run<T, DPL>(k + lk.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dqk, vec, kv);
+    load_run<T, DPL>(v + lv.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dv, vec, vv);
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) { gk[j] = 0.f; gv[j] = 0.f; }
+
+    for_each_query(p, K.m0, K.m1, K.m2, [&](int o0, int o1, int o2, int i0, int i1, int i2, int) {
+        for (int r = 0; r < p.rep; ++r) {
+            const int h = K.h * p.rep + r;
+            float qv[DPL], dov[DPL];
+            load_run<T, DPL>(q + lq.at(K.b, i0, i1, i2, h), d0, p.Dqk, vec, qv);
+            load_run<T, DPL>(dout + ldo.at(K.b, o0, o1, o2, h), d0, p.Dv, vec, dov);
+            const float L = lse[ll.at(K.b, o0, o1, o2, h)];
+            const float di = delta[lde.at(K.b, o0, o1, o2, h)];
+            float s = 0.f, dp = 0.f;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) { s = fmaf(qv[j], kv[j], s); dp = fmaf(dov[j], vv[j], dp); }
+            s = group_sum<LPQ>(s) * p.scale;
+            dp = group_sum<LPQ>(dp);
+            const float pr = expf(s - L);
+            const float ds = pr * (dp - di);
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) {
+                gv[j] = fmaf(pr, dov[j], gv[j]);
+                gk[j] = fmaf(ds, qv[j], gk[j]);
+            }
+        }
+    });
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) gk[j] *= p.scale;
+    store_run<T, DPL>(dk + ldk.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dqk, vec, gk);
+    store_run<T, DPL>(dv + ldv.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dv, vec, gv);
+}
+
+// ---------------------------------------------------------------------------
+// Split QK backward.  dq (query side) and dk (key side); grad of an invalid
+// entry is zero, and both carry the logit scale when has_scale.
+// ---------------------------------------------------------------------------
+template <typename T, int DPL, int LPQ>
+__global__ __launch_bounds__(256) void k_qk_bwd_q(Prob p, int vec,
+                                                  const T* __restrict__ da, Lay lda,
+                                                  const T* __restrict__ k, Lay lk,
+                                                  T* __restrict__ dq, Lay ldq) {
+    const long long qi = group_index(LPQ);
+    if (qi >= static_cast<long long>(p.B) * p.nout * p.Hq) return;
+    const int d0 = (threadIdx.x % LPQ) * DPL;
+    const QPos Q = decode_query(p, qi);
+    const T* row = da + lda.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h);
+    float acc[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+    for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
+        if (!ok) return;
+        const float g = to_f(row[e]);
+        float kv[DPL];
+        load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, Q.h), d0, p.Dqk, vec, kv);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(g, kv[j], acc[j]);
+    });
+    if (p.has_scale) {
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[j] *= p.scale;
+    }
+    store_run<T, DPL>(dq + ldq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, acc);
+}
+
+template <typename T, int DPL, int LPQ>
+__global__ __launch_bounds__(256) void k_qk_bwd_k(Prob p, int vec,
+                                                  const T* __restrict__ da, Lay lda,
+                                                  const T* __restrict__ q, Lay lq,
+                                                  T* __restrict__ dk, Lay ldk) {
+    const long long ki = group_index(LPQ);
+    if (ki >= static_cast<long long>(p.B) * p.nkey * p.Hkv) return;
+    const int d0 = (threadIdx.x % LPQ) * DPL;
+    const KPos K = decode_key(p, ki, p.Hkv);
+    float acc[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+    for_each_query(p, K.m0, K.m1, K.m2, [&](int o0, int o1, int o2, int i0, int i1, int i2, int e) {
+        const float g = to_f(da[lda.at(K.b, o0, o1, o2, K.h) + e]);
+        float qv[DPL];
+        load_run<T, DPL>(q + lq.at(K.b, i0, i1, i2, K.h), d0, p.Dqk, vec, qv);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(g, qv[j], acc[j]);
+    });
+    if (p.has_scale) {
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[j] *= p.scale;
+    }
+    store_run<T, DPL>(dk + ldk.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dqk, vec, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Split AV backward: dattn (query side) and dv (key side).
+// ---------------------------------------------------------------------------
+template <typename T, int DPL, int LPQ>
+__global__ __launch_bounds__(256) void k_av_bwd_a(Prob p, int vec,
+                                                  const T* __restrict__ dout, Lay ldo,
+                                                  const T* __restrict__ v, Lay lv,
+                                                  T* __restrict__ da, Lay lda) {
+    const long long qi = group_index(LPQ);
+    if (qi >= static_cast<long long>(p.B) * p.nout * p.Hq) return;
+    const int d0 = (threadIdx.x % LPQ) * DPL;
+    const QPos Q = decode_query(p, qi);
+    float dov[DPL];
+    load_run<T, DPL>(dout + ldo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, dov);
+    T* row = da + lda.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h);
+    for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
+        float g = 0.f;
+        if (ok) {
+            float vv[DPL];
+            load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, Q.h), d0, p.Dv, vec, vv);
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) acc = fmaf(dov[j], vv[j], acc);
+            g = group_sum<LPQ>(acc);
+        }
+        if (d0 == 0) row[e] = from_f<T>(g);
+    });
+}
+
+template <typename T, int DPL, int LPQ>
+__global__ __launch_bounds__(256) void k_av_bwd_v(Prob p, int vec,
+                                                  const T* __restrict__ dout, Lay ldo,
+                                                  const T* __restrict__ attn, Lay la,
+                                                  T* __restrict__ dv, Lay ldv) {
+    const long long ki = group_index(LPQ);
+    if (ki >= static_cast<long long>(p.B) * p.nkey * p.Hkv) return;
+    const int d0 = (threadIdx.x % LPQ) * DPL;
+    const KPos K = decode_key(p, ki, p.Hkv);
+    float acc[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+    for_each_query(p, K.m0, K.m1, K.m2, [&](int o0, int o1, int o2, int, int, int, int e) {
+        const float a = to_f(attn[la.at(K.b, o0, o1, o2, K.h) + e]);
+        float dov[DPL];
+        load_run<T, DPL>(dout + ldo.at(K.b, o0, o1, o2, K.h), d0, p.Dv, vec, dov);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(a, dov[j], acc[j]);
+    });
+    store_run<T, DPL>(dv + ldv.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dv, vec, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Neighbourhood map export (one thread per (query position, neighbour)).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_map(Prob p, int64_t* __restrict__ flat, uint8_t* __restrict__ valid) {
+    const long long t = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= static_cast<long long>(p.nout) * p.kv) return;
+    const int e = static_cast<int>(t % p.kv);
+    long long oq = t / p.kv;
+    const int o2 = static_cast<int>(oq % p.ax[2].out); oq /= p.ax[2].out;
+    const int o1 = static_cast<int>(oq % p.ax[1].out); oq /= p.ax[1].out;
+    const int o0 = static_cast<int>(oq);
+    const int z = e % p.ax[2].k, y = (e / p.ax[2].k) % p.ax[1].k, x = e / (p.ax[2].k * p.ax[1].k);
+    const int os[3] = {o0, o1, o2}, ks[3] = {x, y, z};
+    long long f = 0;
+    bool ok = true;
+    for (int a = 0; a < 3; ++a) {
+        const Axis& A = p.ax[a];
+        const int i = os[a] * A.st;
+        int j = axis_first(A, i) + ks[a] * A.dil;
+        if (A.causal) {
+            ok = ok && (j >= 0) && (j <= i);
+            j = j < 0 ? 0 : (j > A.len - 1 ? A.len - 1 : j);
+        }
+        f = f * A.len + j;
+    }
+    flat[t] = f;
+    valid[t] = ok ? 1 : 0;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Launchers.
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// Lanes-per-query / dims-per-lane configurations, chosen from the head dim.
+template <template <typename, int, int> class Launch, typename T, typename... Args>
+hipError_t by_dim(int D, Args&&... args) {
+    if (D <= 8) return Launch<T, 8, 1>::run(args...);
+    if (D <= 16) return Launch<T, 8, 2>::run(args...);
+    if (D <= 32) return Launch<T, 8, 4>::run(args...);
+    if (D <= 64) return Launch<T, 8, 8>::run(args...);
+    if (D <= 128) return Launch<T, 8, 16>::run(args...);
+    return Launch<T, 16, 16>::run(args...);
+}
+
+template <template <typename, int, int> class Launch, typename... Args>
+hipError_t by_type(int dtype, int D, Args&&... args) {
+    switch (dtype) {
+        case NATTEN_F32: return by_dim<Launch, float>(D, args...);
+        case NATTEN_F16: return by_dim<Launch, f16>(D, args...);
+        default: return by_dim<Launch, bf16>(D, args...);
+    }
+}
+
+inline unsigned grid_for(long long groups, int lpq) {
+    const long long threads = groups * lpq;
+    return static_cast<unsigned>((threads + 255) / 256);
+}
+
+template <typename T, int DPL, int LPQ>
+struct LForward {
+    static hipError_t run(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
+                          Lay lv, void* o, Lay lo, float* lse, Lay ll, hipStream_t s) {
+        const long long n = static_cast<long long>(p.B) * p.nout * p.Hq;
+        NA_LAUNCH("na_forward", (k_forward<T, DPL, LPQ>), dim3(grid_for(n, LPQ)), dim3(256), 0, s, p, vec,
+                           (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (T*)o, lo, lse, ll);
+        return hipGetLastError();
+    }
+};
+
+template <typename T, int DPL, int LPQ>
+struct LQK {
+    static hipError_t run(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, void* a, Lay la,
+                          hipStream_t s) {
+        const long long n = static_cast<long long>(p.B) * p.nout * p.Hq;
+        NA_LAUNCH("na_qk", (k_qk<T, DPL, LPQ>), dim3(grid_for(n, LPQ)), dim3(256), 0, s, p, vec, (const T*)q, lq,
+                           (const T*)k, lk, (T*)a, la);
+        return hipGetLastError();
+    }
+};
+
+template <typename T, int DPL, int LPQ>
+struct LAV {
+    static hipError_t run(const Prob& p, int vec, const void* a, Lay la, const void* v, Lay lv, void* o, Lay lo,
+                          hipStream_t s) {
+        const long long n = static_cast<long long>(p.B) * p.nout * p.Hq;
+        NA_LAUNCH("na_av", (k_av<T, DPL, LPQ>), dim3(grid_for(n, LPQ)), dim3(256), 0, s, p, vec, (const T*)a, la,
+                           (const T*)v, lv, (T*)o, lo);
+        return hipGetLastError();
+    }
+};
+
+template <typename T, int DPL, int LPQ>
+struct LBackward {
+    static hipError_t run(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
+                          Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
+                          const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
+                          float* delta, Lay lde, hipStream_t s) {
+        const long long nq = static_cast<long long>(p.B) * p.nout * p.Hq;
+        NA_LAUNCH("na_bwd_dq", (k_bwd_dq<T, DPL, LPQ>), dim3(grid_for(nq, LPQ)), dim3(256), 0, s, p, vec,
+                           (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (const T*)o, lo, (const T*)dout, ldo,
+                           lse, ll, dlse, ldl, (T*)dq, ldq, delta, lde);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const long long nk = static_cast<long long>(p.B) * p.nkey * p.Hkv;
+        NA_LAUNCH("na_bwd_dkdv", (k_bwd_dkdv<T, DPL, LPQ>), dim3(grid_for(nk, LPQ)), dim3(256), 0, s, p, vec,
+                           (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (const T*)dout, ldo, lse, ll,
+                           (const float*)delta, lde, (T*)dk, ldk, (T*)dv, ldv);
+        return hipGetLastError();
+    }
+};
+
+template <typename T, int DPL, int LPQ>
+struct LQKBwd {
+    static hipError_t run(const Prob& p, int vec, const void* da, Lay lda, const void* q, Lay lq, const void* k,
+                          Lay lk, void* dq, Lay ldq, void* dk, Lay ldk, hipStream_t s) {
+        const long long nq = static_cast<long long>(p.B) * p.nout * p.Hq;
+        NA_LAUNCH("na_qk_bwd_q", (k_qk_bwd_q<T, DPL, LPQ>), dim3(grid_for(nq, LPQ)), dim3(256), 0, s, p, vec,
+                           (const T*)da, lda, (const T*)k, lk, (T*)dq, ldq);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const long long nk = static_cast<long long>(p.B) * p.nkey * p.Hkv;
+        NA_LAUNCH("na_qk_bwd_k", (k_qk_bwd_k<T, DPL, LPQ>), dim3(grid_for(nk, LPQ)), dim3(256), 0, s, p, vec,
+                           (const T*)da, lda, (const T*)q, lq, (T*)dk, ldk);
+        return hipGetLastError();
+    }
+};
+
+template <typename T, int DPL, int LPQ>
+struct LAVBwd {
+    static hipError_t run(const Prob& p, int vec, const void* dout, Lay ldo, const void* a, Lay la, const void* v,
+                          Lay lv, void* da, Lay lda, void* dv, Lay ldv, hipStream_t s) {
+        const long long nq = static_cast<long long>(p.B) * p.nout * p.Hq;
+        NA_LAUNCH("na_av_bwd_a", (k_av_bwd_a<T, DPL, LPQ>), dim3(grid_for(nq, LPQ)), dim3(256), 0, s, p, vec,
+                           (const T*)dout, ldo, (const T*)v, lv, (T*)da, lda);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const long long nk = static_cast<long long>(p.B) * p.nkey * p.Hkv;
+        NA_LAUNCH("na_av_bwd_v", (k_av_bwd_v<T, DPL, LPQ>), dim3(grid_for(nk, LPQ)), dim3(256), 0, s, p, vec,
+                           (const T*)dout, ldo, (const T*)a, la, (T*)dv, ldv);
+        return hipGetLastError();
+    }
+};
+
+}  // namespace
+
+hipError_t generic_forward(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
+                           Lay lv, void* o, Lay lo, float* lse, Lay ll, int dtype, hipStream_t s) {
+    return by_type<LForward>(dtype, p.Dqk > p.Dv ? p.Dqk : p.Dv, p, vec, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
+}
+
+hipError_t generic_qk(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, void* a, Lay la,
+                      int dtype, hipStream_t s) {
+    return by_type<LQK>(dtype, p.Dqk, p, vec, q, lq, k, lk, a, la, s);
+}
+
+hipError_t generic_av(const Prob& p, int vec, const void* a, Lay la, const void* v, Lay lv, void* o, Lay lo,
+                      int dtype, hipStream_t s) {
+    return by_type<LAV>(dtype, p.Dv, p, vec, a, la, v, lv, o, lo, s);
+}
+
+hipError_t generic_backward(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
+                            Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
+                            const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
+                            float* delta, Lay lde, int dtype, hipStream_t s) {
+    return by_type<LBackward>(dtype, p.Dqk > p.Dv ? p.Dqk : p.Dv, p, vec, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl, dq,
+                              ldq, dk, ldk, dv, ldv, delta, lde, s);
+}
+
+hipError_t generic_qk_backward(const Prob& p, int vec, const void* da, Lay lda, const void* q, Lay lq,
+                               const void* k, Lay lk, void* dq, Lay ldq, void* dk, Lay ldk, int dtype,
+                               hipStream_t s) {
+    return by_type<LQKBwd>(dtype, p.Dqk, p, vec, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, s);
+}
+
+hipError_t generic_av_backward(const Prob& p, int vec, const void* dout, Lay ldo, const void* a, Lay la,
+                               const void* v, Lay lv, void* da, Lay lda, void* dv, Lay ldv, int dtype,
+                               hipStream_t s) {
+    return by_type<LAVBwd>(dtype, p.Dv, p, vec, dout, ldo, a, la, v, lv, da, lda, dv, ldv, s);
+}
+
+hipError_t neighborhood_map(const Prob& p, int64_t* flat, uint8_t* valid, hipStream_t s) {
+    const long long n = static_cast<long long>(p.nout) * p.kv;
+    if (n == 0) return hipSuccess;
+    NA_LAUNCH("na_map", k_map, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, p, flat, valid);
+    return hipGetLastError();
+}
+
+}  // namespace na

@@ -1,0 +1,38 @@
+// Host-side launch entry points shared between the kernel files and the C ABI.
+#pragma once
+
+#include "na_common.h"
+
+namespace na {
+
+// Optional event timing around each launch (na_profile.hip).
+void prof_begin(const char* name, hipStream_t s);
+void prof_end(hipStream_t s);
+
+hipError_t generic_forward(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
+                           Lay lv, void* o, Lay lo, float* lse, Lay ll, int dtype, hipStream_t s);
+hipError_t generic_qk(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, void* a, Lay la,
+                      int dtype, hipStream_t s);
+hipError_t generic_av(const Prob& p, int vec, const void* a, Lay la, const void* v, Lay lv, void* o, Lay lo,
+                      int dtype, hipStream_t s);
+hipError_t generic_backward(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
+                            Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
+                            const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
+                            float* delta, Lay lde, int dtype, hipStream_t s);
+hipError_t generic_qk_backward(const Prob& p, int vec, const void* da, Lay lda, const void* q, Lay lq,
+                               const void* k, Lay lk, void* dq, Lay ldq, void* dk, Lay ldk, int dtype,
+                               hipStream_t s);
+hipError_t generic_av_backward(const Prob& p, int vec, const void* dout, Lay ldo, const void* a, Lay la,
+                               const void* v, Lay lv, void* da, Lay lda, void* dv, Lay ldv, int dtype,
+                               hipStream_t s);
+hipError_t neighborhood_map(const Prob& p, int64_t* flat, uint8_t* valid, hipStream_t s);
+
+}  // namespace na
+
+// Launch with optional event timing (see na_profile.hip).
+#define NA_LAUNCH(name, kernel, grid, block, shmem, stream, ...)                     \
+    do {                                                                             \
+        ::na::prof_begin(name, stream);                                              \
+        hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);         \
+        ::na::prof_end(stream);                                                      \
+    } while (0)

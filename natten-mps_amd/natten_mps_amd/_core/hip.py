@@ -1,0 +1,355 @@
+"""The ``'hip'`` backend: neighbourhood attention on MI355X (gfx950) through
+libnatten_hip.so.
+
+Module contract (same names and argument order as the reference backends,
+``_core/ops.py:22-32`` and the hooks the autograd factory looks up,
+``autograd/_factory.py:37-38,66-67`` of /root/reference/src/natten_mps):
+
+* ``na{r}d_forward(q, k, v, kernel_size, stride, dilation, is_causal, scale)``
+* ``na{r}d_forward_with_lse(...) -> (out, lse)`` -- lse is fp32 ``[B, *sp_out, Hq]``
+* ``na{r}d_fused_backward(d_out, q, k, v, out, lse, kernel_size, dilation,
+  stride, is_causal, scale, d_lse=None) -> (dq, dk, dv)``
+* ``na{r}d_qk_forward(q, k, kernel_size, dilation, stride, is_causal, scale)``
+* ``na{r}d_av_forward(attn, v, kernel_size, dilation, stride, is_causal)``
+* ``na{r}d_qk_backward(d_attn, q, k, kernel_size, dilation, stride, is_causal,
+  scale=None) -> (dq, dk)``
+* ``na{r}d_av_backward(d_out, attn, v, kernel_size, dilation, stride,
+  is_causal) -> (d_attn, dv)``
+
+Tensors stay spatial-first ``[B, *sp, H, D]``; the kernels read them through
+their strides (only a non-unit innermost stride forces a copy), in their own
+dtype (no bf16 upcast copies).  K/V may carry fewer heads than Q (native GQA:
+query head h uses kv head ``h // (Hq/Hkv)``).
+
+There is no CPU path: CPU tensors or dtypes other than fp32/fp16/bf16 raise.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+
+# Functional-layer capability flags.
+NATIVE_GQA = True
+FUSED_LSE = True
+
+
+def is_available() -> bool:
+    if not _lib.is_built():
+        return False
+    try:
+        if not torch.cuda.is_available():
+            return False
+        _lib.load()
+    except Exception:
+        return False
+    return True
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+
+def _ceil_div(a: int, b: int) -> int:
+    return (a + b - 1) // b
+
+
+def _on_device(*ts: Optional[torch.Tensor]) -> None:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "natten_mps_amd 'hip' backend: tensors must live on a ROCm GPU "
+                f"(got a tensor on {t.device}). Move them with .cuda()."
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError("natten_mps_amd 'hip' backend: all tensors must be on the same GPU.")
+
+
+def _inner(t: torch.Tensor) -> torch.Tensor:
+    """The kernels need a unit stride on the innermost dim only."""
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _same_dtype(*ts: Optional[torch.Tensor]) -> None:
+    dts = {t.dtype for t in ts if t is not None}
+    if len(dts) > 1:
+        raise TypeError(f"natten_mps_amd 'hip' backend: mixed dtypes {sorted(map(str, dts))}.")
+
+
+def _byref(x):
+    return ctypes.byref(x)
+
+
+def _fused_problem(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale):
+    sp = tuple(q.shape[1:1 + rank])
+    return _lib.problem(
+        batch=q.shape[0], heads_q=q.shape[-2], heads_kv=k.shape[-2], dim_qk=q.shape[-1], dim_v=v.shape[-1],
+        dtype=_lib.dtype_code(q), length=sp, out_length=[_ceil_div(n, s) for n, s in zip(sp, stride)],
+        kernel_size=kernel_size, dilation=dilation, stride=stride, is_causal=is_causal, scale=scale,
+    )
+
+
+def _check_qkv(rank, q, k, v):
+    nd = rank + 3
+    if q.ndim != nd or k.ndim != nd or v.ndim != nd:
+        raise ValueError(f"na{rank}d expects query/key/value with {nd} dims [B, *spatial, heads, dim].")
+    if q.shape[:1 + rank] != k.shape[:1 + rank] or k.shape[:-1] != v.shape[:-1]:
+        raise ValueError("query/key/value batch and spatial dims must match, and key/value heads must match.")
+    if q.shape[-1] != k.shape[-1]:
+        raise ValueError("query and key head dims must match.")
+    if q.shape[-2] % k.shape[-2] != 0:
+        raise ValueError(f"heads_q ({q.shape[-2]}) must be divisible by heads_kv ({k.shape[-2]}).")
+
+
+# ---------------------------------------------------------------------------
+# fused forward / backward
+# ---------------------------------------------------------------------------
+
+
+def forward_with_lse(rank: int, q, k, v, kernel_size, stride, dilation, is_causal, scale):
+    _check_qkv(rank, q, k, v)
+    _on_device(q, k, v)
+    _same_dtype(q, k, v)
+    q, k, v = _inner(q), _inner(k), _inner(v)
+    scale_value = float(q.shape[-1] ** -0.5 if scale is None else scale)
+    prob = _fused_problem(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_value)
+    out_sp = tuple(prob.out_length[3 - rank:])
+    B, Hq = q.shape[0], q.shape[-2]
+    out = torch.empty((B, *out_sp, Hq, v.shape[-1]), dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, *out_sp, Hq), dtype=torch.float32, device=q.device)
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        rc = lib.natten_hip_forward(
+            _byref(prob),
+            _lib.ptr(q), _byref(_lib.layout(q, rank, 1)),
+            _lib.ptr(k), _byref(_lib.layout(k, rank, 1)),
+            _lib.ptr(v), _byref(_lib.layout(v, rank, 1)),
+            _lib.ptr(out), _byref(_lib.layout(out, rank, 1)),
+            _lib.ptr(lse), _byref(_lib.layout(lse, rank, 0)),
+            _lib.stream_of(q),
+        )
+    _lib.check(rc, "forward")
+    return out, lse
+
+
+def fused_backward(rank: int, d_out, q, k, v, out, lse, kernel_size, dilation, stride, is_causal, scale,
+                   d_lse=None):
+    _check_qkv(rank, q, k, v)
+    _on_device(d_out, q, k, v, out, lse, d_lse)
+    _same_dtype(d_out, q, k, v, out)
+    q, k, v, out, d_out = (_inner(t) for t in (q, k, v, out, d_out))
+    scale_value = float(q.shape[-1] ** -0.5 if scale is None else scale)
+    prob = _fused_problem(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_value)
+    lse = lse.to(torch.float32)
+    if d_lse is not None:
+        d_lse = d_lse.to(torch.float32)
+    strided = any(s != 1 for s in stride)
+    dq = (torch.zeros if strided else torch.empty)(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    delta = torch.empty(lse.shape, dtype=torch.float32, device=q.device)
+    lib = _lib.load()
+    L = lambda t, tr: _byref(_lib.layout(t, rank, tr))  # noqa: E731
+    with torch.cuda.device(q.device):
+        rc = lib.natten_hip_backward(
+            _byref(prob),
+            _lib.ptr(q), L(q, 1), _lib.ptr(k), L(k, 1), _lib.ptr(v), L(v, 1),
+            _lib.ptr(out), L(out, 1), _lib.ptr(d_out), L(d_out, 1),
+            _lib.ptr(lse), L(lse, 0),
+            _lib.ptr(d_lse), (L(d_lse, 0) if d_lse is not None else None),
+            _lib.ptr(dq), L(dq, 1), _lib.ptr(dk), L(dk, 1), _lib.ptr(dv), L(dv, 1),
+            _lib.ptr(delta), L(delta, 0),
+            _lib.stream_of(q),
+        )
+    _lib.check(rc, "backward")
+    return dq, dk, dv
+
+
+def forward(rank: int, q, k, v, kernel_size, stride, dilation, is_causal, scale):
+    return forward_with_lse(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale)[0]
+
+
+# ---------------------------------------------------------------------------
+# split QK / AV and their backward
+# ---------------------------------------------------------------------------
+
+
+def _split_problem(rank, ref, heads, dim_qk, dim_v, sp, out_sp, kernel_size, dilation, stride, is_causal, scale):
+    return _lib.problem(
+        batch=ref.shape[0], heads_q=heads, heads_kv=heads, dim_qk=dim_qk, dim_v=dim_v,
+        dtype=_lib.dtype_code(ref), length=sp, out_length=out_sp, kernel_size=kernel_size,
+        dilation=dilation, stride=stride, is_causal=is_causal, scale=scale,
+    )
+
+
+def _attn_extent(rank, attn, sp, stride):
+    out_sp = tuple(attn.shape[1:1 + rank])
+    for n_out, n, s in zip(out_sp, sp, stride):
+        if s != 1 and n_out != _ceil_div(n, s):
+            raise ValueError(f"attn spatial extent {out_sp} does not match ceil({tuple(sp)}/{tuple(stride)}).")
+        if n_out > n:
+            raise ValueError("attn spatial dimensions cannot exceed value spatial dimensions.")
+    return out_sp
+
+
+def qk_forward(rank: int, q, k, kernel_size, dilation, stride, is_causal, scale):
+    if q.ndim != rank + 3 or q.shape != k.shape:
+        raise ValueError(f"na{rank}d_qk expects query/key of identical shape [B, *spatial, heads, dim].")
+    _on_device(q, k)
+    _same_dtype(q, k)
+    q, k = _inner(q), _inner(k)
+    sp = tuple(q.shape[1:1 + rank])
+    out_sp = tuple(_ceil_div(n, s) for n, s in zip(sp, stride))
+    kv = 1
+    for x in kernel_size:
+        kv *= x
+    prob = _split_problem(rank, q, q.shape[-2], q.shape[-1], q.shape[-1], sp, out_sp, kernel_size, dilation,
+                          stride, is_causal, scale)
+    attn = torch.empty((q.shape[0], *out_sp, q.shape[-2], kv), dtype=q.dtype, device=q.device)
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        rc = lib.natten_hip_qk_forward(
+            _byref(prob), _lib.ptr(q), _byref(_lib.layout(q, rank, 1)), _lib.ptr(k),
+            _byref(_lib.layout(k, rank, 1)), _lib.ptr(attn), _byref(_lib.layout(attn, rank, 1)),
+            _lib.stream_of(q))
+    _lib.check(rc, "qk_forward")
+    return attn
+
+
+def av_forward(rank: int, attn, v, kernel_size, dilation, stride, is_causal):
+    if attn.ndim != rank + 3 or v.ndim != rank + 3:
+        raise ValueError(f"na{rank}d_av expects attn [B, *spatial, heads, KV] and value [B, *spatial, heads, dim].")
+    if attn.shape[0] != v.shape[0] or attn.shape[-2] != v.shape[-2]:
+        raise ValueError("Batch and head dimensions of attn/value must match.")
+    _on_device(attn, v)
+    _same_dtype(attn, v)
+    attn, v = _inner(attn), _inner(v)
+    sp = tuple(v.shape[1:1 + rank])
+    out_sp = _attn_extent(rank, attn, sp, stride)
+    prob = _split_problem(rank, v, v.shape[-2], v.shape[-1], v.shape[-1], sp, out_sp, kernel_size, dilation,
+                          stride, is_causal, None)
+    if attn.shape[-1] != prob.kernel[0] * prob.kernel[1] * prob.kernel[2]:
+        raise ValueError("attn last dim must equal the kernel volume.")
+    out = torch.empty((v.shape[0], *out_sp, v.shape[-2], v.shape[-1]), dtype=v.dtype, device=v.device)
+    lib = _lib.load()
+    with torch.cuda.device(v.device):
+        rc = lib.natten_hip_av_forward(
+            _byref(prob), _lib.ptr(attn), _byref(_lib.layout(attn, rank, 1)), _lib.ptr(v),
+            _byref(_lib.layout(v, rank, 1)), _lib.ptr(out), _byref(_lib.layout(out, rank, 1)),
+            _lib.stream_of(v))
+    _lib.check(rc, "av_forward")
+    return out
+
+
+def qk_backward(rank: int, d_attn, q, k, kernel_size, dilation, stride, is_causal, scale=None):
+    _on_device(d_attn, q, k)
+    d_attn = d_attn.to(q.dtype)
+    d_attn, q, k = _inner(d_attn), _inner(q), _inner(k)
+    sp = tuple(q.shape[1:1 + rank])
+    out_sp = _attn_extent(rank, d_attn, sp, stride)
+    prob = _split_problem(rank, q, q.shape[-2], q.shape[-1], q.shape[-1], sp, out_sp, kernel_size, dilation,
+                          stride, is_causal, scale)
+    strided = any(s != 1 for s in stride) or out_sp != sp
+    dq = (torch.zeros if strided else torch.empty)(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    lib = _lib.load()
+    L = lambda t: _byref(_lib.layout(t, rank, 1))  # noqa: E731
+    with torch.cuda.device(q.device):
+        rc = lib.natten_hip_qk_backward(
+            _byref(prob), _lib.ptr(d_attn), L(d_attn), _lib.ptr(q), L(q), _lib.ptr(k), L(k),
+            _lib.ptr(dq), L(dq), _lib.ptr(dk), L(dk), _lib.stream_of(q))
+    _lib.check(rc, "qk_backward")
+    return dq, dk
+
+
+def av_backward(rank: int, d_out, attn, v, kernel_size, dilation, stride, is_causal):
+    _on_device(d_out, attn, v)
+    d_out = d_out.to(v.dtype)
+    attn = attn.to(v.dtype)
+    d_out, attn, v = _inner(d_out), _inner(attn), _inner(v)
+    sp = tuple(v.shape[1:1 + rank])
+    out_sp = _attn_extent(rank, attn, sp, stride)
+    prob = _split_problem(rank, v, v.shape[-2], v.shape[-1], v.shape[-1], sp, out_sp, kernel_size, dilation,
+                          stride, is_causal, None)
+    d_attn = torch.empty(attn.shape, dtype=attn.dtype, device=attn.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    lib = _lib.load()
+    L = lambda t: _byref(_lib.layout(t, rank, 1))  # noqa: E731
+    with torch.cuda.device(v.device):
+        rc = lib.natten_hip_av_backward(
+            _byref(prob), _lib.ptr(d_out), L(d_out), _lib.ptr(attn), L(attn), _lib.ptr(v), L(v),
+            _lib.ptr(d_attn), L(d_attn), _lib.ptr(dv), L(dv), _lib.stream_of(v))
+    _lib.check(rc, "av_backward")
+    return d_attn, dv
+
+
+def neighborhood_map(rank: int, spatial: Sequence[int], kernel_size, dilation, stride, is_causal,
+                     device=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The fused op's flattened neighbour map ``[*sp_out, KV]`` (int64) and
+    validity (bool), computed by the device kernel."""
+    device = torch.device("cuda") if device is None else torch.device(device)
+    out_sp = [_ceil_div(n, s) for n, s in zip(spatial, stride)]
+    kv = 1
+    for x in kernel_size:
+        kv *= x
+    prob = _lib.problem(batch=1, heads_q=1, heads_kv=1, dim_qk=1, dim_v=1, dtype=_lib.F32, length=spatial,
+                        out_length=out_sp, kernel_size=kernel_size, dilation=dilation, stride=stride,
+                        is_causal=is_causal, scale=None)
+    flat = torch.empty((*out_sp, kv), dtype=torch.int64, device=device)
+    valid = torch.empty((*out_sp, kv), dtype=torch.uint8, device=device)
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        rc = lib.natten_hip_neighborhood_map(_byref(prob), _lib.ptr(flat), _lib.ptr(valid),
+                                             ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
+    _lib.check(rc, "neighborhood_map")
+    return flat, valid.bool()
+
+
+# ---------------------------------------------------------------------------
+# rank-specific names (the backend-module contract)
+# ---------------------------------------------------------------------------
+
+
+def _bind(rank: int) -> None:
+    g = globals()
+
+    def fwd(q, k, v, kernel_size, stride, dilation, is_causal, scale):
+        return forward(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale)
+
+    def fwd_lse(q, k, v, kernel_size, stride, dilation, is_causal, scale):
+        return forward_with_lse(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale)
+
+    def fbwd(d_out, q, k, v, out, lse, kernel_size, dilation, stride, is_causal, scale, d_lse=None):
+        return fused_backward(rank, d_out, q, k, v, out, lse, kernel_size, dilation, stride, is_causal, scale, d_lse)
+
+    def qk(q, k, kernel_size, dilation, stride=(1,) * rank, is_causal=(False,) * rank, scale=None):
+        return qk_forward(rank, q, k, kernel_size, dilation, stride, is_causal, scale)
+
+    def av(attn, v, kernel_size, dilation, stride=(1,) * rank, is_causal=(False,) * rank):
+        return av_forward(rank, attn, v, kernel_size, dilation, stride, is_causal)
+
+    def qkb(d_attn, q, k, kernel_size, dilation, stride=(1,) * rank, is_causal=(False,) * rank, scale=None):
+        return qk_backward(rank, d_attn, q, k, kernel_size, dilation, stride, is_causal, scale)
+
+    def avb(d_out, attn, v, kernel_size, dilation, stride=(1,) * rank, is_causal=(False,) * rank):
+        return av_backward(rank, d_out, attn, v, kernel_size, dilation, stride, is_causal)
+
+    for suffix, fn in (("forward", fwd), ("forward_with_lse", fwd_lse), ("fused_backward", fbwd),
+                       ("qk_forward", qk), ("av_forward", av), ("qk_backward", qkb), ("av_backward", avb)):
+        name = f"na{rank}d_{suffix}"
+        fn.__name__ = fn.__qualname__ = name
+        g[name] = fn
+
+
+for _r in (1, 2, 3):
+    _bind(_r)
+del _r

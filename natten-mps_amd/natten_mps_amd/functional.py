@@ -1,0 +1,323 @@
+"""Functional neighbourhood-attention API (``functional.py:1-675`` of
+/root/reference/src/natten_mps): ``na1d/na2d/na3d``, ``na{1,2,3}d_qk`` and
+``na{1,2,3}d_av``, with the same arguments, validation, defaults and
+composition:
+
+* GQA/MQA: K/V may have fewer heads; query head h uses kv head
+  ``h // (Hq/Hkv)`` (the reference's ``repeat_interleave``, ``:27-31``).
+  Backends that declare ``NATIVE_GQA`` receive the un-expanded K/V.
+* Full-window fast path: kernel >= every spatial dim, stride 1, non-causal ->
+  ``F.scaled_dot_product_attention`` (``:148-206``).
+* ``return_lse`` / ``additional_keys`` (``:285-299``): NA output and LSE, plus
+  dense attention over the extra tokens, merged with ``merge_attentions``.
+  Backends that declare ``FUSED_LSE`` produce the NA output and LSE in one
+  fused pass (differentiable through both); others use the reference's
+  split QK -> logsumexp/softmax -> AV composition.
+* A backend named ``'pure'`` (a differentiable torch backend) is called
+  directly, bypassing the autograd Functions (``:301-302``).
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple, Union
+
+import torch
+import torch.nn.functional as F
+
+from natten_mps_amd._core import ops
+from natten_mps_amd.autograd import na1d as _ag1, na2d as _ag2, na3d as _ag3
+from natten_mps_amd.utils.params import (
+    check_dilation_kernel_vs_input,
+    check_kernel_size_vs_input,
+    check_stride_vs_kernel,
+    normalize_kernel_size,
+    normalize_tuple_param,
+)
+
+_AG = {1: _ag1, 2: _ag2, 3: _ag3}
+_LAYOUTS = {1: "[B, L, H, D]", 2: "[B, H, W, heads, dim]", 3: "[B, D, H, W, heads, dim]"}
+
+
+def _normalize_is_causal(is_causal, rank: int) -> tuple:
+    return tuple(bool(v) for v in normalize_tuple_param(is_causal, rank, "is_causal"))
+
+
+def _repeat_kv(x: torch.Tensor, n_rep: int) -> torch.Tensor:
+    """Expand KV heads to the query heads (GQA/MQA)."""
+    return x if n_rep == 1 else x.repeat_interleave(n_rep, dim=-2)
+
+
+def _validate_qkv(query, key, value, rank: int) -> int:
+    """Shape checks with GQA; returns the kv repeat factor (``:34-71``)."""
+    nd = rank + 3
+    if query.ndim != nd or key.ndim != nd or value.ndim != nd:
+        raise ValueError(f"na{rank}d expects query/key/value with shape {_LAYOUTS[rank]}.")
+    sq, sk, sv = query.shape[1:-2], key.shape[1:-2], value.shape[1:-2]
+    if sq != sk or sq != sv:
+        raise ValueError(f"Spatial dimensions must match: Q={sq}, K={sk}, V={sv}.")
+    if query.shape[0] != key.shape[0] or query.shape[0] != value.shape[0]:
+        raise ValueError("Batch dimensions must match.")
+    hq, dq = query.shape[-2], query.shape[-1]
+    hkv, dk = key.shape[-2], key.shape[-1]
+    if dq != dk:
+        raise ValueError(f"Head dim must match between Q and K: Q has {dq}, K has {dk}.")
+    if key.shape[-2] != value.shape[-2]:
+        raise ValueError(f"K and V must have same number of heads: K={key.shape[-2]}, V={value.shape[-2]}.")
+    if hq % hkv != 0:
+        raise ValueError(f"heads_q ({hq}) must be divisible by heads_kv ({hkv}) for GQA.")
+    return hq // hkv
+
+
+def _validate_additional_kv(query, additional_keys, additional_values, kv_repeat):
+    """Checks and GQA-expands the extra tokens (``:113-145``)."""
+    if additional_keys is None and additional_values is None:
+        return None, None
+    if additional_keys is None or additional_values is None:
+        raise ValueError("additional_keys and additional_values must both be provided or both None.")
+    ak, av = additional_keys, additional_values
+    if ak.ndim != 4 or av.ndim != 4:
+        raise ValueError("additional_keys/additional_values must be 4D: [B, N_extra, heads_kv, dim].")
+    if ak.shape[0] != query.shape[0]:
+        raise ValueError("additional_keys batch must match query batch.")
+    if av.shape[0] != query.shape[0]:
+        raise ValueError("additional_values batch must match query batch.")
+    if ak.shape[-1] != query.shape[-1]:
+        raise ValueError("additional_keys head dim must match query head dim.")
+    if av.shape[-1] != query.shape[-1]:
+        raise ValueError("additional_values head dim must match query head dim.")
+    if ak.shape[-2] != av.shape[-2]:
+        raise ValueError("additional_keys and additional_values must have same number of heads.")
+    if ak.shape[1] != av.shape[1]:
+        raise ValueError("additional_keys and additional_values must have same N_extra.")
+    return _repeat_kv(ak, kv_repeat), _repeat_kv(av, kv_repeat)
+
+
+def _full_attn_with_lse(query, key, value, scale: float):
+    """Dense attention of every query over ``key/value [B, N, H, D]`` with its
+    LSE ``[B, *spatial, H]`` (``:74-110``)."""
+    sp = query.shape[1:-2]
+    B, H, D = query.shape[0], query.shape[-2], query.shape[-1]
+    S = 1
+    for s in sp:
+        S *= s
+    q_t = query.reshape(B, S, H, D).permute(0, 2, 1, 3)
+    k_t = key.permute(0, 2, 3, 1).contiguous()          # [B, H, D, N]
+    logits = torch.matmul(q_t, k_t) * scale              # [B, H, S, N]
+    lse = torch.logsumexp(logits, dim=-1)
+    attn = torch.softmax(logits, dim=-1)
+    out = torch.matmul(attn, value.permute(0, 2, 1, 3).contiguous())
+    out = out.permute(0, 2, 1, 3).reshape(B, *sp, H, value.shape[-1])
+    lse = lse.permute(0, 2, 1).reshape(B, *sp, H)
+    return out, lse
+
+
+def _is_full_attention(kernel_size, spatial_shape) -> bool:
+    return all(k >= s for k, s in zip(kernel_size, spatial_shape))
+
+
+def _sdpa_forward(query, key, value, scale, spatial_shape, return_lse=False,
+                  additional_keys=None, additional_values=None):
+    """Kernel covering the whole input: plain attention (``:148-206``)."""
+    B, H, D = query.shape[0], query.shape[-2], query.shape[-1]
+    S = 1
+    for s in spatial_shape:
+        S *= s
+    k_all = key.reshape(B, S, H, D)
+    v_all = value.reshape(B, S, H, value.shape[-1])
+    if additional_keys is not None:
+        k_all = torch.cat([k_all, additional_keys], dim=1)
+        v_all = torch.cat([v_all, additional_values], dim=1)
+    q_t = query.reshape(B, -1, H, D).permute(0, 2, 1, 3)
+    k_t = k_all.permute(0, 2, 1, 3)
+    v_t = v_all.permute(0, 2, 1, 3)
+    out = F.scaled_dot_product_attention(q_t, k_t, v_t, scale=scale)
+    out = out.permute(0, 2, 1, 3).reshape(B, *spatial_shape, H, value.shape[-1])
+    if return_lse:
+        logits = torch.matmul(q_t, k_t.transpose(-2, -1).contiguous()) * scale
+        lse = torch.logsumexp(logits, dim=-1).permute(0, 2, 1).reshape(B, *spatial_shape, H)
+        return out, lse
+    return out
+
+
+def _using_pure_backend() -> bool:
+    return ops.get_backend() == "pure"
+
+
+def _na(rank, query, key, value, kernel_size, stride, dilation, is_causal, scale, return_lse,
+        additional_keys, additional_values):
+    kv_repeat = _validate_qkv(query, key, value, rank)
+    add_k, add_v = _validate_additional_kv(query, additional_keys, additional_values, kv_repeat)
+    ks = normalize_kernel_size(kernel_size, rank)
+    st = normalize_tuple_param(stride, rank, "stride")
+    dil = normalize_tuple_param(dilation, rank, "dilation")
+    causal = _normalize_is_causal(is_causal, rank)
+    spatial = tuple(query.shape[1:1 + rank])
+    check_kernel_size_vs_input(ks, spatial)
+    check_stride_vs_kernel(st, ks)
+    check_dilation_kernel_vs_input(dil, ks, spatial)
+    scale_value = query.shape[-1] ** -0.5 if scale is None else float(scale)
+
+    if _is_full_attention(ks, spatial) and all(s == 1 for s in st) and not any(causal):
+        return _sdpa_forward(query, _repeat_kv(key, kv_repeat), _repeat_kv(value, kv_repeat), scale_value,
+                             spatial, return_lse=return_lse, additional_keys=add_k, additional_values=add_v)
+
+    pure = _using_pure_backend()
+    mod = ops.active_module()
+    native_gqa = bool(getattr(mod, "NATIVE_GQA", False)) and not pure
+    if native_gqa:
+        k_in, v_in = key, value
+    else:
+        k_in, v_in = _repeat_kv(key, kv_repeat), _repeat_kv(value, kv_repeat)
+    has_additional = add_k is not None
+    ag = _AG[rank]
+
+    if has_additional or return_lse:
+        if getattr(mod, "FUSED_LSE", False) and not pure:
+            fn = getattr(ag, f"NeighborhoodAttention{rank}DLSEFunction")
+            out, lse = fn.apply(query, k_in, v_in, ks, st, dil, causal, scale_value)
+            if not has_additional:
+                lse = lse.to(query.dtype)
+        else:
+            qk = globals()[f"na{rank}d_qk"]
+            av = globals()[f"na{rank}d_av"]
+            logits = qk(query, k_in, kernel_size=ks, dilation=dil, stride=st, is_causal=causal)
+            logits_scaled = logits * scale_value
+            lse = torch.logsumexp(logits_scaled, dim=-1)
+            attn = torch.softmax(logits_scaled, dim=-1)
+            out = av(attn, v_in, kernel_size=ks, dilation=dil, stride=st, is_causal=causal)
+        if has_additional:
+            from natten_mps_amd.merge import merge_attentions
+            out_extra, lse_extra = _full_attn_with_lse(query, add_k, add_v, scale_value)
+            out, lse = merge_attentions([out, out_extra], [lse, lse_extra])
+        if return_lse:
+            return out, lse
+        return out
+
+    if pure:
+        return getattr(ops, f"na{rank}d_forward")(query, k_in, v_in, ks, st, dil, causal, scale_value)
+    fn = getattr(ag, f"NeighborhoodAttention{rank}DFunction")
+    return fn.apply(query, k_in, v_in, ks, st, dil, causal, scale_value)
+
+
+def na1d(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+         kernel_size: Union[int, Tuple[int]], stride: Union[int, Tuple[int]] = 1,
+         dilation: Union[int, Tuple[int]] = 1, is_causal: Union[bool, Tuple[bool]] = False,
+         scale: Optional[float] = None, return_lse: bool = False,
+         additional_keys: Optional[torch.Tensor] = None, additional_values: Optional[torch.Tensor] = None):
+    """1-D neighbourhood attention over ``[B, L, H, D]`` (``functional.py:213-303``).
+
+    Returns ``[B, L_out, H_q, D]`` (``L_out = ceil(L/stride)``), or
+    ``(out, lse)`` with ``lse`` ``[B, L_out, H_q]`` when ``return_lse``."""
+    return _na(1, query, key, value, kernel_size, stride, dilation, is_causal, scale, return_lse,
+               additional_keys, additional_values)
+
+
+def na2d(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+         kernel_size: Union[int, Tuple[int, int]], stride: Union[int, Tuple[int, int]] = 1,
+         dilation: Union[int, Tuple[int, int]] = 1, is_causal: Union[bool, Tuple[bool, bool]] = False,
+         scale: Optional[float] = None, return_lse: bool = False,
+         additional_keys: Optional[torch.Tensor] = None, additional_values: Optional[torch.Tensor] = None):
+    """2-D neighbourhood attention over ``[B, H, W, heads, dim]`` (``functional.py:306-394``)."""
+    return _na(2, query, key, value, kernel_size, stride, dilation, is_causal, scale, return_lse,
+               additional_keys, additional_values)
+
+
+def na3d(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+         kernel_size: Union[int, Tuple[int, int, int]], stride: Union[int, Tuple[int, int, int]] = 1,
+         dilation: Union[int, Tuple[int, int, int]] = 1,
+         is_causal: Union[bool, Tuple[bool, bool, bool]] = False,
+         scale: Optional[float] = None, return_lse: bool = False,
+         additional_keys: Optional[torch.Tensor] = None, additional_values: Optional[torch.Tensor] = None):
+    """3-D neighbourhood attention over ``[B, D, H, W, heads, dim]`` (``functional.py:522-611``)."""
+    return _na(3, query, key, value, kernel_size, stride, dilation, is_causal, scale, return_lse,
+               additional_keys, additional_values)
+
+
+# ---------------------------------------------------------------------------
+# split ops (functional.py:397-519, 614-675)
+# ---------------------------------------------------------------------------
+
+
+def _qk(rank, query, key, kernel_size, dilation, stride, is_causal, scale):
+    if query.ndim != rank + 3 or key.ndim != rank + 3:
+        raise ValueError(f"na{rank}d_qk expects query/key with shape {_LAYOUTS[rank]}.")
+    if query.shape != key.shape:
+        raise ValueError(f"query and key must share the same shape in na{rank}d_qk.")
+    ks = normalize_kernel_size(kernel_size, rank)
+    dil = normalize_tuple_param(dilation, rank, "dilation")
+    st = normalize_tuple_param(stride, rank, "stride")
+    causal = _normalize_is_causal(is_causal, rank)
+    spatial = tuple(query.shape[1:1 + rank])
+    check_kernel_size_vs_input(ks, spatial)
+    check_dilation_kernel_vs_input(dil, ks, spatial)
+    if _using_pure_backend():
+        return getattr(ops, f"na{rank}d_qk_forward")(query, key, ks, dil, st, causal, scale)
+    return getattr(_AG[rank], f"NA{rank}DQKFunction").apply(query, key, ks, dil, st, causal, scale)
+
+
+def _av(rank, attn, value, kernel_size, dilation, stride, is_causal):
+    if attn.ndim != rank + 3:
+        raise ValueError(f"na{rank}d_av expects attn with shape [B, *spatial, heads, K].")
+    if value.ndim != rank + 3:
+        raise ValueError(f"na{rank}d_av expects value with shape {_LAYOUTS[rank]}.")
+    if attn.shape[0] != value.shape[0] or attn.shape[-2] != value.shape[-2]:
+        raise ValueError(f"na{rank}d_av requires attn/value to match on batch and heads dimensions.")
+    if any(a > v for a, v in zip(attn.shape[1:1 + rank], value.shape[1:1 + rank])):
+        raise ValueError(f"na{rank}d_av attn spatial size cannot exceed value spatial size.")
+    ks = normalize_kernel_size(kernel_size, rank)
+    dil = normalize_tuple_param(dilation, rank, "dilation")
+    st = normalize_tuple_param(stride, rank, "stride")
+    causal = _normalize_is_causal(is_causal, rank)
+    vol = 1
+    for k in ks:
+        vol *= k
+    if attn.shape[-1] != vol:
+        raise ValueError(f"na{rank}d_av attn last dim ({attn.shape[-1]}) must match kernel volume ({vol}).")
+    spatial = tuple(value.shape[1:1 + rank])
+    check_kernel_size_vs_input(ks, spatial)
+    check_dilation_kernel_vs_input(dil, ks, spatial)
+    if _using_pure_backend():
+        return getattr(ops, f"na{rank}d_av_forward")(attn, value, ks, dil, st, causal)
+    return getattr(_AG[rank], f"NA{rank}DAVFunction").apply(attn, value, ks, dil, st, causal)
+
+
+def na1d_qk(query, key, kernel_size, dilation=1, *, stride=1, is_causal=False, scale=None):
+    """Unscaled (unless ``scale``) logits ``[B, L_out, H, K]``; causal-invalid entries are -inf."""
+    return _qk(1, query, key, kernel_size, dilation, stride, is_causal, scale)
+
+
+def na2d_qk(query, key, kernel_size, dilation=1, *, stride=1, is_causal=False, scale=None):
+    """Logits ``[B, H_out, W_out, heads, kh*kw]``."""
+    return _qk(2, query, key, kernel_size, dilation, stride, is_causal, scale)
+
+
+def na3d_qk(query, key, kernel_size, dilation=1, *, stride=1, is_causal=False, scale=None):
+    """Logits ``[B, D_out, H_out, W_out, heads, kd*kh*kw]``."""
+    return _qk(3, query, key, kernel_size, dilation, stride, is_causal, scale)
+
+
+def na1d_av(attn, value, kernel_size, dilation=1, *, stride=1, is_causal=False):
+    """``out = sum_k attn_k v_k`` over each neighbourhood."""
+    return _av(1, attn, value, kernel_size, dilation, stride, is_causal)
+
+
+def na2d_av(attn, value, kernel_size, dilation=1, *, stride=1, is_causal=False):
+    return _av(2, attn, value, kernel_size, dilation, stride, is_causal)
+
+
+def na3d_av(attn, value, kernel_size, dilation=1, *, stride=1, is_causal=False):
+    return _av(3, attn, value, kernel_size, dilation, stride, is_causal)
+
+
+# ---------------------------------------------------------------------------
+# variable-length attention: not part of this build
+# ---------------------------------------------------------------------------
+
+
+def _varlen_unsupported(*_args, **_kwargs):
+    raise NotImplementedError(
+        "variable-length neighborhood attention (na{1,2,3}d_varlen) is not implemented by natten_mps_amd; "
+        "pad to a common size and call na1d/na2d/na3d per size group."
+    )
+
+
+na1d_varlen = na2d_varlen = na3d_varlen = _varlen_unsupported

@@ -1,0 +1,105 @@
+"""The C-ABI library without a GPU: it loads, exports every entry point
+include/natten_hip.h declares, its structs have the layout the ctypes binding
+assumes, and argument validation (host code that runs before any launch)
+returns the documented status codes."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+from natten_mps_amd._core import _lib
+
+HEADER = os.path.join(ROOT, "include", "natten_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(natten_hip_\w+)\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.is_built():
+        pytest.fail("libnatten_hip.so is not built (run python natten-mps_amd/build_lib.py)")
+    return _lib.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    declared = _declared()
+    assert len(declared) >= 9
+    assert set(declared) == set(_lib.ENTRY_POINTS)
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (natten_hip_\w+)", out))
+    assert set(declared) <= exported
+    assert lib.natten_hip_abi_version() == _lib.ABI_VERSION
+
+
+def test_struct_layout_matches_header(tmp_path):
+    src = tmp_path / "probe.c"
+    src.write_text(r'''
+#include <stddef.h>
+#include <stdio.h>
+#include "natten_hip.h"
+int main(void) {
+  printf("%zu %zu %zu %zu %zu %zu\n", sizeof(natten_problem_t), offsetof(natten_problem_t, scale),
+         offsetof(natten_problem_t, length), offsetof(natten_problem_t, causal),
+         sizeof(natten_layout_t), offsetof(natten_layout_t, head));
+  return 0;
+}
+''')
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-I" + os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    P, L = _lib.Problem, _lib.Layout
+    assert got == [ctypes.sizeof(P), P.scale.offset, P.length.offset, P.causal.offset, ctypes.sizeof(L),
+                   L.head.offset]
+
+
+def _prob(**over):
+    kw = dict(batch=1, heads_q=2, heads_kv=2, dim_qk=8, dim_v=8, dtype=_lib.F32, length=(16,), out_length=(16,),
+              kernel_size=(5,), dilation=(1,), stride=(1,), is_causal=(False,), scale=0.5)
+    kw.update(over)
+    return _lib.problem(**kw)
+
+
+@pytest.mark.parametrize("over, code, text", [
+    (dict(kernel_size=(5,), dilation=(4,)), 1, "exceeds length"),
+    (dict(heads_q=3, heads_kv=2), 1, "divisible"),
+    (dict(dim_qk=300, dim_v=300), 2, "above 256"),
+    (dict(out_length=(8,)), 1, "query extent"),
+    (dict(length=(6,), out_length=(6,), kernel_size=(6,)), 2, "even kernel"),
+    (dict(dtype=7), 1, "dtype"),
+    (dict(batch=0), 1, "batch"),
+])
+def test_validation_codes(lib, over, code, text):
+    lay = ctypes.byref(_lib.Layout())
+    dummy = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    rc = lib.natten_hip_forward(ctypes.byref(_prob(**over)), dummy, lay, dummy, lay, dummy, lay, dummy, lay,
+                                dummy, lay, None)
+    assert rc == code
+    assert text in lib.natten_hip_last_error().decode()
+
+
+def test_null_operand_rejected(lib):
+    lay = ctypes.byref(_lib.Layout())
+    rc = lib.natten_hip_forward(ctypes.byref(_prob()), None, lay, None, lay, None, lay, None, lay, None, lay, None)
+    assert rc == 1 and "NULL" in lib.natten_hip_last_error().decode()
+
+
+def test_split_ops_need_equal_heads(lib):
+    lay = ctypes.byref(_lib.Layout())
+    d = ctypes.c_void_p(16)
+    rc = lib.natten_hip_qk_forward(ctypes.byref(_prob(heads_q=4, heads_kv=2)), d, lay, d, lay, d, lay, None)
+    assert rc == 1 and "heads_q == heads_kv" in lib.natten_hip_last_error().decode()
+
+
+def test_python_errors_map_to_exceptions(lib):
+    with pytest.raises(ValueError, match="exceeds length"):
+        _lib.check(lib.natten_hip_forward(ctypes.byref(_prob(dilation=(4,))), *([ctypes.c_void_p(16),
+                   ctypes.byref(_lib.Layout())] * 5), None), "forward")

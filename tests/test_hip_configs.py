@@ -1,0 +1,123 @@
+"""The five BASELINE configurations on the 'hip' backend at their full sizes.
+
+Inputs: ``torch.Generator().manual_seed(1000 + cfg)``, order q, k, v, dO, each
+``randn`` in fp32 then cast.  The oracle is evaluated where it is exact and
+affordable on the host:
+
+* cfg 1, 2: the whole problem (cfg 1 also against the reference's golden output);
+* cfg 3: batch items 0-1 (batch items are independent);
+* cfg 4: batch item 0, the prefix of 2048 positions (a causal 1-D window never
+  reaches forward, so a prefix is self-contained; dK/dV are compared where
+  every contributing query lies in the prefix);
+* cfg 5: batch item 0, head 0 (heads are independent, Hq == Hkv).
+
+bf16 tolerance 2e-2 (the oracle runs in fp32 on the same bf16 inputs); fp32 1e-5.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle.pure as P
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0") if torch.cuda.is_available() else None
+
+
+@pytest.fixture(autouse=True)
+def _hip():
+    import natten_mps_amd
+
+    natten_mps_amd.set_backend("hip")
+
+
+def _seeded(cfg, shapes, dtype):
+    g = torch.Generator().manual_seed(1000 + cfg)
+    return [torch.randn(s, generator=g, dtype=torch.float32).to(dtype) for s in shapes]
+
+
+def _run(fn, q, k, v, do, **kw):
+    leaves = [t.to(DEV).requires_grad_(True) for t in (q, k, v)]
+    out = fn(*leaves, **kw)
+    out.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    return out.detach().cpu(), [t.grad.cpu() for t in leaves]
+
+
+def _oracle(rank, q, k, v, do, ks, st, dil, causal):
+    leaves = [t.float().clone().requires_grad_(True) for t in (q, k, v)]
+    out = P.forward(rank, *leaves, ks, st, dil, causal, None)
+    out.backward(do.float())
+    return out.detach(), [t.grad for t in leaves]
+
+
+def _close(a, b, tol, name):
+    torch.testing.assert_close(a.float(), b.float(), atol=tol, rtol=tol, msg=lambda m: f"{name}: {m}")
+
+
+def test_config1_na1d_fp32(golden):
+    from natten_mps_amd import functional as F
+
+    q, k, v = _seeded(1, [(2, 128, 4, 32)] * 3, torch.float32)
+    out = F.na1d(q.to(DEV), k.to(DEV), v.to(DEV), kernel_size=7, scale=32 ** -0.5).cpu()
+    _close(out, golden.tensor("cfg1/out"), 1e-5, "cfg1 out")
+
+
+@pytest.mark.parametrize("causal", [(False, False), (True, False)])
+def test_config2_na2d_fp32(causal):
+    from natten_mps_amd import functional as F
+
+    q, k, v, do = _seeded(2, [(2, 32, 32, 4, 32)] * 4, torch.float32)
+    out, grads = _run(F.na2d, q, k, v, do, kernel_size=7, is_causal=causal)
+    ref, rgrads = _oracle(2, q, k, v, do, (7, 7), (1, 1), (1, 1), causal)
+    _close(out, ref, 1e-5, "out")
+    for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
+        _close(a, b, 1e-5, n)
+
+
+@pytest.mark.parametrize("dil", [1, 8])
+def test_config3_na2d_bf16(dil):
+    from natten_mps_amd import functional as F
+
+    q, k, v, do = _seeded(3, [(16, 56, 56, 4, 32)] * 4, torch.bfloat16)
+    out, grads = _run(F.na2d, q, k, v, do, kernel_size=7, dilation=dil)
+    sl = slice(0, 2)
+    ref, rgrads = _oracle(2, q[sl], k[sl], v[sl], do[sl], (7, 7), (1, 1), (dil, dil), (False, False))
+    _close(out[sl], ref, 2e-2, "out")
+    for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
+        _close(a[sl], b, 2e-2, n)
+    # fused vs split QK -> softmax -> AV on the device, whole problem
+    qd, kd, vd = (t.to(DEV) for t in (q, k, v))
+    logits = F.na2d_qk(qd, kd, 7, dil) * 32 ** -0.5
+    split = F.na2d_av(torch.softmax(logits.float(), -1).to(torch.bfloat16), vd, 7, dil)
+    _close(split.cpu(), out, 2e-2, "fused vs split")
+
+
+@pytest.mark.parametrize("dil", [1, 4])
+def test_config4_na1d_gqa_causal_bf16(dil):
+    from natten_mps_amd import functional as F
+
+    q, k, v, do = _seeded(4, [(4, 16384, 8, 64), (4, 16384, 2, 64), (4, 16384, 2, 64), (4, 16384, 8, 64)],
+                          torch.bfloat16)
+    out, grads = _run(F.na1d, q, k, v, do, kernel_size=33, dilation=dil, is_causal=True)
+    n = 2048
+    ref, rgrads = _oracle(1, q[:1, :n], k[:1, :n], v[:1, :n], do[:1, :n], (33,), (1,), (dil,), (True,))
+    _close(out[:1, :n], ref, 2e-2, "out")
+    _close(grads[0][:1, :n], rgrads[0], 2e-2, "dq")
+    m = n - 32 * dil
+    _close(grads[1][:1, :m], rgrads[1][:, :m], 2e-2, "dk")
+    _close(grads[2][:1, :m], rgrads[2][:, :m], 2e-2, "dv")
+
+
+def test_config5_na3d_bf16():
+    from natten_mps_amd import functional as F
+
+    q, k, v, do = _seeded(5, [(2, 16, 32, 32, 8, 64)] * 4, torch.bfloat16)
+    ks, dil = (3, 7, 7), (1, 2, 2)
+    out, grads = _run(F.na3d, q, k, v, do, kernel_size=ks, dilation=dil)
+    sl = (slice(0, 1), Ellipsis, slice(0, 1), slice(None))
+    ref, rgrads = _oracle(3, q[sl], k[sl], v[sl], do[sl], ks, (1, 1, 1), dil, (False, False, False))
+    _close(out[sl], ref, 2e-2, "out")
+    for n_, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
+        _close(a[sl], b, 2e-2, n_)

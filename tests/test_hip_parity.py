@@ -1,0 +1,362 @@
+"""Parity of the 'hip' backend (gfx950 kernels through the C ABI) with the CPU
+oracle on identical seeded inputs.
+
+Tolerances (north star): fp32 outputs and gradients within 1e-5 abs/rel;
+bf16 / fp16 within 2e-2 (compared with the oracle evaluated in fp32 on the
+same rounded inputs, and for bf16 also with the oracle evaluated in bf16);
+index maps bit-exact.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle.pure as P
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0") if torch.cuda.is_available() else None
+
+
+@pytest.fixture(autouse=True)
+def _hip():
+    import natten_mps_amd
+
+    natten_mps_amd.set_backend("hip")
+    yield
+
+
+def _tol(dtype):
+    return dict(atol=1e-5, rtol=1e-5) if dtype == torch.float32 else dict(atol=2e-2, rtol=2e-2)
+
+
+def _inputs(seed, shapes, dtype):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(s, generator=g, dtype=torch.float32).to(dtype) for s in shapes]
+
+
+def _hip_fwd_bwd(fn, tensors, do, **kw):
+    leaves = [t.to(DEV).requires_grad_(True) for t in tensors]
+    out = fn(*leaves, **kw)
+    out.backward(do.to(DEV))
+    return out.detach().cpu(), [t.grad.cpu() for t in leaves]
+
+
+def _oracle_fwd_bwd(rank, tensors, do, ks, st, dil, causal, scale=None, dtype=torch.float32):
+    leaves = [t.to(dtype).clone().requires_grad_(True) for t in tensors]
+    out = P.forward(rank, *leaves, ks, st, dil, causal, scale)
+    out.backward(do.to(dtype))
+    return out.detach(), [t.grad for t in leaves]
+
+
+def _close(a, b, dtype, name=""):
+    torch.testing.assert_close(a.float(), b.float(), **_tol(dtype), msg=lambda m: f"{name}: {m}")
+
+
+# ---------------------------------------------------------------------------
+# availability and index maps
+# ---------------------------------------------------------------------------
+
+
+def test_backend_is_hip_and_library_loaded():
+    import natten_mps_amd
+    from natten_mps_amd._core import _lib, hip
+
+    assert hip.is_available()
+    natten_mps_amd.set_backend("auto")
+    assert natten_mps_amd.get_backend() == "hip"
+    assert _lib.load().natten_hip_abi_version() == _lib.ABI_VERSION
+
+
+MAP_CASES = [
+    ((37,), (5,), (3,), (2,), (True,)),
+    ((10, 12), (5, 3), (2, 1), (2, 3), (True, False)),
+    ((56, 56), (7, 7), (8, 8), (1, 1), (False, False)),
+    ((56, 56), (7, 7), (1, 1), (1, 1), (False, False)),
+    ((5, 6, 7), (3, 3, 3), (1, 1, 2), (2, 1, 1), (True, True, True)),
+    ((16, 32, 32), (3, 7, 7), (1, 2, 2), (1, 1, 1), (False, False, False)),
+    ((16384,), (33,), (4,), (1,), (True,)),
+]
+
+
+@pytest.mark.parametrize("case", MAP_CASES)
+def test_neighborhood_map_bit_exact(case):
+    from natten_mps_amd._core import hip
+
+    spatial, ks, dil, st, causal = case
+    rank = len(spatial)
+    flat, valid = hip.neighborhood_map(rank, spatial, ks, dil, st, causal, DEV)
+    ref_flat, ref_valid = P.neighborhood(rank, spatial, ks, dil, st, causal)
+    assert torch.equal(flat.cpu().reshape(ref_flat.shape), ref_flat)
+    if ref_valid is None:
+        assert bool(valid.all())
+    else:
+        assert torch.equal(valid.cpu().reshape(ref_valid.shape), ref_valid)
+
+
+# ---------------------------------------------------------------------------
+# fused forward + backward
+# ---------------------------------------------------------------------------
+
+FUSED = [
+    # rank, spatial, hq, hkv, dim, ks, st, dil, causal, scale
+    (1, (37,), 2, 2, 16, (5,), (1,), (1,), (False,), None),
+    (1, (37,), 2, 2, 16, (5,), (1,), (3,), (True,), 0.3),
+    (1, (40,), 4, 2, 32, (7,), (2,), (2,), (False,), None),
+    (1, (41,), 2, 2, 17, (5,), (3,), (2,), (True,), None),
+    (1, (16,), 2, 2, 8, (4,), (1,), (1,), (False,), None),
+    (2, (12, 14), 2, 2, 32, (3, 5), (1, 1), (1, 2), (False, False), None),
+    (2, (12, 14), 4, 1, 16, (5, 5), (1, 1), (2, 1), (True, False), None),
+    (2, (12, 14), 2, 2, 64, (3, 3), (2, 1), (1, 1), (False, True), None),
+    (2, (11, 13), 2, 2, 24, (3, 5), (2, 3), (1, 2), (True, True), 0.5),
+    (2, (9, 9), 2, 2, 128, (7, 7), (1, 1), (1, 1), (False, False), None),
+    (2, (8, 8), 1, 1, 256, (3, 3), (1, 1), (2, 2), (False, False), None),
+    (3, (6, 7, 8), 2, 2, 32, (3, 3, 5), (1, 1, 1), (1, 2, 1), (False, False, False), None),
+    (3, (6, 7, 8), 4, 2, 16, (3, 3, 3), (1, 2, 1), (2, 1, 1), (False, True, False), None),
+    (3, (5, 6, 7), 2, 2, 8, (3, 3, 3), (1, 1, 2), (1, 1, 2), (True, True, True), None),
+]
+
+
+@pytest.mark.parametrize("case", FUSED)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_fused_forward_backward(case, dtype):
+    from natten_mps_amd import functional as F
+
+    rank, sp, hq, hkv, dim, ks, st, dil, causal, scale = case
+    if dtype != torch.float32 and dim > 64:
+        pytest.skip("half-precision covered at dim <= 64 here")
+    q, k, v = _inputs(11, [(2, *sp, hq, dim), (2, *sp, hkv, dim), (2, *sp, hkv, dim)], dtype)
+    out_sp = [(n + s - 1) // s for n, s in zip(sp, st)]
+    (do,) = _inputs(12, [(2, *out_sp, hq, dim)], dtype)
+    fn = getattr(F, f"na{rank}d")
+    out, grads = _hip_fwd_bwd(fn, (q, k, v), do, kernel_size=ks, stride=st, dilation=dil, is_causal=causal,
+                              scale=scale)
+    assert out.dtype == dtype
+    ref, rgrads = _oracle_fwd_bwd(rank, (q, k, v), do, ks, st, dil, causal, scale)
+    _close(out, ref, dtype, "out")
+    for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
+        _close(a, b, dtype, n)
+
+
+def test_lse_matches_logsumexp():
+    from natten_mps_amd._core import hip
+
+    q, k, v = _inputs(21, [(2, 10, 12, 2, 16)] * 3, torch.float32)
+    out, lse = hip.forward_with_lse(2, q.to(DEV), k.to(DEV), v.to(DEV), (3, 5), (1, 1), (2, 1), (True, False), None)
+    logits = P.na2d_qk_forward(q, k, (3, 5), (2, 1), (1, 1), (True, False), 16 ** -0.5)
+    torch.testing.assert_close(lse.cpu(), torch.logsumexp(logits, -1), atol=1e-5, rtol=1e-5)
+    assert lse.dtype == torch.float32 and lse.shape == (2, 10, 12, 2)
+
+
+def test_bf16_against_bf16_oracle():
+    """North-star definition: hip bf16 vs the oracle run in bf16 on the CPU."""
+    from natten_mps_amd import functional as F
+
+    q, k, v, do = _inputs(31, [(2, 16, 16, 4, 32)] * 4, torch.bfloat16)
+    out, grads = _hip_fwd_bwd(F.na2d, (q, k, v), do, kernel_size=7)
+    ref, rgrads = _oracle_fwd_bwd(2, (q, k, v), do, (7, 7), (1, 1), (1, 1), (False, False), dtype=torch.bfloat16)
+    _close(out, ref, torch.bfloat16, "out")
+    for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
+        _close(a, b, torch.bfloat16, n)
+
+
+def test_noncontiguous_views_from_module_layout():
+    """q/k/v as strided views of one qkv projection (the nn modules' layout)."""
+    from natten_mps_amd import functional as F
+
+    (x,) = _inputs(41, [(2, 9, 11, 3, 2, 32)], torch.float32)
+    (do,) = _inputs(42, [(2, 9, 11, 2, 32)], torch.float32)
+    xd = x.to(DEV).requires_grad_(True)
+    q, k, v = xd.permute(3, 0, 1, 2, 4, 5).unbind(0)
+    out = F.na2d(q, k, v, kernel_size=5, dilation=(1, 2))
+    out.backward(do.to(DEV))
+    xr = x.clone().requires_grad_(True)
+    qr, kr, vr = xr.permute(3, 0, 1, 2, 4, 5).unbind(0)
+    ref = P.na2d_forward(qr, kr, vr, (5, 5), (1, 1), (1, 2), (False, False), None)
+    ref.backward(do)
+    _close(out.detach().cpu(), ref.detach(), torch.float32, "out")
+    _close(xd.grad.cpu(), xr.grad, torch.float32, "dx")
+
+
+def test_dim_v_differs_from_dim_qk():
+    from natten_mps_amd._core import hip
+
+    q, k = _inputs(51, [(2, 20, 2, 16)] * 2, torch.float32)
+    (v,) = _inputs(52, [(2, 20, 2, 48)], torch.float32)
+    out, lse = hip.forward_with_lse(1, q.to(DEV), k.to(DEV), v.to(DEV), (5,), (1,), (2,), (False,), None)
+    logits = P.na1d_qk_forward(q, k, (5,), (2,), (1,), (False,), 16 ** -0.5)
+    ref = P.na1d_av_forward(torch.softmax(logits, -1), v, (5,), (2,), (1,), (False,))
+    _close(out.cpu(), ref, torch.float32, "out")
+
+
+# ---------------------------------------------------------------------------
+# split QK / AV
+# ---------------------------------------------------------------------------
+
+SPLIT = [
+    (1, (30,), (5,), (2,), (1,), (False,), None),
+    (1, (31,), (5,), (1,), (2,), (True,), 0.25),
+    (2, (9, 10), (3, 5), (1, 2), (1, 1), (True, False), None),
+    (2, (9, 10), (3, 3), (1, 1), (2, 2), (False, False), 0.7),
+    (3, (5, 6, 7), (3, 3, 3), (1, 2, 1), (1, 1, 2), (False, False, True), None),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_split_qk_av(case, dtype):
+    from natten_mps_amd import functional as F
+
+    rank, sp, ks, dil, st, causal, scale = case
+    q, k, v = _inputs(61, [(2, *sp, 2, 16)] * 3, dtype)
+    qk = getattr(F, f"na{rank}d_qk")
+    av = getattr(F, f"na{rank}d_av")
+    qd, kd = q.to(DEV).requires_grad_(True), k.to(DEV).requires_grad_(True)
+    logits = qk(qd, kd, ks, dil, stride=st, is_causal=causal, scale=scale)
+    ref_q, ref_k = q.float().requires_grad_(True), k.float().requires_grad_(True)
+    ref_logits = getattr(P, f"na{rank}d_qk_forward")(ref_q, ref_k, ks, dil, st, causal, scale)
+    finite = torch.isfinite(ref_logits)
+    assert torch.equal(torch.isfinite(logits.detach().cpu()), finite)
+    _close(logits.detach().cpu()[finite], ref_logits.detach()[finite], dtype, "logits")
+    (dl,) = _inputs(62, [tuple(ref_logits.shape)], dtype)
+    dl = torch.where(finite, dl, torch.zeros_like(dl))
+    logits.backward(dl.to(DEV))
+    ref_logits.backward(dl.float())
+    _close(qd.grad.cpu(), ref_q.grad, dtype, "dq")
+    _close(kd.grad.cpu(), ref_k.grad, dtype, "dk")
+
+    attn = torch.softmax(torch.where(finite, ref_logits.detach(), torch.full_like(ref_logits, -1e30)), -1)
+    ad, vd = attn.to(dtype).to(DEV).requires_grad_(True), v.to(DEV).requires_grad_(True)
+    out = av(ad, vd, ks, dil, stride=st, is_causal=causal)
+    ref_a, ref_v = attn.to(dtype).float().requires_grad_(True), v.float().requires_grad_(True)
+    ref_out = getattr(P, f"na{rank}d_av_forward")(ref_a, ref_v, ks, dil, st, causal)
+    _close(out.detach().cpu(), ref_out.detach(), dtype, "av out")
+    (do,) = _inputs(63, [tuple(ref_out.shape)], dtype)
+    out.backward(do.to(DEV))
+    ref_out.backward(do.float())
+    _close(ad.grad.cpu(), ref_a.grad, dtype, "dattn")
+    _close(vd.grad.cpu(), ref_v.grad, dtype, "dv")
+
+
+def test_fused_equals_split_composition():
+    """Reference check (tests/test_backward_parity.py): fused vs split QK ->
+    softmax -> AV, outputs and gradients."""
+    from natten_mps_amd import functional as F
+
+    q, k, v, do = (t.to(DEV) for t in _inputs(71, [(2, 12, 12, 4, 32)] * 4, torch.float32))
+    a = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    out = F.na2d(*a, kernel_size=5, dilation=2, is_causal=(False, True))
+    out.backward(do)
+    b = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    logits = F.na2d_qk(b[0], b[1], 5, 2, is_causal=(False, True)) * 32 ** -0.5
+    out2 = F.na2d_av(torch.softmax(logits, -1), b[2], 5, 2, is_causal=(False, True))
+    out2.backward(do)
+    torch.testing.assert_close(out, out2, atol=1e-5, rtol=1e-5)
+    for x, y in zip(a, b):
+        torch.testing.assert_close(x.grad, y.grad, atol=1e-5, rtol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# GQA, return_lse, additional_keys, modules
+# ---------------------------------------------------------------------------
+
+
+def test_gqa_native_matches_expanded():
+    from natten_mps_amd import functional as F
+
+    q, k, v, do = _inputs(81, [(2, 24, 8, 16), (2, 24, 2, 16), (2, 24, 2, 16), (2, 24, 8, 16)], torch.float32)
+    out, grads = _hip_fwd_bwd(F.na1d, (q, k, v), do, kernel_size=7, dilation=2, is_causal=True)
+    ref, rgrads = _oracle_fwd_bwd(1, (q, k, v), do, (7,), (1,), (2,), (True,))
+    _close(out, ref, torch.float32, "out")
+    for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
+        assert a.shape == b.shape
+        _close(a, b, torch.float32, n)
+
+
+def test_return_lse_and_additional_keys_match_oracle_composition(pure_backend):
+    """hip fused-with-LSE + merge vs the functional layer over the oracle
+    (itself pinned to the reference by the golden 'func' cases)."""
+    import natten_mps_amd
+    from natten_mps_amd import functional as F
+
+    q, k, v, ak, av, do = _inputs(91, [(2, 9, 10, 4, 16), (2, 9, 10, 2, 16), (2, 9, 10, 2, 16),
+                                       (2, 2, 2, 16), (2, 2, 2, 16), (2, 9, 10, 4, 16)], torch.float32)
+    (dl,) = _inputs(92, [(2, 9, 10, 4)], torch.float32)
+
+    def run(device):
+        leaves = [t.to(device).requires_grad_(True) for t in (q, k, v, ak, av)]
+        out, lse = F.na2d(*leaves[:3], kernel_size=3, dilation=(2, 1), return_lse=True,
+                          additional_keys=leaves[3], additional_values=leaves[4])
+        torch.autograd.backward([out, lse], [do.to(device), dl.to(device)])
+        return [out.detach().cpu(), lse.detach().cpu()] + [t.grad.cpu() for t in leaves]
+
+    ref = run("cpu")                       # oracle backend ('pure')
+    natten_mps_amd.set_backend("hip")
+    got = run(DEV)
+    for n, a, b in zip(("out", "lse", "dq", "dk", "dv", "dak", "dav"), got, ref):
+        _close(a, b, torch.float32, n)
+
+
+def test_return_lse_only():
+    from natten_mps_amd import functional as F
+
+    q, k, v = _inputs(93, [(1, 30, 2, 16)] * 3, torch.bfloat16)
+    out, lse = F.na1d(q.to(DEV), k.to(DEV), v.to(DEV), kernel_size=5, return_lse=True)
+    assert lse.dtype == torch.bfloat16 and lse.shape == (1, 30, 2)
+    logits = P.na1d_qk_forward(q.float(), k.float(), (5,), (1,), (1,), (False,), 16 ** -0.5)
+    _close(lse.cpu(), torch.logsumexp(logits, -1), torch.bfloat16, "lse")
+
+
+@pytest.mark.parametrize("rank", [1, 2, 3])
+def test_module_forward_backward(rank):
+    import natten_mps_amd
+
+    torch.manual_seed(0)
+    cls = getattr(natten_mps_amd, f"NeighborhoodAttention{rank}D")
+    m = cls(embed_dim=32, num_heads=4, kernel_size=3, num_kv_heads=2).to(DEV)
+    shape = {1: (2, 20, 32), 2: (2, 8, 9, 32), 3: (2, 5, 6, 7, 32)}[rank]
+    x = torch.randn(shape, device=DEV, requires_grad=True)
+    y = m(x)
+    y.sum().backward()
+    assert y.shape == x.shape and torch.isfinite(x.grad).all()
+    m_cpu = cls(embed_dim=32, num_heads=4, kernel_size=3, num_kv_heads=2)
+    m_cpu.load_state_dict({k_: t.cpu() for k_, t in m.state_dict().items()})
+    import oracle.pure as oracle_pure
+    from natten_mps_amd._core import ops
+    natten_mps_amd.register_backend("pure", oracle_pure)
+    try:
+        natten_mps_amd.set_backend("pure")
+        ref = m_cpu(x.detach().cpu())
+    finally:
+        ops.unregister_backend("pure")
+    _close(y.detach().cpu(), ref.detach(), torch.float32, "module out")
+
+
+def test_cpu_tensors_raise_with_hip_backend():
+    from natten_mps_amd import functional as F
+
+    q = torch.randn(1, 8, 2, 4)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        F.na1d(q, q, q, kernel_size=3)
+
+
+# ---------------------------------------------------------------------------
+# golden vectors from the reference, run through hip
+# ---------------------------------------------------------------------------
+
+
+def test_golden_fused_cases_on_hip(golden):
+    for c in golden.cases("fwd"):
+        p = c["key"]
+        dtype = getattr(torch, c["dtype"])
+        q, k, v, do = (golden.tensor(p + n) for n in ("q", "k", "v", "dout"))
+        from natten_mps_amd._core import hip
+        leaves = [t.to(DEV).requires_grad_(True) for t in (q, k, v)]
+        fn = getattr(hip, f"na{c['rank']}d_forward_with_lse")
+        args = (tuple(c["kernel_size"]), tuple(c["stride"]), tuple(c["dilation"]), tuple(c["is_causal"]), c["scale"])
+        out, lse = fn(*[t.detach() for t in leaves], *args)
+        dq, dk, dv = getattr(hip, f"na{c['rank']}d_fused_backward")(
+            do.to(DEV), *[t.detach() for t in leaves], out, lse, args[0], args[2], args[1], args[3],
+            float(q.shape[-1] ** -0.5 if c["scale"] is None else c["scale"]))
+        for n, a in (("out", out), ("dq", dq), ("dk", dk), ("dv", dv)):
+            _close(a.cpu(), golden.tensor(p + n), dtype, f"{p}{n}")

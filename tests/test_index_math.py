@@ -1,0 +1,184 @@
+"""Window rule and index maps: the oracle (Python and C), and the device index
+code (na_common.h, built for the host) against the reference's known answers,
+a textbook definition, brute force, and each other."""
+from __future__ import annotations
+
+import ctypes
+import itertools
+import os
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.pure as P
+from conftest import ROOT
+from natten_mps_amd._core import _lib
+
+BUILD = os.path.join(ROOT, "tests", "native", "_build")
+
+
+@pytest.fixture(scope="module")
+def host_idx():
+    os.makedirs(BUILD, exist_ok=True)
+    out = os.path.join(BUILD, "libindex_host.so")
+    subprocess.run(["/opt/rocm/bin/hipcc", "-O1", "-std=c++17", "-fPIC", "-shared",
+                    "-I" + os.path.join(ROOT, "include"), "-I" + os.path.join(ROOT, "natten-mps_amd", "csrc"),
+                    os.path.join(ROOT, "tests", "native", "index_host.cpp"), "-o", out], check=True)
+    lib = ctypes.CDLL(out)
+    lib.host_window_start.restype = ctypes.c_int
+    lib.host_window_start.argtypes = [ctypes.c_int] * 4
+    lib.host_neighbor_map.argtypes = [ctypes.POINTER(_lib.Problem), ctypes.c_void_p, ctypes.c_void_p]
+    lib.host_inverse_mismatch.argtypes = [ctypes.POINTER(_lib.Problem)]
+    lib.host_inverse_mismatch.restype = ctypes.c_longlong
+    return lib
+
+
+@pytest.fixture(scope="module")
+def c_oracle():
+    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
+    lib = ctypes.CDLL(os.path.join(ROOT, "oracle", "_build", "liboracle_window.so"))
+    lib.oracle_window_start.restype = ctypes.c_int64
+    lib.oracle_window_start.argtypes = [ctypes.c_int64] * 4
+    return lib
+
+
+def _problem(spatial, ks, dil, st, causal):
+    return _lib.problem(batch=1, heads_q=1, heads_kv=1, dim_qk=1, dim_v=1, dtype=_lib.F32, length=spatial,
+                        out_length=[(n + s - 1) // s for n, s in zip(spatial, st)], kernel_size=ks,
+                        dilation=dil, stride=st, is_causal=causal, scale=None)
+
+
+def _sweep_starts(maxL=30):
+    for L in range(1, maxL + 1):
+        for K in range(1, L + 1):
+            for d in range(1, L // K + 1):
+                yield L, K, d
+
+
+# -- window start ---------------------------------------------------------
+
+
+def test_known_answers():
+    # tests/test_shift_semantics.py:66-99 of the reference
+    assert P.window_start(0, 10, 3, 1) == 0
+    assert P.window_start(9, 10, 3, 1) == 7
+    assert P.window_start(5, 11, 5, 1) == 3
+    for i in range(20):
+        s = P.window_start(i, 20, 3, 2)
+        assert 0 <= s and s + 2 * 2 <= 19
+        assert len({s + k * 2 for k in range(3)}) == 3
+    assert P.window_end(4, 9, 5, 1) == P.window_start(4, 9, 5, 1) + 4
+
+
+def test_odd_kernel_matches_textbook_definition():
+    """Odd K: the window is the run of K positions of i's residue class,
+    centred on i and shifted inwards to fit the axis."""
+    for L, K, d in _sweep_starts():
+        if K % 2 == 0:
+            continue
+        for i in range(L):
+            r, j = i % d, i // d
+            n_cls = (L - r + d - 1) // d
+            want = r + min(max(j - K // 2, 0), n_cls - K) * d
+            assert P.window_start(i, L, K, d) == want, (i, L, K, d)
+
+
+def test_vectorised_equals_scalar():
+    for L, K, d in _sweep_starts(24):
+        got = P.window_start_vec(torch.arange(L), L, K, d).tolist()
+        assert got == [P.window_start(i, L, K, d) for i in range(L)]
+
+
+def test_out_of_range_only_for_even_kernel_equal_to_axis():
+    """The device code rejects exactly this case; everywhere else every window
+    lies inside the axis and starts are non-decreasing along a residue class
+    (what the key -> queries enumeration relies on)."""
+    for L, K, d in _sweep_starts():
+        starts = [P.window_start(i, L, K, d) for i in range(L)]
+        oor = any(s < 0 or s + (K - 1) * d > L - 1 for s in starts)
+        assert oor == (d == 1 and K % 2 == 0 and K == L), (L, K, d)
+        if oor:
+            continue
+        for r in range(d):
+            cls = starts[r::d]
+            assert all(a <= b for a, b in zip(cls, cls[1:])), (L, K, d, r)
+            assert all(s % d == r for s in cls)
+
+
+def test_c_oracle_and_device_rule_agree(c_oracle, host_idx):
+    for L, K, d in _sweep_starts(24):
+        for i in range(L):
+            want = P.window_start(i, L, K, d)
+            assert c_oracle.oracle_window_start(i, L, K, d) == want
+            assert host_idx.host_window_start(i, L, K, d) == want
+
+
+# -- neighbourhood maps ------------------------------------------------------
+
+MAP_CASES = [
+    ((37,), (5,), (1,), (1,), (False,)),
+    ((37,), (5,), (3,), (2,), (True,)),
+    ((40,), (9,), (4,), (3,), (False,)),
+    ((16,), (4,), (1,), (1,), (False,)),
+    ((10, 12), (3, 5), (1, 2), (1, 1), (False, False)),
+    ((10, 12), (5, 3), (2, 1), (2, 3), (True, False)),
+    ((9, 11), (3, 5), (3, 2), (3, 1), (True, True)),
+    ((56, 56), (7, 7), (8, 8), (1, 1), (False, False)),
+    ((6, 7, 8), (3, 3, 5), (1, 2, 1), (1, 1, 2), (False, True, False)),
+    ((5, 6, 7), (3, 3, 3), (1, 1, 2), (2, 1, 1), (True, True, True)),
+    ((16, 32, 32), (3, 7, 7), (1, 2, 2), (1, 1, 1), (False, False, False)),
+]
+
+
+def _oracle_map(spatial, ks, dil, st, causal):
+    flat, valid = P.neighborhood(len(spatial), spatial, ks, dil, st, causal)
+    if len(spatial) == 1:
+        flat = flat  # [n_out, K]
+    if valid is None:
+        valid = torch.ones_like(flat, dtype=torch.bool)
+    return flat.reshape(-1, flat.shape[-1]), valid.reshape(-1, flat.shape[-1])
+
+
+@pytest.mark.parametrize("case", MAP_CASES)
+def test_device_index_code_map_equals_oracle(case, host_idx, c_oracle):
+    spatial, ks, dil, st, causal = case
+    flat, valid = _oracle_map(spatial, ks, dil, st, causal)
+    prob = _problem(spatial, ks, dil, st, causal)
+    got_f = np.empty(flat.numel(), dtype=np.int64)
+    got_v = np.empty(flat.numel(), dtype=np.uint8)
+    host_idx.host_neighbor_map(ctypes.byref(prob), got_f.ctypes.data, got_v.ctypes.data)
+    assert np.array_equal(got_f, flat.reshape(-1).numpy())
+    assert np.array_equal(got_v.astype(bool), valid.reshape(-1).numpy())
+    # the C restatement of the oracle
+    pad = lambda v, f: [f] * (3 - len(v)) + list(v)  # noqa: E731
+    arr = lambda v: (ctypes.c_int64 * 3)(*pad(v, 1))  # noqa: E731
+    cf = np.empty(flat.numel(), dtype=np.int64)
+    cv = np.empty(flat.numel(), dtype=np.uint8)
+    c_oracle.oracle_neighborhood(arr(spatial), arr(ks), arr(dil), arr(st),
+                                 (ctypes.c_int * 3)(*pad([int(c) for c in causal], 0)),
+                                 cf.ctypes.data_as(ctypes.c_void_p), cv.ctypes.data_as(ctypes.c_void_p))
+    assert np.array_equal(cf, flat.reshape(-1).numpy())
+    assert np.array_equal(cv.astype(bool), valid.reshape(-1).numpy())
+
+
+def test_inverse_enumeration_is_exact(host_idx):
+    """Key -> queries enumeration (used by every dK/dV kernel) visits exactly
+    the valid (query, neighbour) pairs of the forward, for a sweep of 1-D and
+    2-D shapes including causal, stride and dilation."""
+    n = 0
+    for L, K, d in _sweep_starts(14):
+        if d == 1 and K % 2 == 0 and K == L:
+            continue
+        for s, c in itertools.product((1, 2, 3), (False, True)):
+            if s > K:
+                continue
+            assert host_idx.host_inverse_mismatch(ctypes.byref(_problem((L,), (K,), (d,), (s,), (c,)))) == 0
+            n += 1
+    for case in MAP_CASES[4:]:
+        spatial, ks, dil, st, causal = case
+        if np.prod(spatial) > 2000:
+            continue
+        assert host_idx.host_inverse_mismatch(ctypes.byref(_problem(spatial, ks, dil, st, causal))) == 0
+    assert n > 500
