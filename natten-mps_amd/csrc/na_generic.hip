@@ -182,17 +182,36 @@ __global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec,
     const QPos Q = decode_query(p, qi);
     const int hk = Q.h / p.rep;
 
-    float qv[DPL], dov[DPL], ov[DPL];
+    float qv[DPL], dov[DPL];
     load_run<T, DPL>(q + lq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, qv);
     load_run<T, DPL>(dout + ldo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, dov);
-    load_run<T, DPL>(o + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, ov);
+    const float L = lse[ll.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)];
     float di = 0.f;
+    if constexpr (sizeof(T) == 4) {
+        // delta = dO . O: exact enough when O was stored in fp32.
+        float ov[DPL];
+        load_run<T, DPL>(o + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, ov);
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) di = fmaf(dov[j], ov[j], di);
-    di = group_sum<LPQ>(di);
+        for (int j = 0; j < DPL; ++j) di = fmaf(dov[j], ov[j], di);
+        di = group_sum<LPQ>(di);
+    } else {
+        // 16-bit O carries ~2^-9 relative rounding; use the equivalent
+        // delta = sum_k P_k (dO . v_k) from an extra pass instead.
+        for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int, bool ok) {
+            if (!ok) return;
+            float kv[DPL], vv[DPL];
+            load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk, vec, kv);
+            load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, hk), d0, p.Dv, vec, vv);
+            float s = 0.f, dp = 0.f;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) { s = fmaf(qv[j], kv[j], s); dp = fmaf(dov[j], vv[j], dp); }
+            s = group_sum<LPQ>(s) * p.scale;
+            dp = group_sum<LPQ>(dp);
+            di = fmaf(expf(s - L), dp, di);
+        });
+    }
     if (dlse) di -= dlse[ldl.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)];
     if (d0 == 0) delta[lde.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = di;
-    const float L = lse[ll.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)];
 
     float acc[DPL];
 #pragma unroll

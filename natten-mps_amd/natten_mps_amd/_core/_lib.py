@@ -71,7 +71,7 @@ _SIGNATURES = {
     "natten_hip_abi_version": ([], ctypes.c_int),
     "natten_hip_last_error": ([], ctypes.c_char_p),
     "natten_hip_forward": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP], ctypes.c_int),
-    "natten_hip_backward": ([_P(Problem)] + [_VP, _LP] * 12 + [_VP], ctypes.c_int),
+    "natten_hip_backward": ([_P(Problem)] + [_VP, _LP] * 11 + [_VP], ctypes.c_int),
     "natten_hip_qk_forward": ([_P(Problem)] + [_VP, _LP] * 3 + [_VP], ctypes.c_int),
     "natten_hip_av_forward": ([_P(Problem)] + [_VP, _LP] * 3 + [_VP], ctypes.c_int),
     "natten_hip_qk_backward": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP], ctypes.c_int),

@@ -103,3 +103,15 @@ def test_python_errors_map_to_exceptions(lib):
     with pytest.raises(ValueError, match="exceeds length"):
         _lib.check(lib.natten_hip_forward(ctypes.byref(_prob(dilation=(4,))), *([ctypes.c_void_p(16),
                    ctypes.byref(_lib.Layout())] * 5), None), "forward")
+
+
+def test_ctypes_arity_matches_header():
+    """Every binding takes exactly the parameters the header declares."""
+    import re as _re
+
+    text = open(HEADER).read()
+    for name, (args, _) in _lib._SIGNATURES.items():
+        m = _re.search(rf"\b{name}\(([^)]*)\)", text)
+        assert m, name
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(args), (name, len(params), len(args))

@@ -284,7 +284,7 @@ def test_return_lse_and_additional_keys_match_oracle_composition(pure_backend):
     (dl,) = _inputs(92, [(2, 9, 10, 4)], torch.float32)
 
     def run(device):
-        leaves = [t.to(device).requires_grad_(True) for t in (q, k, v, ak, av)]
+        leaves = [t.detach().clone().to(device).requires_grad_(True) for t in (q, k, v, ak, av)]
         out, lse = F.na2d(*leaves[:3], kernel_size=3, dilation=(2, 1), return_lse=True,
                           additional_keys=leaves[3], additional_values=leaves[4])
         torch.autograd.backward([out, lse], [do.to(device), dl.to(device)])
