@@ -2,6 +2,7 @@
 // validation, problem set-up and kernel selection.  No entry point allocates.
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "na_launch.h"
@@ -113,6 +114,16 @@ bool runs_aligned(int dpl, std::initializer_list<Run> ts) {
     return true;
 }
 
+// NATTEN_HIP_KERNELS=generic selects the vector-ALU kernels everywhere (for
+// A/B comparisons); by default the MFMA tile kernels serve every eligible call.
+bool use_mfma() {
+    static const bool on = [] {
+        const char* e = std::getenv("NATTEN_HIP_KERNELS");
+        return !(e && std::strcmp(e, "generic") == 0);
+    }();
+    return on;
+}
+
 bool any_null(std::initializer_list<const void*> ps) {
     for (auto p : ps)
         if (!p) return true;
@@ -137,8 +148,14 @@ int natten_hip_forward(const natten_problem_t* p, const void* q, const natten_la
     const int D = P.Dqk > P.Dv ? P.Dqk : P.Dv;
     const int vec =
         runs_aligned(dpl_for(D), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {v, lv, P.Dv}, {out, lo, P.Dv}}) ? 1 : 0;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (use_mfma() && na::mfma_eligible(P, p->dtype, D, vec != 0, false) &&
+        na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv)}))
+        return launch_status(na::mfma_forward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), lse,
+                                              to_lay(llse), p->dtype, s),
+                             "forward");
     return launch_status(na::generic_forward(P, vec, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo),
-                                             lse, to_lay(llse), p->dtype, static_cast<hipStream_t>(stream)),
+                                             lse, to_lay(llse), p->dtype, s),
                          "forward");
 }
 
@@ -159,6 +176,13 @@ int natten_hip_backward(const natten_problem_t* p, const void* q, const natten_l
                                               {dout, ldo, P.Dv}, {dq, ldq, P.Dqk}, {dk, ldk, P.Dqk}, {dv, ldv, P.Dv}})
                         ? 1
                         : 0;
+    if (use_mfma() && na::mfma_eligible(P, p->dtype, D, vec != 0, true) &&
+        na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(ldo)}))
+        return launch_status(na::mfma_backward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), dout, to_lay(ldo), lse,
+                                               to_lay(llse), dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv,
+                                               to_lay(ldv), delta, to_lay(ldelta), p->dtype,
+                                               static_cast<hipStream_t>(stream)),
+                             "backward");
     return launch_status(
         na::generic_backward(P, vec, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout, to_lay(ldo),
                              lse, to_lay(llse), dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv,

@@ -36,3 +36,17 @@ hipError_t neighborhood_map(const Prob& p, int64_t* flat, uint8_t* valid, hipStr
         hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);         \
         ::na::prof_end(stream);                                                      \
     } while (0)
+
+namespace na {
+
+// MFMA tile path (na_mfma.hip): bf16/fp16, stride 1, equal head dims 32/64/128.
+bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward);
+bool mfma_offsets_fit(const Prob& p, std::initializer_list<Lay> lays);
+hipError_t mfma_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
+                        Lay lo, float* lse, Lay ll, int dtype, hipStream_t s);
+hipError_t mfma_backward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
+                         const void* dout, Lay ldo, const float* lse, Lay ll, const float* dlse, Lay ldl, void* dq,
+                         Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv, float* delta, Lay lde, int dtype,
+                         hipStream_t s);
+
+}  // namespace na

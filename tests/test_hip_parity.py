@@ -114,6 +114,15 @@ FUSED = [
     (3, (6, 7, 8), 2, 2, 32, (3, 3, 5), (1, 1, 1), (1, 2, 1), (False, False, False), None),
     (3, (6, 7, 8), 4, 2, 16, (3, 3, 3), (1, 2, 1), (2, 1, 1), (False, True, False), None),
     (3, (5, 6, 7), 2, 2, 8, (3, 3, 3), (1, 1, 2), (1, 1, 2), (True, True, True), None),
+    # stride-1 cases with head dim 32/64 (the MFMA tile path for fp16/bf16)
+    (1, (150,), 4, 2, 64, (9,), (1,), (3,), (True,), None),
+    (1, (100,), 2, 2, 32, (33,), (1,), (1,), (False,), None),
+    (2, (13, 17), 2, 2, 32, (3, 5), (1, 1), (2, 3), (True, True), 0.2),
+    (2, (20, 21), 4, 1, 64, (7, 5), (1, 1), (1, 2), (False, False), None),
+    (2, (10, 12), 2, 2, 32, (4, 4), (1, 1), (1, 2), (False, False), None),
+    (2, (24, 24), 2, 2, 32, (7, 7), (1, 1), (3, 3), (False, True), None),
+    (3, (6, 9, 10), 2, 2, 32, (3, 3, 5), (1, 1, 1), (2, 1, 1), (False, True, False), None),
+    (3, (5, 12, 12), 4, 2, 64, (3, 5, 5), (1, 1, 1), (1, 2, 2), (False, False, False), None),
 ]
 
 
@@ -360,3 +369,15 @@ def test_golden_fused_cases_on_hip(golden):
             float(q.shape[-1] ** -0.5 if c["scale"] is None else c["scale"]))
         for n, a in (("out", out), ("dq", dq), ("dk", dk), ("dv", dv)):
             _close(a.cpu(), golden.tensor(p + n), dtype, f"{p}{n}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_head_dim_128_tile_path(dtype):
+    from natten_mps_amd import functional as F
+
+    q, k, v, do = _inputs(101, [(1, 12, 13, 2, 128)] * 4, dtype)
+    out, grads = _hip_fwd_bwd(F.na2d, (q, k, v), do, kernel_size=5, dilation=(2, 1))
+    ref, rgrads = _oracle_fwd_bwd(2, (q, k, v), do, (5, 5), (1, 1), (2, 1), (False, False))
+    _close(out, ref, dtype, "out")
+    for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
+        _close(a, b, dtype, n)
