@@ -51,10 +51,13 @@ def kernel_bytes(name, B, N, Hq, Hkv, D, esz):
     """Algorithmic HBM bytes of one launch (compulsory traffic: every operand
     read once, every result written once; K/V at Hkv heads; fp32 LSE/delta)."""
     tq, tkv, lse = B * N * Hq * D * esz, B * N * Hkv * D * esz, B * N * Hq * 4
+    fwd = tq + 2 * tkv + tq + lse                 # q, k, v -> out, lse
+    bwd_q = tq + 2 * tkv + tq + lse + tq + lse    # q, k, v, dout, lse -> dq, delta
+    bwd_kv = tq + 2 * tkv + tq + 2 * lse + 2 * tkv  # q, k, v, dout, lse, delta -> dk, dv
     return {
-        "na_forward": tq + 2 * tkv + tq + lse,                 # q, k, v -> out, lse
-        "na_bwd_dq": tq + 2 * tkv + 2 * tq + lse + tq + lse,   # q, k, v, out, dout, lse -> dq, delta
-        "na_bwd_dkdv": tq + 2 * tkv + tq + 2 * lse + 2 * tkv,  # q, k, v, dout, lse, delta -> dk, dv
+        "na_forward": fwd, "na_fwd_mfma": fwd,
+        "na_bwd_dq": bwd_q + tq, "na_bwd_q_mfma": bwd_q,   # the vector kernel also reads out
+        "na_bwd_dkdv": bwd_kv, "na_bwd_kv_mfma": bwd_kv,
     }.get(name)
 
 
@@ -137,17 +140,25 @@ def main():
     torch.cuda.synchronize()
     _lib.profile_read(reset=True)
 
-    _lib.profile_enable(True)
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        step()
-    stop.record()
-    torch.cuda.synchronize()
-    _lib.profile_enable(False)
-    ms = start.elapsed_time(stop) / args.steps
+    def timed(profile):
+        _lib.profile_enable(profile)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(args.steps):
+            step()
+        stop.record()
+        torch.cuda.synchronize()
+        _lib.profile_enable(False)
+        return start.elapsed_time(stop) / args.steps
+
+    # the step time is taken with the per-launch event timing off; the same K
+    # steps are then repeated with every library launch bracketed by HIP events
+    # on its stream, which gives the per-kernel durations for the roofline
+    ms = timed(False)
+    ms_profiled = timed(True)
     stats = _lib.profile_read(reset=True)
+    _log(f"step {ms:.4f} ms (with per-launch events: {ms_profiled:.4f} ms)")
 
     pairs = B * Hq * _valid_pairs((H, W), (K, K), (dil, dil), (1, 1), (False, False), dev)
     flops = 14.0 * pairs * D

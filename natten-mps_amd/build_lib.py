@@ -30,6 +30,8 @@ FLAGS = [
     "-fPIC",
     # keep hipcc from forming packed-fp32 (v_pk_*_f32) instructions
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs (no AGPR copies around the softmax)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
     "-I" + os.path.join(ROOT, "include"),
     "-I" + CSRC,

@@ -178,7 +178,8 @@ int natten_hip_backward(const natten_problem_t* p, const void* q, const natten_l
                         : 0;
     if (use_mfma() && na::mfma_eligible(P, p->dtype, D, vec != 0, true) &&
         na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(ldo)}))
-        return launch_status(na::mfma_backward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), dout, to_lay(ldo), lse,
+        return launch_status(na::mfma_backward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout,
+                                               to_lay(ldo), lse,
                                                to_lay(llse), dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv,
                                                to_lay(ldv), delta, to_lay(ldelta), p->dtype,
                                                static_cast<hipStream_t>(stream)),

@@ -99,6 +99,54 @@ __host__ __device__ inline bool axis_query_range(const Axis& a, int m, int& t_lo
     return lo <= hi;
 }
 
+// Residue-class view of one axis.  With dilation d the positions r, r+d, ...
+// form class r with n = ceil((L - r)/d) members; a window never leaves its
+// class and, in class coordinates j = (i - r)/d, is the undilated run
+// [ws(j), ws(j) + K - 1].  The window rule above becomes, with h = K/2:
+//   causal:      ws(j) = j - (K - 1)
+//   non-causal:  ws(j) = 0 for j < h;  B for j + h >= n;  j - h otherwise,
+// with B = n - 1 - 2h when d == 1 or r < L % d, and B = n - K otherwise (the
+// two agree for odd K).  No divisions: kernels evaluate it per lane.
+struct ClassAxis {
+    int n, K, h, B, causal;
+};
+
+__host__ __device__ inline ClassAxis class_axis(const Axis& a, int r) {
+    ClassAxis c;
+    c.n = (a.len - r + a.dil - 1) / a.dil;
+    c.K = a.k;
+    c.h = a.k / 2;
+    c.causal = a.causal;
+    c.B = (a.dil == 1 || r < a.len % a.dil) ? c.n - 1 - 2 * c.h : c.n - a.k;
+    return c;
+}
+
+__host__ __device__ inline int class_ws(const ClassAxis& c, int j) {
+    if (c.causal) return j - (c.K - 1);
+    if (j < c.h) return 0;
+    if (j + c.h >= c.n) return c.B;
+    return j - c.h;
+}
+
+// Class range [jlo, jhi] of the queries whose windows hold key u (empty when
+// jlo > jhi).  ws is non-decreasing, so {j : ws(j) <= u} is a prefix and
+// {j : ws(j) + K - 1 >= u} a suffix of the class.
+__host__ __device__ inline void class_span(const ClassAxis& c, int u, int& jlo, int& jhi) {
+    if (c.causal) {
+        jlo = u;
+        jhi = u + c.K - 1 < c.n - 1 ? u + c.K - 1 : c.n - 1;
+        return;
+    }
+    jhi = u >= c.B ? c.n - 1 : u + c.h;
+    const int v = u - c.K + 1;  // smallest j with ws(j) >= v
+    if (v <= 0)
+        jlo = 0;
+    else if (v + c.h < c.n - c.h)
+        jlo = v + c.h;
+    else
+        jlo = c.B >= v ? c.n - c.h : c.n;
+}
+
 // f(j0, j1, j2, e, valid) for each neighbour e (row-major over the kernel) of
 // the query at (i0, i1, i2).  Invalid (causal) neighbours have j < 0 on some
 // axis and must not be dereferenced.

@@ -45,8 +45,8 @@ bool mfma_offsets_fit(const Prob& p, std::initializer_list<Lay> lays);
 hipError_t mfma_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
                         Lay lo, float* lse, Lay ll, int dtype, hipStream_t s);
 hipError_t mfma_backward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
-                         const void* dout, Lay ldo, const float* lse, Lay ll, const float* dlse, Lay ldl, void* dq,
-                         Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv, float* delta, Lay lde, int dtype,
-                         hipStream_t s);
+                         const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
+                         const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
+                         float* delta, Lay lde, int dtype, hipStream_t s);
 
 }  // namespace na

@@ -91,40 +91,27 @@ __device__ __forceinline__ float max_groups(float v) {
     return fmaxf(v, __shfl_xor(v, 32));
 }
 
-// Class extent, window start (class coordinates) of query j, and the class
-// range of queries whose windows hold key u (empty: jlo > jhi).
-__device__ __forceinline__ int n_class(const Axis& A, int r) { return (A.len - r + A.dil - 1) / A.dil; }
-
-__device__ __forceinline__ int ws_class(const Axis& A, int r, int j) {
-    return (axis_first(A, r + j * A.dil) - r) / A.dil;  // exact: the start shares the residue
-}
-
-__device__ __forceinline__ void q_span(const Axis& A, int r, int u, int& jlo, int& jhi) {
-    int tlo, thi;
-    if (axis_query_range(A, r + u * A.dil, tlo, thi)) {
-        jlo = u + tlo;
-        jhi = u + thi;
-    } else {
-        jlo = 1;
-        jhi = 0;
-    }
-}
-
 }  // namespace
 
 // Host-chosen tile: extents (class coordinates) of a workgroup's box, tiles
-// per class per axis, waves per workgroup and staged LDS slots per slice.
+// per class per axis, waves per workgroup, and the staged slice layout: slot
+// = a1 * rowlen + a2 for union row a1 and column a2, with rowlen = 2^rowshift
+// >= 8 covering the widest union row (so a lane's 8 consecutive slots never
+// straddle two rows), `slots` = staged slots per slice (multiple of 32).
 struct TileShape {
     int T[3];
     int ntile[3];
     int waves;
     int slots;
+    int rowlen;
+    int rowshift;
 };
 
 namespace {
 
 struct Block {
     int b, h, r[3], J[3], E[3], lo[3], U[3];
+    ClassAxis c[3];
 };
 
 // Workgroup -> (batch, head, residues, tile origin J, clipped extent E) and
@@ -144,31 +131,23 @@ __device__ __forceinline__ bool decode_block(const Prob& p, const TileShape& ts,
     }
     k.b = bid;
     for (int a = 0; a < 3; ++a) {
-        const Axis& A = p.ax[a];
-        const int n = n_class(A, k.r[a]);
+        const ClassAxis c = class_axis(p.ax[a], k.r[a]);
+        k.c[a] = c;
         k.J[a] = t[a] * ts.T[a];
-        const int jend = min(k.J[a] + ts.T[a], n) - 1;
+        const int jend = min(k.J[a] + ts.T[a], c.n) - 1;
         k.E[a] = jend - k.J[a] + 1;
         if (k.E[a] <= 0) return false;
         int lo, hi;
         if (!key_tile) {
-            lo = max(ws_class(A, k.r[a], k.J[a]), 0);
-            hi = min(ws_class(A, k.r[a], jend) + A.k - 1, n - 1);
+            lo = max(class_ws(c, k.J[a]), 0);
+            hi = min(class_ws(c, jend) + c.K - 1, c.n - 1);
         } else {
-            // spans are monotone over attended keys; keys attended by nobody
-            // (possible only at an even-kernel border) are skipped
-            lo = 1 << 30;
-            hi = -1;
-            for (int u = k.J[a]; u <= jend; ++u) {
-                int a0, a1;
-                q_span(A, k.r[a], u, a0, a1);
-                if (a0 <= a1) { lo = a0; break; }
-            }
-            for (int u = jend; u >= k.J[a]; --u) {
-                int a0, a1;
-                q_span(A, k.r[a], u, a0, a1);
-                if (a0 <= a1) { hi = a1; break; }
-            }
+            // both span ends are non-decreasing in the key; keys attended by
+            // nobody (only past the last window at an even-kernel border) sit
+            // at the end and leave hi unchanged
+            int x;
+            class_span(c, k.J[a], lo, x);
+            class_span(c, jend, x, hi);
         }
         k.lo[a] = lo;
         k.U[a] = hi >= lo ? hi - lo + 1 : 0;
@@ -181,12 +160,11 @@ __device__ __forceinline__ bool decode_block(const Prob& p, const TileShape& ts,
 // union.  Offsets inside one (batch, head, axis-0 plane) fit in 32 bits
 // (checked on the host).
 template <typename T, int D>
-__device__ __forceinline__ void stage(const Prob& p, const Block& k, const T* __restrict__ g, Lay lay, int h,
-                                      int p0, int slots, T* rows, T* trans) {
+__device__ __forceinline__ void stage(const Prob& p, const Block& k, const TileShape& ts, const T* __restrict__ g,
+                                      Lay lay, int h, int p0, T* rows, T* trans) {
     constexpr int V8 = D / 8;
+    const int slots = ts.slots;
     const int part = threadIdx.x % V8;
-    const int S = k.U[1] * k.U[2];
-    const float inv = 1.f / static_cast<float>(max(k.U[2], 1));
     const T* base = g + static_cast<long long>(k.b) * lay.b + static_cast<long long>(h) * lay.h +
                     static_cast<long long>(p0) * lay.s0 + part * 8;
     const int s1 = static_cast<int>(lay.s1), s2 = static_cast<int>(lay.s2);
@@ -194,16 +172,15 @@ __device__ __forceinline__ void stage(const Prob& p, const Block& k, const T* __
     const int c1 = k.r[1] + k.lo[1] * d1, c2 = k.r[2] + k.lo[2] * d2;
 #pragma unroll 2
     for (int sp = threadIdx.x / V8; 2 * sp < slots; sp += blockDim.x / V8) {
+        // the pair 2sp, 2sp+1 shares a union row (rowlen is even)
+        const int a1 = (2 * sp) >> ts.rowshift, a2 = (2 * sp) & (ts.rowlen - 1);
+        const bool row_ok = a1 < k.U[1];
+        const T* src = base + (c1 + a1 * d1) * s1 + (c2 + a2 * d2) * s2;
         uint4 x[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            const int s = 2 * sp + e;
             x[e] = make_uint4(0, 0, 0, 0);
-            if (s < S) {
-                const int a1 = static_cast<int>((static_cast<float>(s) + 0.5f) * inv);
-                const int a2 = s - a1 * k.U[2];
-                x[e] = *reinterpret_cast<const uint4*>(base + (c1 + a1 * d1) * s1 + (c2 + a2 * d2) * s2);
-            }
+            if (row_ok && a2 + e < k.U[2]) x[e] = *reinterpret_cast<const uint4*>(src + e * d2 * s2);
         }
         if (rows) {
 #pragma unroll
@@ -221,16 +198,13 @@ __device__ __forceinline__ void stage(const Prob& p, const Block& k, const T* __
 }
 
 // Stage per-slot fp32 values (lse in the log2 domain, delta) of the slice.
-__device__ __forceinline__ void stage_scalars(const Prob& p, const Block& k, int h, int p0, int slots,
+__device__ __forceinline__ void stage_scalars(const Prob& p, const Block& k, const TileShape& ts, int h, int p0,
                                               const float* __restrict__ lse, Lay ll, const float* __restrict__ delta,
                                               Lay lde, float* L2s, float* Ds) {
-    const int S = k.U[1] * k.U[2];
-    const float inv = 1.f / static_cast<float>(max(k.U[2], 1));
-    for (int s = threadIdx.x; s < slots; s += blockDim.x) {
+    for (int s = threadIdx.x; s < ts.slots; s += blockDim.x) {
         float l2 = 0.f, dd = 0.f;
-        if (s < S) {
-            const int a1 = static_cast<int>((static_cast<float>(s) + 0.5f) * inv);
-            const int a2 = s - a1 * k.U[2];
+        const int a1 = s >> ts.rowshift, a2 = s & (ts.rowlen - 1);
+        if (a1 < k.U[1] && a2 < k.U[2]) {
             const int p1 = k.r[1] + (k.lo[1] + a1) * p.ax[1].dil, p2 = k.r[2] + (k.lo[2] + a2) * p.ax[2].dil;
             l2 = lse[ll.at(k.b, p0, p1, p2, h)] * kLog2e;
             dd = delta[lde.at(k.b, p0, p1, p2, h)];
@@ -272,13 +246,12 @@ struct Span {
 __device__ __forceinline__ Span lane_span(const Prob& p, const Block& k, const Item& it, bool key_side) {
     Span sp;
     for (int a = 0; a < 3; ++a) {
-        const Axis& A = p.ax[a];
         int lo, hi;
         if (!key_side) {
-            lo = ws_class(A, k.r[a], it.j[a]);
-            hi = lo + A.k - 1;
+            lo = class_ws(k.c[a], it.j[a]);
+            hi = lo + k.c[a].K - 1;
         } else {
-            q_span(A, k.r[a], it.j[a], lo, hi);
+            class_span(k.c[a], it.j[a], lo, hi);
         }
         sp.lo[a] = lo - k.lo[a];
         sp.hi[a] = hi - k.lo[a];
@@ -289,19 +262,21 @@ __device__ __forceinline__ Span lane_span(const Prob& p, const Block& k, const I
     return sp;
 }
 
-// Slots 32c + 8grp + e (e < 8) of slice u0: admissible for this lane?
-__device__ __forceinline__ unsigned chunk_mask(const Span& sp, bool in0, int s0, int U2, float invU2) {
-    unsigned m = 0;
-    if (!in0) return 0;
-    int a1 = static_cast<int>((static_cast<float>(s0) + 0.5f) * invU2);
-    int a2 = s0 - a1 * U2;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const bool ok = a1 >= sp.lo[1] && a1 <= sp.hi[1] && a2 >= sp.lo[2] && a2 <= sp.hi[2];
-        m |= ok ? (1u << e) : 0u;
-        if (++a2 == U2) { a2 = 0; ++a1; }
-    }
-    return m;
+// Bit e set when slot s0 + e (s0 a multiple of 8, so all in one union row) is
+// admissible for this lane: its row in [lo1, hi1] and column in [lo2, hi2].
+// Padding columns lie past hi2 and padding rows past hi1.
+__device__ __forceinline__ unsigned chunk_mask(const Span& sp, bool in0, int s0, const TileShape& ts) {
+    const int a1 = s0 >> ts.rowshift, a2 = s0 & (ts.rowlen - 1);
+    if (!in0 || a1 < sp.lo[1] || a1 > sp.hi[1]) return 0u;
+    const int lo = sp.lo[2] - a2, hi = sp.hi[2] - a2;  // admissible bit range
+    if (hi < 0 || lo > 7) return 0u;
+    return (0xFFu << (lo > 0 ? lo : 0)) & (0xFFu >> (hi < 7 ? 7 - hi : 0));
+}
+
+// First and last chunk covering the wave's admissible box.
+__device__ __forceinline__ void chunk_range(const Span& sp, const TileShape& ts, int& c0, int& c1) {
+    c0 = (sp.wlo[1] * ts.rowlen + sp.wlo[2]) >> 5;
+    c1 = (sp.whi[1] * ts.rowlen + sp.whi[2]) >> 5;
 }
 
 // Score block: rows = 32 slots of chunk c (A operand from row-major LDS),
@@ -380,31 +355,27 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T*
     f32x4_t acc[D / 16];
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m = -INFINITY, lsum = 0.f;
+    float m = -INFINITY, lsum = 0.f;  // running max and sum, log2 domain (scores times scale*log2 e)
     const float sc2 = p.scale * kLog2e;
-    const int U2 = blk.U[2];
-    const float invU2 = 1.f / static_cast<float>(U2);
+    int c0, c1;
+    chunk_range(sp, ts, c0, c1);
 
     for (int u0 = 0; u0 < blk.U[0]; ++u0) {
         const int p0 = blk.r[0] + (blk.lo[0] + u0) * p.ax[0].dil;
         __syncthreads();
-        stage<T, D>(p, blk, kg, lk, hk, p0, slots, Ks, nullptr);
-        stage<T, D>(p, blk, vg, lv, hk, p0, slots, nullptr, Vt);
+        stage<T, D>(p, blk, ts, kg, lk, hk, p0, Ks, nullptr);
+        stage<T, D>(p, blk, ts, vg, lv, hk, p0, nullptr, Vt);
         __syncthreads();
         if (u0 < sp.wlo[0] || u0 > sp.whi[0]) continue;
         const bool in0 = it.valid && u0 >= sp.lo[0] && u0 <= sp.hi[0];
-        const int first = sp.wlo[1] * U2 + sp.wlo[2], last = sp.whi[1] * U2 + sp.whi[2];
-        for (int c = first >> 5; c <= (last >> 5); ++c) {
+        for (int c = c0; c <= c1; ++c) {
             float sv[8];
             score_chunk<T, D>(Ks, c, col, grp, qf, sv);
-            const unsigned msk = chunk_mask(sp, in0, 32 * c + 8 * grp, U2, invU2);
+            const unsigned msk = chunk_mask(sp, in0, 32 * c + 8 * grp, ts);
             float cmax = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                sv[e] = (msk >> e) & 1u ? sv[e] * sc2 : -INFINITY;
-                cmax = fmaxf(cmax, sv[e]);
-            }
-            const float mnew = fmaxf(m, max_groups(cmax));
+            for (int e = 0; e < 8; ++e) cmax = fmaxf(cmax, (msk >> e) & 1u ? sv[e] : -INFINITY);
+            const float mnew = fmaxf(m, max_groups(cmax) * sc2);
             const float mref = mnew == -INFINITY ? 0.f : mnew;
             const float corr = __builtin_amdgcn_exp2f(m - mref);
             m = mnew;
@@ -413,7 +384,7 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T*
             for (int db = 0; db < D / 16; ++db) acc[db] *= corr;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                sv[e] = __builtin_amdgcn_exp2f(sv[e] - mref);
+                sv[e] = (msk >> e) & 1u ? __builtin_amdgcn_exp2f(fmaf(sv[e], sc2, -mref)) : 0.f;
                 lsum += sv[e];
             }
             accumulate_chunk<T, D>(Vt, slots, c, col, grp, pack8<T>(sv), acc);
@@ -427,13 +398,15 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T*
 }
 
 // ---------------------------------------------------------------------------
-// Backward, query side: delta = sum_k P dP - dlse (exact, from a first pass)
-// and dq = scale * sum_k P (dP - delta) k, with dP = dO . v.
+// Backward, query side: delta = dO . O - dlse (written for the key side) and
+// dq = scale * sum_k P (dP - delta) k, with P = exp(scale q.k - lse) and
+// dP = dO . v.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const T* __restrict__ q, Lay lq,
                                                     const T* __restrict__ kg, Lay lk, const T* __restrict__ vg,
-                                                    Lay lv, const T* __restrict__ dout, Lay ldo,
+                                                    Lay lv, const T* __restrict__ o, Lay lo,
+                                                    const T* __restrict__ dout, Lay ldo,
                                                     const float* __restrict__ lse, Lay ll,
                                                     const float* __restrict__ dlse, Lay ldl, T* __restrict__ dq,
                                                     Lay ldq, float* __restrict__ delta, Lay lde) {
@@ -449,56 +422,51 @@ __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const 
 
     const Item it = wave_item(p, blk, wave, col);
     const Span sp = lane_span(p, blk, it, false);
-    uint4 qf[D / 32], gf[D / 32];
-    load_frags<T, D>(q, lq.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), it.valid, grp, qf);
+    uint4 qf[D / 32], gf[D / 32], of[D / 32];
+    const long long qoff = lq.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h);
+    load_frags<T, D>(q, qoff, it.valid, grp, qf);
     load_frags<T, D>(dout, ldo.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), it.valid, grp, gf);
+    load_frags<T, D>(o, lo.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), it.valid, grp, of);
     const float L2 = it.valid ? lse[ll.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h)] * kLog2e : 0.f;
+    // delta from this lane's 8 head dims per 32, summed over the 4 lane groups
+    float di = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+        const T* g8 = reinterpret_cast<const T*>(&gf[ks]);
+        const T* o8 = reinterpret_cast<const T*>(&of[ks]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) di = fmaf(to_f(g8[e]), to_f(o8[e]), di);
+    }
+    di = sum_groups(di);
+    if (dlse && it.valid) di -= dlse[ldl.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h)];
+    if (it.valid && grp == 0) delta[lde.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h)] = di;
     const float sc2 = p.scale * kLog2e;
-    const int U2 = blk.U[2];
-    const float invU2 = 1.f / static_cast<float>(U2);
+    int c0, c1;
+    chunk_range(sp, ts, c0, c1);
 
     f32x4_t acc[D / 16];
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float di = 0.f;
 
-    for (int pass = 0; pass < 2; ++pass) {
-        for (int u0 = 0; u0 < blk.U[0]; ++u0) {
-            if (pass == 0 || blk.U[0] > 1) {
-                const int p0 = blk.r[0] + (blk.lo[0] + u0) * p.ax[0].dil;
-                __syncthreads();
-                stage<T, D>(p, blk, kg, lk, hk, p0, slots, Ks, Kt);
-                stage<T, D>(p, blk, vg, lv, hk, p0, slots, Vs, nullptr);
-                __syncthreads();
-            }
-            if (u0 < sp.wlo[0] || u0 > sp.whi[0]) continue;
-            const bool in0 = it.valid && u0 >= sp.lo[0] && u0 <= sp.hi[0];
-            const int first = sp.wlo[1] * U2 + sp.wlo[2], last = sp.whi[1] * U2 + sp.whi[2];
-            for (int c = first >> 5; c <= (last >> 5); ++c) {
-                float sv[8], dp[8];
-                score_chunk<T, D>(Ks, c, col, grp, qf, sv);
-                score_chunk<T, D>(Vs, c, col, grp, gf, dp);
-                const unsigned msk = chunk_mask(sp, in0, 32 * c + 8 * grp, U2, invU2);
-                if (pass == 0) {
+    for (int u0 = 0; u0 < blk.U[0]; ++u0) {
+        const int p0 = blk.r[0] + (blk.lo[0] + u0) * p.ax[0].dil;
+        __syncthreads();
+        stage<T, D>(p, blk, ts, kg, lk, hk, p0, Ks, Kt);
+        stage<T, D>(p, blk, ts, vg, lv, hk, p0, Vs, nullptr);
+        __syncthreads();
+        if (u0 < sp.wlo[0] || u0 > sp.whi[0]) continue;
+        const bool in0 = it.valid && u0 >= sp.lo[0] && u0 <= sp.hi[0];
+        for (int c = c0; c <= c1; ++c) {
+            float sv[8], dp[8];
+            score_chunk<T, D>(Ks, c, col, grp, qf, sv);
+            score_chunk<T, D>(Vs, c, col, grp, gf, dp);
+            const unsigned msk = chunk_mask(sp, in0, 32 * c + 8 * grp, ts);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float pe = (msk >> e) & 1u ? __builtin_amdgcn_exp2f(sv[e] * sc2 - L2) : 0.f;
-                        di = fmaf(pe, dp[e], di);
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float pe = (msk >> e) & 1u ? __builtin_amdgcn_exp2f(sv[e] * sc2 - L2) : 0.f;
-                        sv[e] = pe * (dp[e] - di);
-                    }
-                    accumulate_chunk<T, D>(Kt, slots, c, col, grp, pack8<T>(sv), acc);
-                }
+            for (int e = 0; e < 8; ++e) {
+                const float pe = (msk >> e) & 1u ? __builtin_amdgcn_exp2f(fmaf(sv[e], sc2, -L2)) : 0.f;
+                sv[e] = pe * (dp[e] - di);
             }
-        }
-        if (pass == 0) {
-            di = sum_groups(di);
-            if (dlse && it.valid) di -= dlse[ldl.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h)];
-            if (it.valid && grp == 0) delta[lde.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h)] = di;
+            accumulate_chunk<T, D>(Kt, slots, c, col, grp, pack8<T>(sv), acc);
         }
     }
     if (!it.valid) return;
@@ -535,8 +503,8 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
     load_frags<T, D>(kg, lk.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), it.valid, grp, kf);
     load_frags<T, D>(vg, lv.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), it.valid, grp, vf);
     const float sc2 = p.scale * kLog2e;
-    const int U2 = blk.U[2];
-    const float invU2 = 1.f / static_cast<float>(max(U2, 1));
+    int c0, c1;
+    chunk_range(sp, ts, c0, c1);
 
     f32x4_t gk[D / 16], gv[D / 16];
 #pragma unroll
@@ -550,19 +518,18 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
         for (int u0 = 0; u0 < blk.U[0]; ++u0) {
             const int p0 = blk.r[0] + (blk.lo[0] + u0) * p.ax[0].dil;
             __syncthreads();
-            stage<T, D>(p, blk, q, lq, h, p0, slots, Qs, Qt);
-            stage<T, D>(p, blk, dout, ldo, h, p0, slots, Gs, Gt);
-            stage_scalars(p, blk, h, p0, slots, lse, ll, delta, lde, L2s, Ds);
+            stage<T, D>(p, blk, ts, q, lq, h, p0, Qs, Qt);
+            stage<T, D>(p, blk, ts, dout, ldo, h, p0, Gs, Gt);
+            stage_scalars(p, blk, ts, h, p0, lse, ll, delta, lde, L2s, Ds);
             __syncthreads();
             if (u0 < sp.wlo[0] || u0 > sp.whi[0]) continue;
             const bool in0 = it.valid && u0 >= sp.lo[0] && u0 <= sp.hi[0];
-            const int first = sp.wlo[1] * U2 + sp.wlo[2], last = sp.whi[1] * U2 + sp.whi[2];
-            for (int c = first >> 5; c <= (last >> 5); ++c) {
+            for (int c = c0; c <= c1; ++c) {
                 float sv[8], dp[8];
                 score_chunk<T, D>(Qs, c, col, grp, kf, sv);
                 score_chunk<T, D>(Gs, c, col, grp, vf, dp);
-                const unsigned msk = chunk_mask(sp, in0, 32 * c + 8 * grp, U2, invU2);
                 const int s0 = 32 * c + 8 * grp;
+                const unsigned msk = chunk_mask(sp, in0, s0, ts);
                 const float4 la = *reinterpret_cast<const float4*>(L2s + s0);
                 const float4 lb = *reinterpret_cast<const float4*>(L2s + s0 + 4);
                 const float4 da = *reinterpret_cast<const float4*>(Ds + s0);
@@ -572,7 +539,7 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
                 float pe[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    pe[e] = (msk >> e) & 1u ? __builtin_amdgcn_exp2f(sv[e] * sc2 - l2[e]) : 0.f;
+                    pe[e] = (msk >> e) & 1u ? __builtin_amdgcn_exp2f(fmaf(sv[e], sc2, -l2[e])) : 0.f;
                     sv[e] = pe[e] * (dp[e] - dd[e]);
                 }
                 accumulate_chunk<T, D>(Gt, slots, c, col, grp, pack8<T>(pe), gv);
@@ -599,31 +566,23 @@ constexpr size_t kLdsBudget = 64 * 1024;
 
 int n_class_h(const Axis& A, int r) { return (A.len - r + A.dil - 1) / A.dil; }
 
-int ws_class_h(const Axis& A, int r, int j) { return (axis_first(A, r + j * A.dil) - r) / A.dil; }
-
 // Largest union extent on one axis over every class and tile (the same
 // spans decode_block computes on the device).
 int union_extent(const Axis& A, int T, bool key_tile) {
     int best = 1;
     for (int r = 0; r < A.dil; ++r) {
-        const int n = n_class_h(A, r);
-        for (int J = 0; J < n; J += T) {
-            const int jend = (J + T < n ? J + T : n) - 1;
-            int lo = 1 << 30, hi = -1;
+        const ClassAxis c = class_axis(A, r);
+        for (int J = 0; J < c.n; J += T) {
+            const int jend = (J + T < c.n ? J + T : c.n) - 1;
+            int lo, hi, x;
             if (!key_tile) {
-                lo = ws_class_h(A, r, J);
+                lo = class_ws(c, J);
                 lo = lo > 0 ? lo : 0;
-                hi = ws_class_h(A, r, jend) + A.k - 1;
-                hi = hi < n - 1 ? hi : n - 1;
+                hi = class_ws(c, jend) + c.K - 1;
+                hi = hi < c.n - 1 ? hi : c.n - 1;
             } else {
-                for (int u = J; u <= jend; ++u) {
-                    int tl, th;
-                    if (axis_query_range(A, r + u * A.dil, tl, th)) { lo = u + tl; break; }
-                }
-                for (int u = jend; u >= J; --u) {
-                    int tl, th;
-                    if (axis_query_range(A, r + u * A.dil, tl, th)) { hi = u + th; break; }
-                }
+                class_span(c, J, lo, x);
+                class_span(c, jend, x, hi);
             }
             if (hi - lo + 1 > best) best = hi - lo + 1;
         }
@@ -662,7 +621,10 @@ bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts) {
         ts.waves = (cnt + 15) / 16;
         const int u1 = union_extent(p.ax[1], ts.T[1], kind == kBackwardKV);
         const int u2 = union_extent(p.ax[2], ts.T[2], kind == kBackwardKV);
-        ts.slots = ((u1 * u2 + 31) / 32) * 32;
+        ts.rowshift = 3;
+        while ((1 << ts.rowshift) < u2) ++ts.rowshift;
+        ts.rowlen = 1 << ts.rowshift;
+        ts.slots = ((u1 * ts.rowlen + 31) / 32) * 32;
         if (lds_bytes(kind, ts.slots, D) <= kLdsBudget) return true;
     }
     return false;
@@ -706,8 +668,9 @@ hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
 
 template <typename T, int D>
 hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
-                      const void* dout, Lay ldo, const float* lse, Lay ll, const float* dlse, Lay ldl, void* dq,
-                      Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv, float* delta, Lay lde, hipStream_t s) {
+                      const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
+                      const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
+                      float* delta, Lay lde, hipStream_t s) {
     TileShape tq{}, tk{};
     choose_tile(p, kBackwardQ, D, tq);
     choose_tile(p, kBackwardKV, D, tk);
@@ -716,7 +679,7 @@ hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
     allow_lds(k_bwd_kv_mfma<T, D>, shk);
     NA_LAUNCH("na_bwd_q_mfma", (k_bwd_q_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tq, p.Hq))),
               dim3(64 * tq.waves), shq, s, p, tq, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv,
-              (const T*)dout, ldo, lse, ll, dlse, ldl, (T*)dq, ldq, delta, lde);
+              (const T*)o, lo, (const T*)dout, ldo, lse, ll, dlse, ldl, (T*)dq, ldq, delta, lde);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     NA_LAUNCH("na_bwd_kv_mfma", (k_bwd_kv_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tk, p.Hkv))),
@@ -728,7 +691,7 @@ hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
 }  // namespace
 
 bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward) {
-    if (dtype == NATTEN_F32 || !aligned) return false;
+    if (dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f)) return false;
     if (p.Dqk != p.Dv || !(D == 32 || D == 64 || D == 128)) return false;
     for (int a = 0; a < 3; ++a)
         if (p.ax[a].st != 1) return false;
@@ -757,11 +720,12 @@ hipError_t mfma_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay
 }
 
 hipError_t mfma_backward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
-                         const void* dout, Lay ldo, const float* lse, Lay ll, const float* dlse, Lay ldl, void* dq,
-                         Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv, float* delta, Lay lde, int dtype,
-                         hipStream_t s) {
-#define NA_BWD(T, DD) \
-    return launch_bwd<T, DD>(p, q, lq, k, lk, v, lv, dout, ldo, lse, ll, dlse, ldl, dq, ldq, dk, ldk, dv, ldv, delta, lde, s)
+                         const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
+                         const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
+                         float* delta, Lay lde, int dtype, hipStream_t s) {
+#define NA_BWD(T, DD)                                                                                            \
+    return launch_bwd<T, DD>(p, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl, dq, ldq, dk, ldk, dv, \
+                             ldv, delta, lde, s)
     if (dtype == NATTEN_BF16) {
         if (p.Dqk == 32) NA_BWD(bf16, 32);
         if (p.Dqk == 64) NA_BWD(bf16, 64);

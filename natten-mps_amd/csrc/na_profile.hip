@@ -29,14 +29,29 @@ std::atomic<int> g_on{0};
 std::mutex g_mu;
 std::vector<Pending> g_pending;
 std::vector<Stat> g_stats;
+std::vector<hipEvent_t> g_free;  // recycled events (creating one per launch is slow)
 thread_local Pending t_open{nullptr, nullptr, nullptr};
+
+hipEvent_t take_event() {
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (!g_free.empty()) {
+            hipEvent_t e = g_free.back();
+            g_free.pop_back();
+            return e;
+        }
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
 
 }  // namespace
 
 void prof_begin(const char* name, hipStream_t s) {
     if (!g_on.load(std::memory_order_relaxed)) return;
-    Pending p{name, nullptr, nullptr};
-    if (hipEventCreate(&p.start) != hipSuccess || hipEventCreate(&p.stop) != hipSuccess) return;
+    Pending p{name, take_event(), take_event()};
+    if (!p.start || !p.stop) return;
     hipEventRecord(p.start, s);
     t_open = p;
 }
@@ -76,8 +91,8 @@ int natten_hip_profile_read(natten_kernel_stat_t* out, int max_entries, int rese
             if (ms < st->min_ms) st->min_ms = ms;
             if (ms > st->max_ms) st->max_ms = ms;
         }
-        hipEventDestroy(p.start);
-        hipEventDestroy(p.stop);
+        na::g_free.push_back(p.start);
+        na::g_free.push_back(p.stop);
     }
     na::g_pending.clear();
     const int n = static_cast<int>(na::g_stats.size());

@@ -112,64 +112,126 @@ def _check_qkv(rank, q, k, v):
 
 # ---------------------------------------------------------------------------
 # fused forward / backward
+#
+# The per-call host work (validation, problem descriptor, stride layouts) is
+# cached per call signature -- shapes, strides, dtype, device and parameters --
+# so a repeated call costs two allocations and one C call.
 # ---------------------------------------------------------------------------
 
+_FWD_CACHE: dict = {}
+_BWD_CACHE: dict = {}
+_CACHE_MAX = 512
 
-def forward_with_lse(rank: int, q, k, v, kernel_size, stride, dilation, is_causal, scale):
+
+class _Sig:
+    __slots__ = ("prob", "refs", "out_shape", "lse_shape", "strided", "device")
+
+
+def _raw_stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _launch(device, fn, *args):
+    """Call a C entry point with the tensors' device current."""
+    if torch.cuda.current_device() != device.index:
+        with torch.cuda.device(device):
+            return fn(*args)
+    return fn(*args)
+
+
+def _fwd_sig(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_value):
     _check_qkv(rank, q, k, v)
     _on_device(q, k, v)
     _same_dtype(q, k, v)
+    sig = _Sig()
+    sig.prob = _fused_problem(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_value)
+    out_sp = tuple(sig.prob.out_length[3 - rank:])
+    B, Hq = q.shape[0], q.shape[-2]
+    sig.out_shape = (B, *out_sp, Hq, v.shape[-1])
+    sig.lse_shape = (B, *out_sp, Hq)
+    sig.device = q.device
+    out = torch.empty(sig.out_shape, dtype=q.dtype, device="meta")
+    lse = torch.empty(sig.lse_shape, dtype=torch.float32, device="meta")
+    lays = [_lib.layout(t, rank, 1) for t in (q, k, v, out)] + [_lib.layout(lse, rank, 0)]
+    sig.refs = [lays, [ctypes.byref(x) for x in lays]]
+    return sig
+
+
+def forward_with_lse(rank: int, q, k, v, kernel_size, stride, dilation, is_causal, scale):
     q, k, v = _inner(q), _inner(k), _inner(v)
     scale_value = float(q.shape[-1] ** -0.5 if scale is None else scale)
-    prob = _fused_problem(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_value)
-    out_sp = tuple(prob.out_length[3 - rank:])
-    B, Hq = q.shape[0], q.shape[-2]
-    out = torch.empty((B, *out_sp, Hq, v.shape[-1]), dtype=q.dtype, device=q.device)
-    lse = torch.empty((B, *out_sp, Hq), dtype=torch.float32, device=q.device)
+    key = (rank, q.dtype, k.dtype, v.dtype, q.device, k.device, v.device, q.shape, q.stride(), k.shape,
+           k.stride(), v.shape, v.stride(), tuple(kernel_size), tuple(stride), tuple(dilation), tuple(is_causal),
+           scale_value)
+    sig = _FWD_CACHE.get(key)
+    if sig is None:
+        sig = _fwd_sig(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_value)
+        if len(_FWD_CACHE) >= _CACHE_MAX:
+            _FWD_CACHE.clear()
+        _FWD_CACHE[key] = sig
+    out = torch.empty(sig.out_shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty(sig.lse_shape, dtype=torch.float32, device=q.device)
+    r = sig.refs[1]
     lib = _lib.load()
-    with torch.cuda.device(q.device):
-        rc = lib.natten_hip_forward(
-            _byref(prob),
-            _lib.ptr(q), _byref(_lib.layout(q, rank, 1)),
-            _lib.ptr(k), _byref(_lib.layout(k, rank, 1)),
-            _lib.ptr(v), _byref(_lib.layout(v, rank, 1)),
-            _lib.ptr(out), _byref(_lib.layout(out, rank, 1)),
-            _lib.ptr(lse), _byref(_lib.layout(lse, rank, 0)),
-            _lib.stream_of(q),
-        )
+    rc = _launch(q.device, lib.natten_hip_forward, ctypes.byref(sig.prob),
+                 q.data_ptr(), r[0], k.data_ptr(), r[1], v.data_ptr(), r[2], out.data_ptr(), r[3],
+                 lse.data_ptr(), r[4], _raw_stream(q.device))
     _lib.check(rc, "forward")
     return out, lse
 
 
-def fused_backward(rank: int, d_out, q, k, v, out, lse, kernel_size, dilation, stride, is_causal, scale,
-                   d_lse=None):
+def _bwd_sig(rank, d_out, q, k, v, out, lse, d_lse, kernel_size, stride, dilation, is_causal, scale_value):
     _check_qkv(rank, q, k, v)
     _on_device(d_out, q, k, v, out, lse, d_lse)
     _same_dtype(d_out, q, k, v, out)
-    q, k, v, out, d_out = (_inner(t) for t in (q, k, v, out, d_out))
+    if lse.dtype != torch.float32 or (d_lse is not None and d_lse.dtype != torch.float32):
+        raise TypeError("lse and its gradient must be float32")
+    sig = _Sig()
+    sig.prob = _fused_problem(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_value)
+    sig.strided = any(s != 1 for s in stride)
+    sig.device = q.device
+    sig.lse_shape = tuple(lse.shape)
+    meta = lambda t: torch.empty(t.shape, dtype=t.dtype, device="meta")  # noqa: E731
+    lays = [_lib.layout(t, rank, 1) for t in (q, k, v, out, d_out)]
+    lays += [_lib.layout(lse, rank, 0), _lib.layout(d_lse, rank, 0) if d_lse is not None else None]
+    lays += [_lib.layout(meta(t), rank, 1) for t in (q, k, v)]
+    lays += [_lib.layout(torch.empty(sig.lse_shape, device="meta"), rank, 0)]
+    sig.refs = [lays, [ctypes.byref(x) if x is not None else None for x in lays]]
+    return sig
+
+
+def fused_backward(rank: int, d_out, q, k, v, out, lse, kernel_size, dilation, stride, is_causal, scale,
+                   d_lse=None):
+    q, k, v, out, d_out = _inner(q), _inner(k), _inner(v), _inner(out), _inner(d_out)
+    if lse.dtype != torch.float32 or not lse.is_contiguous():
+        lse = lse.to(torch.float32).contiguous()
+    if d_lse is not None and (d_lse.dtype != torch.float32 or not d_lse.is_contiguous()):
+        d_lse = d_lse.to(torch.float32).contiguous()
     scale_value = float(q.shape[-1] ** -0.5 if scale is None else scale)
-    prob = _fused_problem(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_value)
-    lse = lse.to(torch.float32)
-    if d_lse is not None:
-        d_lse = d_lse.to(torch.float32)
-    strided = any(s != 1 for s in stride)
-    dq = (torch.zeros if strided else torch.empty)(q.shape, dtype=q.dtype, device=q.device)
+    key = (rank, q.dtype, k.dtype, v.dtype, out.dtype, d_out.dtype, q.device, k.device, v.device, out.device,
+           d_out.device, lse.device, None if d_lse is None else d_lse.device, q.shape, q.stride(), k.shape,
+           k.stride(), v.shape, v.stride(), out.shape, out.stride(), d_out.shape, d_out.stride(), lse.shape,
+           None if d_lse is None else d_lse.shape, tuple(kernel_size), tuple(stride), tuple(dilation),
+           tuple(is_causal), scale_value)
+    sig = _BWD_CACHE.get(key)
+    if sig is None:
+        sig = _bwd_sig(rank, d_out, q, k, v, out, lse, d_lse, kernel_size, stride, dilation, is_causal,
+                       scale_value)
+        if len(_BWD_CACHE) >= _CACHE_MAX:
+            _BWD_CACHE.clear()
+        _BWD_CACHE[key] = sig
+    dq = (torch.zeros if sig.strided else torch.empty)(q.shape, dtype=q.dtype, device=q.device)
     dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
     dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
-    delta = torch.empty(lse.shape, dtype=torch.float32, device=q.device)
+    delta = torch.empty(sig.lse_shape, dtype=torch.float32, device=q.device)
+    r = sig.refs[1]
     lib = _lib.load()
-    L = lambda t, tr: _byref(_lib.layout(t, rank, tr))  # noqa: E731
-    with torch.cuda.device(q.device):
-        rc = lib.natten_hip_backward(
-            _byref(prob),
-            _lib.ptr(q), L(q, 1), _lib.ptr(k), L(k, 1), _lib.ptr(v), L(v, 1),
-            _lib.ptr(out), L(out, 1), _lib.ptr(d_out), L(d_out, 1),
-            _lib.ptr(lse), L(lse, 0),
-            _lib.ptr(d_lse), (L(d_lse, 0) if d_lse is not None else None),
-            _lib.ptr(dq), L(dq, 1), _lib.ptr(dk), L(dk, 1), _lib.ptr(dv), L(dv, 1),
-            _lib.ptr(delta), L(delta, 0),
-            _lib.stream_of(q),
-        )
+    rc = _launch(q.device, lib.natten_hip_backward, ctypes.byref(sig.prob),
+                 q.data_ptr(), r[0], k.data_ptr(), r[1], v.data_ptr(), r[2], out.data_ptr(), r[3],
+                 d_out.data_ptr(), r[4], lse.data_ptr(), r[5],
+                 d_lse.data_ptr() if d_lse is not None else None, r[6],
+                 dq.data_ptr(), r[7], dk.data_ptr(), r[8], dv.data_ptr(), r[9], delta.data_ptr(), r[10],
+                 _raw_stream(q.device))
     _lib.check(rc, "backward")
     return dq, dk, dv
 

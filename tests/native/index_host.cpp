@@ -73,4 +73,32 @@ long long host_inverse_mismatch(const natten_problem_t* p) {
     return bad;
 }
 
+// Class-coordinate closed forms (class_ws, class_span) against the window
+// rule on positions and brute-force membership, for every residue class of
+// axis 2.  Returns the number of disagreements.
+long long host_class_mismatch(const natten_problem_t* p) {
+    const na::Prob P = make(p);
+    const na::Axis& A = P.ax[2];
+    long long bad = 0;
+    for (int r = 0; r < A.dil; ++r) {
+        const na::ClassAxis c = na::class_axis(A, r);
+        if (c.n != (A.len - r + A.dil - 1) / A.dil) ++bad;
+        for (int j = 0; j < c.n; ++j) {
+            const int want = (na::axis_first(A, r + j * A.dil) - r) / A.dil;
+            if (na::class_ws(c, j) != want) ++bad;
+        }
+        for (int u = 0; u < c.n; ++u) {
+            int lo, hi;
+            na::class_span(c, u, lo, hi);
+            for (int j = 0; j < c.n; ++j) {
+                const int ws = na::class_ws(c, j);
+                const bool member = u >= ws && u <= ws + A.k - 1 && u >= 0;
+                const bool in = j >= lo && j <= hi;
+                if (member != in) ++bad;
+            }
+        }
+    }
+    return bad;
+}
+
 }  // extern "C"

@@ -32,7 +32,24 @@ def host_idx():
     lib.host_neighbor_map.argtypes = [ctypes.POINTER(_lib.Problem), ctypes.c_void_p, ctypes.c_void_p]
     lib.host_inverse_mismatch.argtypes = [ctypes.POINTER(_lib.Problem)]
     lib.host_inverse_mismatch.restype = ctypes.c_longlong
+    lib.host_class_mismatch.argtypes = [ctypes.POINTER(_lib.Problem)]
+    lib.host_class_mismatch.restype = ctypes.c_longlong
     return lib
+
+
+def test_class_coordinate_closed_forms(host_idx):
+    """The division-free class-coordinate window start and inverse span used
+    by the MFMA tile kernels equal the window rule and brute-force membership
+    for every (L, K, d, causal, residue) with L <= 30."""
+    n = 0
+    for L, K, d in _sweep_starts(30):
+        if d == 1 and K % 2 == 0 and K == L:
+            continue
+        for c in (False, True):
+            assert host_idx.host_class_mismatch(ctypes.byref(_problem((L,), (K,), (d,), (1,), (c,)))) == 0, \
+                (L, K, d, c)
+            n += 1
+    assert n > 1000
 
 
 @pytest.fixture(scope="module")
