@@ -14,7 +14,8 @@ from typing import Optional, Sequence
 import torch
 
 LIB_NAME = "libnatten_hip.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), LIB_NAME)
+LIB_PATH = os.environ.get("NATTEN_HIP_LIB") or os.path.join(
+    os.path.dirname(os.path.dirname(os.path.abspath(__file__))), LIB_NAME)
 ABI_VERSION = 1
 
 F32, F16, BF16 = 0, 1, 2

@@ -1,9 +1,10 @@
 """Pins the CPU oracle (oracle/pure.py) and the host composition layer to the
 reference's own outputs: every golden case written from the reference by
 tests/golden/make_golden.py.  Forward outputs and index maps must match bit
-for bit on the same torch build; gradients within 1e-6, because torch's CPU
-backward of the neighbour gather accumulates in a thread-dependent order
-(two runs of the reference itself differ by ~2e-7)."""
+for bit on the same torch build; fp32 gradients within atol 5e-6 / rtol 1e-5,
+because torch's CPU backward of the neighbour gather accumulates in a
+thread-dependent order (two runs of the reference itself differ by up to
+~1e-6 on O(0.1) values; a dropped or misplaced term moves them by O(1e-2))."""
 from __future__ import annotations
 
 import hashlib
@@ -30,8 +31,10 @@ def _version(golden):
 
 
 def _close_grad(a, b):
-    tol = 1e-6 if a.dtype == torch.float32 else 1e-2
-    torch.testing.assert_close(a, b, atol=tol, rtol=tol)
+    if a.dtype == torch.float32:
+        torch.testing.assert_close(a, b, atol=5e-6, rtol=1e-5)
+    else:
+        torch.testing.assert_close(a, b, atol=1e-2, rtol=1e-2)
 
 
 def _grads(fn, inputs, out_grad):
