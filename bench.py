@@ -1,11 +1,14 @@
 """Benchmark of the hot path: na2d forward+backward, DiNAT scale
 (B=16, 56x56, 4 heads, head dim 32, kernel 7, bf16), on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--dilation 1] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--dilation 1] [--no-cpu] [--no-graph]
 
 A step is one forward + backward pass through the public API
 (``natten_mps_amd.na2d`` then ``torch.autograd.grad``) on synthetic seeded
-inputs already resident in HBM.  Prints one JSON line (rank 0):
+inputs already resident in HBM.  The step is timed eagerly and, captured
+once in a HIP graph (torch.cuda.CUDAGraph), as graph replays whose outputs
+are checked equal to eager steps; the step time reported is the replay's
+(the eager one is in ``config.eager_ms_per_step``).  Prints one JSON line:
 
 * value / unit: effective TFLOP/s = (fwd 4*P*D + bwd 10*P*D) / step time,
   with P = B * Hq * (valid query-key pairs of the neighbourhood map);
@@ -107,6 +110,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--dilation", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-graph", action="store_true", help="time eager steps only")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -140,25 +144,58 @@ def main():
     torch.cuda.synchronize()
     _lib.profile_read(reset=True)
 
-    def timed(profile):
+    def timed(run, profile=False):
         _lib.profile_enable(profile)
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         start.record()
         for _ in range(args.steps):
-            step()
+            run()
         stop.record()
         torch.cuda.synchronize()
         _lib.profile_enable(False)
         return start.elapsed_time(stop) / args.steps
 
-    # the step time is taken with the per-launch event timing off; the same K
-    # steps are then repeated with every library launch bracketed by HIP events
-    # on its stream, which gives the per-kernel durations for the roofline
-    ms = timed(False)
-    ms_profiled = timed(True)
+    # eager step time with the per-launch event timing off; the same K steps
+    # are then repeated with every library launch bracketed by HIP events on
+    # its stream, which gives the per-kernel durations for the roofline
+    ms_eager = timed(step)
+    ms_profiled = timed(step, profile=True)
     stats = _lib.profile_read(reset=True)
-    _log(f"step {ms:.4f} ms (with per-launch events: {ms_profiled:.4f} ms)")
+    _log(f"eager step {ms_eager:.4f} ms (with per-launch events: {ms_profiled:.4f} ms)")
+
+    # the same step captured once in a HIP graph (forward + autograd backward)
+    # and replayed: identical kernels and buffers without the per-step host
+    # work.  Every replay is checked bit for bit against an eager step, with
+    # eager work and synchronisation between the replays.
+    ms_graph, graph_ok = None, False
+    if not args.no_graph:
+        try:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    step()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                g_out = step()
+            ref = [t.clone() for t in step()]
+            graph_ok = True
+            for _ in range(3):
+                graph.replay()
+                torch.cuda.synchronize()
+                graph_ok &= all(torch.equal(a, b) for a, b in zip(g_out, ref))
+                ref = [t.clone() for t in step()]
+                torch.cuda.synchronize()
+            if graph_ok:
+                ms_graph = timed(graph.replay)
+                _log(f"graph step {ms_graph:.4f} ms")
+            else:
+                _log("graph replay differs from the eager step; reporting the eager time")
+        except Exception as e:  # capture is an optimisation of the timing, never required
+            _log("graph capture failed:", repr(e))
+    ms = ms_graph if ms_graph is not None else ms_eager
 
     pairs = B * Hq * _valid_pairs((H, W), (K, K), (dil, dil), (1, 1), (False, False), dev)
     flops = 14.0 * pairs * D
@@ -204,6 +241,8 @@ def main():
         "data": "synthetic (seeded randn, resident in HBM)",
         "config": {"workload": f"na2d fwd+bwd B=16 56x56 heads=4 dim=32 K=7 dilation={dil} bf16 (BASELINE config 3)",
                    "global_batch": B, "seq_len": H * W, "parallelism": "single GPU",
+                   "timing": "HIP graph replay of the eager step (checked equal)" if ms_graph is not None
+                   else "eager", "eager_ms_per_step": round(ms_eager, 4),
                    "hbm_floor_frac_step": round(fwd_bwd_bytes / 8e12 / (ms * 1e-3), 4)},
         "roofline": roof,
         "cpu_baseline": cpu,

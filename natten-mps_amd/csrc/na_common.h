@@ -99,6 +99,30 @@ __host__ __device__ inline bool axis_query_range(const Axis& a, int m, int& t_lo
     return lo <= hi;
 }
 
+// Division by an invariant d >= 1 of 0 <= n < 2^31 with one multiply-high:
+// with l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1,
+//   n / d = (mulhi(n, m) + n) >> l
+// (the round-up method of Granlund and Montgomery, "Division by invariant
+// integers using multiplication", 1994; n + mulhi stays below 2^32 for
+// n < 2^31).  The kernels decode workgroup indices with it, in scalar
+// registers, instead of the emulated integer division.
+struct FastDiv {
+    uint32_t mul, shift, d;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    const uint64_t m = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+    return FastDiv{static_cast<uint32_t>(m), l, d};
+}
+
+__host__ __device__ inline int fdiv(int n, const FastDiv& f) {
+    const uint32_t u = static_cast<uint32_t>(n);
+    const uint32_t hi = static_cast<uint32_t>((static_cast<uint64_t>(u) * f.mul) >> 32);
+    return static_cast<int>((hi + u) >> f.shift);
+}
+
 // Residue-class view of one axis.  With dilation d the positions r, r+d, ...
 // form class r with n = ceil((L - r)/d) members; a window never leaves its
 // class and, in class coordinates j = (i - r)/d, is the undilated run

@@ -5,22 +5,42 @@
 // every key of its window share the class, and inside a class the window is
 // an undilated run of K positions (class coordinates j = (i - r) / d).  A
 // workgroup owns a box of up to 64 queries (or keys) of one class triple
-// (r0, r1, r2) and one (batch, head).  The union of their windows (or, for
-// keys, of the queries attending them) is a box in class coordinates, staged
-// one axis-0 plane ("slice") at a time in LDS, slot = (u1-lo1)*U2 + (u2-lo2),
-// zero padded to a multiple of 32, both row-major (Xs[slot][D]) and, where a
-// product contracts over slots, transposed (Xt[D][slot]).
+// (r0, r1, r2) and one (batch, head), with power-of-two extents T[a].  The
+// union of their windows (or, for keys, of the queries attending them) is a
+// box in class coordinates, staged one axis-0 plane ("slice") at a time in
+// LDS: slot = a1 * rowlen + a2 for union row a1 and column a2, rowlen =
+// 2^rowshift >= 8, the slot count padded to a multiple of 32.
+//
+// LDS holds each staged operand once, row-major X[slot][D], the 16-byte
+// pieces of a row permuted by an XOR swizzle of the slot (spreads the MFMA
+// operand reads over the banks).  Rows arrive straight from global memory
+// through buffer loads into LDS (no register round trip); slots outside the
+// union load out of the buffer's range and land as zeros.  Products that
+// contract over slots read their operand transposed with ds_read_b64_tr_b16.
 //
 // Each wave owns 16 queries (keys) and walks the staged slots 32 at a time
-// with v_mfma_f32_16x16x32: the score block is computed with the slots as
-// MFMA rows, split over two 16-row blocks whose rows interleave so that every
-// lane ends up holding 8 consecutive slots of one query (key) -- exactly the
-// B-operand layout of the following product that contracts over those slots.
+// ("chunks") with v_mfma_f32_16x16x32: the score block is computed with the
+// slots as MFMA rows, split over two 16-row blocks whose rows interleave so
+// that every lane ends up holding 8 consecutive slots of one query (key) --
+// exactly the B-operand layout of the following product over those slots.
+//
+// Masking.  A lane's 8 slots lie in one union row (rowlen >= 8), so the
+// window test splits into a row test (one per lane and chunk) and a column
+// test, which is fixed per lane for the whole tile when rows are at most 32
+// slots.  Columns enter the score MFMA as its accumulator input (0 or -inf);
+// a failed row test moves the lane's exponent offset to -inf, so its
+// probabilities come out exactly 0.
+//
 // Softmax runs in the log2 domain in fp32; probabilities and score gradients
 // enter the second product rounded to the input dtype, accumulators are fp32.
+// Row sums of the forward come from the same rounded probabilities through
+// one more MFMA against a block of ones.
 //
 // MFMA lane layout (16x16x32): A row = lane%16, B column = lane%16, both with
 // k = 8*(lane/16) .. +7; C column = lane%16, rows 4*(lane/16) .. +3.
+#include <cstdlib>
+#include <cstring>
+
 #include "na_launch.h"
 
 namespace na {
@@ -33,16 +53,23 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kPad = 8;  // elements of padding per LDS row (spreads rows over banks)
+constexpr int kMaxItems = 64;
+// buffer range of a staged plane; out-of-union slots read at kOutOfRange
+constexpr int kPlaneBytes = 0x7FFFFFF0;
+constexpr uint32_t kOutOfRange = 0x80000000u;
 
 template <typename T>
 struct Mma;
 
 template <>
 struct Mma<bf16> {
+    static constexpr uint32_t kOnes = 0x3F803F80u;  // two bf16 1.0
     __device__ static __forceinline__ f32x4_t run(uint4 a, uint4 b, f32x4_t c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                        __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
@@ -54,6 +81,7 @@ struct Mma<bf16> {
 
 template <>
 struct Mma<f16> {
+    static constexpr uint32_t kOnes = 0x3C003C00u;  // two fp16 1.0
     __device__ static __forceinline__ f32x4_t run(uint4 a, uint4 b, f32x4_t c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
                                                       __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
@@ -64,47 +92,56 @@ struct Mma<f16> {
 };
 
 template <typename T>
-__device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
-    return make_uint4(Mma<T>::pack(v[0], v[1]), Mma<T>::pack(v[2], v[3]), Mma<T>::pack(v[4], v[5]),
-                      Mma<T>::pack(v[6], v[7]));
+__device__ __forceinline__ uint4 pack8(const f32x4_t (&v)[2]) {
+    return make_uint4(Mma<T>::pack(v[0][0], v[0][1]), Mma<T>::pack(v[0][2], v[0][3]),
+                      Mma<T>::pack(v[1][0], v[1][1]), Mma<T>::pack(v[1][2], v[1][3]));
 }
 
-__device__ __forceinline__ int imin16(int v) {
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) v = min(v, __shfl_xor(v, m));
-    return v;
+// Reductions over the four 16-lane rows of the wave (lanes i, i+16, i+32,
+// i+48): v_permlane16_swap / v_permlane32_swap exchange rows between two
+// registers, here both the same value.
+__device__ __forceinline__ float max_rows(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-__device__ __forceinline__ int imax16(int v) {
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) v = max(v, __shfl_xor(v, m));
-    return v;
+__device__ __forceinline__ float sum_rows(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-__device__ __forceinline__ float sum_groups(float v) {
-    v += __shfl_xor(v, 16);
-    return v + __shfl_xor(v, 32);
+__device__ __forceinline__ float max8(const f32x4_t (&s)[2]) {
+    return fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                 fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
 }
 
-__device__ __forceinline__ float max_groups(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16));
-    return fmaxf(v, __shfl_xor(v, 32));
+// XOR swizzle of the 16-byte pieces of LDS row `row` (D / 8 pieces per row):
+// the 16 rows one score-operand read touches (rows 8x + y + 4b, x, y < 4)
+// land on distinct banks for every head dim.
+template <int D>
+__device__ __forceinline__ int swz(int row) {
+    if constexpr (D == 32) return (row >> 3) & 3;
+    else if constexpr (D == 64) return (((row >> 3) & 3) << 1) | ((row >> 1) & 1);
+    else return (((row >> 3) & 3) << 2) | (row & 3);
 }
+
+__device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 }  // namespace
 
-// Host-chosen tile: extents (class coordinates) of a workgroup's box, tiles
-// per class per axis, waves per workgroup, and the staged slice layout: slot
-// = a1 * rowlen + a2 for union row a1 and column a2, with rowlen = 2^rowshift
-// >= 8 covering the widest union row (so a lane's 8 consecutive slots never
-// straddle two rows), `slots` = staged slots per slice (multiple of 32).
+// Host-chosen tile: power-of-two extents T = 2^tshift (class coordinates) of a
+// workgroup's box, tiles per class per axis, waves per workgroup, the staged
+// slice layout (slot = a1 * 2^rowshift + a2, `slots` per slice, a multiple of
+// 32), len % dil per axis, and divisors for decoding the workgroup index.
 struct TileShape {
-    int T[3];
-    int ntile[3];
-    int waves;
-    int slots;
-    int rowlen;
-    int rowshift;
+    int T[3], tshift[3], ntile[3];
+    int waves, slots, rowshift;
+    int lenmod[3];
+    FastDiv heads, rep, tiles[3], dil[3];
 };
 
 namespace {
@@ -114,24 +151,36 @@ struct Block {
     ClassAxis c[3];
 };
 
+__device__ __forceinline__ ClassAxis class_axis_of(const Axis& a, int r, const FastDiv& dil, int lenmod) {
+    ClassAxis c;
+    c.n = a.dil == 1 ? a.len : fdiv(a.len - r + a.dil - 1, dil);
+    c.K = a.k;
+    c.h = a.k >> 1;
+    c.causal = a.causal;
+    c.B = (a.dil == 1 || r < lenmod) ? c.n - 1 - 2 * c.h : c.n - a.k;
+    return c;
+}
+
 // Workgroup -> (batch, head, residues, tile origin J, clipped extent E) and
 // the union box [lo, lo+U) of the windows of its queries (key_tile = false)
 // or of the queries attending its keys (key_tile = true).  False: empty tile.
-__device__ __forceinline__ bool decode_block(const Prob& p, const TileShape& ts, int heads, bool key_tile,
-                                             Block& k) {
-    int bid = xcd_block(blockIdx.x, gridDim.x);
-    k.h = bid % heads;
-    bid /= heads;
+__device__ __forceinline__ bool decode_block(const Prob& p, const TileShape& ts, bool key_tile, Block& k) {
+    int x = xcd_block(blockIdx.x, gridDim.x);
+    int q = fdiv(x, ts.heads);
+    k.h = x - q * static_cast<int>(ts.heads.d);
+    x = q;
     int t[3];
     for (int a = 2; a >= 0; --a) {
-        t[a] = bid % ts.ntile[a];
-        bid /= ts.ntile[a];
-        k.r[a] = bid % p.ax[a].dil;
-        bid /= p.ax[a].dil;
+        q = fdiv(x, ts.tiles[a]);
+        t[a] = x - q * static_cast<int>(ts.tiles[a].d);
+        x = q;
+        q = fdiv(x, ts.dil[a]);
+        k.r[a] = x - q * static_cast<int>(ts.dil[a].d);
+        x = q;
     }
-    k.b = bid;
+    k.b = x;
     for (int a = 0; a < 3; ++a) {
-        const ClassAxis c = class_axis(p.ax[a], k.r[a]);
+        const ClassAxis c = class_axis_of(p.ax[a], k.r[a], ts.dil[a], ts.lenmod[a]);
         k.c[a] = c;
         k.J[a] = t[a] * ts.T[a];
         const int jend = min(k.J[a] + ts.T[a], c.n) - 1;
@@ -145,9 +194,9 @@ __device__ __forceinline__ bool decode_block(const Prob& p, const TileShape& ts,
             // both span ends are non-decreasing in the key; keys attended by
             // nobody (only past the last window at an even-kernel border) sit
             // at the end and leave hi unchanged
-            int x;
-            class_span(c, k.J[a], lo, x);
-            class_span(c, jend, x, hi);
+            int x2;
+            class_span(c, k.J[a], lo, x2);
+            class_span(c, jend, x2, hi);
         }
         k.lo[a] = lo;
         k.U[a] = hi >= lo ? hi - lo + 1 : 0;
@@ -155,158 +204,189 @@ __device__ __forceinline__ bool decode_block(const Prob& p, const TileShape& ts,
     return true;
 }
 
-// Stage the slice of the union at axis-0 position p0 (all slots < `slots`):
-// rows[slot][D] row-major and/or trans[D][slot] transposed, zeros past the
-// union.  Offsets inside one (batch, head, axis-0 plane) fit in 32 bits
-// (checked on the host).
+// Admissible box of a query (its window) or key (its attending queries) in
+// class coordinates.
+__device__ __forceinline__ void item_box(const ClassAxis& c, int j, bool key_side, int& lo, int& hi) {
+    if (!key_side) {
+        lo = class_ws(c, j);
+        hi = lo + c.K - 1;
+    } else {
+        class_span(c, j, lo, hi);
+    }
+}
+
+// The wave's part of the tile: items f = 16w .. 16w+15 in row-major tile
+// order; with power-of-two extents they cover a box.  Its admissible box
+// (union-relative, clipped to the union) follows from the box corners since
+// window ends are non-decreasing per axis.  Chunks c0..c1 cover it.
+struct WaveGeo {
+    bool any;
+    int lo[3], hi[3];
+    int c0, c1;
+};
+
+__device__ __forceinline__ WaveGeo wave_geo(const TileShape& ts, const Block& k, int wave, bool key_side) {
+    WaveGeo g;
+    const int f0 = wave * 16, s2 = ts.tshift[2], s1 = ts.tshift[1];
+    int lo[3], hi[3];
+    if (ts.T[2] >= 16) {
+        lo[2] = f0 & (ts.T[2] - 1);
+        hi[2] = lo[2] + 15;
+        lo[1] = hi[1] = (f0 >> s2) & (ts.T[1] - 1);
+        lo[0] = hi[0] = f0 >> (s2 + s1);
+    } else if (ts.T[2] * ts.T[1] >= 16) {
+        lo[2] = 0;
+        hi[2] = ts.T[2] - 1;
+        lo[1] = (f0 >> s2) & (ts.T[1] - 1);
+        hi[1] = lo[1] + (16 >> s2) - 1;
+        lo[0] = hi[0] = f0 >> (s2 + s1);
+    } else {
+        lo[2] = 0;
+        hi[2] = ts.T[2] - 1;
+        lo[1] = 0;
+        hi[1] = ts.T[1] - 1;
+        lo[0] = f0 >> (s2 + s1);
+        hi[0] = lo[0] + (16 >> (s2 + s1)) - 1;
+    }
+    g.any = true;
+    for (int a = 0; a < 3; ++a) {
+        hi[a] = min(hi[a], k.E[a] - 1);
+        if (lo[a] > hi[a]) g.any = false;
+    }
+    for (int a = 0; a < 3; ++a) {
+        int l0, h0, l1, h1;
+        item_box(k.c[a], k.J[a] + lo[a], key_side, l0, h0);
+        item_box(k.c[a], k.J[a] + max(hi[a], lo[a]), key_side, l1, h1);
+        g.lo[a] = max(l0 - k.lo[a], 0);
+        g.hi[a] = min(h1 - k.lo[a], k.U[a] - 1);
+        if (g.lo[a] > g.hi[a]) g.any = false;
+    }
+    g.c0 = (g.lo[1] * (1 << ts.rowshift) + g.lo[2]) >> 5;
+    g.c1 = (g.hi[1] * (1 << ts.rowshift) + g.hi[2]) >> 5;
+    return g;
+}
+
+// One lane's query (or key): validity, position and admissible box
+// (union-relative; empty on axis 0 for lanes past the tile).
+struct Lane {
+    bool valid;
+    int pos[3], lo[3], hi[3];
+};
+
+__device__ __forceinline__ Lane lane_item(const Prob& p, const TileShape& ts, const Block& k, int wave, int col,
+                                          bool key_side) {
+    Lane ln;
+    const int f = wave * 16 + col, s2 = ts.tshift[2], s1 = ts.tshift[1];
+    int e[3];
+    e[2] = f & (ts.T[2] - 1);
+    e[1] = (f >> s2) & (ts.T[1] - 1);
+    e[0] = f >> (s2 + s1);
+    ln.valid = e[0] < k.E[0] && e[1] < k.E[1] && e[2] < k.E[2];
+    for (int a = 0; a < 3; ++a) {
+        const int j = k.J[a] + (ln.valid ? e[a] : 0);
+        ln.pos[a] = k.r[a] + j * p.ax[a].dil;
+        int lo, hi;
+        item_box(k.c[a], j, key_side, lo, hi);
+        ln.lo[a] = lo - k.lo[a];
+        ln.hi[a] = hi - k.lo[a];
+    }
+    if (!ln.valid) {
+        ln.lo[0] = 1 << 30;
+        ln.hi[0] = -1;
+    }
+    return ln;
+}
+
+// Column part of the mask for chunk c as the score MFMA's accumulator input:
+// 0 where the lane's slot 32c + 8grp + 4b + i lies in its column range, -inf
+// elsewhere.
+__device__ __forceinline__ void column_bias(const Lane& ln, int rowshift, int c, int grp, f32x4_t (&bias)[2]) {
+    const int col0 = (32 * c + 8 * grp) & ((1 << rowshift) - 1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int cc = col0 + e;
+        bias[e >> 2][e & 3] = (cc >= ln.lo[2] && cc <= ln.hi[2]) ? 0.f : -INFINITY;
+    }
+}
+
+__device__ __forceinline__ bool row_ok(const Lane& ln, int rowshift, bool in0, int c, int grp) {
+    const int row = (32 * c + 8 * grp) >> rowshift;
+    return in0 && row >= ln.lo[1] && row <= ln.hi[1];
+}
+
+template <typename T>
+__device__ __forceinline__ const T* plane_of(const T* g, const Lay& lay, int b, int h, int p0) {
+    return g + static_cast<long long>(b) * lay.b + static_cast<long long>(h) * lay.h +
+           static_cast<long long>(p0) * lay.s0;
+}
+
+// Stage the union slice of one axis-0 plane (base `plane`) into X[slot][D]:
+// each wave instruction moves 64 / (D/8) rows, lane l the 16-byte piece
+// l % (D/8) of row l / (D/8), holding logical piece (l % (D/8)) ^ swz(row).
+// In-plane offsets fit in 31 bits and strides are non-negative (checked on
+// the host).
 template <typename T, int D>
-__device__ __forceinline__ void stage(const Prob& p, const Block& k, const TileShape& ts, const T* __restrict__ g,
-                                      Lay lay, int h, int p0, T* rows, T* trans) {
-    constexpr int V8 = D / 8;
-    const int slots = ts.slots;
-    const int part = threadIdx.x % V8;
-    const T* base = g + static_cast<long long>(k.b) * lay.b + static_cast<long long>(h) * lay.h +
-                    static_cast<long long>(p0) * lay.s0 + part * 8;
-    const int s1 = static_cast<int>(lay.s1), s2 = static_cast<int>(lay.s2);
+__device__ __forceinline__ void stage_rows(const Prob& p, const Block& k, const TileShape& ts, const T* plane,
+                                           const Lay& lay, T* X, int wave, int lane) {
+    constexpr int P = D / 8, RPI = 64 / P;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(plane), static_cast<short>(0), kPlaneBytes, 0x00020000);
     const int d1 = p.ax[1].dil, d2 = p.ax[2].dil;
     const int c1 = k.r[1] + k.lo[1] * d1, c2 = k.r[2] + k.lo[2] * d2;
-#pragma unroll 2
-    for (int sp = threadIdx.x / V8; 2 * sp < slots; sp += blockDim.x / V8) {
-        // the pair 2sp, 2sp+1 shares a union row (rowlen is even)
-        const int a1 = (2 * sp) >> ts.rowshift, a2 = (2 * sp) & (ts.rowlen - 1);
-        const bool row_ok = a1 < k.U[1];
-        const T* src = base + (c1 + a1 * d1) * s1 + (c2 + a2 * d2) * s2;
-        uint4 x[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            x[e] = make_uint4(0, 0, 0, 0);
-            if (row_ok && a2 + e < k.U[2]) x[e] = *reinterpret_cast<const uint4*>(src + e * d2 * s2);
-        }
-        if (rows) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e) *reinterpret_cast<uint4*>(rows + (2 * sp + e) * (D + kPad) + part * 8) = x[e];
-        }
-        if (trans) {
-            const uint16_t* a = reinterpret_cast<const uint16_t*>(&x[0]);
-            const uint16_t* b = reinterpret_cast<const uint16_t*>(&x[1]);
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                *reinterpret_cast<uint32_t*>(trans + (part * 8 + j) * (slots + kPad) + 2 * sp) =
-                    static_cast<uint32_t>(a[j]) | (static_cast<uint32_t>(b[j]) << 16);
-        }
+    const int s1 = static_cast<int>(lay.s1), s2 = static_cast<int>(lay.s2);
+    const int mask2 = (1 << ts.rowshift) - 1;
+    const int n_inst = ts.slots / RPI;
+    for (int i = wave; i < n_inst; i += ts.waves) {
+        const int slot = i * RPI + lane / P;
+        const int kb = (lane % P) ^ swz<D>(slot);
+        const int a1 = slot >> ts.rowshift, a2 = slot & mask2;
+        const bool ok = a1 < k.U[1] && a2 < k.U[2];
+        const uint32_t off =
+            ok ? static_cast<uint32_t>(((c1 + a1 * d1) * s1 + (c2 + a2 * d2) * s2 + kb * 8) * static_cast<int>(sizeof(T)))
+               : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(X + i * RPI * D), 16, off, 0, 0, 0);
     }
 }
 
-// Stage per-slot fp32 values (lse in the log2 domain, delta) of the slice.
-__device__ __forceinline__ void stage_scalars(const Prob& p, const Block& k, const TileShape& ts, int h, int p0,
-                                              const float* __restrict__ lse, Lay ll, const float* __restrict__ delta,
-                                              Lay lde, float* L2s, float* Ds) {
-    for (int s = threadIdx.x; s < ts.slots; s += blockDim.x) {
-        float l2 = 0.f, dd = 0.f;
-        const int a1 = s >> ts.rowshift, a2 = s & (ts.rowlen - 1);
-        if (a1 < k.U[1] && a2 < k.U[2]) {
-            const int p1 = k.r[1] + (k.lo[1] + a1) * p.ax[1].dil, p2 = k.r[2] + (k.lo[2] + a2) * p.ax[2].dil;
-            l2 = lse[ll.at(k.b, p0, p1, p2, h)] * kLog2e;
-            dd = delta[lde.at(k.b, p0, p1, p2, h)];
-        }
-        L2s[s] = l2;
-        Ds[s] = dd;
-    }
-}
-
-// One lane's query (or key) of the wave: class coordinates and position.
-struct Item {
-    bool valid;
-    int j[3], pos[3];
-};
-
-__device__ __forceinline__ Item wave_item(const Prob& p, const Block& k, int wave, int col) {
-    Item it;
-    const int n = k.E[0] * k.E[1] * k.E[2];
-    const int f = wave * 16 + col;
-    it.valid = f < n;
-    const int ff = it.valid ? f : 0;
-    const int e2 = ff % k.E[2], e1 = (ff / k.E[2]) % k.E[1], e0 = ff / (k.E[2] * k.E[1]);
-    const int e[3] = {e0, e1, e2};
-    for (int a = 0; a < 3; ++a) {
-        it.j[a] = k.J[a] + e[a];
-        it.pos[a] = k.r[a] + it.j[a] * p.ax[a].dil;
-    }
-    return it;
-}
-
-// The lane's admissible box in union-relative coordinates [rel_lo, rel_hi]
-// per axis (windows for a query, attending queries for a key), and the
-// wave-wide slot range covering all of them (for skipping slices/chunks).
-struct Span {
-    int lo[3], hi[3];   // lane, relative to the union origin
-    int wlo[3], whi[3]; // wave
-};
-
-__device__ __forceinline__ Span lane_span(const Prob& p, const Block& k, const Item& it, bool key_side) {
-    Span sp;
-    for (int a = 0; a < 3; ++a) {
-        int lo, hi;
-        if (!key_side) {
-            lo = class_ws(k.c[a], it.j[a]);
-            hi = lo + k.c[a].K - 1;
-        } else {
-            class_span(k.c[a], it.j[a], lo, hi);
-        }
-        sp.lo[a] = lo - k.lo[a];
-        sp.hi[a] = hi - k.lo[a];
-        const bool live = it.valid && lo <= hi;
-        sp.wlo[a] = imin16(live ? max(sp.lo[a], 0) : 1 << 30);
-        sp.whi[a] = imax16(live ? min(sp.hi[a], k.U[a] - 1) : -(1 << 30));
-    }
-    return sp;
-}
-
-// Bit e set when slot s0 + e (s0 a multiple of 8, so all in one union row) is
-// admissible for this lane: its row in [lo1, hi1] and column in [lo2, hi2].
-// Padding columns lie past hi2 and padding rows past hi1.
-__device__ __forceinline__ unsigned chunk_mask(const Span& sp, bool in0, int s0, const TileShape& ts) {
-    const int a1 = s0 >> ts.rowshift, a2 = s0 & (ts.rowlen - 1);
-    if (!in0 || a1 < sp.lo[1] || a1 > sp.hi[1]) return 0u;
-    const int lo = sp.lo[2] - a2, hi = sp.hi[2] - a2;  // admissible bit range
-    if (hi < 0 || lo > 7) return 0u;
-    return (0xFFu << (lo > 0 ? lo : 0)) & (0xFFu >> (hi < 7 ? 7 - hi : 0));
-}
-
-// First and last chunk covering the wave's admissible box.
-__device__ __forceinline__ void chunk_range(const Span& sp, const TileShape& ts, int& c0, int& c1) {
-    c0 = (sp.wlo[1] * ts.rowlen + sp.wlo[2]) >> 5;
-    c1 = (sp.whi[1] * ts.rowlen + sp.whi[2]) >> 5;
-}
-
-// Score block: rows = 32 slots of chunk c (A operand from row-major LDS),
-// columns = the wave's 16 items (B operand fragments).  Returns the lane's 8
-// slots 32c + 8grp + [0..7] in order.
+// Score block of chunk c: rows = its 32 slots (A operand, row-major X),
+// columns = the wave's 16 items (B fragments); out[b] starts from bias[b].
+// The lane receives slots 32c + 8grp + 4b + i (i < 4) in out[b][i].
 template <typename T, int D>
-__device__ __forceinline__ void score_chunk(const T* rows, int c, int col, int grp, const uint4 (&frag)[D / 32],
-                                            float (&out)[8]) {
+__device__ __forceinline__ void score_chunk(const T* X, int c, int col, int grp, const uint4 (&frag)[D / 32],
+                                            const f32x4_t (&bias)[2], f32x4_t (&out)[2]) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         const int row = 32 * c + 8 * (col >> 2) + 4 * b + (col & 3);
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        f32x4_t acc = bias[b];
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) {
-            const uint4 a = *reinterpret_cast<const uint4*>(rows + row * (D + kPad) + ks * 32 + grp * 8);
+            const int kb = (ks * 4 + grp) ^ swz<D>(row);
+            const uint4 a = *reinterpret_cast<const uint4*>(X + row * D + kb * 8);
             acc = Mma<T>::run(a, frag[ks], acc);
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) out[4 * b + i] = acc[i];
+        out[b] = acc;
     }
 }
 
-// acc[db] (16 head dims x 16 items) += trans[d][32 slots of chunk c] * packed.
+// acc[db] (16 head dims x 16 items) += X^T[db*16 .. +15][32 slots of chunk c]
+// * packed.  The A operand (row = head dim, k = 8 consecutive slots) comes
+// from row-major X through two transposing reads: in 16-lane row g, lane j
+// points at X[32c + 8g + j/4 (+4)][db*16 + 4(j%4) ..] and lane i receives
+// X[32c + 8g + m (+4)][db*16 + i], m < 4.
 template <typename T, int D>
-__device__ __forceinline__ void accumulate_chunk(const T* trans, int slots, int c, int col, int grp, uint4 packed,
-                                                 f32x4_t (&acc)[D / 16]) {
+__device__ __forceinline__ void accumulate_chunk(const T* X, int c, int lane, uint4 packed, f32x4_t (&acc)[D / 16]) {
+    const int g = lane >> 4, j = lane & 15;
+    const int r0 = 32 * c + 8 * g + (j >> 2), r1 = r0 + 4;
+    const int sub = (j & 1) * 4;
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
-        const uint4 a = *reinterpret_cast<const uint4*>(trans + (db * 16 + col) * (slots + kPad) + 32 * c + 8 * grp);
-        acc[db] = Mma<T>::run(a, packed, acc[db]);
+        const int kb = 2 * db + ((j & 3) >> 1);
+        const T* a0 = X + r0 * D + ((kb ^ swz<D>(r0)) * 8) + sub;
+        const T* a1 = X + r1 * D + ((kb ^ swz<D>(r1)) * 8) + sub;
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)a0);
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)a1);
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+        acc[db] = Mma<T>::run(make_uint4(l2.x, l2.y, h2.x, h2.y), packed, acc[db]);
     }
 }
 
@@ -330,8 +410,12 @@ __device__ __forceinline__ void store_rows(T* __restrict__ g, long long off, int
     }
 }
 
+__device__ __forceinline__ int kv_head(const TileShape& ts, int h) { return ts.rep.d == 1 ? h : fdiv(h, ts.rep); }
+
 // ---------------------------------------------------------------------------
 // Forward: out = softmax(scale q.k) v over each window, lse (natural log).
+// Online softmax over groups of up to 4 chunks (one max reduction and one
+// rescale per group).
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T* __restrict__ q, Lay lq,
@@ -340,67 +424,85 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T*
                                                   Lay ll) {
     extern __shared__ __align__(16) unsigned char smem[];
     Block blk;
-    if (!decode_block(p, ts, p.Hq, false, blk)) return;
-    const int slots = ts.slots;
+    if (!decode_block(p, ts, false, blk)) return;
     T* Ks = reinterpret_cast<T*>(smem);
-    T* Vt = Ks + slots * (D + kPad);
+    T* Vs = Ks + ts.slots * D;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, grp = lane >> 4;
-    const int hk = blk.h / p.rep;
+    const int hk = kv_head(ts, blk.h);
 
-    const Item it = wave_item(p, blk, wave, col);
-    const Span sp = lane_span(p, blk, it, false);
+    const WaveGeo wg = wave_geo(ts, blk, wave, false);
+    const Lane ln = lane_item(p, ts, blk, wave, col, false);
     uint4 qf[D / 32];
-    load_frags<T, D>(q, lq.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), it.valid, grp, qf);
+    load_frags<T, D>(q, lq.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, qf);
+    const bool wide = ts.rowshift > 5;  // column pattern changes from chunk to chunk
+    f32x4_t cb[2];
+    column_bias(ln, ts.rowshift, 0, grp, cb);
 
     f32x4_t acc[D / 16];
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m = -INFINITY, lsum = 0.f;  // running max and sum, log2 domain (scores times scale*log2 e)
+    f32x4_t lacc = {0.f, 0.f, 0.f, 0.f};
+    const uint4 ones = make_uint4(Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes);
+    float m = -INFINITY;  // running max, log2 domain (scores times scale * log2 e)
     const float sc2 = p.scale * kLog2e;
-    int c0, c1;
-    chunk_range(sp, ts, c0, c1);
 
     for (int u0 = 0; u0 < blk.U[0]; ++u0) {
         const int p0 = blk.r[0] + (blk.lo[0] + u0) * p.ax[0].dil;
         __syncthreads();
-        stage<T, D>(p, blk, ts, kg, lk, hk, p0, Ks, nullptr);
-        stage<T, D>(p, blk, ts, vg, lv, hk, p0, nullptr, Vt);
+        stage_rows<T, D>(p, blk, ts, plane_of(kg, lk, blk.b, hk, p0), lk, Ks, wave, lane);
+        stage_rows<T, D>(p, blk, ts, plane_of(vg, lv, blk.b, hk, p0), lv, Vs, wave, lane);
+        wait_loads();
         __syncthreads();
-        if (u0 < sp.wlo[0] || u0 > sp.whi[0]) continue;
-        const bool in0 = it.valid && u0 >= sp.lo[0] && u0 <= sp.hi[0];
-        for (int c = c0; c <= c1; ++c) {
-            float sv[8];
-            score_chunk<T, D>(Ks, c, col, grp, qf, sv);
-            const unsigned msk = chunk_mask(sp, in0, 32 * c + 8 * grp, ts);
-            float cmax = -INFINITY;
+        if (!wg.any || u0 < wg.lo[0] || u0 > wg.hi[0]) continue;
+        const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
+        for (int c = wg.c0; c <= wg.c1; c += 4) {
+            const int n = min(4, wg.c1 - c + 1);
+            f32x4_t s[4][2];
+            bool rv[4];
+            float cm = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) cmax = fmaxf(cmax, (msk >> e) & 1u ? sv[e] : -INFINITY);
-            const float mnew = fmaxf(m, max_groups(cmax) * sc2);
+            for (int g = 0; g < 4; ++g) {
+                if (g < n) {
+                    f32x4_t bias[2] = {cb[0], cb[1]};
+                    if (wide) column_bias(ln, ts.rowshift, c + g, grp, bias);
+                    score_chunk<T, D>(Ks, c + g, col, grp, qf, bias, s[g]);
+                    rv[g] = row_ok(ln, ts.rowshift, in0, c + g, grp);
+                    cm = fmaxf(cm, rv[g] ? max8(s[g]) : -INFINITY);
+                }
+            }
+            const float mnew = fmaxf(m, max_rows(cm) * sc2);
             const float mref = mnew == -INFINITY ? 0.f : mnew;
             const float corr = __builtin_amdgcn_exp2f(m - mref);
             m = mnew;
-            lsum *= corr;
+            lacc *= corr;
 #pragma unroll
             for (int db = 0; db < D / 16; ++db) acc[db] *= corr;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                sv[e] = (msk >> e) & 1u ? __builtin_amdgcn_exp2f(fmaf(sv[e], sc2, -mref)) : 0.f;
-                lsum += sv[e];
+            for (int g = 0; g < 4; ++g) {
+                if (g < n) {
+                    const float off = rv[g] ? -mref : -INFINITY;
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) s[g][b][i] = __builtin_amdgcn_exp2f(fmaf(s[g][b][i], sc2, off));
+                    const uint4 pk = pack8<T>(s[g]);
+                    accumulate_chunk<T, D>(Vs, c + g, lane, pk, acc);
+                    lacc = Mma<T>::run(ones, pk, lacc);
+                }
             }
-            accumulate_chunk<T, D>(Vt, slots, c, col, grp, pack8<T>(sv), acc);
         }
     }
 
-    lsum = sum_groups(lsum);
-    if (!it.valid) return;
-    store_rows<T, D>(out, lo.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), grp, acc, 1.f / lsum);
-    if (grp == 0) lse[ll.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h)] = (m + __log2f(lsum)) * kLn2;
+    if (!ln.valid) return;
+    const float lsum = lacc[0];
+    store_rows<T, D>(out, lo.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), grp, acc, 1.f / lsum);
+    if (grp == 0) lse[ll.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h)] = (m + __log2f(lsum)) * kLn2;
 }
 
 // ---------------------------------------------------------------------------
 // Backward, query side: delta = dO . O - dlse (written for the key side) and
 // dq = scale * sum_k P (dP - delta) k, with P = exp(scale q.k - lse) and
-// dP = dO . v.
+// dP = dO . v.  The dP product starts from -delta.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const T* __restrict__ q, Lay lq,
@@ -412,23 +514,20 @@ __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const 
                                                     Lay ldq, float* __restrict__ delta, Lay lde) {
     extern __shared__ __align__(16) unsigned char smem[];
     Block blk;
-    if (!decode_block(p, ts, p.Hq, false, blk)) return;
-    const int slots = ts.slots;
+    if (!decode_block(p, ts, false, blk)) return;
     T* Ks = reinterpret_cast<T*>(smem);
-    T* Vs = Ks + slots * (D + kPad);
-    T* Kt = Vs + slots * (D + kPad);
+    T* Vs = Ks + ts.slots * D;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, grp = lane >> 4;
-    const int hk = blk.h / p.rep;
+    const int hk = kv_head(ts, blk.h);
 
-    const Item it = wave_item(p, blk, wave, col);
-    const Span sp = lane_span(p, blk, it, false);
+    const WaveGeo wg = wave_geo(ts, blk, wave, false);
+    const Lane ln = lane_item(p, ts, blk, wave, col, false);
     uint4 qf[D / 32], gf[D / 32], of[D / 32];
-    const long long qoff = lq.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h);
-    load_frags<T, D>(q, qoff, it.valid, grp, qf);
-    load_frags<T, D>(dout, ldo.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), it.valid, grp, gf);
-    load_frags<T, D>(o, lo.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), it.valid, grp, of);
-    const float L2 = it.valid ? lse[ll.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h)] * kLog2e : 0.f;
-    // delta from this lane's 8 head dims per 32, summed over the 4 lane groups
+    load_frags<T, D>(q, lq.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, qf);
+    load_frags<T, D>(dout, ldo.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, gf);
+    load_frags<T, D>(o, lo.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, of);
+    const float L2 = ln.valid ? lse[ll.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h)] * kLog2e : 0.f;
+    // delta from this lane's 8 head dims per 32, summed over the 4 lane rows
     float di = 0.f;
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
@@ -437,12 +536,14 @@ __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const 
 #pragma unroll
         for (int e = 0; e < 8; ++e) di = fmaf(to_f(g8[e]), to_f(o8[e]), di);
     }
-    di = sum_groups(di);
-    if (dlse && it.valid) di -= dlse[ldl.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h)];
-    if (it.valid && grp == 0) delta[lde.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h)] = di;
+    di = sum_rows(di);
+    if (dlse && ln.valid) di -= dlse[ldl.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h)];
+    if (ln.valid && grp == 0) delta[lde.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h)] = di;
+    const f32x4_t nd[2] = {f32x4_t{-di, -di, -di, -di}, f32x4_t{-di, -di, -di, -di}};
     const float sc2 = p.scale * kLog2e;
-    int c0, c1;
-    chunk_range(sp, ts, c0, c1);
+    const bool wide = ts.rowshift > 5;
+    f32x4_t cb[2];
+    column_bias(ln, ts.rowshift, 0, grp, cb);
 
     f32x4_t acc[D / 16];
 #pragma unroll
@@ -451,32 +552,35 @@ __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const 
     for (int u0 = 0; u0 < blk.U[0]; ++u0) {
         const int p0 = blk.r[0] + (blk.lo[0] + u0) * p.ax[0].dil;
         __syncthreads();
-        stage<T, D>(p, blk, ts, kg, lk, hk, p0, Ks, Kt);
-        stage<T, D>(p, blk, ts, vg, lv, hk, p0, Vs, nullptr);
+        stage_rows<T, D>(p, blk, ts, plane_of(kg, lk, blk.b, hk, p0), lk, Ks, wave, lane);
+        stage_rows<T, D>(p, blk, ts, plane_of(vg, lv, blk.b, hk, p0), lv, Vs, wave, lane);
+        wait_loads();
         __syncthreads();
-        if (u0 < sp.wlo[0] || u0 > sp.whi[0]) continue;
-        const bool in0 = it.valid && u0 >= sp.lo[0] && u0 <= sp.hi[0];
-        for (int c = c0; c <= c1; ++c) {
-            float sv[8], dp[8];
-            score_chunk<T, D>(Ks, c, col, grp, qf, sv);
-            score_chunk<T, D>(Vs, c, col, grp, gf, dp);
-            const unsigned msk = chunk_mask(sp, in0, 32 * c + 8 * grp, ts);
+        if (!wg.any || u0 < wg.lo[0] || u0 > wg.hi[0]) continue;
+        const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
+        for (int c = wg.c0; c <= wg.c1; ++c) {
+            f32x4_t bias[2] = {cb[0], cb[1]};
+            if (wide) column_bias(ln, ts.rowshift, c, grp, bias);
+            f32x4_t s[2], dp[2];
+            score_chunk<T, D>(Ks, c, col, grp, qf, bias, s);
+            score_chunk<T, D>(Vs, c, col, grp, gf, nd, dp);
+            const float off = row_ok(ln, ts.rowshift, in0, c, grp) ? -L2 : -INFINITY;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float pe = (msk >> e) & 1u ? __builtin_amdgcn_exp2f(fmaf(sv[e], sc2, -L2)) : 0.f;
-                sv[e] = pe * (dp[e] - di);
-            }
-            accumulate_chunk<T, D>(Kt, slots, c, col, grp, pack8<T>(sv), acc);
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[b][i] = __builtin_amdgcn_exp2f(fmaf(s[b][i], sc2, off)) * dp[b][i];
+            accumulate_chunk<T, D>(Ks, c, lane, pack8<T>(s), acc);
         }
     }
-    if (!it.valid) return;
-    store_rows<T, D>(dq, ldq.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), grp, acc, p.scale);
+    if (ln.valid) store_rows<T, D>(dq, ldq.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), grp, acc, p.scale);
 }
 
 // ---------------------------------------------------------------------------
 // Backward, key side: for each key/value position, over every query (of each
 // q head in the GQA group) whose window holds it:
 //   dv = sum P dO,   dk = scale * sum P (dP - delta) q.
+// Per staged slot: -lse * log2 e and -delta (fp32); 8 further -inf entries
+// serve lanes whose row test fails.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const T* __restrict__ q, Lay lq,
@@ -487,24 +591,25 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
                                                      T* __restrict__ dk, Lay ldk, T* __restrict__ dv, Lay ldv) {
     extern __shared__ __align__(16) unsigned char smem[];
     Block blk;
-    if (!decode_block(p, ts, p.Hkv, true, blk)) return;
+    if (!decode_block(p, ts, true, blk)) return;
     const int slots = ts.slots;
     T* Qs = reinterpret_cast<T*>(smem);
-    T* Gs = Qs + slots * (D + kPad);
-    T* Qt = Gs + slots * (D + kPad);
-    T* Gt = Qt + D * (slots + kPad);
-    float* L2s = reinterpret_cast<float*>(Gt + D * (slots + kPad));
-    float* Ds = L2s + slots;
+    T* Gs = Qs + slots * D;
+    float* NL = reinterpret_cast<float*>(Gs + slots * D);  // slots + 8
+    float* ND = NL + slots + 8;                            // slots
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, grp = lane >> 4;
+    if (threadIdx.x < 8) NL[slots + threadIdx.x] = -INFINITY;
 
-    const Item it = wave_item(p, blk, wave, col);
-    const Span sp = lane_span(p, blk, it, true);
+    const WaveGeo wg = wave_geo(ts, blk, wave, true);
+    const Lane ln = lane_item(p, ts, blk, wave, col, true);
     uint4 kf[D / 32], vf[D / 32];
-    load_frags<T, D>(kg, lk.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), it.valid, grp, kf);
-    load_frags<T, D>(vg, lv.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), it.valid, grp, vf);
+    load_frags<T, D>(kg, lk.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, kf);
+    load_frags<T, D>(vg, lv.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, vf);
     const float sc2 = p.scale * kLog2e;
-    int c0, c1;
-    chunk_range(sp, ts, c0, c1);
+    const bool wide = ts.rowshift > 5;
+    f32x4_t cb[2];
+    column_bias(ln, ts.rowshift, 0, grp, cb);
+    const int d1 = p.ax[1].dil, d2 = p.ax[2].dil, mask2 = (1 << ts.rowshift) - 1;
 
     f32x4_t gk[D / 16], gv[D / 16];
 #pragma unroll
@@ -513,43 +618,55 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
         gv[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int r = 0; r < p.rep; ++r) {
-        const int h = blk.h * p.rep + r;
+    for (int r = 0; r < static_cast<int>(ts.rep.d); ++r) {
+        const int h = blk.h * static_cast<int>(ts.rep.d) + r;
         for (int u0 = 0; u0 < blk.U[0]; ++u0) {
             const int p0 = blk.r[0] + (blk.lo[0] + u0) * p.ax[0].dil;
             __syncthreads();
-            stage<T, D>(p, blk, ts, q, lq, h, p0, Qs, Qt);
-            stage<T, D>(p, blk, ts, dout, ldo, h, p0, Gs, Gt);
-            stage_scalars(p, blk, ts, h, p0, lse, ll, delta, lde, L2s, Ds);
-            __syncthreads();
-            if (u0 < sp.wlo[0] || u0 > sp.whi[0]) continue;
-            const bool in0 = it.valid && u0 >= sp.lo[0] && u0 <= sp.hi[0];
-            for (int c = c0; c <= c1; ++c) {
-                float sv[8], dp[8];
-                score_chunk<T, D>(Qs, c, col, grp, kf, sv);
-                score_chunk<T, D>(Gs, c, col, grp, vf, dp);
-                const int s0 = 32 * c + 8 * grp;
-                const unsigned msk = chunk_mask(sp, in0, s0, ts);
-                const float4 la = *reinterpret_cast<const float4*>(L2s + s0);
-                const float4 lb = *reinterpret_cast<const float4*>(L2s + s0 + 4);
-                const float4 da = *reinterpret_cast<const float4*>(Ds + s0);
-                const float4 db4 = *reinterpret_cast<const float4*>(Ds + s0 + 4);
-                const float l2[8] = {la.x, la.y, la.z, la.w, lb.x, lb.y, lb.z, lb.w};
-                const float dd[8] = {da.x, da.y, da.z, da.w, db4.x, db4.y, db4.z, db4.w};
-                float pe[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    pe[e] = (msk >> e) & 1u ? __builtin_amdgcn_exp2f(fmaf(sv[e], sc2, -l2[e])) : 0.f;
-                    sv[e] = pe[e] * (dp[e] - dd[e]);
+            stage_rows<T, D>(p, blk, ts, plane_of(q, lq, blk.b, h, p0), lq, Qs, wave, lane);
+            stage_rows<T, D>(p, blk, ts, plane_of(dout, ldo, blk.b, h, p0), ldo, Gs, wave, lane);
+            for (int s = threadIdx.x; s < slots; s += blockDim.x) {
+                const int a1 = s >> ts.rowshift, a2 = s & mask2;
+                float nl = 0.f, nd = 0.f;
+                if (a1 < blk.U[1] && a2 < blk.U[2]) {
+                    const int p1 = blk.r[1] + (blk.lo[1] + a1) * d1, p2 = blk.r[2] + (blk.lo[2] + a2) * d2;
+                    nl = -lse[ll.at(blk.b, p0, p1, p2, h)] * kLog2e;
+                    nd = -delta[lde.at(blk.b, p0, p1, p2, h)];
                 }
-                accumulate_chunk<T, D>(Gt, slots, c, col, grp, pack8<T>(pe), gv);
-                accumulate_chunk<T, D>(Qt, slots, c, col, grp, pack8<T>(sv), gk);
+                NL[s] = nl;
+                ND[s] = nd;
+            }
+            wait_loads();
+            __syncthreads();
+            if (!wg.any || u0 < wg.lo[0] || u0 > wg.hi[0]) continue;
+            const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
+            for (int c = wg.c0; c <= wg.c1; ++c) {
+                const int s0 = 32 * c + 8 * grp;
+                f32x4_t bias[2] = {cb[0], cb[1]};
+                if (wide) column_bias(ln, ts.rowshift, c, grp, bias);
+                const f32x4_t ndc[2] = {*reinterpret_cast<const f32x4_t*>(ND + s0),
+                                        *reinterpret_cast<const f32x4_t*>(ND + s0 + 4)};
+                f32x4_t s[2], dp[2];
+                score_chunk<T, D>(Qs, c, col, grp, kf, bias, s);
+                score_chunk<T, D>(Gs, c, col, grp, vf, ndc, dp);
+                const float* nlp = row_ok(ln, ts.rowshift, in0, c, grp) ? NL + s0 : NL + slots;
+                const f32x4_t nl[2] = {*reinterpret_cast<const f32x4_t*>(nlp),
+                                       *reinterpret_cast<const f32x4_t*>(nlp + 4)};
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        s[b][i] = __builtin_amdgcn_exp2f(fmaf(s[b][i], sc2, nl[b][i]));
+                        dp[b][i] *= s[b][i];
+                    }
+                accumulate_chunk<T, D>(Gs, c, lane, pack8<T>(s), gv);
+                accumulate_chunk<T, D>(Qs, c, lane, pack8<T>(dp), gk);
             }
         }
     }
-    if (!it.valid) return;
-    store_rows<T, D>(dk, ldk.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), grp, gk, p.scale);
-    store_rows<T, D>(dv, ldv.at(blk.b, it.pos[0], it.pos[1], it.pos[2], blk.h), grp, gv, 1.f);
+    if (!ln.valid) return;
+    store_rows<T, D>(dk, ldk.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), grp, gk, p.scale);
+    store_rows<T, D>(dv, ldv.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), grp, gv, 1.f);
 }
 
 }  // namespace
@@ -565,6 +682,18 @@ enum Kind { kForward = 0, kBackwardQ = 1, kBackwardKV = 2 };
 constexpr size_t kLdsBudget = 64 * 1024;
 
 int n_class_h(const Axis& A, int r) { return (A.len - r + A.dil - 1) / A.dil; }
+
+int pow2_at_least(int x) {
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+int log2_of(int x) {
+    int l = 0;
+    while ((1 << l) < x) ++l;
+    return l;
+}
 
 // Largest union extent on one axis over every class and tile (the same
 // spans decode_block computes on the device).
@@ -591,50 +720,48 @@ int union_extent(const Axis& A, int T, bool key_tile) {
 }
 
 size_t lds_bytes(Kind kind, int slots, int D) {
-    const size_t rows = static_cast<size_t>(slots) * (D + kPad) * 2;
-    const size_t trans = static_cast<size_t>(D) * (slots + kPad) * 2;
-    switch (kind) {
-        case kForward: return rows + trans;
-        case kBackwardQ: return 2 * rows + trans;
-        default: return 2 * rows + 2 * trans + 2 * static_cast<size_t>(slots) * 4;
-    }
+    const size_t rows = static_cast<size_t>(slots) * D * 2;
+    return kind == kBackwardKV ? 2 * rows + (2 * static_cast<size_t>(slots) + 8) * 4 : 2 * rows;
 }
 
-// Workgroup box in class coordinates: up to 64 items (4 waves), innermost
-// axis first; halved until the staged union fits the LDS budget.
+// Workgroup box in class coordinates: up to 64 items (4 waves), power-of-two
+// extents, innermost axis first (8 wide unless the problem is 1-D); halved
+// until the staged union fits the LDS budget.
 bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts) {
     int n[3];
     for (int a = 0; a < 3; ++a) n[a] = n_class_h(p.ax[a], 0);  // class 0 is the longest
-    for (int items = 64; items >= 16; items /= 2) {
+    for (int items = kMaxItems; items >= 16; items /= 2) {
         if (n[0] == 1 && n[1] == 1) {
-            ts.T[2] = n[2] < items ? n[2] : items;
+            ts.T[2] = std::min(pow2_at_least(n[2]), items);
             ts.T[1] = ts.T[0] = 1;
         } else {
-            ts.T[2] = n[2] < 8 ? n[2] : 8;
-            const int r1 = items / ts.T[2] > 0 ? items / ts.T[2] : 1;
-            ts.T[1] = n[1] < r1 ? n[1] : r1;
-            const int r0 = items / (ts.T[2] * ts.T[1]) > 0 ? items / (ts.T[2] * ts.T[1]) : 1;
-            ts.T[0] = n[0] < r0 ? n[0] : r0;
+            ts.T[2] = std::min(pow2_at_least(n[2]), 8);
+            ts.T[1] = std::min(pow2_at_least(n[1]), std::max(items / ts.T[2], 1));
+            ts.T[0] = std::min(pow2_at_least(n[0]), std::max(items / (ts.T[2] * ts.T[1]), 1));
         }
-        for (int a = 0; a < 3; ++a) ts.ntile[a] = (n[a] + ts.T[a] - 1) / ts.T[a];
+        for (int a = 0; a < 3; ++a) {
+            ts.tshift[a] = log2_of(ts.T[a]);
+            ts.ntile[a] = (n[a] + ts.T[a] - 1) / ts.T[a];
+        }
         const int cnt = ts.T[0] * ts.T[1] * ts.T[2];
-        ts.waves = (cnt + 15) / 16;
+        ts.waves = std::max(1, (cnt + 15) / 16);
         const int u1 = union_extent(p.ax[1], ts.T[1], kind == kBackwardKV);
         const int u2 = union_extent(p.ax[2], ts.T[2], kind == kBackwardKV);
-        ts.rowshift = 3;
-        while ((1 << ts.rowshift) < u2) ++ts.rowshift;
-        ts.rowlen = 1 << ts.rowshift;
-        ts.slots = ((u1 * ts.rowlen + 31) / 32) * 32;
-        if (lds_bytes(kind, ts.slots, D) <= kLdsBudget) return true;
+        ts.rowshift = std::max(3, log2_of(u2));
+        ts.slots = ((u1 * (1 << ts.rowshift) + 31) / 32) * 32;
+        if (lds_bytes(kind, ts.slots, D) <= kLdsBudget) {
+            const int heads = kind == kBackwardKV ? p.Hkv : p.Hq;
+            ts.heads = make_fastdiv(static_cast<uint32_t>(heads));
+            ts.rep = make_fastdiv(static_cast<uint32_t>(p.rep));
+            for (int a = 0; a < 3; ++a) {
+                ts.tiles[a] = make_fastdiv(static_cast<uint32_t>(ts.ntile[a]));
+                ts.dil[a] = make_fastdiv(static_cast<uint32_t>(p.ax[a].dil));
+                ts.lenmod[a] = p.ax[a].len % p.ax[a].dil;
+            }
+            return true;
+        }
     }
     return false;
-}
-
-template <typename K>
-void allow_lds(K kernel, size_t bytes) {
-    if (bytes > 64 * 1024)
-        hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(bytes));
 }
 
 long long grid_blocks(const Prob& p, const TileShape& ts, int heads) {
@@ -643,23 +770,33 @@ long long grid_blocks(const Prob& p, const TileShape& ts, int heads) {
     return nb;
 }
 
-// 32-bit offsets inside one (batch, head, axis-0 plane) for every operand.
+// Staged operands: non-negative strides, and every in-plane byte offset (axes
+// 1 and 2, plus a row of 128 head dims) inside the buffer range of a plane.
 bool offsets_fit(const Prob& p, std::initializer_list<Lay> lays) {
     for (const Lay& l : lays) {
-        const long long m = (static_cast<long long>(p.ax[1].len) - 1) * (l.s1 < 0 ? -l.s1 : l.s1) +
-                            (static_cast<long long>(p.ax[2].len) - 1) * (l.s2 < 0 ? -l.s2 : l.s2) + 256;
-        if (m >= (1LL << 31)) return false;
+        if (l.b < 0 || l.s0 < 0 || l.s1 < 0 || l.s2 < 0 || l.h < 0) return false;
+        const long long m = (static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
+                            (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + 128;
+        if (m * 2 >= kPlaneBytes) return false;
     }
     return true;
+}
+
+template <typename K>
+hipError_t allow_lds(K kernel, size_t bytes) {
+    if (bytes <= 64 * 1024) return hipSuccess;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(bytes));
 }
 
 template <typename T, int D>
 hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
                       Lay lo, float* lse, Lay ll, hipStream_t s) {
     TileShape ts{};
-    choose_tile(p, kForward, D, ts);
+    if (!choose_tile(p, kForward, D, ts)) return hipErrorInvalidValue;
     const size_t shm = lds_bytes(kForward, ts.slots, D);
-    allow_lds(k_fwd_mfma<T, D>, shm);
+    hipError_t e = allow_lds(k_fwd_mfma<T, D>, shm);
+    if (e != hipSuccess) return e;
     NA_LAUNCH("na_fwd_mfma", (k_fwd_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, ts, p.Hq))),
               dim3(64 * ts.waves), shm, s, p, ts, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (T*)o, lo, lse,
               ll);
@@ -672,15 +809,15 @@ hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
                       const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
                       float* delta, Lay lde, hipStream_t s) {
     TileShape tq{}, tk{};
-    choose_tile(p, kBackwardQ, D, tq);
-    choose_tile(p, kBackwardKV, D, tk);
+    if (!choose_tile(p, kBackwardQ, D, tq) || !choose_tile(p, kBackwardKV, D, tk)) return hipErrorInvalidValue;
     const size_t shq = lds_bytes(kBackwardQ, tq.slots, D), shk = lds_bytes(kBackwardKV, tk.slots, D);
-    allow_lds(k_bwd_q_mfma<T, D>, shq);
-    allow_lds(k_bwd_kv_mfma<T, D>, shk);
+    hipError_t e = allow_lds(k_bwd_q_mfma<T, D>, shq);
+    if (e == hipSuccess) e = allow_lds(k_bwd_kv_mfma<T, D>, shk);
+    if (e != hipSuccess) return e;
     NA_LAUNCH("na_bwd_q_mfma", (k_bwd_q_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tq, p.Hq))),
               dim3(64 * tq.waves), shq, s, p, tq, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv,
               (const T*)o, lo, (const T*)dout, ldo, lse, ll, dlse, ldl, (T*)dq, ldq, delta, lde);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     NA_LAUNCH("na_bwd_kv_mfma", (k_bwd_kv_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tk, p.Hkv))),
               dim3(64 * tk.waves), shk, s, p, tk, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv,
@@ -695,11 +832,13 @@ bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward)
     if (p.Dqk != p.Dv || !(D == 32 || D == 64 || D == 128)) return false;
     for (int a = 0; a < 3; ++a)
         if (p.ax[a].st != 1) return false;
+    // tile indices (the launch grid) stay in 31 bits
     TileShape ts{};
-    if (!choose_tile(p, kForward, D, ts)) return false;
-    if (backward && (!choose_tile(p, kBackwardQ, D, ts) || !choose_tile(p, kBackwardKV, D, ts))) return false;
-    // grid and per-plane offsets stay in 32 bits
-    if (grid_blocks(p, ts, p.Hq) >= (1LL << 31)) return false;
+    if (!choose_tile(p, kForward, D, ts) || grid_blocks(p, ts, p.Hq) >= (1LL << 31)) return false;
+    if (backward) {
+        if (!choose_tile(p, kBackwardQ, D, ts) || grid_blocks(p, ts, p.Hq) >= (1LL << 31)) return false;
+        if (!choose_tile(p, kBackwardKV, D, ts) || grid_blocks(p, ts, p.Hkv) >= (1LL << 31)) return false;
+    }
     return true;
 }
 

@@ -102,3 +102,19 @@ long long host_class_mismatch(const natten_problem_t* p) {
 }
 
 }  // extern "C"
+
+extern "C" {
+
+// Number of n in [0, n_max) (stepping by `step`, plus the last 4096 below
+// n_max) for which the multiply-high division disagrees with n / d.
+long long host_fastdiv_errors(uint32_t d, int n_max, int step) {
+    const na::FastDiv f = na::make_fastdiv(d);
+    long long bad = 0;
+    for (long long n = 0; n < n_max; n += step)
+        if (na::fdiv(static_cast<int>(n), f) != static_cast<int>(n / d)) ++bad;
+    for (long long n = n_max > 4096 ? n_max - 4096 : 0; n < n_max; ++n)
+        if (na::fdiv(static_cast<int>(n), f) != static_cast<int>(n / d)) ++bad;
+    return bad;
+}
+
+}  // extern "C"

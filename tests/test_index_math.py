@@ -34,7 +34,22 @@ def host_idx():
     lib.host_inverse_mismatch.restype = ctypes.c_longlong
     lib.host_class_mismatch.argtypes = [ctypes.POINTER(_lib.Problem)]
     lib.host_class_mismatch.restype = ctypes.c_longlong
+    lib.host_fastdiv_errors.argtypes = [ctypes.c_uint32, ctypes.c_int, ctypes.c_int]
+    lib.host_fastdiv_errors.restype = ctypes.c_longlong
     return lib
+
+
+def test_fastdiv_matches_integer_division(host_idx):
+    """The multiply-high division the tile kernels decode workgroup indices
+    with equals n // d: every n below 2^20 for d <= 300 and every power of
+    two, and a stride-sampled sweep up to 2^31 - 1 (plus its top 4096
+    values) for divisors near powers of two and a few large odd ones."""
+    small = list(range(1, 301)) + [1 << k for k in range(9, 31)]
+    for d in small:
+        assert host_idx.host_fastdiv_errors(d, 1 << 20, 1) == 0, d
+    large = [(1 << k) + o for k in range(2, 31) for o in (-1, 1)] + [3, 7, 641, 65537, 999983, 2147483647]
+    for d in large:
+        assert host_idx.host_fastdiv_errors(d, (1 << 31) - 1, 9973) == 0, d
 
 
 def test_class_coordinate_closed_forms(host_idx):
