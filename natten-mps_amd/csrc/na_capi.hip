@@ -150,7 +150,7 @@ int natten_hip_forward(const natten_problem_t* p, const void* q, const natten_la
         runs_aligned(dpl_for(D), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {v, lv, P.Dv}, {out, lo, P.Dv}}) ? 1 : 0;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (use_mfma() && na::mfma_eligible(P, p->dtype, D, vec != 0, false) &&
-        na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv)}))
+        na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(llse)}))
         return launch_status(na::mfma_forward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), lse,
                                               to_lay(llse), p->dtype, s),
                              "forward");
@@ -177,7 +177,9 @@ int natten_hip_backward(const natten_problem_t* p, const void* q, const natten_l
                         ? 1
                         : 0;
     if (use_mfma() && na::mfma_eligible(P, p->dtype, D, vec != 0, true) &&
-        na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(ldo)}))
+        na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(ldo), to_lay(llse),
+                                 to_lay(ldq), to_lay(ldk), to_lay(ldv), to_lay(ldelta)}) &&
+        (!dlse || na::mfma_offsets_fit(P, {to_lay(ldlse)})))
         return launch_status(na::mfma_backward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout,
                                                to_lay(ldo), lse,
                                                to_lay(llse), dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv,

@@ -38,8 +38,11 @@
 //
 // MFMA lane layout (16x16x32): A row = lane%16, B column = lane%16, both with
 // k = 8*(lane/16) .. +7; C column = lane%16, rows 4*(lane/16) .. +3.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <vector>
 
 #include "na_launch.h"
 
@@ -123,11 +126,24 @@ __device__ __forceinline__ float max8(const f32x4_t (&s)[2]) {
 // the 16 rows one score-operand read touches (rows 8x + y + 4b, x, y < 4)
 // land on distinct banks for every head dim.
 template <int D>
-__device__ __forceinline__ int swz(int row) {
+__host__ __device__ constexpr int swz(int row) {
     if constexpr (D == 32) return (row >> 3) & 3;
     else if constexpr (D == 64) return (((row >> 3) & 3) << 1) | ((row >> 1) & 1);
     else return (((row >> 3) & 3) << 2) | (row & 3);
 }
+
+// Staging moves R = 64 / (D/8) rows per wave instruction; the swizzle of row
+// iR + l (l < R) splits into disjoint bits of i and of l, so the lane part of
+// the LDS/global offsets is fixed for a whole tile.
+template <int D>
+constexpr bool swz_splits() {
+    constexpr int R = 64 / (D / 8);
+    for (int i = 0; i < 256; ++i)
+        for (int l = 0; l < R; ++l)
+            if (swz<D>(i * R + l) != (swz<D>(i * R) ^ swz<D>(l))) return false;
+    return true;
+}
+static_assert(swz_splits<32>() && swz_splits<64>() && swz_splits<128>(), "swizzle must split");
 
 __device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
@@ -136,18 +152,28 @@ __device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)"
 // Host-chosen tile: power-of-two extents T = 2^tshift (class coordinates) of a
 // workgroup's box, tiles per class per axis, waves per workgroup, the staged
 // slice layout (slot = a1 * 2^rowshift + a2, `slots` per slice, a multiple of
-// 32), len % dil per axis, and divisors for decoding the workgroup index.
+// 32), len % dil per axis, the run of (batch, head) pairs a workgroup works
+// through for its box, and divisors for decoding the workgroup index.
 struct TileShape {
     int T[3], tshift[3], ntile[3];
     int waves, slots, rowshift;
     int lenmod[3];
-    FastDiv heads, rep, tiles[3], dil[3];
+    int nbh, bh_per;  // (batch, head) pairs, and how many one workgroup runs
+    FastDiv heads, rep, chunks, tiles[3], dil[3];
+};
+
+// Operand layout as the kernels take it: 64-bit batch and head strides, and
+// 32-bit strides inside one (batch, head) (the host checks the offsets fit).
+struct LayK {
+    long long b, h;
+    int s0, s1, s2, pad;
 };
 
 namespace {
 
 struct Block {
-    int b, h, r[3], J[3], E[3], lo[3], U[3];
+    int bh0, bh1;  // run of flattened (batch, head) indices
+    int r[3], J[3], E[3], lo[3], U[3];
     ClassAxis c[3];
 };
 
@@ -161,13 +187,15 @@ __device__ __forceinline__ ClassAxis class_axis_of(const Axis& a, int r, const F
     return c;
 }
 
-// Workgroup -> (batch, head, residues, tile origin J, clipped extent E) and
-// the union box [lo, lo+U) of the windows of its queries (key_tile = false)
-// or of the queries attending its keys (key_tile = true).  False: empty tile.
+// Workgroup -> (run of (batch, head) pairs, residues, tile origin J, clipped
+// extent E) and the union box [lo, lo+U) of the windows of its queries
+// (key_tile = false) or of the queries attending its keys (key_tile = true).
+// The geometry is the same for every (batch, head).  False: empty tile.
 __device__ __forceinline__ bool decode_block(const Prob& p, const TileShape& ts, bool key_tile, Block& k) {
     int x = xcd_block(blockIdx.x, gridDim.x);
-    int q = fdiv(x, ts.heads);
-    k.h = x - q * static_cast<int>(ts.heads.d);
+    int q = fdiv(x, ts.chunks);
+    k.bh0 = (x - q * static_cast<int>(ts.chunks.d)) * ts.bh_per;
+    k.bh1 = min(k.bh0 + ts.bh_per, ts.nbh);
     x = q;
     int t[3];
     for (int a = 2; a >= 0; --a) {
@@ -178,7 +206,6 @@ __device__ __forceinline__ bool decode_block(const Prob& p, const TileShape& ts,
         k.r[a] = x - q * static_cast<int>(ts.dil[a].d);
         x = q;
     }
-    k.b = x;
     for (int a = 0; a < 3; ++a) {
         const ClassAxis c = class_axis_of(p.ax[a], k.r[a], ts.dil[a], ts.lenmod[a]);
         k.c[a] = c;
@@ -314,37 +341,80 @@ __device__ __forceinline__ bool row_ok(const Lane& ln, int rowshift, bool in0, i
     return in0 && row >= ln.lo[1] && row <= ln.hi[1];
 }
 
+// Per-(batch, head) base pointer and the 32-bit offset of a position inside
+// it (the host checks that every such offset fits in 31 bits).
 template <typename T>
-__device__ __forceinline__ const T* plane_of(const T* g, const Lay& lay, int b, int h, int p0) {
-    return g + static_cast<long long>(b) * lay.b + static_cast<long long>(h) * lay.h +
-           static_cast<long long>(p0) * lay.s0;
+__device__ __forceinline__ T* bh_ptr(T* g, const LayK& lay, int b, int h) {
+    return g + static_cast<long long>(b) * lay.b + static_cast<long long>(h) * lay.h;
 }
 
-// Stage the union slice of one axis-0 plane (base `plane`) into X[slot][D]:
-// each wave instruction moves 64 / (D/8) rows, lane l the 16-byte piece
-// l % (D/8) of row l / (D/8), holding logical piece (l % (D/8)) ^ swz(row).
-// In-plane offsets fit in 31 bits and strides are non-negative (checked on
-// the host).
+__device__ __forceinline__ int vol_off(const LayK& lay, const int (&pos)[3]) {
+    return pos[0] * lay.s0 + pos[1] * lay.s1 + pos[2] * lay.s2;
+}
+
+template <typename T>
+__device__ __forceinline__ const T* plane_of(const T* g, const LayK& lay, int b, int h, int p0) {
+    return bh_ptr(g, lay, b, h) + p0 * lay.s0;
+}
+
+// Staging of union slices into X[slot][D], two operands at a time (same
+// slot layout, own strides): each wave instruction moves R = 64 / (D/8)
+// rows, lane l the 16-byte piece l % (D/8) of row l / (D/8), holding logical
+// piece (l % (D/8)) ^ swz(row).  With slot = iR + l/(D/8), union row and
+// column split into an instruction part (scalar) and a lane part fixed per
+// tile.  In-plane offsets fit in 31 bits and strides are non-negative
+// (checked on the host).
+struct StageMap {
+    int lrow, lcol;    // lane's row / column inside an instruction's rows
+    int lane_a, lane_b;  // lane part of the byte offset, operands a and b
+    int kb16;          // lane part of the swizzled piece, times 16
+};
+
 template <typename T, int D>
-__device__ __forceinline__ void stage_rows(const Prob& p, const Block& k, const TileShape& ts, const T* plane,
-                                           const Lay& lay, T* X, int wave, int lane) {
-    constexpr int P = D / 8, RPI = 64 / P;
-    const __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(plane), static_cast<short>(0), kPlaneBytes, 0x00020000);
+__device__ __forceinline__ StageMap stage_map(const Prob& p, const TileShape& ts, const LayK& la, const LayK& lb,
+                                              int lane) {
+    constexpr int P = D / 8;
+    StageMap m;
+    const int l = lane / P;
+    m.lrow = l >> ts.rowshift;
+    m.lcol = l & ((1 << ts.rowshift) - 1);
+    const int d1 = p.ax[1].dil, d2 = p.ax[2].dil;
+    m.lane_a = (m.lrow * d1 * la.s1 + m.lcol * d2 * la.s2) * static_cast<int>(sizeof(T));
+    m.lane_b = (m.lrow * d1 * lb.s1 + m.lcol * d2 * lb.s2) * static_cast<int>(sizeof(T));
+    m.kb16 = ((lane % P) ^ swz<D>(l)) << 4;
+    return m;
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void stage_pair(const Prob& p, const Block& k, const TileShape& ts, const StageMap& m,
+                                           const T* plane_a, const LayK& la, T* Xa, const T* plane_b, const LayK& lb,
+                                           T* Xb, int wave) {
+    constexpr int R = 64 / (D / 8);
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(plane_a), static_cast<short>(0), kPlaneBytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(plane_b), static_cast<short>(0), kPlaneBytes, 0x00020000);
     const int d1 = p.ax[1].dil, d2 = p.ax[2].dil;
     const int c1 = k.r[1] + k.lo[1] * d1, c2 = k.r[2] + k.lo[2] * d2;
-    const int s1 = static_cast<int>(lay.s1), s2 = static_cast<int>(lay.s2);
     const int mask2 = (1 << ts.rowshift) - 1;
-    const int n_inst = ts.slots / RPI;
+    const int n_inst = ts.slots / R;
+    constexpr int E = static_cast<int>(sizeof(T));
     for (int i = wave; i < n_inst; i += ts.waves) {
-        const int slot = i * RPI + lane / P;
-        const int kb = (lane % P) ^ swz<D>(slot);
-        const int a1 = slot >> ts.rowshift, a2 = slot & mask2;
-        const bool ok = a1 < k.U[1] && a2 < k.U[2];
-        const uint32_t off =
-            ok ? static_cast<uint32_t>(((c1 + a1 * d1) * s1 + (c2 + a2 * d2) * s2 + kb * 8) * static_cast<int>(sizeof(T)))
-               : kOutOfRange;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(X + i * RPI * D), 16, off, 0, 0, 0);
+        // instruction part in scalar registers; the lane part was fixed per tile
+        const int irow = (i * R) >> ts.rowshift, icol = (i * R) & mask2;
+        const int r1 = c1 + irow * d1, r2 = c2 + icol * d2;
+        const int sa = __builtin_amdgcn_readfirstlane((r1 * la.s1 + r2 * la.s2) * E);
+        const int sb = __builtin_amdgcn_readfirstlane((r1 * lb.s1 + r2 * lb.s2) * E);
+        const int kbh = __builtin_amdgcn_readfirstlane(swz<D>(i * R) << 4);
+        const int lim_r = __builtin_amdgcn_readfirstlane(k.U[1] - irow);
+        const int lim_c = __builtin_amdgcn_readfirstlane(k.U[2] - icol);
+        const int kb = m.kb16 ^ kbh;
+        // out-of-union slots: set bit 31, past the buffer range (offsets < 2^31)
+        const uint32_t bad = (m.lrow < lim_r && m.lcol < lim_c) ? 0u : kOutOfRange;
+        const uint32_t oa = static_cast<uint32_t>(sa + m.lane_a + kb) | bad;
+        const uint32_t ob = static_cast<uint32_t>(sb + m.lane_b + kb) | bad;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(Xa + i * R * D), 16, oa, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(Xb + i * R * D), 16, ob, 0, 0, 0);
     }
 }
 
@@ -410,7 +480,43 @@ __device__ __forceinline__ void store_rows(T* __restrict__ g, long long off, int
     }
 }
 
+// (batch, head) of flattened index bh (batch-major).
+__device__ __forceinline__ void split_bh(const TileShape& ts, int bh, int& b, int& h) {
+    b = fdiv(bh, ts.heads);
+    h = bh - b * static_cast<int>(ts.heads.d);
+}
+
 __device__ __forceinline__ int kv_head(const TileShape& ts, int h) { return ts.rep.d == 1 ? h : fdiv(h, ts.rep); }
+
+// Walk of a workgroup over its (batch, head) pairs and axis-0 slices.  The
+// loads of the next slice are issued as soon as the current one is no longer
+// read, and the very first right after decoding the tile, so that the
+// per-lane setup runs while they are in flight.
+struct Walk {
+    int bh, u0, b, h;
+};
+
+__device__ __forceinline__ void walk_start(const TileShape& ts, const Block& k, Walk& w) {
+    w.bh = k.bh0;
+    w.u0 = 0;
+    split_bh(ts, w.bh, w.b, w.h);
+}
+
+// Advance to the next slice; false past the last one.  `new_pair` reports a
+// change of (batch, head).
+__device__ __forceinline__ bool walk_next(const TileShape& ts, const Block& k, Walk& w, bool& new_pair) {
+    new_pair = false;
+    if (++w.u0 < k.U[0]) return true;
+    w.u0 = 0;
+    if (++w.bh >= k.bh1) return false;
+    split_bh(ts, w.bh, w.b, w.h);
+    new_pair = true;
+    return true;
+}
+
+__device__ __forceinline__ int slice_pos(const Prob& p, const Block& k, int u0) {
+    return k.r[0] + (k.lo[0] + u0) * p.ax[0].dil;
+}
 
 // ---------------------------------------------------------------------------
 // Forward: out = softmax(scale q.k) v over each window, lse (natural log).
@@ -418,85 +524,101 @@ __device__ __forceinline__ int kv_head(const TileShape& ts, int h) { return ts.r
 // rescale per group).
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T* __restrict__ q, Lay lq,
-                                                  const T* __restrict__ kg, Lay lk, const T* __restrict__ vg,
-                                                  Lay lv, T* __restrict__ out, Lay lo, float* __restrict__ lse,
-                                                  Lay ll) {
+__global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T* __restrict__ q, LayK lq,
+                                                  const T* __restrict__ kg, LayK lk, const T* __restrict__ vg,
+                                                  LayK lv, T* __restrict__ out, LayK lo, float* __restrict__ lse,
+                                                  LayK ll) {
     extern __shared__ __align__(16) unsigned char smem[];
     Block blk;
     if (!decode_block(p, ts, false, blk)) return;
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + ts.slots * D;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, grp = lane >> 4;
-    const int hk = kv_head(ts, blk.h);
-
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
+    const StageMap sm = stage_map<T, D>(p, ts, lk, lv, lane);
+    Walk w;
+    walk_start(ts, blk, w);
+    {
+        const int p0 = slice_pos(p, blk, 0), hk = kv_head(ts, w.h);
+        stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0), lv,
+                         Vs, wave);
+    }
     const WaveGeo wg = wave_geo(ts, blk, wave, false);
     const Lane ln = lane_item(p, ts, blk, wave, col, false);
-    uint4 qf[D / 32];
-    load_frags<T, D>(q, lq.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, qf);
     const bool wide = ts.rowshift > 5;  // column pattern changes from chunk to chunk
     f32x4_t cb[2];
     column_bias(ln, ts.rowshift, 0, grp, cb);
-
-    f32x4_t acc[D / 16];
-#pragma unroll
-    for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    f32x4_t lacc = {0.f, 0.f, 0.f, 0.f};
     const uint4 ones = make_uint4(Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes);
-    float m = -INFINITY;  // running max, log2 domain (scores times scale * log2 e)
     const float sc2 = p.scale * kLog2e;
 
-    for (int u0 = 0; u0 < blk.U[0]; ++u0) {
-        const int p0 = blk.r[0] + (blk.lo[0] + u0) * p.ax[0].dil;
-        __syncthreads();
-        stage_rows<T, D>(p, blk, ts, plane_of(kg, lk, blk.b, hk, p0), lk, Ks, wave, lane);
-        stage_rows<T, D>(p, blk, ts, plane_of(vg, lv, blk.b, hk, p0), lv, Vs, wave, lane);
+    uint4 qf[D / 32];
+    f32x4_t acc[D / 16], lacc;
+    float m;
+    bool more = true, fresh = true;
+    while (more) {
+        const int b = w.b, h = w.h, u0 = w.u0;
+        if (fresh) {
+            load_frags<T, D>(bh_ptr(q, lq, b, h), vol_off(lq, ln.pos), ln.valid, grp, qf);
+#pragma unroll
+            for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            lacc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            m = -INFINITY;  // running max, log2 domain (scores times scale * log2 e)
+        }
         wait_loads();
         __syncthreads();
-        if (!wg.any || u0 < wg.lo[0] || u0 > wg.hi[0]) continue;
-        const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
-        for (int c = wg.c0; c <= wg.c1; c += 4) {
-            const int n = min(4, wg.c1 - c + 1);
-            f32x4_t s[4][2];
-            bool rv[4];
-            float cm = -INFINITY;
+        if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
+            const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
+            for (int c = wg.c0; c <= wg.c1; c += 4) {
+                const int n = min(4, wg.c1 - c + 1);
+                f32x4_t s[4][2];
+                bool rv[4];
+                float cm = -INFINITY;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                if (g < n) {
-                    f32x4_t bias[2] = {cb[0], cb[1]};
-                    if (wide) column_bias(ln, ts.rowshift, c + g, grp, bias);
-                    score_chunk<T, D>(Ks, c + g, col, grp, qf, bias, s[g]);
-                    rv[g] = row_ok(ln, ts.rowshift, in0, c + g, grp);
-                    cm = fmaxf(cm, rv[g] ? max8(s[g]) : -INFINITY);
+                for (int g = 0; g < 4; ++g) {
+                    if (g < n) {
+                        f32x4_t bias[2] = {cb[0], cb[1]};
+                        if (wide) column_bias(ln, ts.rowshift, c + g, grp, bias);
+                        score_chunk<T, D>(Ks, c + g, col, grp, qf, bias, s[g]);
+                        rv[g] = row_ok(ln, ts.rowshift, in0, c + g, grp);
+                        cm = fmaxf(cm, rv[g] ? max8(s[g]) : -INFINITY);
+                    }
                 }
-            }
-            const float mnew = fmaxf(m, max_rows(cm) * sc2);
-            const float mref = mnew == -INFINITY ? 0.f : mnew;
-            const float corr = __builtin_amdgcn_exp2f(m - mref);
-            m = mnew;
-            lacc *= corr;
+                const float mnew = fmaxf(m, max_rows(cm) * sc2);
+                const float mref = mnew == -INFINITY ? 0.f : mnew;
+                const float corr = __builtin_amdgcn_exp2f(m - mref);
+                m = mnew;
+                lacc *= corr;
 #pragma unroll
-            for (int db = 0; db < D / 16; ++db) acc[db] *= corr;
+                for (int db = 0; db < D / 16; ++db) acc[db] *= corr;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                if (g < n) {
-                    const float off = rv[g] ? -mref : -INFINITY;
+                for (int g = 0; g < 4; ++g) {
+                    if (g < n) {
+                        const float off = rv[g] ? -mref : -INFINITY;
 #pragma unroll
-                    for (int b = 0; b < 2; ++b)
+                        for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) s[g][b][i] = __builtin_amdgcn_exp2f(fmaf(s[g][b][i], sc2, off));
-                    const uint4 pk = pack8<T>(s[g]);
-                    accumulate_chunk<T, D>(Vs, c + g, lane, pk, acc);
-                    lacc = Mma<T>::run(ones, pk, lacc);
+                            for (int i = 0; i < 4; ++i)
+                                s[g][bb][i] = __builtin_amdgcn_exp2f(fmaf(s[g][bb][i], sc2, off));
+                        const uint4 pk = pack8<T>(s[g]);
+                        accumulate_chunk<T, D>(Vs, c + g, lane, pk, acc);
+                        lacc = Mma<T>::run(ones, pk, lacc);
+                    }
                 }
             }
         }
+        more = walk_next(ts, blk, w, fresh);
+        __syncthreads();  // the slice is no longer read
+        if (more) {
+            const int p0 = slice_pos(p, blk, w.u0), hk = kv_head(ts, w.h);
+            stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0),
+                             lv, Vs, wave);
+        }
+        if ((fresh || !more) && ln.valid) {
+            const float lsum = lacc[0];
+            store_rows<T, D>(bh_ptr(out, lo, b, h), vol_off(lo, ln.pos), grp, acc, 1.f / lsum);
+            if (grp == 0) bh_ptr(lse, ll, b, h)[vol_off(ll, ln.pos)] = (m + __log2f(lsum)) * kLn2;
+        }
     }
-
-    if (!ln.valid) return;
-    const float lsum = lacc[0];
-    store_rows<T, D>(out, lo.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), grp, acc, 1.f / lsum);
-    if (grp == 0) lse[ll.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h)] = (m + __log2f(lsum)) * kLn2;
 }
 
 // ---------------------------------------------------------------------------
@@ -505,74 +627,92 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T*
 // dP = dO . v.  The dP product starts from -delta.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const T* __restrict__ q, Lay lq,
-                                                    const T* __restrict__ kg, Lay lk, const T* __restrict__ vg,
-                                                    Lay lv, const T* __restrict__ o, Lay lo,
-                                                    const T* __restrict__ dout, Lay ldo,
-                                                    const float* __restrict__ lse, Lay ll,
-                                                    const float* __restrict__ dlse, Lay ldl, T* __restrict__ dq,
-                                                    Lay ldq, float* __restrict__ delta, Lay lde) {
+__global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const T* __restrict__ q, LayK lq,
+                                                    const T* __restrict__ kg, LayK lk, const T* __restrict__ vg,
+                                                    LayK lv, const T* __restrict__ o, LayK lo,
+                                                    const T* __restrict__ dout, LayK ldo,
+                                                    const float* __restrict__ lse, LayK ll,
+                                                    const float* __restrict__ dlse, LayK ldl, T* __restrict__ dq,
+                                                    LayK ldq, float* __restrict__ delta, LayK lde) {
     extern __shared__ __align__(16) unsigned char smem[];
     Block blk;
     if (!decode_block(p, ts, false, blk)) return;
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + ts.slots * D;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, grp = lane >> 4;
-    const int hk = kv_head(ts, blk.h);
-
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
+    const StageMap sm = stage_map<T, D>(p, ts, lk, lv, lane);
+    Walk w;
+    walk_start(ts, blk, w);
+    {
+        const int p0 = slice_pos(p, blk, 0), hk = kv_head(ts, w.h);
+        stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0), lv,
+                         Vs, wave);
+    }
     const WaveGeo wg = wave_geo(ts, blk, wave, false);
     const Lane ln = lane_item(p, ts, blk, wave, col, false);
-    uint4 qf[D / 32], gf[D / 32], of[D / 32];
-    load_frags<T, D>(q, lq.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, qf);
-    load_frags<T, D>(dout, ldo.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, gf);
-    load_frags<T, D>(o, lo.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, of);
-    const float L2 = ln.valid ? lse[ll.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h)] * kLog2e : 0.f;
-    // delta from this lane's 8 head dims per 32, summed over the 4 lane rows
-    float di = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) {
-        const T* g8 = reinterpret_cast<const T*>(&gf[ks]);
-        const T* o8 = reinterpret_cast<const T*>(&of[ks]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) di = fmaf(to_f(g8[e]), to_f(o8[e]), di);
-    }
-    di = sum_rows(di);
-    if (dlse && ln.valid) di -= dlse[ldl.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h)];
-    if (ln.valid && grp == 0) delta[lde.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h)] = di;
-    const f32x4_t nd[2] = {f32x4_t{-di, -di, -di, -di}, f32x4_t{-di, -di, -di, -di}};
     const float sc2 = p.scale * kLog2e;
     const bool wide = ts.rowshift > 5;
     f32x4_t cb[2];
     column_bias(ln, ts.rowshift, 0, grp, cb);
 
-    f32x4_t acc[D / 16];
+    uint4 qf[D / 32], gf[D / 32];
+    f32x4_t acc[D / 16], nd[2];
+    float L2;
+    bool more = true, fresh = true;
+    while (more) {
+        const int b = w.b, h = w.h, u0 = w.u0;
+        if (fresh) {
+            uint4 of[D / 32];
+            load_frags<T, D>(bh_ptr(q, lq, b, h), vol_off(lq, ln.pos), ln.valid, grp, qf);
+            load_frags<T, D>(bh_ptr(dout, ldo, b, h), vol_off(ldo, ln.pos), ln.valid, grp, gf);
+            load_frags<T, D>(bh_ptr(o, lo, b, h), vol_off(lo, ln.pos), ln.valid, grp, of);
+            L2 = ln.valid ? bh_ptr(lse, ll, b, h)[vol_off(ll, ln.pos)] * kLog2e : 0.f;
+            // delta from this lane's 8 head dims per 32, summed over the 4 lane rows
+            float di = 0.f;
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    for (int u0 = 0; u0 < blk.U[0]; ++u0) {
-        const int p0 = blk.r[0] + (blk.lo[0] + u0) * p.ax[0].dil;
-        __syncthreads();
-        stage_rows<T, D>(p, blk, ts, plane_of(kg, lk, blk.b, hk, p0), lk, Ks, wave, lane);
-        stage_rows<T, D>(p, blk, ts, plane_of(vg, lv, blk.b, hk, p0), lv, Vs, wave, lane);
+            for (int ks = 0; ks < D / 32; ++ks) {
+                const T* g8 = reinterpret_cast<const T*>(&gf[ks]);
+                const T* o8 = reinterpret_cast<const T*>(&of[ks]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) di = fmaf(to_f(g8[e]), to_f(o8[e]), di);
+            }
+            di = sum_rows(di);
+            if (dlse && ln.valid) di -= bh_ptr(dlse, ldl, b, h)[vol_off(ldl, ln.pos)];
+            if (ln.valid && grp == 0) bh_ptr(delta, lde, b, h)[vol_off(lde, ln.pos)] = di;
+            nd[0] = nd[1] = f32x4_t{-di, -di, -di, -di};
+#pragma unroll
+            for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
         wait_loads();
         __syncthreads();
-        if (!wg.any || u0 < wg.lo[0] || u0 > wg.hi[0]) continue;
-        const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
-        for (int c = wg.c0; c <= wg.c1; ++c) {
-            f32x4_t bias[2] = {cb[0], cb[1]};
-            if (wide) column_bias(ln, ts.rowshift, c, grp, bias);
-            f32x4_t s[2], dp[2];
-            score_chunk<T, D>(Ks, c, col, grp, qf, bias, s);
-            score_chunk<T, D>(Vs, c, col, grp, gf, nd, dp);
-            const float off = row_ok(ln, ts.rowshift, in0, c, grp) ? -L2 : -INFINITY;
+        if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
+            const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
+            for (int c = wg.c0; c <= wg.c1; ++c) {
+                f32x4_t bias[2] = {cb[0], cb[1]};
+                if (wide) column_bias(ln, ts.rowshift, c, grp, bias);
+                f32x4_t s[2], dp[2];
+                score_chunk<T, D>(Ks, c, col, grp, qf, bias, s);
+                score_chunk<T, D>(Vs, c, col, grp, gf, nd, dp);
+                const float off = row_ok(ln, ts.rowshift, in0, c, grp) ? -L2 : -INFINITY;
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
+                for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) s[b][i] = __builtin_amdgcn_exp2f(fmaf(s[b][i], sc2, off)) * dp[b][i];
-            accumulate_chunk<T, D>(Ks, c, lane, pack8<T>(s), acc);
+                    for (int i = 0; i < 4; ++i)
+                        s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], sc2, off)) * dp[bb][i];
+                accumulate_chunk<T, D>(Ks, c, lane, pack8<T>(s), acc);
+            }
         }
+        more = walk_next(ts, blk, w, fresh);
+        __syncthreads();  // the slice is no longer read
+        if (more) {
+            const int p0 = slice_pos(p, blk, w.u0), hk = kv_head(ts, w.h);
+            stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0),
+                             lv, Vs, wave);
+        }
+        if ((fresh || !more) && ln.valid)
+            store_rows<T, D>(bh_ptr(dq, ldq, b, h), vol_off(ldq, ln.pos), grp, acc, p.scale);
     }
-    if (ln.valid) store_rows<T, D>(dq, ldq.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), grp, acc, p.scale);
 }
 
 // ---------------------------------------------------------------------------
@@ -580,15 +720,37 @@ __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const 
 // q head in the GQA group) whose window holds it:
 //   dv = sum P dO,   dk = scale * sum P (dP - delta) q.
 // Per staged slot: -lse * log2 e and -delta (fp32); 8 further -inf entries
-// serve lanes whose row test fails.
+// serve lanes whose row test fails.  Runs over (batch, kv head) pairs; the
+// walk's slices cover the GQA group's q heads one after the other.
 // ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void stage_scalars(const Prob& p, const Block& k, const TileShape& ts, int b, int h,
+                                              int p0, const float* __restrict__ lse, const LayK& ll,
+                                              const float* __restrict__ delta, const LayK& lde, float* NL,
+                                              float* ND) {
+    const int d1 = p.ax[1].dil, d2 = p.ax[2].dil, mask2 = (1 << ts.rowshift) - 1;
+    const float* lb = bh_ptr(lse, ll, b, h) + p0 * ll.s0;
+    const float* db = bh_ptr(delta, lde, b, h) + p0 * lde.s0;
+    for (int s = threadIdx.x; s < ts.slots; s += blockDim.x) {
+        const int a1 = s >> ts.rowshift, a2 = s & mask2;
+        float nl = 0.f, nd = 0.f;
+        if (a1 < k.U[1] && a2 < k.U[2]) {
+            const int p1 = k.r[1] + (k.lo[1] + a1) * d1, p2 = k.r[2] + (k.lo[2] + a2) * d2;
+            nl = -lb[p1 * ll.s1 + p2 * ll.s2] * kLog2e;
+            nd = -db[p1 * lde.s1 + p2 * lde.s2];
+        }
+        NL[s] = nl;
+        ND[s] = nd;
+    }
+}
+
 template <typename T, int D>
-__global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const T* __restrict__ q, Lay lq,
-                                                     const T* __restrict__ kg, Lay lk, const T* __restrict__ vg,
-                                                     Lay lv, const T* __restrict__ dout, Lay ldo,
-                                                     const float* __restrict__ lse, Lay ll,
-                                                     const float* __restrict__ delta, Lay lde,
-                                                     T* __restrict__ dk, Lay ldk, T* __restrict__ dv, Lay ldv) {
+__global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const T* __restrict__ q, LayK lq,
+                                                     const T* __restrict__ kg, LayK lk, const T* __restrict__ vg,
+                                                     LayK lv, const T* __restrict__ dout, LayK ldo,
+                                                     const float* __restrict__ lse, LayK ll,
+                                                     const float* __restrict__ delta, LayK lde,
+                                                     T* __restrict__ dk, LayK ldk, T* __restrict__ dv, LayK ldv) {
     extern __shared__ __align__(16) unsigned char smem[];
     Block blk;
     if (!decode_block(p, ts, true, blk)) return;
@@ -597,48 +759,44 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
     T* Gs = Qs + slots * D;
     float* NL = reinterpret_cast<float*>(Gs + slots * D);  // slots + 8
     float* ND = NL + slots + 8;                            // slots
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, col = lane & 15, grp = lane >> 4;
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
+    const int rep = static_cast<int>(ts.rep.d);
+    const StageMap sm = stage_map<T, D>(p, ts, lq, ldo, lane);
+    // the walk runs over (batch, kv head, q head of the group, slice): its
+    // slice counter spans rep * U0
+    Walk w;
+    walk_start(ts, blk, w);
+    const int nsl = rep * blk.U[0];
+    stage_pair<T, D>(p, blk, ts, sm, plane_of(q, lq, w.b, w.h * rep, slice_pos(p, blk, 0)), lq, Qs,
+                     plane_of(dout, ldo, w.b, w.h * rep, slice_pos(p, blk, 0)), ldo, Gs, wave);
     if (threadIdx.x < 8) NL[slots + threadIdx.x] = -INFINITY;
-
     const WaveGeo wg = wave_geo(ts, blk, wave, true);
     const Lane ln = lane_item(p, ts, blk, wave, col, true);
-    uint4 kf[D / 32], vf[D / 32];
-    load_frags<T, D>(kg, lk.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, kf);
-    load_frags<T, D>(vg, lv.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), ln.valid, grp, vf);
     const float sc2 = p.scale * kLog2e;
     const bool wide = ts.rowshift > 5;
     f32x4_t cb[2];
     column_bias(ln, ts.rowshift, 0, grp, cb);
-    const int d1 = p.ax[1].dil, d2 = p.ax[2].dil, mask2 = (1 << ts.rowshift) - 1;
+    stage_scalars<T>(p, blk, ts, w.b, w.h * rep, slice_pos(p, blk, 0), lse, ll, delta, lde, NL, ND);
 
+    uint4 kf[D / 32], vf[D / 32];
     f32x4_t gk[D / 16], gv[D / 16];
+    bool more = true, fresh = true;
+    int sl = 0;  // slice index within the pair: q head (sl / U0) and axis-0 slice (sl % U0)
+    while (more) {
+        const int b = w.b, hk = w.h, u0 = sl % blk.U[0];
+        if (fresh) {
+            load_frags<T, D>(bh_ptr(kg, lk, b, hk), vol_off(lk, ln.pos), ln.valid, grp, kf);
+            load_frags<T, D>(bh_ptr(vg, lv, b, hk), vol_off(lv, ln.pos), ln.valid, grp, vf);
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db) {
-        gk[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        gv[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-
-    for (int r = 0; r < static_cast<int>(ts.rep.d); ++r) {
-        const int h = blk.h * static_cast<int>(ts.rep.d) + r;
-        for (int u0 = 0; u0 < blk.U[0]; ++u0) {
-            const int p0 = blk.r[0] + (blk.lo[0] + u0) * p.ax[0].dil;
-            __syncthreads();
-            stage_rows<T, D>(p, blk, ts, plane_of(q, lq, blk.b, h, p0), lq, Qs, wave, lane);
-            stage_rows<T, D>(p, blk, ts, plane_of(dout, ldo, blk.b, h, p0), ldo, Gs, wave, lane);
-            for (int s = threadIdx.x; s < slots; s += blockDim.x) {
-                const int a1 = s >> ts.rowshift, a2 = s & mask2;
-                float nl = 0.f, nd = 0.f;
-                if (a1 < blk.U[1] && a2 < blk.U[2]) {
-                    const int p1 = blk.r[1] + (blk.lo[1] + a1) * d1, p2 = blk.r[2] + (blk.lo[2] + a2) * d2;
-                    nl = -lse[ll.at(blk.b, p0, p1, p2, h)] * kLog2e;
-                    nd = -delta[lde.at(blk.b, p0, p1, p2, h)];
-                }
-                NL[s] = nl;
-                ND[s] = nd;
+            for (int db = 0; db < D / 16; ++db) {
+                gk[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                gv[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
             }
-            wait_loads();
-            __syncthreads();
-            if (!wg.any || u0 < wg.lo[0] || u0 > wg.hi[0]) continue;
+        }
+        wait_loads();
+        __syncthreads();
+        if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
             for (int c = wg.c0; c <= wg.c1; ++c) {
                 const int s0 = 32 * c + 8 * grp;
@@ -653,20 +811,36 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
                 const f32x4_t nl[2] = {*reinterpret_cast<const f32x4_t*>(nlp),
                                        *reinterpret_cast<const f32x4_t*>(nlp + 4)};
 #pragma unroll
-                for (int b = 0; b < 2; ++b)
+                for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        s[b][i] = __builtin_amdgcn_exp2f(fmaf(s[b][i], sc2, nl[b][i]));
-                        dp[b][i] *= s[b][i];
+                        s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], sc2, nl[bb][i]));
+                        dp[bb][i] *= s[bb][i];
                     }
                 accumulate_chunk<T, D>(Gs, c, lane, pack8<T>(s), gv);
                 accumulate_chunk<T, D>(Qs, c, lane, pack8<T>(dp), gk);
             }
         }
+        // next slice: within the pair (q heads x axis-0 slices), else the next pair
+        fresh = false;
+        if (++sl >= nsl) {
+            sl = 0;
+            more = ++w.bh < blk.bh1;
+            if (more) split_bh(ts, w.bh, w.b, w.h);
+            fresh = true;
+        }
+        __syncthreads();  // the slice is no longer read
+        if (more) {
+            const int h = w.h * rep + sl / blk.U[0], p0 = slice_pos(p, blk, sl % blk.U[0]);
+            stage_pair<T, D>(p, blk, ts, sm, plane_of(q, lq, w.b, h, p0), lq, Qs, plane_of(dout, ldo, w.b, h, p0),
+                             ldo, Gs, wave);
+            stage_scalars<T>(p, blk, ts, w.b, h, p0, lse, ll, delta, lde, NL, ND);
+        }
+        if (fresh && ln.valid) {
+            store_rows<T, D>(bh_ptr(dk, ldk, b, hk), vol_off(ldk, ln.pos), grp, gk, p.scale);
+            store_rows<T, D>(bh_ptr(dv, ldv, b, hk), vol_off(ldv, ln.pos), grp, gv, 1.f);
+        }
     }
-    if (!ln.valid) return;
-    store_rows<T, D>(dk, ldk.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), grp, gk, p.scale);
-    store_rows<T, D>(dv, ldv.at(blk.b, ln.pos[0], ln.pos[1], ln.pos[2], blk.h), grp, gv, 1.f);
 }
 
 }  // namespace
@@ -724,6 +898,11 @@ size_t lds_bytes(Kind kind, int slots, int D) {
     return kind == kBackwardKV ? 2 * rows + (2 * static_cast<size_t>(slots) + 8) * 4 : 2 * rows;
 }
 
+void set_bh_per(TileShape& ts, int per) {
+    ts.bh_per = per;
+    ts.chunks = make_fastdiv(static_cast<uint32_t>((ts.nbh + per - 1) / per));
+}
+
 // Workgroup box in class coordinates: up to 64 items (4 waves), power-of-two
 // extents, innermost axis first (8 wide unless the problem is 1-D); halved
 // until the staged union fits the LDS budget.
@@ -752,6 +931,8 @@ bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts) {
         if (lds_bytes(kind, ts.slots, D) <= kLdsBudget) {
             const int heads = kind == kBackwardKV ? p.Hkv : p.Hq;
             ts.heads = make_fastdiv(static_cast<uint32_t>(heads));
+            ts.nbh = p.B * heads;
+            set_bh_per(ts, 1);
             ts.rep = make_fastdiv(static_cast<uint32_t>(p.rep));
             for (int a = 0; a < 3; ++a) {
                 ts.tiles[a] = make_fastdiv(static_cast<uint32_t>(ts.ntile[a]));
@@ -764,23 +945,69 @@ bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts) {
     return false;
 }
 
-long long grid_blocks(const Prob& p, const TileShape& ts, int heads) {
-    long long nb = static_cast<long long>(p.B) * heads;
+long long spatial_tiles(const Prob& p, const TileShape& ts) {
+    long long nb = 1;
     for (int a = 0; a < 3; ++a) nb *= static_cast<long long>(p.ax[a].dil) * ts.ntile[a];
     return nb;
 }
 
-// Staged operands: non-negative strides, and every in-plane byte offset (axes
-// 1 and 2, plus a row of 128 head dims) inside the buffer range of a plane.
+long long grid_blocks(const Prob& p, const TileShape& ts) { return spatial_tiles(p, ts) * ts.chunks.d; }
+
+// Workgroups of `kernel` (block threads, shm bytes of LDS) resident on the
+// current device at once; cached per (kernel, block, shm, device).
+template <typename K>
+long long resident_blocks(K kernel, int block, size_t shm) {
+    struct Entry {
+        const void* f;
+        int block;
+        size_t shm;
+        int dev;
+        long long n;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    const void* f = reinterpret_cast<const void*>(kernel);
+    std::lock_guard<std::mutex> g(mu);
+    for (const Entry& e : cache)
+        if (e.f == f && e.block == block && e.shm == shm && e.dev == dev) return e.n;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, shm) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
+    cache.push_back(Entry{f, block, shm, dev, static_cast<long long>(per_cu) * cus});
+    return cache.back().n;
+}
+
+// (batch, head) pairs per workgroup: enough workgroups to fill the device
+// about twice over; NATTEN_HIP_BH_PER=n fixes it (tuning).
+void fit_bh_per(const Prob& p, TileShape& ts, long long resident) {
+    static const int forced = [] {
+        const char* e = std::getenv("NATTEN_HIP_BH_PER");
+        return e ? std::atoi(e) : 0;
+    }();
+    const long long spatial = spatial_tiles(p, ts);
+    long long per = forced > 0 ? forced : (spatial * ts.nbh) / (2 * resident);
+    per = std::max(1LL, std::min<long long>(per, ts.nbh));
+    set_bh_per(ts, static_cast<int>(per));
+}
+
+// Every operand: non-negative strides and every offset inside one (batch,
+// head) (plus a row of 128 head dims) in 31 bits; staged operands' in-plane
+// byte offsets (axes 1 and 2) inside the buffer range of a plane.
 bool offsets_fit(const Prob& p, std::initializer_list<Lay> lays) {
     for (const Lay& l : lays) {
         if (l.b < 0 || l.s0 < 0 || l.s1 < 0 || l.s2 < 0 || l.h < 0) return false;
-        const long long m = (static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
-                            (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + 128;
-        if (m * 2 >= kPlaneBytes) return false;
+        const long long plane = (static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
+                                (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + 128;
+        const long long vol = (static_cast<long long>(p.ax[0].len) - 1) * l.s0 + plane;
+        if (plane * 2 >= kPlaneBytes || vol >= (1LL << 31)) return false;
     }
     return true;
 }
+
+LayK to_k(const Lay& l) { return LayK{l.b, l.h, static_cast<int>(l.s0), static_cast<int>(l.s1), static_cast<int>(l.s2), 0}; }
 
 template <typename K>
 hipError_t allow_lds(K kernel, size_t bytes) {
@@ -797,9 +1024,10 @@ hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
     const size_t shm = lds_bytes(kForward, ts.slots, D);
     hipError_t e = allow_lds(k_fwd_mfma<T, D>, shm);
     if (e != hipSuccess) return e;
-    NA_LAUNCH("na_fwd_mfma", (k_fwd_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, ts, p.Hq))),
-              dim3(64 * ts.waves), shm, s, p, ts, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (T*)o, lo, lse,
-              ll);
+    fit_bh_per(p, ts, resident_blocks(k_fwd_mfma<T, D>, 64 * ts.waves, shm));
+    NA_LAUNCH("na_fwd_mfma", (k_fwd_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, ts))),
+              dim3(64 * ts.waves), shm, s, p, ts, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
+              (T*)o, to_k(lo), lse, to_k(ll));
     return hipGetLastError();
 }
 
@@ -814,14 +1042,18 @@ hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
     hipError_t e = allow_lds(k_bwd_q_mfma<T, D>, shq);
     if (e == hipSuccess) e = allow_lds(k_bwd_kv_mfma<T, D>, shk);
     if (e != hipSuccess) return e;
-    NA_LAUNCH("na_bwd_q_mfma", (k_bwd_q_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tq, p.Hq))),
-              dim3(64 * tq.waves), shq, s, p, tq, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv,
-              (const T*)o, lo, (const T*)dout, ldo, lse, ll, dlse, ldl, (T*)dq, ldq, delta, lde);
+    fit_bh_per(p, tq, resident_blocks(k_bwd_q_mfma<T, D>, 64 * tq.waves, shq));
+    fit_bh_per(p, tk, resident_blocks(k_bwd_kv_mfma<T, D>, 64 * tk.waves, shk));
+    NA_LAUNCH("na_bwd_q_mfma", (k_bwd_q_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tq))),
+              dim3(64 * tq.waves), shq, s, p, tq, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
+              (const T*)o, to_k(lo), (const T*)dout, to_k(ldo), lse, to_k(ll), dlse, to_k(ldl), (T*)dq, to_k(ldq), delta,
+              to_k(lde));
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    NA_LAUNCH("na_bwd_kv_mfma", (k_bwd_kv_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tk, p.Hkv))),
-              dim3(64 * tk.waves), shk, s, p, tk, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv,
-              (const T*)dout, ldo, lse, ll, (const float*)delta, lde, (T*)dk, ldk, (T*)dv, ldv);
+    NA_LAUNCH("na_bwd_kv_mfma", (k_bwd_kv_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tk))),
+              dim3(64 * tk.waves), shk, s, p, tk, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
+              (const T*)dout, to_k(ldo), lse, to_k(ll), (const float*)delta, to_k(lde), (T*)dk, to_k(ldk), (T*)dv,
+              to_k(ldv));
     return hipGetLastError();
 }
 
@@ -834,10 +1066,10 @@ bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward)
         if (p.ax[a].st != 1) return false;
     // tile indices (the launch grid) stay in 31 bits
     TileShape ts{};
-    if (!choose_tile(p, kForward, D, ts) || grid_blocks(p, ts, p.Hq) >= (1LL << 31)) return false;
+    if (!choose_tile(p, kForward, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
     if (backward) {
-        if (!choose_tile(p, kBackwardQ, D, ts) || grid_blocks(p, ts, p.Hq) >= (1LL << 31)) return false;
-        if (!choose_tile(p, kBackwardKV, D, ts) || grid_blocks(p, ts, p.Hkv) >= (1LL << 31)) return false;
+        if (!choose_tile(p, kBackwardQ, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
+        if (!choose_tile(p, kBackwardKV, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
     }
     return true;
 }
