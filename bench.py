@@ -1,21 +1,28 @@
-"""Benchmark of the hot path: na2d forward+backward, DiNAT scale
-(B=16, 56x56, 4 heads, head dim 32, kernel 7, bf16), on one MI355X.
+"""Benchmark of the hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--dilation 1] [--no-cpu] [--no-graph]
+                    [--config 3] [--causal FF]
 
-A step is one forward + backward pass through the public API
-(``natten_mps_amd.na2d`` then ``torch.autograd.grad``) on synthetic seeded
-inputs already resident in HBM.  The step is timed eagerly and, captured
-once in a HIP graph (torch.cuda.CUDAGraph), as graph replays whose outputs
-are checked equal to eager steps; the step time reported is the replay's
-(the eager one is in ``config.eager_ms_per_step``).  Prints one JSON line:
+Default workload: na2d forward+backward at DiNAT scale (B=16, 56x56, 4 heads,
+head dim 32, kernel 7, bf16), BASELINE config 3.  ``--config N`` runs another
+of the five BASELINE configs instead (``--dilation`` for configs 3 and 4,
+``--causal TF`` for config 2); only config 3 carries the CPU baseline.
+
+A step is one pass through the public API (``natten_mps_amd.na{1,2,3}d``, then
+``torch.autograd.grad`` for the configs with a backward) on synthetic seeded
+inputs already resident in HBM.  The step is timed eagerly and, captured once
+in a HIP graph (torch.cuda.CUDAGraph), as graph replays whose outputs are
+checked equal to eager steps; the step time reported is the replay's (the
+eager one is in ``config.eager_ms_per_step``).  Prints one JSON line:
 
 * value / unit: effective TFLOP/s = (fwd 4*P*D + bwd 10*P*D) / step time,
   with P = B * Hq * (valid query-key pairs of the neighbourhood map);
 * roofline: for the kernel with the largest share of GPU time, its
   algorithmic HBM bytes per launch / its mean launch time (HIP events
   bracketing each launch on its stream, recorded during the timed steps),
-  against 8 TB/s;
+  against 8 TB/s; ``traffic`` is the HBM bytes per launch measured with
+  rocprofv3 (FETCH_SIZE x 2 + WRITE_SIZE, calibrated on a copy kernel) for
+  the same kernel and workload, read from profiles/traffic.txt when present;
 * cpu_baseline: the CPU oracle (the reference's pure algorithm) timed on the
   host for a bounded sample of the same workload.
 """
@@ -36,17 +43,31 @@ for _p in (ROOT, os.path.join(ROOT, "natten-mps_amd")):
 HBM_PEAK_GBS = 8000.0
 METRIC = "na2d fwd+bwd ms & effective TFLOP/s (56×56,K=7,bf16); % of roofline"
 
-CFG = dict(B=16, H=56, W=56, heads=4, dim=32, kernel=7)
+# BASELINE configs
+CONFIGS = {
+    1: dict(batch=2, spatial=(128,), heads=4, kv_heads=4, dim=32, kernel=(7,), dilation=(1,), causal=(False,),
+            dtype="float32", backward=False, seed=1001),
+    2: dict(batch=2, spatial=(32, 32), heads=4, kv_heads=4, dim=32, kernel=(7, 7), dilation=(1, 1),
+            causal=(False, False), dtype="float32", backward=True, seed=1002),
+    3: dict(batch=16, spatial=(56, 56), heads=4, kv_heads=4, dim=32, kernel=(7, 7), dilation=(1, 1),
+            causal=(False, False), dtype="bfloat16", backward=True, seed=1003),
+    4: dict(batch=4, spatial=(16384,), heads=8, kv_heads=2, dim=64, kernel=(33,), dilation=(1,), causal=(True,),
+            dtype="bfloat16", backward=True, seed=1004),
+    5: dict(batch=2, spatial=(16, 32, 32), heads=8, kv_heads=8, dim=64, kernel=(3, 7, 7), dilation=(1, 2, 2),
+            causal=(False, False, False), dtype="bfloat16", backward=True, seed=1005),
+}
+DTYPE_TAG = {"float32": "fp32", "bfloat16": "bf16", "float16": "fp16"}
 
 
 def _log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def _valid_pairs(spatial, kernel, dilation, stride, causal, device):
+def _valid_pairs(spatial, kernel, dilation, causal, device):
     from natten_mps_amd._core import hip
 
-    _, valid = hip.neighborhood_map(len(spatial), spatial, kernel, dilation, stride, causal, device)
+    ones = (1,) * len(spatial)
+    _, valid = hip.neighborhood_map(len(spatial), spatial, kernel, dilation, ones, causal, device)
     return int(valid.sum().item())
 
 
@@ -55,28 +76,52 @@ def kernel_bytes(name, B, N, Hq, Hkv, D, esz):
     read once, every result written once; K/V at Hkv heads; fp32 LSE/delta)."""
     tq, tkv, lse = B * N * Hq * D * esz, B * N * Hkv * D * esz, B * N * Hq * 4
     fwd = tq + 2 * tkv + tq + lse                 # q, k, v -> out, lse
-    bwd_q = tq + 2 * tkv + tq + lse + tq + lse    # q, k, v, dout, lse -> dq, delta
+    bwd_q = tq + 2 * tkv + tq + lse + tq + lse    # q, k, v, dout, o, lse -> dq, delta
+    bwd_q_mfma = bwd_q + tq                       # ... the tile kernel also reads o
     bwd_kv = tq + 2 * tkv + tq + 2 * lse + 2 * tkv  # q, k, v, dout, lse, delta -> dk, dv
     return {
         "na_forward": fwd, "na_fwd_mfma": fwd,
-        "na_bwd_dq": bwd_q + tq, "na_bwd_q_mfma": bwd_q,   # the vector kernel also reads out
+        "na_bwd_dq": bwd_q, "na_bwd_q_mfma": bwd_q_mfma,
         "na_bwd_dkdv": bwd_kv, "na_bwd_kv_mfma": bwd_kv,
     }.get(name)
 
 
+def step_bytes(B, N, Hq, Hkv, D, esz, backward):
+    """Compulsory HBM bytes of a step: forward reads q, k, v and writes out,
+    lse; backward reads q, k, v, out, dout, lse and writes dq, dk, dv."""
+    tq, tkv, lse = B * N * Hq * D * esz, B * N * Hkv * D * esz, B * N * Hq * 4
+    fwd = 2 * tq + 2 * tkv + lse
+    bwd = 3 * tq + 2 * tkv + lse + tq + 2 * tkv
+    return fwd + (bwd if backward else 0)
+
+
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch from profiles/traffic.txt ("kernel workload bytes")."""
+    path = os.path.join(ROOT, "profiles", "traffic.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 3 and not line.startswith("#") and parts[0] == kernel and parts[1] == workload:
+                return int(parts[2])
+    return None
+
+
 def cpu_baseline(dilation, budget_s=20.0):
     """The oracle (reference pure algorithm, torch on the host CPU) on a
-    bounded sample: the same problem at batch 1 (1/16 of the workload), bf16,
+    bounded sample: config 3 at batch 1 (1/16 of the workload), bf16,
     forward + backward, median of the timed repeats."""
     import torch
 
     import oracle.pure as P
 
+    cfg = CONFIGS[3]
     torch.set_num_threads(os.cpu_count() or 1)
-    g = torch.Generator().manual_seed(1003)
-    shape = (1, CFG["H"], CFG["W"], CFG["heads"], CFG["dim"])
+    g = torch.Generator().manual_seed(cfg["seed"])
+    shape = (1, *cfg["spatial"], cfg["heads"], cfg["dim"])
     q, k, v, do = (torch.randn(shape, generator=g).to(torch.bfloat16) for _ in range(4))
-    ks, dil = (CFG["kernel"],) * 2, (dilation,) * 2
+    ks, dil = cfg["kernel"], (dilation,) * 2
 
     def step():
         leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
@@ -89,8 +134,11 @@ def cpu_baseline(dilation, budget_s=20.0):
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
-    pairs = CFG["H"] * CFG["W"] * CFG["kernel"] ** 2 * CFG["heads"]  # non-causal: windows always full
-    flops = 14.0 * pairs * CFG["dim"]
+    n = 1
+    for s in cfg["spatial"]:
+        n *= s
+    pairs = n * cfg["kernel"][0] * cfg["kernel"][1] * cfg["heads"]  # non-causal: windows always full
+    flops = 14.0 * pairs * cfg["dim"]
     med = statistics.median(times)
     return {
         "value": flops / med / 1e12,
@@ -108,7 +156,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--dilation", type=int, default=1)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
+    ap.add_argument("--dilation", type=int, default=None, help="dilation of configs 3 and 4 (default 1)")
+    ap.add_argument("--causal", default=None, help="config 2 causal flags, e.g. TF")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="time eager steps only")
     args = ap.parse_args()
@@ -125,19 +175,36 @@ def main():
     from natten_mps_amd import functional as F
     from natten_mps_amd._core import _lib
 
+    cfg = dict(CONFIGS[args.config])
+    rank = len(cfg["spatial"])
+    if args.dilation is not None and args.config in (3, 4):
+        cfg["dilation"] = (args.dilation,) * rank
+    if args.causal is not None and args.config == 2:
+        cfg["causal"] = tuple(c.upper() == "T" for c in args.causal)
     natten_mps_amd.set_backend("hip")
     dev = torch.device("cuda:0")
-    B, H, W, Hq, D, K = CFG["B"], CFG["H"], CFG["W"], CFG["heads"], CFG["dim"], CFG["kernel"]
-    dil = args.dilation
-    g = torch.Generator().manual_seed(1003)
-    q, k, v, do = (torch.randn((B, H, W, Hq, D), generator=g).to(torch.bfloat16).to(dev) for _ in range(4))
-    q.requires_grad_(True)
-    k.requires_grad_(True)
-    v.requires_grad_(True)
+    dtype = getattr(torch, cfg["dtype"])
+    B, Hq, Hkv, D = cfg["batch"], cfg["heads"], cfg["kv_heads"], cfg["dim"]
+    N = 1
+    for s in cfg["spatial"]:
+        N *= s
+    g = torch.Generator().manual_seed(cfg["seed"])
+
+    def make(h):
+        return torch.randn((B, *cfg["spatial"], h, D), generator=g).to(dtype).to(dev)
+
+    q, k, v, do = make(Hq), make(Hkv), make(Hkv), make(Hq)
+    na = {1: F.na1d, 2: F.na2d, 3: F.na3d}[rank]
+    leaves = (q, k, v)
+    if cfg["backward"]:
+        for t in leaves:
+            t.requires_grad_(True)
 
     def step():
-        out = F.na2d(q, k, v, kernel_size=K, dilation=dil)
-        return torch.autograd.grad(out, (q, k, v), do)
+        out = na(q, k, v, kernel_size=cfg["kernel"], dilation=cfg["dilation"], is_causal=cfg["causal"])
+        if not cfg["backward"]:
+            return (out,)
+        return torch.autograd.grad(out, leaves, do)
 
     for _ in range(args.warmup):
         step()
@@ -168,7 +235,7 @@ def main():
     # and replayed: identical kernels and buffers without the per-step host
     # work.  Every replay is checked bit for bit against an eager step, with
     # eager work and synchronisation between the replays.
-    ms_graph, graph_ok = None, False
+    ms_graph = None
     if not args.no_graph:
         try:
             side = torch.cuda.Stream()
@@ -197,37 +264,44 @@ def main():
             _log("graph capture failed:", repr(e))
     ms = ms_graph if ms_graph is not None else ms_eager
 
-    pairs = B * Hq * _valid_pairs((H, W), (K, K), (dil, dil), (1, 1), (False, False), dev)
-    flops = 14.0 * pairs * D
+    pairs = B * Hq * _valid_pairs(cfg["spatial"], cfg["kernel"], cfg["dilation"], cfg["causal"], dev)
+    flops = (14.0 if cfg["backward"] else 4.0) * pairs * D
     tflops = flops / (ms * 1e-3) / 1e12
+    esz = torch.tensor([], dtype=dtype).element_size()
+    sbytes = step_bytes(B, N, Hq, Hkv, D, esz, cfg["backward"])
 
     gpu_total = sum(s[1] for s in stats.values())
     for name, (n, tot, mn, mx) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
         _log(f"  {name:14s} launches={n:4d} mean={tot / n * 1e3:8.1f} us  min={mn * 1e3:8.1f}  max={mx * 1e3:8.1f}"
              f"  share={tot / gpu_total:5.1%}")
-    dom = max(stats.items(), key=lambda kv: kv[1][1])
-    dom_name, (dn, dtot, _, _) = dom
-    nbytes = kernel_bytes(dom_name, B, H * W, Hq, Hq, D, 2)
+    dil_tag = "x".join(str(d) for d in cfg["dilation"])
+    workload = f"config{args.config}_d{dil_tag}"
+    dom_name, (dn, dtot, _, _) = max(stats.items(), key=lambda kv: kv[1][1])
+    nbytes = kernel_bytes(dom_name, B, N, Hq, Hkv, D, esz)
     mean_s = dtot / dn * 1e-3
     roof = None
     if nbytes is not None:
         gbs = nbytes / mean_s / 1e9
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom_name,
-                "mean_us": round(mean_s * 1e6, 2), "alg_bytes": nbytes}
-    fwd_bwd_bytes = (4 * B * H * W * Hq * D * 2 + B * H * W * Hq * 4) + (8 * B * H * W * Hq * D * 2 + 2 * B * H * W * Hq * 4)
-    _log(f"step {ms:.3f} ms  {tflops:.2f} TFLOP/s  fwd+bwd HBM floor {fwd_bwd_bytes / 8e12 * 1e6:.1f} us "
-         f"-> {fwd_bwd_bytes / 8e12 / (ms * 1e-3):.1%} of roofline (step)")
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_name, workload),
+                "kernel": dom_name, "mean_us": round(mean_s * 1e6, 2), "alg_bytes": nbytes}
+    _log(f"step {ms:.4f} ms  {tflops:.2f} TFLOP/s  {sbytes / (ms * 1e-3) / 1e9:.0f} GB/s  "
+         f"HBM floor {sbytes / 8e12 * 1e6:.1f} us -> {sbytes / 8e12 / (ms * 1e-3):.1%} of roofline (step)")
 
     cpu = None
-    if not args.no_cpu:
+    if args.config == 3 and not args.no_cpu:
         try:
-            cpu = cpu_baseline(dil)
+            cpu = cpu_baseline(cfg["dilation"][0])
         except Exception as e:  # the baseline is reported, never required
             _log("cpu baseline failed:", repr(e))
 
+    shape = "x".join(str(s) for s in cfg["spatial"])
+    causal_tag = "".join("T" if c else "F" for c in cfg["causal"])
+    desc = (f"na{rank}d {'fwd+bwd' if cfg['backward'] else 'fwd'} B={B} {shape} heads={Hq}/{Hkv} dim={D} "
+            f"K={cfg['kernel']} dilation={cfg['dilation']} causal={causal_tag} {DTYPE_TAG[cfg['dtype']]} "
+            f"(BASELINE config {args.config})")
     print(json.dumps({
-        "metric": METRIC,
+        "metric": METRIC if args.config == 3 else f"na{rank}d step ms & effective TFLOP/s (config {args.config})",
         "value": round(tflops, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -237,13 +311,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": DTYPE_TAG[cfg["dtype"]],
         "data": "synthetic (seeded randn, resident in HBM)",
-        "config": {"workload": f"na2d fwd+bwd B=16 56x56 heads=4 dim=32 K=7 dilation={dil} bf16 (BASELINE config 3)",
-                   "global_batch": B, "seq_len": H * W, "parallelism": "single GPU",
+        "config": {"workload": desc, "global_batch": B, "seq_len": N, "parallelism": "single GPU",
                    "timing": "HIP graph replay of the eager step (checked equal)" if ms_graph is not None
                    else "eager", "eager_ms_per_step": round(ms_eager, 4),
-                   "hbm_floor_frac_step": round(fwd_bwd_bytes / 8e12 / (ms * 1e-3), 4)},
+                   "step_hbm_bytes": sbytes, "step_gbs": round(sbytes / (ms * 1e-3) / 1e9, 1),
+                   "hbm_floor_frac_step": round(sbytes / 8e12 / (ms * 1e-3), 4)},
         "roofline": roof,
         "cpu_baseline": cpu,
     }), flush=True)
