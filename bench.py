@@ -161,6 +161,8 @@ def main():
     ap.add_argument("--causal", default=None, help="config 2 causal flags, e.g. TF")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="time eager steps only")
+    ap.add_argument("--copy-probe", type=float, default=None, metavar="MB",
+                    help="only run device-to-device copies of this many MB (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -170,6 +172,18 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_probe is not None:
+        # a plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch
+        # give the factors that turn those counters into HBM bytes
+        n = int(args.copy_probe * 1e6) // 2
+        src = torch.randn(n, device="cuda:0").to(torch.bfloat16)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": 2 * n, "copies": args.steps}), flush=True)
+        return
 
     import natten_mps_amd
     from natten_mps_amd import functional as F

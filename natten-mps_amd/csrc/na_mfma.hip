@@ -152,14 +152,14 @@ __device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)"
 // Host-chosen tile: power-of-two extents T = 2^tshift (class coordinates) of a
 // workgroup's box, tiles per class per axis, waves per workgroup, the staged
 // slice layout (slot = a1 * 2^rowshift + a2, `slots` per slice, a multiple of
-// 32), len % dil per axis, the run of (batch, head) pairs a workgroup works
-// through for its box, and divisors for decoding the workgroup index.
+// 32), len % dil per axis, the run of heads a workgroup works through for
+// its box, and divisors for decoding the workgroup index.
 struct TileShape {
     int T[3], tshift[3], ntile[3];
     int waves, slots, rowshift;
     int lenmod[3];
-    int nbh, bh_per;  // (batch, head) pairs, and how many one workgroup runs
-    FastDiv heads, rep, chunks, tiles[3], dil[3];
+    int nheads, h_per;  // heads, and how many of them one workgroup runs
+    FastDiv rep, hchunks, tiles[3], dil[3];
 };
 
 // Operand layout as the kernels take it: 64-bit batch and head strides, and
@@ -172,7 +172,7 @@ struct LayK {
 namespace {
 
 struct Block {
-    int bh0, bh1;  // run of flattened (batch, head) indices
+    int b, h0, h1;  // batch and run of heads [h0, h1)
     int r[3], J[3], E[3], lo[3], U[3];
     ClassAxis c[3];
 };
@@ -187,15 +187,17 @@ __device__ __forceinline__ ClassAxis class_axis_of(const Axis& a, int r, const F
     return c;
 }
 
-// Workgroup -> (run of (batch, head) pairs, residues, tile origin J, clipped
-// extent E) and the union box [lo, lo+U) of the windows of its queries
-// (key_tile = false) or of the queries attending its keys (key_tile = true).
-// The geometry is the same for every (batch, head).  False: empty tile.
+// Workgroup -> (batch, run of heads, residues, tile origin J, clipped extent
+// E) and the union box [lo, lo+U) of the windows of its queries (key_tile =
+// false) or of the queries attending its keys (key_tile = true).  The
+// geometry is the same for every (batch, head).  Heads vary fastest, then
+// tiles, then batch, so that neighbouring tiles (which share halo rows) run
+// close together in time on the same XCD.  False: empty tile.
 __device__ __forceinline__ bool decode_block(const Prob& p, const TileShape& ts, bool key_tile, Block& k) {
     int x = xcd_block(blockIdx.x, gridDim.x);
-    int q = fdiv(x, ts.chunks);
-    k.bh0 = (x - q * static_cast<int>(ts.chunks.d)) * ts.bh_per;
-    k.bh1 = min(k.bh0 + ts.bh_per, ts.nbh);
+    int q = fdiv(x, ts.hchunks);
+    k.h0 = (x - q * static_cast<int>(ts.hchunks.d)) * ts.h_per;
+    k.h1 = min(k.h0 + ts.h_per, ts.nheads);
     x = q;
     int t[3];
     for (int a = 2; a >= 0; --a) {
@@ -206,6 +208,7 @@ __device__ __forceinline__ bool decode_block(const Prob& p, const TileShape& ts,
         k.r[a] = x - q * static_cast<int>(ts.dil[a].d);
         x = q;
     }
+    k.b = x;
     for (int a = 0; a < 3; ++a) {
         const ClassAxis c = class_axis_of(p.ax[a], k.r[a], ts.dil[a], ts.lenmod[a]);
         k.c[a] = c;
@@ -480,12 +483,6 @@ __device__ __forceinline__ void store_rows(T* __restrict__ g, long long off, int
     }
 }
 
-// (batch, head) of flattened index bh (batch-major).
-__device__ __forceinline__ void split_bh(const TileShape& ts, int bh, int& b, int& h) {
-    b = fdiv(bh, ts.heads);
-    h = bh - b * static_cast<int>(ts.heads.d);
-}
-
 __device__ __forceinline__ int kv_head(const TileShape& ts, int h) { return ts.rep.d == 1 ? h : fdiv(h, ts.rep); }
 
 // Walk of a workgroup over its (batch, head) pairs and axis-0 slices.  The
@@ -493,23 +490,22 @@ __device__ __forceinline__ int kv_head(const TileShape& ts, int h) { return ts.r
 // read, and the very first right after decoding the tile, so that the
 // per-lane setup runs while they are in flight.
 struct Walk {
-    int bh, u0, b, h;
+    int h, u0, b;
 };
 
-__device__ __forceinline__ void walk_start(const TileShape& ts, const Block& k, Walk& w) {
-    w.bh = k.bh0;
+__device__ __forceinline__ void walk_start(const Block& k, Walk& w) {
+    w.h = k.h0;
     w.u0 = 0;
-    split_bh(ts, w.bh, w.b, w.h);
+    w.b = k.b;
 }
 
 // Advance to the next slice; false past the last one.  `new_pair` reports a
-// change of (batch, head).
-__device__ __forceinline__ bool walk_next(const TileShape& ts, const Block& k, Walk& w, bool& new_pair) {
+// change of head.
+__device__ __forceinline__ bool walk_next(const Block& k, Walk& w, bool& new_pair) {
     new_pair = false;
     if (++w.u0 < k.U[0]) return true;
     w.u0 = 0;
-    if (++w.bh >= k.bh1) return false;
-    split_bh(ts, w.bh, w.b, w.h);
+    if (++w.h >= k.h1) return false;
     new_pair = true;
     return true;
 }
@@ -537,7 +533,7 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T*
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
     const StageMap sm = stage_map<T, D>(p, ts, lk, lv, lane);
     Walk w;
-    walk_start(ts, blk, w);
+    walk_start(blk, w);
     {
         const int p0 = slice_pos(p, blk, 0), hk = kv_head(ts, w.h);
         stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0), lv,
@@ -606,7 +602,7 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T*
                 }
             }
         }
-        more = walk_next(ts, blk, w, fresh);
+        more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
         if (more) {
             const int p0 = slice_pos(p, blk, w.u0), hk = kv_head(ts, w.h);
@@ -643,7 +639,7 @@ __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
     const StageMap sm = stage_map<T, D>(p, ts, lk, lv, lane);
     Walk w;
-    walk_start(ts, blk, w);
+    walk_start(blk, w);
     {
         const int p0 = slice_pos(p, blk, 0), hk = kv_head(ts, w.h);
         stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0), lv,
@@ -703,7 +699,7 @@ __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const 
                 accumulate_chunk<T, D>(Ks, c, lane, pack8<T>(s), acc);
             }
         }
-        more = walk_next(ts, blk, w, fresh);
+        more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
         if (more) {
             const int p0 = slice_pos(p, blk, w.u0), hk = kv_head(ts, w.h);
@@ -766,7 +762,7 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
     // the walk runs over (batch, kv head, q head of the group, slice): its
     // slice counter spans rep * U0
     Walk w;
-    walk_start(ts, blk, w);
+    walk_start(blk, w);
     const int nsl = rep * blk.U[0];
     stage_pair<T, D>(p, blk, ts, sm, plane_of(q, lq, w.b, w.h * rep, slice_pos(p, blk, 0)), lq, Qs,
                      plane_of(dout, ldo, w.b, w.h * rep, slice_pos(p, blk, 0)), ldo, Gs, wave);
@@ -825,8 +821,7 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
         fresh = false;
         if (++sl >= nsl) {
             sl = 0;
-            more = ++w.bh < blk.bh1;
-            if (more) split_bh(ts, w.bh, w.b, w.h);
+            more = ++w.h < blk.h1;
             fresh = true;
         }
         __syncthreads();  // the slice is no longer read
@@ -898,9 +893,9 @@ size_t lds_bytes(Kind kind, int slots, int D) {
     return kind == kBackwardKV ? 2 * rows + (2 * static_cast<size_t>(slots) + 8) * 4 : 2 * rows;
 }
 
-void set_bh_per(TileShape& ts, int per) {
-    ts.bh_per = per;
-    ts.chunks = make_fastdiv(static_cast<uint32_t>((ts.nbh + per - 1) / per));
+void set_h_per(TileShape& ts, int per) {
+    ts.h_per = per;
+    ts.hchunks = make_fastdiv(static_cast<uint32_t>((ts.nheads + per - 1) / per));
 }
 
 // Workgroup box in class coordinates: up to 64 items (4 waves), power-of-two
@@ -930,9 +925,8 @@ bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts) {
         ts.slots = ((u1 * (1 << ts.rowshift) + 31) / 32) * 32;
         if (lds_bytes(kind, ts.slots, D) <= kLdsBudget) {
             const int heads = kind == kBackwardKV ? p.Hkv : p.Hq;
-            ts.heads = make_fastdiv(static_cast<uint32_t>(heads));
-            ts.nbh = p.B * heads;
-            set_bh_per(ts, 1);
+            ts.nheads = heads;
+            set_h_per(ts, 1);
             ts.rep = make_fastdiv(static_cast<uint32_t>(p.rep));
             for (int a = 0; a < 3; ++a) {
                 ts.tiles[a] = make_fastdiv(static_cast<uint32_t>(ts.ntile[a]));
@@ -951,7 +945,9 @@ long long spatial_tiles(const Prob& p, const TileShape& ts) {
     return nb;
 }
 
-long long grid_blocks(const Prob& p, const TileShape& ts) { return spatial_tiles(p, ts) * ts.chunks.d; }
+long long grid_blocks(const Prob& p, const TileShape& ts) {
+    return spatial_tiles(p, ts) * p.B * static_cast<long long>(ts.hchunks.d);
+}
 
 // Workgroups of `kernel` (block threads, shm bytes of LDS) resident on the
 // current device at once; cached per (kernel, block, shm, device).
@@ -980,17 +976,17 @@ long long resident_blocks(K kernel, int block, size_t shm) {
     return cache.back().n;
 }
 
-// (batch, head) pairs per workgroup: enough workgroups to fill the device
-// about twice over; NATTEN_HIP_BH_PER=n fixes it (tuning).
-void fit_bh_per(const Prob& p, TileShape& ts, long long resident) {
+// Heads per workgroup: one unless the grid would still fill the device about
+// twice over with more; NATTEN_HIP_HEADS_PER=n fixes it (tuning).
+void fit_h_per(const Prob& p, TileShape& ts, long long resident) {
     static const int forced = [] {
-        const char* e = std::getenv("NATTEN_HIP_BH_PER");
+        const char* e = std::getenv("NATTEN_HIP_HEADS_PER");
         return e ? std::atoi(e) : 0;
     }();
-    const long long spatial = spatial_tiles(p, ts);
-    long long per = forced > 0 ? forced : (spatial * ts.nbh) / (2 * resident);
-    per = std::max(1LL, std::min<long long>(per, ts.nbh));
-    set_bh_per(ts, static_cast<int>(per));
+    const long long cells = spatial_tiles(p, ts) * p.B;
+    long long per = forced > 0 ? forced : (cells * ts.nheads) / (4 * resident);
+    per = std::max(1LL, std::min<long long>(per, ts.nheads));
+    set_h_per(ts, static_cast<int>(per));
 }
 
 // Every operand: non-negative strides and every offset inside one (batch,
@@ -1024,7 +1020,7 @@ hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
     const size_t shm = lds_bytes(kForward, ts.slots, D);
     hipError_t e = allow_lds(k_fwd_mfma<T, D>, shm);
     if (e != hipSuccess) return e;
-    fit_bh_per(p, ts, resident_blocks(k_fwd_mfma<T, D>, 64 * ts.waves, shm));
+    fit_h_per(p, ts, resident_blocks(k_fwd_mfma<T, D>, 64 * ts.waves, shm));
     NA_LAUNCH("na_fwd_mfma", (k_fwd_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, ts))),
               dim3(64 * ts.waves), shm, s, p, ts, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
               (T*)o, to_k(lo), lse, to_k(ll));
@@ -1042,8 +1038,8 @@ hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
     hipError_t e = allow_lds(k_bwd_q_mfma<T, D>, shq);
     if (e == hipSuccess) e = allow_lds(k_bwd_kv_mfma<T, D>, shk);
     if (e != hipSuccess) return e;
-    fit_bh_per(p, tq, resident_blocks(k_bwd_q_mfma<T, D>, 64 * tq.waves, shq));
-    fit_bh_per(p, tk, resident_blocks(k_bwd_kv_mfma<T, D>, 64 * tk.waves, shk));
+    fit_h_per(p, tq, resident_blocks(k_bwd_q_mfma<T, D>, 64 * tq.waves, shq));
+    fit_h_per(p, tk, resident_blocks(k_bwd_kv_mfma<T, D>, 64 * tk.waves, shk));
     NA_LAUNCH("na_bwd_q_mfma", (k_bwd_q_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tq))),
               dim3(64 * tq.waves), shq, s, p, tq, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
               (const T*)o, to_k(lo), (const T*)dout, to_k(ldo), lse, to_k(ll), dlse, to_k(ldl), (T*)dq, to_k(ldq), delta,
