@@ -187,53 +187,6 @@ __device__ __forceinline__ ClassAxis class_axis_of(const Axis& a, int r, const F
     return c;
 }
 
-// Workgroup -> (batch, run of heads, residues, tile origin J, clipped extent
-// E) and the union box [lo, lo+U) of the windows of its queries (key_tile =
-// false) or of the queries attending its keys (key_tile = true).  The
-// geometry is the same for every (batch, head).  Heads vary fastest, then
-// tiles, then batch, so that neighbouring tiles (which share halo rows) run
-// close together in time on the same XCD.  False: empty tile.
-__device__ __forceinline__ bool decode_block(const Prob& p, const TileShape& ts, bool key_tile, Block& k) {
-    int x = xcd_block(blockIdx.x, gridDim.x);
-    int q = fdiv(x, ts.hchunks);
-    k.h0 = (x - q * static_cast<int>(ts.hchunks.d)) * ts.h_per;
-    k.h1 = min(k.h0 + ts.h_per, ts.nheads);
-    x = q;
-    int t[3];
-    for (int a = 2; a >= 0; --a) {
-        q = fdiv(x, ts.tiles[a]);
-        t[a] = x - q * static_cast<int>(ts.tiles[a].d);
-        x = q;
-        q = fdiv(x, ts.dil[a]);
-        k.r[a] = x - q * static_cast<int>(ts.dil[a].d);
-        x = q;
-    }
-    k.b = x;
-    for (int a = 0; a < 3; ++a) {
-        const ClassAxis c = class_axis_of(p.ax[a], k.r[a], ts.dil[a], ts.lenmod[a]);
-        k.c[a] = c;
-        k.J[a] = t[a] * ts.T[a];
-        const int jend = min(k.J[a] + ts.T[a], c.n) - 1;
-        k.E[a] = jend - k.J[a] + 1;
-        if (k.E[a] <= 0) return false;
-        int lo, hi;
-        if (!key_tile) {
-            lo = max(class_ws(c, k.J[a]), 0);
-            hi = min(class_ws(c, jend) + c.K - 1, c.n - 1);
-        } else {
-            // both span ends are non-decreasing in the key; keys attended by
-            // nobody (only past the last window at an even-kernel border) sit
-            // at the end and leave hi unchanged
-            int x2;
-            class_span(c, k.J[a], lo, x2);
-            class_span(c, jend, x2, hi);
-        }
-        k.lo[a] = lo;
-        k.U[a] = hi >= lo ? hi - lo + 1 : 0;
-    }
-    return true;
-}
-
 // Admissible box of a query (its window) or key (its attending queries) in
 // class coordinates.
 __device__ __forceinline__ void item_box(const ClassAxis& c, int j, bool key_side, int& lo, int& hi) {
@@ -255,45 +208,140 @@ struct WaveGeo {
     int c0, c1;
 };
 
-__device__ __forceinline__ WaveGeo wave_geo(const TileShape& ts, const Block& k, int wave, bool key_side) {
-    WaveGeo g;
+// Workgroup -> (batch, run of heads, residues, tile origin J, clipped extent
+// E) and the union box [lo, lo+U) of the windows of its queries (KEY false)
+// or of the queries attending its keys (KEY true), plus the wave's box.  The
+// geometry is the same for every (batch, head).  Heads vary fastest, then
+// tiles, then batch, so that neighbouring tiles (which share halo rows) run
+// close together in time on the same XCD.  The index decode is scalar; the
+// per-axis work runs with one axis per lane (lanes 0, 1, 2) and is read back
+// into scalar registers.  False: empty tile.
+template <bool KEY>
+__device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts, int wave, Block& k, WaveGeo& g) {
+    int x = xcd_block(blockIdx.x, gridDim.x);
+    int q = fdiv(x, ts.hchunks);
+    k.h0 = (x - q * static_cast<int>(ts.hchunks.d)) * ts.h_per;
+    k.h1 = min(k.h0 + ts.h_per, ts.nheads);
+    x = q;
+    int t[3];
+    for (int a = 2; a >= 0; --a) {
+        q = fdiv(x, ts.tiles[a]);
+        t[a] = x - q * static_cast<int>(ts.tiles[a].d);
+        x = q;
+        q = fdiv(x, ts.dil[a]);
+        k.r[a] = x - q * static_cast<int>(ts.dil[a].d);
+        x = q;
+    }
+    k.b = x;
+
+    // the wave's item range per axis (tile coordinates)
     const int f0 = wave * 16, s2 = ts.tshift[2], s1 = ts.tshift[1];
-    int lo[3], hi[3];
+    int il[3], ih[3];
     if (ts.T[2] >= 16) {
-        lo[2] = f0 & (ts.T[2] - 1);
-        hi[2] = lo[2] + 15;
-        lo[1] = hi[1] = (f0 >> s2) & (ts.T[1] - 1);
-        lo[0] = hi[0] = f0 >> (s2 + s1);
+        il[2] = f0 & (ts.T[2] - 1);
+        ih[2] = il[2] + 15;
+        il[1] = ih[1] = (f0 >> s2) & (ts.T[1] - 1);
+        il[0] = ih[0] = f0 >> (s2 + s1);
     } else if (ts.T[2] * ts.T[1] >= 16) {
-        lo[2] = 0;
-        hi[2] = ts.T[2] - 1;
-        lo[1] = (f0 >> s2) & (ts.T[1] - 1);
-        hi[1] = lo[1] + (16 >> s2) - 1;
-        lo[0] = hi[0] = f0 >> (s2 + s1);
+        il[2] = 0;
+        ih[2] = ts.T[2] - 1;
+        il[1] = (f0 >> s2) & (ts.T[1] - 1);
+        ih[1] = il[1] + (16 >> s2) - 1;
+        il[0] = ih[0] = f0 >> (s2 + s1);
     } else {
-        lo[2] = 0;
-        hi[2] = ts.T[2] - 1;
-        lo[1] = 0;
-        hi[1] = ts.T[1] - 1;
-        lo[0] = f0 >> (s2 + s1);
-        hi[0] = lo[0] + (16 >> (s2 + s1)) - 1;
+        il[2] = 0;
+        ih[2] = ts.T[2] - 1;
+        il[1] = 0;
+        ih[1] = ts.T[1] - 1;
+        il[0] = f0 >> (s2 + s1);
+        ih[0] = il[0] + (16 >> (s2 + s1)) - 1;
     }
+
+    // one axis per lane
+    const int lane = threadIdx.x & 63;
+    const bool l0 = lane == 0, l1 = lane == 1;
+#define NA_PICK(field) (l0 ? (field(0)) : l1 ? (field(1)) : (field(2)))
+#define F_LEN(a) p.ax[a].len
+#define F_K(a) p.ax[a].k
+#define F_DIL(a) p.ax[a].dil
+#define F_CAUSAL(a) p.ax[a].causal
+#define F_LENMOD(a) ts.lenmod[a]
+#define F_T(a) ts.T[a]
+#define F_DMUL(a) ts.dil[a].mul
+#define F_DSH(a) ts.dil[a].shift
+#define F_TT(a) t[a]
+#define F_RR(a) k.r[a]
+#define F_IL(a) il[a]
+#define F_IH(a) ih[a]
+    const int len = NA_PICK(F_LEN), K = NA_PICK(F_K), dil = NA_PICK(F_DIL), causal = NA_PICK(F_CAUSAL);
+    const int lenmod = NA_PICK(F_LENMOD), T = NA_PICK(F_T), tt = NA_PICK(F_TT), rr = NA_PICK(F_RR);
+    const int wl = NA_PICK(F_IL), wh = NA_PICK(F_IH);
+    const FastDiv fd{static_cast<uint32_t>(NA_PICK(F_DMUL)), static_cast<uint32_t>(NA_PICK(F_DSH)),
+                     static_cast<uint32_t>(dil)};
+#undef F_LEN
+#undef F_K
+#undef F_DIL
+#undef F_CAUSAL
+#undef F_LENMOD
+#undef F_T
+#undef F_DMUL
+#undef F_DSH
+#undef F_TT
+#undef F_RR
+#undef F_IL
+#undef F_IH
+#undef NA_PICK
+    ClassAxis c;
+    c.n = dil == 1 ? len : fdiv(len - rr + dil - 1, fd);
+    c.K = K;
+    c.h = K >> 1;
+    c.causal = causal;
+    c.B = (dil == 1 || rr < lenmod) ? c.n - 1 - 2 * c.h : c.n - K;
+    const int J = tt * T;
+    const int jend = min(J + T, c.n) - 1;
+    const int E = jend - J + 1;
+    int lo, hi;
+    if (!KEY) {
+        lo = max(class_ws(c, J), 0);
+        hi = min(class_ws(c, jend) + K - 1, c.n - 1);
+    } else {
+        // both span ends are non-decreasing in the key; keys attended by
+        // nobody (only past the last window at an even-kernel border) sit
+        // at the end and leave hi unchanged
+        int x2;
+        class_span(c, J, lo, x2);
+        class_span(c, jend, x2, hi);
+    }
+    const int U = hi >= lo ? hi - lo + 1 : 0;
+    const int whc = min(wh, E - 1);
+    int bl, bh, el, eh;
+    item_box(c, J + wl, KEY, bl, bh);
+    item_box(c, J + max(whc, wl), KEY, el, eh);
+    const int glo = max(bl - lo, 0), ghi = min(eh - lo, U - 1);
+    const int tile_ok = E > 0 ? 1 : 0;
+    const int wave_ok = (wl <= whc && glo <= ghi) ? 1 : 0;
+
+    bool nonempty = true;
     g.any = true;
+#pragma unroll
     for (int a = 0; a < 3; ++a) {
-        hi[a] = min(hi[a], k.E[a] - 1);
-        if (lo[a] > hi[a]) g.any = false;
-    }
-    for (int a = 0; a < 3; ++a) {
-        int l0, h0, l1, h1;
-        item_box(k.c[a], k.J[a] + lo[a], key_side, l0, h0);
-        item_box(k.c[a], k.J[a] + max(hi[a], lo[a]), key_side, l1, h1);
-        g.lo[a] = max(l0 - k.lo[a], 0);
-        g.hi[a] = min(h1 - k.lo[a], k.U[a] - 1);
-        if (g.lo[a] > g.hi[a]) g.any = false;
+        k.J[a] = __builtin_amdgcn_readlane(J, a);
+        k.E[a] = __builtin_amdgcn_readlane(E, a);
+        k.lo[a] = __builtin_amdgcn_readlane(lo, a);
+        k.U[a] = __builtin_amdgcn_readlane(U, a);
+        k.c[a].n = __builtin_amdgcn_readlane(c.n, a);
+        k.c[a].B = __builtin_amdgcn_readlane(c.B, a);
+        k.c[a].K = p.ax[a].k;
+        k.c[a].h = p.ax[a].k >> 1;
+        k.c[a].causal = p.ax[a].causal;
+        g.lo[a] = __builtin_amdgcn_readlane(glo, a);
+        g.hi[a] = __builtin_amdgcn_readlane(ghi, a);
+        nonempty = nonempty && __builtin_amdgcn_readlane(tile_ok, a) != 0;
+        g.any = g.any && __builtin_amdgcn_readlane(wave_ok, a) != 0;
     }
     g.c0 = (g.lo[1] * (1 << ts.rowshift) + g.lo[2]) >> 5;
     g.c1 = (g.hi[1] * (1 << ts.rowshift) + g.hi[2]) >> 5;
-    return g;
+    return nonempty;
 }
 
 // One lane's query (or key): validity, position and admissible box
@@ -525,12 +573,14 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T*
                                                   LayK lv, T* __restrict__ out, LayK lo, float* __restrict__ lse,
                                                   LayK ll) {
     extern __shared__ __align__(16) unsigned char smem[];
-    Block blk;
-    if (!decode_block(p, ts, false, blk)) return;
+    constexpr bool KEY_SIDE = false;
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + ts.slots * D;
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
+    Block blk;
+    WaveGeo wg;
+    if (!tile_geometry<KEY_SIDE>(p, ts, wave, blk, wg)) return;
     const StageMap sm = stage_map<T, D>(p, ts, lk, lv, lane);
     Walk w;
     walk_start(blk, w);
@@ -539,7 +589,6 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T*
         stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0), lv,
                          Vs, wave);
     }
-    const WaveGeo wg = wave_geo(ts, blk, wave, false);
     const Lane ln = lane_item(p, ts, blk, wave, col, false);
     const bool wide = ts.rowshift > 5;  // column pattern changes from chunk to chunk
     f32x4_t cb[2];
@@ -631,12 +680,14 @@ __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const 
                                                     const float* __restrict__ dlse, LayK ldl, T* __restrict__ dq,
                                                     LayK ldq, float* __restrict__ delta, LayK lde) {
     extern __shared__ __align__(16) unsigned char smem[];
-    Block blk;
-    if (!decode_block(p, ts, false, blk)) return;
+    constexpr bool KEY_SIDE = false;
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + ts.slots * D;
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
+    Block blk;
+    WaveGeo wg;
+    if (!tile_geometry<KEY_SIDE>(p, ts, wave, blk, wg)) return;
     const StageMap sm = stage_map<T, D>(p, ts, lk, lv, lane);
     Walk w;
     walk_start(blk, w);
@@ -645,7 +696,6 @@ __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const 
         stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0), lv,
                          Vs, wave);
     }
-    const WaveGeo wg = wave_geo(ts, blk, wave, false);
     const Lane ln = lane_item(p, ts, blk, wave, col, false);
     const float sc2 = p.scale * kLog2e;
     const bool wide = ts.rowshift > 5;
@@ -748,8 +798,7 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
                                                      const float* __restrict__ delta, LayK lde,
                                                      T* __restrict__ dk, LayK ldk, T* __restrict__ dv, LayK ldv) {
     extern __shared__ __align__(16) unsigned char smem[];
-    Block blk;
-    if (!decode_block(p, ts, true, blk)) return;
+    constexpr bool KEY_SIDE = true;
     const int slots = ts.slots;
     T* Qs = reinterpret_cast<T*>(smem);
     T* Gs = Qs + slots * D;
@@ -757,6 +806,9 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
     float* ND = NL + slots + 8;                            // slots
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
+    Block blk;
+    WaveGeo wg;
+    if (!tile_geometry<KEY_SIDE>(p, ts, wave, blk, wg)) return;
     const int rep = static_cast<int>(ts.rep.d);
     const StageMap sm = stage_map<T, D>(p, ts, lq, ldo, lane);
     // the walk runs over (batch, kv head, q head of the group, slice): its
@@ -767,7 +819,6 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
     stage_pair<T, D>(p, blk, ts, sm, plane_of(q, lq, w.b, w.h * rep, slice_pos(p, blk, 0)), lq, Qs,
                      plane_of(dout, ldo, w.b, w.h * rep, slice_pos(p, blk, 0)), ldo, Gs, wave);
     if (threadIdx.x < 8) NL[slots + threadIdx.x] = -INFINITY;
-    const WaveGeo wg = wave_geo(ts, blk, wave, true);
     const Lane ln = lane_item(p, ts, blk, wave, col, true);
     const float sc2 = p.scale * kLog2e;
     const bool wide = ts.rowshift > 5;
