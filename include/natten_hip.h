@@ -3,8 +3,12 @@
  * (libnatten_hip.so).
  *
  * Plain pointers, sizes and element strides; no torch types.  The caller owns
- * every buffer (inputs, outputs, workspaces) and the stream; no entry point
- * allocates device memory.  Every entry point returns 0 on success and a
+ * every buffer (inputs, outputs, workspaces) and the stream.  The only device
+ * memory the library allocates itself is a small table of tile geometry per
+ * problem shape (a few hundred bytes per tile), built on the first call with
+ * that shape outside stream capture and kept until the process ends; during
+ * capture, or when the tables would pass 64 MiB, the kernels compute the same
+ * geometry themselves.  Every entry point returns 0 on success and a
  * non-zero natten_status_t otherwise, with a message available from
  * natten_hip_last_error().  Launches are asynchronous on `stream` (a
  * hipStream_t; NULL = the default stream).

@@ -171,6 +171,68 @@ __host__ __device__ inline void class_span(const ClassAxis& c, int u, int& jlo, 
         jlo = c.B >= v ? c.n - c.h : c.n;
 }
 
+// Admissible box of a query (its window) or key (its attending queries) in
+// class coordinates.
+__host__ __device__ inline void item_box(const ClassAxis& c, int j, bool key_side, int& lo, int& hi) {
+    if (!key_side) {
+        lo = class_ws(c, j);
+        hi = lo + c.K - 1;
+    } else {
+        class_span(c, j, lo, hi);
+    }
+}
+
+__host__ __device__ inline int imin(int a, int b) { return a < b ? a : b; }
+__host__ __device__ inline int imax(int a, int b) { return a > b ? a : b; }
+
+// One axis of a tile: class (n, B) of residue r, tile origin J = tT, clipped
+// extent E, the union [lo, lo+U) of its queries' windows (key: of the
+// queries attending its keys), and the admissible box [glo, ghi] of the
+// wave's items [wl, wh] (union-relative, clipped to the union).  Window ends
+// are non-decreasing along the axis, so the box follows from its corners.
+struct AxisGeo {
+    int J, E, lo, U, n, B, glo, ghi, tile_ok, wave_ok;
+};
+
+__host__ __device__ inline AxisGeo axis_geometry(int len, int K, int dil, int causal, int lenmod, int T, int t,
+                                                 int r, int wl, int wh, bool key, const FastDiv& fd) {
+    AxisGeo o;
+    ClassAxis c;
+    c.n = dil == 1 ? len : fdiv(len - r + dil - 1, fd);
+    c.K = K;
+    c.h = K >> 1;
+    c.causal = causal;
+    c.B = (dil == 1 || r < lenmod) ? c.n - 1 - 2 * c.h : c.n - K;
+    o.n = c.n;
+    o.B = c.B;
+    o.J = t * T;
+    const int jend = imin(o.J + T, c.n) - 1;
+    o.E = jend - o.J + 1;
+    int lo, hi;
+    if (!key) {
+        lo = imax(class_ws(c, o.J), 0);
+        hi = imin(class_ws(c, jend) + K - 1, c.n - 1);
+    } else {
+        // both span ends are non-decreasing in the key; keys attended by
+        // nobody (only past the last window at an even-kernel border) sit
+        // at the end and leave hi unchanged
+        int x2;
+        class_span(c, o.J, lo, x2);
+        class_span(c, jend, x2, hi);
+    }
+    o.lo = lo;
+    o.U = hi >= lo ? hi - lo + 1 : 0;
+    const int whc = imin(wh, o.E - 1);
+    int bl, bh, el, eh;
+    item_box(c, o.J + wl, key, bl, bh);
+    item_box(c, o.J + imax(whc, wl), key, el, eh);
+    o.glo = imax(bl - lo, 0);
+    o.ghi = imin(eh - lo, o.U - 1);
+    o.tile_ok = o.E > 0 ? 1 : 0;
+    o.wave_ok = (wl <= whc && o.glo <= o.ghi) ? 1 : 0;
+    return o;
+}
+
 // f(j0, j1, j2, e, valid) for each neighbour e (row-major over the kernel) of
 // the query at (i0, i1, i2).  Invalid (causal) neighbours have j < 0 on some
 // axis and must not be dereferenced.

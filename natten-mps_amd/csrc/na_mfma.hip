@@ -39,6 +39,7 @@
 // MFMA lane layout (16x16x32): A row = lane%16, B column = lane%16, both with
 // k = 8*(lane/16) .. +7; C column = lane%16, rows 4*(lane/16) .. +3.
 #include <algorithm>
+#include <cstddef>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -159,7 +160,7 @@ struct TileShape {
     int waves, slots, rowshift;
     int lenmod[3];
     int nheads, h_per;  // heads, and how many of them one workgroup runs
-    FastDiv rep, hchunks, tiles[3], dil[3];
+    FastDiv rep, hchunks, spatial, tiles[3], dil[3];
 };
 
 // Operand layout as the kernels take it: 64-bit batch and head strides, and
@@ -187,56 +188,11 @@ __device__ __forceinline__ ClassAxis class_axis_of(const Axis& a, int r, const F
     return c;
 }
 
-// Admissible box of a query (its window) or key (its attending queries) in
-// class coordinates.
-__device__ __forceinline__ void item_box(const ClassAxis& c, int j, bool key_side, int& lo, int& hi) {
-    if (!key_side) {
-        lo = class_ws(c, j);
-        hi = lo + c.K - 1;
-    } else {
-        class_span(c, j, lo, hi);
-    }
-}
-
 // The wave's part of the tile: items f = 16w .. 16w+15 in row-major tile
-// order; with power-of-two extents they cover a box.  Its admissible box
-// (union-relative, clipped to the union) follows from the box corners since
-// window ends are non-decreasing per axis.  Chunks c0..c1 cover it.
-struct WaveGeo {
-    bool any;
-    int lo[3], hi[3];
-    int c0, c1;
-};
-
-// Workgroup -> (batch, run of heads, residues, tile origin J, clipped extent
-// E) and the union box [lo, lo+U) of the windows of its queries (KEY false)
-// or of the queries attending its keys (KEY true), plus the wave's box.  The
-// geometry is the same for every (batch, head).  Heads vary fastest, then
-// tiles, then batch, so that neighbouring tiles (which share halo rows) run
-// close together in time on the same XCD.  The index decode is scalar; the
-// per-axis work runs with one axis per lane (lanes 0, 1, 2) and is read back
-// into scalar registers.  False: empty tile.
-template <bool KEY>
-__device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts, int wave, Block& k, WaveGeo& g) {
-    int x = xcd_block(blockIdx.x, gridDim.x);
-    int q = fdiv(x, ts.hchunks);
-    k.h0 = (x - q * static_cast<int>(ts.hchunks.d)) * ts.h_per;
-    k.h1 = min(k.h0 + ts.h_per, ts.nheads);
-    x = q;
-    int t[3];
-    for (int a = 2; a >= 0; --a) {
-        q = fdiv(x, ts.tiles[a]);
-        t[a] = x - q * static_cast<int>(ts.tiles[a].d);
-        x = q;
-        q = fdiv(x, ts.dil[a]);
-        k.r[a] = x - q * static_cast<int>(ts.dil[a].d);
-        x = q;
-    }
-    k.b = x;
-
-    // the wave's item range per axis (tile coordinates)
+// order; with power-of-two extents they cover a box, items [il, ih] per axis
+// (before clipping to the tile's extent).
+__host__ __device__ inline void wave_items(const TileShape& ts, int wave, int (&il)[3], int (&ih)[3]) {
     const int f0 = wave * 16, s2 = ts.tshift[2], s1 = ts.tshift[1];
-    int il[3], ih[3];
     if (ts.T[2] >= 16) {
         il[2] = f0 & (ts.T[2] - 1);
         ih[2] = il[2] + 15;
@@ -256,6 +212,84 @@ __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts
         il[0] = f0 >> (s2 + s1);
         ih[0] = il[0] + (16 >> (s2 + s1)) - 1;
     }
+}
+
+// The wave's admissible box (union-relative) and the chunks c0..c1 covering it.
+struct WaveGeo {
+    bool any;
+    int lo[3], hi[3];
+    int c0, c1;
+};
+
+// Host-built per-tile geometry records (kRecDwords ints per spatial tile):
+//   [0..2] r   [3..5] J   [6..8] E   [9..11] lo   [12..14] U   [15..17] n
+//   [18..20] B   [21] nonempty   then per wave w < 4 at 24 + 8w:
+//   any, lo0, hi0, lo1, hi1, lo2, hi2, c0 | c1 << 16
+constexpr int kRecDwords = 64;
+
+__host__ __device__ inline void spatial_coords(const TileShape& ts, int s, int (&t)[3], int (&r)[3]) {
+    for (int a = 2; a >= 0; --a) {
+        int q = fdiv(s, ts.tiles[a]);
+        t[a] = s - q * static_cast<int>(ts.tiles[a].d);
+        s = q;
+        q = fdiv(s, ts.dil[a]);
+        r[a] = s - q * static_cast<int>(ts.dil[a].d);
+        s = q;
+    }
+}
+
+// Workgroup -> (batch, run of heads, residues, tile origin J, clipped extent
+// E) and the union box [lo, lo+U) of the windows of its queries (KEY false)
+// or of the queries attending its keys (KEY true), plus the wave's box.  The
+// geometry is the same for every (batch, head).  Heads vary fastest, then
+// tiles, then batch, so that neighbouring tiles (which share halo rows) run
+// close together in time on the same XCD.  With a host-built table (geo) the
+// tile's record is read with scalar loads; without one the per-axis work
+// runs with one axis per lane (lanes 0, 1, 2) and is read back into scalar
+// registers.  False: empty tile.
+template <bool KEY>
+__device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts, const int* __restrict__ geo,
+                                              int wave, Block& k, WaveGeo& g) {
+    int x = xcd_block(blockIdx.x, gridDim.x);
+    int q = fdiv(x, ts.hchunks);
+    k.h0 = (x - q * static_cast<int>(ts.hchunks.d)) * ts.h_per;
+    k.h1 = min(k.h0 + ts.h_per, ts.nheads);
+    x = q;
+    q = fdiv(x, ts.spatial);
+    const int s = x - q * static_cast<int>(ts.spatial.d);
+    k.b = q;
+
+    if (geo) {
+        const int* rec = geo + s * kRecDwords;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            k.r[a] = rec[a];
+            k.J[a] = rec[3 + a];
+            k.E[a] = rec[6 + a];
+            k.lo[a] = rec[9 + a];
+            k.U[a] = rec[12 + a];
+            k.c[a].n = rec[15 + a];
+            k.c[a].B = rec[18 + a];
+            k.c[a].K = p.ax[a].k;
+            k.c[a].h = p.ax[a].k >> 1;
+            k.c[a].causal = p.ax[a].causal;
+        }
+        const int* wr = rec + 24 + 8 * wave;
+        g.any = wr[0] != 0;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            g.lo[a] = wr[1 + 2 * a];
+            g.hi[a] = wr[2 + 2 * a];
+        }
+        g.c0 = wr[7] & 0xFFFF;
+        g.c1 = wr[7] >> 16;
+        return rec[21] != 0;
+    }
+
+    int t[3];
+    spatial_coords(ts, s, t, k.r);
+    int il[3], ih[3];
+    wave_items(ts, wave, il, ih);
 
     // one axis per lane
     const int lane = threadIdx.x & 63;
@@ -273,11 +307,12 @@ __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts
 #define F_RR(a) k.r[a]
 #define F_IL(a) il[a]
 #define F_IH(a) ih[a]
-    const int len = NA_PICK(F_LEN), K = NA_PICK(F_K), dil = NA_PICK(F_DIL), causal = NA_PICK(F_CAUSAL);
-    const int lenmod = NA_PICK(F_LENMOD), T = NA_PICK(F_T), tt = NA_PICK(F_TT), rr = NA_PICK(F_RR);
-    const int wl = NA_PICK(F_IL), wh = NA_PICK(F_IH);
+    const int dil = NA_PICK(F_DIL);
     const FastDiv fd{static_cast<uint32_t>(NA_PICK(F_DMUL)), static_cast<uint32_t>(NA_PICK(F_DSH)),
                      static_cast<uint32_t>(dil)};
+    const AxisGeo ag = axis_geometry(NA_PICK(F_LEN), NA_PICK(F_K), dil, NA_PICK(F_CAUSAL), NA_PICK(F_LENMOD),
+                                     NA_PICK(F_T), NA_PICK(F_TT), NA_PICK(F_RR), NA_PICK(F_IL), NA_PICK(F_IH), KEY,
+                                     fd);
 #undef F_LEN
 #undef F_K
 #undef F_DIL
@@ -291,53 +326,24 @@ __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts
 #undef F_IL
 #undef F_IH
 #undef NA_PICK
-    ClassAxis c;
-    c.n = dil == 1 ? len : fdiv(len - rr + dil - 1, fd);
-    c.K = K;
-    c.h = K >> 1;
-    c.causal = causal;
-    c.B = (dil == 1 || rr < lenmod) ? c.n - 1 - 2 * c.h : c.n - K;
-    const int J = tt * T;
-    const int jend = min(J + T, c.n) - 1;
-    const int E = jend - J + 1;
-    int lo, hi;
-    if (!KEY) {
-        lo = max(class_ws(c, J), 0);
-        hi = min(class_ws(c, jend) + K - 1, c.n - 1);
-    } else {
-        // both span ends are non-decreasing in the key; keys attended by
-        // nobody (only past the last window at an even-kernel border) sit
-        // at the end and leave hi unchanged
-        int x2;
-        class_span(c, J, lo, x2);
-        class_span(c, jend, x2, hi);
-    }
-    const int U = hi >= lo ? hi - lo + 1 : 0;
-    const int whc = min(wh, E - 1);
-    int bl, bh, el, eh;
-    item_box(c, J + wl, KEY, bl, bh);
-    item_box(c, J + max(whc, wl), KEY, el, eh);
-    const int glo = max(bl - lo, 0), ghi = min(eh - lo, U - 1);
-    const int tile_ok = E > 0 ? 1 : 0;
-    const int wave_ok = (wl <= whc && glo <= ghi) ? 1 : 0;
 
     bool nonempty = true;
     g.any = true;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
-        k.J[a] = __builtin_amdgcn_readlane(J, a);
-        k.E[a] = __builtin_amdgcn_readlane(E, a);
-        k.lo[a] = __builtin_amdgcn_readlane(lo, a);
-        k.U[a] = __builtin_amdgcn_readlane(U, a);
-        k.c[a].n = __builtin_amdgcn_readlane(c.n, a);
-        k.c[a].B = __builtin_amdgcn_readlane(c.B, a);
+        k.J[a] = __builtin_amdgcn_readlane(ag.J, a);
+        k.E[a] = __builtin_amdgcn_readlane(ag.E, a);
+        k.lo[a] = __builtin_amdgcn_readlane(ag.lo, a);
+        k.U[a] = __builtin_amdgcn_readlane(ag.U, a);
+        k.c[a].n = __builtin_amdgcn_readlane(ag.n, a);
+        k.c[a].B = __builtin_amdgcn_readlane(ag.B, a);
         k.c[a].K = p.ax[a].k;
         k.c[a].h = p.ax[a].k >> 1;
         k.c[a].causal = p.ax[a].causal;
-        g.lo[a] = __builtin_amdgcn_readlane(glo, a);
-        g.hi[a] = __builtin_amdgcn_readlane(ghi, a);
-        nonempty = nonempty && __builtin_amdgcn_readlane(tile_ok, a) != 0;
-        g.any = g.any && __builtin_amdgcn_readlane(wave_ok, a) != 0;
+        g.lo[a] = __builtin_amdgcn_readlane(ag.glo, a);
+        g.hi[a] = __builtin_amdgcn_readlane(ag.ghi, a);
+        nonempty = nonempty && __builtin_amdgcn_readlane(ag.tile_ok, a) != 0;
+        g.any = g.any && __builtin_amdgcn_readlane(ag.wave_ok, a) != 0;
     }
     g.c0 = (g.lo[1] * (1 << ts.rowshift) + g.lo[2]) >> 5;
     g.c1 = (g.hi[1] * (1 << ts.rowshift) + g.hi[2]) >> 5;
@@ -568,7 +574,7 @@ __device__ __forceinline__ int slice_pos(const Prob& p, const Block& k, int u0) 
 // rescale per group).
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T* __restrict__ q, LayK lq,
+__global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq,
                                                   const T* __restrict__ kg, LayK lk, const T* __restrict__ vg,
                                                   LayK lv, T* __restrict__ out, LayK lo, float* __restrict__ lse,
                                                   LayK ll) {
@@ -580,7 +586,7 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T*
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
     Block blk;
     WaveGeo wg;
-    if (!tile_geometry<KEY_SIDE>(p, ts, wave, blk, wg)) return;
+    if (!tile_geometry<KEY_SIDE>(p, ts, geo, wave, blk, wg)) return;
     const StageMap sm = stage_map<T, D>(p, ts, lk, lv, lane);
     Walk w;
     walk_start(blk, w);
@@ -672,7 +678,7 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const T*
 // dP = dO . v.  The dP product starts from -delta.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const T* __restrict__ q, LayK lq,
+__global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq,
                                                     const T* __restrict__ kg, LayK lk, const T* __restrict__ vg,
                                                     LayK lv, const T* __restrict__ o, LayK lo,
                                                     const T* __restrict__ dout, LayK ldo,
@@ -687,7 +693,7 @@ __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
     Block blk;
     WaveGeo wg;
-    if (!tile_geometry<KEY_SIDE>(p, ts, wave, blk, wg)) return;
+    if (!tile_geometry<KEY_SIDE>(p, ts, geo, wave, blk, wg)) return;
     const StageMap sm = stage_map<T, D>(p, ts, lk, lv, lane);
     Walk w;
     walk_start(blk, w);
@@ -791,7 +797,7 @@ __device__ __forceinline__ void stage_scalars(const Prob& p, const Block& k, con
 }
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const T* __restrict__ q, LayK lq,
+__global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq,
                                                      const T* __restrict__ kg, LayK lk, const T* __restrict__ vg,
                                                      LayK lv, const T* __restrict__ dout, LayK ldo,
                                                      const float* __restrict__ lse, LayK ll,
@@ -808,7 +814,7 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
     Block blk;
     WaveGeo wg;
-    if (!tile_geometry<KEY_SIDE>(p, ts, wave, blk, wg)) return;
+    if (!tile_geometry<KEY_SIDE>(p, ts, geo, wave, blk, wg)) return;
     const int rep = static_cast<int>(ts.rep.d);
     const StageMap sm = stage_map<T, D>(p, ts, lq, ldo, lane);
     // the walk runs over (batch, kv head, q head of the group, slice): its
@@ -979,11 +985,15 @@ bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts) {
             ts.nheads = heads;
             set_h_per(ts, 1);
             ts.rep = make_fastdiv(static_cast<uint32_t>(p.rep));
+            long long spatial = 1;
             for (int a = 0; a < 3; ++a) {
                 ts.tiles[a] = make_fastdiv(static_cast<uint32_t>(ts.ntile[a]));
                 ts.dil[a] = make_fastdiv(static_cast<uint32_t>(p.ax[a].dil));
                 ts.lenmod[a] = p.ax[a].len % p.ax[a].dil;
+                spatial *= static_cast<long long>(ts.ntile[a]) * p.ax[a].dil;
             }
+            if (spatial >= (1LL << 31)) return false;
+            ts.spatial = make_fastdiv(static_cast<uint32_t>(spatial));
             return true;
         }
     }
@@ -1054,6 +1064,103 @@ bool offsets_fit(const Prob& p, std::initializer_list<Lay> lays) {
     return true;
 }
 
+// Per-tile geometry records, built on the host once per (device, tile kind,
+// problem geometry) and kept for the life of the process; launches read
+// their tile's record instead of recomputing it.  Not built while the stream
+// is being captured (the kernels then compute the geometry themselves), nor
+// past kGeoMaxBytes in total.  NATTEN_HIP_GEOMETRY=device disables the
+// tables (A/B and tests).
+constexpr size_t kGeoMaxBytes = size_t(64) << 20;
+
+struct GeoEntry {
+    int dev, key;
+    int len[3], k[3], dil[3], causal[3], T[3], waves, rowshift;
+    int* ptr;
+};
+
+const int* geometry_table(const Prob& p, const TileShape& ts, bool key_tile, hipStream_t stream) {
+    const char* env = std::getenv("NATTEN_HIP_GEOMETRY");
+    if (env && std::strcmp(env, "device") == 0) return nullptr;
+    static std::mutex mu;
+    static std::vector<GeoEntry> cache;
+    static size_t total = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    GeoEntry key{};
+    key.dev = dev;
+    key.key = key_tile ? 1 : 0;
+    for (int a = 0; a < 3; ++a) {
+        key.len[a] = p.ax[a].len;
+        key.k[a] = p.ax[a].k;
+        key.dil[a] = p.ax[a].dil;
+        key.causal[a] = p.ax[a].causal;
+        key.T[a] = ts.T[a];
+    }
+    key.waves = ts.waves;
+    key.rowshift = ts.rowshift;
+    std::lock_guard<std::mutex> g(mu);
+    for (const GeoEntry& e : cache)
+        if (std::memcmp(&e, &key, offsetof(GeoEntry, ptr)) == 0) return e.ptr;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
+    const long long S = ts.spatial.d;
+    const size_t bytes = static_cast<size_t>(S) * kRecDwords * sizeof(int);
+    if (total + bytes > kGeoMaxBytes) return nullptr;
+    std::vector<int> h(static_cast<size_t>(S) * kRecDwords, 0);
+    for (int s = 0; s < S; ++s) {
+        int* rec = h.data() + static_cast<size_t>(s) * kRecDwords;
+        int t[3], r[3];
+        spatial_coords(ts, s, t, r);
+        int nonempty = 1;
+        for (int w = 0; w < 4; ++w) {
+            int il[3], ih[3];
+            wave_items(ts, w, il, ih);
+            int* wr = rec + 24 + 8 * w;
+            int any = w < ts.waves ? 1 : 0, glo[3], ghi[3];
+            for (int a = 0; a < 3; ++a) {
+                const AxisGeo ag = axis_geometry(p.ax[a].len, p.ax[a].k, p.ax[a].dil, p.ax[a].causal, ts.lenmod[a],
+                                                 ts.T[a], t[a], r[a], il[a], ih[a], key_tile, ts.dil[a]);
+                if (w == 0) {
+                    rec[a] = r[a];
+                    rec[3 + a] = ag.J;
+                    rec[6 + a] = ag.E;
+                    rec[9 + a] = ag.lo;
+                    rec[12 + a] = ag.U;
+                    rec[15 + a] = ag.n;
+                    rec[18 + a] = ag.B;
+                    nonempty &= ag.tile_ok;
+                }
+                any &= ag.wave_ok;
+                glo[a] = ag.glo;
+                ghi[a] = ag.ghi;
+            }
+            wr[0] = any;
+            for (int a = 0; a < 3; ++a) {
+                wr[1 + 2 * a] = glo[a];
+                wr[2 + 2 * a] = ghi[a];
+            }
+            const int c0 = (glo[1] * (1 << ts.rowshift) + glo[2]) >> 5;
+            const int c1 = (ghi[1] * (1 << ts.rowshift) + ghi[2]) >> 5;
+            wr[7] = (c0 & 0xFFFF) | (c1 << 16);
+        }
+        rec[21] = nonempty;
+    }
+    int* d = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&d), bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (hipMemcpy(d, h.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(d);
+        return nullptr;
+    }
+    key.ptr = d;
+    cache.push_back(key);
+    total += bytes;
+    return d;
+}
+
 LayK to_k(const Lay& l) { return LayK{l.b, l.h, static_cast<int>(l.s0), static_cast<int>(l.s1), static_cast<int>(l.s2), 0}; }
 
 template <typename K>
@@ -1072,8 +1179,9 @@ hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
     hipError_t e = allow_lds(k_fwd_mfma<T, D>, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(k_fwd_mfma<T, D>, 64 * ts.waves, shm));
+    const int* geo = geometry_table(p, ts, false, s);
     NA_LAUNCH("na_fwd_mfma", (k_fwd_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, ts))),
-              dim3(64 * ts.waves), shm, s, p, ts, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
+              dim3(64 * ts.waves), shm, s, p, ts, geo, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
               (T*)o, to_k(lo), lse, to_k(ll));
     return hipGetLastError();
 }
@@ -1091,14 +1199,16 @@ hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
     if (e != hipSuccess) return e;
     fit_h_per(p, tq, resident_blocks(k_bwd_q_mfma<T, D>, 64 * tq.waves, shq));
     fit_h_per(p, tk, resident_blocks(k_bwd_kv_mfma<T, D>, 64 * tk.waves, shk));
+    const int* gq = geometry_table(p, tq, false, s);
+    const int* gk = geometry_table(p, tk, true, s);
     NA_LAUNCH("na_bwd_q_mfma", (k_bwd_q_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tq))),
-              dim3(64 * tq.waves), shq, s, p, tq, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
+              dim3(64 * tq.waves), shq, s, p, tq, gq, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
               (const T*)o, to_k(lo), (const T*)dout, to_k(ldo), lse, to_k(ll), dlse, to_k(ldl), (T*)dq, to_k(ldq), delta,
               to_k(lde));
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     NA_LAUNCH("na_bwd_kv_mfma", (k_bwd_kv_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tk))),
-              dim3(64 * tk.waves), shk, s, p, tk, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
+              dim3(64 * tk.waves), shk, s, p, tk, gk, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
               (const T*)dout, to_k(ldo), lse, to_k(ll), (const float*)delta, to_k(lde), (T*)dk, to_k(ldk), (T*)dv,
               to_k(ldv));
     return hipGetLastError();

@@ -1,9 +1,11 @@
 // Host build of the device index code (na_common.h): the same window rule,
 // neighbour enumeration and inverse (key -> queries) enumeration the kernels
 // run, exported for the CPU tests through ctypes.
+#include <algorithm>
 #include <cstdint>
 #include <set>
 #include <tuple>
+#include <vector>
 
 #include "na_common.h"
 
@@ -114,6 +116,68 @@ long long host_fastdiv_errors(uint32_t d, int n_max, int step) {
         if (na::fdiv(static_cast<int>(n), f) != static_cast<int>(n / d)) ++bad;
     for (long long n = n_max > 4096 ? n_max - 4096 : 0; n < n_max; ++n)
         if (na::fdiv(static_cast<int>(n), f) != static_cast<int>(n / d)) ++bad;
+    return bad;
+}
+
+}  // extern "C"
+
+extern "C" {
+
+// Tile geometry (axis_geometry, shared by the host-built tables and the
+// kernels) against brute force on one axis: for every residue class, tile
+// of T items and wave item range [wl, wh], the union box must equal the
+// min/max of the class coordinates the tile's items need (their window
+// members, or the queries attending a key) and the wave box must contain
+// what the wave's items need, equal to it when every key is attended.
+// Returns the number of mismatches.
+long long host_tile_geometry_mismatch(int L, int K, int d, int causal, int T, int key) {
+    na::Axis A{L, L, K, d, 1, causal};
+    long long bad = 0;
+    const na::FastDiv fd = na::make_fastdiv(static_cast<uint32_t>(d));
+    for (int r = 0; r < d && r < L; ++r) {
+        const int n = (L - r + d - 1) / d;
+        // class coordinates needed by class item j: [need_lo[j], need_hi[j]]
+        std::vector<int> need_lo(n, 1 << 30), need_hi(n, -(1 << 30));
+        for (int qj = 0; qj < n; ++qj) {
+            const int i = r + qj * d;
+            const int f = na::axis_first(A, i);
+            for (int x = 0; x < K; ++x) {
+                const int m = f + x * d;
+                if (m < 0 || m >= L) continue;
+                const int mj = (m - r) / d;
+                const int item = key ? mj : qj, other = key ? qj : mj;
+                need_lo[item] = std::min(need_lo[item], other);
+                need_hi[item] = std::max(need_hi[item], other);
+            }
+        }
+        bool all_attended = true;
+        for (int j = 0; j < n; ++j) all_attended = all_attended && need_lo[j] <= need_hi[j];
+        for (int t = 0; t * T < n; ++t) {
+            for (int wl = 0; wl < T; ++wl)
+                for (int wh = wl; wh < T; ++wh) {
+                    const na::AxisGeo g = na::axis_geometry(L, K, d, causal, L % d, T, t, r, wl, wh, key != 0, fd);
+                    const int J = t * T, E = std::min(T, n - J);
+                    if (g.J != J || g.E != E || g.n != n || !g.tile_ok) { ++bad; continue; }
+                    int ulo = 1 << 30, uhi = -(1 << 30);
+                    for (int j = J; j < J + E; ++j) {
+                        ulo = std::min(ulo, need_lo[j]);
+                        uhi = std::max(uhi, need_hi[j]);
+                    }
+                    if (ulo <= uhi && (g.lo != ulo || g.U != uhi - ulo + 1)) { ++bad; continue; }
+                    const int whc = std::min(wh, E - 1);
+                    int blo = 1 << 30, bhi = -(1 << 30);
+                    for (int j = J + wl; j <= J + whc; ++j) {
+                        blo = std::min(blo, need_lo[j]);
+                        bhi = std::max(bhi, need_hi[j]);
+                    }
+                    const bool has = blo <= bhi;
+                    if (!has) continue;
+                    const int rlo = blo - g.lo, rhi = bhi - g.lo;
+                    if (!g.wave_ok || g.glo > rlo || g.ghi < rhi) { ++bad; continue; }
+                    if (all_attended && (g.glo != rlo || g.ghi != rhi)) ++bad;
+                }
+        }
+    }
     return bad;
 }
 

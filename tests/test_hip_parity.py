@@ -381,3 +381,30 @@ def test_head_dim_128_tile_path(dtype):
     _close(out, ref, dtype, "out")
     for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
         _close(a, b, dtype, n)
+
+
+@pytest.mark.parametrize("rank, spatial, ks, dil, causal, heads", [
+    (2, (56, 56), (7, 7), (1, 1), (False, False), (4, 4)),
+    (2, (56, 56), (7, 7), (8, 8), (False, False), (4, 4)),
+    (1, (300,), (33,), (4,), (True,), (4, 2)),
+    (3, (6, 10, 12), (3, 5, 5), (1, 2, 2), (False, False, False), (2, 2)),
+    (2, (13, 17), (4, 6), (2, 1), (True, False), (2, 1)),
+])
+def test_geometry_tables_match_in_kernel_geometry(monkeypatch, rank, spatial, ks, dil, causal, heads):
+    """The tile kernels read host-built per-tile geometry records, or compute
+    the same geometry in the kernel (NATTEN_HIP_GEOMETRY=device, and during
+    graph capture): both must give identical bits."""
+    from natten_mps_amd import functional as F
+
+    fn = {1: F.na1d, 2: F.na2d, 3: F.na3d}[rank]
+    hq, hkv = heads
+    q, k, v, do = _inputs(97, [(2, *spatial, hq, 32), (2, *spatial, hkv, 32), (2, *spatial, hkv, 32),
+                               (2, *spatial, hq, 32)], torch.bfloat16)
+    kw = dict(kernel_size=ks, dilation=dil, is_causal=causal)
+    monkeypatch.delenv("NATTEN_HIP_GEOMETRY", raising=False)
+    out_t, grads_t = _hip_fwd_bwd(fn, (q, k, v), do, **kw)
+    monkeypatch.setenv("NATTEN_HIP_GEOMETRY", "device")
+    out_d, grads_d = _hip_fwd_bwd(fn, (q, k, v), do, **kw)
+    assert torch.equal(out_t, out_d)
+    for a, b in zip(grads_t, grads_d):
+        assert torch.equal(a, b)

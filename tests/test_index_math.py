@@ -36,7 +36,32 @@ def host_idx():
     lib.host_class_mismatch.restype = ctypes.c_longlong
     lib.host_fastdiv_errors.argtypes = [ctypes.c_uint32, ctypes.c_int, ctypes.c_int]
     lib.host_fastdiv_errors.restype = ctypes.c_longlong
+    lib.host_tile_geometry_mismatch.argtypes = [ctypes.c_int] * 6
+    lib.host_tile_geometry_mismatch.restype = ctypes.c_longlong
     return lib
+
+
+def test_tile_geometry_against_brute_force(host_idx):
+    """axis_geometry -- the per-axis tile geometry the tile kernels read from
+    host-built tables or compute in-kernel -- against brute-force window
+    enumeration: union boxes exact, wave boxes containing (and, with every
+    key attended, equal to) what their items need; all residues, tiles and
+    wave item ranges, query and key tiles, causal and not."""
+    n = 0
+    for L in (1, 2, 3, 5, 8, 13, 24):
+        for K in range(1, min(L, 9) + 1):
+            for d in range(1, 5):
+                if K * d > L and not (d == 1):
+                    continue
+                for causal in (0, 1):
+                    if not causal and d == 1 and K % 2 == 0 and K == L:
+                        continue
+                    for T in (1, 2, 4, 8, 16):
+                        for key in (0, 1):
+                            assert host_idx.host_tile_geometry_mismatch(L, K, d, causal, T, key) == 0, \
+                                (L, K, d, causal, T, key)
+                            n += 1
+    assert n > 1000
 
 
 def test_fastdiv_matches_integer_division(host_idx):
