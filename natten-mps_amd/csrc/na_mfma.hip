@@ -43,6 +43,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "na_launch.h"
@@ -104,11 +105,14 @@ __device__ __forceinline__ uint4 pack8(const f32x4_t (&v)[2]) {
 // Reductions over the four 16-lane rows of the wave (lanes i, i+16, i+32,
 // i+48): v_permlane16_swap / v_permlane32_swap exchange rows between two
 // registers, here both the same value.
+// NaN-propagating maximum (v_maximum3_f32 on gfx950, no operand quieting).
+__device__ __forceinline__ float fmaxp(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 __device__ __forceinline__ float max_rows(float v) {
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    v = fmaxp(__uint_as_float(a[0]), __uint_as_float(a[1]));
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    return fmaxp(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ float sum_rows(float v) {
@@ -119,8 +123,10 @@ __device__ __forceinline__ float sum_rows(float v) {
 }
 
 __device__ __forceinline__ float max8(const f32x4_t (&s)[2]) {
-    return fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                 fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    const float a = fmaxp(fmaxp(s[0][0], s[0][1]), s[0][2]);
+    const float b = fmaxp(fmaxp(s[0][3], s[1][0]), s[1][1]);
+    const float c = fmaxp(fmaxp(s[1][2], s[1][3]), a);
+    return fmaxp(b, c);
 }
 
 // XOR swizzle of the 16-byte pieces of LDS row `row` (D / 8 pieces per row):
@@ -619,43 +625,54 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const in
         __syncthreads();
         if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
-            for (int c = wg.c0; c <= wg.c1; c += 4) {
-                const int n = min(4, wg.c1 - c + 1);
-                f32x4_t s[4][2];
-                bool rv[4];
-                float cm = -INFINITY;
+            const auto chunks = [&](auto wide_tag) {
+                constexpr bool WIDE = decltype(wide_tag)::value;
+                for (int c = wg.c0; c <= wg.c1; c += 4) {
+                    const int n = min(4, wg.c1 - c + 1);
+                    f32x4_t s[4][2];
+                    bool rv[4];
+                    float cm = -INFINITY;
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    if (g < n) {
-                        f32x4_t bias[2] = {cb[0], cb[1]};
-                        if (wide) column_bias(ln, ts.rowshift, c + g, grp, bias);
-                        score_chunk<T, D>(Ks, c + g, col, grp, qf, bias, s[g]);
-                        rv[g] = row_ok(ln, ts.rowshift, in0, c + g, grp);
-                        cm = fmaxf(cm, rv[g] ? max8(s[g]) : -INFINITY);
+                    for (int g = 0; g < 4; ++g) {
+                        if (g < n) {
+                            if constexpr (!WIDE) {
+                                score_chunk<T, D>(Ks, c + g, col, grp, qf, cb, s[g]);
+                            } else {
+                                f32x4_t bias[2];
+                                column_bias(ln, ts.rowshift, c + g, grp, bias);
+                                score_chunk<T, D>(Ks, c + g, col, grp, qf, bias, s[g]);
+                            }
+                            rv[g] = row_ok(ln, ts.rowshift, in0, c + g, grp);
+                            cm = fmaxp(cm, rv[g] ? max8(s[g]) : -INFINITY);
+                        }
+                    }
+                    const float mnew = fmaxp(m, max_rows(cm) * sc2);
+                    const float mref = mnew == -INFINITY ? 0.f : mnew;
+                    const float corr = __builtin_amdgcn_exp2f(m - mref);
+                    m = mnew;
+                    lacc *= corr;
+#pragma unroll
+                    for (int db = 0; db < D / 16; ++db) acc[db] *= corr;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        if (g < n) {
+                            const float off = rv[g] ? -mref : -INFINITY;
+#pragma unroll
+                            for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+                                for (int i = 0; i < 4; ++i)
+                                    s[g][bb][i] = __builtin_amdgcn_exp2f(fmaf(s[g][bb][i], sc2, off));
+                            const uint4 pk = pack8<T>(s[g]);
+                            accumulate_chunk<T, D>(Vs, c + g, lane, pk, acc);
+                            lacc = Mma<T>::run(ones, pk, lacc);
+                        }
                     }
                 }
-                const float mnew = fmaxf(m, max_rows(cm) * sc2);
-                const float mref = mnew == -INFINITY ? 0.f : mnew;
-                const float corr = __builtin_amdgcn_exp2f(m - mref);
-                m = mnew;
-                lacc *= corr;
-#pragma unroll
-                for (int db = 0; db < D / 16; ++db) acc[db] *= corr;
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    if (g < n) {
-                        const float off = rv[g] ? -mref : -INFINITY;
-#pragma unroll
-                        for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-                            for (int i = 0; i < 4; ++i)
-                                s[g][bb][i] = __builtin_amdgcn_exp2f(fmaf(s[g][bb][i], sc2, off));
-                        const uint4 pk = pack8<T>(s[g]);
-                        accumulate_chunk<T, D>(Vs, c + g, lane, pk, acc);
-                        lacc = Mma<T>::run(ones, pk, lacc);
-                    }
-                }
-            }
+            };
+            if (wide)
+                chunks(std::true_type{});
+            else
+                chunks(std::false_type{});
         }
         more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
@@ -740,20 +757,31 @@ __global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const 
         __syncthreads();
         if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
-            for (int c = wg.c0; c <= wg.c1; ++c) {
-                f32x4_t bias[2] = {cb[0], cb[1]};
-                if (wide) column_bias(ln, ts.rowshift, c, grp, bias);
-                f32x4_t s[2], dp[2];
-                score_chunk<T, D>(Ks, c, col, grp, qf, bias, s);
-                score_chunk<T, D>(Vs, c, col, grp, gf, nd, dp);
-                const float off = row_ok(ln, ts.rowshift, in0, c, grp) ? -L2 : -INFINITY;
+            const auto chunks = [&](auto wide_tag) {
+                constexpr bool WIDE = decltype(wide_tag)::value;
+                for (int c = wg.c0; c <= wg.c1; ++c) {
+                    f32x4_t s[2], dp[2];
+                    if constexpr (!WIDE) {
+                        score_chunk<T, D>(Ks, c, col, grp, qf, cb, s);
+                    } else {
+                        f32x4_t bias[2];
+                        column_bias(ln, ts.rowshift, c, grp, bias);
+                        score_chunk<T, D>(Ks, c, col, grp, qf, bias, s);
+                    }
+                    score_chunk<T, D>(Vs, c, col, grp, gf, nd, dp);
+                    const float off = row_ok(ln, ts.rowshift, in0, c, grp) ? -L2 : -INFINITY;
 #pragma unroll
-                for (int bb = 0; bb < 2; ++bb)
+                    for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], sc2, off)) * dp[bb][i];
-                accumulate_chunk<T, D>(Ks, c, lane, pack8<T>(s), acc);
-            }
+                        for (int i = 0; i < 4; ++i)
+                            s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], sc2, off)) * dp[bb][i];
+                    accumulate_chunk<T, D>(Ks, c, lane, pack8<T>(s), acc);
+                }
+            };
+            if (wide)
+                chunks(std::true_type{});
+            else
+                chunks(std::false_type{});
         }
         more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
@@ -851,28 +879,39 @@ __global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const
         __syncthreads();
         if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
-            for (int c = wg.c0; c <= wg.c1; ++c) {
-                const int s0 = 32 * c + 8 * grp;
-                f32x4_t bias[2] = {cb[0], cb[1]};
-                if (wide) column_bias(ln, ts.rowshift, c, grp, bias);
-                const f32x4_t ndc[2] = {*reinterpret_cast<const f32x4_t*>(ND + s0),
-                                        *reinterpret_cast<const f32x4_t*>(ND + s0 + 4)};
-                f32x4_t s[2], dp[2];
-                score_chunk<T, D>(Qs, c, col, grp, kf, bias, s);
-                score_chunk<T, D>(Gs, c, col, grp, vf, ndc, dp);
-                const float* nlp = row_ok(ln, ts.rowshift, in0, c, grp) ? NL + s0 : NL + slots;
-                const f32x4_t nl[2] = {*reinterpret_cast<const f32x4_t*>(nlp),
-                                       *reinterpret_cast<const f32x4_t*>(nlp + 4)};
-#pragma unroll
-                for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], sc2, nl[bb][i]));
-                        dp[bb][i] *= s[bb][i];
+            const auto chunks = [&](auto wide_tag) {
+                constexpr bool WIDE = decltype(wide_tag)::value;
+                for (int c = wg.c0; c <= wg.c1; ++c) {
+                    const int s0 = 32 * c + 8 * grp;
+                    const f32x4_t ndc[2] = {*reinterpret_cast<const f32x4_t*>(ND + s0),
+                                            *reinterpret_cast<const f32x4_t*>(ND + s0 + 4)};
+                    f32x4_t s[2], dp[2];
+                    if constexpr (!WIDE) {
+                        score_chunk<T, D>(Qs, c, col, grp, kf, cb, s);
+                    } else {
+                        f32x4_t bias[2];
+                        column_bias(ln, ts.rowshift, c, grp, bias);
+                        score_chunk<T, D>(Qs, c, col, grp, kf, bias, s);
                     }
-                accumulate_chunk<T, D>(Gs, c, lane, pack8<T>(s), gv);
-                accumulate_chunk<T, D>(Qs, c, lane, pack8<T>(dp), gk);
-            }
+                    score_chunk<T, D>(Gs, c, col, grp, vf, ndc, dp);
+                    const float* nlp = row_ok(ln, ts.rowshift, in0, c, grp) ? NL + s0 : NL + slots;
+                    const f32x4_t nl[2] = {*reinterpret_cast<const f32x4_t*>(nlp),
+                                           *reinterpret_cast<const f32x4_t*>(nlp + 4)};
+#pragma unroll
+                    for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], sc2, nl[bb][i]));
+                            dp[bb][i] *= s[bb][i];
+                        }
+                    accumulate_chunk<T, D>(Gs, c, lane, pack8<T>(s), gv);
+                    accumulate_chunk<T, D>(Qs, c, lane, pack8<T>(dp), gk);
+                }
+            };
+            if (wide)
+                chunks(std::true_type{});
+            else
+                chunks(std::false_type{});
         }
         // next slice: within the pair (q heads x axis-0 slices), else the next pair
         fresh = false;
