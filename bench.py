@@ -19,8 +19,8 @@ eager one is in ``config.eager_ms_per_step``).  Prints one JSON line:
   with P = B * Hq * (valid query-key pairs of the neighbourhood map);
 * roofline: for the kernel with the largest share of GPU time, its
   algorithmic HBM bytes per launch / its mean launch time (HIP events
-  bracketing each launch on its stream, recorded during the timed steps),
-  against 8 TB/s; ``traffic`` is the HBM bytes per launch measured with
+  bracketing each launch on its stream, over K eager steps that the host
+  queues while the GPU spins, so host launch gaps stay out), against 8 TB/s; ``traffic`` is the HBM bytes per launch measured with
   rocprofv3 (FETCH_SIZE x 2 + WRITE_SIZE, calibrated on a copy kernel) for
   the same kernel and workload, read from profiles/traffic.txt when present;
 * cpu_baseline: the CPU oracle (the reference's pure algorithm) timed on the
@@ -225,10 +225,26 @@ def main():
     torch.cuda.synchronize()
     _lib.profile_read(reset=True)
 
-    def timed(run, profile=False):
+    def spin_cycles_per_ms():
+        """GPU clock cycles of torch's spin kernel per millisecond."""
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        a.record()
+        torch.cuda._sleep(2_000_000)
+        b.record()
+        torch.cuda.synchronize()
+        return 2_000_000 / max(a.elapsed_time(b), 1e-3)
+
+    def timed(run, profile=False, head_start_ms=0.0):
+        """Mean GPU time per call of run() over K calls.  With head_start_ms
+        the stream first spins that long, so that the host queues the K calls
+        while the GPU is busy and no host launch gap falls inside the timed
+        region (or inside the per-launch intervals)."""
         _lib.profile_enable(profile)
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        if head_start_ms > 0:
+            torch.cuda._sleep(int(head_start_ms * cycles_per_ms))
         start.record()
         for _ in range(args.steps):
             run()
@@ -239,11 +255,14 @@ def main():
 
     # eager step time with the per-launch event timing off; the same K steps
     # are then repeated with every library launch bracketed by HIP events on
-    # its stream, which gives the per-kernel durations for the roofline
+    # its stream, which gives the per-kernel durations for the roofline.  The
+    # host is slower than the GPU on an eager step, so the bracketed pass
+    # starts behind a spin long enough for the host to queue all K steps.
     ms_eager = timed(step)
-    ms_profiled = timed(step, profile=True)
+    cycles_per_ms = spin_cycles_per_ms()
+    ms_profiled = timed(step, profile=True, head_start_ms=2.0 * args.steps * ms_eager + 5.0)
     stats = _lib.profile_read(reset=True)
-    _log(f"eager step {ms_eager:.4f} ms (with per-launch events: {ms_profiled:.4f} ms)")
+    _log(f"eager step {ms_eager:.4f} ms (queued ahead, with per-launch events: {ms_profiled:.4f} ms)")
 
     # the same step captured once in a HIP graph (forward + autograd backward)
     # and replayed: identical kernels and buffers without the per-step host

@@ -41,8 +41,11 @@ hipEvent_t take_event() {
             return e;
         }
     }
+    // timing-only events: no system-scope fence (cache write-back and
+    // invalidate) on record, which would slow the bracketed kernel and
+    // stretch the interval
     hipEvent_t e = nullptr;
-    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
     return e;
 }
 
