@@ -35,6 +35,10 @@
  *   natten_hip_av_backward     _core/metal.py:1473-1611 (a/v backward kernels)
  *   natten_hip_neighborhood_map _core/pure.py:91-129, 335-387 (index maps; the
  *                              Metal backend has no equivalent export)
+ *   natten_hip_varlen_forward  _core/metal.py:624-811 na{1,2,3}d_varlen_forward
+ *                              (and _core/pure.py:573-673)
+ *   natten_hip_varlen_backward functional.py:721-754, 804-835, 860-893 (the
+ *                              per-sample autograd loops of _NA{1,2,3}DVarlenFunction)
  */
 #ifndef NATTEN_HIP_H
 #define NATTEN_HIP_H
@@ -157,6 +161,36 @@ int natten_hip_av_backward(const natten_problem_t *p,
 int natten_hip_neighborhood_map(const natten_problem_t *p,
                                 int64_t *flat, uint8_t *valid,
                                 void *stream);
+
+/* Variable-length fused forward / backward.  The problem describes the
+ * padded (maximum) extents, stride 1; lens (device memory, int32 [batch][3],
+ * padded axes first as in `length`) holds each sample's own extent per axis,
+ * with kernel * dilation <= lens[b][a] <= length[a].  Sample b attends within
+ * its own extent exactly as an unpadded problem of that size would; outputs
+ * and gradients at padding positions are zero (lse and delta there are 0).
+ * A sample whose extents are out of range (or an even kernel equal to its
+ * extent, non-causal, dilation 1) comes out all zero.  Other arguments as for
+ * natten_hip_forward / natten_hip_backward. */
+int natten_hip_varlen_forward(const natten_problem_t *p, const int32_t *lens,
+                              const void *q, const natten_layout_t *lq,
+                              const void *k, const natten_layout_t *lk,
+                              const void *v, const natten_layout_t *lv,
+                              void *out, const natten_layout_t *lo,
+                              float *lse, const natten_layout_t *llse,
+                              void *stream);
+
+int natten_hip_varlen_backward(const natten_problem_t *p, const int32_t *lens,
+                               const void *q, const natten_layout_t *lq,
+                               const void *k, const natten_layout_t *lk,
+                               const void *v, const natten_layout_t *lv,
+                               const void *out, const natten_layout_t *lo,
+                               const void *dout, const natten_layout_t *ldo,
+                               const float *lse, const natten_layout_t *llse,
+                               void *dq, const natten_layout_t *ldq,
+                               void *dk, const natten_layout_t *ldk,
+                               void *dv, const natten_layout_t *ldv,
+                               float *delta, const natten_layout_t *ldelta,
+                               void *stream);
 
 /* Per-kernel timing (no counterpart in the reference; for benchmarks and
  * profiling).  While enabled, every kernel launch of the library is bracketed

@@ -251,6 +251,51 @@ int natten_hip_av_backward(const natten_problem_t* p, const void* dout, const na
                          "av_backward");
 }
 
+int natten_hip_varlen_forward(const natten_problem_t* p, const int32_t* lens, const void* q,
+                              const natten_layout_t* lq, const void* k, const natten_layout_t* lk, const void* v,
+                              const natten_layout_t* lv, void* out, const natten_layout_t* lo, float* lse,
+                              const natten_layout_t* llse, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, true, P);
+    if (rc) return rc;
+    if (any_null({lens, q, k, v, out, lse, lq, lk, lv, lo, llse})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    for (int a = 0; a < 3; ++a)
+        if (P.ax[a].st != 1) return fail(NATTEN_ERR_INVALID, "variable-length attention needs stride 1");
+    const int D = P.Dqk > P.Dv ? P.Dqk : P.Dv;
+    const int vec =
+        runs_aligned(dpl_for(D), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {v, lv, P.Dv}, {out, lo, P.Dv}}) ? 1 : 0;
+    return launch_status(na::generic_forward(P, vec, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo),
+                                             lse, to_lay(llse), p->dtype, static_cast<hipStream_t>(stream), lens),
+                         "varlen_forward");
+}
+
+int natten_hip_varlen_backward(const natten_problem_t* p, const int32_t* lens, const void* q,
+                               const natten_layout_t* lq, const void* k, const natten_layout_t* lk, const void* v,
+                               const natten_layout_t* lv, const void* out, const natten_layout_t* lo,
+                               const void* dout, const natten_layout_t* ldo, const float* lse,
+                               const natten_layout_t* llse, void* dq, const natten_layout_t* ldq, void* dk,
+                               const natten_layout_t* ldk, void* dv, const natten_layout_t* ldv, float* delta,
+                               const natten_layout_t* ldelta, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, true, P);
+    if (rc) return rc;
+    if (any_null({lens, q, k, v, out, dout, lse, dq, dk, dv, delta, lq, lk, lv, lo, ldo, llse, ldq, ldk, ldv,
+                  ldelta}))
+        return fail(NATTEN_ERR_INVALID, "NULL operand");
+    for (int a = 0; a < 3; ++a)
+        if (P.ax[a].st != 1) return fail(NATTEN_ERR_INVALID, "variable-length attention needs stride 1");
+    const int D = P.Dqk > P.Dv ? P.Dqk : P.Dv;
+    const int vec = runs_aligned(dpl_for(D), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {v, lv, P.Dv}, {out, lo, P.Dv},
+                                              {dout, ldo, P.Dv}, {dq, ldq, P.Dqk}, {dk, ldk, P.Dqk}, {dv, ldv, P.Dv}})
+                        ? 1
+                        : 0;
+    return launch_status(
+        na::generic_backward(P, vec, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout, to_lay(ldo),
+                             lse, to_lay(llse), nullptr, na::Lay{}, dq, to_lay(ldq), dk, to_lay(ldk), dv, to_lay(ldv),
+                             delta, to_lay(ldelta), p->dtype, static_cast<hipStream_t>(stream), lens),
+        "varlen_backward");
+}
+
 int natten_hip_neighborhood_map(const natten_problem_t* p, int64_t* flat, uint8_t* valid, void* stream) {
     na::Prob P;
     int rc = make_prob(p, true, P);

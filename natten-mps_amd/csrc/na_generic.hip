@@ -54,11 +54,41 @@ __device__ __forceinline__ long long group_index(int lpq) {
     return (static_cast<long long>(blk) * blockDim.x + threadIdx.x) / lpq;
 }
 
+// Variable-length problems: lens[b * 3 + a] is sample b's extent on padded
+// axis a (stride 1).  It replaces the problem's (maximum) extent in the window
+// rule; positions past it are padding.  A sample whose extents fall outside
+// [kernel * dilation, maximum], or hit the even-kernel-equal-to-length case,
+// is all padding.  False: (i0, i1, i2) is padding for its sample.
+__device__ __forceinline__ bool sample_extent(Prob& p, const int* __restrict__ lens, int b, int i0, int i1,
+                                              int i2) {
+    int L[3];
+    bool ok = true;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const Axis& A = p.ax[a];
+        L[a] = lens[b * 3 + a];
+        ok = ok && L[a] >= A.k * A.dil && L[a] <= A.len &&
+             !(!A.causal && A.dil == 1 && (A.k % 2) == 0 && A.k == L[a]);
+    }
+    if (!ok || i0 >= L[0] || i1 >= L[1] || i2 >= L[2]) return false;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) p.ax[a].len = p.ax[a].out = L[a];
+    return true;
+}
+
+template <typename T, int DPL>
+__device__ __forceinline__ void store_zero(T* g, int d0, int D, int vec) {
+    float z[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) z[j] = 0.f;
+    store_run<T, DPL>(g, d0, D, vec, z);
+}
+
 // ---------------------------------------------------------------------------
 // Fused forward with online softmax.
 // ---------------------------------------------------------------------------
 template <typename T, int DPL, int LPQ>
-__global__ __launch_bounds__(256) void k_forward(Prob p, int vec,
+__global__ __launch_bounds__(256) void k_forward(Prob p, int vec, const int* __restrict__ lens,
                                                  const T* __restrict__ q, Lay lq,
                                                  const T* __restrict__ k, Lay lk,
                                                  const T* __restrict__ v, Lay lv,
@@ -69,6 +99,11 @@ __global__ __launch_bounds__(256) void k_forward(Prob p, int vec,
     const int d0 = (threadIdx.x % LPQ) * DPL;
     const QPos Q = decode_query(p, qi);
     const int hk = Q.h / p.rep;
+    if (lens && !sample_extent(p, lens, Q.b, Q.i0, Q.i1, Q.i2)) {
+        store_zero<T, DPL>(out + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec);
+        if (d0 == 0) lse[ll.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = 0.f;
+        return;
+    }
 
     float qv[DPL];
     load_run<T, DPL>(q + lq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, qv);
@@ -166,7 +201,7 @@ __global__ __launch_bounds__(256) void k_av(Prob p, int vec,
 // dq = scale * sum_k P (dO.v_k - delta) k_k with P = exp(scale q.k - lse).
 // ---------------------------------------------------------------------------
 template <typename T, int DPL, int LPQ>
-__global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec,
+__global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec, const int* __restrict__ lens,
                                                 const T* __restrict__ q, Lay lq,
                                                 const T* __restrict__ k, Lay lk,
                                                 const T* __restrict__ v, Lay lv,
@@ -181,6 +216,11 @@ __global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec,
     const int d0 = (threadIdx.x % LPQ) * DPL;
     const QPos Q = decode_query(p, qi);
     const int hk = Q.h / p.rep;
+    if (lens && !sample_extent(p, lens, Q.b, Q.i0, Q.i1, Q.i2)) {
+        store_zero<T, DPL>(dq + ldq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec);
+        if (d0 == 0) delta[lde.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = 0.f;
+        return;
+    }
 
     float qv[DPL], dov[DPL];
     load_run<T, DPL>(q + lq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, qv);
@@ -242,7 +282,7 @@ __global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec,
 // atomics); recomputes P from q, k and lse.
 // ---------------------------------------------------------------------------
 template <typename T, int DPL, int LPQ>
-__global__ __launch_bounds__(256) void k_bwd_dkdv(Prob p, int vec,
+__global__ __launch_bounds__(256) void k_bwd_dkdv(Prob p, int vec, const int* __restrict__ lens,
                                                   const T* __restrict__ q, Lay lq,
                                                   const T* __restrict__ k, Lay lk,
                                                   const T* __restrict__ v, Lay lv,
@@ -255,6 +295,11 @@ __global__ __launch_bounds__(256) void k_bwd_dkdv(Prob p, int vec,
     if (ki >= static_cast<long long>(p.B) * p.nkey * p.Hkv) return;
     const int d0 = (threadIdx.x % LPQ) * DPL;
     const KPos K = decode_key(p, ki, p.Hkv);
+    if (lens && !sample_extent(p, lens, K.b, K.m0, K.m1, K.m2)) {
+        store_zero<T, DPL>(dk + ldk.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dqk, vec);
+        store_zero<T, DPL>(dv + ldv.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dv, vec);
+        return;
+    }
 
     float kv[DPL], vv[DPL], gk[DPL], gv[DPL];
     load_run<T, DPL>(k + lk.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dqk, vec, kv);
@@ -463,11 +508,12 @@ inline unsigned grid_for(long long groups, int lpq) {
 
 template <typename T, int DPL, int LPQ>
 struct LForward {
-    static hipError_t run(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
-                          Lay lv, void* o, Lay lo, float* lse, Lay ll, hipStream_t s) {
+    static hipError_t run(const Prob& p, int vec, const int* lens, const void* q, Lay lq, const void* k, Lay lk,
+                          const void* v, Lay lv, void* o, Lay lo, float* lse, Lay ll, hipStream_t s) {
         const long long n = static_cast<long long>(p.B) * p.nout * p.Hq;
-        NA_LAUNCH("na_forward", (k_forward<T, DPL, LPQ>), dim3(grid_for(n, LPQ)), dim3(256), 0, s, p, vec,
-                           (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (T*)o, lo, lse, ll);
+        NA_LAUNCH(lens ? "na_varlen_forward" : "na_forward", (k_forward<T, DPL, LPQ>), dim3(grid_for(n, LPQ)),
+                  dim3(256), 0, s, p, vec, lens, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (T*)o, lo, lse,
+                  ll);
         return hipGetLastError();
     }
 };
@@ -496,20 +542,21 @@ struct LAV {
 
 template <typename T, int DPL, int LPQ>
 struct LBackward {
-    static hipError_t run(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
-                          Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
-                          const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
-                          float* delta, Lay lde, hipStream_t s) {
+    static hipError_t run(const Prob& p, int vec, const int* lens, const void* q, Lay lq, const void* k, Lay lk,
+                          const void* v, Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse,
+                          Lay ll, const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv,
+                          Lay ldv, float* delta, Lay lde, hipStream_t s) {
         const long long nq = static_cast<long long>(p.B) * p.nout * p.Hq;
-        NA_LAUNCH("na_bwd_dq", (k_bwd_dq<T, DPL, LPQ>), dim3(grid_for(nq, LPQ)), dim3(256), 0, s, p, vec,
-                           (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (const T*)o, lo, (const T*)dout, ldo,
-                           lse, ll, dlse, ldl, (T*)dq, ldq, delta, lde);
+        NA_LAUNCH(lens ? "na_varlen_bwd_dq" : "na_bwd_dq", (k_bwd_dq<T, DPL, LPQ>), dim3(grid_for(nq, LPQ)),
+                  dim3(256), 0, s, p, vec, lens, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (const T*)o, lo,
+                  (const T*)dout, ldo, lse, ll, dlse, ldl, (T*)dq, ldq, delta, lde);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const long long nk = static_cast<long long>(p.B) * p.nkey * p.Hkv;
-        NA_LAUNCH("na_bwd_dkdv", (k_bwd_dkdv<T, DPL, LPQ>), dim3(grid_for(nk, LPQ)), dim3(256), 0, s, p, vec,
-                           (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (const T*)dout, ldo, lse, ll,
-                           (const float*)delta, lde, (T*)dk, ldk, (T*)dv, ldv);
+        NA_LAUNCH(lens ? "na_varlen_bwd_dkdv" : "na_bwd_dkdv", (k_bwd_dkdv<T, DPL, LPQ>),
+                  dim3(grid_for(nk, LPQ)), dim3(256), 0, s, p, vec, lens, (const T*)q, lq, (const T*)k, lk,
+                  (const T*)v, lv, (const T*)dout, ldo, lse, ll, (const float*)delta, lde, (T*)dk, ldk, (T*)dv,
+                  ldv);
         return hipGetLastError();
     }
 };
@@ -549,8 +596,9 @@ struct LAVBwd {
 }  // namespace
 
 hipError_t generic_forward(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
-                           Lay lv, void* o, Lay lo, float* lse, Lay ll, int dtype, hipStream_t s) {
-    return by_type<LForward>(dtype, p.Dqk > p.Dv ? p.Dqk : p.Dv, p, vec, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
+                           Lay lv, void* o, Lay lo, float* lse, Lay ll, int dtype, hipStream_t s, const int* lens) {
+    return by_type<LForward>(dtype, p.Dqk > p.Dv ? p.Dqk : p.Dv, p, vec, lens, q, lq, k, lk, v, lv, o, lo, lse, ll,
+                             s);
 }
 
 hipError_t generic_qk(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, void* a, Lay la,
@@ -566,9 +614,9 @@ hipError_t generic_av(const Prob& p, int vec, const void* a, Lay la, const void*
 hipError_t generic_backward(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
                             Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                             const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
-                            float* delta, Lay lde, int dtype, hipStream_t s) {
-    return by_type<LBackward>(dtype, p.Dqk > p.Dv ? p.Dqk : p.Dv, p, vec, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl, dq,
-                              ldq, dk, ldk, dv, ldv, delta, lde, s);
+                            float* delta, Lay lde, int dtype, hipStream_t s, const int* lens) {
+    return by_type<LBackward>(dtype, p.Dqk > p.Dv ? p.Dqk : p.Dv, p, vec, lens, q, lq, k, lk, v, lv, o, lo, dout,
+                              ldo, lse, ll, dlse, ldl, dq, ldq, dk, ldk, dv, ldv, delta, lde, s);
 }
 
 hipError_t generic_qk_backward(const Prob& p, int vec, const void* da, Lay lda, const void* q, Lay lq,

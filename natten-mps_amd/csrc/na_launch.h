@@ -9,8 +9,11 @@ namespace na {
 void prof_begin(const char* name, hipStream_t s);
 void prof_end(hipStream_t s);
 
+// `lens` (device, int32 [B][3]): per-sample extents of a variable-length
+// problem, or null.
 hipError_t generic_forward(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
-                           Lay lv, void* o, Lay lo, float* lse, Lay ll, int dtype, hipStream_t s);
+                           Lay lv, void* o, Lay lo, float* lse, Lay ll, int dtype, hipStream_t s,
+                           const int* lens = nullptr);
 hipError_t generic_qk(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, void* a, Lay la,
                       int dtype, hipStream_t s);
 hipError_t generic_av(const Prob& p, int vec, const void* a, Lay la, const void* v, Lay lv, void* o, Lay lo,
@@ -18,7 +21,7 @@ hipError_t generic_av(const Prob& p, int vec, const void* a, Lay la, const void*
 hipError_t generic_backward(const Prob& p, int vec, const void* q, Lay lq, const void* k, Lay lk, const void* v,
                             Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                             const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
-                            float* delta, Lay lde, int dtype, hipStream_t s);
+                            float* delta, Lay lde, int dtype, hipStream_t s, const int* lens = nullptr);
 hipError_t generic_qk_backward(const Prob& p, int vec, const void* da, Lay lda, const void* q, Lay lq,
                                const void* k, Lay lk, void* dq, Lay ldq, void* dk, Lay ldk, int dtype,
                                hipStream_t s);

@@ -15,6 +15,10 @@ Module contract (same names and argument order as the reference backends,
   scale=None) -> (dq, dk)``
 * ``na{r}d_av_backward(d_out, attn, v, kernel_size, dilation, stride,
   is_causal) -> (d_attn, dv)``
+* ``na{r}d_varlen_forward(q, k, v, sizes, kernel_size, dilation, scale)``
+  (``_core/metal.py:624-811``), plus ``na{r}d_varlen_forward_with_lse`` and
+  ``na{r}d_varlen_backward(d_out, q, k, v, out, lse, sizes, kernel_size,
+  dilation, scale) -> (dq, dk, dv)`` for the autograd Function
 
 Tensors stay spatial-first ``[B, *sp, H, D]``; the kernels read them through
 their strides (only a non-unit innermost stride forces a copy), in their own
@@ -377,6 +381,71 @@ def neighborhood_map(rank: int, spatial: Sequence[int], kernel_size, dilation, s
 
 
 # ---------------------------------------------------------------------------
+# variable-length fused forward / backward (_core/metal.py:624-811 and the
+# per-sample backward loops of functional.py:721-754, 804-835, 860-893)
+# ---------------------------------------------------------------------------
+
+
+def _varlen_lens(rank: int, sizes: torch.Tensor, device) -> torch.Tensor:
+    """Per-sample extents ``[B, rank]`` -> int32 ``[B, 3]`` on the device,
+    padded (leading) axes set to 1."""
+    s = sizes.reshape(sizes.shape[0], rank).to(device=device, dtype=torch.int32)
+    if rank < 3:
+        s = torch.cat([torch.ones((s.shape[0], 3 - rank), dtype=torch.int32, device=device), s], dim=1)
+    return s.contiguous()
+
+
+def _varlen_problem(rank, q, k, v, kernel_size, dilation, scale_value):
+    _check_qkv(rank, q, k, v)
+    _on_device(q, k, v)
+    _same_dtype(q, k, v)
+    return _fused_problem(rank, q, k, v, kernel_size, (1,) * rank, dilation, (False,) * rank, scale_value)
+
+
+def varlen_forward_with_lse(rank: int, q, k, v, sizes, kernel_size, dilation, scale):
+    """Fused forward of a padded batch whose sample b has spatial extent
+    ``sizes[b]`` (``[B, rank]`` ints): ``(out, lse)``, zero at padding."""
+    q, k, v = _inner(q), _inner(k), _inner(v)
+    scale_value = float(q.shape[-1] ** -0.5 if scale is None else scale)
+    prob = _varlen_problem(rank, q, k, v, kernel_size, dilation, scale_value)
+    lens = _varlen_lens(rank, sizes, q.device)
+    B, Hq = q.shape[0], q.shape[-2]
+    sp = tuple(q.shape[1:1 + rank])
+    out = torch.empty((B, *sp, Hq, v.shape[-1]), dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, *sp, Hq), dtype=torch.float32, device=q.device)
+    L = lambda t, tr=1: _byref(_lib.layout(t, rank, tr))  # noqa: E731
+    lib = _lib.load()
+    rc = _launch(q.device, lib.natten_hip_varlen_forward, _byref(prob), lens.data_ptr(),
+                 q.data_ptr(), L(q), k.data_ptr(), L(k), v.data_ptr(), L(v), out.data_ptr(), L(out),
+                 lse.data_ptr(), L(lse, 0), _raw_stream(q.device))
+    _lib.check(rc, "varlen_forward")
+    return out, lse
+
+
+def varlen_backward(rank: int, d_out, q, k, v, out, lse, sizes, kernel_size, dilation, scale):
+    """``(dq, dk, dv)`` of :func:`varlen_forward_with_lse`, zero at padding."""
+    q, k, v, out, d_out = _inner(q), _inner(k), _inner(v), _inner(out), _inner(d_out.to(q.dtype))
+    lse = lse.to(torch.float32).contiguous()
+    scale_value = float(q.shape[-1] ** -0.5 if scale is None else scale)
+    prob = _varlen_problem(rank, q, k, v, kernel_size, dilation, scale_value)
+    _on_device(d_out, out, lse)
+    lens = _varlen_lens(rank, sizes, q.device)
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    delta = torch.empty(lse.shape, dtype=torch.float32, device=q.device)
+    L = lambda t, tr=1: _byref(_lib.layout(t, rank, tr))  # noqa: E731
+    lib = _lib.load()
+    rc = _launch(q.device, lib.natten_hip_varlen_backward, _byref(prob), lens.data_ptr(),
+                 q.data_ptr(), L(q), k.data_ptr(), L(k), v.data_ptr(), L(v), out.data_ptr(), L(out),
+                 d_out.data_ptr(), L(d_out), lse.data_ptr(), L(lse, 0), dq.data_ptr(), L(dq),
+                 dk.data_ptr(), L(dk), dv.data_ptr(), L(dv), delta.data_ptr(), L(delta, 0),
+                 _raw_stream(q.device))
+    _lib.check(rc, "varlen_backward")
+    return dq, dk, dv
+
+
+# ---------------------------------------------------------------------------
 # rank-specific names (the backend-module contract)
 # ---------------------------------------------------------------------------
 
@@ -405,8 +474,19 @@ def _bind(rank: int) -> None:
     def avb(d_out, attn, v, kernel_size, dilation, stride=(1,) * rank, is_causal=(False,) * rank):
         return av_backward(rank, d_out, attn, v, kernel_size, dilation, stride, is_causal)
 
+    def vfwd(q, k, v, sizes, kernel_size, dilation, scale):
+        return varlen_forward_with_lse(rank, q, k, v, sizes, kernel_size, dilation, scale)[0]
+
+    def vfwd_lse(q, k, v, sizes, kernel_size, dilation, scale):
+        return varlen_forward_with_lse(rank, q, k, v, sizes, kernel_size, dilation, scale)
+
+    def vbwd(d_out, q, k, v, out, lse, sizes, kernel_size, dilation, scale):
+        return varlen_backward(rank, d_out, q, k, v, out, lse, sizes, kernel_size, dilation, scale)
+
     for suffix, fn in (("forward", fwd), ("forward_with_lse", fwd_lse), ("fused_backward", fbwd),
-                       ("qk_forward", qk), ("av_forward", av), ("qk_backward", qkb), ("av_backward", avb)):
+                       ("qk_forward", qk), ("av_forward", av), ("qk_backward", qkb), ("av_backward", avb),
+                       ("varlen_forward", vfwd), ("varlen_forward_with_lse", vfwd_lse),
+                       ("varlen_backward", vbwd)):
         name = f"na{rank}d_{suffix}"
         fn.__name__ = fn.__qualname__ = name
         g[name] = fn

@@ -309,15 +309,141 @@ def na3d_av(attn, value, kernel_size, dilation=1, *, stride=1, is_causal=False):
 
 
 # ---------------------------------------------------------------------------
-# variable-length attention: not part of this build
+# variable-length attention (functional.py:678-1026)
+#
+# Tensors are padded to a common extent; sample b attends within its own
+# extent only (its windows follow the rule for that extent), and outputs and
+# gradients at padding positions are zero.  The 'hip' backend runs all
+# samples in one launch per op, each reading its extent from a device array;
+# the backward is the fused varlen backward (no per-sample autograd loop).
 # ---------------------------------------------------------------------------
 
 
-def _varlen_unsupported(*_args, **_kwargs):
-    raise NotImplementedError(
-        "variable-length neighborhood attention (na{1,2,3}d_varlen) is not implemented by natten_mps_amd; "
-        "pad to a common size and call na1d/na2d/na3d per size group."
-    )
+def _validate_seq_lens(seq_lens: torch.Tensor, batch_size: int, l_max: int, kernel_size: int) -> None:
+    """``functional.py:678-700``."""
+    if seq_lens.ndim != 1 or seq_lens.shape[0] != batch_size:
+        raise ValueError(
+            f"seq_lens must be a 1-D tensor of length B={batch_size}, got shape {tuple(seq_lens.shape)}.")
+    if seq_lens.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"seq_lens must be int32 or int64, got {seq_lens.dtype}.")
+    min_len = int(seq_lens.min().item())
+    max_len = int(seq_lens.max().item())
+    if min_len < kernel_size:
+        raise ValueError(
+            f"All seq_lens must be >= kernel_size ({kernel_size}), but min(seq_lens)={min_len}.")
+    if max_len > l_max:
+        raise ValueError(f"All seq_lens must be <= L_max ({l_max}), but max(seq_lens)={max_len}.")
 
 
-na1d_varlen = na2d_varlen = na3d_varlen = _varlen_unsupported
+def _validate_spatial_sizes(spatial_sizes: torch.Tensor, batch_size: int, max_spatial: tuple, kernel_size: tuple,
+                            rank: int) -> None:
+    """``functional.py:757-787``."""
+    if spatial_sizes.ndim != 2 or spatial_sizes.shape[0] != batch_size or spatial_sizes.shape[1] != rank:
+        raise ValueError(f"spatial_sizes must be a [B, {rank}] tensor, got shape {tuple(spatial_sizes.shape)}.")
+    if spatial_sizes.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"spatial_sizes must be int32 or int64, got {spatial_sizes.dtype}.")
+    for d in range(rank):
+        min_dim = int(spatial_sizes[:, d].min().item())
+        max_dim = int(spatial_sizes[:, d].max().item())
+        if min_dim < kernel_size[d]:
+            raise ValueError(
+                f"All spatial_sizes[:,{d}] must be >= kernel_size[{d}] ({kernel_size[d]}), but min={min_dim}.")
+        if max_dim > max_spatial[d]:
+            raise ValueError(
+                f"All spatial_sizes[:,{d}] must be <= max_spatial[{d}] ({max_spatial[d]}), but max={max_dim}.")
+
+
+class _NAVarlenFunction(torch.autograd.Function):
+    """Fused varlen forward with LSE and the fused varlen backward of the
+    active backend (the reference's ``_NA{1,2,3}DVarlenFunction``,
+    ``functional.py:703-754``, with the per-sample loop replaced)."""
+
+    @staticmethod
+    def forward(ctx, rank, mod, query, key, value, sizes, ks, dil, scale):
+        out, lse = getattr(mod, f"na{rank}d_varlen_forward_with_lse")(query, key, value, sizes, ks, dil, scale)
+        ctx.rank, ctx.mod, ctx.ks, ctx.dil, ctx.scale = rank, mod, ks, dil, scale
+        ctx.save_for_backward(query, key, value, out, lse, sizes)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        q, k, v, out, lse, sizes = ctx.saved_tensors
+        dq, dk, dv = getattr(ctx.mod, f"na{ctx.rank}d_varlen_backward")(
+            grad_out.contiguous(), q, k, v, out, lse, sizes, ctx.ks, ctx.dil, ctx.scale)
+        return None, None, dq, dk, dv, None, None, None, None
+
+
+def _varlen_per_sample(rank, query, key, value, sizes, ks, dil, scale_value):
+    """Per-sample composition through the rank's na*d (``_core/pure.py:573-673``):
+    used by backends without fused varlen ops, and for samples whose extent
+    equals an even kernel on every axis (the reference's full-window path)."""
+    na = {1: na1d, 2: na2d, 3: na3d}[rank]
+    out = torch.zeros_like(query)
+    for b in range(query.shape[0]):
+        ext = [int(x) for x in sizes[b].reshape(-1).tolist()]
+        idx = (slice(b, b + 1),) + tuple(slice(0, n) for n in ext)
+        out[idx] = na(query[idx], key[idx], value[idx], kernel_size=ks, dilation=dil, scale=scale_value)
+    return out
+
+
+def _varlen(rank, query, key, value, sizes, kernel_size, dilation, scale):
+    nd = rank + 3
+    if query.ndim != nd or key.ndim != nd or value.ndim != nd:
+        raise ValueError(f"na{rank}d_varlen expects query/key/value with shape {_LAYOUTS[rank]}.")
+    if query.shape != key.shape or query.shape != value.shape:
+        raise ValueError("query, key, and value must have identical shapes.")
+    B = query.shape[0]
+    ks = normalize_kernel_size(kernel_size, rank)
+    dil = normalize_tuple_param(dilation, rank, "dilation")
+    max_sp = tuple(query.shape[1:1 + rank])
+    if rank == 1:
+        _validate_seq_lens(sizes, B, max_sp[0], ks[0])
+    else:
+        _validate_spatial_sizes(sizes, B, max_sp, ks, rank)
+    sizes2 = sizes.reshape(B, rank)
+    # a sample's extent must hold the dilated kernel, as na*d on its slice requires
+    for ext in {tuple(int(x) for x in row) for row in sizes2.tolist()}:
+        check_dilation_kernel_vs_input(dil, ks, ext)
+    scale_value = query.shape[-1] ** -0.5 if scale is None else float(scale)
+
+    mod = ops.active_module()
+    fused = not _using_pure_backend() and hasattr(mod, f"na{rank}d_varlen_forward_with_lse")
+    if not fused:
+        return _varlen_per_sample(rank, query, key, value, sizes2, ks, dil, scale_value)
+    out = _NAVarlenFunction.apply(rank, mod, query, key, value, sizes2, ks, dil, scale_value)
+    # samples with every extent equal to its (even) kernel take the full-window
+    # path of na*d, whose windows the neighbourhood rule does not describe
+    full = [b for b, row in enumerate(sizes2.tolist())
+            if all(n == k for n, k in zip(row, ks)) and any(k % 2 == 0 for k in ks)]
+    if full:
+        out = out.clone()
+        sel = torch.tensor(full, dtype=torch.long)
+        out[sel] = _varlen_per_sample(rank, query[sel], key[sel], value[sel], sizes2[sel], ks, dil, scale_value)
+    return out
+
+
+def na1d_varlen(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, seq_lens: torch.Tensor,
+                kernel_size: Union[int, Tuple[int]], dilation: Union[int, Tuple[int]] = 1,
+                scale: Optional[float] = None) -> torch.Tensor:
+    """Variable-length 1-D neighbourhood attention (``functional.py:897-933``):
+    ``[B, L_max, H, D]`` tensors, ``seq_lens`` ``[B]`` int with
+    ``kernel_size <= seq_lens[b] <= L_max``; positions past ``seq_lens[b]``
+    are zero in the output."""
+    return _varlen(1, query, key, value, seq_lens, kernel_size, dilation, scale)
+
+
+def na2d_varlen(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, spatial_sizes: torch.Tensor,
+                kernel_size: Union[int, Tuple[int, int]], dilation: Union[int, Tuple[int, int]] = 1,
+                scale: Optional[float] = None) -> torch.Tensor:
+    """Variable-length 2-D neighbourhood attention (``functional.py:936-975``):
+    ``[B, H_max, W_max, heads, D]`` tensors and ``spatial_sizes`` ``[B, 2]``."""
+    return _varlen(2, query, key, value, spatial_sizes, kernel_size, dilation, scale)
+
+
+def na3d_varlen(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, spatial_sizes: torch.Tensor,
+                kernel_size: Union[int, Tuple[int, int, int]], dilation: Union[int, Tuple[int, int, int]] = 1,
+                scale: Optional[float] = None) -> torch.Tensor:
+    """Variable-length 3-D neighbourhood attention (``functional.py:978-1019``):
+    ``[B, D_max, H_max, W_max, heads, dim]`` tensors and ``spatial_sizes``
+    ``[B, 3]``."""
+    return _varlen(3, query, key, value, spatial_sizes, kernel_size, dilation, scale)

@@ -11,7 +11,7 @@ def get_support_matrix() -> dict:
             "available": hip.is_available(),
             "forward": {"na1d": True, "na2d": True, "na3d": True, "split_qk_av": True},
             "backward": {"na1d": True, "na2d": True, "na3d": True, "split_qk_av": True},
-            "varlen": {"na1d": False, "na2d": False, "na3d": False},
+            "varlen": {"na1d": True, "na2d": True, "na3d": True},
             "fusion": {"na1d": True, "na2d": True, "na3d": True},
             "constraints": [
                 "Requires a ROCm GPU (gfx950 / MI355X) and the built libnatten_hip.so.",
@@ -20,6 +20,8 @@ def get_support_matrix() -> dict:
                 "Native GQA/MQA (no K/V expansion); fused forward writes the LSE, fused backward "
                 "accepts an LSE gradient (return_lse, additional_keys).",
                 "An even kernel equal to a non-causal, undilated axis length is rejected.",
+                "Variable-length (na{1,2,3}d_varlen): one launch per op for the whole padded batch, "
+                "fused backward; padding positions are zero.",
             ],
         },
     }

@@ -413,6 +413,38 @@ def na3d_av_backward(*args, **kwargs):
 # ---------------------------------------------------------------------------
 
 
+# ---------------------------------------------------------------------------
+# Variable-length forward (pure.py:573-673): the padded batch is processed
+# per sample on the sample's own extent; padding stays zero.
+# ---------------------------------------------------------------------------
+
+
+def _varlen(rank, fwd, q, k, v, sizes, kernel_size, dilation, scale):
+    out = torch.zeros_like(q)
+    stride = (1,) * rank
+    causal = (False,) * rank
+    for b in range(q.shape[0]):
+        ext = [int(x) for x in sizes[b].reshape(-1).tolist()]
+        idx = (slice(b, b + 1),) + tuple(slice(0, n) for n in ext)
+        out[idx] = fwd(q[idx], k[idx], v[idx], kernel_size, stride, dilation, causal, scale)
+    return out
+
+
+def na1d_varlen_forward(q, k, v, seq_lens, kernel_size, dilation, scale):
+    """``pure.py:573-600``."""
+    return _varlen(1, na1d_forward, q, k, v, seq_lens.reshape(-1, 1), kernel_size, dilation, scale)
+
+
+def na2d_varlen_forward(q, k, v, spatial_sizes, kernel_size, dilation, scale):
+    """``pure.py:608-636``."""
+    return _varlen(2, na2d_forward, q, k, v, spatial_sizes, kernel_size, dilation, scale)
+
+
+def na3d_varlen_forward(q, k, v, spatial_sizes, kernel_size, dilation, scale):
+    """``pure.py:644-673``."""
+    return _varlen(3, na3d_forward, q, k, v, spatial_sizes, kernel_size, dilation, scale)
+
+
 def forward(rank: int, q, k, v, kernel_size: Sequence[int], stride: Sequence[int],
             dilation: Sequence[int], is_causal: Sequence[bool], scale):
     """Rank-dispatching fused forward with GQA by ``repeat_interleave``
