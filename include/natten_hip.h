@@ -39,6 +39,11 @@
  *                              (and _core/pure.py:573-673)
  *   natten_hip_varlen_backward functional.py:721-754, 804-835, 860-893 (the
  *                              per-sample autograd loops of _NA{1,2,3}DVarlenFunction)
+ *   natten_hip_rpb_qk_forward  extras/allin1/functional.py:47-100, 153-250 and
+ *                              extras/allin1/metal.py (natten{1,2}dqkrpb)
+ *   natten_hip_rpb_av_forward  extras/allin1/functional.py:103-150, 253-325 (natten{1,2}dav)
+ *   natten_hip_rpb_qk_backward extras/allin1/functional.py:333-365, 413-448 (QK+RPB backward)
+ *   natten_hip_rpb_av_backward extras/allin1/functional.py:368-400, 451-485 (AV backward)
  */
 #ifndef NATTEN_HIP_H
 #define NATTEN_HIP_H
@@ -190,6 +195,52 @@ int natten_hip_varlen_backward(const natten_problem_t *p, const int32_t *lens,
                                void *dk, const natten_layout_t *ldk,
                                void *dv, const natten_layout_t *ldv,
                                float *delta, const natten_layout_t *ldelta,
+                               void *stream);
+
+/* Relative-position-bias split ops of DiNAT-style models (1-D or 2-D: the
+ * padded axis 0 has length and kernel 1; stride 1, non-causal, heads_q ==
+ * heads_kv).  They follow NATTEN 0.17's shifted windows: per axis, the start
+ * is phase-aligned to the query's residue class mod the dilation and may be
+ * negative near the borders for an even kernel, the window ends at
+ * min(len, start + kernel * dilation), and a neighbour is valid when it lies
+ * in [0, end).  Its bias index per axis is get_pb_start(query) + its offset,
+ * clamped to [0, 2K-2].
+ *   rpb_qk:  attn = q . k_neighbour + rpb[h, bias]   (-inf when invalid; the
+ *            logits are not scaled: scale q beforehand); rpb may be NULL
+ *   rpb_av:  out = sum over valid neighbours of attn * v_neighbour
+ *   rpb_qk_backward: dq, dk over valid pairs; drpb (may be NULL) sums dattn
+ *            over every entry at each bias index
+ *   rpb_av_backward: dattn (0 for invalid neighbours), dv
+ * rpb and drpb are contiguous [H, 2K1-1, 2K2-1] (1-D: [H, 2K-1]) in the
+ * problem's dtype; attn is [B, *sp, H, K1*K2]. */
+int natten_hip_rpb_qk_forward(const natten_problem_t *p,
+                              const void *q, const natten_layout_t *lq,
+                              const void *k, const natten_layout_t *lk,
+                              const void *rpb,
+                              void *attn, const natten_layout_t *la,
+                              void *stream);
+
+int natten_hip_rpb_av_forward(const natten_problem_t *p,
+                              const void *attn, const natten_layout_t *la,
+                              const void *v, const natten_layout_t *lv,
+                              void *out, const natten_layout_t *lo,
+                              void *stream);
+
+int natten_hip_rpb_qk_backward(const natten_problem_t *p,
+                               const void *dattn, const natten_layout_t *lda,
+                               const void *q, const natten_layout_t *lq,
+                               const void *k, const natten_layout_t *lk,
+                               void *dq, const natten_layout_t *ldq,
+                               void *dk, const natten_layout_t *ldk,
+                               void *drpb,
+                               void *stream);
+
+int natten_hip_rpb_av_backward(const natten_problem_t *p,
+                               const void *dout, const natten_layout_t *ldo,
+                               const void *attn, const natten_layout_t *la,
+                               const void *v, const natten_layout_t *lv,
+                               void *dattn, const natten_layout_t *lda,
+                               void *dv, const natten_layout_t *ldv,
                                void *stream);
 
 /* Per-kernel timing (no counterpart in the reference; for benchmarks and

@@ -40,7 +40,9 @@ int elem_size(int dtype) { return dtype == NATTEN_F32 ? 4 : 2; }
 
 // Validates the problem and fills the kernel-side descriptor.  `fused` ops use
 // out = ceil(len/stride); split ops may use a shorter query extent at stride 1.
-int make_prob(const natten_problem_t* p, bool fused, na::Prob& P) {
+// `shifted_windows` (the relative-position-bias ops, whose window rule
+// covers an even kernel equal to the axis) skips that one rejection.
+int make_prob(const natten_problem_t* p, bool fused, na::Prob& P, bool shifted_windows = false) {
     if (!p) return fail(NATTEN_ERR_INVALID, "problem is NULL");
     if (p->dtype < NATTEN_F32 || p->dtype > NATTEN_BF16) return fail(NATTEN_ERR_INVALID, "bad dtype %d", p->dtype);
     if (p->batch < 1 || p->heads_q < 1 || p->heads_kv < 1)
@@ -81,7 +83,7 @@ int make_prob(const natten_problem_t* p, bool fused, na::Prob& P) {
                         A.out, A.len, A.st);
         // The reference rule places the window at -1 only in this case (even
         // kernel equal to the axis, no dilation, non-causal); no defined result.
-        if (!A.causal && A.dil == 1 && (A.k % 2) == 0 && A.k == A.len)
+        if (!shifted_windows && !A.causal && A.dil == 1 && (A.k % 2) == 0 && A.k == A.len)
             return fail(NATTEN_ERR_UNSUPPORTED,
                         "axis %d: an even kernel (%d) equal to the axis length is not supported", a, A.k);
         P.kv *= A.k;
@@ -294,6 +296,70 @@ int natten_hip_varlen_backward(const natten_problem_t* p, const int32_t* lens, c
                              lse, to_lay(llse), nullptr, na::Lay{}, dq, to_lay(ldq), dk, to_lay(ldk), dv, to_lay(ldv),
                              delta, to_lay(ldelta), p->dtype, static_cast<hipStream_t>(stream), lens),
         "varlen_backward");
+}
+
+// Relative-position-bias ops: rank <= 2 (padded axis 0 of length and kernel
+// 1), stride 1, non-causal, equal head counts.
+static int make_rpb_prob(const natten_problem_t* p, na::Prob& P) {
+    int rc = make_prob(p, true, P, true);
+    if (rc) return rc;
+    if (P.rep != 1) return fail(NATTEN_ERR_INVALID, "relative-position-bias ops need heads_q == heads_kv");
+    if (P.ax[0].len != 1 || P.ax[0].k != 1)
+        return fail(NATTEN_ERR_INVALID, "relative-position-bias ops are 1-D or 2-D (axis 0 must be trivial)");
+    for (int a = 0; a < 3; ++a)
+        if (P.ax[a].st != 1 || P.ax[a].causal)
+            return fail(NATTEN_ERR_INVALID, "relative-position-bias ops need stride 1 and no causal mask");
+    return NATTEN_OK;
+}
+
+int natten_hip_rpb_qk_forward(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
+                              const natten_layout_t* lk, const void* rpb, void* attn, const natten_layout_t* la,
+                              void* stream) {
+    na::Prob P;
+    int rc = make_rpb_prob(p, P);
+    if (rc) return rc;
+    if (any_null({q, k, attn, lq, lk, la})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    return launch_status(na::rpb_qk(P, q, to_lay(lq), k, to_lay(lk), rpb, attn, to_lay(la), p->dtype,
+                                    static_cast<hipStream_t>(stream)),
+                         "rpb_qk_forward");
+}
+
+int natten_hip_rpb_av_forward(const natten_problem_t* p, const void* attn, const natten_layout_t* la, const void* v,
+                              const natten_layout_t* lv, void* out, const natten_layout_t* lo, void* stream) {
+    na::Prob P;
+    int rc = make_rpb_prob(p, P);
+    if (rc) return rc;
+    if (any_null({attn, v, out, la, lv, lo})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    return launch_status(na::rpb_av(P, attn, to_lay(la), v, to_lay(lv), out, to_lay(lo), p->dtype,
+                                    static_cast<hipStream_t>(stream)),
+                         "rpb_av_forward");
+}
+
+int natten_hip_rpb_qk_backward(const natten_problem_t* p, const void* dattn, const natten_layout_t* lda,
+                               const void* q, const natten_layout_t* lq, const void* k, const natten_layout_t* lk,
+                               void* dq, const natten_layout_t* ldq, void* dk, const natten_layout_t* ldk, void* drpb,
+                               void* stream) {
+    na::Prob P;
+    int rc = make_rpb_prob(p, P);
+    if (rc) return rc;
+    if (any_null({dattn, q, k, dq, dk, lda, lq, lk, ldq, ldk})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    return launch_status(na::rpb_qk_backward(P, dattn, to_lay(lda), q, to_lay(lq), k, to_lay(lk), dq, to_lay(ldq), dk,
+                                             to_lay(ldk), drpb, p->dtype, static_cast<hipStream_t>(stream)),
+                         "rpb_qk_backward");
+}
+
+int natten_hip_rpb_av_backward(const natten_problem_t* p, const void* dout, const natten_layout_t* ldo,
+                               const void* attn, const natten_layout_t* la, const void* v, const natten_layout_t* lv,
+                               void* dattn, const natten_layout_t* lda, void* dv, const natten_layout_t* ldv,
+                               void* stream) {
+    na::Prob P;
+    int rc = make_rpb_prob(p, P);
+    if (rc) return rc;
+    if (any_null({dout, attn, v, dattn, dv, ldo, la, lv, lda, ldv})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    return launch_status(na::rpb_av_backward(P, dout, to_lay(ldo), attn, to_lay(la), v, to_lay(lv), dattn,
+                                             to_lay(lda), dv, to_lay(ldv), p->dtype,
+                                             static_cast<hipStream_t>(stream)),
+                         "rpb_av_backward");
 }
 
 int natten_hip_neighborhood_map(const natten_problem_t* p, int64_t* flat, uint8_t* valid, void* stream) {

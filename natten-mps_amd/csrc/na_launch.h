@@ -30,6 +30,17 @@ hipError_t generic_av_backward(const Prob& p, int vec, const void* dout, Lay ldo
                                hipStream_t s);
 hipError_t neighborhood_map(const Prob& p, int64_t* flat, uint8_t* valid, hipStream_t s);
 
+// Relative-position-bias split ops (na_rpb.hip): padded axes 1 and 2 carry
+// the problem; rpb / drpb are contiguous [H, 2K1-1, 2K2-1] (rpb may be null).
+hipError_t rpb_qk(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* rpb, void* attn, Lay la,
+                  int dtype, hipStream_t s);
+hipError_t rpb_av(const Prob& p, const void* attn, Lay la, const void* v, Lay lv, void* out, Lay lo, int dtype,
+                  hipStream_t s);
+hipError_t rpb_qk_backward(const Prob& p, const void* da, Lay lda, const void* q, Lay lq, const void* k, Lay lk,
+                           void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, int dtype, hipStream_t s);
+hipError_t rpb_av_backward(const Prob& p, const void* dout, Lay ldo, const void* attn, Lay la, const void* v, Lay lv,
+                           void* da, Lay lda, void* dv, Lay ldv, int dtype, hipStream_t s);
+
 }  // namespace na
 
 // Launch with optional event timing (see na_profile.hip).

@@ -33,6 +33,10 @@ ENTRY_POINTS = (
     "natten_hip_neighborhood_map",
     "natten_hip_varlen_forward",
     "natten_hip_varlen_backward",
+    "natten_hip_rpb_qk_forward",
+    "natten_hip_rpb_av_forward",
+    "natten_hip_rpb_qk_backward",
+    "natten_hip_rpb_av_backward",
     "natten_hip_profile_enable",
     "natten_hip_profile_read",
 )
@@ -82,6 +86,10 @@ _SIGNATURES = {
     "natten_hip_neighborhood_map": ([_P(Problem), _VP, _VP, _VP], ctypes.c_int),
     "natten_hip_varlen_forward": ([_P(Problem), _VP] + [_VP, _LP] * 5 + [_VP], ctypes.c_int),
     "natten_hip_varlen_backward": ([_P(Problem), _VP] + [_VP, _LP] * 10 + [_VP], ctypes.c_int),
+    "natten_hip_rpb_qk_forward": ([_P(Problem)] + [_VP, _LP] * 2 + [_VP] + [_VP, _LP] + [_VP], ctypes.c_int),
+    "natten_hip_rpb_av_forward": ([_P(Problem)] + [_VP, _LP] * 3 + [_VP], ctypes.c_int),
+    "natten_hip_rpb_qk_backward": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP, _VP], ctypes.c_int),
+    "natten_hip_rpb_av_backward": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP], ctypes.c_int),
     "natten_hip_profile_enable": ([ctypes.c_int], ctypes.c_int),
     "natten_hip_profile_read": ([_P(KernelStat), ctypes.c_int, ctypes.c_int], ctypes.c_int),
 }

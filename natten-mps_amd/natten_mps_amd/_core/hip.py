@@ -446,6 +446,98 @@ def varlen_backward(rank: int, d_out, q, k, v, out, lse, sizes, kernel_size, dil
 
 
 # ---------------------------------------------------------------------------
+# relative-position-bias split ops (extras/allin1/functional.py:47-485):
+# NATTEN 0.17 shifted windows, 1-D and 2-D, spatial-first tensors
+# ---------------------------------------------------------------------------
+
+
+def _rpb_problem(rank, ref, heads, dim_qk, dim_v, kernel_size, dilation):
+    sp = tuple(ref.shape[1:1 + rank])
+    return _lib.problem(
+        batch=ref.shape[0], heads_q=heads, heads_kv=heads, dim_qk=dim_qk, dim_v=dim_v, dtype=_lib.dtype_code(ref),
+        length=sp, out_length=sp, kernel_size=kernel_size, dilation=dilation, stride=(1,) * rank,
+        is_causal=(False,) * rank, scale=None,
+    )
+
+
+def _rpb_table(rank, rpb, heads, kernel_size, dtype):
+    if rpb is None:
+        return None
+    want = (heads, *[2 * k - 1 for k in kernel_size])
+    if tuple(rpb.shape) != want:
+        raise ValueError(f"rpb must have shape {want}, got {tuple(rpb.shape)}.")
+    return rpb.to(dtype).contiguous()
+
+
+def rpb_qk_forward(rank: int, q, k, rpb, kernel_size, dilation):
+    """Logits ``[B, *sp, H, prod(kernel)]`` = q . k + rpb (unscaled), -inf at
+    invalid neighbours."""
+    _on_device(q, k, rpb)
+    _same_dtype(q, k)
+    q, k = _inner(q), _inner(k)
+    H = q.shape[-2]
+    table = _rpb_table(rank, rpb, H, kernel_size, q.dtype)
+    prob = _rpb_problem(rank, q, H, q.shape[-1], q.shape[-1], kernel_size, dilation)
+    kv = 1
+    for x in kernel_size:
+        kv *= x
+    attn = torch.empty((*q.shape[:-1], kv), dtype=q.dtype, device=q.device)
+    L = lambda t: _byref(_lib.layout(t, rank, 1))  # noqa: E731
+    rc = _launch(q.device, _lib.load().natten_hip_rpb_qk_forward, _byref(prob), _lib.ptr(q), L(q), _lib.ptr(k),
+                 L(k), _lib.ptr(table), _lib.ptr(attn), L(attn), _raw_stream(q.device))
+    _lib.check(rc, "rpb_qk_forward")
+    return attn
+
+
+def rpb_av_forward(rank: int, attn, v, kernel_size, dilation):
+    _on_device(attn, v)
+    attn = _inner(attn.to(v.dtype))
+    v = _inner(v)
+    prob = _rpb_problem(rank, v, v.shape[-2], v.shape[-1], v.shape[-1], kernel_size, dilation)
+    out = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    L = lambda t: _byref(_lib.layout(t, rank, 1))  # noqa: E731
+    rc = _launch(v.device, _lib.load().natten_hip_rpb_av_forward, _byref(prob), _lib.ptr(attn), L(attn),
+                 _lib.ptr(v), L(v), _lib.ptr(out), L(out), _raw_stream(v.device))
+    _lib.check(rc, "rpb_av_forward")
+    return out
+
+
+def rpb_qk_backward(rank: int, d_attn, q, k, with_rpb: bool, kernel_size, dilation):
+    """``(dq, dk, drpb)``; drpb is None when the op had no bias."""
+    _on_device(d_attn, q, k)
+    d_attn = _inner(d_attn.to(q.dtype))
+    q, k = _inner(q), _inner(k)
+    H = q.shape[-2]
+    prob = _rpb_problem(rank, q, H, q.shape[-1], q.shape[-1], kernel_size, dilation)
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    drpb = (torch.empty((H, *[2 * x - 1 for x in kernel_size]), dtype=q.dtype, device=q.device)
+            if with_rpb else None)
+    L = lambda t: _byref(_lib.layout(t, rank, 1))  # noqa: E731
+    rc = _launch(q.device, _lib.load().natten_hip_rpb_qk_backward, _byref(prob), _lib.ptr(d_attn), L(d_attn),
+                 _lib.ptr(q), L(q), _lib.ptr(k), L(k), _lib.ptr(dq), L(dq), _lib.ptr(dk), L(dk), _lib.ptr(drpb),
+                 _raw_stream(q.device))
+    _lib.check(rc, "rpb_qk_backward")
+    return dq, dk, drpb
+
+
+def rpb_av_backward(rank: int, d_out, attn, v, kernel_size, dilation):
+    _on_device(d_out, attn, v)
+    d_out = _inner(d_out.to(v.dtype))
+    attn = _inner(attn.to(v.dtype))
+    v = _inner(v)
+    prob = _rpb_problem(rank, v, v.shape[-2], v.shape[-1], v.shape[-1], kernel_size, dilation)
+    d_attn = torch.empty(attn.shape, dtype=attn.dtype, device=attn.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    L = lambda t: _byref(_lib.layout(t, rank, 1))  # noqa: E731
+    rc = _launch(v.device, _lib.load().natten_hip_rpb_av_backward, _byref(prob), _lib.ptr(d_out), L(d_out),
+                 _lib.ptr(attn), L(attn), _lib.ptr(v), L(v), _lib.ptr(d_attn), L(d_attn), _lib.ptr(dv), L(dv),
+                 _raw_stream(v.device))
+    _lib.check(rc, "rpb_av_backward")
+    return d_attn, dv
+
+
+# ---------------------------------------------------------------------------
 # rank-specific names (the backend-module contract)
 # ---------------------------------------------------------------------------
 

@@ -13,6 +13,8 @@ def get_support_matrix() -> dict:
             "backward": {"na1d": True, "na2d": True, "na3d": True, "split_qk_av": True},
             "varlen": {"na1d": True, "na2d": True, "na3d": True},
             "fusion": {"na1d": True, "na2d": True, "na3d": True},
+            "extras_allin1": {"na1d_qk_rpb": True, "na1d_av_fused": True, "na2d_qk_rpb": True,
+                              "na2d_av_fused": True},
             "constraints": [
                 "Requires a ROCm GPU (gfx950 / MI355X) and the built libnatten_hip.so.",
                 "float32, float16 and bfloat16; head dims up to 256 (q/k and v may differ).",

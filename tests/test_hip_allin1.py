@@ -1,0 +1,145 @@
+"""extras/allin1 on the 'hip' backend (natten_hip_rpb_*) against the CPU
+oracle (oracle/allin1.py): QK+RPB logits, AV, and the gradients of q, k,
+rpb, attn and v, for 1-D and 2-D, odd and even kernels, with and without
+dilation and bias.
+
+Tolerances: fp32 1e-5 (logits, outputs, dq, dk, dattn, dv), 1e-4 for the
+bias gradient (a sum over every query of the batch); bf16 logits/outputs
+2e-2 against the oracle in fp32 on the same rounded inputs.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle.allin1 as A
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0") if torch.cuda.is_available() else None
+
+
+def _rand(shape, seed, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32).to(dtype)
+
+
+CASES_1D = [(2, 24, 3, 16, 5, 1), (1, 33, 2, 32, 7, 3), (2, 9, 2, 8, 2, 2), (1, 20, 4, 16, 4, 2), (2, 12, 2, 8, 3, 4)]
+CASES_2D = [(2, 10, 12, 2, 16, 3, 1), (1, 14, 11, 3, 32, 5, 2), (1, 9, 9, 2, 8, 4, 2), (1, 7, 8, 2, 16, 7, 1)]
+
+
+@pytest.mark.parametrize("with_rpb", [True, False])
+@pytest.mark.parametrize("case", CASES_1D, ids=lambda c: "B{}L{}H{}D{}K{}d{}".format(*c))
+def test_rpb_1d_forward_backward(case, with_rpb):
+    from natten_mps_amd.extras.allin1 import na1d_av_fused, na1d_qk_rpb
+
+    B, L, H, D, K, d = case
+    q, k, v, go = (_rand((B, L, H, D), s) for s in (1, 2, 3, 4))
+    rpb = _rand((H, 2 * K - 1), 5) if with_rpb else None
+    ga = _rand((B, L, H, K), 6)
+    # logits and their gradients
+    leaves = [t.to(DEV).requires_grad_(True) for t in (q, k)]
+    r_dev = rpb.to(DEV).requires_grad_(True) if with_rpb else None
+    logits = na1d_qk_rpb(leaves[0], leaves[1], r_dev, K, d, scale=0.25)
+    ref_leaves = [t.double().requires_grad_(True) for t in (q, k)]
+    r_ref = rpb.double().requires_grad_(True) if with_rpb else None
+    ref = A.na1d_qk_rpb(ref_leaves[0], ref_leaves[1], r_ref, K, d, scale=0.25)
+    torch.testing.assert_close(logits.cpu().double(), ref, atol=1e-5, rtol=1e-5)
+    fin = torch.isfinite(ref)
+    ga_masked = torch.where(fin, ga.double(), torch.zeros((), dtype=torch.float64))
+    (logits * ga_masked.float().to(DEV)).masked_fill(~fin.to(DEV), 0).sum().backward()
+    (ref.masked_fill(~fin, 0) * ga_masked).sum().backward()
+    for name, a, b in (("q", leaves[0], ref_leaves[0]), ("k", leaves[1], ref_leaves[1])):
+        torch.testing.assert_close(a.grad.cpu().double(), b.grad, atol=1e-5, rtol=1e-5, msg=lambda m: f"d{name}: {m}")
+    if with_rpb:
+        torch.testing.assert_close(r_dev.grad.cpu().double(), r_ref.grad, atol=1e-4, rtol=1e-4)
+    # AV and its gradients
+    attn = ref.detach().float().softmax(-1)
+    a_dev, v_dev = attn.to(DEV).requires_grad_(True), v.to(DEV).requires_grad_(True)
+    out = na1d_av_fused(a_dev, v_dev, K, d)
+    a_ref, v_ref = attn.double().requires_grad_(True), v.double().requires_grad_(True)
+    out_ref = A.av_1d(a_ref, v_ref, K, d)
+    torch.testing.assert_close(out.cpu().double(), out_ref, atol=1e-5, rtol=1e-5)
+    out.backward(go.to(DEV))
+    out_ref.backward(go.double())
+    torch.testing.assert_close(a_dev.grad.cpu().double(), a_ref.grad, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(v_dev.grad.cpu().double(), v_ref.grad, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("case", CASES_2D, ids=lambda c: "B{}X{}Y{}H{}D{}K{}d{}".format(*c))
+def test_rpb_2d_forward_backward(case):
+    from natten_mps_amd.extras.allin1 import na2d_av_fused, na2d_qk_rpb
+
+    B, X, Y, H, D, K, d = case
+    q, k, v, go = (_rand((B, X, Y, H, D), s) for s in (7, 8, 9, 10))
+    rpb = _rand((H, 2 * K - 1, 2 * K - 1), 11)
+    ga = _rand((B, X, Y, H, K * K), 12)
+    leaves = [t.to(DEV).requires_grad_(True) for t in (q, k, rpb)]
+    logits = na2d_qk_rpb(leaves[0], leaves[1], leaves[2], K, d)
+    ref_leaves = [t.double().requires_grad_(True) for t in (q, k, rpb)]
+    ref = A.na2d_qk_rpb(*ref_leaves, K, d)
+    torch.testing.assert_close(logits.cpu().double(), ref, atol=1e-5, rtol=1e-5)
+    fin = torch.isfinite(ref)
+    ga_masked = torch.where(fin, ga.double(), torch.zeros((), dtype=torch.float64))
+    (logits * ga_masked.float().to(DEV)).masked_fill(~fin.to(DEV), 0).sum().backward()
+    (ref.masked_fill(~fin, 0) * ga_masked).sum().backward()
+    for name, a, b, tol in (("q", leaves[0], ref_leaves[0], 1e-5), ("k", leaves[1], ref_leaves[1], 1e-5),
+                            ("rpb", leaves[2], ref_leaves[2], 1e-4)):
+        torch.testing.assert_close(a.grad.cpu().double(), b.grad, atol=tol, rtol=tol, msg=lambda m: f"d{name}: {m}")
+    attn = ref.detach().float().softmax(-1)
+    a_dev, v_dev = attn.to(DEV).requires_grad_(True), v.to(DEV).requires_grad_(True)
+    out = na2d_av_fused(a_dev, v_dev, K, d)
+    a_ref, v_ref = attn.double().requires_grad_(True), v.double().requires_grad_(True)
+    out_ref = A.av_2d(a_ref, v_ref, K, d)
+    torch.testing.assert_close(out.cpu().double(), out_ref, atol=1e-5, rtol=1e-5)
+    out.backward(go.to(DEV))
+    out_ref.backward(go.double())
+    torch.testing.assert_close(a_dev.grad.cpu().double(), a_ref.grad, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(v_dev.grad.cpu().double(), v_ref.grad, atol=1e-5, rtol=1e-5)
+
+
+def test_rpb_bias_gradient_counts_masked_entries():
+    """The bias enters every logit, masked or not, so its gradient sums the
+    upstream gradient over every entry (even kernel, dilation: some masked)."""
+    from natten_mps_amd.extras.allin1 import na1d_qk_rpb
+
+    B, L, H, D, K, d = 1, 5, 1, 4, 2, 2
+    q, k = _rand((B, L, H, D), 13), _rand((B, L, H, D), 14)
+    rpb = torch.zeros(H, 2 * K - 1, device=DEV, requires_grad=True)
+    logits = na1d_qk_rpb(q.to(DEV), k.to(DEV), rpb, K, d)
+    assert torch.isinf(logits).any()
+    logits.backward(torch.ones_like(logits))
+    r = rpb.detach().clone().cpu().double().requires_grad_(True)
+    A.na1d_qk_rpb(q.double(), k.double(), r, K, d).backward(torch.ones(B, L, H, K, dtype=torch.float64))
+    torch.testing.assert_close(rpb.grad.cpu().double(), r.grad, atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rpb_half_precision(dtype):
+    from natten_mps_amd.extras.allin1 import na2d_av_fused, na2d_qk_rpb
+
+    q, k, v = (_rand((2, 12, 12, 2, 32), s, dtype) for s in (15, 16, 17))
+    rpb = _rand((2, 9, 9), 18, dtype)
+    logits = na2d_qk_rpb(q.to(DEV), k.to(DEV), rpb.to(DEV), 5, 2, scale=32 ** -0.5)
+    ref = A.na2d_qk_rpb(q.float(), k.float(), rpb.float(), 5, 2, scale=32 ** -0.5)
+    torch.testing.assert_close(logits.cpu().float(), ref, atol=2e-2, rtol=2e-2)
+    attn = ref.softmax(-1)
+    out = na2d_av_fused(attn.to(dtype).to(DEV), v.to(DEV), 5, 2)
+    torch.testing.assert_close(out.cpu().float(), A.av_2d(attn.to(dtype).float(), v.float(), 5, 2), atol=2e-2,
+                               rtol=2e-2)
+
+
+def test_rpb_validation():
+    from natten_mps_amd.extras.allin1 import na1d_qk_rpb, na2d_qk_rpb
+    from natten_mps_amd.extras.allin1.functional import natten2dqkrpb
+
+    q = torch.randn(1, 6, 2, 4, device=DEV)
+    with pytest.raises(ValueError, match="kernel_size \\* dilation must be <= axis length"):
+        na1d_qk_rpb(q, q, None, 4, 2)
+    with pytest.raises(ValueError, match="4D"):
+        na1d_qk_rpb(q[0], q[0], None, 3)
+    q2 = torch.randn(1, 8, 8, 2, 4, device=DEV)
+    with pytest.raises(ValueError, match="square kernels"):
+        natten2dqkrpb(q2, q2, None, (3, 5), 1)
+    with pytest.raises(ValueError, match="rpb must have shape"):
+        na2d_qk_rpb(q2, q2, torch.zeros(2, 5, device=DEV), 3)
