@@ -545,6 +545,18 @@ __device__ __forceinline__ void store_rows(T* __restrict__ g, long long off, int
 
 __device__ __forceinline__ int kv_head(const TileShape& ts, int h) { return ts.rep.d == 1 ? h : fdiv(h, ts.rep); }
 
+// Operand layout groups a kernel instance assumes (chosen by the host).
+// kLayOne: every 16-bit operand has q's layout and every fp32 row operand
+// lse's.  kLayTwo: the query-side 16-bit operands (q, out, dO, dq) share q's
+// layout, the key-side ones (k, v, dk, dv) k's, the fp32 rows lse's (GQA).
+// kLayGeneral: each operand its own.  Fewer distinct layouts keep fewer
+// scalar registers live, which at head dim 32 removes the SGPR spills.
+constexpr int kLayGeneral = 0, kLayOne = 1, kLayTwo = 2;
+
+// Head dim 32 runs 4 waves per SIMD (at most 128 VGPRs); saying so lets the
+// register allocator trade VGPRs for SGPRs instead of spilling SGPRs.
+#define NA_OCCUPANCY(D) __attribute__((amdgpu_waves_per_eu((D) == 32 ? 4 : 1)))
+
 // Walk of a workgroup over its (batch, head) pairs and axis-0 slices.  The
 // loads of the next slice are issued as soon as the current one is no longer
 // read, and the very first right after decoding the tile, so that the
@@ -579,11 +591,14 @@ __device__ __forceinline__ int slice_pos(const Prob& p, const Block& k, int u0) 
 // Online softmax over groups of up to 4 chunks (one max reduction and one
 // rescale per group).
 // ---------------------------------------------------------------------------
-template <typename T, int D>
-__global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq,
-                                                  const T* __restrict__ kg, LayK lk, const T* __restrict__ vg,
-                                                  LayK lv, T* __restrict__ out, LayK lo, float* __restrict__ lse,
-                                                  LayK ll) {
+template <typename T, int D, int LAY>
+__global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_fwd_mfma(
+    Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
+    LayK lk_in, const T* __restrict__ vg, LayK lv_in, T* __restrict__ out, LayK lo_in, float* __restrict__ lse,
+    LayK ll) {
+    const LayK& lk = LAY == kLayOne ? lq : lk_in;
+    const LayK& lv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : lv_in;
+    const LayK& lo = LAY == kLayGeneral ? lo_in : lq;
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr bool KEY_SIDE = false;
     T* Ks = reinterpret_cast<T*>(smem);
@@ -694,14 +709,19 @@ __global__ __launch_bounds__(256) void k_fwd_mfma(Prob p, TileShape ts, const in
 // dq = scale * sum_k P (dP - delta) k, with P = exp(scale q.k - lse) and
 // dP = dO . v.  The dP product starts from -delta.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
-__global__ __launch_bounds__(256) void k_bwd_q_mfma(Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq,
-                                                    const T* __restrict__ kg, LayK lk, const T* __restrict__ vg,
-                                                    LayK lv, const T* __restrict__ o, LayK lo,
-                                                    const T* __restrict__ dout, LayK ldo,
-                                                    const float* __restrict__ lse, LayK ll,
-                                                    const float* __restrict__ dlse, LayK ldl, T* __restrict__ dq,
-                                                    LayK ldq, float* __restrict__ delta, LayK lde) {
+template <typename T, int D, int LAY>
+__global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_bwd_q_mfma(
+    Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
+    LayK lk_in, const T* __restrict__ vg, LayK lv_in, const T* __restrict__ o, LayK lo_in,
+    const T* __restrict__ dout, LayK ldo_in, const float* __restrict__ lse, LayK ll, const float* __restrict__ dlse,
+    LayK ldl_in, T* __restrict__ dq, LayK ldq_in, float* __restrict__ delta, LayK lde_in) {
+    const LayK& lk = LAY == kLayOne ? lq : lk_in;
+    const LayK& lv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : lv_in;
+    const LayK& lo = LAY == kLayGeneral ? lo_in : lq;
+    const LayK& ldo = LAY == kLayGeneral ? ldo_in : lq;
+    const LayK& ldq = LAY == kLayGeneral ? ldq_in : lq;
+    const LayK& ldl = LAY == kLayGeneral ? ldl_in : ll;
+    const LayK& lde = LAY == kLayGeneral ? lde_in : ll;
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr bool KEY_SIDE = false;
     T* Ks = reinterpret_cast<T*>(smem);
@@ -824,13 +844,18 @@ __device__ __forceinline__ void stage_scalars(const Prob& p, const Block& k, con
     }
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void k_bwd_kv_mfma(Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq,
-                                                     const T* __restrict__ kg, LayK lk, const T* __restrict__ vg,
-                                                     LayK lv, const T* __restrict__ dout, LayK ldo,
-                                                     const float* __restrict__ lse, LayK ll,
-                                                     const float* __restrict__ delta, LayK lde,
-                                                     T* __restrict__ dk, LayK ldk, T* __restrict__ dv, LayK ldv) {
+template <typename T, int D, int LAY>
+__global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_bwd_kv_mfma(
+    Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
+    LayK lk_in, const T* __restrict__ vg, LayK lv_in, const T* __restrict__ dout, LayK ldo_in,
+    const float* __restrict__ lse, LayK ll, const float* __restrict__ delta, LayK lde_in, T* __restrict__ dk,
+    LayK ldk_in, T* __restrict__ dv, LayK ldv_in) {
+    const LayK& lk = LAY == kLayOne ? lq : lk_in;
+    const LayK& lv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : lv_in;
+    const LayK& ldk = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : ldk_in;
+    const LayK& ldv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : ldv_in;
+    const LayK& ldo = LAY == kLayGeneral ? ldo_in : lq;
+    const LayK& lde = LAY == kLayGeneral ? lde_in : ll;
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr bool KEY_SIDE = true;
     const int slots = ts.slots;
@@ -1209,19 +1234,78 @@ hipError_t allow_lds(K kernel, size_t bytes) {
                                static_cast<int>(bytes));
 }
 
-template <typename T, int D>
+bool same_lay(const Lay& a, const Lay& b) {
+    return a.b == b.b && a.h == b.h && a.s0 == b.s0 && a.s1 == b.s1 && a.s2 == b.s2;
+}
+
+bool all_same(std::initializer_list<Lay> g) {
+    for (const Lay& l : g)
+        if (!same_lay(l, *g.begin())) return false;
+    return true;
+}
+
+// Layout group for a launch from its query-side and key-side 16-bit operands
+// and its fp32 row operands (first of each list is the one the kernel reads).
+int layout_group(std::initializer_list<Lay> qside, std::initializer_list<Lay> kvside,
+                 std::initializer_list<Lay> rows) {
+    if (!all_same(qside) || !all_same(kvside) || !all_same(rows)) return kLayGeneral;
+    return same_lay(*qside.begin(), *kvside.begin()) ? kLayOne : kLayTwo;
+}
+
+template <typename T, int D, int LAY>
 hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
                       Lay lo, float* lse, Lay ll, hipStream_t s) {
     TileShape ts{};
     if (!choose_tile(p, kForward, D, ts)) return hipErrorInvalidValue;
     const size_t shm = lds_bytes(kForward, ts.slots, D);
-    hipError_t e = allow_lds(k_fwd_mfma<T, D>, shm);
+    hipError_t e = allow_lds(k_fwd_mfma<T, D, LAY>, shm);
     if (e != hipSuccess) return e;
-    fit_h_per(p, ts, resident_blocks(k_fwd_mfma<T, D>, 64 * ts.waves, shm));
+    fit_h_per(p, ts, resident_blocks(k_fwd_mfma<T, D, LAY>, 64 * ts.waves, shm));
     const int* geo = geometry_table(p, ts, false, s);
-    NA_LAUNCH("na_fwd_mfma", (k_fwd_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, ts))),
-              dim3(64 * ts.waves), shm, s, p, ts, geo, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
-              (T*)o, to_k(lo), lse, to_k(ll));
+    NA_LAUNCH("na_fwd_mfma", (k_fwd_mfma<T, D, LAY>), dim3(static_cast<unsigned>(grid_blocks(p, ts))),
+              dim3(64 * ts.waves), shm, s, p, ts, geo, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v,
+              to_k(lv), (T*)o, to_k(lo), lse, to_k(ll));
+    return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
+                      Lay lo, float* lse, Lay ll, hipStream_t s) {
+    switch (layout_group({lq, lo}, {lk, lv}, {ll})) {
+        case kLayOne:
+            return launch_fwd<T, D, kLayOne>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
+        case kLayTwo:
+            return launch_fwd<T, D, kLayTwo>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
+        default:
+            return launch_fwd<T, D, kLayGeneral>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
+    }
+}
+
+template <typename T, int D, int LAY>
+hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
+                      const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
+                      const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
+                      float* delta, Lay lde, hipStream_t s) {
+    TileShape tq{}, tk{};
+    if (!choose_tile(p, kBackwardQ, D, tq) || !choose_tile(p, kBackwardKV, D, tk)) return hipErrorInvalidValue;
+    const size_t shq = lds_bytes(kBackwardQ, tq.slots, D), shk = lds_bytes(kBackwardKV, tk.slots, D);
+    hipError_t e = allow_lds(k_bwd_q_mfma<T, D, LAY>, shq);
+    if (e == hipSuccess) e = allow_lds(k_bwd_kv_mfma<T, D, LAY>, shk);
+    if (e != hipSuccess) return e;
+    fit_h_per(p, tq, resident_blocks(k_bwd_q_mfma<T, D, LAY>, 64 * tq.waves, shq));
+    fit_h_per(p, tk, resident_blocks(k_bwd_kv_mfma<T, D, LAY>, 64 * tk.waves, shk));
+    const int* gq = geometry_table(p, tq, false, s);
+    const int* gk = geometry_table(p, tk, true, s);
+    NA_LAUNCH("na_bwd_q_mfma", (k_bwd_q_mfma<T, D, LAY>), dim3(static_cast<unsigned>(grid_blocks(p, tq))),
+              dim3(64 * tq.waves), shq, s, p, tq, gq, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v,
+              to_k(lv), (const T*)o, to_k(lo), (const T*)dout, to_k(ldo), lse, to_k(ll), dlse, to_k(ldl), (T*)dq,
+              to_k(ldq), delta, to_k(lde));
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    NA_LAUNCH("na_bwd_kv_mfma", (k_bwd_kv_mfma<T, D, LAY>), dim3(static_cast<unsigned>(grid_blocks(p, tk))),
+              dim3(64 * tk.waves), shk, s, p, tk, gk, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v,
+              to_k(lv), (const T*)dout, to_k(ldo), lse, to_k(ll), (const float*)delta, to_k(lde), (T*)dk, to_k(ldk),
+              (T*)dv, to_k(ldv));
     return hipGetLastError();
 }
 
@@ -1230,27 +1314,20 @@ hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
                       const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                       const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
                       float* delta, Lay lde, hipStream_t s) {
-    TileShape tq{}, tk{};
-    if (!choose_tile(p, kBackwardQ, D, tq) || !choose_tile(p, kBackwardKV, D, tk)) return hipErrorInvalidValue;
-    const size_t shq = lds_bytes(kBackwardQ, tq.slots, D), shk = lds_bytes(kBackwardKV, tk.slots, D);
-    hipError_t e = allow_lds(k_bwd_q_mfma<T, D>, shq);
-    if (e == hipSuccess) e = allow_lds(k_bwd_kv_mfma<T, D>, shk);
-    if (e != hipSuccess) return e;
-    fit_h_per(p, tq, resident_blocks(k_bwd_q_mfma<T, D>, 64 * tq.waves, shq));
-    fit_h_per(p, tk, resident_blocks(k_bwd_kv_mfma<T, D>, 64 * tk.waves, shk));
-    const int* gq = geometry_table(p, tq, false, s);
-    const int* gk = geometry_table(p, tk, true, s);
-    NA_LAUNCH("na_bwd_q_mfma", (k_bwd_q_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tq))),
-              dim3(64 * tq.waves), shq, s, p, tq, gq, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
-              (const T*)o, to_k(lo), (const T*)dout, to_k(ldo), lse, to_k(ll), dlse, to_k(ldl), (T*)dq, to_k(ldq), delta,
-              to_k(lde));
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    NA_LAUNCH("na_bwd_kv_mfma", (k_bwd_kv_mfma<T, D>), dim3(static_cast<unsigned>(grid_blocks(p, tk))),
-              dim3(64 * tk.waves), shk, s, p, tk, gk, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv),
-              (const T*)dout, to_k(ldo), lse, to_k(ll), (const float*)delta, to_k(lde), (T*)dk, to_k(ldk), (T*)dv,
-              to_k(ldv));
-    return hipGetLastError();
+    // without dlse its layout is never read
+    const int g = layout_group({lq, lo, ldo, ldq}, {lk, lv, ldk, ldv}, {ll, lde, dlse ? ldl : ll});
+#define NA_BWD_LAY(L)                                                                                          \
+    return launch_bwd<T, D, L>(p, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl, dq, ldq, dk, ldk, dv, \
+                               ldv, delta, lde, s)
+    switch (g) {
+        case kLayOne:
+            NA_BWD_LAY(kLayOne);
+        case kLayTwo:
+            NA_BWD_LAY(kLayTwo);
+        default:
+            NA_BWD_LAY(kLayGeneral);
+    }
+#undef NA_BWD_LAY
 }
 
 }  // namespace

@@ -187,6 +187,37 @@ def test_noncontiguous_views_from_module_layout():
     _close(xd.grad.cpu(), xr.grad, torch.float32, "dx")
 
 
+@pytest.mark.parametrize("dim", [32, 64])
+@pytest.mark.parametrize("layout", ["one", "two", "general"])
+def test_mfma_layout_groups(layout, dim):
+    """The bf16 tile kernels come in three instances by operand layout: all
+    16-bit operands alike ("one"), query side and key side each alike (GQA,
+    "two"), and per operand ("general": q, k, v strided views of one qkv
+    tensor, out contiguous).  Each against the oracle in fp32 on the same
+    rounded inputs."""
+    from natten_mps_amd import functional as F
+
+    B, X, Y = 2, 12, 13
+    hq, hkv = (4, 2) if layout == "two" else (2, 2)
+    (do,) = _inputs(44, [(B, X, Y, hq, dim)], torch.bfloat16)
+    if layout == "general":
+        (x,) = _inputs(43, [(B, X, Y, 3, hq, dim)], torch.bfloat16)
+        xd = x.to(DEV).requires_grad_(True)
+        leaves = xd.permute(3, 0, 1, 2, 4, 5).unbind(0)
+        out = F.na2d(*leaves, kernel_size=5, dilation=(2, 1))
+        out.backward(do.to(DEV))
+        got = [xd.grad.cpu()[:, :, :, i] for i in range(3)]
+        qkv = [t.cpu() for t in x.unbind(3)]
+    else:
+        qkv = _inputs(45, [(B, X, Y, hq, dim), (B, X, Y, hkv, dim), (B, X, Y, hkv, dim)], torch.bfloat16)
+        out, got = _hip_fwd_bwd(F.na2d, qkv, do, kernel_size=5, dilation=(2, 1))
+    ref, rgrads = _oracle_fwd_bwd(2, qkv, do, (5, 5), (1, 1), (2, 1), (False, False))
+    _close(out.detach().cpu(), ref, torch.bfloat16, "out")
+    for n, a, b in zip(("dq", "dk", "dv"), got, rgrads):
+        assert a.shape == b.shape
+        _close(a, b, torch.bfloat16, n)
+
+
 def test_dim_v_differs_from_dim_qk():
     from natten_mps_amd._core import hip
 
