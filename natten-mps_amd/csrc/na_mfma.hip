@@ -553,9 +553,13 @@ __device__ __forceinline__ int kv_head(const TileShape& ts, int h) { return ts.r
 // scalar registers live, which at head dim 32 removes the SGPR spills.
 constexpr int kLayGeneral = 0, kLayOne = 1, kLayTwo = 2;
 
-// Head dim 32 runs 4 waves per SIMD (at most 128 VGPRs); saying so lets the
-// register allocator trade VGPRs for SGPRs instead of spilling SGPRs.
-#define NA_OCCUPANCY(D) __attribute__((amdgpu_waves_per_eu((D) == 32 ? 4 : 1)))
+// Waves per SIMD a head-dim-32 instance is built for (4: at most 128 VGPRs,
+// 5: at most 96).  Saying so lets the register allocator trade VGPRs for
+// SGPRs instead of spilling SGPRs, and the backward instances without the
+// per-chunk column pattern fit 5 waves.  WIDE instances handle unions whose
+// rows exceed 32 slots, where the column mask changes from chunk to chunk;
+// keeping them apart leaves the common instance its smaller register need.
+#define NA_OCCUPANCY(D, W) __attribute__((amdgpu_waves_per_eu((D) == 32 ? (W) : 1)))
 
 // Walk of a workgroup over its (batch, head) pairs and axis-0 slices.  The
 // loads of the next slice are issued as soon as the current one is no longer
@@ -591,8 +595,8 @@ __device__ __forceinline__ int slice_pos(const Prob& p, const Block& k, int u0) 
 // Online softmax over groups of up to 4 chunks (one max reduction and one
 // rescale per group).
 // ---------------------------------------------------------------------------
-template <typename T, int D, int LAY>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_fwd_mfma(
+template <typename T, int D, int LAY, bool WIDE>
+__global__ __launch_bounds__(256) NA_OCCUPANCY(D, 4) void k_fwd_mfma(
     Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
     LayK lk_in, const T* __restrict__ vg, LayK lv_in, T* __restrict__ out, LayK lo_in, float* __restrict__ lse,
     LayK ll) {
@@ -617,9 +621,8 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_fwd_mfma(
                          Vs, wave);
     }
     const Lane ln = lane_item(p, ts, blk, wave, col, false);
-    const bool wide = ts.rowshift > 5;  // column pattern changes from chunk to chunk
     f32x4_t cb[2];
-    column_bias(ln, ts.rowshift, 0, grp, cb);
+    if constexpr (!WIDE) column_bias(ln, ts.rowshift, 0, grp, cb);
     const uint4 ones = make_uint4(Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes);
     const float sc2 = p.scale * kLog2e;
 
@@ -640,8 +643,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_fwd_mfma(
         __syncthreads();
         if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
-            const auto chunks = [&](auto wide_tag) {
-                constexpr bool WIDE = decltype(wide_tag)::value;
+            const auto chunks = [&](auto) {
                 for (int c = wg.c0; c <= wg.c1; c += 4) {
                     const int n = min(4, wg.c1 - c + 1);
                     f32x4_t s[4][2];
@@ -684,10 +686,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_fwd_mfma(
                     }
                 }
             };
-            if (wide)
-                chunks(std::true_type{});
-            else
-                chunks(std::false_type{});
+            chunks(std::integral_constant<bool, WIDE>{});
         }
         more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
@@ -709,8 +708,8 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_fwd_mfma(
 // dq = scale * sum_k P (dP - delta) k, with P = exp(scale q.k - lse) and
 // dP = dO . v.  The dP product starts from -delta.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int LAY>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_bwd_q_mfma(
+template <typename T, int D, int LAY, bool WIDE>
+__global__ __launch_bounds__(256) NA_OCCUPANCY(D, (WIDE ? 4 : 5)) void k_bwd_q_mfma(
     Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
     LayK lk_in, const T* __restrict__ vg, LayK lv_in, const T* __restrict__ o, LayK lo_in,
     const T* __restrict__ dout, LayK ldo_in, const float* __restrict__ lse, LayK ll, const float* __restrict__ dlse,
@@ -741,9 +740,8 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_bwd_q_mfma(
     }
     const Lane ln = lane_item(p, ts, blk, wave, col, false);
     const float sc2 = p.scale * kLog2e;
-    const bool wide = ts.rowshift > 5;
     f32x4_t cb[2];
-    column_bias(ln, ts.rowshift, 0, grp, cb);
+    if constexpr (!WIDE) column_bias(ln, ts.rowshift, 0, grp, cb);
 
     uint4 qf[D / 32], gf[D / 32];
     f32x4_t acc[D / 16], nd[2];
@@ -777,8 +775,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_bwd_q_mfma(
         __syncthreads();
         if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
-            const auto chunks = [&](auto wide_tag) {
-                constexpr bool WIDE = decltype(wide_tag)::value;
+            const auto chunks = [&](auto) {
                 for (int c = wg.c0; c <= wg.c1; ++c) {
                     f32x4_t s[2], dp[2];
                     if constexpr (!WIDE) {
@@ -798,10 +795,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_bwd_q_mfma(
                     accumulate_chunk<T, D>(Ks, c, lane, pack8<T>(s), acc);
                 }
             };
-            if (wide)
-                chunks(std::true_type{});
-            else
-                chunks(std::false_type{});
+            chunks(std::integral_constant<bool, WIDE>{});
         }
         more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
@@ -844,8 +838,8 @@ __device__ __forceinline__ void stage_scalars(const Prob& p, const Block& k, con
     }
 }
 
-template <typename T, int D, int LAY>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_bwd_kv_mfma(
+template <typename T, int D, int LAY, bool WIDE>
+__global__ __launch_bounds__(256) NA_OCCUPANCY(D, (WIDE ? 4 : 5)) void k_bwd_kv_mfma(
     Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
     LayK lk_in, const T* __restrict__ vg, LayK lv_in, const T* __restrict__ dout, LayK ldo_in,
     const float* __restrict__ lse, LayK ll, const float* __restrict__ delta, LayK lde_in, T* __restrict__ dk,
@@ -880,9 +874,8 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_bwd_kv_mfma(
     if (threadIdx.x < 8) NL[slots + threadIdx.x] = -INFINITY;
     const Lane ln = lane_item(p, ts, blk, wave, col, true);
     const float sc2 = p.scale * kLog2e;
-    const bool wide = ts.rowshift > 5;
     f32x4_t cb[2];
-    column_bias(ln, ts.rowshift, 0, grp, cb);
+    if constexpr (!WIDE) column_bias(ln, ts.rowshift, 0, grp, cb);
     stage_scalars<T>(p, blk, ts, w.b, w.h * rep, slice_pos(p, blk, 0), lse, ll, delta, lde, NL, ND);
 
     uint4 kf[D / 32], vf[D / 32];
@@ -904,8 +897,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_bwd_kv_mfma(
         __syncthreads();
         if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
-            const auto chunks = [&](auto wide_tag) {
-                constexpr bool WIDE = decltype(wide_tag)::value;
+            const auto chunks = [&](auto) {
                 for (int c = wg.c0; c <= wg.c1; ++c) {
                     const int s0 = 32 * c + 8 * grp;
                     const f32x4_t ndc[2] = {*reinterpret_cast<const f32x4_t*>(ND + s0),
@@ -933,10 +925,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D) void k_bwd_kv_mfma(
                     accumulate_chunk<T, D>(Qs, c, lane, pack8<T>(dp), gk);
                 }
             };
-            if (wide)
-                chunks(std::true_type{});
-            else
-                chunks(std::false_type{});
+            chunks(std::integral_constant<bool, WIDE>{});
         }
         // next slice: within the pair (q heads x axis-0 slices), else the next pair
         fresh = false;
@@ -1252,20 +1241,28 @@ int layout_group(std::initializer_list<Lay> qside, std::initializer_list<Lay> kv
     return same_lay(*qside.begin(), *kvside.begin()) ? kLayOne : kLayTwo;
 }
 
+template <typename T, int D, int LAY, bool WIDE>
+hipError_t run_fwd(const Prob& p, TileShape ts, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
+                   void* o, Lay lo, float* lse, Lay ll, hipStream_t s) {
+    const auto kern = k_fwd_mfma<T, D, LAY, WIDE>;
+    const size_t shm = lds_bytes(kForward, ts.slots, D);
+    hipError_t e = allow_lds(kern, shm);
+    if (e != hipSuccess) return e;
+    fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    const int* geo = geometry_table(p, ts, false, s);
+    NA_LAUNCH("na_fwd_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, p,
+              ts, geo, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv), (T*)o, to_k(lo), lse,
+              to_k(ll));
+    return hipGetLastError();
+}
+
 template <typename T, int D, int LAY>
 hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
                       Lay lo, float* lse, Lay ll, hipStream_t s) {
     TileShape ts{};
     if (!choose_tile(p, kForward, D, ts)) return hipErrorInvalidValue;
-    const size_t shm = lds_bytes(kForward, ts.slots, D);
-    hipError_t e = allow_lds(k_fwd_mfma<T, D, LAY>, shm);
-    if (e != hipSuccess) return e;
-    fit_h_per(p, ts, resident_blocks(k_fwd_mfma<T, D, LAY>, 64 * ts.waves, shm));
-    const int* geo = geometry_table(p, ts, false, s);
-    NA_LAUNCH("na_fwd_mfma", (k_fwd_mfma<T, D, LAY>), dim3(static_cast<unsigned>(grid_blocks(p, ts))),
-              dim3(64 * ts.waves), shm, s, p, ts, geo, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v,
-              to_k(lv), (T*)o, to_k(lo), lse, to_k(ll));
-    return hipGetLastError();
+    if (ts.rowshift > 5) return run_fwd<T, D, LAY, true>(p, ts, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
+    return run_fwd<T, D, LAY, false>(p, ts, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
 }
 
 template <typename T, int D>
@@ -1281,6 +1278,38 @@ hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
     }
 }
 
+template <typename T, int D, int LAY, bool WIDE>
+hipError_t run_bwd_q(const Prob& p, TileShape ts, const void* q, Lay lq, const void* k, Lay lk, const void* v,
+                     Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
+                     const float* dlse, Lay ldl, void* dq, Lay ldq, float* delta, Lay lde, hipStream_t s) {
+    const auto kern = k_bwd_q_mfma<T, D, LAY, WIDE>;
+    const size_t shm = lds_bytes(kBackwardQ, ts.slots, D);
+    hipError_t e = allow_lds(kern, shm);
+    if (e != hipSuccess) return e;
+    fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    const int* geo = geometry_table(p, ts, false, s);
+    NA_LAUNCH("na_bwd_q_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s,
+              p, ts, geo, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv), (const T*)o, to_k(lo),
+              (const T*)dout, to_k(ldo), lse, to_k(ll), dlse, to_k(ldl), (T*)dq, to_k(ldq), delta, to_k(lde));
+    return hipGetLastError();
+}
+
+template <typename T, int D, int LAY, bool WIDE>
+hipError_t run_bwd_kv(const Prob& p, TileShape ts, const void* q, Lay lq, const void* k, Lay lk, const void* v,
+                      Lay lv, const void* dout, Lay ldo, const float* lse, Lay ll, const float* delta, Lay lde,
+                      void* dk, Lay ldk, void* dv, Lay ldv, hipStream_t s) {
+    const auto kern = k_bwd_kv_mfma<T, D, LAY, WIDE>;
+    const size_t shm = lds_bytes(kBackwardKV, ts.slots, D);
+    hipError_t e = allow_lds(kern, shm);
+    if (e != hipSuccess) return e;
+    fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    const int* geo = geometry_table(p, ts, true, s);
+    NA_LAUNCH("na_bwd_kv_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s,
+              p, ts, geo, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv), (const T*)dout,
+              to_k(ldo), lse, to_k(ll), delta, to_k(lde), (T*)dk, to_k(ldk), (T*)dv, to_k(ldv));
+    return hipGetLastError();
+}
+
 template <typename T, int D, int LAY>
 hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
                       const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
@@ -1288,25 +1317,17 @@ hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
                       float* delta, Lay lde, hipStream_t s) {
     TileShape tq{}, tk{};
     if (!choose_tile(p, kBackwardQ, D, tq) || !choose_tile(p, kBackwardKV, D, tk)) return hipErrorInvalidValue;
-    const size_t shq = lds_bytes(kBackwardQ, tq.slots, D), shk = lds_bytes(kBackwardKV, tk.slots, D);
-    hipError_t e = allow_lds(k_bwd_q_mfma<T, D, LAY>, shq);
-    if (e == hipSuccess) e = allow_lds(k_bwd_kv_mfma<T, D, LAY>, shk);
+    hipError_t e = tq.rowshift > 5
+                       ? run_bwd_q<T, D, LAY, true>(p, tq, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl,
+                                                    dq, ldq, delta, lde, s)
+                       : run_bwd_q<T, D, LAY, false>(p, tq, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl,
+                                                     dq, ldq, delta, lde, s);
     if (e != hipSuccess) return e;
-    fit_h_per(p, tq, resident_blocks(k_bwd_q_mfma<T, D, LAY>, 64 * tq.waves, shq));
-    fit_h_per(p, tk, resident_blocks(k_bwd_kv_mfma<T, D, LAY>, 64 * tk.waves, shk));
-    const int* gq = geometry_table(p, tq, false, s);
-    const int* gk = geometry_table(p, tk, true, s);
-    NA_LAUNCH("na_bwd_q_mfma", (k_bwd_q_mfma<T, D, LAY>), dim3(static_cast<unsigned>(grid_blocks(p, tq))),
-              dim3(64 * tq.waves), shq, s, p, tq, gq, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v,
-              to_k(lv), (const T*)o, to_k(lo), (const T*)dout, to_k(ldo), lse, to_k(ll), dlse, to_k(ldl), (T*)dq,
-              to_k(ldq), delta, to_k(lde));
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    NA_LAUNCH("na_bwd_kv_mfma", (k_bwd_kv_mfma<T, D, LAY>), dim3(static_cast<unsigned>(grid_blocks(p, tk))),
-              dim3(64 * tk.waves), shk, s, p, tk, gk, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v,
-              to_k(lv), (const T*)dout, to_k(ldo), lse, to_k(ll), (const float*)delta, to_k(lde), (T*)dk, to_k(ldk),
-              (T*)dv, to_k(ldv));
-    return hipGetLastError();
+    if (tk.rowshift > 5)
+        return run_bwd_kv<T, D, LAY, true>(p, tk, q, lq, k, lk, v, lv, dout, ldo, lse, ll, delta, lde, dk, ldk, dv,
+                                           ldv, s);
+    return run_bwd_kv<T, D, LAY, false>(p, tk, q, lq, k, lk, v, lv, dout, ldo, lse, ll, delta, lde, dk, ldk, dv, ldv,
+                                        s);
 }
 
 template <typename T, int D>
