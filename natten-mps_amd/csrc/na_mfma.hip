@@ -553,13 +553,30 @@ __device__ __forceinline__ int kv_head(const TileShape& ts, int h) { return ts.r
 // scalar registers live, which at head dim 32 removes the SGPR spills.
 constexpr int kLayGeneral = 0, kLayOne = 1, kLayTwo = 2;
 
-// Waves per SIMD a head-dim-32 instance is built for (4: at most 128 VGPRs,
-// 5: at most 96).  Saying so lets the register allocator trade VGPRs for
-// SGPRs instead of spilling SGPRs, and the backward instances without the
-// per-chunk column pattern fit 5 waves.  WIDE instances handle unions whose
-// rows exceed 32 slots, where the column mask changes from chunk to chunk;
+// Waves per SIMD an instance is built for (4: at most 128 VGPRs, 5: at most
+// 96; 1: no constraint).  Saying so lets the register allocator trade VGPRs
+// for SGPRs instead of spilling SGPRs.  The choices are the measured best on
+// MI355X that spill no VGPRs: at head dim 32 every instance without the
+// per-chunk column pattern fits 5 waves; at head dim 64 the dQ kernel and
+// the wide dK/dV kernel fit 4.  WIDE instances handle unions whose rows
+// exceed 32 slots, where the column mask changes from chunk to chunk;
 // keeping them apart leaves the common instance its smaller register need.
-#define NA_OCCUPANCY(D, W) __attribute__((amdgpu_waves_per_eu((D) == 32 ? (W) : 1)))
+enum KernelId { kKernFwd, kKernBwdQ, kKernBwdKV };
+
+constexpr int waves_per_simd(KernelId k, int D, bool wide) {
+    if (D == 32) return wide ? 4 : 5;
+    if (D == 64) return k == kKernBwdQ || (k == kKernBwdKV && wide) ? 4 : 1;
+    return 1;
+}
+
+#define NA_OCCUPANCY(K, D, WIDE) __attribute__((amdgpu_waves_per_eu(waves_per_simd(K, D, WIDE))))
+
+// Chunks per online-softmax group in the forward (one max reduction and one
+// rescale per group); two keep head dim 32 within 96 VGPRs.
+template <int D>
+constexpr int fwd_group() {
+    return D == 32 ? 2 : 4;
+}
 
 // Walk of a workgroup over its (batch, head) pairs and axis-0 slices.  The
 // loads of the next slice are issued as soon as the current one is no longer
@@ -592,11 +609,11 @@ __device__ __forceinline__ int slice_pos(const Prob& p, const Block& k, int u0) 
 
 // ---------------------------------------------------------------------------
 // Forward: out = softmax(scale q.k) v over each window, lse (natural log).
-// Online softmax over groups of up to 4 chunks (one max reduction and one
-// rescale per group).
+// Online softmax over groups of fwd_group<D>() chunks (one max reduction and
+// one rescale per group).
 // ---------------------------------------------------------------------------
 template <typename T, int D, int LAY, bool WIDE>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(D, 4) void k_fwd_mfma(
+__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfma(
     Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
     LayK lk_in, const T* __restrict__ vg, LayK lv_in, T* __restrict__ out, LayK lo_in, float* __restrict__ lse,
     LayK ll) {
@@ -644,13 +661,14 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D, 4) void k_fwd_mfma(
         if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
             const auto chunks = [&](auto) {
-                for (int c = wg.c0; c <= wg.c1; c += 4) {
-                    const int n = min(4, wg.c1 - c + 1);
-                    f32x4_t s[4][2];
-                    bool rv[4];
+                constexpr int FG = fwd_group<D>();
+                for (int c = wg.c0; c <= wg.c1; c += FG) {
+                    const int n = min(FG, wg.c1 - c + 1);
+                    f32x4_t s[FG][2];
+                    bool rv[FG];
                     float cm = -INFINITY;
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
+                    for (int g = 0; g < FG; ++g) {
                         if (g < n) {
                             if constexpr (!WIDE) {
                                 score_chunk<T, D>(Ks, c + g, col, grp, qf, cb, s[g]);
@@ -671,7 +689,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D, 4) void k_fwd_mfma(
 #pragma unroll
                     for (int db = 0; db < D / 16; ++db) acc[db] *= corr;
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
+                    for (int g = 0; g < FG; ++g) {
                         if (g < n) {
                             const float off = rv[g] ? -mref : -INFINITY;
 #pragma unroll
@@ -709,7 +727,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(D, 4) void k_fwd_mfma(
 // dP = dO . v.  The dP product starts from -delta.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int LAY, bool WIDE>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(D, (WIDE ? 4 : 5)) void k_bwd_q_mfma(
+__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_mfma(
     Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
     LayK lk_in, const T* __restrict__ vg, LayK lv_in, const T* __restrict__ o, LayK lo_in,
     const T* __restrict__ dout, LayK ldo_in, const float* __restrict__ lse, LayK ll, const float* __restrict__ dlse,
@@ -839,7 +857,7 @@ __device__ __forceinline__ void stage_scalars(const Prob& p, const Block& k, con
 }
 
 template <typename T, int D, int LAY, bool WIDE>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(D, (WIDE ? 4 : 5)) void k_bwd_kv_mfma(
+__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_kv_mfma(
     Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
     LayK lk_in, const T* __restrict__ vg, LayK lv_in, const T* __restrict__ dout, LayK ldo_in,
     const float* __restrict__ lse, LayK ll, const float* __restrict__ delta, LayK lde_in, T* __restrict__ dk,
