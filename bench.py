@@ -307,7 +307,8 @@ def main():
     for name, (n, tot, mn, mx) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
         _log(f"  {name:14s} launches={n:4d} mean={tot / n * 1e3:8.1f} us  min={mn * 1e3:8.1f}  max={mx * 1e3:8.1f}"
              f"  share={tot / gpu_total:5.1%}")
-    dil_tag = "x".join(str(d) for d in cfg["dilation"])
+    dils = [str(d) for d in cfg["dilation"]]
+    dil_tag = dils[0] if len(set(dils)) == 1 else "x".join(dils)
     workload = f"config{args.config}_d{dil_tag}"
     dom_name, (dn, dtot, _, _) = max(stats.items(), key=lambda kv: kv[1][1])
     nbytes = kernel_bytes(dom_name, B, N, Hq, Hkv, D, esz)
