@@ -364,6 +364,16 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Workgroup barrier after ordinary LDS stores (ds_write) that other waves
+// read next.  The compiler emits no LDS counter wait before a workgroup
+// barrier (it takes LDS operations as ordered across waves); on MI355X a
+// store issued just before the barrier was not always seen by another
+// wave's read after it, so the wait is explicit here.
+__device__ __forceinline__ void lds_publish_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();
+}
+
 // Blocks are dealt round-robin to the 8 XCDs; remap so that each XCD works on
 // one contiguous range of logical blocks (neighbouring tiles share K/V lines in
 // that XCD's L2).  Identity on the tail that does not fill all 8.

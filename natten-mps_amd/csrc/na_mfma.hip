@@ -912,7 +912,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_k
             }
         }
         wait_loads();
-        __syncthreads();
+        lds_publish_barrier();  // staged rows and the slice's -lse / -delta
         if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
             const auto chunks = [&](auto) {

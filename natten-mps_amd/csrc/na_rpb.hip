@@ -224,10 +224,10 @@ __global__ __launch_bounds__(256) void k_rpb_dbias(RProb p, const T* __restrict_
         }
     }
     part[threadIdx.x] = acc;
-    __syncthreads();
+    lds_publish_barrier();
     for (int s = blockDim.x / 2; s > 0; s >>= 1) {
         if (threadIdx.x < s) part[threadIdx.x] += part[threadIdx.x + s];
-        __syncthreads();
+        lds_publish_barrier();
     }
     if (threadIdx.x == 0) drpb[h * nb + rb] = from_f<T>(part[0]);
 }

@@ -121,3 +121,31 @@ def test_config5_na3d_bf16():
     _close(out[sl], ref, 2e-2, "out")
     for n_, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
         _close(a[sl], b, 2e-2, n_)
+
+
+@pytest.mark.parametrize("cfg", [4, 5])
+def test_backward_is_bitwise_deterministic(cfg):
+    """The dK/dV gather has no atomics, so repeated backward passes agree bit
+    for bit over the whole tensors (not only the slices the oracle checks).
+    Covers the key-side walk over several staged slices per workgroup: the
+    GQA group's q heads (cfg 4) and the axis-0 planes of a 3-D union (cfg 5),
+    whose per-slice -lse / -delta rows go through LDS stores and a barrier."""
+    from natten_mps_amd import functional as F
+
+    if cfg == 4:
+        shapes = [(4, 16384, 8, 64), (4, 16384, 2, 64), (4, 16384, 2, 64), (4, 16384, 8, 64)]
+        fn, kw = F.na1d, dict(kernel_size=33, dilation=1, is_causal=True)
+    else:
+        shapes = [(2, 16, 32, 32, 8, 64)] * 4
+        fn, kw = F.na3d, dict(kernel_size=(3, 7, 7), dilation=(1, 2, 2))
+    q, k, v, do = (t.to(DEV) for t in _seeded(cfg, shapes, torch.bfloat16))
+    leaves = [t.requires_grad_(True) for t in (q, k, v)]
+
+    def step():
+        out = fn(*leaves, **kw)
+        return [out.detach()] + list(torch.autograd.grad(out, leaves, do))
+
+    ref = step()
+    for _ in range(4):
+        for name, a, b in zip(("out", "dq", "dk", "dv"), step(), ref):
+            assert torch.equal(a, b), f"{name}: {int((a != b).sum())} elements differ between runs"
