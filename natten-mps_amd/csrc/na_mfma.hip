@@ -65,6 +65,8 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kMaxItems = 64;
+// bytes of LDS before the staged operands (see lds_base)
+constexpr int kLdsPad = 16;
 // buffer range of a staged plane; out-of-union slots read at kOutOfRange
 constexpr int kPlaneBytes = 0x7FFFFFF0;
 constexpr uint32_t kOutOfRange = 0x80000000u;
@@ -543,6 +545,16 @@ __device__ __forceinline__ void store_rows(T* __restrict__ g, long long off, int
     }
 }
 
+// The staged operands start at LDS address kLdsPad, reached through a
+// constant address instead of the dynamic `extern __shared__` symbol: the
+// compiler then folds the base into each ds_read's offset field (through the
+// symbol it re-adds the base with one VALU per LDS address and chunk).  Not
+// address 0: a constant 0 becomes a null pointer, and the generic null
+// pointer is not LDS.  Every launch allocates kLdsPad more bytes.
+__device__ __forceinline__ unsigned char* lds_base() {
+    return (unsigned char*)((__attribute__((address_space(3))) unsigned char*)(kLdsPad));
+}
+
 __device__ __forceinline__ int kv_head(const TileShape& ts, int h) { return ts.rep.d == 1 ? h : fdiv(h, ts.rep); }
 
 // Operand layout groups a kernel instance assumes (chosen by the host).
@@ -620,7 +632,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfm
     const LayK& lk = LAY == kLayOne ? lq : lk_in;
     const LayK& lv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : lv_in;
     const LayK& lo = LAY == kLayGeneral ? lo_in : lq;
-    extern __shared__ __align__(16) unsigned char smem[];
+    unsigned char* smem = lds_base();
     constexpr bool KEY_SIDE = false;
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + ts.slots * D;
@@ -739,7 +751,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_
     const LayK& ldq = LAY == kLayGeneral ? ldq_in : lq;
     const LayK& ldl = LAY == kLayGeneral ? ldl_in : ll;
     const LayK& lde = LAY == kLayGeneral ? lde_in : ll;
-    extern __shared__ __align__(16) unsigned char smem[];
+    unsigned char* smem = lds_base();
     constexpr bool KEY_SIDE = false;
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + ts.slots * D;
@@ -868,7 +880,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_k
     const LayK& ldv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : ldv_in;
     const LayK& ldo = LAY == kLayGeneral ? ldo_in : lq;
     const LayK& lde = LAY == kLayGeneral ? lde_in : ll;
-    extern __shared__ __align__(16) unsigned char smem[];
+    unsigned char* smem = lds_base();
     constexpr bool KEY_SIDE = true;
     const int slots = ts.slots;
     T* Qs = reinterpret_cast<T*>(smem);
@@ -1018,7 +1030,7 @@ int union_extent(const Axis& A, int T, bool key_tile) {
 
 size_t lds_bytes(Kind kind, int slots, int D) {
     const size_t rows = static_cast<size_t>(slots) * D * 2;
-    return kind == kBackwardKV ? 2 * rows + (2 * static_cast<size_t>(slots) + 8) * 4 : 2 * rows;
+    return kLdsPad + (kind == kBackwardKV ? 2 * rows + (2 * static_cast<size_t>(slots) + 8) * 4 : 2 * rows);
 }
 
 void set_h_per(TileShape& ts, int per) {
