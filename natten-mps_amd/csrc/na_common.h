@@ -286,6 +286,70 @@ __host__ __device__ inline void for_each_query(const Prob& p, int m0, int m1, in
     }
 }
 
+// Split iteration for latency-bound vector kernels: `split` lane groups share
+// one query (key); group `sp` takes every split-th index of the outermost
+// axis whose kernel extent exceeds 1, so each group walks about 1/split of
+// the neighbours (attending queries) and the loads of the groups are in
+// flight together.  The callers combine the groups' partial results.
+__host__ __device__ inline int split_axis(const Prob& p) {
+    return p.ax[0].k > 1 ? 0 : p.ax[1].k > 1 ? 1 : 2;
+}
+
+template <class F>
+__device__ __forceinline__ void for_each_neighbor_split(const Prob& p, int i0, int i1, int i2, int sp, int split,
+                                                        F&& f) {
+    const Axis &A0 = p.ax[0], &A1 = p.ax[1], &A2 = p.ax[2];
+    const int f0 = axis_first(A0, i0), f1 = axis_first(A1, i1), f2 = axis_first(A2, i2);
+    const int sa = split_axis(p);
+    const int x0 = sa == 0 ? sp : 0, xs = sa == 0 ? split : 1;
+    const int y0 = sa == 1 ? sp : 0, ys = sa == 1 ? split : 1;
+    const int z0 = sa == 2 ? sp : 0, zs = sa == 2 ? split : 1;
+    for (int x = x0; x < A0.k; x += xs) {
+        const int j0 = f0 + x * A0.dil;
+        for (int y = y0; y < A1.k; y += ys) {
+            const int j1 = f1 + y * A1.dil;
+            for (int z = z0; z < A2.k; z += zs) {
+                const int j2 = f2 + z * A2.dil;
+                f(j0, j1, j2, (x * A1.k + y) * A2.k + z, (j0 >= 0) & (j1 >= 0) & (j2 >= 0));
+            }
+        }
+    }
+}
+
+template <class F>
+__device__ __forceinline__ void for_each_query_split(const Prob& p, int m0, int m1, int m2, int sp, int split,
+                                                     F&& f) {
+    const Axis &A0 = p.ax[0], &A1 = p.ax[1], &A2 = p.ax[2];
+    int l0, h0, l1, h1, l2, h2;
+    if (!axis_query_range(A0, m0, l0, h0)) return;
+    if (!axis_query_range(A1, m1, l1, h1)) return;
+    if (!axis_query_range(A2, m2, l2, h2)) return;
+    const int sa = split_axis(p);
+    const int s0 = sa == 0 ? split : 1, s1 = sa == 1 ? split : 1, s2 = sa == 2 ? split : 1;
+    for (int t0 = l0 + (sa == 0 ? sp : 0); t0 <= h0; t0 += s0) {
+        const int i0 = m0 + t0 * A0.dil;
+        if (i0 % A0.st) continue;
+        const int o0 = i0 / A0.st;
+        if (o0 >= A0.out) continue;
+        const int x = (m0 - axis_first(A0, i0)) / A0.dil;
+        for (int t1 = l1 + (sa == 1 ? sp : 0); t1 <= h1; t1 += s1) {
+            const int i1 = m1 + t1 * A1.dil;
+            if (i1 % A1.st) continue;
+            const int o1 = i1 / A1.st;
+            if (o1 >= A1.out) continue;
+            const int y = (m1 - axis_first(A1, i1)) / A1.dil;
+            for (int t2 = l2 + (sa == 2 ? sp : 0); t2 <= h2; t2 += s2) {
+                const int i2 = m2 + t2 * A2.dil;
+                if (i2 % A2.st) continue;
+                const int o2 = i2 / A2.st;
+                if (o2 >= A2.out) continue;
+                const int z = (m2 - axis_first(A2, i2)) / A2.dil;
+                f(o0, o1, o2, i0, i1, i2, (x * A1.k + y) * A2.k + z);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Element types.  bf16 is carried as raw bits; fp32 -> bf16 rounds to nearest
 // even with NaN kept quiet, the same rounding torch uses.
@@ -361,6 +425,20 @@ template <int LPQ>
 __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
     for (int m = LPQ / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, LPQ);
+    return v;
+}
+
+// Sum / max over the `split` lane groups (LPQ lanes each, consecutive) of
+// one query or key, in a fixed butterfly order.
+template <int LPQ>
+__device__ __forceinline__ float split_sum(float v, int split) {
+    for (int m = split >> 1; m >= 1; m >>= 1) v += __shfl_xor(v, m * LPQ);
+    return v;
+}
+
+template <int LPQ>
+__device__ __forceinline__ float split_max(float v, int split) {
+    for (int m = split >> 1; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m * LPQ));
     return v;
 }
 

@@ -10,6 +10,8 @@
 // read straight from global memory; the overlap between neighbouring windows
 // is served by L1/L2 (blocks are remapped so each XCD walks a contiguous
 // range).
+#include <cstdlib>
+
 #include "na_launch.h"
 
 namespace na {
@@ -88,20 +90,21 @@ __device__ __forceinline__ void store_zero(T* g, int d0, int D, int vec) {
 // Fused forward with online softmax.
 // ---------------------------------------------------------------------------
 template <typename T, int DPL, int LPQ>
-__global__ __launch_bounds__(256) void k_forward(Prob p, int vec, const int* __restrict__ lens,
+__global__ __launch_bounds__(256) void k_forward(Prob p, int vec, int split, const int* __restrict__ lens,
                                                  const T* __restrict__ q, Lay lq,
                                                  const T* __restrict__ k, Lay lk,
                                                  const T* __restrict__ v, Lay lv,
                                                  T* __restrict__ out, Lay lo,
                                                  float* __restrict__ lse, Lay ll) {
-    const long long qi = group_index(LPQ);
+    const long long qi = group_index(LPQ * split);
     if (qi >= static_cast<long long>(p.B) * p.nout * p.Hq) return;
     const int d0 = (threadIdx.x % LPQ) * DPL;
+    const int sp = (threadIdx.x / LPQ) % split;
     const QPos Q = decode_query(p, qi);
     const int hk = Q.h / p.rep;
     if (lens && !sample_extent(p, lens, Q.b, Q.i0, Q.i1, Q.i2)) {
-        store_zero<T, DPL>(out + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec);
-        if (d0 == 0) lse[ll.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = 0.f;
+        if (sp == 0) store_zero<T, DPL>(out + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec);
+        if (sp == 0 && d0 == 0) lse[ll.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = 0.f;
         return;
     }
 
@@ -111,7 +114,7 @@ __global__ __launch_bounds__(256) void k_forward(Prob p, int vec, const int* __r
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
 
-    for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int, bool ok) {
+    for_each_neighbor_split(p, Q.i0, Q.i1, Q.i2, sp, split, [&](int j0, int j1, int j2, int, bool ok) {
         if (!ok) return;
         float kv[DPL], vv[DPL];
         load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk, vec, kv);
@@ -133,10 +136,19 @@ __global__ __launch_bounds__(256) void k_forward(Prob p, int vec, const int* __r
         for (int j = 0; j < DPL; ++j) acc[j] = fmaf(e, vv[j], acc[j]);
     });
 
+    if (split > 1) {
+        // merge the groups' softmax states (a group may have seen no neighbour)
+        const float mall = split_max<LPQ>(m, split);
+        const float c = m == -INFINITY ? 0.f : expf(m - mall);
+        l = split_sum<LPQ>(l * c, split);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[j] = split_sum<LPQ>(acc[j] * c, split);
+        m = mall;
+    }
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[j] = acc[j] / l;
-    store_run<T, DPL>(out + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, acc);
-    if (d0 == 0) lse[ll.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = m + logf(l);
+    if (sp == 0) store_run<T, DPL>(out + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, acc);
+    if (sp == 0 && d0 == 0) lse[ll.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = m + logf(l);
 }
 
 // ---------------------------------------------------------------------------
@@ -201,7 +213,7 @@ __global__ __launch_bounds__(256) void k_av(Prob p, int vec,
 // dq = scale * sum_k P (dO.v_k - delta) k_k with P = exp(scale q.k - lse).
 // ---------------------------------------------------------------------------
 template <typename T, int DPL, int LPQ>
-__global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec, const int* __restrict__ lens,
+__global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec, int split, const int* __restrict__ lens,
                                                 const T* __restrict__ q, Lay lq,
                                                 const T* __restrict__ k, Lay lk,
                                                 const T* __restrict__ v, Lay lv,
@@ -211,14 +223,15 @@ __global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec, const int* __re
                                                 const float* __restrict__ dlse, Lay ldl,
                                                 T* __restrict__ dq, Lay ldq,
                                                 float* __restrict__ delta, Lay lde) {
-    const long long qi = group_index(LPQ);
+    const long long qi = group_index(LPQ * split);
     if (qi >= static_cast<long long>(p.B) * p.nout * p.Hq) return;
     const int d0 = (threadIdx.x % LPQ) * DPL;
+    const int sp = (threadIdx.x / LPQ) % split;
     const QPos Q = decode_query(p, qi);
     const int hk = Q.h / p.rep;
     if (lens && !sample_extent(p, lens, Q.b, Q.i0, Q.i1, Q.i2)) {
-        store_zero<T, DPL>(dq + ldq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec);
-        if (d0 == 0) delta[lde.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = 0.f;
+        if (sp == 0) store_zero<T, DPL>(dq + ldq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec);
+        if (sp == 0 && d0 == 0) delta[lde.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = 0.f;
         return;
     }
 
@@ -237,7 +250,7 @@ __global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec, const int* __re
     } else {
         // 16-bit O carries ~2^-9 relative rounding; use the equivalent
         // delta = sum_k P_k (dO . v_k) from an extra pass instead.
-        for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int, bool ok) {
+        for_each_neighbor_split(p, Q.i0, Q.i1, Q.i2, sp, split, [&](int j0, int j1, int j2, int, bool ok) {
             if (!ok) return;
             float kv[DPL], vv[DPL];
             load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk, vec, kv);
@@ -249,14 +262,15 @@ __global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec, const int* __re
             dp = group_sum<LPQ>(dp);
             di = fmaf(expf(s - L), dp, di);
         });
+        di = split_sum<LPQ>(di, split);
     }
     if (dlse) di -= dlse[ldl.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)];
-    if (d0 == 0) delta[lde.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = di;
+    if (sp == 0 && d0 == 0) delta[lde.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h)] = di;
 
     float acc[DPL];
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
-    for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int, bool ok) {
+    for_each_neighbor_split(p, Q.i0, Q.i1, Q.i2, sp, split, [&](int j0, int j1, int j2, int, bool ok) {
         if (!ok) return;
         float kv[DPL], vv[DPL];
         load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk, vec, kv);
@@ -271,8 +285,8 @@ __global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec, const int* __re
         for (int j = 0; j < DPL; ++j) acc[j] = fmaf(ds, kv[j], acc[j]);
     });
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) acc[j] *= p.scale;
-    store_run<T, DPL>(dq + ldq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, acc);
+    for (int j = 0; j < DPL; ++j) acc[j] = split_sum<LPQ>(acc[j], split) * p.scale;
+    if (sp == 0) store_run<T, DPL>(dq + ldq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -282,7 +296,7 @@ __global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec, const int* __re
 // atomics); recomputes P from q, k and lse.
 // ---------------------------------------------------------------------------
 template <typename T, int DPL, int LPQ>
-__global__ __launch_bounds__(256) void k_bwd_dkdv(Prob p, int vec, const int* __restrict__ lens,
+__global__ __launch_bounds__(256) void k_bwd_dkdv(Prob p, int vec, int split, const int* __restrict__ lens,
                                                   const T* __restrict__ q, Lay lq,
                                                   const T* __restrict__ k, Lay lk,
                                                   const T* __restrict__ v, Lay lv,
@@ -291,13 +305,14 @@ __global__ __launch_bounds__(256) void k_bwd_dkdv(Prob p, int vec, const int* __
                                                   const float* __restrict__ delta, Lay lde,
                                                   T* __restrict__ dk, Lay ldk,
                                                   T* __restrict__ dv, Lay ldv) {
-    const long long ki = group_index(LPQ);
+    const long long ki = group_index(LPQ * split);
     if (ki >= static_cast<long long>(p.B) * p.nkey * p.Hkv) return;
     const int d0 = (threadIdx.x % LPQ) * DPL;
+    const int sp = (threadIdx.x / LPQ) % split;
     const KPos K = decode_key(p, ki, p.Hkv);
     if (lens && !sample_extent(p, lens, K.b, K.m0, K.m1, K.m2)) {
-        store_zero<T, DPL>(dk + ldk.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dqk, vec);
-        store_zero<T, DPL>(dv + ldv.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dv, vec);
+        if (sp == 0) store_zero<T, DPL>(dk + ldk.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dqk, vec);
+        if (sp == 0) store_zero<T, DPL>(dv + ldv.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dv, vec);
         return;
     }
 
@@ -307,7 +322,7 @@ __global__ __launch_bounds__(256) void k_bwd_dkdv(Prob p, int vec, const int* __
 #pragma unroll
     for (int j = 0; j < DPL; ++j) { gk[j] = 0.f; gv[j] = 0.f; }
 
-    for_each_query(p, K.m0, K.m1, K.m2, [&](int o0, int o1, int o2, int i0, int i1, int i2, int) {
+    for_each_query_split(p, K.m0, K.m1, K.m2, sp, split, [&](int o0, int o1, int o2, int i0, int i1, int i2, int) {
         for (int r = 0; r < p.rep; ++r) {
             const int h = K.h * p.rep + r;
             float qv[DPL], dov[DPL];
@@ -330,9 +345,12 @@ __global__ __launch_bounds__(256) void k_bwd_dkdv(Prob p, int vec, const int* __
         }
     });
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) gk[j] *= p.scale;
-    store_run<T, DPL>(dk + ldk.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dqk, vec, gk);
-    store_run<T, DPL>(dv + ldv.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dv, vec, gv);
+    for (int j = 0; j < DPL; ++j) {
+        gk[j] = split_sum<LPQ>(gk[j], split) * p.scale;
+        gv[j] = split_sum<LPQ>(gv[j], split);
+    }
+    if (sp == 0) store_run<T, DPL>(dk + ldk.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dqk, vec, gk);
+    if (sp == 0) store_run<T, DPL>(dv + ldv.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dv, vec, gv);
 }
 
 // ---------------------------------------------------------------------------
@@ -506,13 +524,38 @@ inline unsigned grid_for(long long groups, int lpq) {
     return static_cast<unsigned>((threads + 255) / 256);
 }
 
+// Lane groups per query (key) for the fused vector kernels.  Each group walks
+// its neighbours (attending queries) one after another, every step waiting
+// on its loads, so a small problem (few groups) is bound by that chain.
+// Splitting the walk over up to 8 groups, until the launch holds about 8
+// waves per SIMD of a 256-CU device, shortens the chain; groups stay within
+// one wave (lpq * split <= 64) and never outnumber the split axis's kernel
+// positions.  NATTEN_HIP_SPLIT=n fixes it (tuning).
+inline int choose_split(const Prob& p, long long groups, int lpq) {
+    static const int forced = [] {
+        const char* e = std::getenv("NATTEN_HIP_SPLIT");
+        return e ? std::atoi(e) : 0;
+    }();
+    const int kmax = p.ax[split_axis(p)].k;
+    constexpr long long kTargetWaves = 256LL * 4 * 8;
+    int split = 1;
+    if (forced > 0) {
+        while (split * 2 <= forced && split * 2 * lpq <= 64) split *= 2;
+        return split;
+    }
+    const long long waves = (groups * lpq + 63) / 64;
+    while (split < 8 && split * 2 * lpq <= 64 && split * 2 <= kmax && waves * split < kTargetWaves) split *= 2;
+    return split;
+}
+
 template <typename T, int DPL, int LPQ>
 struct LForward {
     static hipError_t run(const Prob& p, int vec, const int* lens, const void* q, Lay lq, const void* k, Lay lk,
                           const void* v, Lay lv, void* o, Lay lo, float* lse, Lay ll, hipStream_t s) {
         const long long n = static_cast<long long>(p.B) * p.nout * p.Hq;
-        NA_LAUNCH(lens ? "na_varlen_forward" : "na_forward", (k_forward<T, DPL, LPQ>), dim3(grid_for(n, LPQ)),
-                  dim3(256), 0, s, p, vec, lens, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (T*)o, lo, lse,
+        const int split = choose_split(p, n, LPQ);
+        NA_LAUNCH(lens ? "na_varlen_forward" : "na_forward", (k_forward<T, DPL, LPQ>),
+                  dim3(grid_for(n, LPQ * split)), dim3(256), 0, s, p, vec, split, lens, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (T*)o, lo, lse,
                   ll);
         return hipGetLastError();
     }
@@ -547,14 +590,16 @@ struct LBackward {
                           Lay ll, const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv,
                           Lay ldv, float* delta, Lay lde, hipStream_t s) {
         const long long nq = static_cast<long long>(p.B) * p.nout * p.Hq;
-        NA_LAUNCH(lens ? "na_varlen_bwd_dq" : "na_bwd_dq", (k_bwd_dq<T, DPL, LPQ>), dim3(grid_for(nq, LPQ)),
-                  dim3(256), 0, s, p, vec, lens, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (const T*)o, lo,
+        const int sq = choose_split(p, nq, LPQ);
+        NA_LAUNCH(lens ? "na_varlen_bwd_dq" : "na_bwd_dq", (k_bwd_dq<T, DPL, LPQ>), dim3(grid_for(nq, LPQ * sq)),
+                  dim3(256), 0, s, p, vec, sq, lens, (const T*)q, lq, (const T*)k, lk, (const T*)v, lv, (const T*)o, lo,
                   (const T*)dout, ldo, lse, ll, dlse, ldl, (T*)dq, ldq, delta, lde);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const long long nk = static_cast<long long>(p.B) * p.nkey * p.Hkv;
+        const int sk = choose_split(p, nk, LPQ);
         NA_LAUNCH(lens ? "na_varlen_bwd_dkdv" : "na_bwd_dkdv", (k_bwd_dkdv<T, DPL, LPQ>),
-                  dim3(grid_for(nk, LPQ)), dim3(256), 0, s, p, vec, lens, (const T*)q, lq, (const T*)k, lk,
+                  dim3(grid_for(nk, LPQ * sk)), dim3(256), 0, s, p, vec, sk, lens, (const T*)q, lq, (const T*)k, lk,
                   (const T*)v, lv, (const T*)dout, ldo, lse, ll, (const float*)delta, lde, (T*)dk, ldk, (T*)dv,
                   ldv);
         return hipGetLastError();
