@@ -49,19 +49,32 @@ hipEvent_t take_event() {
     return e;
 }
 
+void give_back(const Pending& p) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (p.start) g_free.push_back(p.start);
+    if (p.stop) g_free.push_back(p.stop);
+}
+
 }  // namespace
 
 void prof_begin(const char* name, hipStream_t s) {
     if (!g_on.load(std::memory_order_relaxed)) return;
     Pending p{name, take_event(), take_event()};
-    if (!p.start || !p.stop) return;
-    hipEventRecord(p.start, s);
+    // a failed record leaves the launch untimed; the launch itself proceeds
+    if (!p.start || !p.stop || hipEventRecord(p.start, s) != hipSuccess) {
+        give_back(p);
+        return;
+    }
     t_open = p;
 }
 
 void prof_end(hipStream_t s) {
     if (!t_open.name) return;
-    hipEventRecord(t_open.stop, s);
+    if (hipEventRecord(t_open.stop, s) != hipSuccess) {
+        give_back(t_open);
+        t_open = Pending{nullptr, nullptr, nullptr};
+        return;
+    }
     std::lock_guard<std::mutex> lk(g_mu);
     g_pending.push_back(t_open);
     t_open = Pending{nullptr, nullptr, nullptr};
