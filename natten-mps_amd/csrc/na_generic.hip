@@ -87,6 +87,90 @@ __device__ __forceinline__ void store_zero(T* g, int d0, int D, int vec) {
 }
 
 // ---------------------------------------------------------------------------
+// Pipelined walks.  A group's walk over its neighbours (or attending
+// queries) waits on each step's loads; with `walk_*_pipelined` the loads of
+// the next U steps are already in flight.  `fetch` issues a step's loads and
+// returns the raw registers (no use of the loaded values, so no wait), `use`
+// consumes them, in the same order as the plain walk.  Only for 16-byte
+// aligned runs (`vec`): lanes past the head dim read the row start and drop
+// it when unpacking; masked (causal) neighbours load from a clamped position
+// and are skipped by `use`.  fetch(j0, j1, j2, e) gets the neighbour's
+// position and index, use(step, e, valid) its registers.
+// ---------------------------------------------------------------------------
+template <typename T, int N>
+struct Raw {
+    static constexpr int NW = (N * static_cast<int>(sizeof(T))) / 16;
+    uint4 w[NW];
+};
+
+template <typename T, int N>
+__device__ __forceinline__ Raw<T, N> fetch_run(const T* __restrict__ p, int d0, int D) {
+    Raw<T, N> r;
+    const uint4* src = reinterpret_cast<const uint4*>(p + (d0 < D ? d0 : 0));
+#pragma unroll
+    for (int w = 0; w < Raw<T, N>::NW; ++w) r.w[w] = src[w];
+    return r;
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void unpack_run(const Raw<T, N>& r, int d0, int D, float (&out)[N]) {
+    const T* e = reinterpret_cast<const T*>(r.w);
+#pragma unroll
+    for (int j = 0; j < N; ++j) out[j] = d0 < D ? to_f(e[j]) : 0.f;
+}
+
+// Steps in flight: about 8 runs of 16 bytes per lane.
+template <typename T, int DPL, int RUNS>
+constexpr int pipe_depth() {
+    constexpr int w = Raw<T, DPL>::NW * RUNS;
+    return w >= 4 ? 2 : 8 / w;
+}
+
+template <int U, class Fetch, class Use>
+__device__ __forceinline__ void walk_neighbors_pipelined(const Prob& p, int i0, int i1, int i2, int sp, int split,
+                                                         Fetch&& fetch, Use&& use) {
+    const Axis &A0 = p.ax[0], &A1 = p.ax[1], &A2 = p.ax[2];
+    const int f0 = axis_first(A0, i0), f1 = axis_first(A1, i1), f2 = axis_first(A2, i2);
+    const int sa = split_axis(p);
+    const int x0 = sa == 0 ? sp : 0, xs = sa == 0 ? split : 1;
+    const int y0 = sa == 1 ? sp : 0, ys = sa == 1 ? split : 1;
+    const int z0 = sa == 2 ? sp : 0, zs = sa == 2 ? split : 1;
+    const int nx = x0 < A0.k ? (A0.k - x0 + xs - 1) / xs : 0;
+    const int ny = y0 < A1.k ? (A1.k - y0 + ys - 1) / ys : 0;
+    const int nz = z0 < A2.k ? (A2.k - z0 + zs - 1) / zs : 0;
+    const int total = nx * ny * nz;
+    using P = decltype(fetch(0, 0, 0, 0));
+    int x = x0, y = y0, z = z0;
+    // blocks of U steps: every fetch of a block is issued before the first
+    // use, unconditionally (past the end the cursor stays on the last step),
+    // so the compiler waits for each step's loads with the rest in flight
+    for (int i = 0; i < total; i += U) {
+        P buf[U];
+        int eb[U];
+        bool okb[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j0 = f0 + x * A0.dil, j1 = f1 + y * A1.dil, j2 = f2 + z * A2.dil;
+            okb[u] = (j0 >= 0) & (j1 >= 0) & (j2 >= 0);
+            eb[u] = (x * A1.k + y) * A2.k + z;
+            buf[u] = fetch(j0 < 0 ? 0 : j0, j1 < 0 ? 0 : j1, j2 < 0 ? 0 : j2, eb[u]);
+            if (i + u + 1 < total) {
+                if ((z += zs) >= A2.k) {
+                    z = z0;
+                    if ((y += ys) >= A1.k) {
+                        y = y0;
+                        x += xs;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (i + u < total) use(buf[u], eb[u], okb[u]);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Fused forward with online softmax.
 // ---------------------------------------------------------------------------
 template <typename T, int DPL, int LPQ>
@@ -114,11 +198,7 @@ __global__ __launch_bounds__(256) void k_forward(Prob p, int vec, int split, con
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
 
-    for_each_neighbor_split(p, Q.i0, Q.i1, Q.i2, sp, split, [&](int j0, int j1, int j2, int, bool ok) {
-        if (!ok) return;
-        float kv[DPL], vv[DPL];
-        load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk, vec, kv);
-        load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, hk), d0, p.Dv, vec, vv);
+    const auto step = [&](const float (&kv)[DPL], const float (&vv)[DPL]) {
         float s = 0.f;
 #pragma unroll
         for (int j = 0; j < DPL; ++j) s = fmaf(qv[j], kv[j], s);
@@ -134,7 +214,33 @@ __global__ __launch_bounds__(256) void k_forward(Prob p, int vec, int split, con
         l += e;
 #pragma unroll
         for (int j = 0; j < DPL; ++j) acc[j] = fmaf(e, vv[j], acc[j]);
-    });
+    };
+    if (vec) {
+        struct Step {
+            Raw<T, DPL> k, v;
+        };
+        walk_neighbors_pipelined<pipe_depth<T, DPL, 2>()>(
+            p, Q.i0, Q.i1, Q.i2, sp, split,
+            [&](int j0, int j1, int j2, int) {
+                return Step{fetch_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk),
+                            fetch_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, hk), d0, p.Dv)};
+            },
+            [&](const Step& st, int, bool ok) {
+                if (!ok) return;
+                float kv[DPL], vv[DPL];
+                unpack_run<T, DPL>(st.k, d0, p.Dqk, kv);
+                unpack_run<T, DPL>(st.v, d0, p.Dv, vv);
+                step(kv, vv);
+            });
+    } else {
+        for_each_neighbor_split(p, Q.i0, Q.i1, Q.i2, sp, split, [&](int j0, int j1, int j2, int, bool ok) {
+            if (!ok) return;
+            float kv[DPL], vv[DPL];
+            load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk, vec, kv);
+            load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, hk), d0, p.Dv, vec, vv);
+            step(kv, vv);
+        });
+    }
 
     if (split > 1) {
         // merge the groups' softmax states (a group may have seen no neighbour)
@@ -166,6 +272,22 @@ __global__ __launch_bounds__(256) void k_qk(Prob p, int vec,
     float qv[DPL];
     load_run<T, DPL>(q + lq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, qv);
     T* row = attn + la.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h);
+    if (vec) {
+        walk_neighbors_pipelined<pipe_depth<T, DPL, 1>()>(
+            p, Q.i0, Q.i1, Q.i2, 0, 1,
+            [&](int j0, int j1, int j2, int) { return fetch_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, Q.h), d0, p.Dqk); },
+            [&](const Raw<T, DPL>& r, int e, bool ok) {
+                float kv[DPL];
+                unpack_run<T, DPL>(r, d0, p.Dqk, kv);
+                float acc = 0.f;
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) acc = fmaf(qv[j], kv[j], acc);
+                float s = ok ? group_sum<LPQ>(acc) : -INFINITY;
+                if (p.has_scale) s *= p.scale;
+                if (d0 == 0) row[e] = from_f<T>(s);
+            });
+        return;
+    }
     for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
         float s = -INFINITY;
         if (ok) {
@@ -197,14 +319,34 @@ __global__ __launch_bounds__(256) void k_av(Prob p, int vec,
     float acc[DPL];
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
-    for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
-        if (!ok) return;
-        const float a = to_f(row[e]);
-        float vv[DPL];
-        load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, Q.h), d0, p.Dv, vec, vv);
+    if (vec) {
+        struct Step {
+            Raw<T, DPL> v;
+            T a;
+        };
+        walk_neighbors_pipelined<pipe_depth<T, DPL, 1>()>(
+            p, Q.i0, Q.i1, Q.i2, 0, 1,
+            [&](int j0, int j1, int j2, int e) {
+                return Step{fetch_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, Q.h), d0, p.Dv), row[e]};
+            },
+            [&](Step& st, int, bool ok) {
+                if (!ok) return;
+                const float a = to_f(st.a);
+                float vv[DPL];
+                unpack_run<T, DPL>(st.v, d0, p.Dv, vv);
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(a, vv[j], acc[j]);
-    });
+                for (int j = 0; j < DPL; ++j) acc[j] = fmaf(a, vv[j], acc[j]);
+            });
+    } else {
+        for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
+            if (!ok) return;
+            const float a = to_f(row[e]);
+            float vv[DPL];
+            load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, Q.h), d0, p.Dv, vec, vv);
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) acc[j] = fmaf(a, vv[j], acc[j]);
+        });
+    }
     store_run<T, DPL>(out + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, acc);
 }
 
@@ -270,11 +412,7 @@ __global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec, int split, cons
     float acc[DPL];
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
-    for_each_neighbor_split(p, Q.i0, Q.i1, Q.i2, sp, split, [&](int j0, int j1, int j2, int, bool ok) {
-        if (!ok) return;
-        float kv[DPL], vv[DPL];
-        load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk, vec, kv);
-        load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, hk), d0, p.Dv, vec, vv);
+    const auto step = [&](const float (&kv)[DPL], const float (&vv)[DPL]) {
         float s = 0.f, dp = 0.f;
 #pragma unroll
         for (int j = 0; j < DPL; ++j) { s = fmaf(qv[j], kv[j], s); dp = fmaf(dov[j], vv[j], dp); }
@@ -283,7 +421,33 @@ __global__ __launch_bounds__(256) void k_bwd_dq(Prob p, int vec, int split, cons
         const float ds = expf(s - L) * (dp - di);
 #pragma unroll
         for (int j = 0; j < DPL; ++j) acc[j] = fmaf(ds, kv[j], acc[j]);
-    });
+    };
+    if (vec) {
+        struct Step {
+            Raw<T, DPL> k, v;
+        };
+        walk_neighbors_pipelined<pipe_depth<T, DPL, 2>()>(
+            p, Q.i0, Q.i1, Q.i2, sp, split,
+            [&](int j0, int j1, int j2, int) {
+                return Step{fetch_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk),
+                            fetch_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, hk), d0, p.Dv)};
+            },
+            [&](const Step& st, int, bool ok) {
+                if (!ok) return;
+                float kv[DPL], vv[DPL];
+                unpack_run<T, DPL>(st.k, d0, p.Dqk, kv);
+                unpack_run<T, DPL>(st.v, d0, p.Dv, vv);
+                step(kv, vv);
+            });
+    } else {
+        for_each_neighbor_split(p, Q.i0, Q.i1, Q.i2, sp, split, [&](int j0, int j1, int j2, int, bool ok) {
+            if (!ok) return;
+            float kv[DPL], vv[DPL];
+            load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, hk), d0, p.Dqk, vec, kv);
+            load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, hk), d0, p.Dv, vec, vv);
+            step(kv, vv);
+        });
+    }
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[j] = split_sum<LPQ>(acc[j], split) * p.scale;
     if (sp == 0) store_run<T, DPL>(dq + ldq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, acc);
@@ -370,14 +534,34 @@ __global__ __launch_bounds__(256) void k_qk_bwd_q(Prob p, int vec,
     float acc[DPL];
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
-    for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
-        if (!ok) return;
-        const float g = to_f(row[e]);
-        float kv[DPL];
-        load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, Q.h), d0, p.Dqk, vec, kv);
+    if (vec) {
+        struct Step {
+            Raw<T, DPL> k;
+            T g;
+        };
+        walk_neighbors_pipelined<pipe_depth<T, DPL, 1>()>(
+            p, Q.i0, Q.i1, Q.i2, 0, 1,
+            [&](int j0, int j1, int j2, int e) {
+                return Step{fetch_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, Q.h), d0, p.Dqk), row[e]};
+            },
+            [&](Step& st, int, bool ok) {
+                if (!ok) return;
+                const float g = to_f(st.g);
+                float kv[DPL];
+                unpack_run<T, DPL>(st.k, d0, p.Dqk, kv);
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(g, kv[j], acc[j]);
-    });
+                for (int j = 0; j < DPL; ++j) acc[j] = fmaf(g, kv[j], acc[j]);
+            });
+    } else {
+        for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
+            if (!ok) return;
+            const float g = to_f(row[e]);
+            float kv[DPL];
+            load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, Q.h), d0, p.Dqk, vec, kv);
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) acc[j] = fmaf(g, kv[j], acc[j]);
+        });
+    }
     if (p.has_scale) {
 #pragma unroll
         for (int j = 0; j < DPL; ++j) acc[j] *= p.scale;
@@ -426,6 +610,21 @@ __global__ __launch_bounds__(256) void k_av_bwd_a(Prob p, int vec,
     float dov[DPL];
     load_run<T, DPL>(dout + ldo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, dov);
     T* row = da + lda.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h);
+    if (vec) {
+        walk_neighbors_pipelined<pipe_depth<T, DPL, 1>()>(
+            p, Q.i0, Q.i1, Q.i2, 0, 1,
+            [&](int j0, int j1, int j2, int) { return fetch_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, Q.h), d0, p.Dv); },
+            [&](const Raw<T, DPL>& r, int e, bool ok) {
+                float vv[DPL];
+                unpack_run<T, DPL>(r, d0, p.Dv, vv);
+                float acc = 0.f;
+#pragma unroll
+                for (int j = 0; j < DPL; ++j) acc = fmaf(dov[j], vv[j], acc);
+                const float g = ok ? group_sum<LPQ>(acc) : 0.f;
+                if (d0 == 0) row[e] = from_f<T>(g);
+            });
+        return;
+    }
     for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
         float g = 0.f;
         if (ok) {
