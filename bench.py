@@ -1,7 +1,7 @@
 """Benchmark of the hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--dilation 1] [--no-cpu] [--no-graph]
-                    [--config 3] [--causal FF]
+                    [--no-split] [--config 3] [--causal FF]
 
 Default workload: na2d forward+backward at DiNAT scale (B=16, 56x56, 4 heads,
 head dim 32, kernel 7, bf16), BASELINE config 3.  ``--config N`` runs another
@@ -24,7 +24,10 @@ eager one is in ``config.eager_ms_per_step``).  Prints one JSON line:
   rocprofv3 (FETCH_SIZE x 2 + WRITE_SIZE, calibrated on a copy kernel) for
   the same kernel and workload, read from profiles/traffic.txt when present;
 * cpu_baseline: the CPU oracle (the reference's pure algorithm) timed on the
-  host for a bounded sample of the same workload.
+  host for a bounded sample of the same workload;
+* split_path (config 3): the split composition na2d_qk -> softmax -> na2d_av
+  (forward + backward) timed eagerly, and its largest absolute difference
+  from the fused path's outputs and gradients.
 """
 from __future__ import annotations
 
@@ -108,6 +111,35 @@ def measured_traffic(kernel, workload):
     return None
 
 
+def compare_split(leaves, do, cfg, timed, args):
+    """The split composition of config 3 (na2d_qk -> softmax -> na2d_av,
+    forward + autograd backward) timed like the fused eager step, and its
+    largest absolute difference from the fused path (outputs and gradients)."""
+    import torch
+
+    from natten_mps_amd import functional as F
+
+    ks, dil = cfg["kernel"], cfg["dilation"]
+    scale = cfg["dim"] ** -0.5
+
+    def split_step():
+        attn = F.na2d_qk(leaves[0], leaves[1], kernel_size=ks, dilation=dil, scale=scale)
+        out = F.na2d_av(attn.softmax(-1), leaves[2], kernel_size=ks, dilation=dil)
+        return (out,) + torch.autograd.grad(out, leaves, do)
+
+    def fused_full():
+        out = F.na2d(*leaves, kernel_size=ks, dilation=dil)
+        return (out,) + torch.autograd.grad(out, leaves, do)
+
+    for _ in range(args.warmup):
+        split_step()
+    ms = timed(split_step)
+    a, b = fused_full(), split_step()
+    diff = max(float((x.detach().float() - y.detach().float()).abs().max()) for x, y in zip(a, b))
+    return {"ms_per_step": round(ms, 4), "max_abs_diff": diff, "timing": "eager",
+            "ops": "na2d_qk -> softmax -> na2d_av, forward + backward"}
+
+
 def cpu_baseline(dilation, budget_s=20.0):
     """The oracle (reference pure algorithm, torch on the host CPU) on a
     bounded sample: config 3 at batch 1 (1/16 of the workload), bf16,
@@ -161,6 +193,7 @@ def main():
     ap.add_argument("--causal", default=None, help="config 2 causal flags, e.g. TF")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="time eager steps only")
+    ap.add_argument("--no-split", action="store_true", help="skip the split-path comparison of config 3")
     ap.add_argument("--copy-probe", type=float, default=None, metavar="MB",
                     help="only run device-to-device copies of this many MB (calibrates rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -322,6 +355,19 @@ def main():
     _log(f"step {ms:.4f} ms  {tflops:.2f} TFLOP/s  {sbytes / (ms * 1e-3) / 1e9:.0f} GB/s  "
          f"HBM floor {sbytes / 8e12 * 1e6:.1f} us -> {sbytes / 8e12 / (ms * 1e-3):.1%} of roofline (step)")
 
+    # config 3 asks for the fused path against the split composition
+    # na2d_qk -> softmax -> na2d_av (forward and backward through autograd):
+    # its step time (eager, queued ahead like the fused eager step) and the
+    # largest difference between the two paths' outputs and gradients
+    split_path = None
+    if args.config == 3 and not args.no_split:
+        try:
+            split_path = compare_split(leaves, do, cfg, timed, args)
+            _log(f"split path step {split_path['ms_per_step']:.4f} ms, max |fused - split| "
+                 f"{split_path['max_abs_diff']:.3g}")
+        except Exception as e:  # a comparison, never required
+            _log("split comparison failed:", repr(e))
+
     cpu = None
     if args.config == 3 and not args.no_cpu:
         try:
@@ -354,6 +400,7 @@ def main():
                    "hbm_floor_frac_step": round(sbytes / 8e12 / (ms * 1e-3), 4)},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "split_path": split_path,
     }), flush=True)
 
 
