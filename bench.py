@@ -131,13 +131,20 @@ def compare_split(leaves, do, cfg, timed, args):
         out = F.na2d(*leaves, kernel_size=ks, dilation=dil)
         return (out,) + torch.autograd.grad(out, leaves, do)
 
+    from natten_mps_amd._core import _lib
+
     for _ in range(args.warmup):
         split_step()
     ms = timed(split_step)
+    # per-launch event timing of the library's kernels (the softmax and its
+    # gradient are torch's own), queued behind a spin as for the fused step
+    _lib.profile_read(reset=True)
+    timed(split_step, profile=True, head_start_ms=2.0 * args.steps * ms + 5.0)
+    kernels = {name: round(tot / n * 1e3, 1) for name, (n, tot, _, _) in _lib.profile_read(reset=True).items()}
     a, b = fused_full(), split_step()
     diff = max(float((x.detach().float() - y.detach().float()).abs().max()) for x, y in zip(a, b))
     return {"ms_per_step": round(ms, 4), "max_abs_diff": diff, "timing": "eager",
-            "ops": "na2d_qk -> softmax -> na2d_av, forward + backward"}
+            "ops": "na2d_qk -> softmax -> na2d_av, forward + backward", "kernel_mean_us": kernels}
 
 
 def cpu_baseline(dilation, budget_s=20.0):

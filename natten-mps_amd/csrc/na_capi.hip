@@ -203,8 +203,12 @@ int natten_hip_qk_forward(const natten_problem_t* p, const void* q, const natten
     if (P.rep != 1) return fail(NATTEN_ERR_INVALID, "split QK needs heads_q == heads_kv");
     if (any_null({q, k, attn, lq, lk, la})) return fail(NATTEN_ERR_INVALID, "NULL operand");
     const int vec = runs_aligned(dpl_for(P.Dqk), {{q, lq, P.Dqk}, {k, lk, P.Dqk}}) ? 1 : 0;
-    return launch_status(na::generic_qk(P, vec, q, to_lay(lq), k, to_lay(lk), attn, to_lay(la), p->dtype,
-                                        static_cast<hipStream_t>(stream)),
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (use_mfma() && na::mfma_split_eligible(P, p->dtype, P.Dqk, vec != 0, to_lay(la), {to_lay(lq), to_lay(lk)}))
+        return launch_status(na::mfma_split_dot("na_qk_mfma", P, P.Dqk, q, to_lay(lq), k, to_lay(lk), attn,
+                                                to_lay(la), P.has_scale ? P.scale : 1.f, -INFINITY, p->dtype, s),
+                             "qk_forward");
+    return launch_status(na::generic_qk(P, vec, q, to_lay(lq), k, to_lay(lk), attn, to_lay(la), p->dtype, s),
                          "qk_forward");
 }
 
@@ -216,8 +220,12 @@ int natten_hip_av_forward(const natten_problem_t* p, const void* attn, const nat
     if (P.rep != 1) return fail(NATTEN_ERR_INVALID, "split AV needs heads_q == heads_kv");
     if (any_null({attn, v, out, la, lv, lo})) return fail(NATTEN_ERR_INVALID, "NULL operand");
     const int vec = runs_aligned(dpl_for(P.Dv), {{v, lv, P.Dv}, {out, lo, P.Dv}}) ? 1 : 0;
-    return launch_status(na::generic_av(P, vec, attn, to_lay(la), v, to_lay(lv), out, to_lay(lo), p->dtype,
-                                        static_cast<hipStream_t>(stream)),
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (use_mfma() && na::mfma_split_eligible(P, p->dtype, P.Dv, vec != 0, to_lay(la), {to_lay(lv), to_lay(lo)}))
+        return launch_status(na::mfma_split_wsum("na_av_mfma", P, P.Dv, attn, to_lay(la), v, to_lay(lv), out,
+                                                 to_lay(lo), 1.f, p->dtype, s),
+                             "av_forward");
+    return launch_status(na::generic_av(P, vec, attn, to_lay(la), v, to_lay(lv), out, to_lay(lo), p->dtype, s),
                          "av_forward");
 }
 
@@ -231,9 +239,19 @@ int natten_hip_qk_backward(const natten_problem_t* p, const void* dattn, const n
     if (any_null({dattn, q, k, dq, dk, lda, lq, lk, ldq, ldk})) return fail(NATTEN_ERR_INVALID, "NULL operand");
     const int vec =
         runs_aligned(dpl_for(P.Dqk), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {dq, ldq, P.Dqk}, {dk, ldk, P.Dqk}}) ? 1 : 0;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int sides = na::kQuerySide | na::kKeySide;
+    if (use_mfma() &&
+        na::mfma_split_eligible(P, p->dtype, P.Dqk, vec != 0, to_lay(lda), {to_lay(lk), to_lay(ldq)})) {
+        const int rc2 = launch_status(na::mfma_split_wsum("na_qk_bwd_q_mfma", P, P.Dqk, dattn, to_lay(lda), k,
+                                                          to_lay(lk), dq, to_lay(ldq), P.has_scale ? P.scale : 1.f,
+                                                          p->dtype, s),
+                                      "qk_backward");
+        if (rc2) return rc2;
+        sides = na::kKeySide;
+    }
     return launch_status(na::generic_qk_backward(P, vec, dattn, to_lay(lda), q, to_lay(lq), k, to_lay(lk), dq,
-                                                 to_lay(ldq), dk, to_lay(ldk), p->dtype,
-                                                 static_cast<hipStream_t>(stream)),
+                                                 to_lay(ldq), dk, to_lay(ldk), p->dtype, s, sides),
                          "qk_backward");
 }
 
@@ -247,9 +265,18 @@ int natten_hip_av_backward(const natten_problem_t* p, const void* dout, const na
     if (P.rep != 1) return fail(NATTEN_ERR_INVALID, "split AV needs heads_q == heads_kv");
     if (any_null({dout, attn, v, dattn, dv, ldo, la, lv, lda, ldv})) return fail(NATTEN_ERR_INVALID, "NULL operand");
     const int vec = runs_aligned(dpl_for(P.Dv), {{dout, ldo, P.Dv}, {v, lv, P.Dv}, {dv, ldv, P.Dv}}) ? 1 : 0;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int sides = na::kQuerySide | na::kKeySide;
+    if (use_mfma() &&
+        na::mfma_split_eligible(P, p->dtype, P.Dv, vec != 0, to_lay(lda), {to_lay(ldo), to_lay(lv)})) {
+        const int rc2 = launch_status(na::mfma_split_dot("na_av_bwd_a_mfma", P, P.Dv, dout, to_lay(ldo), v,
+                                                         to_lay(lv), dattn, to_lay(lda), 1.f, 0.f, p->dtype, s),
+                                      "av_backward");
+        if (rc2) return rc2;
+        sides = na::kKeySide;
+    }
     return launch_status(na::generic_av_backward(P, vec, dout, to_lay(ldo), attn, to_lay(la), v, to_lay(lv), dattn,
-                                                 to_lay(lda), dv, to_lay(ldv), p->dtype,
-                                                 static_cast<hipStream_t>(stream)),
+                                                 to_lay(lda), dv, to_lay(ldv), p->dtype, s, sides),
                          "av_backward");
 }
 

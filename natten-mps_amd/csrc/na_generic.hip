@@ -808,12 +808,15 @@ struct LBackward {
 template <typename T, int DPL, int LPQ>
 struct LQKBwd {
     static hipError_t run(const Prob& p, int vec, const void* da, Lay lda, const void* q, Lay lq, const void* k,
-                          Lay lk, void* dq, Lay ldq, void* dk, Lay ldk, hipStream_t s) {
-        const long long nq = static_cast<long long>(p.B) * p.nout * p.Hq;
-        NA_LAUNCH("na_qk_bwd_q", (k_qk_bwd_q<T, DPL, LPQ>), dim3(grid_for(nq, LPQ)), dim3(256), 0, s, p, vec,
-                           (const T*)da, lda, (const T*)k, lk, (T*)dq, ldq);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+                          Lay lk, void* dq, Lay ldq, void* dk, Lay ldk, int sides, hipStream_t s) {
+        if (sides & kQuerySide) {
+            const long long nq = static_cast<long long>(p.B) * p.nout * p.Hq;
+            NA_LAUNCH("na_qk_bwd_q", (k_qk_bwd_q<T, DPL, LPQ>), dim3(grid_for(nq, LPQ)), dim3(256), 0, s, p, vec,
+                      (const T*)da, lda, (const T*)k, lk, (T*)dq, ldq);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+        if (!(sides & kKeySide)) return hipSuccess;
         const long long nk = static_cast<long long>(p.B) * p.nkey * p.Hkv;
         NA_LAUNCH("na_qk_bwd_k", (k_qk_bwd_k<T, DPL, LPQ>), dim3(grid_for(nk, LPQ)), dim3(256), 0, s, p, vec,
                            (const T*)da, lda, (const T*)q, lq, (T*)dk, ldk);
@@ -824,12 +827,15 @@ struct LQKBwd {
 template <typename T, int DPL, int LPQ>
 struct LAVBwd {
     static hipError_t run(const Prob& p, int vec, const void* dout, Lay ldo, const void* a, Lay la, const void* v,
-                          Lay lv, void* da, Lay lda, void* dv, Lay ldv, hipStream_t s) {
-        const long long nq = static_cast<long long>(p.B) * p.nout * p.Hq;
-        NA_LAUNCH("na_av_bwd_a", (k_av_bwd_a<T, DPL, LPQ>), dim3(grid_for(nq, LPQ)), dim3(256), 0, s, p, vec,
-                           (const T*)dout, ldo, (const T*)v, lv, (T*)da, lda);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+                          Lay lv, void* da, Lay lda, void* dv, Lay ldv, int sides, hipStream_t s) {
+        if (sides & kQuerySide) {
+            const long long nq = static_cast<long long>(p.B) * p.nout * p.Hq;
+            NA_LAUNCH("na_av_bwd_a", (k_av_bwd_a<T, DPL, LPQ>), dim3(grid_for(nq, LPQ)), dim3(256), 0, s, p, vec,
+                      (const T*)dout, ldo, (const T*)v, lv, (T*)da, lda);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+        if (!(sides & kKeySide)) return hipSuccess;
         const long long nk = static_cast<long long>(p.B) * p.nkey * p.Hkv;
         NA_LAUNCH("na_av_bwd_v", (k_av_bwd_v<T, DPL, LPQ>), dim3(grid_for(nk, LPQ)), dim3(256), 0, s, p, vec,
                            (const T*)dout, ldo, (const T*)a, la, (T*)dv, ldv);
@@ -865,14 +871,14 @@ hipError_t generic_backward(const Prob& p, int vec, const void* q, Lay lq, const
 
 hipError_t generic_qk_backward(const Prob& p, int vec, const void* da, Lay lda, const void* q, Lay lq,
                                const void* k, Lay lk, void* dq, Lay ldq, void* dk, Lay ldk, int dtype,
-                               hipStream_t s) {
-    return by_type<LQKBwd>(dtype, p.Dqk, p, vec, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, s);
+                               hipStream_t s, int sides) {
+    return by_type<LQKBwd>(dtype, p.Dqk, p, vec, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, sides, s);
 }
 
 hipError_t generic_av_backward(const Prob& p, int vec, const void* dout, Lay ldo, const void* a, Lay la,
                                const void* v, Lay lv, void* da, Lay lda, void* dv, Lay ldv, int dtype,
-                               hipStream_t s) {
-    return by_type<LAVBwd>(dtype, p.Dv, p, vec, dout, ldo, a, la, v, lv, da, lda, dv, ldv, s);
+                               hipStream_t s, int sides) {
+    return by_type<LAVBwd>(dtype, p.Dv, p, vec, dout, ldo, a, la, v, lv, da, lda, dv, ldv, sides, s);
 }
 
 hipError_t neighborhood_map(const Prob& p, int64_t* flat, uint8_t* valid, hipStream_t s) {

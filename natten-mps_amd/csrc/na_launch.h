@@ -22,12 +22,15 @@ hipError_t generic_backward(const Prob& p, int vec, const void* q, Lay lq, const
                             Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                             const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
                             float* delta, Lay lde, int dtype, hipStream_t s, const int* lens = nullptr);
+// Split backward: `sides` selects the query side (dq / dattn) and the key
+// side (dk / dv).
+constexpr int kQuerySide = 1, kKeySide = 2;
 hipError_t generic_qk_backward(const Prob& p, int vec, const void* da, Lay lda, const void* q, Lay lq,
                                const void* k, Lay lk, void* dq, Lay ldq, void* dk, Lay ldk, int dtype,
-                               hipStream_t s);
+                               hipStream_t s, int sides = kQuerySide | kKeySide);
 hipError_t generic_av_backward(const Prob& p, int vec, const void* dout, Lay ldo, const void* a, Lay la,
                                const void* v, Lay lv, void* da, Lay lda, void* dv, Lay ldv, int dtype,
-                               hipStream_t s);
+                               hipStream_t s, int sides = kQuerySide | kKeySide);
 hipError_t neighborhood_map(const Prob& p, int64_t* flat, uint8_t* valid, hipStream_t s);
 
 // Relative-position-bias split ops (na_rpb.hip): padded axes 1 and 2 carry
@@ -62,5 +65,16 @@ hipError_t mfma_backward(const Prob& p, const void* q, Lay lq, const void* k, La
                          const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                          const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
                          float* delta, Lay lde, int dtype, hipStream_t s);
+
+// Split ops on the MFMA tile path, query side: `rows` is the operand of KV
+// entries per query (attn or dattn), `staged` the operands staged per tile.
+bool mfma_split_eligible(const Prob& p, int dtype, int D, bool aligned, const Lay& rows,
+                         std::initializer_list<Lay> staged);
+// out[q][e] = mul * (a[q] . x[nbr(q, e)]), `fill` at invalid neighbours.
+hipError_t mfma_split_dot(const char* name, const Prob& p, int D, const void* a, Lay la, const void* x, Lay lx,
+                          void* o, Lay lo, float mul, float fill, int dtype, hipStream_t s);
+// out[q] = mul * sum over valid e of w[q][e] x[nbr(q, e)].
+hipError_t mfma_split_wsum(const char* name, const Prob& p, int D, const void* w, Lay lw, const void* x, Lay lx,
+                           void* o, Lay lo, float mul, int dtype, hipStream_t s);
 
 }  // namespace na

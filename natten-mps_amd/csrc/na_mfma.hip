@@ -423,7 +423,7 @@ __device__ __forceinline__ const T* plane_of(const T* g, const LayK& lay, int b,
 }
 
 // Staging of union slices into X[slot][D], two operands at a time (same
-// slot layout, own strides): each wave instruction moves R = 64 / (D/8)
+// slot layout, own strides; one when PAIR is false): each wave instruction moves R = 64 / (D/8)
 // rows, lane l the 16-byte piece l % (D/8) of row l / (D/8), holding logical
 // piece (l % (D/8)) ^ swz(row).  With slot = iR + l/(D/8), union row and
 // column split into an instruction part (scalar) and a lane part fixed per
@@ -450,7 +450,7 @@ __device__ __forceinline__ StageMap stage_map(const Prob& p, const TileShape& ts
     return m;
 }
 
-template <typename T, int D>
+template <typename T, int D, bool PAIR = true>
 __device__ __forceinline__ void stage_pair(const Prob& p, const Block& k, const TileShape& ts, const StageMap& m,
                                            const T* plane_a, const LayK& la, T* Xa, const T* plane_b, const LayK& lb,
                                            T* Xb, int wave) {
@@ -479,7 +479,7 @@ __device__ __forceinline__ void stage_pair(const Prob& p, const Block& k, const 
         const uint32_t oa = static_cast<uint32_t>(sa + m.lane_a + kb) | bad;
         const uint32_t ob = static_cast<uint32_t>(sb + m.lane_b + kb) | bad;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(Xa + i * R * D), 16, oa, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(Xb + i * R * D), 16, ob, 0, 0, 0);
+        if constexpr (PAIR) __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(Xb + i * R * D), 16, ob, 0, 0, 0);
     }
 }
 
@@ -978,6 +978,228 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_k
     }
 }
 
+// ---------------------------------------------------------------------------
+// Split products, query side (the split QK / AV ops and the query side of
+// their backward), over the union the forward stages:
+//   k_dot_mfma:  out[q][e] = mul * (a[q] . x[nbr(q, e)]) for each valid
+//                neighbour e, `fill` for the others (QK: a = q, x = k,
+//                fill -inf; AV backward dattn: a = dO, x = v, fill 0);
+//   k_wsum_mfma: out[q] = mul * sum over valid e of w[q][e] x[nbr(q, e)]
+//                (AV: w = attn, x = v; QK backward dq: w = dattn, x = k).
+//
+// Rows of KV entries (row-major over the kernel axes, contiguous in global
+// memory) pass through an LDS block per wave: 16 rows, one per query, each
+// with its kernel rows (n0, n1) spread P2 = K2 + 8 entries apart and 8
+// entries ahead of the first, so that every run of K2 entries has 8 spare
+// entries on either side.  A lane's 8 slots of a chunk are consecutive
+// columns of one union row, i.e. consecutive entries of one kernel row; when
+// they meet the window at all, the 8 entries they address stay inside that
+// row's run and its spares.  Reads of spares give 0 (the wsum block is
+// cleared first), writes to spares are never read back (dot), so the chunk
+// loop needs no per-entry tests.  Global memory sees whole rows: one
+// 16-bit buffer access per query, lanes over consecutive entries, the row's
+// offset in a scalar register.
+// ---------------------------------------------------------------------------
+
+// LDS block of one wave, in 16-bit entries: 16 rows of `pitch` entries, then
+// 8 zero entries (reads of chunks outside the window) and 8 entries that
+// writes of such chunks go to.
+struct RowBlock {
+    int p2, pitch;
+};
+
+__host__ __device__ inline RowBlock row_block(const Prob& p) {
+    RowBlock r;
+    r.p2 = p.ax[2].k + 8;
+    r.pitch = (p.ax[0].k * p.ax[1].k * r.p2 + 8 + 1) & ~1;
+    return r;
+}
+
+__host__ __device__ inline int row_block_entries(const Prob& p) { return 16 * row_block(p).pitch + 16; }
+
+// Entry index (from the lane's row start) of the first of the lane's slots
+// of chunk c, or -1 when those 8 slots miss its window.
+__device__ __forceinline__ int chunk_entry(const Prob& p, const Lane& ln, const RowBlock& rb, int rowshift, bool in0,
+                                           int u0, int c, int grp) {
+    const int s0 = 32 * c + 8 * grp, r = s0 >> rowshift, col0 = s0 & ((1 << rowshift) - 1);
+    const bool ok = in0 && r >= ln.lo[1] && r <= ln.hi[1] && col0 <= ln.hi[2] && col0 + 7 >= ln.lo[2];
+    return ok ? ((u0 - ln.lo[0]) * p.ax[1].k + r - ln.lo[1]) * rb.p2 + 8 + col0 - ln.lo[2] : -1;
+}
+
+// Position in a row block of the entries e = lane + 64 t (t < 4) a lane
+// moves between global memory and LDS, -1 past the row's end.
+__device__ __forceinline__ void lane_entries(const Prob& p, const RowBlock& rb, int lane, int (&pos)[4]) {
+    const int k2 = p.ax[2].k;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int e = lane + 64 * t;
+        pos[t] = e < p.kv ? (e / k2) * rb.p2 + 8 + e % k2 : -1;
+    }
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), kPlaneBytes, 0x00020000);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_dot_mfma(Prob p, TileShape ts, const int* __restrict__ geo,
+                                                  const T* __restrict__ a, LayK la, const T* __restrict__ xg, LayK lx,
+                                                  T* __restrict__ out, LayK lo, float mul, float fill) {
+    unsigned char* smem = lds_base();
+    T* Xs = reinterpret_cast<T*>(smem);
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
+    const RowBlock rb = row_block(p);
+    uint16_t* const Rw = reinterpret_cast<uint16_t*>(Xs + ts.slots * D) + wave * row_block_entries(p);
+    uint16_t* const dummy = Rw + 16 * rb.pitch + 8;
+    Block blk;
+    WaveGeo wg;
+    if (!tile_geometry<false>(p, ts, geo, wave, blk, wg)) return;
+    const StageMap sm = stage_map<T, D>(p, ts, lx, lx, lane);
+    Walk w;
+    walk_start(blk, w);
+    {
+        const T* pl = plane_of(xg, lx, w.b, w.h, slice_pos(p, blk, 0));
+        stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
+    }
+    const Lane ln = lane_item(p, ts, blk, wave, col, false);
+    const int orow = ln.valid ? vol_off(lo, ln.pos) : -1;
+    int epos[4];
+    lane_entries(p, rb, lane, epos);
+    const f32x4_t zero[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+    const uint32_t fill2 = Mma<T>::pack(fill, fill);
+    const uint4 fill8 = make_uint4(fill2, fill2, fill2, fill2);
+    uint16_t* const myrow = Rw + col * rb.pitch;
+    const int nfill = rb.pitch * 2;  // 16-byte pieces of the 16 rows
+    uint4 af[D / 32];
+    bool more = true, fresh = true;
+    while (more) {
+        const int b = w.b, h = w.h, u0 = w.u0;
+        if (fresh) {
+            load_frags<T, D>(bh_ptr(a, la, b, h), vol_off(la, ln.pos), ln.valid, grp, af);
+            for (int i = lane; i < nfill; i += 64) reinterpret_cast<uint4*>(Rw)[i] = fill8;
+        }
+        wait_loads();
+        __syncthreads();
+        if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
+            const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
+            for (int c = wg.c0; c <= wg.c1; ++c) {
+                f32x4_t sc[2];
+                score_chunk<T, D>(Xs, c, col, grp, af, zero, sc);
+                const int e0 = chunk_entry(p, ln, rb, ts.rowshift, in0, u0, c, grp);
+                uint16_t* dst = e0 >= 0 ? myrow + e0 : dummy;
+#pragma unroll
+                for (int i = 0; i < 8; i += 2) {
+                    const uint32_t v = Mma<T>::pack(sc[i >> 2][i & 3] * mul, sc[i >> 2][(i & 3) + 1] * mul);
+                    dst[i] = static_cast<uint16_t>(v);
+                    dst[i + 1] = static_cast<uint16_t>(v >> 16);
+                }
+            }
+        }
+        more = walk_next(blk, w, fresh);
+        __syncthreads();  // the slice is no longer read
+        if (more) {
+            const T* pl = plane_of(xg, lx, w.b, w.h, slice_pos(p, blk, w.u0));
+            stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
+        }
+        if (fresh || !more) {
+            // the 16 rows, 64 entries at a time: all LDS reads, then the stores
+            const __amdgpu_buffer_rsrc_t ro = rows_rsrc(bh_ptr(out, lo, b, h));
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (64 * t >= p.kv) break;
+                if (epos[t] >= 0) {
+                    uint16_t v[16];
+#pragma unroll
+                    for (int qq = 0; qq < 16; ++qq) v[qq] = Rw[qq * rb.pitch + epos[t]];
+#pragma unroll
+                    for (int qq = 0; qq < 16; ++qq) {
+                        const int off = __builtin_amdgcn_readlane(orow, qq);
+                        if (off >= 0) __builtin_amdgcn_raw_buffer_store_b16(v[qq], ro, (lane + 64 * t) * 2, off * 2, 0);
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_wsum_mfma(Prob p, TileShape ts, const int* __restrict__ geo,
+                                                   const T* __restrict__ wt, LayK lw, const T* __restrict__ xg,
+                                                   LayK lx, T* __restrict__ out, LayK lo, float mul) {
+    unsigned char* smem = lds_base();
+    T* Xs = reinterpret_cast<T*>(smem);
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
+    const RowBlock rb = row_block(p);
+    uint16_t* const Rw = reinterpret_cast<uint16_t*>(Xs + ts.slots * D) + wave * row_block_entries(p);
+    const uint16_t* const zeros = Rw + 16 * rb.pitch;
+    Block blk;
+    WaveGeo wg;
+    if (!tile_geometry<false>(p, ts, geo, wave, blk, wg)) return;
+    const StageMap sm = stage_map<T, D>(p, ts, lx, lx, lane);
+    Walk w;
+    walk_start(blk, w);
+    {
+        const T* pl = plane_of(xg, lx, w.b, w.h, slice_pos(p, blk, 0));
+        stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
+    }
+    const Lane ln = lane_item(p, ts, blk, wave, col, false);
+    const int wrow = ln.valid ? vol_off(lw, ln.pos) : -1;
+    int epos[4];
+    lane_entries(p, rb, lane, epos);
+    const uint16_t* const myrow = Rw + col * rb.pitch;
+    const int nclear = rb.pitch * 2 + 2;  // 16-byte pieces of the block
+    f32x4_t acc[D / 16];
+    bool more = true, fresh = true;
+    while (more) {
+        const int b = w.b, h = w.h, u0 = w.u0;
+        if (fresh) {
+#pragma unroll
+            for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            for (int i = lane; i < nclear; i += 64) reinterpret_cast<uint4*>(Rw)[i] = make_uint4(0u, 0u, 0u, 0u);
+            // the 16 rows, 64 entries at a time: all loads, then the LDS
+            // writes (rows of queries past the tile read row 0 and are never
+            // read back)
+            const __amdgpu_buffer_rsrc_t rw = rows_rsrc(bh_ptr(wt, lw, b, h));
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (64 * t >= p.kv) break;
+                if (epos[t] >= 0) {
+                    uint16_t v[16];
+#pragma unroll
+                    for (int qq = 0; qq < 16; ++qq)
+                        v[qq] = __builtin_amdgcn_raw_buffer_load_b16(
+                            rw, (lane + 64 * t) * 2, max(__builtin_amdgcn_readlane(wrow, qq), 0) * 2, 0);
+#pragma unroll
+                    for (int qq = 0; qq < 16; ++qq) Rw[qq * rb.pitch + epos[t]] = v[qq];
+                }
+            }
+        }
+        wait_loads();
+        __syncthreads();
+        if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
+            const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
+            for (int c = wg.c0; c <= wg.c1; ++c) {
+                const int e0 = chunk_entry(p, ln, rb, ts.rowshift, in0, u0, c, grp);
+                const uint16_t* src = e0 >= 0 ? myrow + e0 : zeros;
+                uint32_t wv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    wv[i] = static_cast<uint32_t>(src[2 * i]) | (static_cast<uint32_t>(src[2 * i + 1]) << 16);
+                accumulate_chunk<T, D>(Xs, c, lane, make_uint4(wv[0], wv[1], wv[2], wv[3]), acc);
+            }
+        }
+        more = walk_next(blk, w, fresh);
+        __syncthreads();  // the slice is no longer read
+        if (more) {
+            const T* pl = plane_of(xg, lx, w.b, w.h, slice_pos(p, blk, w.u0));
+            stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
+        }
+        if ((fresh || !more) && ln.valid) store_rows<T, D>(bh_ptr(out, lo, b, h), vol_off(lo, ln.pos), grp, acc, mul);
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -986,7 +1208,13 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_k
 
 namespace {
 
-enum Kind { kForward = 0, kBackwardQ = 1, kBackwardKV = 2 };
+enum Kind { kForward = 0, kBackwardQ = 1, kBackwardKV = 2, kSplit = 3 };
+
+// Entries per row (KV) up to which the split kernels take a call (a lane
+// moves at most 4 entries of a row), and the LDS their row blocks may take
+// per workgroup.
+constexpr int kSplitMaxKV = 256;
+constexpr size_t kSplitRowsBudget = 48 * 1024;
 
 constexpr size_t kLdsBudget = 64 * 1024;
 
@@ -1028,8 +1256,10 @@ int union_extent(const Axis& A, int T, bool key_tile) {
     return best;
 }
 
+// Staged operands (split kernels: one; their row blocks come on top).
 size_t lds_bytes(Kind kind, int slots, int D) {
     const size_t rows = static_cast<size_t>(slots) * D * 2;
+    if (kind == kSplit) return kLdsPad + rows;
     return kLdsPad + (kind == kBackwardKV ? 2 * rows + (2 * static_cast<size_t>(slots) + 8) * 4 : 2 * rows);
 }
 
@@ -1381,7 +1611,95 @@ hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
 #undef NA_BWD_LAY
 }
 
+// Split kernels: one staged operand plus a row block per wave.  Heads of q
+// and k/v are equal for the split ops (rep 1).
+size_t split_lds_bytes(const Prob& p, const TileShape& ts, int D) {
+    return lds_bytes(kSplit, ts.slots, D) + static_cast<size_t>(ts.waves) * row_block_entries(p) * 2;
+}
+
+template <typename T, int D>
+hipError_t run_dot(const char* name, const Prob& p, const void* a, Lay la, const void* x, Lay lx, void* o, Lay lo,
+                   float mul, float fill, hipStream_t s) {
+    TileShape ts{};
+    if (!choose_tile(p, kSplit, D, ts)) return hipErrorInvalidValue;
+    const auto kern = k_dot_mfma<T, D>;
+    const size_t shm = split_lds_bytes(p, ts, D);
+    hipError_t e = allow_lds(kern, shm);
+    if (e != hipSuccess) return e;
+    fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    const int* geo = geometry_table(p, ts, false, s);
+    NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, p, ts, geo,
+              (const T*)a, to_k(la), (const T*)x, to_k(lx), (T*)o, to_k(lo), mul, fill);
+    return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t run_wsum(const char* name, const Prob& p, const void* w, Lay lw, const void* x, Lay lx, void* o, Lay lo,
+                    float mul, hipStream_t s) {
+    TileShape ts{};
+    if (!choose_tile(p, kSplit, D, ts)) return hipErrorInvalidValue;
+    const auto kern = k_wsum_mfma<T, D>;
+    const size_t shm = split_lds_bytes(p, ts, D);
+    hipError_t e = allow_lds(kern, shm);
+    if (e != hipSuccess) return e;
+    fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    const int* geo = geometry_table(p, ts, false, s);
+    NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, p, ts, geo,
+              (const T*)w, to_k(lw), (const T*)x, to_k(lx), (T*)o, to_k(lo), mul);
+    return hipGetLastError();
+}
+
+// Rows of KV entries: non-negative strides, every entry of one (batch, head)
+// at a 31-bit offset.
+bool rows_fit(const Prob& p, const Lay& l) {
+    if (l.b < 0 || l.s0 < 0 || l.s1 < 0 || l.s2 < 0 || l.h < 0) return false;
+    const long long vol = (static_cast<long long>(p.ax[0].len) - 1) * l.s0 +
+                          (static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
+                          (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + p.kv;
+    return vol < (1LL << 31);
+}
+
 }  // namespace
+
+bool mfma_split_eligible(const Prob& p, int dtype, int D, bool aligned, const Lay& rows,
+                         std::initializer_list<Lay> staged) {
+    if (dtype == NATTEN_F32 || !aligned || p.rep != 1) return false;
+    if (!(D == 32 || D == 64 || D == 128) || p.kv > kSplitMaxKV) return false;
+    if (static_cast<size_t>(4) * row_block_entries(p) * 2 > kSplitRowsBudget) return false;
+    for (int a = 0; a < 3; ++a)
+        if (p.ax[a].st != 1) return false;
+    TileShape ts{};
+    if (!choose_tile(p, kSplit, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
+    return rows_fit(p, rows) && offsets_fit(p, staged);
+}
+
+hipError_t mfma_split_dot(const char* name, const Prob& p, int D, const void* a, Lay la, const void* x, Lay lx,
+                          void* o, Lay lo, float mul, float fill, int dtype, hipStream_t s) {
+#define NA_DOT(T, DD) return run_dot<T, DD>(name, p, a, la, x, lx, o, lo, mul, fill, s)
+    if (dtype == NATTEN_BF16) {
+        if (D == 32) NA_DOT(bf16, 32);
+        if (D == 64) NA_DOT(bf16, 64);
+        NA_DOT(bf16, 128);
+    }
+    if (D == 32) NA_DOT(f16, 32);
+    if (D == 64) NA_DOT(f16, 64);
+    NA_DOT(f16, 128);
+#undef NA_DOT
+}
+
+hipError_t mfma_split_wsum(const char* name, const Prob& p, int D, const void* w, Lay lw, const void* x, Lay lx,
+                           void* o, Lay lo, float mul, int dtype, hipStream_t s) {
+#define NA_WSUM(T, DD) return run_wsum<T, DD>(name, p, w, lw, x, lx, o, lo, mul, s)
+    if (dtype == NATTEN_BF16) {
+        if (D == 32) NA_WSUM(bf16, 32);
+        if (D == 64) NA_WSUM(bf16, 64);
+        NA_WSUM(bf16, 128);
+    }
+    if (D == 32) NA_WSUM(f16, 32);
+    if (D == 64) NA_WSUM(f16, 64);
+    NA_WSUM(f16, 128);
+#undef NA_WSUM
+}
 
 bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward) {
     if (dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f)) return false;

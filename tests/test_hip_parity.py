@@ -278,6 +278,63 @@ def test_split_qk_av(case, dtype):
     _close(vd.grad.cpu(), ref_v.grad, dtype, "dv")
 
 
+SPLIT_TILE = [
+    (1, (200,), (9,), (3,), (True,), None),
+    (1, (150,), (33,), (1,), (False,), 0.2),
+    (2, (17, 19), (7, 7), (1, 1), (False, False), None),
+    (2, (20, 23), (5, 7), (2, 3), (True, False), 0.3),
+    (3, (6, 9, 10), (3, 3, 5), (1, 2, 1), (False, True, False), None),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_TILE)
+@pytest.mark.parametrize("dim,dtype", [(32, torch.bfloat16), (64, torch.float16), (128, torch.bfloat16)])
+def test_split_ops_tile_path(case, dim, dtype):
+    """The split QK / AV ops at head dims 32/64/128 in 16-bit run the MFMA tile
+    kernels (query side: logits, AV output, dq, dattn) and match the oracle."""
+    from natten_mps_amd import functional as F
+    from natten_mps_amd._core import _lib
+
+    rank, sp, ks, dil, causal, scale = case
+    q, k, v = _inputs(81, [(2, *sp, 2, dim)] * 3, dtype)
+    qk = getattr(F, f"na{rank}d_qk")
+    av = getattr(F, f"na{rank}d_av")
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        qd, kd = q.to(DEV).requires_grad_(True), k.to(DEV).requires_grad_(True)
+        logits = qk(qd, kd, ks, dil, is_causal=causal, scale=scale)
+        ref_q, ref_k = q.float().requires_grad_(True), k.float().requires_grad_(True)
+        ref_logits = getattr(P, f"na{rank}d_qk_forward")(ref_q, ref_k, ks, dil, (1,) * rank, causal, scale)
+        finite = torch.isfinite(ref_logits)
+        assert torch.equal(torch.isfinite(logits.detach().cpu()), finite)
+        _close(logits.detach().cpu()[finite], ref_logits.detach()[finite], dtype, "logits")
+        (dl,) = _inputs(82, [tuple(ref_logits.shape)], dtype)
+        dl = torch.where(finite, dl, torch.zeros_like(dl))
+        logits.backward(dl.to(DEV))
+        ref_logits.backward(dl.float())
+        _close(qd.grad.cpu(), ref_q.grad, dtype, "dq")
+        _close(kd.grad.cpu(), ref_k.grad, dtype, "dk")
+
+        attn = torch.softmax(torch.where(finite, ref_logits.detach(), torch.full_like(ref_logits, -1e30)), -1)
+        ad, vd = attn.to(dtype).to(DEV).requires_grad_(True), v.to(DEV).requires_grad_(True)
+        out = av(ad, vd, ks, dil, is_causal=causal)
+        ref_a, ref_v = attn.to(dtype).float().requires_grad_(True), v.float().requires_grad_(True)
+        ref_out = getattr(P, f"na{rank}d_av_forward")(ref_a, ref_v, ks, dil, (1,) * rank, causal)
+        _close(out.detach().cpu(), ref_out.detach(), dtype, "av out")
+        (do,) = _inputs(83, [tuple(ref_out.shape)], dtype)
+        out.backward(do.to(DEV))
+        ref_out.backward(do.float())
+        _close(ad.grad.cpu(), ref_a.grad, dtype, "dattn")
+        _close(vd.grad.cpu(), ref_v.grad, dtype, "dv")
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    ran = _lib.profile_read(reset=True)
+    for name in ("na_qk_mfma", "na_av_mfma", "na_qk_bwd_q_mfma", "na_av_bwd_a_mfma"):
+        assert ran.get(name, (0,))[0] >= 1, (name, sorted(ran))
+
+
 def test_fused_equals_split_composition():
     """Reference check (tests/test_backward_parity.py): fused vs split QK ->
     softmax -> AV, outputs and gradients."""
