@@ -250,6 +250,16 @@ int natten_hip_qk_backward(const natten_problem_t* p, const void* dattn, const n
         if (rc2) return rc2;
         sides = na::kKeySide;
     }
+    if (use_mfma() &&
+        na::mfma_split_key_eligible(P, p->dtype, P.Dqk, vec != 0, to_lay(lda), {to_lay(lq), to_lay(ldk)})) {
+        const int rc2 = launch_status(na::mfma_split_wsum_key("na_qk_bwd_k_mfma", P, P.Dqk, dattn, to_lay(lda), q,
+                                                              to_lay(lq), dk, to_lay(ldk),
+                                                              P.has_scale ? P.scale : 1.f, p->dtype, s),
+                                      "qk_backward");
+        if (rc2) return rc2;
+        sides &= ~na::kKeySide;
+    }
+    if (!sides) return NATTEN_OK;
     return launch_status(na::generic_qk_backward(P, vec, dattn, to_lay(lda), q, to_lay(lq), k, to_lay(lk), dq,
                                                  to_lay(ldq), dk, to_lay(ldk), p->dtype, s, sides),
                          "qk_backward");
@@ -275,6 +285,15 @@ int natten_hip_av_backward(const natten_problem_t* p, const void* dout, const na
         if (rc2) return rc2;
         sides = na::kKeySide;
     }
+    if (use_mfma() &&
+        na::mfma_split_key_eligible(P, p->dtype, P.Dv, vec != 0, to_lay(la), {to_lay(ldo), to_lay(ldv)})) {
+        const int rc2 = launch_status(na::mfma_split_wsum_key("na_av_bwd_v_mfma", P, P.Dv, attn, to_lay(la), dout,
+                                                              to_lay(ldo), dv, to_lay(ldv), 1.f, p->dtype, s),
+                                      "av_backward");
+        if (rc2) return rc2;
+        sides &= ~na::kKeySide;
+    }
+    if (!sides) return NATTEN_OK;
     return launch_status(na::generic_av_backward(P, vec, dout, to_lay(ldo), attn, to_lay(la), v, to_lay(lv), dattn,
                                                  to_lay(lda), dv, to_lay(ldv), p->dtype, s, sides),
                          "av_backward");

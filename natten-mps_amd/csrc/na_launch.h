@@ -73,6 +73,11 @@ bool mfma_split_eligible(const Prob& p, int dtype, int D, bool aligned, const La
 // out[q][e] = mul * (a[q] . x[nbr(q, e)]), `fill` at invalid neighbours.
 hipError_t mfma_split_dot(const char* name, const Prob& p, int D, const void* a, Lay la, const void* x, Lay lx,
                           void* o, Lay lo, float mul, float fill, int dtype, hipStream_t s);
+// Key side: out[k] = mul * sum over the queries q attending k of w[q][e(q, k)] x[q].
+bool mfma_split_key_eligible(const Prob& p, int dtype, int D, bool aligned, const Lay& rows,
+                             std::initializer_list<Lay> staged);
+hipError_t mfma_split_wsum_key(const char* name, const Prob& p, int D, const void* w, Lay lw, const void* x, Lay lx,
+                               void* o, Lay lo, float mul, int dtype, hipStream_t s);
 // out[q] = mul * sum over valid e of w[q][e] x[nbr(q, e)].
 hipError_t mfma_split_wsum(const char* name, const Prob& p, int D, const void* w, Lay lw, const void* x, Lay lx,
                            void* o, Lay lo, float mul, int dtype, hipStream_t s);

@@ -1200,6 +1200,146 @@ __global__ __launch_bounds__(256) void k_wsum_mfma(Prob p, TileShape ts, const i
     }
 }
 
+// ---------------------------------------------------------------------------
+// Split products, key side: out[k] = mul * sum over the queries q whose
+// window holds key k of w[q][e(q, k)] x[q]  (QK backward dk: w = dattn,
+// x = q, mul = scale; AV backward dv: w = attn, x = dO).  Key tiles as in
+// the key-side backward: per slice, the union of the queries attending the
+// tile's keys is staged (x rows by DMA, and each query's row of w, slot
+// after slot, KV entries each).  In class coordinates e(q, k) = keylin(k) -
+// base(q), keylin = sum_a j_a M_a over the key, base = sum_a ws_a(q) M_a
+// over the query's window start (M = K1 K2, K2, 1); a per-slot table
+// OFF[s] = s KV - base(q_s) leaves one add per (key, slot).  Pairs outside
+// the key's query box are masked: rows per chunk, columns per slot.
+// ---------------------------------------------------------------------------
+
+template <typename T>
+__device__ __forceinline__ void stage_key_rows(const Prob& p, const Block& k, const TileShape& ts, int b, int h,
+                                               int u0, const T* __restrict__ wt, const LayK& lw, int* OFF,
+                                               uint16_t* Ws, int wave, int lane) {
+    const int slots = ts.slots, kv = p.kv, mask2 = (1 << ts.rowshift) - 1;
+    const int k1 = p.ax[1].k, k2 = p.ax[2].k;
+    const int ws0 = class_ws(k.c[0], k.lo[0] + u0);
+    const int p0 = slice_pos(p, k, u0);
+    for (int s = threadIdx.x; s < slots; s += blockDim.x) {
+        const int a1 = s >> ts.rowshift, a2 = s & mask2;
+        const int base = (ws0 * k1 + class_ws(k.c[1], k.lo[1] + a1)) * k2 + class_ws(k.c[2], k.lo[2] + a2);
+        OFF[s] = s * kv - base;
+    }
+    const T* wb = bh_ptr(wt, lw, b, h) + p0 * lw.s0;
+    const __amdgpu_buffer_rsrc_t rw = rows_rsrc(wb);
+    const int d1 = p.ax[1].dil, d2 = p.ax[2].dil;
+    for (int sb = wave * 16; sb < slots; sb += 64) {
+        // lanes 0..15: row offsets of slots sb .. sb + 15 (0 outside the union:
+        // such rows are loaded but never read)
+        int off = 0;
+        {
+            const int s = sb + (lane & 15), a1 = s >> ts.rowshift, a2 = s & mask2;
+            if (a1 < k.U[1] && a2 < k.U[2])
+                off = (k.r[1] + (k.lo[1] + a1) * d1) * lw.s1 + (k.r[2] + (k.lo[2] + a2) * d2) * lw.s2;
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            if (64 * t >= kv) break;
+            const int e = lane + 64 * t;
+            if (e < kv) {
+                uint16_t v[16];
+#pragma unroll
+                for (int m = 0; m < 16; ++m)
+                    v[m] = __builtin_amdgcn_raw_buffer_load_b16(rw, e * 2, __builtin_amdgcn_readlane(off, m) * 2, 0);
+#pragma unroll
+                for (int m = 0; m < 16; ++m) Ws[(sb + m) * kv + e] = v[m];
+            }
+        }
+    }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_wsum_key_mfma(Prob p, TileShape ts, const int* __restrict__ geo,
+                                                       const T* __restrict__ wt, LayK lw, const T* __restrict__ xg,
+                                                       LayK lx, T* __restrict__ out, LayK lo, float mul) {
+    unsigned char* smem = lds_base();
+    const int slots = ts.slots, kv = p.kv;
+    T* Xs = reinterpret_cast<T*>(smem);
+    int* OFF = reinterpret_cast<int*>(Xs + slots * D);
+    uint16_t* Ws = reinterpret_cast<uint16_t*>(OFF + slots);
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
+    Block blk;
+    WaveGeo wg;
+    if (!tile_geometry<true>(p, ts, geo, wave, blk, wg)) return;
+    const StageMap sm = stage_map<T, D>(p, ts, lx, lx, lane);
+    Walk w;
+    walk_start(blk, w);
+    {
+        const T* pl = plane_of(xg, lx, w.b, w.h, slice_pos(p, blk, 0));
+        stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
+    }
+    stage_key_rows<T>(p, blk, ts, w.b, w.h, 0, wt, lw, OFF, Ws, wave, lane);
+    const Lane ln = lane_item(p, ts, blk, wave, col, true);
+    int keylin;
+    {
+        const int f = wave * 16 + col, s2 = ts.tshift[2], s1 = ts.tshift[1];
+        const int e2 = f & (ts.T[2] - 1), e1 = (f >> s2) & (ts.T[1] - 1), e0 = f >> (s2 + s1);
+        keylin = ((blk.J[0] + e0) * p.ax[1].k + blk.J[1] + e1) * p.ax[2].k + blk.J[2] + e2;
+    }
+    const int last = slots * kv - 1;
+    // column masks (two entries per word) of the lane's 8 slots; fixed per
+    // tile when union rows are at most 32 slots
+    const auto col_masks = [&](int c, uint32_t (&cm)[4]) {
+        const int col0 = (32 * c + 8 * grp) & ((1 << ts.rowshift) - 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ca = col0 + 2 * i, cb = ca + 1;
+            cm[i] = ((ca >= ln.lo[2] && ca <= ln.hi[2]) ? 0xFFFFu : 0u) |
+                    ((cb >= ln.lo[2] && cb <= ln.hi[2]) ? 0xFFFF0000u : 0u);
+        }
+    };
+    uint32_t cm0[4];
+    col_masks(0, cm0);
+    const bool wide = ts.rowshift > 5;
+    f32x4_t acc[D / 16];
+    bool more = true, fresh = true;
+    while (more) {
+        const int b = w.b, h = w.h, u0 = w.u0;
+        if (fresh) {
+#pragma unroll
+            for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        wait_loads();
+        lds_publish_barrier();  // staged rows, the rows of w and OFF
+        if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
+            const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
+            for (int c = wg.c0; c <= wg.c1; ++c) {
+                const int s0 = 32 * c + 8 * grp;
+                uint32_t cm[4] = {cm0[0], cm0[1], cm0[2], cm0[3]};
+                if (wide) col_masks(c, cm);
+                const bool rok = row_ok(ln, ts.rowshift, in0, c, grp);
+                const int4 oa = *reinterpret_cast<const int4*>(OFF + s0);
+                const int4 ob = *reinterpret_cast<const int4*>(OFF + s0 + 4);
+                const int o[8] = {oa.x, oa.y, oa.z, oa.w, ob.x, ob.y, ob.z, ob.w};
+                uint32_t wv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int ia = min(max(o[2 * i] + keylin, 0), last);
+                    const int ib = min(max(o[2 * i + 1] + keylin, 0), last);
+                    const uint32_t v = static_cast<uint32_t>(Ws[ia]) | (static_cast<uint32_t>(Ws[ib]) << 16);
+                    wv[i] = rok ? (v & cm[i]) : 0u;
+                }
+                accumulate_chunk<T, D>(Xs, c, lane, make_uint4(wv[0], wv[1], wv[2], wv[3]), acc);
+            }
+        }
+        more = walk_next(blk, w, fresh);
+        __syncthreads();  // the slice is no longer read
+        if (more) {
+            const T* pl = plane_of(xg, lx, w.b, w.h, slice_pos(p, blk, w.u0));
+            stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
+            stage_key_rows<T>(p, blk, ts, w.b, w.h, w.u0, wt, lw, OFF, Ws, wave, lane);
+        }
+        if ((fresh || !more) && ln.valid) store_rows<T, D>(bh_ptr(out, lo, b, h), vol_off(lo, ln.pos), grp, acc, mul);
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -1208,13 +1348,16 @@ __global__ __launch_bounds__(256) void k_wsum_mfma(Prob p, TileShape ts, const i
 
 namespace {
 
-enum Kind { kForward = 0, kBackwardQ = 1, kBackwardKV = 2, kSplit = 3 };
+enum Kind { kForward = 0, kBackwardQ = 1, kBackwardKV = 2, kSplit = 3, kSplitKey = 4 };
 
 // Entries per row (KV) up to which the split kernels take a call (a lane
 // moves at most 4 entries of a row), and the LDS their row blocks may take
 // per workgroup.
 constexpr int kSplitMaxKV = 256;
 constexpr size_t kSplitRowsBudget = 48 * 1024;
+// LDS of the key-side split kernel per workgroup (x rows, OFF and the rows
+// of w of one slice's queries).
+constexpr size_t kSplitKeyLds = 128 * 1024;
 
 constexpr size_t kLdsBudget = 64 * 1024;
 
@@ -1259,7 +1402,7 @@ int union_extent(const Axis& A, int T, bool key_tile) {
 // Staged operands (split kernels: one; their row blocks come on top).
 size_t lds_bytes(Kind kind, int slots, int D) {
     const size_t rows = static_cast<size_t>(slots) * D * 2;
-    if (kind == kSplit) return kLdsPad + rows;
+    if (kind == kSplit || kind == kSplitKey) return kLdsPad + rows;
     return kLdsPad + (kind == kBackwardKV ? 2 * rows + (2 * static_cast<size_t>(slots) + 8) * 4 : 2 * rows);
 }
 
@@ -1289,12 +1432,13 @@ bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts) {
         }
         const int cnt = ts.T[0] * ts.T[1] * ts.T[2];
         ts.waves = std::max(1, (cnt + 15) / 16);
-        const int u1 = union_extent(p.ax[1], ts.T[1], kind == kBackwardKV);
-        const int u2 = union_extent(p.ax[2], ts.T[2], kind == kBackwardKV);
+        const bool key_tile = kind == kBackwardKV || kind == kSplitKey;
+        const int u1 = union_extent(p.ax[1], ts.T[1], key_tile);
+        const int u2 = union_extent(p.ax[2], ts.T[2], key_tile);
         ts.rowshift = std::max(3, log2_of(u2));
         ts.slots = ((u1 * (1 << ts.rowshift) + 31) / 32) * 32;
         if (lds_bytes(kind, ts.slots, D) <= kLdsBudget) {
-            const int heads = kind == kBackwardKV ? p.Hkv : p.Hq;
+            const int heads = key_tile ? p.Hkv : p.Hq;
             ts.nheads = heads;
             set_h_per(ts, 1);
             ts.rep = make_fastdiv(static_cast<uint32_t>(p.rep));
@@ -1649,6 +1793,28 @@ hipError_t run_wsum(const char* name, const Prob& p, const void* w, Lay lw, cons
     return hipGetLastError();
 }
 
+// Key-side split kernel: the staged operand, OFF (one int per slot) and the
+// slots' rows of KV 16-bit entries.
+size_t split_key_lds_bytes(const Prob& p, const TileShape& ts, int D) {
+    return lds_bytes(kSplitKey, ts.slots, D) + static_cast<size_t>(ts.slots) * (4 + 2 * p.kv);
+}
+
+template <typename T, int D>
+hipError_t run_wsum_key(const char* name, const Prob& p, const void* w, Lay lw, const void* x, Lay lx, void* o,
+                        Lay lo, float mul, hipStream_t s) {
+    TileShape ts{};
+    if (!choose_tile(p, kSplitKey, D, ts)) return hipErrorInvalidValue;
+    const auto kern = k_wsum_key_mfma<T, D>;
+    const size_t shm = split_key_lds_bytes(p, ts, D);
+    hipError_t e = allow_lds(kern, shm);
+    if (e != hipSuccess) return e;
+    fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    const int* geo = geometry_table(p, ts, true, s);
+    NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, p, ts, geo,
+              (const T*)w, to_k(lw), (const T*)x, to_k(lx), (T*)o, to_k(lo), mul);
+    return hipGetLastError();
+}
+
 // Rows of KV entries: non-negative strides, every entry of one (batch, head)
 // at a 31-bit offset.
 bool rows_fit(const Prob& p, const Lay& l) {
@@ -1671,6 +1837,33 @@ bool mfma_split_eligible(const Prob& p, int dtype, int D, bool aligned, const La
     TileShape ts{};
     if (!choose_tile(p, kSplit, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
     return rows_fit(p, rows) && offsets_fit(p, staged);
+}
+
+bool mfma_split_key_eligible(const Prob& p, int dtype, int D, bool aligned, const Lay& rows,
+                             std::initializer_list<Lay> staged) {
+    if (dtype == NATTEN_F32 || !aligned || p.rep != 1) return false;
+    if (!(D == 32 || D == 64 || D == 128) || p.kv > kSplitMaxKV) return false;
+    for (int a = 0; a < 3; ++a)
+        if (p.ax[a].st != 1) return false;
+    TileShape ts{};
+    if (!choose_tile(p, kSplitKey, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
+    if (split_key_lds_bytes(p, ts, D) > kSplitKeyLds || static_cast<long long>(ts.slots) * p.kv >= (1LL << 30))
+        return false;
+    return rows_fit(p, rows) && offsets_fit(p, staged);
+}
+
+hipError_t mfma_split_wsum_key(const char* name, const Prob& p, int D, const void* w, Lay lw, const void* x, Lay lx,
+                               void* o, Lay lo, float mul, int dtype, hipStream_t s) {
+#define NA_WSUMK(T, DD) return run_wsum_key<T, DD>(name, p, w, lw, x, lx, o, lo, mul, s)
+    if (dtype == NATTEN_BF16) {
+        if (D == 32) NA_WSUMK(bf16, 32);
+        if (D == 64) NA_WSUMK(bf16, 64);
+        NA_WSUMK(bf16, 128);
+    }
+    if (D == 32) NA_WSUMK(f16, 32);
+    if (D == 64) NA_WSUMK(f16, 64);
+    NA_WSUMK(f16, 128);
+#undef NA_WSUMK
 }
 
 hipError_t mfma_split_dot(const char* name, const Prob& p, int D, const void* a, Lay la, const void* x, Lay lx,

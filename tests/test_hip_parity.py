@@ -291,7 +291,7 @@ SPLIT_TILE = [
 @pytest.mark.parametrize("dim,dtype", [(32, torch.bfloat16), (64, torch.float16), (128, torch.bfloat16)])
 def test_split_ops_tile_path(case, dim, dtype):
     """The split QK / AV ops at head dims 32/64/128 in 16-bit run the MFMA tile
-    kernels (query side: logits, AV output, dq, dattn) and match the oracle."""
+    kernels (logits, AV output, and all four gradients) and match the oracle."""
     from natten_mps_amd import functional as F
     from natten_mps_amd._core import _lib
 
@@ -331,7 +331,8 @@ def test_split_ops_tile_path(case, dim, dtype):
     finally:
         _lib.profile_enable(False)
     ran = _lib.profile_read(reset=True)
-    for name in ("na_qk_mfma", "na_av_mfma", "na_qk_bwd_q_mfma", "na_av_bwd_a_mfma"):
+    for name in ("na_qk_mfma", "na_av_mfma", "na_qk_bwd_q_mfma", "na_av_bwd_a_mfma", "na_qk_bwd_k_mfma",
+                 "na_av_bwd_v_mfma"):
         assert ran.get(name, (0,))[0] >= 1, (name, sorted(ran))
 
 
