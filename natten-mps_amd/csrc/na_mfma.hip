@@ -1030,10 +1030,14 @@ __device__ __forceinline__ int chunk_entry(const Prob& p, const Lane& ln, const 
 // moves between global memory and LDS, -1 past the row's end.
 __device__ __forceinline__ void lane_entries(const Prob& p, const RowBlock& rb, int lane, int (&pos)[4]) {
     const int k2 = p.ax[2].k;
+    // e / k2 for e < 256, k2 <= 256: (e + 1/2) / k2 lies at least 1/(2 k2) from
+    // an integer, far beyond the float rounding of the product
+    const float inv = 1.f / static_cast<float>(k2);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const int e = lane + 64 * t;
-        pos[t] = e < p.kv ? (e / k2) * rb.p2 + 8 + e % k2 : -1;
+        const int row = static_cast<int>((static_cast<float>(e) + 0.5f) * inv);
+        pos[t] = e < p.kv ? row * rb.p2 + 8 + (e - row * k2) : -1;
     }
 }
 
@@ -1041,10 +1045,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), kPlaneBytes, 0x00020000);
 }
 
-template <typename T, int D>
+// SAME: the two [B, *sp, H, D] operands share one layout (one set of strides
+// kept in scalar registers instead of two).
+template <typename T, int D, bool SAME>
 __global__ __launch_bounds__(256) void k_dot_mfma(Prob p, TileShape ts, const int* __restrict__ geo,
-                                                  const T* __restrict__ a, LayK la, const T* __restrict__ xg, LayK lx,
-                                                  T* __restrict__ out, LayK lo, float mul, float fill) {
+                                                  const T* __restrict__ a, LayK la_in, const T* __restrict__ xg,
+                                                  LayK lx, T* __restrict__ out, LayK lo, float mul, float fill) {
+    const LayK& la = SAME ? lx : la_in;
     unsigned char* smem = lds_base();
     T* Xs = reinterpret_cast<T*>(smem);
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
@@ -1123,10 +1130,11 @@ __global__ __launch_bounds__(256) void k_dot_mfma(Prob p, TileShape ts, const in
     }
 }
 
-template <typename T, int D>
+template <typename T, int D, bool SAME>
 __global__ __launch_bounds__(256) void k_wsum_mfma(Prob p, TileShape ts, const int* __restrict__ geo,
                                                    const T* __restrict__ wt, LayK lw, const T* __restrict__ xg,
-                                                   LayK lx, T* __restrict__ out, LayK lo, float mul) {
+                                                   LayK lx, T* __restrict__ out, LayK lo_in, float mul) {
+    const LayK& lo = SAME ? lx : lo_in;
     unsigned char* smem = lds_base();
     T* Xs = reinterpret_cast<T*>(smem);
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
@@ -1254,10 +1262,11 @@ __device__ __forceinline__ void stage_key_rows(const Prob& p, const Block& k, co
     }
 }
 
-template <typename T, int D>
+template <typename T, int D, bool SAME>
 __global__ __launch_bounds__(256) void k_wsum_key_mfma(Prob p, TileShape ts, const int* __restrict__ geo,
                                                        const T* __restrict__ wt, LayK lw, const T* __restrict__ xg,
-                                                       LayK lx, T* __restrict__ out, LayK lo, float mul) {
+                                                       LayK lx, T* __restrict__ out, LayK lo_in, float mul) {
+    const LayK& lo = SAME ? lx : lo_in;
     unsigned char* smem = lds_base();
     const int slots = ts.slots, kv = p.kv;
     T* Xs = reinterpret_cast<T*>(smem);
@@ -1271,11 +1280,6 @@ __global__ __launch_bounds__(256) void k_wsum_key_mfma(Prob p, TileShape ts, con
     const StageMap sm = stage_map<T, D>(p, ts, lx, lx, lane);
     Walk w;
     walk_start(blk, w);
-    {
-        const T* pl = plane_of(xg, lx, w.b, w.h, slice_pos(p, blk, 0));
-        stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
-    }
-    stage_key_rows<T>(p, blk, ts, w.b, w.h, 0, wt, lw, OFF, Ws, wave, lane);
     const Lane ln = lane_item(p, ts, blk, wave, col, true);
     int keylin;
     {
@@ -1302,6 +1306,12 @@ __global__ __launch_bounds__(256) void k_wsum_key_mfma(Prob p, TileShape ts, con
     bool more = true, fresh = true;
     while (more) {
         const int b = w.b, h = w.h, u0 = w.u0;
+        {
+            // one staging site (the walk's first slice and every later one)
+            const T* pl = plane_of(xg, lx, b, h, slice_pos(p, blk, u0));
+            stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
+            stage_key_rows<T>(p, blk, ts, b, h, u0, wt, lw, OFF, Ws, wave, lane);
+        }
         if (fresh) {
 #pragma unroll
             for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -1331,11 +1341,6 @@ __global__ __launch_bounds__(256) void k_wsum_key_mfma(Prob p, TileShape ts, con
         }
         more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
-        if (more) {
-            const T* pl = plane_of(xg, lx, w.b, w.h, slice_pos(p, blk, w.u0));
-            stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
-            stage_key_rows<T>(p, blk, ts, w.b, w.h, w.u0, wt, lw, OFF, Ws, wave, lane);
-        }
         if ((fresh || !more) && ln.valid) store_rows<T, D>(bh_ptr(out, lo, b, h), vol_off(lo, ln.pos), grp, acc, mul);
     }
 }
@@ -1761,12 +1766,12 @@ size_t split_lds_bytes(const Prob& p, const TileShape& ts, int D) {
     return lds_bytes(kSplit, ts.slots, D) + static_cast<size_t>(ts.waves) * row_block_entries(p) * 2;
 }
 
-template <typename T, int D>
-hipError_t run_dot(const char* name, const Prob& p, const void* a, Lay la, const void* x, Lay lx, void* o, Lay lo,
+template <typename T, int D, bool SAME>
+hipError_t run_dot_as(const char* name, const Prob& p, const void* a, Lay la, const void* x, Lay lx, void* o, Lay lo,
                    float mul, float fill, hipStream_t s) {
     TileShape ts{};
     if (!choose_tile(p, kSplit, D, ts)) return hipErrorInvalidValue;
-    const auto kern = k_dot_mfma<T, D>;
+    const auto kern = k_dot_mfma<T, D, SAME>;
     const size_t shm = split_lds_bytes(p, ts, D);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
@@ -1778,11 +1783,18 @@ hipError_t run_dot(const char* name, const Prob& p, const void* a, Lay la, const
 }
 
 template <typename T, int D>
-hipError_t run_wsum(const char* name, const Prob& p, const void* w, Lay lw, const void* x, Lay lx, void* o, Lay lo,
+hipError_t run_dot(const char* name, const Prob& p, const void* a, Lay la, const void* x, Lay lx, void* o, Lay lo,
+                   float mul, float fill, hipStream_t s) {
+    if (same_lay(la, lx)) return run_dot_as<T, D, true>(name, p, a, la, x, lx, o, lo, mul, fill, s);
+    return run_dot_as<T, D, false>(name, p, a, la, x, lx, o, lo, mul, fill, s);
+}
+
+template <typename T, int D, bool SAME>
+hipError_t run_wsum_as(const char* name, const Prob& p, const void* w, Lay lw, const void* x, Lay lx, void* o, Lay lo,
                     float mul, hipStream_t s) {
     TileShape ts{};
     if (!choose_tile(p, kSplit, D, ts)) return hipErrorInvalidValue;
-    const auto kern = k_wsum_mfma<T, D>;
+    const auto kern = k_wsum_mfma<T, D, SAME>;
     const size_t shm = split_lds_bytes(p, ts, D);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
@@ -1793,18 +1805,25 @@ hipError_t run_wsum(const char* name, const Prob& p, const void* w, Lay lw, cons
     return hipGetLastError();
 }
 
+template <typename T, int D>
+hipError_t run_wsum(const char* name, const Prob& p, const void* w, Lay lw, const void* x, Lay lx, void* o, Lay lo,
+                    float mul, hipStream_t s) {
+    if (same_lay(lx, lo)) return run_wsum_as<T, D, true>(name, p, w, lw, x, lx, o, lo, mul, s);
+    return run_wsum_as<T, D, false>(name, p, w, lw, x, lx, o, lo, mul, s);
+}
+
 // Key-side split kernel: the staged operand, OFF (one int per slot) and the
 // slots' rows of KV 16-bit entries.
 size_t split_key_lds_bytes(const Prob& p, const TileShape& ts, int D) {
     return lds_bytes(kSplitKey, ts.slots, D) + static_cast<size_t>(ts.slots) * (4 + 2 * p.kv);
 }
 
-template <typename T, int D>
-hipError_t run_wsum_key(const char* name, const Prob& p, const void* w, Lay lw, const void* x, Lay lx, void* o,
+template <typename T, int D, bool SAME>
+hipError_t run_wsum_key_as(const char* name, const Prob& p, const void* w, Lay lw, const void* x, Lay lx, void* o,
                         Lay lo, float mul, hipStream_t s) {
     TileShape ts{};
     if (!choose_tile(p, kSplitKey, D, ts)) return hipErrorInvalidValue;
-    const auto kern = k_wsum_key_mfma<T, D>;
+    const auto kern = k_wsum_key_mfma<T, D, SAME>;
     const size_t shm = split_key_lds_bytes(p, ts, D);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
@@ -1813,6 +1832,13 @@ hipError_t run_wsum_key(const char* name, const Prob& p, const void* w, Lay lw, 
     NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, p, ts, geo,
               (const T*)w, to_k(lw), (const T*)x, to_k(lx), (T*)o, to_k(lo), mul);
     return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t run_wsum_key(const char* name, const Prob& p, const void* w, Lay lw, const void* x, Lay lx, void* o,
+                        Lay lo, float mul, hipStream_t s) {
+    if (same_lay(lx, lo)) return run_wsum_key_as<T, D, true>(name, p, w, lw, x, lx, o, lo, mul, s);
+    return run_wsum_key_as<T, D, false>(name, p, w, lw, x, lx, o, lo, mul, s);
 }
 
 // Rows of KV entries: non-negative strides, every entry of one (batch, head)
