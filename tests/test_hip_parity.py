@@ -336,6 +336,52 @@ def test_split_ops_tile_path(case, dim, dtype):
         assert ran.get(name, (0,))[0] >= 1, (name, sorted(ran))
 
 
+def test_split_ops_tile_path_strided_views():
+    """Split ops on the tile path with q/k/v as strided views of one qkv
+    projection and the attention weights as a head-major tensor's permuted
+    view (operands in different layouts)."""
+    from natten_mps_amd import functional as F
+    from natten_mps_amd._core import _lib
+
+    (x,) = _inputs(85, [(2, 13, 15, 3, 2, 32)], torch.bfloat16)
+    xd = x.to(DEV).requires_grad_(True)
+    q, k, v = xd.permute(3, 0, 1, 2, 4, 5).unbind(0)
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        logits = F.na2d_qk(q, k, 7, (1, 2), scale=0.3)
+        # softmax in a head-major copy, handed over as a permuted view
+        attn = torch.softmax(logits.float().permute(0, 3, 1, 2, 4).contiguous(), -1).to(torch.bfloat16)
+        attn = attn.permute(0, 2, 3, 1, 4)
+        out = F.na2d_av(attn, v, 7, (1, 2))
+        (do,) = _inputs(86, [tuple(out.shape)], torch.bfloat16)
+        out.backward(do.to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    ran = _lib.profile_read(reset=True)
+    for name in ("na_qk_mfma", "na_av_mfma", "na_qk_bwd_q_mfma", "na_av_bwd_a_mfma", "na_qk_bwd_k_mfma",
+                 "na_av_bwd_v_mfma"):
+        assert ran.get(name, (0,))[0] >= 1, (name, sorted(ran))
+
+    xr = x.float().requires_grad_(True)
+    qr, kr, vr = xr.permute(3, 0, 1, 2, 4, 5).unbind(0)
+    ref_logits = P.na2d_qk_forward(qr, kr, (7, 7), (1, 2), (1, 1), (False, False), 0.3)
+    _close(logits.detach().cpu(), ref_logits.detach(), torch.bfloat16, "logits")
+    ref_attn = torch.softmax(ref_logits, -1).to(torch.bfloat16).float()
+    ref_out = P.na2d_av_forward(ref_attn, vr, (7, 7), (1, 2), (1, 1), (False, False))
+    _close(out.detach().cpu(), ref_out.detach(), torch.bfloat16, "out")
+    # gradient through av (dattn, dv) and, via the bf16 attention, qk
+    ref_attn = ref_attn.detach().requires_grad_(True)
+    ref_out = P.na2d_av_forward(ref_attn, vr, (7, 7), (1, 2), (1, 1), (False, False))
+    ref_out.backward(do.float())
+    dattn = ref_attn.grad
+    sm = torch.softmax(ref_logits.detach(), -1)
+    dlogits = sm * (dattn - (dattn * sm).sum(-1, keepdim=True))
+    ref_logits.backward(dlogits)
+    _close(xd.grad.cpu(), xr.grad, torch.bfloat16, "dqkv")
+
+
 def test_fused_equals_split_composition():
     """Reference check (tests/test_backward_parity.py): fused vs split QK ->
     softmax -> AV, outputs and gradients."""
