@@ -1221,43 +1221,57 @@ __global__ __launch_bounds__(256) void k_wsum_mfma(Prob p, TileShape ts, const i
 // the key's query box are masked: rows per chunk, columns per slot.
 // ---------------------------------------------------------------------------
 
+// Entries per slot of the key-side weight rows in LDS: a row plus one
+// entry of parity, rounded to whole 32-bit words.
+__host__ __device__ inline int key_row_pitch(const Prob& p) { return (p.kv + 2) & ~1; }
+
+// Rows of w of one slice's union queries into Ws (pitch entries per slot)
+// and the entry table OFF.  Rows are read as aligned 32-bit words, two rows
+// per wave instruction (lanes 0-31 and 32-63), only the words that hold
+// entries of the row; a row whose first entry sits in the upper half of
+// its word lands one entry late in LDS, which OFF accounts for.
 template <typename T>
 __device__ __forceinline__ void stage_key_rows(const Prob& p, const Block& k, const TileShape& ts, int b, int h,
                                                int u0, const T* __restrict__ wt, const LayK& lw, int* OFF,
                                                uint16_t* Ws, int wave, int lane) {
-    const int slots = ts.slots, kv = p.kv, mask2 = (1 << ts.rowshift) - 1;
-    const int k1 = p.ax[1].k, k2 = p.ax[2].k;
+    const int slots = ts.slots, kv = p.kv, mask2 = (1 << ts.rowshift) - 1, pitch = key_row_pitch(p);
+    const int k1 = p.ax[1].k, k2 = p.ax[2].k, d1 = p.ax[1].dil, d2 = p.ax[2].dil;
+    const T* wb = bh_ptr(wt, lw, b, h) + slice_pos(p, k, u0) * lw.s0;
+    const int lead = static_cast<int>((reinterpret_cast<uintptr_t>(wb) >> 1) & 1);  // wb is 4-byte aligned + 2 lead
+    const __amdgpu_buffer_rsrc_t rw = rows_rsrc(wb - lead);
+    // in-plane offset of slot s's row (row 0 for slots outside the union:
+    // loaded, never read)
+    const auto row_off = [&](int s) {
+        const int a1 = s >> ts.rowshift, a2 = s & mask2;
+        return (a1 < k.U[1] && a2 < k.U[2])
+                   ? (k.r[1] + (k.lo[1] + a1) * d1) * lw.s1 + (k.r[2] + (k.lo[2] + a2) * d2) * lw.s2
+                   : 0;
+    };
     const int ws0 = class_ws(k.c[0], k.lo[0] + u0);
-    const int p0 = slice_pos(p, k, u0);
     for (int s = threadIdx.x; s < slots; s += blockDim.x) {
         const int a1 = s >> ts.rowshift, a2 = s & mask2;
         const int base = (ws0 * k1 + class_ws(k.c[1], k.lo[1] + a1)) * k2 + class_ws(k.c[2], k.lo[2] + a2);
-        OFF[s] = s * kv - base;
+        OFF[s] = s * pitch + ((row_off(s) + lead) & 1) - base;
     }
-    const T* wb = bh_ptr(wt, lw, b, h) + p0 * lw.s0;
-    const __amdgpu_buffer_rsrc_t rw = rows_rsrc(wb);
-    const int d1 = p.ax[1].dil, d2 = p.ax[2].dil;
+    uint32_t* Ws32 = reinterpret_cast<uint32_t*>(Ws);
+    const int half = lane >> 5, groups = ((kv + 2) / 2 + 31) / 32;  // 32-word groups of a row
     for (int sb = wave * 16; sb < slots; sb += 64) {
-        // lanes 0..15: row offsets of slots sb .. sb + 15 (0 outside the union:
-        // such rows are loaded but never read)
-        int off = 0;
-        {
-            const int s = sb + (lane & 15), a1 = s >> ts.rowshift, a2 = s & mask2;
-            if (a1 < k.U[1] && a2 < k.U[2])
-                off = (k.r[1] + (k.lo[1] + a1) * d1) * lw.s1 + (k.r[2] + (k.lo[2] + a2) * d2) * lw.s2;
-        }
+        const int offs = row_off(sb + (lane & 15));  // lanes 0..15: slots sb .. sb + 15
+        for (int g = 0; g < groups; ++g) {
+            const int j = (lane & 31) + 32 * g;
+            uint32_t v[8];
+            bool in[8];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            if (64 * t >= kv) break;
-            const int e = lane + 64 * t;
-            if (e < kv) {
-                uint16_t v[16];
-#pragma unroll
-                for (int m = 0; m < 16; ++m)
-                    v[m] = __builtin_amdgcn_raw_buffer_load_b16(rw, e * 2, __builtin_amdgcn_readlane(off, m) * 2, 0);
-#pragma unroll
-                for (int m = 0; m < 16; ++m) Ws[(sb + m) * kv + e] = v[m];
+            for (int m = 0; m < 8; ++m) {
+                const int o0 = __builtin_amdgcn_readlane(offs, 2 * m);
+                const int o1 = __builtin_amdgcn_readlane(offs, 2 * m + 1);
+                const int first = (half ? o1 : o0) + lead;  // entry index from the aligned base
+                in[m] = j < (((first & 1) + kv + 1) >> 1);   // words holding entries of the row
+                v[m] = in[m] ? __builtin_amdgcn_raw_buffer_load_b32(rw, ((first >> 1) + j) * 4, 0, 0) : 0u;
             }
+#pragma unroll
+            for (int m = 0; m < 8; ++m)
+                if (in[m]) Ws32[(sb + 2 * m + half) * (pitch >> 1) + j] = v[m];
         }
     }
 }
@@ -1287,7 +1301,7 @@ __global__ __launch_bounds__(256) void k_wsum_key_mfma(Prob p, TileShape ts, con
         const int e2 = f & (ts.T[2] - 1), e1 = (f >> s2) & (ts.T[1] - 1), e0 = f >> (s2 + s1);
         keylin = ((blk.J[0] + e0) * p.ax[1].k + blk.J[1] + e1) * p.ax[2].k + blk.J[2] + e2;
     }
-    const int last = slots * kv - 1;
+    const int last = slots * key_row_pitch(p) - 1;
     // column masks (two entries per word) of the lane's 8 slots; fixed per
     // tile when union rows are at most 32 slots
     const auto col_masks = [&](int c, uint32_t (&cm)[4]) {
@@ -1815,7 +1829,7 @@ hipError_t run_wsum(const char* name, const Prob& p, const void* w, Lay lw, cons
 // Key-side split kernel: the staged operand, OFF (one int per slot) and the
 // slots' rows of KV 16-bit entries.
 size_t split_key_lds_bytes(const Prob& p, const TileShape& ts, int D) {
-    return lds_bytes(kSplitKey, ts.slots, D) + static_cast<size_t>(ts.slots) * (4 + 2 * p.kv);
+    return lds_bytes(kSplitKey, ts.slots, D) + static_cast<size_t>(ts.slots) * (4 + 2 * key_row_pitch(p));
 }
 
 template <typename T, int D, bool SAME>
@@ -1873,7 +1887,7 @@ bool mfma_split_key_eligible(const Prob& p, int dtype, int D, bool aligned, cons
         if (p.ax[a].st != 1) return false;
     TileShape ts{};
     if (!choose_tile(p, kSplitKey, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
-    if (split_key_lds_bytes(p, ts, D) > kSplitKeyLds || static_cast<long long>(ts.slots) * p.kv >= (1LL << 30))
+    if (split_key_lds_bytes(p, ts, D) > kSplitKeyLds)
         return false;
     return rows_fit(p, rows) && offsets_fit(p, staged);
 }
