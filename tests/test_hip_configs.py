@@ -87,11 +87,17 @@ def test_config3_na2d_bf16(dil):
     _close(out[sl], ref, 2e-2, "out")
     for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
         _close(a[sl], b, 2e-2, n)
-    # fused vs split QK -> softmax -> AV on the device, whole problem
-    qd, kd, vd = (t.to(DEV) for t in (q, k, v))
+    # fused vs split QK -> softmax -> AV on the device, whole problem,
+    # forward and backward (the split path rounds its logits, probabilities
+    # and their gradients to bf16 on the way, hence the wider bound on the
+    # gradients)
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
     logits = F.na2d_qk(qd, kd, 7, dil) * 32 ** -0.5
     split = F.na2d_av(torch.softmax(logits.float(), -1).to(torch.bfloat16), vd, 7, dil)
-    _close(split.cpu(), out, 2e-2, "fused vs split")
+    _close(split.detach().cpu(), out, 2e-2, "fused vs split")
+    split.backward(do.to(DEV))
+    for n, t, g in zip(("dq", "dk", "dv"), (qd, kd, vd), grads):
+        _close(t.grad.cpu(), g, 5e-2, f"fused vs split {n}")
 
 
 @pytest.mark.parametrize("dil", [1, 4])
