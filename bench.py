@@ -141,10 +141,18 @@ def compare_split(leaves, do, cfg, timed, args):
     _lib.profile_read(reset=True)
     timed(split_step, profile=True, head_start_ms=2.0 * args.steps * ms + 5.0)
     kernels = {name: round(tot / n * 1e3, 1) for name, (n, tot, _, _) in _lib.profile_read(reset=True).items()}
+    # every split launch reads or writes two [B, *sp, H, D] operands and one
+    # [B, *sp, H, KV] tensor of logits / weights (algorithmic bytes)
+    q = leaves[0]
+    kv = ks[0] * ks[1]
+    split_bytes = q.numel() * q.element_size() * (2 + kv / q.shape[-1])
+    kernel_frac = {name: round(split_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)
+                   for name, us in kernels.items() if name.endswith("_mfma") and us > 0}
     a, b = fused_full(), split_step()
     diff = max(float((x.detach().float() - y.detach().float()).abs().max()) for x, y in zip(a, b))
     return {"ms_per_step": round(ms, 4), "max_abs_diff": diff, "timing": "eager",
-            "ops": "na2d_qk -> softmax -> na2d_av, forward + backward", "kernel_mean_us": kernels}
+            "ops": "na2d_qk -> softmax -> na2d_av, forward + backward", "kernel_mean_us": kernels,
+            "kernel_alg_bytes": int(split_bytes), "kernel_hbm_frac": kernel_frac}
 
 
 def cpu_baseline(dilation, budget_s=20.0):
