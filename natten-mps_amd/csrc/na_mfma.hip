@@ -1255,7 +1255,7 @@ __device__ __forceinline__ void stage_key_rows(const Prob& p, const Block& k, co
     }
     uint32_t* Ws32 = reinterpret_cast<uint32_t*>(Ws);
     const int half = lane >> 5, groups = ((kv + 2) / 2 + 31) / 32;  // 32-word groups of a row
-    for (int sb = wave * 16; sb < slots; sb += 64) {
+    for (int sb = wave * 16; sb < slots; sb += 16 * ts.waves) {
         const int offs = row_off(sb + (lane & 15));  // lanes 0..15: slots sb .. sb + 15
         for (int g = 0; g < groups; ++g) {
             const int j = (lane & 31) + 32 * g;

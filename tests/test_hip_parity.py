@@ -336,6 +336,63 @@ def test_split_ops_tile_path(case, dim, dtype):
         assert ran.get(name, (0,))[0] >= 1, (name, sorted(ran))
 
 
+def _random_split_cases(n, seed=2024):
+    import random
+
+    rnd = random.Random(seed)
+    cases = []
+    for _ in range(n):
+        rank = rnd.choice([1, 1, 2, 2, 2, 3])
+        ks, dil, sp, causal = [], [], [], []
+        for a in range(rank):
+            k = rnd.choice([3, 5, 7] + ([9, 13] if rank == 1 else []))
+            d = rnd.choice([1, 1, 2, 3])
+            lo = k * d
+            sp.append(rnd.randint(lo, lo + (40 if rank == 1 else 12)))
+            ks.append(k)
+            dil.append(d)
+            causal.append(rnd.random() < 0.3)
+        cases.append((rank, tuple(sp), tuple(ks), tuple(dil), tuple(causal),
+                      rnd.choice([None, 0.125, 0.5]), rnd.choice([32, 64]),
+                      rnd.choice([torch.bfloat16, torch.float16])))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_split_cases(24))
+def test_split_ops_tile_path_random(case):
+    """Seeded random geometries (rank, lengths, kernel sizes, dilations,
+    causal axes, scale, head dim, 16-bit dtype) through the split ops' tile
+    kernels, forward and all four gradients, against the oracle."""
+    from natten_mps_amd import functional as F
+
+    rank, sp, ks, dil, causal, scale, dim, dtype = case
+    q, k, v = _inputs(87, [(1, *sp, 2, dim)] * 3, dtype)
+    qd, kd = q.to(DEV).requires_grad_(True), k.to(DEV).requires_grad_(True)
+    logits = getattr(F, f"na{rank}d_qk")(qd, kd, ks, dil, is_causal=causal, scale=scale)
+    ref_q, ref_k = q.float().requires_grad_(True), k.float().requires_grad_(True)
+    ref_logits = getattr(P, f"na{rank}d_qk_forward")(ref_q, ref_k, ks, dil, (1,) * rank, causal, scale)
+    finite = torch.isfinite(ref_logits)
+    assert torch.equal(torch.isfinite(logits.detach().cpu()), finite)
+    _close(logits.detach().cpu()[finite], ref_logits.detach()[finite], dtype, "logits")
+    (dl,) = _inputs(88, [tuple(ref_logits.shape)], dtype)
+    dl = torch.where(finite, dl, torch.zeros_like(dl))
+    logits.backward(dl.to(DEV))
+    ref_logits.backward(dl.float())
+    _close(qd.grad.cpu(), ref_q.grad, dtype, "dq")
+    _close(kd.grad.cpu(), ref_k.grad, dtype, "dk")
+    attn = torch.softmax(torch.where(finite, ref_logits.detach(), torch.full_like(ref_logits, -1e30)), -1)
+    ad, vd = attn.to(dtype).to(DEV).requires_grad_(True), v.to(DEV).requires_grad_(True)
+    out = getattr(F, f"na{rank}d_av")(ad, vd, ks, dil, is_causal=causal)
+    ref_a, ref_v = attn.to(dtype).float().requires_grad_(True), v.float().requires_grad_(True)
+    ref_out = getattr(P, f"na{rank}d_av_forward")(ref_a, ref_v, ks, dil, (1,) * rank, causal)
+    _close(out.detach().cpu(), ref_out.detach(), dtype, "av out")
+    (do,) = _inputs(89, [tuple(ref_out.shape)], dtype)
+    out.backward(do.to(DEV))
+    ref_out.backward(do.float())
+    _close(ad.grad.cpu(), ref_a.grad, dtype, "dattn")
+    _close(vd.grad.cpu(), ref_v.grad, dtype, "dv")
+
+
 def test_split_ops_tile_path_strided_views():
     """Split ops on the tile path with q/k/v as strided views of one qkv
     projection and the attention weights as a head-major tensor's permuted
