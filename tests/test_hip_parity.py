@@ -393,6 +393,45 @@ def test_split_ops_tile_path_random(case):
     _close(vd.grad.cpu(), ref_v.grad, dtype, "dv")
 
 
+def _random_fused_cases(n, seed=4048):
+    import random
+
+    rnd = random.Random(seed)
+    cases = []
+    for _ in range(n):
+        rank = rnd.choice([1, 2, 2, 3])
+        ks, dil, sp, causal = [], [], [], []
+        for a in range(rank):
+            k = rnd.choice([3, 5, 7] + ([9, 15, 33] if rank == 1 else []))
+            d = rnd.choice([1, 1, 2, 3])
+            sp.append(rnd.randint(k * d, k * d + (70 if rank == 1 else 14)))
+            ks.append(k)
+            dil.append(d)
+            causal.append(rnd.random() < 0.3)
+        hkv = rnd.choice([1, 2])
+        cases.append((rank, tuple(sp), tuple(ks), tuple(dil), tuple(causal), rnd.choice([None, 0.2]),
+                      rnd.choice([32, 32, 64, 128]), hkv * rnd.choice([1, 2]), hkv,
+                      rnd.choice([torch.bfloat16, torch.float16])))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_fused_cases(24))
+def test_fused_tile_path_random(case):
+    """Seeded random geometries (rank, lengths, kernel sizes, dilations,
+    causal axes, scale, head dim, GQA, 16-bit dtype) through the fused MFMA
+    forward and backward, against the oracle in fp32 on the same inputs."""
+    from natten_mps_amd import functional as F
+
+    rank, sp, ks, dil, causal, scale, dim, hq, hkv, dtype = case
+    q, k, v, do = _inputs(91, [(2, *sp, hq, dim), (2, *sp, hkv, dim), (2, *sp, hkv, dim), (2, *sp, hq, dim)], dtype)
+    fn = getattr(F, f"na{rank}d")
+    out, grads = _hip_fwd_bwd(fn, (q, k, v), do, kernel_size=ks, dilation=dil, is_causal=causal, scale=scale)
+    ref, rgrads = _oracle_fwd_bwd(rank, (q, k, v), do, ks, (1,) * rank, dil, causal, scale)
+    _close(out, ref, dtype, "out")
+    for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
+        _close(a, b, dtype, n)
+
+
 def test_split_ops_tile_path_strided_views():
     """Split ops on the tile path with q/k/v as strided views of one qkv
     projection and the attention weights as a head-major tensor's permuted
