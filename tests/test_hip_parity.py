@@ -432,6 +432,40 @@ def test_fused_tile_path_random(case):
         _close(a, b, dtype, n)
 
 
+def test_split_ops_tile_path_heads_per_workgroup():
+    """A problem large enough that the split tile kernels run two heads per
+    workgroup (16 x 64 x 64 positions, 12 heads); batch 0 is checked
+    against the oracle, forward and all four gradients."""
+    from natten_mps_amd import functional as F
+
+    q, k, v = _inputs(93, [(16, 64, 64, 12, 32)] * 3, torch.bfloat16)
+    qd, kd = q.to(DEV).requires_grad_(True), k.to(DEV).requires_grad_(True)
+    logits = F.na2d_qk(qd, kd, 7, 1, scale=32 ** -0.5)
+    attn = torch.softmax(logits.float(), -1).to(torch.bfloat16)
+    ad = attn.detach().requires_grad_(True)
+    vd = v.to(DEV).requires_grad_(True)
+    out = F.na2d_av(ad, vd, 7, 1)
+    (do,) = _inputs(94, [tuple(out.shape)], torch.bfloat16)
+    out.backward(do.to(DEV))
+    (dl,) = _inputs(95, [tuple(logits.shape)], torch.bfloat16)
+    logits.backward(dl.to(DEV))
+
+    s0 = slice(0, 1)
+    ref_q, ref_k = q[s0].float().requires_grad_(True), k[s0].float().requires_grad_(True)
+    ref_logits = P.na2d_qk_forward(ref_q, ref_k, (7, 7), (1, 1), (1, 1), (False, False), 32 ** -0.5)
+    _close(logits.detach()[s0].cpu(), ref_logits.detach(), torch.bfloat16, "logits")
+    ref_logits.backward(dl[s0].float())
+    _close(qd.grad[s0].cpu(), ref_q.grad, torch.bfloat16, "dq")
+    _close(kd.grad[s0].cpu(), ref_k.grad, torch.bfloat16, "dk")
+    ref_a = attn[s0].detach().cpu().float().requires_grad_(True)
+    ref_v = v[s0].float().requires_grad_(True)
+    ref_out = P.na2d_av_forward(ref_a, ref_v, (7, 7), (1, 1), (1, 1), (False, False))
+    _close(out.detach()[s0].cpu(), ref_out.detach(), torch.bfloat16, "out")
+    ref_out.backward(do[s0].float())
+    _close(ad.grad[s0].cpu(), ref_a.grad, torch.bfloat16, "dattn")
+    _close(vd.grad[s0].cpu(), ref_v.grad, torch.bfloat16, "dv")
+
+
 def test_split_ops_tile_path_strided_views():
     """Split ops on the tile path with q/k/v as strided views of one qkv
     projection and the attention weights as a head-major tensor's permuted
