@@ -615,6 +615,12 @@ __device__ __forceinline__ bool walk_next(const Block& k, Walk& w, bool& new_pai
     return true;
 }
 
+// True when the next (q head) h1 of the walk reads the staged K/V of h0
+// unchanged: one slice per head and the same kv head (GQA group).
+__device__ __forceinline__ bool same_rows(const TileShape& ts, const Block& k, int h0, int h1) {
+    return k.U[0] == 1 && kv_head(ts, h0) == kv_head(ts, h1);
+}
+
 __device__ __forceinline__ int slice_pos(const Prob& p, const Block& k, int u0) {
     return k.r[0] + (k.lo[0] + u0) * p.ax[0].dil;
 }
@@ -720,7 +726,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfm
         }
         more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
-        if (more) {
+        if (more && !same_rows(ts, blk, h, w.h)) {
             const int p0 = slice_pos(p, blk, w.u0), hk = kv_head(ts, w.h);
             stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0),
                              lv, Vs, wave);
@@ -829,7 +835,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_
         }
         more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
-        if (more) {
+        if (more && !same_rows(ts, blk, h, w.h)) {
             const int p0 = slice_pos(p, blk, w.u0), hk = kv_head(ts, w.h);
             stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0),
                              lv, Vs, wave);
