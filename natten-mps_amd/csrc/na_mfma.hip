@@ -994,43 +994,31 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_k
 //                (AV: w = attn, x = v; QK backward dq: w = dattn, x = k).
 //
 // Rows of KV entries (row-major over the kernel axes, contiguous in global
-// memory) pass through an LDS block per wave: 16 rows, one per query, each
-// with its kernel rows (n0, n1) spread P2 = K2 + 8 entries apart and 8
-// entries ahead of the first, so that every run of K2 entries has 8 spare
-// entries on either side.  A lane's 8 slots of a chunk are consecutive
-// columns of one union row, i.e. consecutive entries of one kernel row; when
-// they meet the window at all, the 8 entries they address stay inside that
-// row's run and its spares.  Reads of spares give 0 (the wsum block is
-// cleared first), writes to spares are never read back (dot), so the chunk
-// loop needs no per-entry tests.  Global memory sees whole rows: one
-// 16-bit buffer access per query, lanes over consecutive entries, the row's
-// offset in a scalar register.
+// memory) pass through an LDS block per wave: 16 rows, one per query.  A
+// lane's 8 slots of a chunk are consecutive columns of one union row, i.e.
+// consecutive entries of one kernel row where they meet the window; each
+// entry outside the window is redirected to a zero (reads) or scratch
+// (writes) entry by one select on its address, so the chunk loop has no
+// branches.  Global memory sees whole rows: one 16-bit buffer access per
+// query, lanes over consecutive entries, the row's offset in a scalar
+// register.
 // ---------------------------------------------------------------------------
 
-// LDS block of one wave, in 16-bit entries: 16 rows of `pitch` entries, then
-// 8 zero entries (reads of chunks outside the window) and 8 entries that
-// writes of such chunks go to.
+// LDS block of one wave, in 16-bit entries: 16 rows of `pitch` entries
+// (kernel rows of p2 = K2 entries), then 8 zero entries (reads outside the
+// window) and 8 entries that writes outside the window go to.
 struct RowBlock {
     int p2, pitch;
 };
 
 __host__ __device__ inline RowBlock row_block(const Prob& p) {
     RowBlock r;
-    r.p2 = p.ax[2].k + 8;
-    r.pitch = (p.ax[0].k * p.ax[1].k * r.p2 + 8 + 1) & ~1;
+    r.p2 = p.ax[2].k;
+    r.pitch = (p.ax[0].k * p.ax[1].k * r.p2 + 1) & ~1;
     return r;
 }
 
 __host__ __device__ inline int row_block_entries(const Prob& p) { return 16 * row_block(p).pitch + 16; }
-
-// Entry index (from the lane's row start) of the first of the lane's slots
-// of chunk c, or -1 when those 8 slots miss its window.
-__device__ __forceinline__ int chunk_entry(const Prob& p, const Lane& ln, const RowBlock& rb, int rowshift, bool in0,
-                                           int u0, int c, int grp) {
-    const int s0 = 32 * c + 8 * grp, r = s0 >> rowshift, col0 = s0 & ((1 << rowshift) - 1);
-    const bool ok = in0 && r >= ln.lo[1] && r <= ln.hi[1] && col0 <= ln.hi[2] && col0 + 7 >= ln.lo[2];
-    return ok ? ((u0 - ln.lo[0]) * p.ax[1].k + r - ln.lo[1]) * rb.p2 + 8 + col0 - ln.lo[2] : -1;
-}
 
 // Position in a row block of the entries e = lane + 64 t (t < 4) a lane
 // moves between global memory and LDS, -1 past the row's end.
@@ -1043,7 +1031,7 @@ __device__ __forceinline__ void lane_entries(const Prob& p, const RowBlock& rb, 
     for (int t = 0; t < 4; ++t) {
         const int e = lane + 64 * t;
         const int row = static_cast<int>((static_cast<float>(e) + 0.5f) * inv);
-        pos[t] = e < p.kv ? row * rb.p2 + 8 + (e - row * k2) : -1;
+        pos[t] = e < p.kv ? row * rb.p2 + (e - row * k2) : -1;
     }
 }
 
@@ -1099,13 +1087,18 @@ __global__ __launch_bounds__(256) void k_dot_mfma(Prob p, TileShape ts, const in
             for (int c = wg.c0; c <= wg.c1; ++c) {
                 f32x4_t sc[2];
                 score_chunk<T, D>(Xs, c, col, grp, af, zero, sc);
-                const int e0 = chunk_entry(p, ln, rb, ts.rowshift, in0, u0, c, grp);
-                uint16_t* dst = e0 >= 0 ? myrow + e0 : dummy;
+                const int s0 = 32 * c + 8 * grp, r = s0 >> ts.rowshift, col0 = s0 & ((1 << ts.rowshift) - 1);
+                const bool rok = in0 && r >= ln.lo[1] && r <= ln.hi[1];
+                const int e0 = ((u0 - ln.lo[0]) * p.ax[1].k + r - ln.lo[1]) * rb.p2 + col0 - ln.lo[2];
+                const int d = rok ? col0 - ln.lo[2] : 0x40000000;
+                const unsigned k2 = static_cast<unsigned>(p.ax[2].k);
 #pragma unroll
                 for (int i = 0; i < 8; i += 2) {
                     const uint32_t v = Mma<T>::pack(sc[i >> 2][i & 3] * mul, sc[i >> 2][(i & 3) + 1] * mul);
-                    dst[i] = static_cast<uint16_t>(v);
-                    dst[i + 1] = static_cast<uint16_t>(v >> 16);
+                    uint16_t* a0 = static_cast<unsigned>(d + i) < k2 ? myrow + e0 + i : dummy;
+                    uint16_t* a1 = static_cast<unsigned>(d + i + 1) < k2 ? myrow + e0 + i + 1 : dummy;
+                    *a0 = static_cast<uint16_t>(v);
+                    *a1 = static_cast<uint16_t>(v >> 16);
                 }
             }
         }
@@ -1195,12 +1188,18 @@ __global__ __launch_bounds__(256) void k_wsum_mfma(Prob p, TileShape ts, const i
         if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
             for (int c = wg.c0; c <= wg.c1; ++c) {
-                const int e0 = chunk_entry(p, ln, rb, ts.rowshift, in0, u0, c, grp);
-                const uint16_t* src = e0 >= 0 ? myrow + e0 : zeros;
+                const int s0 = 32 * c + 8 * grp, r = s0 >> ts.rowshift, col0 = s0 & ((1 << ts.rowshift) - 1);
+                const bool rok = in0 && r >= ln.lo[1] && r <= ln.hi[1];
+                const int e0 = ((u0 - ln.lo[0]) * p.ax[1].k + r - ln.lo[1]) * rb.p2 + col0 - ln.lo[2];
+                const int d = rok ? col0 - ln.lo[2] : 0x40000000;
+                const unsigned k2 = static_cast<unsigned>(p.ax[2].k);
                 uint32_t wv[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    wv[i] = static_cast<uint32_t>(src[2 * i]) | (static_cast<uint32_t>(src[2 * i + 1]) << 16);
+                for (int i = 0; i < 4; ++i) {
+                    const uint16_t* a0 = static_cast<unsigned>(d + 2 * i) < k2 ? myrow + e0 + 2 * i : zeros;
+                    const uint16_t* a1 = static_cast<unsigned>(d + 2 * i + 1) < k2 ? myrow + e0 + 2 * i + 1 : zeros;
+                    wv[i] = static_cast<uint32_t>(*a0) | (static_cast<uint32_t>(*a1) << 16);
+                }
                 accumulate_chunk<T, D>(Xs, c, lane, make_uint4(wv[0], wv[1], wv[2], wv[3]), acc);
             }
         }
