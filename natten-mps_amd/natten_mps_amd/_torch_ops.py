@@ -64,16 +64,22 @@ def _define(rank: int) -> None:
     torch.library.impl(LIB, av_name, "Meta")(av_meta)
     torch.library.impl(LIB, fwd_name, "Meta")(fwd_meta)
 
-    # -- autograd ---------------------------------------------------------
+    # -- backward ops ---------------------------------------------------------
+    # The gradients are ops of their own (with Meta kernels), so that a
+    # compiled graph's backward traces them as opaque calls instead of
+    # tracing into the library with fake tensors.
+    LIB.define(f"{fwd_name}_backward(Tensor grad_out, Tensor query, Tensor key, Tensor value, int[] kernel_size, "
+               "int[] stride, int[] dilation, bool[] is_causal, float? scale) -> (Tensor, Tensor, Tensor)")
+    LIB.define(f"{qk_name}_backward(Tensor grad_attn, Tensor query, Tensor key, int[] kernel_size, int[] dilation, "
+               "int[] stride, bool[] is_causal, float? scale) -> (Tensor, Tensor)")
+    LIB.define(f"{av_name}_backward(Tensor grad_out, Tensor attn, Tensor value, int[] kernel_size, int[] dilation, "
+               "int[] stride, bool[] is_causal) -> (Tensor, Tensor)")
 
-    def _setup_fwd(ctx, inputs, output):
-        q, k, v, kernel_size, stride, dilation, is_causal, scale = inputs
-        ctx.params = (tuple(kernel_size), tuple(stride), tuple(dilation), tuple(is_causal), scale)
-        ctx.save_for_backward(q, k, v)
+    def _dense(grads, like):
+        return tuple(torch.zeros_like(t) if g is None else g for g, t in zip(grads, like))
 
-    def _fwd_backward(ctx, grad_output):
-        q, k, v = ctx.saved_tensors
-        ks, st, dil, causal, scale = ctx.params
+    def fwd_bwd_impl(grad_output, q, k, v, kernel_size, stride, dilation, is_causal, scale):
+        ks, st, dil, causal = tuple(kernel_size), tuple(stride), tuple(dilation), tuple(is_causal)
         sc = float(q.shape[-1] ** -0.5 if scale is None else scale)
         mod = ops.active_module()
         with_lse = getattr(mod, f"na{rank}d_forward_with_lse", None)
@@ -81,47 +87,78 @@ def _define(rank: int) -> None:
         if with_lse is not None and fused is not None:
             out, lse = with_lse(q, k, v, ks, st, dil, causal, sc)
             if lse is not None:
-                dq, dk, dv = fused(grad_output, q, k, v, out, lse, ks, dil, st, causal, sc)
-                return dq, dk, dv, None, None, None, None, None
+                return tuple(fused(grad_output, q, k, v, out, lse, ks, dil, st, causal, sc))
         res = _split_backward(rank, mod, grad_output, q, k, v, ks, st, dil, causal, sc)
         if res is None:
             with torch.enable_grad():
                 leaves = [t.detach().requires_grad_(True) for t in (q, k, v)]
                 out = getattr(mod, f"na{rank}d_forward")(*leaves, ks, st, dil, causal, sc)
                 res = torch.autograd.grad(out, leaves, grad_output, allow_unused=True)
-        return res[0], res[1], res[2], None, None, None, None, None
+        return _dense(res[:3], (q, k, v))
 
-    def _setup_qk(ctx, inputs, output):
-        q, k, kernel_size, dilation, stride, is_causal, scale = inputs
-        ctx.params = (tuple(kernel_size), tuple(dilation), tuple(stride), tuple(is_causal), scale)
-        ctx.save_for_backward(q, k)
-
-    def _qk_backward(ctx, grad_output):
-        q, k = ctx.saved_tensors
-        ks, dil, st, causal, scale = ctx.params
+    def qk_bwd_impl(grad_output, q, k, kernel_size, dilation, stride, is_causal, scale):
+        ks, dil, st, causal = tuple(kernel_size), tuple(dilation), tuple(stride), tuple(is_causal)
         res = getattr(ops, f"na{rank}d_qk_backward")(grad_output, q, k, ks, dil, st, causal, scale=scale)
         if res is None:
             with torch.enable_grad():
                 leaves = [t.detach().requires_grad_(True) for t in (q, k)]
                 out = qk_fwd(*leaves, ks, dil, st, causal, scale)
                 res = torch.autograd.grad(out, leaves, grad_output, allow_unused=True)
-        return res[0], res[1], None, None, None, None, None
+        return _dense(res[:2], (q, k))
 
-    def _setup_av(ctx, inputs, output):
-        attn, v, kernel_size, dilation, stride, is_causal = inputs
-        ctx.params = (tuple(kernel_size), tuple(dilation), tuple(stride), tuple(is_causal))
-        ctx.save_for_backward(attn, v)
-
-    def _av_backward(ctx, grad_output):
-        attn, v = ctx.saved_tensors
-        ks, dil, st, causal = ctx.params
+    def av_bwd_impl(grad_output, attn, v, kernel_size, dilation, stride, is_causal):
+        ks, dil, st, causal = tuple(kernel_size), tuple(dilation), tuple(stride), tuple(is_causal)
         res = getattr(ops, f"na{rank}d_av_backward")(grad_output, attn, v, ks, dil, st, causal)
         if res is None:
             with torch.enable_grad():
                 leaves = [t.detach().requires_grad_(True) for t in (attn, v)]
                 out = av_fwd(*leaves, ks, dil, st, causal)
                 res = torch.autograd.grad(out, leaves, grad_output, allow_unused=True)
-        return res[0], res[1], None, None, None, None
+        return _dense(res[:2], (attn, v))
+
+    for key in ("CUDA", "CPU"):
+        torch.library.impl(LIB, f"{fwd_name}_backward", key)(fwd_bwd_impl)
+        torch.library.impl(LIB, f"{qk_name}_backward", key)(qk_bwd_impl)
+        torch.library.impl(LIB, f"{av_name}_backward", key)(av_bwd_impl)
+    torch.library.impl(LIB, f"{fwd_name}_backward", "Meta")(
+        lambda g, q, k, v, *a: (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)))
+    torch.library.impl(LIB, f"{qk_name}_backward", "Meta")(
+        lambda g, q, k, *a: (torch.empty_like(q), torch.empty_like(k)))
+    torch.library.impl(LIB, f"{av_name}_backward", "Meta")(
+        lambda g, attn, v, *a: (torch.empty_like(attn), torch.empty_like(v)))
+
+    # -- autograd -------------------------------------------------------------
+    this = getattr(torch.ops, LIB.ns)
+
+    def _setup_fwd(ctx, inputs, output):
+        q, k, v, kernel_size, stride, dilation, is_causal, scale = inputs
+        ctx.params = (list(kernel_size), list(stride), list(dilation), list(is_causal), scale)
+        ctx.save_for_backward(q, k, v)
+
+    def _fwd_backward(ctx, grad_output):
+        q, k, v = ctx.saved_tensors
+        dq, dk, dv = getattr(this, f"{fwd_name}_backward")(grad_output, q, k, v, *ctx.params)
+        return dq, dk, dv, None, None, None, None, None
+
+    def _setup_qk(ctx, inputs, output):
+        q, k, kernel_size, dilation, stride, is_causal, scale = inputs
+        ctx.params = (list(kernel_size), list(dilation), list(stride), list(is_causal), scale)
+        ctx.save_for_backward(q, k)
+
+    def _qk_backward(ctx, grad_output):
+        q, k = ctx.saved_tensors
+        dq, dk = getattr(this, f"{qk_name}_backward")(grad_output, q, k, *ctx.params)
+        return dq, dk, None, None, None, None, None
+
+    def _setup_av(ctx, inputs, output):
+        attn, v, kernel_size, dilation, stride, is_causal = inputs
+        ctx.params = (list(kernel_size), list(dilation), list(stride), list(is_causal))
+        ctx.save_for_backward(attn, v)
+
+    def _av_backward(ctx, grad_output):
+        attn, v = ctx.saved_tensors
+        dattn, dv = getattr(this, f"{av_name}_backward")(grad_output, attn, v, *ctx.params)
+        return dattn, dv, None, None, None, None
 
     torch.library.register_autograd(f"natten_mps_amd::{fwd_name}", _fwd_backward, setup_context=_setup_fwd)
     torch.library.register_autograd(f"natten_mps_amd::{qk_name}", _qk_backward, setup_context=_setup_qk)

@@ -512,6 +512,41 @@ def test_split_ops_tile_path_strided_views():
     _close(xd.grad.cpu(), xr.grad, torch.bfloat16, "dqkv")
 
 
+def test_torch_library_ops_trace_under_compile():
+    """The torch.library ops (natten_mps_amd::na2d_fwd / na2d_qk / na2d_av)
+    trace with fake tensors under torch.compile(fullgraph=True) and, run
+    through the compiled graph (aot_eager: no code generation), give the
+    eager functional results bit for bit, forward and backward."""
+    import natten_mps_amd._torch_ops  # noqa: F401  (registers the ops)
+    from natten_mps_amd import functional as F
+
+    ops = torch.ops.natten_mps_amd
+    q, k, v, do = (t.to(DEV) for t in _inputs(97, [(2, 12, 14, 2, 32)] * 4, torch.bfloat16))
+
+    def fused(q, k, v):
+        return ops.na2d_fwd(q, k, v, [5, 5], [1, 1], [1, 2], [False, True], None)
+
+    def split(q, k, v):
+        logits = ops.na2d_qk(q, k, [5, 5], [1, 2], [1, 1], [False, True], 0.25)
+        return ops.na2d_av(torch.softmax(logits, -1), v, [5, 5], [1, 2], [1, 1], [False, True])
+
+    for fn, ref_fn in ((fused, lambda a, b, c: F.na2d(a, b, c, 5, dilation=(1, 2), is_causal=(False, True))),
+                       (split, lambda a, b, c: F.na2d_av(torch.softmax(F.na2d_qk(a, b, 5, (1, 2), is_causal=(False, True),
+                                                                                  scale=0.25), -1),
+                                                          c, 5, (1, 2), is_causal=(False, True)))):
+        torch._dynamo.reset()
+        compiled = torch.compile(fn, fullgraph=True, backend="aot_eager")
+        a = [t.clone().requires_grad_(True) for t in (q, k, v)]
+        out = compiled(*a)
+        out.backward(do)
+        b = [t.clone().requires_grad_(True) for t in (q, k, v)]
+        ref = ref_fn(*b)
+        ref.backward(do)
+        assert torch.equal(out, ref)
+        for x, y in zip(a, b):
+            assert torch.equal(x.grad, y.grad)
+
+
 def test_fused_equals_split_composition():
     """Reference check (tests/test_backward_parity.py): fused vs split QK ->
     softmax -> AV, outputs and gradients."""
