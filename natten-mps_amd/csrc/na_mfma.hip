@@ -186,16 +186,6 @@ struct Block {
     ClassAxis c[3];
 };
 
-__device__ __forceinline__ ClassAxis class_axis_of(const Axis& a, int r, const FastDiv& dil, int lenmod) {
-    ClassAxis c;
-    c.n = a.dil == 1 ? a.len : fdiv(a.len - r + a.dil - 1, dil);
-    c.K = a.k;
-    c.h = a.k >> 1;
-    c.causal = a.causal;
-    c.B = (a.dil == 1 || r < lenmod) ? c.n - 1 - 2 * c.h : c.n - a.k;
-    return c;
-}
-
 // The wave's part of the tile: items f = 16w .. 16w+15 in row-major tile
 // order; with power-of-two extents they cover a box, items [il, ih] per axis
 // (before clipping to the tile's extent).
@@ -1287,7 +1277,7 @@ __global__ __launch_bounds__(256) void k_wsum_key_mfma(Prob p, TileShape ts, con
                                                        LayK lx, T* __restrict__ out, LayK lo_in, float mul) {
     const LayK& lo = SAME ? lx : lo_in;
     unsigned char* smem = lds_base();
-    const int slots = ts.slots, kv = p.kv;
+    const int slots = ts.slots;
     T* Xs = reinterpret_cast<T*>(smem);
     int* OFF = reinterpret_cast<int*>(Xs + slots * D);
     uint16_t* Ws = reinterpret_cast<uint16_t*>(OFF + slots);
