@@ -1234,19 +1234,19 @@ __device__ __forceinline__ void stage_key_rows(const Prob& p, const Block& k, co
     const T* wb = bh_ptr(wt, lw, b, h) + slice_pos(p, k, u0) * lw.s0;
     const int lead = static_cast<int>((reinterpret_cast<uintptr_t>(wb) >> 1) & 1);  // wb is 4-byte aligned + 2 lead
     const __amdgpu_buffer_rsrc_t rw = rows_rsrc(wb - lead);
-    // in-plane offset of slot s's row (row 0 for slots outside the union:
-    // loaded, never read)
+    // in-plane offset of slot s's row, -1 for slots outside the union (not
+    // loaded; their LDS rows are never read unmasked)
     const auto row_off = [&](int s) {
         const int a1 = s >> ts.rowshift, a2 = s & mask2;
         return (a1 < k.U[1] && a2 < k.U[2])
                    ? (k.r[1] + (k.lo[1] + a1) * d1) * lw.s1 + (k.r[2] + (k.lo[2] + a2) * d2) * lw.s2
-                   : 0;
+                   : -1;
     };
     const int ws0 = class_ws(k.c[0], k.lo[0] + u0);
     for (int s = threadIdx.x; s < slots; s += blockDim.x) {
         const int a1 = s >> ts.rowshift, a2 = s & mask2;
         const int base = (ws0 * k1 + class_ws(k.c[1], k.lo[1] + a1)) * k2 + class_ws(k.c[2], k.lo[2] + a2);
-        OFF[s] = s * pitch + ((row_off(s) + lead) & 1) - base;
+        OFF[s] = s * pitch + ((max(row_off(s), 0) + lead) & 1) - base;
     }
     uint32_t* Ws32 = reinterpret_cast<uint32_t*>(Ws);
     const int half = lane >> 5, groups = ((kv + 2) / 2 + 31) / 32;  // 32-word groups of a row
@@ -1260,8 +1260,9 @@ __device__ __forceinline__ void stage_key_rows(const Prob& p, const Block& k, co
             for (int m = 0; m < 8; ++m) {
                 const int o0 = __builtin_amdgcn_readlane(offs, 2 * m);
                 const int o1 = __builtin_amdgcn_readlane(offs, 2 * m + 1);
-                const int first = (half ? o1 : o0) + lead;  // entry index from the aligned base
-                in[m] = j < (((first & 1) + kv + 1) >> 1);   // words holding entries of the row
+                const int off = half ? o1 : o0;
+                const int first = off + lead;  // entry index from the aligned base
+                in[m] = off >= 0 && j < (((first & 1) + kv + 1) >> 1);  // words holding entries of the row
                 v[m] = in[m] ? __builtin_amdgcn_raw_buffer_load_b32(rw, ((first >> 1) + j) * 4, 0, 0) : 0u;
             }
 #pragma unroll
