@@ -93,6 +93,15 @@ typedef struct {
 int natten_hip_abi_version(void);
 const char *natten_hip_last_error(void);
 
+/* Audit of the MFMA tile kernels (no counterpart in the reference): they
+ * address their staged operands at a constant LDS offset, which is sound
+ * only while no kernel instance declares static LDS.  Every instance is
+ * checked once per process (needs a device); returns 1 when the tile path
+ * is enabled, 0 when an instance has static LDS (the vector kernels then
+ * take every call and a message names it on stderr).  *checked (may be
+ * NULL) receives the number of instances whose attributes were read. */
+int natten_hip_mfma_lds_check(int32_t *checked);
+
 /* Fused forward: out = softmax(scale * q k^T over each neighbourhood) v, and
  * lse = log-sum-exp of the scaled logits (natural log).  Native GQA: query
  * head h reads key/value head h / (Hq/Hkv). */

@@ -140,6 +140,13 @@ int natten_hip_abi_version(void) { return NATTEN_HIP_ABI_VERSION; }
 
 const char* natten_hip_last_error(void) { return g_err; }
 
+int natten_hip_mfma_lds_check(int32_t* checked) {
+    int n = 0;
+    const int ok = na::mfma_lds_audit(&n);
+    if (checked) *checked = n;
+    return ok;
+}
+
 int natten_hip_forward(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
                        const natten_layout_t* lk, const void* v, const natten_layout_t* lv, void* out,
                        const natten_layout_t* lo, float* lse, const natten_layout_t* llse, void* stream) {

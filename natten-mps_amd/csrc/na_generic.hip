@@ -303,6 +303,33 @@ __global__ __launch_bounds__(256) void k_qk(Prob p, int vec,
     });
 }
 
+// Accumulator of the split ops' gathers (AV output, dq, dk, dv): a sum over
+// a whole window (or over every query attending a key), hundreds of products
+// in 3-D.  For fp32 operands it runs in double -- a product of two fp32
+// values is exact there, so the result is the correctly rounded sum, and no
+// summation-order noise of fp32 (which passes 1e-5 relative at 3-D window
+// sizes) reaches the output; 16-bit operands keep fp32 accumulators.
+template <typename T>
+struct GatherAcc {
+    using type = float;
+};
+template <>
+struct GatherAcc<float> {
+    using type = double;
+};
+
+template <typename A>
+__device__ __forceinline__ A gather_fma(float a, float b, A acc) {
+    return static_cast<A>(a) * static_cast<A>(b) + acc;
+}
+
+// acc (times mul) rounded to float for store_run.
+template <typename A, int DPL>
+__device__ __forceinline__ void gather_out(const A (&acc)[DPL], float mul, float (&out)[DPL]) {
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) out[j] = static_cast<float>(acc[j] * static_cast<A>(mul));
+}
+
 // ---------------------------------------------------------------------------
 // Split AV: out = sum_valid attn * v.
 // ---------------------------------------------------------------------------
@@ -316,9 +343,10 @@ __global__ __launch_bounds__(256) void k_av(Prob p, int vec,
     const int d0 = (threadIdx.x % LPQ) * DPL;
     const QPos Q = decode_query(p, qi);
     const T* row = attn + la.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h);
-    float acc[DPL];
+    using A = typename GatherAcc<T>::type;
+    A acc[DPL];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+    for (int j = 0; j < DPL; ++j) acc[j] = 0;
     if (vec) {
         struct Step {
             Raw<T, DPL> v;
@@ -335,7 +363,7 @@ __global__ __launch_bounds__(256) void k_av(Prob p, int vec,
                 float vv[DPL];
                 unpack_run<T, DPL>(st.v, d0, p.Dv, vv);
 #pragma unroll
-                for (int j = 0; j < DPL; ++j) acc[j] = fmaf(a, vv[j], acc[j]);
+                for (int j = 0; j < DPL; ++j) acc[j] = gather_fma(a, vv[j], acc[j]);
             });
     } else {
         for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
@@ -344,10 +372,12 @@ __global__ __launch_bounds__(256) void k_av(Prob p, int vec,
             float vv[DPL];
             load_run<T, DPL>(v + lv.at(Q.b, j0, j1, j2, Q.h), d0, p.Dv, vec, vv);
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) acc[j] = fmaf(a, vv[j], acc[j]);
+            for (int j = 0; j < DPL; ++j) acc[j] = gather_fma(a, vv[j], acc[j]);
         });
     }
-    store_run<T, DPL>(out + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, acc);
+    float res[DPL];
+    gather_out(acc, 1.f, res);
+    store_run<T, DPL>(out + lo.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h), d0, p.Dv, vec, res);
 }
 
 // ---------------------------------------------------------------------------
@@ -531,9 +561,10 @@ __global__ __launch_bounds__(256) void k_qk_bwd_q(Prob p, int vec,
     const int d0 = (threadIdx.x % LPQ) * DPL;
     const QPos Q = decode_query(p, qi);
     const T* row = da + lda.at(Q.b, Q.o0, Q.o1, Q.o2, Q.h);
-    float acc[DPL];
+    using A = typename GatherAcc<T>::type;
+    A acc[DPL];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+    for (int j = 0; j < DPL; ++j) acc[j] = 0;
     if (vec) {
         struct Step {
             Raw<T, DPL> k;
@@ -550,7 +581,7 @@ __global__ __launch_bounds__(256) void k_qk_bwd_q(Prob p, int vec,
                 float kv[DPL];
                 unpack_run<T, DPL>(st.k, d0, p.Dqk, kv);
 #pragma unroll
-                for (int j = 0; j < DPL; ++j) acc[j] = fmaf(g, kv[j], acc[j]);
+                for (int j = 0; j < DPL; ++j) acc[j] = gather_fma(g, kv[j], acc[j]);
             });
     } else {
         for_each_neighbor(p, Q.i0, Q.i1, Q.i2, [&](int j0, int j1, int j2, int e, bool ok) {
@@ -559,14 +590,12 @@ __global__ __launch_bounds__(256) void k_qk_bwd_q(Prob p, int vec,
             float kv[DPL];
             load_run<T, DPL>(k + lk.at(Q.b, j0, j1, j2, Q.h), d0, p.Dqk, vec, kv);
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) acc[j] = fmaf(g, kv[j], acc[j]);
+            for (int j = 0; j < DPL; ++j) acc[j] = gather_fma(g, kv[j], acc[j]);
         });
     }
-    if (p.has_scale) {
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[j] *= p.scale;
-    }
-    store_run<T, DPL>(dq + ldq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, acc);
+    float res[DPL];
+    gather_out(acc, p.has_scale ? p.scale : 1.f, res);
+    store_run<T, DPL>(dq + ldq.at(Q.b, Q.i0, Q.i1, Q.i2, Q.h), d0, p.Dqk, vec, res);
 }
 
 template <typename T, int DPL, int LPQ>
@@ -578,21 +607,20 @@ __global__ __launch_bounds__(256) void k_qk_bwd_k(Prob p, int vec,
     if (ki >= static_cast<long long>(p.B) * p.nkey * p.Hkv) return;
     const int d0 = (threadIdx.x % LPQ) * DPL;
     const KPos K = decode_key(p, ki, p.Hkv);
-    float acc[DPL];
+    using A = typename GatherAcc<T>::type;
+    A acc[DPL];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+    for (int j = 0; j < DPL; ++j) acc[j] = 0;
     for_each_query(p, K.m0, K.m1, K.m2, [&](int o0, int o1, int o2, int i0, int i1, int i2, int e) {
         const float g = to_f(da[lda.at(K.b, o0, o1, o2, K.h) + e]);
         float qv[DPL];
         load_run<T, DPL>(q + lq.at(K.b, i0, i1, i2, K.h), d0, p.Dqk, vec, qv);
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(g, qv[j], acc[j]);
+        for (int j = 0; j < DPL; ++j) acc[j] = gather_fma(g, qv[j], acc[j]);
     });
-    if (p.has_scale) {
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[j] *= p.scale;
-    }
-    store_run<T, DPL>(dk + ldk.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dqk, vec, acc);
+    float res[DPL];
+    gather_out(acc, p.has_scale ? p.scale : 1.f, res);
+    store_run<T, DPL>(dk + ldk.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dqk, vec, res);
 }
 
 // ---------------------------------------------------------------------------
@@ -648,17 +676,20 @@ __global__ __launch_bounds__(256) void k_av_bwd_v(Prob p, int vec,
     if (ki >= static_cast<long long>(p.B) * p.nkey * p.Hkv) return;
     const int d0 = (threadIdx.x % LPQ) * DPL;
     const KPos K = decode_key(p, ki, p.Hkv);
-    float acc[DPL];
+    using A = typename GatherAcc<T>::type;
+    A acc[DPL];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+    for (int j = 0; j < DPL; ++j) acc[j] = 0;
     for_each_query(p, K.m0, K.m1, K.m2, [&](int o0, int o1, int o2, int, int, int, int e) {
         const float a = to_f(attn[la.at(K.b, o0, o1, o2, K.h) + e]);
         float dov[DPL];
         load_run<T, DPL>(dout + ldo.at(K.b, o0, o1, o2, K.h), d0, p.Dv, vec, dov);
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[j] = fmaf(a, dov[j], acc[j]);
+        for (int j = 0; j < DPL; ++j) acc[j] = gather_fma(a, dov[j], acc[j]);
     });
-    store_run<T, DPL>(dv + ldv.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dv, vec, acc);
+    float res[DPL];
+    gather_out(acc, 1.f, res);
+    store_run<T, DPL>(dv + ldv.at(K.b, K.m0, K.m1, K.m2, K.h), d0, p.Dv, vec, res);
 }
 
 // ---------------------------------------------------------------------------

@@ -57,6 +57,11 @@ hipError_t rpb_av_backward(const Prob& p, const void* dout, Lay ldo, const void*
 namespace na {
 
 // MFMA tile path (na_mfma.hip): bf16/fp16, stride 1, equal head dims 32/64/128.
+// mfma_static_lds_ok: no tile kernel instance declares static LDS (checked
+// once per process); mfma_lds_audit returns 1 when so, 0 otherwise, and the
+// number of instances whose attributes were read.
+bool mfma_static_lds_ok();
+int mfma_lds_audit(int* checked);
 bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward);
 bool mfma_offsets_fit(const Prob& p, std::initializer_list<Lay> lays);
 hipError_t mfma_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,

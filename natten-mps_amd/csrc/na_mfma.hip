@@ -40,12 +40,14 @@
 // k = 8*(lane/16) .. +7; C column = lane%16, rows 4*(lane/16) .. +3.
 #include <algorithm>
 #include <cstddef>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <type_traits>
 #include <vector>
 
+#include "na_exact.h"
 #include "na_launch.h"
 
 namespace na {
@@ -57,7 +59,6 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -122,6 +123,34 @@ __device__ __forceinline__ float sum_rows(float v) {
     v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
     const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Sum of a lane's accumulators (plus `extra`): not finite exactly when one
+// of them is not finite (a sum of finite accumulators of this size cannot
+// overflow).
+template <int N>
+__device__ __forceinline__ float lane_sum(const f32x4_t (&a)[N], float extra) {
+    float s = extra;
+#pragma unroll
+    for (int db = 0; db < N; ++db) s += (a[db][0] + a[db][1]) + (a[db][2] + a[db][3]);
+    return s;
+}
+
+// True when a lane's part of an item's result is not finite: the lane then
+// recomputes its dims exactly (na_exact.h).  A contamination from outside the
+// window reaches either every dim of an item (through a probability or score
+// gradient) or only the dims that hold a non-finite operand element, so the
+// lanes of one item need not agree: each lane's finite dims are exact.
+// Tested on the exponent bits, independent of floating-point flags.
+__device__ __forceinline__ bool item_nonfinite(float lane_total) {
+    return (__float_as_uint(lane_total) & 0x7F800000u) == 0x7F800000u;
+}
+
+// x, hidden from value numbering: the recompute after a walk derives the
+// lane's position afresh instead of keeping the walk's copy live through it.
+__device__ __forceinline__ int opaque(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
 }
 
 __device__ __forceinline__ float max8(const f32x4_t (&s)[2]) {
@@ -407,6 +436,8 @@ __device__ __forceinline__ int vol_off(const LayK& lay, const int (&pos)[3]) {
     return pos[0] * lay.s0 + pos[1] * lay.s1 + pos[2] * lay.s2;
 }
 
+__device__ __forceinline__ Strides3 strides3(const LayK& lay) { return Strides3{lay.s0, lay.s1, lay.s2}; }
+
 template <typename T>
 __device__ __forceinline__ const T* plane_of(const T* g, const LayK& lay, int b, int h, int p0) {
     return bh_ptr(g, lay, b, h) + p0 * lay.s0;
@@ -567,7 +598,7 @@ enum KernelId { kKernFwd, kKernBwdQ, kKernBwdKV };
 
 constexpr int waves_per_simd(KernelId k, int D, bool wide) {
     if (D == 32) return wide ? 4 : 5;
-    if (D == 64) return k == kKernBwdQ || (k == kKernBwdKV && wide) ? 4 : 1;
+    if (D == 64) return k == kKernFwd || k == kKernBwdQ || (k == kKernBwdKV && wide) ? 4 : 1;
     return 1;
 }
 
@@ -615,16 +646,131 @@ __device__ __forceinline__ int slice_pos(const Prob& p, const Block& k, int u0) 
     return k.r[0] + (k.lo[0] + u0) * p.ax[0].dil;
 }
 
+// Kernel arguments, one struct per kernel: the kernel receives it by value
+// (its only explicit argument, so it sits at offset 0 of the kernel-argument
+// segment), and the exact recomputation after a walk reads it again from
+// there through the segment pointer -- so the walk holds none of the
+// pointers and layouts only the recomputation needs.
+template <typename T>
+struct FwdArgs {
+    Prob p;
+    TileShape ts;
+    const int* geo;
+    const T *q, *k, *v;
+    T* out;
+    float* lse;
+    LayK lq, lk, lv, lo, ll;
+};
+
+template <typename T>
+struct BwdQArgs {
+    Prob p;
+    TileShape ts;
+    const int* geo;
+    const T *q, *k, *v, *o, *dout;
+    const float *lse, *dlse;
+    T* dq;
+    float* delta;
+    LayK lq, lk, lv, lo, ldo, ll, ldl, ldq, lde;
+};
+
+template <typename T>
+struct BwdKvArgs {
+    Prob p;
+    TileShape ts;
+    const int* geo;
+    const T *q, *k, *v, *dout;
+    const float *lse, *delta;
+    T *dk, *dv;
+    LayK lq, lk, lv, ldo, ll, lde, ldk, ldv;
+};
+
+// Split products: weights w (rows of KV entries), staged operand x, out.
+template <typename T>
+struct WsumArgs {
+    Prob p;
+    TileShape ts;
+    const int* geo;
+    const T *w, *x;
+    T* out;
+    LayK lw, lx, lo;
+    float mul;
+};
+
+// The lane's item from the (XCD-remapped) workgroup index x alone (the
+// decode of tile_geometry without the unions): batch, the workgroup's run of
+// heads [h0, h1) and the position; false for lanes past the tile.
+__device__ __forceinline__ bool lane_position(const Prob& p, const TileShape& ts, int x, int wave, int col, int& b,
+                                              int& h0, int& h1, int (&pos)[3]) {
+    int q = fdiv(x, ts.hchunks);
+    h0 = (x - q * static_cast<int>(ts.hchunks.d)) * ts.h_per;
+    h1 = min(h0 + ts.h_per, ts.nheads);
+    x = q;
+    q = fdiv(x, ts.spatial);
+    const int s = x - q * static_cast<int>(ts.spatial.d);
+    b = q;
+    int t[3], r[3];
+    spatial_coords(ts, s, t, r);
+    const int f = wave * 16 + col, s2 = ts.tshift[2], s1 = ts.tshift[1];
+    const int e[3] = {f >> (s2 + s1), (f >> s2) & (ts.T[1] - 1), f & (ts.T[2] - 1)};
+    bool ok = true;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const int n = fdiv(p.ax[a].len - r[a] + p.ax[a].dil - 1, ts.dil[a]);
+        const int j = t[a] * ts.T[a] + e[a];
+        ok = ok && j < n;
+        pos[a] = r[a] + j * p.ax[a].dil;
+    }
+    return ok;
+}
+
+// The kernel's argument segment as a generic pointer, hidden from value
+// numbering, so that what the recomputation reads through it are fresh
+// scalar loads rather than values the walk would have to keep live.  Valid
+// in kernel code only (the recomputation is inlined into its kernel).
+__device__ __forceinline__ const void* kernargs() {
+    auto ka = __builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ka));
+    return (const void*)ka;  // address-space conversion to a generic pointer
+}
+
 // ---------------------------------------------------------------------------
 // Forward: out = softmax(scale q.k) v over each window, lse (natural log).
 // Online softmax over groups of fwd_group<D>() chunks (one max reduction and
 // one rescale per group).
 // ---------------------------------------------------------------------------
 template <typename T, int D, int LAY, bool WIDE>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfma(
-    Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
-    LayK lk_in, const T* __restrict__ vg, LayK lv_in, T* __restrict__ out, LayK lo_in, float* __restrict__ lse,
-    LayK ll) {
+__device__ __forceinline__ void redo_fwd(const void* kargs, int wg, int wave, int col, int grp) {
+    const FwdArgs<T>& A = *static_cast<const FwdArgs<T>*>(kargs);
+    const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
+    const LayK &ao = LAY == kLayGeneral ? A.lo : aq, &al = A.ll;
+    int b, h0, h1, pos[3];
+    if (!lane_position(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    ExactAxis x[3];
+    for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
+    f32x4_t acc[D / 16];
+#pragma unroll 1
+    for (int h = h0; h < h1; ++h) {
+        const int hk = kv_head(A.ts, h);
+        float lse_v;
+        exact_forward<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), bh_ptr(A.k, ak, b, hk),
+                            strides3(ak), bh_ptr(A.v, av, b, hk), strides3(av), grp, acc, lse_v);
+        store_rows<T, D>(bh_ptr(A.out, ao, b, h), vol_off(ao, pos), grp, acc, 1.f);
+        if (grp == 0) bh_ptr(A.lse, al, b, h)[vol_off(al, pos)] = lse_v;
+    }
+}
+
+template <typename T, int D, int LAY, bool WIDE>
+__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfma(FwdArgs<T> args) {
+    const Prob& p = args.p;
+    const TileShape& ts = args.ts;
+    const int* __restrict__ geo = args.geo;
+    const T* __restrict__ q = args.q;
+    const T* __restrict__ kg = args.k;
+    const T* __restrict__ vg = args.v;
+    T* __restrict__ out = args.out;
+    float* __restrict__ lse = args.lse;
+    const LayK &lq = args.lq, &lk_in = args.lk, &lv_in = args.lv, &lo_in = args.lo, &ll = args.ll;
     const LayK& lk = LAY == kLayOne ? lq : lk_in;
     const LayK& lv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : lv_in;
     const LayK& lo = LAY == kLayGeneral ? lo_in : lq;
@@ -654,7 +800,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfm
     uint4 qf[D / 32];
     f32x4_t acc[D / 16], lacc;
     float m;
-    bool more = true, fresh = true;
+    bool more = true, fresh = true, redo = false;
     while (more) {
         const int b = w.b, h = w.h, u0 = w.u0;
         if (fresh) {
@@ -721,12 +867,18 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfm
             stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0),
                              lv, Vs, wave);
         }
-        if ((fresh || !more) && ln.valid) {
-            const float lsum = lacc[0];
-            store_rows<T, D>(bh_ptr(out, lo, b, h), vol_off(lo, ln.pos), grp, acc, 1.f / lsum);
-            if (grp == 0) bh_ptr(lse, ll, b, h)[vol_off(ll, ln.pos)] = (m + __log2f(lsum)) * kLn2;
+        if (fresh || !more) {
+            redo = redo || (item_nonfinite(lane_sum(acc, lacc[0])) && ln.valid);
+            if (ln.valid) {
+                const float lsum = lacc[0];
+                store_rows<T, D>(bh_ptr(out, lo, b, h), vol_off(lo, ln.pos), grp, acc, 1.f / lsum);
+                if (grp == 0) bh_ptr(lse, ll, b, h)[vol_off(ll, ln.pos)] = (m + __log2f(lsum)) * kLn2;
+            }
         }
     }
+    // items whose tile result was not finite: exact recomputation (the
+    // walk's state is dead here, so this costs the loop no registers)
+    if (redo) redo_fwd<T, D, LAY, WIDE>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
 }
 
 // ---------------------------------------------------------------------------
@@ -735,11 +887,45 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfm
 // dP = dO . v.  The dP product starts from -delta.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int LAY, bool WIDE>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_mfma(
-    Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
-    LayK lk_in, const T* __restrict__ vg, LayK lv_in, const T* __restrict__ o, LayK lo_in,
-    const T* __restrict__ dout, LayK ldo_in, const float* __restrict__ lse, LayK ll, const float* __restrict__ dlse,
-    LayK ldl_in, T* __restrict__ dq, LayK ldq_in, float* __restrict__ delta, LayK lde_in) {
+__device__ __forceinline__ void redo_bwd_q(const void* kargs, int wg, int wave, int col, int grp) {
+    const BwdQArgs<T>& A = *static_cast<const BwdQArgs<T>*>(kargs);
+    const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
+    const LayK &ao = LAY == kLayGeneral ? A.lo : aq, &ado = LAY == kLayGeneral ? A.ldo : aq;
+    const LayK &adq = LAY == kLayGeneral ? A.ldq : aq, &al = A.ll, &adl = LAY == kLayGeneral ? A.ldl : al;
+    int b, h0, h1, pos[3];
+    if (!lane_position(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    ExactAxis x[3];
+    for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
+    f32x4_t acc[D / 16];
+#pragma unroll 1
+    for (int h = h0; h < h1; ++h) {
+        const int hk = kv_head(A.ts, h);
+        const T* do_row = bh_ptr(A.dout, ado, b, h) + vol_off(ado, pos);
+        float di = exact_dot<T, D>(do_row, bh_ptr(A.o, ao, b, h) + vol_off(ao, pos));
+        if (A.dlse) di -= bh_ptr(A.dlse, adl, b, h)[vol_off(adl, pos)];
+        exact_backward_q<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), do_row,
+                               bh_ptr(A.lse, al, b, h)[vol_off(al, pos)], di, bh_ptr(A.k, ak, b, hk), strides3(ak),
+                               bh_ptr(A.v, av, b, hk), strides3(av), grp, acc);
+        store_rows<T, D>(bh_ptr(A.dq, adq, b, h), vol_off(adq, pos), grp, acc, A.p.scale);
+    }
+}
+
+template <typename T, int D, int LAY, bool WIDE>
+__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_mfma(BwdQArgs<T> args) {
+    const Prob& p = args.p;
+    const TileShape& ts = args.ts;
+    const int* __restrict__ geo = args.geo;
+    const T* __restrict__ q = args.q;
+    const T* __restrict__ kg = args.k;
+    const T* __restrict__ vg = args.v;
+    const T* __restrict__ o = args.o;
+    const T* __restrict__ dout = args.dout;
+    const float* __restrict__ lse = args.lse;
+    const float* __restrict__ dlse = args.dlse;
+    T* __restrict__ dq = args.dq;
+    float* __restrict__ delta = args.delta;
+    const LayK &lq = args.lq, &lk_in = args.lk, &lv_in = args.lv, &lo_in = args.lo, &ldo_in = args.ldo;
+    const LayK &ll = args.ll, &ldl_in = args.ldl, &ldq_in = args.ldq, &lde_in = args.lde;
     const LayK& lk = LAY == kLayOne ? lq : lk_in;
     const LayK& lv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : lv_in;
     const LayK& lo = LAY == kLayGeneral ? lo_in : lq;
@@ -772,7 +958,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_
     uint4 qf[D / 32], gf[D / 32];
     f32x4_t acc[D / 16], nd[2];
     float L2;
-    bool more = true, fresh = true;
+    bool more = true, fresh = true, redo = false;
     while (more) {
         const int b = w.b, h = w.h, u0 = w.u0;
         if (fresh) {
@@ -830,9 +1016,12 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_
             stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0),
                              lv, Vs, wave);
         }
-        if ((fresh || !more) && ln.valid)
-            store_rows<T, D>(bh_ptr(dq, ldq, b, h), vol_off(ldq, ln.pos), grp, acc, p.scale);
+        if (fresh || !more) {
+            redo = redo || (item_nonfinite(lane_sum(acc, 0.f)) && ln.valid);
+            if (ln.valid) store_rows<T, D>(bh_ptr(dq, ldq, b, h), vol_off(ldq, ln.pos), grp, acc, p.scale);
+        }
     }
+    if (redo) redo_bwd_q<T, D, LAY, WIDE>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
 }
 
 // ---------------------------------------------------------------------------
@@ -865,11 +1054,55 @@ __device__ __forceinline__ void stage_scalars(const Prob& p, const Block& k, con
 }
 
 template <typename T, int D, int LAY, bool WIDE>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_kv_mfma(
-    Prob p, TileShape ts, const int* __restrict__ geo, const T* __restrict__ q, LayK lq, const T* __restrict__ kg,
-    LayK lk_in, const T* __restrict__ vg, LayK lv_in, const T* __restrict__ dout, LayK ldo_in,
-    const float* __restrict__ lse, LayK ll, const float* __restrict__ delta, LayK lde_in, T* __restrict__ dk,
-    LayK ldk_in, T* __restrict__ dv, LayK ldv_in) {
+__device__ __forceinline__ void redo_bwd_kv(const void* kargs, int wg, int wave, int col, int grp) {
+    const BwdKvArgs<T>& A = *static_cast<const BwdKvArgs<T>*>(kargs);
+    const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
+    const LayK& adk = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.ldk;
+    const LayK& adv = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.ldv;
+    const LayK &ado = LAY == kLayGeneral ? A.ldo : aq, &al = A.ll, &ade = LAY == kLayGeneral ? A.lde : al;
+    int b, h0, h1, pos[3];
+    if (!lane_position(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    ExactAxis x[3];
+    for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
+    f32x4_t g[D / 16];
+    const int rep = A.p.rep;
+#pragma unroll 1
+    for (int hk = h0; hk < h1; ++hk) {
+        const T* k_row = bh_ptr(A.k, ak, b, hk) + vol_off(ak, pos);
+        const T* v_row = bh_ptr(A.v, av, b, hk) + vol_off(av, pos);
+        // dv, then dk, each summed over the q heads of the group
+        exact_zero(g);
+#pragma unroll 1
+        for (int h = hk * rep; h < (hk + 1) * rep; ++h)
+            exact_backward_kv<T, D, true>(A.p.scale, x, k_row, v_row, bh_ptr(A.q, aq, b, h), strides3(aq),
+                                          bh_ptr(A.dout, ado, b, h), strides3(ado), bh_ptr(A.lse, al, b, h),
+                                          strides3(al), bh_ptr(A.delta, ade, b, h), strides3(ade), grp, g);
+        store_rows<T, D>(bh_ptr(A.dv, adv, b, hk), vol_off(adv, pos), grp, g, 1.f);
+        exact_zero(g);
+#pragma unroll 1
+        for (int h = hk * rep; h < (hk + 1) * rep; ++h)
+            exact_backward_kv<T, D, false>(A.p.scale, x, k_row, v_row, bh_ptr(A.q, aq, b, h), strides3(aq),
+                                           bh_ptr(A.dout, ado, b, h), strides3(ado), bh_ptr(A.lse, al, b, h),
+                                           strides3(al), bh_ptr(A.delta, ade, b, h), strides3(ade), grp, g);
+        store_rows<T, D>(bh_ptr(A.dk, adk, b, hk), vol_off(adk, pos), grp, g, A.p.scale);
+    }
+}
+
+template <typename T, int D, int LAY, bool WIDE>
+__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_kv_mfma(BwdKvArgs<T> args) {
+    const Prob& p = args.p;
+    const TileShape& ts = args.ts;
+    const int* __restrict__ geo = args.geo;
+    const T* __restrict__ q = args.q;
+    const T* __restrict__ kg = args.k;
+    const T* __restrict__ vg = args.v;
+    const T* __restrict__ dout = args.dout;
+    const float* __restrict__ lse = args.lse;
+    const float* __restrict__ delta = args.delta;
+    T* __restrict__ dk = args.dk;
+    T* __restrict__ dv = args.dv;
+    const LayK &lq = args.lq, &lk_in = args.lk, &lv_in = args.lv, &ldo_in = args.ldo, &ll = args.ll;
+    const LayK &lde_in = args.lde, &ldk_in = args.ldk, &ldv_in = args.ldv;
     const LayK& lk = LAY == kLayOne ? lq : lk_in;
     const LayK& lv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : lv_in;
     const LayK& ldk = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : ldk_in;
@@ -906,7 +1139,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_k
 
     uint4 kf[D / 32], vf[D / 32];
     f32x4_t gk[D / 16], gv[D / 16];
-    bool more = true, fresh = true;
+    bool more = true, fresh = true, redo = false;
     int sl = 0;  // slice index within the pair: q head (sl / U0) and axis-0 slice (sl % U0)
     while (more) {
         const int b = w.b, hk = w.h, u0 = sl % blk.U[0];
@@ -967,11 +1200,15 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_k
                              ldo, Gs, wave);
             stage_scalars<T>(p, blk, ts, w.b, h, p0, lse, ll, delta, lde, NL, ND);
         }
-        if (fresh && ln.valid) {
-            store_rows<T, D>(bh_ptr(dk, ldk, b, hk), vol_off(ldk, ln.pos), grp, gk, p.scale);
-            store_rows<T, D>(bh_ptr(dv, ldv, b, hk), vol_off(ldv, ln.pos), grp, gv, 1.f);
+        if (fresh) {
+            redo = redo || (item_nonfinite(lane_sum(gk, lane_sum(gv, 0.f))) && ln.valid);
+            if (ln.valid) {
+                store_rows<T, D>(bh_ptr(dk, ldk, b, hk), vol_off(ldk, ln.pos), grp, gk, p.scale);
+                store_rows<T, D>(bh_ptr(dv, ldv, b, hk), vol_off(ldv, ln.pos), grp, gv, 1.f);
+            }
         }
     }
+    if (redo) redo_bwd_kv<T, D, LAY, WIDE>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
 }
 
 // ---------------------------------------------------------------------------
@@ -1120,9 +1357,31 @@ __global__ __launch_bounds__(256) void k_dot_mfma(Prob p, TileShape ts, const in
 }
 
 template <typename T, int D, bool SAME>
-__global__ __launch_bounds__(256) void k_wsum_mfma(Prob p, TileShape ts, const int* __restrict__ geo,
-                                                   const T* __restrict__ wt, LayK lw, const T* __restrict__ xg,
-                                                   LayK lx, T* __restrict__ out, LayK lo_in, float mul) {
+__device__ __forceinline__ void redo_wsum(const void* kargs, int wg, int wave, int col, int grp) {
+    const WsumArgs<T>& A = *static_cast<const WsumArgs<T>*>(kargs);
+    const LayK &aw = A.lw, &ax = A.lx, &ao = SAME ? ax : A.lo;
+    int b, h0, h1, pos[3];
+    if (!lane_position(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    ExactAxis x[3];
+    for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
+    f32x4_t acc[D / 16];
+#pragma unroll 1
+    for (int h = h0; h < h1; ++h) {
+        exact_wsum<T, D>(x, bh_ptr(A.w, aw, b, h) + vol_off(aw, pos), bh_ptr(A.x, ax, b, h), strides3(ax), grp, acc);
+        store_rows<T, D>(bh_ptr(A.out, ao, b, h), vol_off(ao, pos), grp, acc, A.mul);
+    }
+}
+
+template <typename T, int D, bool SAME>
+__global__ __launch_bounds__(256) void k_wsum_mfma(WsumArgs<T> args) {
+    const Prob& p = args.p;
+    const TileShape& ts = args.ts;
+    const int* __restrict__ geo = args.geo;
+    const T* __restrict__ wt = args.w;
+    const T* __restrict__ xg = args.x;
+    T* __restrict__ out = args.out;
+    const LayK &lw = args.lw, &lx = args.lx, &lo_in = args.lo;
+    const float mul = args.mul;
     const LayK& lo = SAME ? lx : lo_in;
     unsigned char* smem = lds_base();
     T* Xs = reinterpret_cast<T*>(smem);
@@ -1148,7 +1407,7 @@ __global__ __launch_bounds__(256) void k_wsum_mfma(Prob p, TileShape ts, const i
     const uint16_t* const myrow = Rw + col * rb.pitch;
     const int nclear = rb.pitch * 2 + 2;  // 16-byte pieces of the block
     f32x4_t acc[D / 16];
-    bool more = true, fresh = true;
+    bool more = true, fresh = true, redo = false;
     while (more) {
         const int b = w.b, h = w.h, u0 = w.u0;
         if (fresh) {
@@ -1199,8 +1458,12 @@ __global__ __launch_bounds__(256) void k_wsum_mfma(Prob p, TileShape ts, const i
             const T* pl = plane_of(xg, lx, w.b, w.h, slice_pos(p, blk, w.u0));
             stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
         }
-        if ((fresh || !more) && ln.valid) store_rows<T, D>(bh_ptr(out, lo, b, h), vol_off(lo, ln.pos), grp, acc, mul);
+        if (fresh || !more) {
+            redo = redo || (item_nonfinite(lane_sum(acc, 0.f)) && ln.valid);
+            if (ln.valid) store_rows<T, D>(bh_ptr(out, lo, b, h), vol_off(lo, ln.pos), grp, acc, mul);
+        }
     }
+    if (redo) redo_wsum<T, D, SAME>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
 }
 
 // ---------------------------------------------------------------------------
@@ -1273,9 +1536,31 @@ __device__ __forceinline__ void stage_key_rows(const Prob& p, const Block& k, co
 }
 
 template <typename T, int D, bool SAME>
-__global__ __launch_bounds__(256) void k_wsum_key_mfma(Prob p, TileShape ts, const int* __restrict__ geo,
-                                                       const T* __restrict__ wt, LayK lw, const T* __restrict__ xg,
-                                                       LayK lx, T* __restrict__ out, LayK lo_in, float mul) {
+__device__ __forceinline__ void redo_wsum_key(const void* kargs, int wg, int wave, int col, int grp) {
+    const WsumArgs<T>& A = *static_cast<const WsumArgs<T>*>(kargs);
+    const LayK &aw = A.lw, &ax = A.lx, &ao = SAME ? ax : A.lo;
+    int b, h0, h1, pos[3];
+    if (!lane_position(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    ExactAxis x[3];
+    for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
+    f32x4_t acc[D / 16];
+#pragma unroll 1
+    for (int h = h0; h < h1; ++h) {
+        exact_wsum_key<T, D>(x, bh_ptr(A.w, aw, b, h), strides3(aw), bh_ptr(A.x, ax, b, h), strides3(ax), grp, acc);
+        store_rows<T, D>(bh_ptr(A.out, ao, b, h), vol_off(ao, pos), grp, acc, A.mul);
+    }
+}
+
+template <typename T, int D, bool SAME>
+__global__ __launch_bounds__(256) void k_wsum_key_mfma(WsumArgs<T> args) {
+    const Prob& p = args.p;
+    const TileShape& ts = args.ts;
+    const int* __restrict__ geo = args.geo;
+    const T* __restrict__ wt = args.w;
+    const T* __restrict__ xg = args.x;
+    T* __restrict__ out = args.out;
+    const LayK &lw = args.lw, &lx = args.lx, &lo_in = args.lo;
+    const float mul = args.mul;
     const LayK& lo = SAME ? lx : lo_in;
     unsigned char* smem = lds_base();
     const int slots = ts.slots;
@@ -1313,7 +1598,7 @@ __global__ __launch_bounds__(256) void k_wsum_key_mfma(Prob p, TileShape ts, con
     col_masks(0, cm0);
     const bool wide = ts.rowshift > 5;
     f32x4_t acc[D / 16];
-    bool more = true, fresh = true;
+    bool more = true, fresh = true, redo = false;
     while (more) {
         const int b = w.b, h = w.h, u0 = w.u0;
         {
@@ -1351,8 +1636,12 @@ __global__ __launch_bounds__(256) void k_wsum_key_mfma(Prob p, TileShape ts, con
         }
         more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
-        if ((fresh || !more) && ln.valid) store_rows<T, D>(bh_ptr(out, lo, b, h), vol_off(lo, ln.pos), grp, acc, mul);
+        if (fresh || !more) {
+            redo = redo || (item_nonfinite(lane_sum(acc, 0.f)) && ln.valid);
+            if (ln.valid) store_rows<T, D>(bh_ptr(out, lo, b, h), vol_off(lo, ln.pos), grp, acc, mul);
+        }
     }
+    if (redo) redo_wsum_key<T, D, SAME>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
 }
 
 }  // namespace
@@ -1669,9 +1958,9 @@ hipError_t run_fwd(const Prob& p, TileShape ts, const void* q, Lay lq, const voi
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
     const int* geo = geometry_table(p, ts, false, s);
-    NA_LAUNCH("na_fwd_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, p,
-              ts, geo, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv), (T*)o, to_k(lo), lse,
-              to_k(ll));
+    const FwdArgs<T> a{p,       ts,       geo,      (const T*)q, (const T*)k, (const T*)v, (T*)o,
+                       lse,     to_k(lq), to_k(lk), to_k(lv),    to_k(lo),    to_k(ll)};
+    NA_LAUNCH("na_fwd_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
     return hipGetLastError();
 }
 
@@ -1707,9 +1996,10 @@ hipError_t run_bwd_q(const Prob& p, TileShape ts, const void* q, Lay lq, const v
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
     const int* geo = geometry_table(p, ts, false, s);
-    NA_LAUNCH("na_bwd_q_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s,
-              p, ts, geo, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv), (const T*)o, to_k(lo),
-              (const T*)dout, to_k(ldo), lse, to_k(ll), dlse, to_k(ldl), (T*)dq, to_k(ldq), delta, to_k(lde));
+    const BwdQArgs<T> a{p,        ts,       geo,      (const T*)q, (const T*)k, (const T*)v, (const T*)o,
+                        (const T*)dout, lse, dlse,  (T*)dq,      delta,       to_k(lq),    to_k(lk),
+                        to_k(lv), to_k(lo), to_k(ldo), to_k(ll),  to_k(ldl),   to_k(ldq),   to_k(lde)};
+    NA_LAUNCH("na_bwd_q_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
     return hipGetLastError();
 }
 
@@ -1723,9 +2013,10 @@ hipError_t run_bwd_kv(const Prob& p, TileShape ts, const void* q, Lay lq, const 
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
     const int* geo = geometry_table(p, ts, true, s);
-    NA_LAUNCH("na_bwd_kv_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s,
-              p, ts, geo, (const T*)q, to_k(lq), (const T*)k, to_k(lk), (const T*)v, to_k(lv), (const T*)dout,
-              to_k(ldo), lse, to_k(ll), delta, to_k(lde), (T*)dk, to_k(ldk), (T*)dv, to_k(ldv));
+    const BwdKvArgs<T> a{p,        ts,       geo,       (const T*)q, (const T*)k, (const T*)v, (const T*)dout,
+                         lse,      delta,    (T*)dk,    (T*)dv,      to_k(lq),    to_k(lk),    to_k(lv),
+                         to_k(ldo), to_k(ll), to_k(lde), to_k(ldk),  to_k(ldv)};
+    NA_LAUNCH("na_bwd_kv_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
     return hipGetLastError();
 }
 
@@ -1810,8 +2101,8 @@ hipError_t run_wsum_as(const char* name, const Prob& p, const void* w, Lay lw, c
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
     const int* geo = geometry_table(p, ts, false, s);
-    NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, p, ts, geo,
-              (const T*)w, to_k(lw), (const T*)x, to_k(lx), (T*)o, to_k(lo), mul);
+    const WsumArgs<T> a{p, ts, geo, (const T*)w, (const T*)x, (T*)o, to_k(lw), to_k(lx), to_k(lo), mul};
+    NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
     return hipGetLastError();
 }
 
@@ -1839,8 +2130,8 @@ hipError_t run_wsum_key_as(const char* name, const Prob& p, const void* w, Lay l
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
     const int* geo = geometry_table(p, ts, true, s);
-    NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, p, ts, geo,
-              (const T*)w, to_k(lw), (const T*)x, to_k(lx), (T*)o, to_k(lo), mul);
+    const WsumArgs<T> a{p, ts, geo, (const T*)w, (const T*)x, (T*)o, to_k(lw), to_k(lx), to_k(lo), mul};
+    NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
     return hipGetLastError();
 }
 
@@ -1851,25 +2142,110 @@ hipError_t run_wsum_key(const char* name, const Prob& p, const void* w, Lay lw, 
     return run_wsum_key_as<T, D, false>(name, p, w, lw, x, lx, o, lo, mul, s);
 }
 
-// Rows of KV entries: non-negative strides, every entry of one (batch, head)
-// at a 31-bit offset.
+// Rows of KV entries: non-negative strides, and every entry of one (batch,
+// head) at a byte offset inside the buffer range of a row resource
+// (kPlaneBytes): the row kernels form byte offsets as 2 * (element offset)
+// in 32-bit arithmetic, and an access past the range would read zeros or
+// drop the store without any error.
 bool rows_fit(const Prob& p, const Lay& l) {
     if (l.b < 0 || l.s0 < 0 || l.s1 < 0 || l.s2 < 0 || l.h < 0) return false;
     const long long vol = (static_cast<long long>(p.ax[0].len) - 1) * l.s0 +
                           (static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
                           (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + p.kv;
-    return vol < (1LL << 31);
+    return (vol + 8) * 2 < kPlaneBytes;
+}
+
+// The tile kernels walk every query position of an axis up to its length: a
+// split op whose attention tensor covers fewer query positions than the
+// value tensor has (allowed at stride 1) goes to the vector kernels, which
+// decode over the attention extent.
+bool full_query_extent(const Prob& p) {
+    for (int a = 0; a < 3; ++a)
+        if (p.ax[a].st != 1 || p.ax[a].out != p.ax[a].len) return false;
+    return true;
+}
+
+// Static-LDS audit: lds_base() places the staged operands at the constant
+// LDS address kLdsPad, which is sound only while no kernel instance declares
+// static __shared__ memory (that would sit at address 0 and overlap them).
+// Every instance is asked once per process; one with static LDS turns the
+// whole tile path off (the vector kernels take every call) with a message.
+struct LdsAudit {
+    int checked = 0, bad = 0;
+};
+
+template <typename K>
+void audit_one(K kernel, const char* what, LdsAudit& a) {
+    hipFuncAttributes attr{};
+    if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel)) != hipSuccess) {
+        (void)hipGetLastError();
+        ++a.bad;
+        std::fprintf(stderr, "natten_hip: cannot read the attributes of %s; MFMA tile kernels disabled\n", what);
+        return;
+    }
+    ++a.checked;
+    if (attr.sharedSizeBytes != 0) {
+        ++a.bad;
+        std::fprintf(stderr,
+                     "natten_hip: %s has %zu bytes of static LDS, which would overlap the operands staged at LDS "
+                     "address %d; MFMA tile kernels disabled\n",
+                     what, static_cast<size_t>(attr.sharedSizeBytes), kLdsPad);
+    }
+}
+
+template <typename T, int D, int LAY>
+void audit_fused(LdsAudit& a) {
+    audit_one(k_fwd_mfma<T, D, LAY, false>, "k_fwd_mfma", a);
+    audit_one(k_fwd_mfma<T, D, LAY, true>, "k_fwd_mfma (wide)", a);
+    audit_one(k_bwd_q_mfma<T, D, LAY, false>, "k_bwd_q_mfma", a);
+    audit_one(k_bwd_q_mfma<T, D, LAY, true>, "k_bwd_q_mfma (wide)", a);
+    audit_one(k_bwd_kv_mfma<T, D, LAY, false>, "k_bwd_kv_mfma", a);
+    audit_one(k_bwd_kv_mfma<T, D, LAY, true>, "k_bwd_kv_mfma (wide)", a);
+}
+
+template <typename T, int D>
+void audit_dim(LdsAudit& a) {
+    audit_fused<T, D, kLayGeneral>(a);
+    audit_fused<T, D, kLayOne>(a);
+    audit_fused<T, D, kLayTwo>(a);
+    audit_one(k_dot_mfma<T, D, true>, "k_dot_mfma", a);
+    audit_one(k_dot_mfma<T, D, false>, "k_dot_mfma", a);
+    audit_one(k_wsum_mfma<T, D, true>, "k_wsum_mfma", a);
+    audit_one(k_wsum_mfma<T, D, false>, "k_wsum_mfma", a);
+    audit_one(k_wsum_key_mfma<T, D, true>, "k_wsum_key_mfma", a);
+    audit_one(k_wsum_key_mfma<T, D, false>, "k_wsum_key_mfma", a);
+}
+
+const LdsAudit& lds_audit() {
+    static const LdsAudit result = [] {
+        LdsAudit a;
+        audit_dim<bf16, 32>(a);
+        audit_dim<bf16, 64>(a);
+        audit_dim<bf16, 128>(a);
+        audit_dim<f16, 32>(a);
+        audit_dim<f16, 64>(a);
+        audit_dim<f16, 128>(a);
+        return a;
+    }();
+    return result;
 }
 
 }  // namespace
 
+bool mfma_static_lds_ok() { return lds_audit().bad == 0; }
+
+int mfma_lds_audit(int* checked) {
+    const LdsAudit& a = lds_audit();
+    if (checked) *checked = a.checked;
+    return a.bad == 0 ? 1 : 0;
+}
+
 bool mfma_split_eligible(const Prob& p, int dtype, int D, bool aligned, const Lay& rows,
                          std::initializer_list<Lay> staged) {
-    if (dtype == NATTEN_F32 || !aligned || p.rep != 1) return false;
+    if (dtype == NATTEN_F32 || !aligned || p.rep != 1 || !mfma_static_lds_ok()) return false;
     if (!(D == 32 || D == 64 || D == 128) || p.kv > kSplitMaxKV) return false;
     if (static_cast<size_t>(4) * row_block_entries(p) * 2 > kSplitRowsBudget) return false;
-    for (int a = 0; a < 3; ++a)
-        if (p.ax[a].st != 1) return false;
+    if (!full_query_extent(p)) return false;
     TileShape ts{};
     if (!choose_tile(p, kSplit, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
     return rows_fit(p, rows) && offsets_fit(p, staged);
@@ -1877,10 +2253,9 @@ bool mfma_split_eligible(const Prob& p, int dtype, int D, bool aligned, const La
 
 bool mfma_split_key_eligible(const Prob& p, int dtype, int D, bool aligned, const Lay& rows,
                              std::initializer_list<Lay> staged) {
-    if (dtype == NATTEN_F32 || !aligned || p.rep != 1) return false;
+    if (dtype == NATTEN_F32 || !aligned || p.rep != 1 || !mfma_static_lds_ok()) return false;
     if (!(D == 32 || D == 64 || D == 128) || p.kv > kSplitMaxKV) return false;
-    for (int a = 0; a < 3; ++a)
-        if (p.ax[a].st != 1) return false;
+    if (!full_query_extent(p)) return false;
     TileShape ts{};
     if (!choose_tile(p, kSplitKey, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
     if (split_key_lds_bytes(p, ts, D) > kSplitKeyLds)
@@ -1931,7 +2306,7 @@ hipError_t mfma_split_wsum(const char* name, const Prob& p, int D, const void* w
 }
 
 bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward) {
-    if (dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f)) return false;
+    if (dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f) || !mfma_static_lds_ok()) return false;
     if (p.Dqk != p.Dv || !(D == 32 || D == 64 || D == 128)) return false;
     for (int a = 0; a < 3; ++a)
         if (p.ax[a].st != 1) return false;

@@ -24,6 +24,7 @@ _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 ENTRY_POINTS = (
     "natten_hip_abi_version",
     "natten_hip_last_error",
+    "natten_hip_mfma_lds_check",
     "natten_hip_forward",
     "natten_hip_backward",
     "natten_hip_qk_forward",
@@ -77,6 +78,7 @@ _LP = _P(Layout)
 _SIGNATURES = {
     "natten_hip_abi_version": ([], ctypes.c_int),
     "natten_hip_last_error": ([], ctypes.c_char_p),
+    "natten_hip_mfma_lds_check": ([_P(ctypes.c_int32)], ctypes.c_int),
     "natten_hip_forward": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP], ctypes.c_int),
     "natten_hip_backward": ([_P(Problem)] + [_VP, _LP] * 11 + [_VP], ctypes.c_int),
     "natten_hip_qk_forward": ([_P(Problem)] + [_VP, _LP] * 3 + [_VP], ctypes.c_int),

@@ -5,12 +5,15 @@ dilation and bias.
 
 Tolerances: fp32 1e-5 (logits, outputs, dq, dk, dattn, dv), 1e-4 for the
 bias gradient (a sum over every query of the batch); bf16 logits/outputs
-2e-2 against the oracle in fp32 on the same rounded inputs.
+the half-precision bound of tests/_parity.py against the oracle in fp32 on
+the same rounded inputs.
 """
 from __future__ import annotations
 
 import pytest
 import torch
+
+from _parity import assert_parity
 
 import oracle.allin1 as A
 
@@ -122,11 +125,10 @@ def test_rpb_half_precision(dtype):
     rpb = _rand((2, 9, 9), 18, dtype)
     logits = na2d_qk_rpb(q.to(DEV), k.to(DEV), rpb.to(DEV), 5, 2, scale=32 ** -0.5)
     ref = A.na2d_qk_rpb(q.float(), k.float(), rpb.float(), 5, 2, scale=32 ** -0.5)
-    torch.testing.assert_close(logits.cpu().float(), ref, atol=2e-2, rtol=2e-2)
+    assert_parity(logits.cpu(), ref, dtype, "rpb logits")
     attn = ref.softmax(-1)
     out = na2d_av_fused(attn.to(dtype).to(DEV), v.to(DEV), 5, 2)
-    torch.testing.assert_close(out.cpu().float(), A.av_2d(attn.to(dtype).float(), v.float(), 5, 2), atol=2e-2,
-                               rtol=2e-2)
+    assert_parity(out.cpu(), A.av_2d(attn.to(dtype).float(), v.float(), 5, 2), dtype, "rpb av")
 
 
 def test_rpb_validation():

@@ -11,7 +11,9 @@ affordable on the host:
   every contributing query lies in the prefix);
 * cfg 5: batch item 0, head 0 (heads are independent, Hq == Hkv).
 
-bf16 tolerance 2e-2 (the oracle runs in fp32 on the same bf16 inputs); fp32 1e-5.
+Bounds: ``tests/_parity.py`` (bf16 within 2e-2 norm-wise relative with an
+elementwise guard, the oracle run in fp32 on the same bf16 inputs; fp32
+within 1e-5 elementwise).
 """
 from __future__ import annotations
 
@@ -19,6 +21,7 @@ import pytest
 import torch
 
 import oracle.pure as P
+from _parity import assert_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -53,7 +56,13 @@ def _oracle(rank, q, k, v, do, ks, st, dil, causal):
 
 
 def _close(a, b, tol, name):
-    torch.testing.assert_close(a.float(), b.float(), atol=tol, rtol=tol, msg=lambda m: f"{name}: {m}")
+    """tol 1e-5: the fp32 bound; 2e-2: the half-precision bound (both from
+    tests/_parity.py); other values: an elementwise bound between two HIP
+    paths (fused against the split composition)."""
+    if tol in (1e-5, 2e-2):
+        assert_parity(a, b, torch.float32 if tol == 1e-5 else torch.bfloat16, name)
+    else:
+        torch.testing.assert_close(a.float(), b.float(), atol=tol, rtol=tol, msg=lambda m: f"{name}: {m}")
 
 
 def test_config1_na1d_fp32(golden):

@@ -1,0 +1,293 @@
+"""Edge cases of the 'hip' backend on the GPU: non-finite inputs outside a
+window, operand extents the tile kernels must refuse, head dims of V that
+differ from Q/K, the LDS audit of the tile kernels, and bitwise determinism
+of the gathers.  Values are checked against the CPU oracle under the bounds
+of tests/_parity.py.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+import oracle.pure as P
+from _parity import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0") if torch.cuda.is_available() else None
+
+
+@pytest.fixture(autouse=True)
+def _hip():
+    import natten_mps_amd
+
+    natten_mps_amd.set_backend("hip")
+
+
+def _inputs(seed, shapes, dtype):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(s, generator=g, dtype=torch.float32).to(dtype) for s in shapes]
+
+
+def _launched(run):
+    """Run `run()` with the library's per-launch timing on; return the names
+    of the kernels it launched."""
+    from natten_mps_amd._core import _lib
+
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        res = run()
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    return res, set(_lib.profile_read(reset=True))
+
+
+# ---------------------------------------------------------------------------
+# the tile kernels' constant LDS base
+# ---------------------------------------------------------------------------
+
+
+def test_mfma_kernels_have_no_static_lds():
+    """Every tile-kernel instance (2 dtypes x 3 head dims x 18 fused and 6
+    split instances) reports 0 bytes of static LDS, so the operands the
+    kernels stage at a constant LDS offset cannot overlap a __shared__
+    array; with one that did, the library would refuse the tile path."""
+    from natten_mps_amd._core import _lib
+
+    n = ctypes.c_int32(0)
+    assert _lib.load().natten_hip_mfma_lds_check(ctypes.byref(n)) == 1
+    assert n.value == 2 * 3 * (18 + 6)
+
+
+# ---------------------------------------------------------------------------
+# extents the tile kernels must not take
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_split_av_with_attn_shorter_than_value(dtype):
+    """na2d_av at stride 1 with attn covering fewer query positions than
+    value has (attn[:, :10, :12] of a 14 x 15 problem; allowed by the
+    reference, _core/pure.py:278-281): forward and backward match the oracle
+    and run on the vector kernels, which decode over the attn extent."""
+    from natten_mps_amd import functional as F
+
+    (v,) = _inputs(301, [(2, 14, 15, 2, 32)], dtype)
+    (logits,) = _inputs(302, [(2, 10, 12, 2, 49)], torch.float32)
+    attn = torch.softmax(logits, -1).to(dtype)
+    (do,) = _inputs(303, [(2, 10, 12, 2, 32)], dtype)
+
+    ad, vd = attn.to(DEV).requires_grad_(True), v.to(DEV).requires_grad_(True)
+
+    def run():
+        out = F.na2d_av(ad, vd, 7, 1)
+        out.backward(do.to(DEV))
+        return out
+
+    out, ran = _launched(run)
+    assert {"na_av", "na_av_bwd_a", "na_av_bwd_v"} <= ran and not any(n.endswith("_mfma") for n in ran), ran
+    ra, rv = attn.float().requires_grad_(True), v.float().requires_grad_(True)
+    ref = P.na2d_av_forward(ra, rv, (7, 7), (1, 1), (1, 1), (False, False))
+    ref.backward(do.float())
+    assert_parity(out, ref, dtype, "out")
+    assert_parity(ad.grad, ra.grad, dtype, "dattn")
+    assert_parity(vd.grad, rv.grad, dtype, "dv")
+
+
+def test_split_rows_past_the_31bit_byte_range_use_vector_kernels():
+    """Logits of one (batch, head) of a 1024 x 1024, 8-head, 13 x 13 problem
+    span 1.4e9 entries: their byte offsets exceed the 31-bit range of the
+    tile kernels' row buffers, so na2d_qk runs on the vector kernel.  Values
+    at an interior and a corner query against the window rule computed
+    directly."""
+    from natten_mps_amd import functional as F
+
+    g = torch.Generator(device=DEV).manual_seed(304)
+    q = torch.randn((1, 1024, 1024, 8, 32), generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn((1, 1024, 1024, 8, 32), generator=g, device=DEV).to(torch.bfloat16)
+    logits, ran = _launched(lambda: F.na2d_qk(q, k, 13, 1))
+    assert "na_qk" in ran and "na_qk_mfma" not in ran, ran
+    for (y, x, h) in ((600, 700, 5), (0, 0, 2), (1023, 1017, 7)):
+        y0 = min(max(y - 6, 0), 1024 - 13)
+        x0 = min(max(x - 6, 0), 1024 - 13)
+        win = k[0, y0:y0 + 13, x0:x0 + 13, h].float().reshape(169, 32)
+        ref = win @ q[0, y, x, h].float()
+        assert_parity(logits[0, y, x, h], ref, torch.bfloat16, f"logits at {(y, x, h)}")
+    del logits, q, k
+    torch.cuda.empty_cache()
+
+
+# ---------------------------------------------------------------------------
+# non-finite values outside a window stay outside it
+# ---------------------------------------------------------------------------
+
+NONFINITE_FUSED = [
+    # rank, spatial, hq, hkv, dim, kernel, dilation, bad position, dtype
+    (2, (20, 22), 2, 2, 32, (7, 7), (1, 1), (9, 10), torch.bfloat16),
+    (2, (24, 24), 4, 2, 64, (5, 5), (2, 2), (11, 12), torch.float16),
+    (3, (6, 12, 12), 2, 2, 32, (3, 5, 5), (1, 1, 2), (3, 6, 5), torch.bfloat16),
+    (1, (200,), 4, 1, 64, (9,), (2,), (100,), torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("value", [float("inf"), float("nan")], ids=["inf", "nan"])
+@pytest.mark.parametrize("which", ["q", "k", "v"])
+@pytest.mark.parametrize("case", NONFINITE_FUSED, ids=lambda c: f"{c[0]}d-{c[4]}-{str(c[8])[6:]}")
+def test_fused_nonfinite_stays_local(case, which, value):
+    """One position of q, k or v (batch 0, every head) set to Inf or NaN.
+    The tile kernels stage that row for neighbouring queries whose windows
+    exclude it; their outputs and gradients must stay finite and equal the
+    oracle's, and exactly the elements the oracle makes non-finite are
+    non-finite."""
+    from natten_mps_amd import functional as F
+
+    rank, sp, hq, hkv, dim, ks, dil, bad, dtype = case
+    q, k, v, do = _inputs(311, [(2, *sp, hq, dim), (2, *sp, hkv, dim), (2, *sp, hkv, dim), (2, *sp, hq, dim)],
+                          dtype)
+    t = {"q": q, "k": k, "v": v}[which]
+    t[(0, *bad)] = value
+    leaves = [x.to(DEV).requires_grad_(True) for x in (q, k, v)]
+    out = getattr(F, f"na{rank}d")(*leaves, kernel_size=ks, dilation=dil)
+    out.backward(do.to(DEV))
+    rl = [x.float().requires_grad_(True) for x in (q, k, v)]
+    ref = P.forward(rank, *rl, ks, (1,) * rank, dil, (False,) * rank, None)
+    ref.backward(do.float())
+    finite = torch.isfinite(ref)
+    assert finite.any() and not finite.all()  # the case reaches some queries and not others
+    assert_parity(out, ref, dtype, "out")
+    for name, a, b in zip(("dq", "dk", "dv"), leaves, rl):
+        assert_parity(a.grad, b.grad, dtype, name)
+
+
+@pytest.mark.parametrize("which", ["q", "k"])
+def test_split_qk_nonfinite_stays_local(which):
+    """Split QK forward and backward (tile kernels) with an Inf row in q or
+    k: logits, dq and dk against the oracle, finiteness included."""
+    from natten_mps_amd import functional as F
+
+    q, k = _inputs(321, [(2, 18, 20, 2, 32)] * 2, torch.bfloat16)
+    {"q": q, "k": k}[which][0, 9, 9] = float("inf")
+    qd, kd = q.to(DEV).requires_grad_(True), k.to(DEV).requires_grad_(True)
+    logits, ran = _launched(lambda: F.na2d_qk(qd, kd, 5, (1, 2), scale=0.25))
+    rq, rk = q.float().requires_grad_(True), k.float().requires_grad_(True)
+    ref = P.na2d_qk_forward(rq, rk, (5, 5), (1, 2), (1, 1), (False, False), 0.25)
+    assert_parity(logits, ref, torch.bfloat16, "logits")
+    (dl,) = _inputs(322, [tuple(ref.shape)], torch.bfloat16)
+    _, ran_b = _launched(lambda: logits.backward(dl.to(DEV)))
+    assert {"na_qk_mfma", "na_qk_bwd_q_mfma", "na_qk_bwd_k_mfma"} <= ran | ran_b
+    ref.backward(dl.float())
+    assert not torch.isfinite(rq.grad).all() or not torch.isfinite(rk.grad).all()
+    assert_parity(qd.grad, rq.grad, torch.bfloat16, "dq")
+    assert_parity(kd.grad, rk.grad, torch.bfloat16, "dk")
+
+
+def test_split_av_nonfinite_stays_local():
+    """Split AV forward and backward (tile kernels) with a NaN row in v."""
+    from natten_mps_amd import functional as F
+
+    (v,) = _inputs(331, [(2, 18, 20, 2, 32)], torch.bfloat16)
+    v[1, 4, 15] = float("nan")
+    (lg,) = _inputs(332, [(2, 18, 20, 2, 25)], torch.float32)
+    attn = torch.softmax(lg, -1).to(torch.bfloat16)
+    ad, vd = attn.to(DEV).requires_grad_(True), v.to(DEV).requires_grad_(True)
+    (do,) = _inputs(333, [(2, 18, 20, 2, 32)], torch.bfloat16)
+
+    def run():
+        out = F.na2d_av(ad, vd, 5, (2, 1))
+        out.backward(do.to(DEV))
+        return out
+
+    out, ran = _launched(run)
+    assert {"na_av_mfma", "na_av_bwd_a_mfma", "na_av_bwd_v_mfma"} <= ran, ran
+    ra, rv = attn.float().requires_grad_(True), v.float().requires_grad_(True)
+    ref = P.na2d_av_forward(ra, rv, (5, 5), (2, 1), (1, 1), (False, False))
+    ref.backward(do.float())
+    assert torch.isfinite(ref).any() and not torch.isfinite(ref).all()
+    assert_parity(out, ref, torch.bfloat16, "out")
+    assert_parity(ad.grad, ra.grad, torch.bfloat16, "dattn")
+    assert_parity(vd.grad, rv.grad, torch.bfloat16, "dv")
+
+
+# ---------------------------------------------------------------------------
+# V with its own head dim (functional.py:56-63 of the reference: NAF-style
+# cross attention, D = 64 for q/k and 256 for v)
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rank", [1, 2])
+def test_dim_v_differs_forward_and_gradients(rank, dtype):
+    from natten_mps_amd import functional as F
+
+    sp, ks, dil = ((40,), 7, 2) if rank == 1 else ((12, 14), (5, 3), (1, 2))
+    q, k, v, do = _inputs(341, [(2, *sp, 2, 64), (2, *sp, 2, 64), (2, *sp, 2, 256), (2, *sp, 2, 256)], dtype)
+    leaves = [x.to(DEV).requires_grad_(True) for x in (q, k, v)]
+    out = getattr(F, f"na{rank}d")(*leaves, kernel_size=ks, dilation=dil)
+    out.backward(do.to(DEV))
+    assert out.shape == (2, *sp, 2, 256)
+    kst = (ks,) * rank if isinstance(ks, int) else ks
+    dlt = (dil,) * rank if isinstance(dil, int) else dil
+    # the reference reaches V with its own head dim through its split
+    # composition (its pure fused op requires identical shapes)
+    rl = [x.float().requires_grad_(True) for x in (q, k, v)]
+    nc = (False,) * rank
+    logits = getattr(P, f"na{rank}d_qk_forward")(rl[0], rl[1], kst, dlt, (1,) * rank, nc, None) * 64 ** -0.5
+    ref = getattr(P, f"na{rank}d_av_forward")(torch.softmax(logits, -1), rl[2], kst, dlt, (1,) * rank, nc)
+    ref.backward(do.float())
+    assert_parity(out, ref, dtype, "out")
+    for name, a, b in zip(("dq", "dk", "dv"), leaves, rl):
+        assert_parity(a.grad, b.grad, dtype, name)
+
+
+# ---------------------------------------------------------------------------
+# bitwise determinism of the gathers (no atomics anywhere)
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dil", [1, 8])
+def test_config3_backward_is_bitwise_deterministic(dil):
+    """Config 3 (B=16, 56 x 56, 4 heads, D=32, K=7, bf16) forward and
+    backward repeated: whole tensors equal bit for bit."""
+    from natten_mps_amd import functional as F
+
+    g = torch.Generator().manual_seed(1003)
+    q, k, v, do = (torch.randn((16, 56, 56, 4, 32), generator=g).to(torch.bfloat16).to(DEV) for _ in range(4))
+    leaves = [t.requires_grad_(True) for t in (q, k, v)]
+
+    def step():
+        out = F.na2d(*leaves, kernel_size=7, dilation=dil)
+        return [out.detach()] + list(torch.autograd.grad(out, leaves, do))
+
+    ref = step()
+    for _ in range(4):
+        for name, a, b in zip(("out", "dq", "dk", "dv"), step(), ref):
+            assert torch.equal(a, b), f"{name}: {int((a != b).sum())} elements differ between runs"
+
+
+def test_split_key_side_multi_slice_is_bitwise_deterministic():
+    """The split ops' key-side tile kernel (dk of QK, dv of AV) on a 3-D
+    problem whose key tiles walk several staged axis-0 slices: repeated
+    backward passes agree bit for bit."""
+    from natten_mps_amd import functional as F
+
+    q, k, v = (t.to(DEV) for t in _inputs(351, [(2, 8, 16, 16, 4, 32)] * 3, torch.bfloat16))
+    (dl,) = _inputs(352, [(2, 8, 16, 16, 4, 75)], torch.bfloat16)
+    (do,) = _inputs(353, [(2, 8, 16, 16, 4, 32)], torch.bfloat16)
+    dl, do = dl.to(DEV), do.to(DEV)
+    leaves = [t.requires_grad_(True) for t in (q, k, v)]
+
+    def step():
+        logits = F.na3d_qk(leaves[0], leaves[1], (3, 5, 5), (2, 1, 2))
+        attn = torch.softmax(logits.detach().float(), -1).to(torch.bfloat16)
+        out = F.na3d_av(attn, leaves[2], (3, 5, 5), (2, 1, 2))
+        return list(torch.autograd.grad(logits, leaves[:2], dl)) + list(torch.autograd.grad(out, [leaves[2]], do))
+
+    (ref, ran) = _launched(step)
+    assert {"na_qk_bwd_k_mfma", "na_av_bwd_v_mfma"} <= ran, ran
+    for _ in range(4):
+        for name, a, b in zip(("dq", "dk", "dv"), step(), ref):
+            assert torch.equal(a, b), f"{name}: {int((a != b).sum())} elements differ between runs"

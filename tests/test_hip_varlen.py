@@ -6,13 +6,15 @@ asymmetric sizes, dilation, custom scale, padding zero in outputs and
 gradients, gradients per sample.
 
 Tolerances: fp32 outputs 1e-5, fp32 gradients 1e-4 (the reference's varlen
-gradient tests); bf16 2e-2 against the oracle evaluated in fp32 on the same
-rounded inputs.
+gradient tests); bf16 under the half-precision bound of tests/_parity.py,
+against the oracle evaluated in fp32 on the same rounded inputs.
 """
 from __future__ import annotations
 
 import pytest
 import torch
+
+from _parity import assert_parity
 
 import oracle.pure as P
 
@@ -62,8 +64,7 @@ def test_varlen_forward_matches_oracle(case, dtype):
     arg = sz[:, 0] if rank == 1 else sz
     out = _fn(rank)(q.to(DEV), k.to(DEV), v.to(DEV), arg.to(DEV), kernel_size=ks, dilation=dil, scale=scale).cpu()
     ref = ORACLE[rank](q.float(), k.float(), v.float(), sz, ks, dil, scale)
-    tol = dict(atol=1e-5, rtol=1e-5) if dtype == torch.float32 else dict(atol=2e-2, rtol=2e-2)
-    torch.testing.assert_close(out.float(), ref, **tol)
+    assert_parity(out, ref, dtype, "varlen out")
     for b, ext in enumerate(sizes):  # padding exactly zero
         mask = torch.ones(shape[1:1 + rank], dtype=torch.bool)
         mask[tuple(slice(0, n) for n in ext)] = False
