@@ -132,6 +132,30 @@ int natten_hip_backward(const natten_problem_t *p,
                         float *delta, const natten_layout_t *ldelta,
                         void *stream);
 
+/* Allocation-free fused backward (no counterpart in the reference): the same
+ * computation and results as natten_hip_backward, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It takes no delta workspace: the delta
+ * rows live in a static device array of the library, at most 4 Mi floats
+ * (batch x query positions x heads_q <= 4,194,304; larger problems return
+ * NATTEN_ERR_UNSUPPORTED), one copy per GPU, held until the process ends.
+ * It calls no hipMalloc/hipFree: the tile kernels then compute their geometry
+ * themselves unless a table for the shape already exists.  Calls that overlap
+ * on one GPU share that array and race; serialise them (one stream, or
+ * events). */
+int natten_hip_backward_noalloc(const natten_problem_t *p,
+                                const void *q, const natten_layout_t *lq,
+                                const void *k, const natten_layout_t *lk,
+                                const void *v, const natten_layout_t *lv,
+                                const void *out, const natten_layout_t *lo,
+                                const void *dout, const natten_layout_t *ldo,
+                                const float *lse, const natten_layout_t *llse,
+                                const float *dlse, const natten_layout_t *ldlse,
+                                void *dq, const natten_layout_t *ldq,
+                                void *dk, const natten_layout_t *ldk,
+                                void *dv, const natten_layout_t *ldv,
+                                void *stream);
+
 /* Split QK: attn[.., kv] = q . k_neighbour (times scale if has_scale); entries
  * of causally invalid neighbours are -inf (times scale).  heads_q == heads_kv. */
 int natten_hip_qk_forward(const natten_problem_t *p,

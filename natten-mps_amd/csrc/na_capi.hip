@@ -1,9 +1,12 @@
 // C ABI of libnatten_hip.so (declared in include/natten_hip.h): argument
-// validation, problem set-up and kernel selection.  No entry point allocates.
+// validation, problem set-up and kernel selection.  The caller passes every
+// buffer; the only device memory the library allocates is the tile-geometry
+// tables of na_mfma.hip, and natten_hip_backward_noalloc allocates none.
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "na_launch.h"
 
@@ -168,15 +171,15 @@ int natten_hip_forward(const natten_problem_t* p, const void* q, const natten_la
                          "forward");
 }
 
-int natten_hip_backward(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
-                        const natten_layout_t* lk, const void* v, const natten_layout_t* lv, const void* out,
-                        const natten_layout_t* lo, const void* dout, const natten_layout_t* ldo, const float* lse,
-                        const natten_layout_t* llse, const float* dlse, const natten_layout_t* ldlse, void* dq,
-                        const natten_layout_t* ldq, void* dk, const natten_layout_t* ldk, void* dv,
-                        const natten_layout_t* ldv, float* delta, const natten_layout_t* ldelta, void* stream) {
-    na::Prob P;
-    int rc = make_prob(p, true, P);
-    if (rc) return rc;
+namespace {
+
+// Shared body of the two backward entry points (the problem already checked).
+int backward_impl(const natten_problem_t* p, const na::Prob& P, const void* q, const natten_layout_t* lq,
+                  const void* k, const natten_layout_t* lk, const void* v, const natten_layout_t* lv,
+                  const void* out, const natten_layout_t* lo, const void* dout, const natten_layout_t* ldo,
+                  const float* lse, const natten_layout_t* llse, const float* dlse, const natten_layout_t* ldlse,
+                  void* dq, const natten_layout_t* ldq, void* dk, const natten_layout_t* ldk, void* dv,
+                  const natten_layout_t* ldv, float* delta, const natten_layout_t* ldelta, void* stream) {
     if (any_null({q, k, v, out, dout, lse, dq, dk, dv, delta, lq, lk, lv, lo, ldo, llse, ldq, ldk, ldv, ldelta}))
         return fail(NATTEN_ERR_INVALID, "NULL operand");
     if (dlse && !ldlse) return fail(NATTEN_ERR_INVALID, "dlse given without a layout");
@@ -200,6 +203,84 @@ int natten_hip_backward(const natten_problem_t* p, const void* q, const natten_l
                              lse, to_lay(llse), dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv,
                              to_lay(ldv), delta, to_lay(ldelta), p->dtype, static_cast<hipStream_t>(stream)),
         "backward");
+}
+
+// Device scratch of natten_hip_backward_noalloc: its fp32 delta rows
+// (batch x query positions x query heads), at most kScratchFloats of them.
+// Each GPU the library runs on holds its own copy until the process ends.
+// The kernels write every delta entry before any is read, so nothing needs
+// clearing between calls; two calls that overlap on one GPU race on it.
+constexpr size_t kScratchFloats = size_t(4) << 20;  // 16 MiB
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per
+// device.  In host code the name `scratch` is a host-side stand-in; only the
+// looked-up address may reach a kernel.
+int scratch_ptr(float** out) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(NATTEN_ERR_LAUNCH, "backward_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(NATTEN_ERR_UNSUPPORTED, "backward_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* ptr = nullptr;
+        const hipError_t es = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (es != hipSuccess || !ptr)
+            return fail(NATTEN_ERR_LAUNCH, "backward_noalloc: hipGetSymbolAddress(scratch): %s",
+                        hipGetErrorString(es));
+        g_scratch[dev] = static_cast<float*>(ptr);
+    }
+    *out = g_scratch[dev];
+    return NATTEN_OK;
+}
+
+}  // namespace
+
+int natten_hip_backward(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
+                        const natten_layout_t* lk, const void* v, const natten_layout_t* lv, const void* out,
+                        const natten_layout_t* lo, const void* dout, const natten_layout_t* ldo, const float* lse,
+                        const natten_layout_t* llse, const float* dlse, const natten_layout_t* ldlse, void* dq,
+                        const natten_layout_t* ldq, void* dk, const natten_layout_t* ldk, void* dv,
+                        const natten_layout_t* ldv, float* delta, const natten_layout_t* ldelta, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, true, P);
+    if (rc) return rc;
+    return backward_impl(p, P, q, lq, k, lk, v, lv, out, lo, dout, ldo, lse, llse, dlse, ldlse, dq, ldq, dk, ldk, dv,
+                         ldv, delta, ldelta, stream);
+}
+
+int natten_hip_backward_noalloc(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
+                                const natten_layout_t* lk, const void* v, const natten_layout_t* lv, const void* out,
+                                const natten_layout_t* lo, const void* dout, const natten_layout_t* ldo,
+                                const float* lse, const natten_layout_t* llse, const float* dlse,
+                                const natten_layout_t* ldlse, void* dq, const natten_layout_t* ldq, void* dk,
+                                const natten_layout_t* ldk, void* dv, const natten_layout_t* ldv, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, true, P);
+    if (rc) return rc;
+    const long long rows = static_cast<long long>(P.B) * P.nout * P.Hq;
+    if (rows > static_cast<long long>(kScratchFloats))
+        return fail(NATTEN_ERR_UNSUPPORTED,
+                    "backward_noalloc: %lld delta rows (batch x query positions x heads) exceed the scratch "
+                    "maximum of %zu; use natten_hip_backward with a caller workspace",
+                    rows, kScratchFloats);
+    float* delta = nullptr;
+    rc = scratch_ptr(&delta);
+    if (rc) return rc;
+    // delta rows contiguous: [B, out0, out1, out2, Hq]
+    natten_layout_t ld{};
+    ld.head = 1;
+    ld.axis[2] = P.Hq;
+    ld.axis[1] = ld.axis[2] * P.ax[2].out;
+    ld.axis[0] = ld.axis[1] * P.ax[1].out;
+    ld.batch = ld.axis[0] * P.ax[0].out;
+    const na::NoDeviceAlloc no_alloc;
+    return backward_impl(p, P, q, lq, k, lk, v, lv, out, lo, dout, ldo, lse, llse, dlse, ldlse, dq, ldq, dk, ldk, dv,
+                         ldv, delta, &ld, stream);
 }
 
 int natten_hip_qk_forward(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,

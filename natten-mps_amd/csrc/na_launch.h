@@ -56,6 +56,22 @@ hipError_t rpb_av_backward(const Prob& p, const void* dout, Lay ldo, const void*
 
 namespace na {
 
+// While a NoDeviceAlloc object lives on a thread, launches from that thread
+// allocate no device memory: the tile kernels read a geometry table only if
+// one was already built for the shape and otherwise compute the geometry
+// themselves (the same values).
+class NoDeviceAlloc {
+public:
+    NoDeviceAlloc();
+    ~NoDeviceAlloc();
+    NoDeviceAlloc(const NoDeviceAlloc&) = delete;
+    NoDeviceAlloc& operator=(const NoDeviceAlloc&) = delete;
+
+private:
+    bool prev_;
+};
+bool device_alloc_allowed();
+
 // MFMA tile path (na_mfma.hip): bf16/fp16, stride 1, equal head dims 32/64/128.
 // mfma_static_lds_ok: no tile kernel instance declares static LDS (checked
 // once per process); mfma_lds_audit returns 1 when so, 0 otherwise, and the

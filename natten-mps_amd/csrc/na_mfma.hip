@@ -1068,8 +1068,8 @@ void fit_h_per(const Prob& p, TileShape& ts, long long resident) {
 // Per-tile geometry records, built on the host once per (device, tile kind,
 // problem geometry) and kept for the life of the process; launches read
 // their tile's record instead of recomputing it.  Not built while the stream
-// is being captured (the kernels then compute the geometry themselves), nor
-// past kGeoMaxBytes in total.  NATTEN_HIP_GEOMETRY=device disables the
+// is being captured or inside a NoDeviceAlloc scope (the kernels then compute
+// the geometry themselves), nor past kGeoMaxBytes in total.  NATTEN_HIP_GEOMETRY=device disables the
 // tables (A/B and tests).
 constexpr size_t kGeoMaxBytes = size_t(64) << 20;
 
@@ -1078,6 +1078,8 @@ struct GeoEntry {
     int len[3], k[3], dil[3], causal[3], T[3], waves, rowshift;
     int* ptr;
 };
+
+thread_local bool t_no_device_alloc = false;
 
 const int* geometry_table(const Prob& p, const TileShape& ts, bool key_tile, hipStream_t stream) {
     const char* env = std::getenv("NATTEN_HIP_GEOMETRY");
@@ -1102,6 +1104,7 @@ const int* geometry_table(const Prob& p, const TileShape& ts, bool key_tile, hip
     std::lock_guard<std::mutex> g(mu);
     for (const GeoEntry& e : cache)
         if (std::memcmp(&e, &key, offsetof(GeoEntry, ptr)) == 0) return e.ptr;
+    if (!device_alloc_allowed()) return nullptr;
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
     const long long S = ts.spatial.d;
@@ -1416,6 +1419,10 @@ const LdsAudit& lds_audit() {
 }
 
 }  // namespace
+
+NoDeviceAlloc::NoDeviceAlloc() : prev_(t_no_device_alloc) { t_no_device_alloc = true; }
+NoDeviceAlloc::~NoDeviceAlloc() { t_no_device_alloc = prev_; }
+bool device_alloc_allowed() { return !t_no_device_alloc; }
 
 bool mfma_static_lds_ok() { return lds_audit().bad == 0; }
 

@@ -27,6 +27,7 @@ ENTRY_POINTS = (
     "natten_hip_mfma_lds_check",
     "natten_hip_forward",
     "natten_hip_backward",
+    "natten_hip_backward_noalloc",
     "natten_hip_qk_forward",
     "natten_hip_av_forward",
     "natten_hip_qk_backward",
@@ -81,6 +82,7 @@ _SIGNATURES = {
     "natten_hip_mfma_lds_check": ([_P(ctypes.c_int32)], ctypes.c_int),
     "natten_hip_forward": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP], ctypes.c_int),
     "natten_hip_backward": ([_P(Problem)] + [_VP, _LP] * 11 + [_VP], ctypes.c_int),
+    "natten_hip_backward_noalloc": ([_P(Problem)] + [_VP, _LP] * 10 + [_VP], ctypes.c_int),
     "natten_hip_qk_forward": ([_P(Problem)] + [_VP, _LP] * 3 + [_VP], ctypes.c_int),
     "natten_hip_av_forward": ([_P(Problem)] + [_VP, _LP] * 3 + [_VP], ctypes.c_int),
     "natten_hip_qk_backward": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP], ctypes.c_int),
