@@ -13,7 +13,9 @@ A step is one pass through the public API (``natten_mps_amd.na{1,2,3}d``, then
 inputs already resident in HBM.  The step is timed eagerly and, captured once
 in a HIP graph (torch.cuda.CUDAGraph), as graph replays whose outputs are
 checked equal to eager steps; the step time reported is the replay's (the
-eager one is in ``config.eager_ms_per_step``).  Prints one JSON line:
+eager one is in ``config.eager_ms_per_step``, and with torch's autograd
+engine kept on the calling thread in
+``config.eager_ms_per_step_autograd_one_thread``).  Prints one JSON line:
 
 * value / unit: effective TFLOP/s = (fwd 4*P*D + bwd 10*P*D) / step time,
   with P = B * Hq * (valid query-key pairs of the neighbourhood map);
@@ -332,10 +334,23 @@ def main():
     # host is slower than the GPU on an eager step, so the bracketed pass
     # starts behind a spin long enough for the host to queue all K steps.
     ms_eager = timed(step)
+    # The same eager step with torch's autograd engine running backward on
+    # the calling thread: the difference is the engine's hand-off to its
+    # per-device worker thread and back (thread wake-ups on the host), not
+    # work of this library.
+    ms_eager_one_thread = None
+    if cfg["backward"]:
+        torch.autograd.set_multithreading_enabled(False)
+        try:
+            ms_eager_one_thread = timed(step)
+        finally:
+            torch.autograd.set_multithreading_enabled(True)
     cycles_per_ms = spin_cycles_per_ms()
     ms_profiled = timed(step, profile=True, head_start_ms=2.0 * args.steps * ms_eager + 5.0)
     stats = _lib.profile_read(reset=True)
     _log(f"eager step {ms_eager:.4f} ms (queued ahead, with per-launch events: {ms_profiled:.4f} ms)")
+    if ms_eager_one_thread is not None:
+        _log(f"eager step with autograd on the calling thread {ms_eager_one_thread:.4f} ms")
 
     # the same step captured once in a HIP graph (forward + autograd backward)
     # and replayed: identical kernels and buffers without the per-step host
@@ -436,6 +451,8 @@ def main():
         "config": {"workload": desc, "global_batch": B, "seq_len": N, "parallelism": "single GPU",
                    "timing": "HIP graph replay of the eager step (checked equal)" if ms_graph is not None
                    else "eager", "eager_ms_per_step": round(ms_eager, 4),
+                   "eager_ms_per_step_autograd_one_thread": None if ms_eager_one_thread is None
+                   else round(ms_eager_one_thread, 4),
                    "step_hbm_bytes": sbytes, "step_gbs": round(sbytes / (ms * 1e-3) / 1e9, 1),
                    "hbm_floor_frac_step": round(sbytes / 8e12 / (ms * 1e-3), 4)},
         "roofline": roof,

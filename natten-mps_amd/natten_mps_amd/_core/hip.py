@@ -41,7 +41,13 @@ NATIVE_GQA = True
 FUSED_LSE = True
 
 
+_AVAILABLE = False
+
+
 def is_available() -> bool:
+    global _AVAILABLE
+    if _AVAILABLE:  # a positive answer cannot change within a process
+        return True
     if not _lib.is_built():
         return False
     try:
@@ -50,6 +56,7 @@ def is_available() -> bool:
         _lib.load()
     except Exception:
         return False
+    _AVAILABLE = True
     return True
 
 
@@ -128,10 +135,16 @@ _CACHE_MAX = 512
 
 
 class _Sig:
-    __slots__ = ("prob", "refs", "out_shape", "lse_shape", "strided", "device")
+    __slots__ = ("prob", "prob_ref", "refs", "out_shape", "lse_shape", "strided", "device")
+
+
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def _raw_stream(device):
+    """hipStream_t of the current stream of `device` (an int)."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -149,6 +162,7 @@ def _fwd_sig(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_valu
     _same_dtype(q, k, v)
     sig = _Sig()
     sig.prob = _fused_problem(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_value)
+    sig.prob_ref = ctypes.byref(sig.prob)
     out_sp = tuple(sig.prob.out_length[3 - rank:])
     B, Hq = q.shape[0], q.shape[-2]
     sig.out_shape = (B, *out_sp, Hq, v.shape[-1])
@@ -177,7 +191,7 @@ def forward_with_lse(rank: int, q, k, v, kernel_size, stride, dilation, is_causa
     lse = torch.empty(sig.lse_shape, dtype=torch.float32, device=q.device)
     r = sig.refs[1]
     lib = _lib.load()
-    rc = _launch(q.device, lib.natten_hip_forward, ctypes.byref(sig.prob),
+    rc = _launch(q.device, lib.natten_hip_forward, sig.prob_ref,
                  q.data_ptr(), r[0], k.data_ptr(), r[1], v.data_ptr(), r[2], out.data_ptr(), r[3],
                  lse.data_ptr(), r[4], _raw_stream(q.device))
     _lib.check(rc, "forward")
@@ -192,6 +206,7 @@ def _bwd_sig(rank, d_out, q, k, v, out, lse, d_lse, kernel_size, stride, dilatio
         raise TypeError("lse and its gradient must be float32")
     sig = _Sig()
     sig.prob = _fused_problem(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_value)
+    sig.prob_ref = ctypes.byref(sig.prob)
     sig.strided = any(s != 1 for s in stride)
     sig.device = q.device
     sig.lse_shape = tuple(lse.shape)
@@ -230,7 +245,7 @@ def fused_backward(rank: int, d_out, q, k, v, out, lse, kernel_size, dilation, s
     delta = torch.empty(sig.lse_shape, dtype=torch.float32, device=q.device)
     r = sig.refs[1]
     lib = _lib.load()
-    rc = _launch(q.device, lib.natten_hip_backward, ctypes.byref(sig.prob),
+    rc = _launch(q.device, lib.natten_hip_backward, sig.prob_ref,
                  q.data_ptr(), r[0], k.data_ptr(), r[1], v.data_ptr(), r[2], out.data_ptr(), r[3],
                  d_out.data_ptr(), r[4], lse.data_ptr(), r[5],
                  d_lse.data_ptr() if d_lse is not None else None, r[6],

@@ -101,18 +101,19 @@ def create_na_autograd_fn(rank: int) -> type:
         @staticmethod
         def backward(ctx, grad_output):
             mod = ctx.mod
-            q = ctx.saved_tensors[0]
+            saved = ctx.saved_tensors
+            q = saved[0]
             scale_value = float(q.shape[-1] ** -0.5 if ctx.scale is None else ctx.scale)
             tail = (None,) * 5
             if ctx.has_lse:
-                q, k, v, lse, out = ctx.saved_tensors
+                q, k, v, lse, out = saved
                 fused = getattr(mod, f"na{rank}d_fused_backward", None)
                 if fused is not None:
                     dq, dk, dv = fused(grad_output, q, k, v, out, lse, ctx.kernel_size, ctx.dilation,
                                        ctx.stride, ctx.is_causal, scale_value)
                     return (dq, dk, dv) + tail
             else:
-                q, k, v = ctx.saved_tensors
+                q, k, v = saved
             res = _split_backward(rank, mod, grad_output, q, k, v, ctx.kernel_size, ctx.stride, ctx.dilation,
                                   ctx.is_causal, scale_value)
             if res is not None:

@@ -142,8 +142,30 @@ def _using_pure_backend() -> bool:
     return ops.get_backend() == "pure"
 
 
-def _na(rank, query, key, value, kernel_size, stride, dilation, is_causal, scale, return_lse,
-        additional_keys, additional_values):
+# Validated, normalised parameters of recent calls, keyed on the tensor shapes
+# and the raw parameters: a repeated call skips the checks (they depend on
+# nothing else).  Parameters that are not hashable, or a scale that is not a
+# plain number, are validated on every call; a failed check is never cached.
+_SETUP_CACHE: dict = {}
+_SETUP_CACHE_MAX = 256
+
+
+def _na_setup(rank, query, key, value, kernel_size, stride, dilation, is_causal, scale, additional_keys,
+              additional_values):
+    """(kv_repeat, kernel, stride, dilation, causal, spatial, scale, full
+    window, extra keys, extra values), checked in the reference's order."""
+    ck = None
+    plain = additional_keys is None and additional_values is None
+    if plain and (scale is None or type(scale) in (float, int)):
+        # element types keep bool kernel sizes (rejected) apart from ints
+        ktypes = tuple(map(type, kernel_size)) if type(kernel_size) is tuple else type(kernel_size)
+        ck = (rank, query.shape, key.shape, value.shape, kernel_size, ktypes, stride, dilation, is_causal, scale)
+        try:
+            hit = _SETUP_CACHE.get(ck)
+        except TypeError:  # unhashable parameters (lists)
+            ck, hit = None, None
+        if hit is not None:
+            return hit
     kv_repeat = _validate_qkv(query, key, value, rank)
     add_k, add_v = _validate_additional_kv(query, additional_keys, additional_values, kv_repeat)
     ks = normalize_kernel_size(kernel_size, rank)
@@ -155,8 +177,22 @@ def _na(rank, query, key, value, kernel_size, stride, dilation, is_causal, scale
     check_stride_vs_kernel(st, ks)
     check_dilation_kernel_vs_input(dil, ks, spatial)
     scale_value = query.shape[-1] ** -0.5 if scale is None else float(scale)
+    full = _is_full_attention(ks, spatial) and all(s == 1 for s in st) and not any(causal)
+    res = (kv_repeat, ks, st, dil, causal, spatial, scale_value, full, add_k, add_v)
+    if ck is not None:
+        if len(_SETUP_CACHE) >= _SETUP_CACHE_MAX:
+            _SETUP_CACHE.clear()
+        _SETUP_CACHE[ck] = res
+    return res
 
-    if _is_full_attention(ks, spatial) and all(s == 1 for s in st) and not any(causal):
+
+def _na(rank, query, key, value, kernel_size, stride, dilation, is_causal, scale, return_lse,
+        additional_keys, additional_values):
+    kv_repeat, ks, st, dil, causal, spatial, scale_value, full, add_k, add_v = _na_setup(
+        rank, query, key, value, kernel_size, stride, dilation, is_causal, scale, additional_keys,
+        additional_values)
+
+    if full:
         return _sdpa_forward(query, _repeat_kv(key, kv_repeat), _repeat_kv(value, kv_repeat), scale_value,
                              spatial, return_lse=return_lse, additional_keys=add_k, additional_values=add_v)
 
