@@ -6,7 +6,8 @@
 Default workload: na2d forward+backward at DiNAT scale (B=16, 56x56, 4 heads,
 head dim 32, kernel 7, bf16), BASELINE config 3.  ``--config N`` runs another
 of the five BASELINE configs instead (``--dilation`` for configs 3 and 4,
-``--causal TF`` for config 2); only config 3 carries the CPU baseline.
+``--causal TF`` for config 2); every config carries the CPU baseline of its
+own workload.
 
 A step is one pass through the public API (``natten_mps_amd.na{1,2,3}d``, then
 ``torch.autograd.grad`` for the configs with a backward) on synthetic seeded
@@ -25,8 +26,12 @@ engine kept on the calling thread in
   queues while the GPU spins, so host launch gaps stay out), against 8 TB/s; ``traffic`` is the HBM bytes per launch measured with
   rocprofv3 (FETCH_SIZE x 2 + WRITE_SIZE, calibrated on a copy kernel) for
   the same kernel and workload, read from profiles/traffic.txt when present;
+* mfma: useful MFMA throughput of each fused tile kernel (the products it
+  needs per valid pair: forward 4·D, dQ 6·D, dK/dV 8·D flops) over its mean
+  launch time, against the 2.5 PFLOP/s dense bf16 peak;
 * cpu_baseline: the CPU oracle (the reference's pure algorithm) timed on the
-  host for a bounded sample of the same workload;
+  host over the same full workload: forward, forward + backward, and the
+  backward as their difference;
 * split_path (config 3): the split composition na2d_qk -> softmax -> na2d_av
   (forward + backward) timed eagerly, and its largest absolute difference
   from the fused path's outputs and gradients.
@@ -46,6 +51,7 @@ for _p in (ROOT, os.path.join(ROOT, "natten-mps_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 / fp16
 METRIC = "na2d fwd+bwd ms & effective TFLOP/s (56×56,K=7,bf16); % of roofline"
 
 # BASELINE configs
@@ -172,7 +178,7 @@ def compare_split(leaves, do, cfg, timed, args):
                 torch.cuda.synchronize()
                 ok &= all(torch.equal(x, y) for x, y in zip(g_out, ref))
             if ok:
-                ms_graph = round(timed(graph.replay), 4)
+                ms_graph = round(timed(graph.replay, head_start_ms=2.0 * args.steps * max(ms, 0.05) + 5.0), 4)
         except Exception as e:  # an optimisation of the timing, never required
             _log("split-path graph capture failed:", repr(e))
     a, b = fused_full(), split_step()
@@ -182,47 +188,86 @@ def compare_split(leaves, do, cfg, timed, args):
             "kernel_alg_bytes": int(split_bytes), "kernel_hbm_frac": kernel_frac}
 
 
-def cpu_baseline(dilation, budget_s=20.0):
-    """The oracle (reference pure algorithm, torch on the host CPU) on a
-    bounded sample: config 3 at batch 1 (1/16 of the workload), bf16,
-    forward + backward, median of the timed repeats."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(cfg, pairs, budget_s=30.0):
+    """The oracle (the reference's pure algorithm, ``oracle/pure.py``: torch
+    on the host CPU) over the FULL workload of the config, in the config's
+    dtype: the forward alone (no autograd), then forward + backward through
+    autograd; the backward is their difference.  GQA K/V are expanded first,
+    as the reference's functional layer does before its pure backend
+    (``functional.py:27-31,65-71``).  Each figure is the median of the
+    timed runs (the first run excluded once there are three), bounded by the
+    budget; ``value`` is the forward + backward (or forward-only) rate in
+    the metric's unit."""
     import torch
 
     import oracle.pure as P
 
-    cfg = CONFIGS[3]
-    torch.set_num_threads(os.cpu_count() or 1)
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    rank = len(cfg["spatial"])
+    dtype = getattr(torch, cfg["dtype"])
+    B, Hq, Hkv, D = cfg["batch"], cfg["heads"], cfg["kv_heads"], cfg["dim"]
     g = torch.Generator().manual_seed(cfg["seed"])
-    shape = (1, *cfg["spatial"], cfg["heads"], cfg["dim"])
-    q, k, v, do = (torch.randn(shape, generator=g).to(torch.bfloat16) for _ in range(4))
-    ks, dil = cfg["kernel"], (dilation,) * 2
 
-    def step():
-        leaves = [t.clone().requires_grad_(True) for t in (q, k, v)]
-        out = P.na2d_forward(*leaves, ks, (1, 1), dil, (False, False), None)
-        torch.autograd.grad(out, leaves, do)
+    def make(h):
+        return torch.randn((B, *cfg["spatial"], h, D), generator=g).to(dtype)
 
-    step()
-    times, t_end = [], time.perf_counter() + budget_s
-    while time.perf_counter() < t_end and len(times) < 20:
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    n = 1
-    for s in cfg["spatial"]:
-        n *= s
-    pairs = n * cfg["kernel"][0] * cfg["kernel"][1] * cfg["heads"]  # non-causal: windows always full
-    flops = 14.0 * pairs * cfg["dim"]
-    med = statistics.median(times)
-    return {
-        "value": flops / med / 1e12,
-        "unit": "TFLOP/s",
-        "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": f"na2d bf16 fwd+bwd at batch 1 of 16 (1/16 of the workload), oracle/pure.py on the host CPU, "
-                  f"median of {len(times)} runs = {med * 1e3:.1f} ms (x16 = {med * 16e3:.0f} ms per full step); "
-                  f"os.cpu_count()={os.cpu_count()}",
-    }
+    q, k, v, do = make(Hq), make(Hkv), make(Hkv), make(Hq)
+    fwd = getattr(P, f"na{rank}d_forward")
+    rep = Hq // Hkv
+    params = (cfg["kernel"], (1,) * rank, cfg["dilation"], cfg["causal"], None)
+
+    def forward(qq, kk, vv):
+        if rep != 1:
+            kk, vv = kk.repeat_interleave(rep, dim=-2), vv.repeat_interleave(rep, dim=-2)
+        return fwd(qq, kk, vv, *params)
+
+    def run_forward():
+        with torch.no_grad():
+            forward(q, k, v)
+
+    def run_step():
+        leaves = [t.detach().requires_grad_(True) for t in (q, k, v)]
+        torch.autograd.grad(forward(*leaves), leaves, do)
+
+    def median_time(fn, share):
+        times, t_end = [], time.perf_counter() + share
+        while not times or (time.perf_counter() < t_end and len(times) < 8):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times[1:] if len(times) >= 3 else times), len(times)
+
+    t_fwd, n_fwd = median_time(run_forward, budget_s / 3)
+    fwd_flops = 4.0 * pairs * D
+    res = {"unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+           "fwd_ms": round(t_fwd * 1e3, 1)}
+    if cfg["backward"]:
+        t_step, n_step = median_time(run_step, 2 * budget_s / 3)
+        res["value"] = 14.0 * pairs * D / t_step / 1e12
+        res["step_ms"] = round(t_step * 1e3, 1)
+        res["bwd_ms"] = round((t_step - t_fwd) * 1e3, 1)
+        timed_runs = f"forward {n_fwd} runs, forward + backward {n_step} runs"
+    else:
+        res["value"] = fwd_flops / t_fwd / 1e12
+        res["step_ms"] = res["fwd_ms"]
+        timed_runs = f"{n_fwd} runs"
+    res["value"] = round(res["value"], 5)
+    res["sample"] = (f"the full workload (batch {B}), oracle/pure.py in {cfg['dtype']} on the host CPU, "
+                     f"{threads} torch threads, median of {timed_runs}; CPU: {_cpu_model()}, "
+                     f"os.cpu_count()={os.cpu_count()}")
+    return res
 
 
 def main():
@@ -377,7 +422,9 @@ def main():
                 ref = [t.clone() for t in step()]
                 torch.cuda.synchronize()
             if graph_ok:
-                ms_graph = timed(graph.replay)
+                # replays queued behind a spin, so that the host's graph
+                # launch cost (tens of µs) stays out of a short step's time
+                ms_graph = timed(graph.replay, head_start_ms=2.0 * args.steps * max(ms_eager, 0.05) + 5.0)
                 _log(f"graph step {ms_graph:.4f} ms")
             else:
                 _log("graph replay differs from the eager step; reporting the eager time")
@@ -407,6 +454,25 @@ def main():
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_name, workload),
                 "kernel": dom_name, "mean_us": round(mean_s * 1e6, 2), "alg_bytes": nbytes}
+    # MFMA utilisation of the fused tile kernels, on useful work: the MFMA
+    # products each kernel needs per valid (query, key) pair and head dim --
+    # forward q.k and p.v (4 flops), dQ kernel q.k, dO.v, dS.k (6), dK/dV
+    # kernel q.k, dO.v, p.dO, dS.q (8) -- over its mean launch time, against
+    # the dense bf16/fp16 MFMA peak.  (The tiles also compute the masked
+    # pairs of their unions; those executed flops are in the counter
+    # profiles, not here.)
+    mfma = None
+    per_pair = {"na_fwd_mfma": 4.0, "na_bwd_q_mfma": 6.0, "na_bwd_kv_mfma": 8.0}
+    if dtype != torch.float32:
+        kern = {}
+        for name, (n, tot, _, _) in stats.items():
+            if name in per_pair:
+                t = tot / n * 1e-3
+                useful = per_pair[name] * pairs * D / t / 1e12
+                kern[name] = {"useful_tflops": round(useful, 2), "frac": round(useful / MFMA_PEAK_TFLOPS, 4),
+                              "mean_us": round(t * 1e6, 2)}
+        mfma = {"peak_tflops": MFMA_PEAK_TFLOPS, "useful_tflops_step": round(tflops, 2),
+                "useful_frac_step": round(tflops / MFMA_PEAK_TFLOPS, 4), "kernels": kern}
     _log(f"step {ms:.4f} ms  {tflops:.2f} TFLOP/s  {sbytes / (ms * 1e-3) / 1e9:.0f} GB/s  "
          f"HBM floor {sbytes / 8e12 * 1e6:.1f} us -> {sbytes / 8e12 / (ms * 1e-3):.1%} of roofline (step)")
 
@@ -424,9 +490,11 @@ def main():
             _log("split comparison failed:", repr(e))
 
     cpu = None
-    if args.config == 3 and not args.no_cpu:
+    if not args.no_cpu:
         try:
-            cpu = cpu_baseline(cfg["dilation"][0])
+            cpu = cpu_baseline(cfg, pairs)
+            _log(f"cpu baseline: forward {cpu['fwd_ms']} ms, step {cpu['step_ms']} ms, {cpu['value']} TFLOP/s "
+                 f"({cpu['cores']} threads)")
         except Exception as e:  # the baseline is reported, never required
             _log("cpu baseline failed:", repr(e))
 
@@ -456,6 +524,7 @@ def main():
                    "step_hbm_bytes": sbytes, "step_gbs": round(sbytes / (ms * 1e-3) / 1e9, 1),
                    "hbm_floor_frac_step": round(sbytes / 8e12 / (ms * 1e-3), 4)},
         "roofline": roof,
+        "mfma": mfma,
         "cpu_baseline": cpu,
         "split_path": split_path,
     }), flush=True)
