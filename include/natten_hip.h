@@ -132,6 +132,53 @@ int natten_hip_backward(const natten_problem_t *p,
                         float *delta, const natten_layout_t *ldelta,
                         void *stream);
 
+/* Global keys (additional_keys / additional_values of the reference's
+ * na{1,2,3}d, functional.py:74-110 and :285-299 with merge.py:21-156 -- there
+ * a split NA pass, dense attention over the extra tokens and a merge of the
+ * two by their log-sum-exps).  Here the extra tokens are keys that every query
+ * attends besides its neighbourhood, inside the fused kernels: out is the
+ * softmax over the neighbourhood and the global keys together, lse its
+ * log-sum-exp.  gk / gv are [B, n_global, heads_kv, dim] (layout: batch,
+ * head, and the token stride in axis[2]; axis[0], axis[1] unused).  These
+ * entry points serve the MFMA tile path only (bf16/fp16, dim_qk == dim_v in
+ * {32, 64, 128}, stride 1, aligned operands) and return
+ * NATTEN_ERR_UNSUPPORTED otherwise; natten_hip_global_supported answers that
+ * from the problem alone (1 / 0; backward != 0 also checks the backward).
+ * The backward also writes dgk / dgv (summed over every query of each GQA
+ * group) and needs an fp32 workspace of natten_hip_global_workspace(p, n)
+ * floats (-1: invalid problem). */
+int natten_hip_global_supported(const natten_problem_t *p, int32_t n_global, int32_t backward);
+int64_t natten_hip_global_workspace(const natten_problem_t *p, int32_t n_global);
+int natten_hip_forward_global(const natten_problem_t *p,
+                              const void *q, const natten_layout_t *lq,
+                              const void *k, const natten_layout_t *lk,
+                              const void *v, const natten_layout_t *lv,
+                              const void *gk, const natten_layout_t *lgk,
+                              const void *gv, const natten_layout_t *lgv,
+                              int32_t n_global,
+                              void *out, const natten_layout_t *lo,
+                              float *lse, const natten_layout_t *llse,
+                              void *stream);
+int natten_hip_backward_global(const natten_problem_t *p,
+                               const void *q, const natten_layout_t *lq,
+                               const void *k, const natten_layout_t *lk,
+                               const void *v, const natten_layout_t *lv,
+                               const void *gk, const natten_layout_t *lgk,
+                               const void *gv, const natten_layout_t *lgv,
+                               int32_t n_global,
+                               const void *out, const natten_layout_t *lo,
+                               const void *dout, const natten_layout_t *ldo,
+                               const float *lse, const natten_layout_t *llse,
+                               const float *dlse, const natten_layout_t *ldlse,
+                               void *dq, const natten_layout_t *ldq,
+                               void *dk, const natten_layout_t *ldk,
+                               void *dv, const natten_layout_t *ldv,
+                               void *dgk, const natten_layout_t *ldgk,
+                               void *dgv, const natten_layout_t *ldgv,
+                               float *delta, const natten_layout_t *ldelta,
+                               float *work, int64_t work_floats,
+                               void *stream);
+
 /* Allocation-free fused backward (no counterpart in the reference): the same
  * computation and results as natten_hip_backward, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,

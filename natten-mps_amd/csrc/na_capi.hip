@@ -283,6 +283,123 @@ int natten_hip_backward_noalloc(const natten_problem_t* p, const void* q, const 
                          ldv, delta, &ld, stream);
 }
 
+namespace {
+
+// Global keys from the ABI: layouts [B, n, Hkv, D] with the token stride in
+// axis[2]; checks shared by the two global-key entry points.
+int make_global(const na::Prob& P, const void* gk, const natten_layout_t* lgk, const void* gv,
+                const natten_layout_t* lgv, int32_t n, na::GlobalSet& g) {
+    if (n < 1) return fail(NATTEN_ERR_INVALID, "global keys: n_global must be >= 1 (got %d)", n);
+    if (any_null({gk, gv, lgk, lgv})) return fail(NATTEN_ERR_INVALID, "NULL global key operand");
+    g.k = gk;
+    g.v = gv;
+    g.lk = to_lay(lgk);
+    g.lv = to_lay(lgv);
+    g.n = n;
+    if (!runs_aligned(8, {{gk, lgk, P.Dqk}, {gv, lgv, P.Dv}}))
+        return fail(NATTEN_ERR_UNSUPPORTED, "global keys: operands must be 16-byte aligned with strides in 8s");
+    return NATTEN_OK;
+}
+
+// The global-key path: the MFMA tile kernels with global-key chunks.
+bool global_eligible(const na::Prob& P, int dtype, int vec, const na::GlobalSet& g, bool backward) {
+    const int D = P.Dqk > P.Dv ? P.Dqk : P.Dv;
+    return use_mfma() && na::mfma_eligible(P, dtype, D, vec != 0, backward, true) &&
+           na::mfma_global_key_ok(P, dtype, g);
+}
+
+}  // namespace
+
+int natten_hip_global_supported(const natten_problem_t* p, int32_t n_global, int32_t backward) {
+    na::Prob P;
+    if (make_prob(p, true, P)) return 0;
+    na::GlobalSet g{};
+    g.n = n_global;
+    g.lk.s2 = g.lv.s2 = static_cast<long long>(p->heads_kv) * p->dim_qk;
+    g.lk.h = g.lv.h = p->dim_qk;
+    return n_global >= 1 && global_eligible(P, p->dtype, 1, g, backward != 0) ? 1 : 0;
+}
+
+int64_t natten_hip_global_workspace(const natten_problem_t* p, int32_t n_global) {
+    na::Prob P;
+    if (make_prob(p, true, P) || n_global < 1) return -1;
+    return static_cast<int64_t>(na::global_workspace_floats(P, n_global));
+}
+
+int natten_hip_forward_global(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
+                              const natten_layout_t* lk, const void* v, const natten_layout_t* lv, const void* gk,
+                              const natten_layout_t* lgk, const void* gv, const natten_layout_t* lgv,
+                              int32_t n_global, void* out, const natten_layout_t* lo, float* lse,
+                              const natten_layout_t* llse, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, true, P);
+    if (rc) return rc;
+    if (any_null({q, k, v, out, lse, lq, lk, lv, lo, llse})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    na::GlobalSet g{};
+    rc = make_global(P, gk, lgk, gv, lgv, n_global, g);
+    if (rc) return rc;
+    const int D = P.Dqk > P.Dv ? P.Dqk : P.Dv;
+    const int vec =
+        runs_aligned(dpl_for(D), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {v, lv, P.Dv}, {out, lo, P.Dv}}) ? 1 : 0;
+    if (!global_eligible(P, p->dtype, vec, g, false) ||
+        !na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(llse)}))
+        return fail(NATTEN_ERR_UNSUPPORTED,
+                    "global keys run on the MFMA tile kernels only (bf16/fp16, head dim 32/64/128, stride 1, "
+                    "aligned operands)");
+    return launch_status(na::mfma_forward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), lse,
+                                          to_lay(llse), p->dtype, static_cast<hipStream_t>(stream), &g),
+                         "forward_global");
+}
+
+int natten_hip_backward_global(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
+                               const natten_layout_t* lk, const void* v, const natten_layout_t* lv, const void* gk,
+                               const natten_layout_t* lgk, const void* gv, const natten_layout_t* lgv,
+                               int32_t n_global, const void* out, const natten_layout_t* lo, const void* dout,
+                               const natten_layout_t* ldo, const float* lse, const natten_layout_t* llse,
+                               const float* dlse, const natten_layout_t* ldlse, void* dq, const natten_layout_t* ldq,
+                               void* dk, const natten_layout_t* ldk, void* dv, const natten_layout_t* ldv, void* dgk,
+                               const natten_layout_t* ldgk, void* dgv, const natten_layout_t* ldgv, float* delta,
+                               const natten_layout_t* ldelta, float* work, int64_t work_floats, void* stream) {
+    na::Prob P;
+    int rc = make_prob(p, true, P);
+    if (rc) return rc;
+    if (any_null({q, k, v, out, dout, lse, dq, dk, dv, delta, lq, lk, lv, lo, ldo, llse, ldq, ldk, ldv, ldelta, dgk,
+                  dgv, ldgk, ldgv, work}))
+        return fail(NATTEN_ERR_INVALID, "NULL operand");
+    if (dlse && !ldlse) return fail(NATTEN_ERR_INVALID, "dlse given without a layout");
+    na::GlobalSet g{};
+    rc = make_global(P, gk, lgk, gv, lgv, n_global, g);
+    if (rc) return rc;
+    if (!runs_aligned(8, {{dgk, ldgk, P.Dqk}, {dgv, ldgv, P.Dv}}))
+        return fail(NATTEN_ERR_UNSUPPORTED, "global keys: gradients must be 16-byte aligned with strides in 8s");
+    const size_t need = na::global_workspace_floats(P, n_global);
+    if (work_floats < 0 || static_cast<size_t>(work_floats) < need)
+        return fail(NATTEN_ERR_INVALID, "backward_global: workspace of %lld floats, %zu needed",
+                    static_cast<long long>(work_floats), need);
+    const int D = P.Dqk > P.Dv ? P.Dqk : P.Dv;
+    const int vec = runs_aligned(dpl_for(D), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {v, lv, P.Dv}, {out, lo, P.Dv},
+                                              {dout, ldo, P.Dv}, {dq, ldq, P.Dqk}, {dk, ldk, P.Dqk}, {dv, ldv, P.Dv}})
+                        ? 1
+                        : 0;
+    if (!global_eligible(P, p->dtype, vec, g, true) ||
+        !na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(ldo), to_lay(llse),
+                                  to_lay(ldq), to_lay(ldk), to_lay(ldv), to_lay(ldelta)}) ||
+        (dlse && !na::mfma_offsets_fit(P, {to_lay(ldlse)})))
+        return fail(NATTEN_ERR_UNSUPPORTED,
+                    "global keys run on the MFMA tile kernels only (bf16/fp16, head dim 32/64/128, stride 1, "
+                    "aligned operands)");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    rc = launch_status(na::mfma_backward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout,
+                                         to_lay(ldo), lse, to_lay(llse), dlse, to_lay(ldlse), dq, to_lay(ldq), dk,
+                                         to_lay(ldk), dv, to_lay(ldv), delta, to_lay(ldelta), p->dtype, s, &g),
+                       "backward_global");
+    if (rc) return rc;
+    return launch_status(na::mfma_global_key_backward(P, q, to_lay(lq), dout, to_lay(ldo), lse, to_lay(llse), delta,
+                                                      to_lay(ldelta), g, dgk, to_lay(ldgk), dgv, to_lay(ldgv), work,
+                                                      p->dtype, s),
+                         "backward_global (global keys)");
+}
+
 int natten_hip_qk_forward(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
                           const natten_layout_t* lk, void* attn, const natten_layout_t* la, void* stream) {
     na::Prob P;

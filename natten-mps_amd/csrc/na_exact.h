@@ -151,6 +151,47 @@ __device__ __forceinline__ void exact_forward(float scale, const ExactAxis (&x)[
     lse = m + logf(l);
 }
 
+// Global keys of one (batch, kv head) for the exact paths: rows k + j * ks,
+// v + j * vs, j < n (every query attends them besides its window).
+template <typename T>
+struct ExactGlobal {
+    const T *k, *v;
+    int ks, vs, n;
+};
+
+// exact_forward over the window and the global keys together.
+template <typename T, int D>
+__device__ __forceinline__ void exact_forward_global(float scale, const ExactAxis (&x)[3], const T* __restrict__ q_row,
+                                                     const T* __restrict__ kb, Strides3 ks,
+                                                     const T* __restrict__ vb, Strides3 vs,
+                                                     const ExactGlobal<T>& g, int grp, f32x4_t (&acc)[D / 16],
+                                                     float& lse) {
+    float m = -INFINITY;
+    exact_window(x, [&](int j0, int j1, int j2, int) {
+        m = __builtin_elementwise_maximum(m, exact_dot<T, D>(q_row, kb + ks.at(j0, j1, j2)) * scale);
+    });
+#pragma unroll 1
+    for (int j = 0; j < g.n; ++j)
+        m = __builtin_elementwise_maximum(m, exact_dot<T, D>(q_row, g.k + j * g.ks) * scale);
+    float l = 0.f;
+    exact_zero(acc);
+    exact_window(x, [&](int j0, int j1, int j2, int) {
+        const float e = expf(exact_dot<T, D>(q_row, kb + ks.at(j0, j1, j2)) * scale - m);
+        l += e;
+        exact_axpy<T, D>(e, vb + vs.at(j0, j1, j2), grp, acc);
+    });
+#pragma unroll 1
+    for (int j = 0; j < g.n; ++j) {
+        const float e = expf(exact_dot<T, D>(q_row, g.k + j * g.ks) * scale - m);
+        l += e;
+        exact_axpy<T, D>(e, g.v + j * g.vs, grp, acc);
+    }
+    const float inv = 1.f / l;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) acc[db] *= inv;
+    lse = m + logf(l);
+}
+
 // Query side of the backward: acc = sum P (dP - delta) k over the window
 // (times scale by the caller), P = exp(scale q.k - lse), dP = dO . v.
 template <typename T, int D>
@@ -165,6 +206,23 @@ __device__ __forceinline__ void exact_backward_q(float scale, const ExactAxis (&
         const float dp = exact_dot<T, D>(do_row, vb + vs.at(j0, j1, j2));
         exact_axpy<T, D>(pr * (dp - delta), kr, grp, acc);
     });
+}
+
+// exact_backward_q over the window and the global keys together.
+template <typename T, int D>
+__device__ __forceinline__ void exact_backward_q_global(float scale, const ExactAxis (&x)[3],
+                                                        const T* __restrict__ q_row, const T* __restrict__ do_row,
+                                                        float lse, float delta, const T* __restrict__ kb, Strides3 ks,
+                                                        const T* __restrict__ vb, Strides3 vs,
+                                                        const ExactGlobal<T>& g, int grp, f32x4_t (&acc)[D / 16]) {
+    exact_backward_q<T, D>(scale, x, q_row, do_row, lse, delta, kb, ks, vb, vs, grp, acc);
+#pragma unroll 1
+    for (int j = 0; j < g.n; ++j) {
+        const T* kr = g.k + j * g.ks;
+        const float pr = expf(exact_dot<T, D>(q_row, kr) * scale - lse);
+        const float dp = exact_dot<T, D>(do_row, g.v + j * g.vs);
+        exact_axpy<T, D>(pr * (dp - delta), kr, grp, acc);
+    }
 }
 
 // Key side of the backward for one key of one q head (the caller sums the

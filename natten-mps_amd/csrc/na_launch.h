@@ -72,20 +72,41 @@ private:
 };
 bool device_alloc_allowed();
 
+// Global keys of a fused call (the reference's additional_keys): rows of
+// keys and values [B, n, Hkv, D] with their batch / head strides and the
+// token stride in s2.
+struct GlobalSet {
+    const void *k, *v;
+    Lay lk, lv;
+    int n;
+};
+
 // MFMA tile path (na_mfma.hip): bf16/fp16, stride 1, equal head dims 32/64/128.
 // mfma_static_lds_ok: no tile kernel instance declares static LDS (checked
 // once per process); mfma_lds_audit returns 1 when so, 0 otherwise, and the
 // number of instances whose attributes were read.
 bool mfma_static_lds_ok();
 int mfma_lds_audit(int* checked);
-bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward);
+// `global`: with global keys (their LDS on top of the tiles').
+bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward, bool global = false);
 bool mfma_offsets_fit(const Prob& p, std::initializer_list<Lay> lays);
 hipError_t mfma_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
-                        Lay lo, float* lse, Lay ll, int dtype, hipStream_t s);
+                        Lay lo, float* lse, Lay ll, int dtype, hipStream_t s, const GlobalSet* g = nullptr);
 hipError_t mfma_backward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
                          const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                          const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
-                         float* delta, Lay lde, int dtype, hipStream_t s);
+                         float* delta, Lay lde, int dtype, hipStream_t s, const GlobalSet* g = nullptr);
+
+// Key side of the global keys' backward (na_global.hip): dk and dv of the
+// global keys (summed over every query of each q head of the group), from the
+// forward's lse and the backward's delta.  Partial sums over slices of the
+// queries go to `work` (global_workspace_floats of them), then one pass adds
+// them in a fixed order.  mfma_global_key_ok: the problem fits the kernel.
+bool mfma_global_key_ok(const Prob& p, int dtype, const GlobalSet& g);
+size_t global_workspace_floats(const Prob& p, int n);
+hipError_t mfma_global_key_backward(const Prob& p, const void* q, Lay lq, const void* dout, Lay ldo, const float* lse,
+                                    Lay ll, const float* delta, Lay lde, const GlobalSet& g, void* dk, Lay ldk,
+                                    void* dv, Lay ldv, float* work, int dtype, hipStream_t s);
 
 // Split ops on the MFMA tile path, query side: `rows` is the operand of KV
 // entries per query (attn or dattn), `staged` the operands staged per tile.

@@ -58,7 +58,12 @@ namespace {
 // Online softmax over groups of fwd_group<D>() chunks (one max reduction and
 // one rescale per group).
 // ---------------------------------------------------------------------------
-template <typename T, int D, int LAY, bool WIDE>
+template <typename T>
+__device__ __forceinline__ ExactGlobal<T> exact_global(const GlobalKeys<T>& g, int b, int hk) {
+    return ExactGlobal<T>{g.k + b * g.kb + hk * g.kh, g.v + b * g.vb + hk * g.vh, g.ks, g.vs, g.n};
+}
+
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
 __device__ __forceinline__ void redo_fwd(const void* kargs, int wg, int wave, int col, int grp) {
     const FwdArgs<T>& A = *static_cast<const FwdArgs<T>*>(kargs);
     const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
@@ -72,14 +77,19 @@ __device__ __forceinline__ void redo_fwd(const void* kargs, int wg, int wave, in
     for (int h = h0; h < h1; ++h) {
         const int hk = kv_head(A.ts, h);
         float lse_v;
-        exact_forward<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), bh_ptr(A.k, ak, b, hk),
-                            strides3(ak), bh_ptr(A.v, av, b, hk), strides3(av), grp, acc, lse_v);
+        if constexpr (GLOBAL)
+            exact_forward_global<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), bh_ptr(A.k, ak, b, hk),
+                                       strides3(ak), bh_ptr(A.v, av, b, hk), strides3(av),
+                                       exact_global(A.gk, b, hk), grp, acc, lse_v);
+        else
+            exact_forward<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), bh_ptr(A.k, ak, b, hk),
+                                strides3(ak), bh_ptr(A.v, av, b, hk), strides3(av), grp, acc, lse_v);
         store_rows<T, D>(bh_ptr(A.out, ao, b, h), vol_off(ao, pos), grp, acc, 1.f);
         if (grp == 0) bh_ptr(A.lse, al, b, h)[vol_off(al, pos)] = lse_v;
     }
 }
 
-template <typename T, int D, int LAY, bool WIDE>
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
 __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfma(FwdArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
@@ -181,6 +191,41 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfm
         }
         more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
+        if constexpr (GLOBAL) {
+            // the finished head's global keys, 32 at a time, continue the
+            // same online softmax (every key valid up to n)
+            if (fresh || !more) {
+                const GlobalKeys<T>& g = args.gk;
+                const int hk = kv_head(ts, h);
+                const T* gkb = g.k + b * g.kb + hk * g.kh;
+                const T* gvb = g.v + b * g.vb + hk * g.vh;
+                T* Xk = Vs + ts.slots * D;
+                T* Xv = Xk + 32 * D;
+                for (int j0 = 0; j0 < g.n; j0 += 32) {
+                    stage_global<T, D>(gkb, g.ks, gvb, g.vs, j0, g.n, Xk, Xv, wave, ts.waves, lane);
+                    wait_loads();
+                    __syncthreads();
+                    f32x4_t xb[2], s[2];
+                    global_bias(j0, g.n, grp, xb);
+                    score_chunk<T, D>(Xk, 0, col, grp, qf, xb, s);
+                    const float mnew = fmaxp(m, max_rows(max8(s)) * sc2);
+                    const float mref = mnew == -INFINITY ? 0.f : mnew;
+                    const float corr = __builtin_amdgcn_exp2f(m - mref);
+                    m = mnew;
+                    lacc *= corr;
+#pragma unroll
+                    for (int db = 0; db < D / 16; ++db) acc[db] *= corr;
+#pragma unroll
+                    for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], sc2, -mref));
+                    const uint4 pk = pack8<T>(s);
+                    accumulate_chunk<T, D>(Xv, 0, lane, pk, acc);
+                    lacc = Mma<T>::run(ones, pk, lacc);
+                    __syncthreads();  // the global rows are no longer read
+                }
+            }
+        }
         if (more && !same_rows(ts, blk, h, w.h)) {
             const int p0 = slice_pos(p, blk, w.u0), hk = kv_head(ts, w.h);
             stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0),
@@ -197,7 +242,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfm
     }
     // items whose tile result was not finite: exact recomputation (the
     // walk's state is dead here, so this costs the loop no registers)
-    if (redo) redo_fwd<T, D, LAY, WIDE>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
+    if (redo) redo_fwd<T, D, LAY, WIDE, GLOBAL>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
 }
 
 // ---------------------------------------------------------------------------
@@ -205,7 +250,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfm
 // dq = scale * sum_k P (dP - delta) k, with P = exp(scale q.k - lse) and
 // dP = dO . v.  The dP product starts from -delta.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int LAY, bool WIDE>
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
 __device__ __forceinline__ void redo_bwd_q(const void* kargs, int wg, int wave, int col, int grp) {
     const BwdQArgs<T>& A = *static_cast<const BwdQArgs<T>*>(kargs);
     const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
@@ -222,14 +267,20 @@ __device__ __forceinline__ void redo_bwd_q(const void* kargs, int wg, int wave, 
         const T* do_row = bh_ptr(A.dout, ado, b, h) + vol_off(ado, pos);
         float di = exact_dot<T, D>(do_row, bh_ptr(A.o, ao, b, h) + vol_off(ao, pos));
         if (A.dlse) di -= bh_ptr(A.dlse, adl, b, h)[vol_off(adl, pos)];
-        exact_backward_q<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), do_row,
-                               bh_ptr(A.lse, al, b, h)[vol_off(al, pos)], di, bh_ptr(A.k, ak, b, hk), strides3(ak),
-                               bh_ptr(A.v, av, b, hk), strides3(av), grp, acc);
+        if constexpr (GLOBAL)
+            exact_backward_q_global<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), do_row,
+                                          bh_ptr(A.lse, al, b, h)[vol_off(al, pos)], di, bh_ptr(A.k, ak, b, hk),
+                                          strides3(ak), bh_ptr(A.v, av, b, hk), strides3(av),
+                                          exact_global(A.gk, b, hk), grp, acc);
+        else
+            exact_backward_q<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), do_row,
+                                   bh_ptr(A.lse, al, b, h)[vol_off(al, pos)], di, bh_ptr(A.k, ak, b, hk),
+                                   strides3(ak), bh_ptr(A.v, av, b, hk), strides3(av), grp, acc);
         store_rows<T, D>(bh_ptr(A.dq, adq, b, h), vol_off(adq, pos), grp, acc, A.p.scale);
     }
 }
 
-template <typename T, int D, int LAY, bool WIDE>
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
 __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_mfma(BwdQArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
@@ -330,6 +381,33 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_
         }
         more = walk_next(blk, w, fresh);
         __syncthreads();  // the slice is no longer read
+        if constexpr (GLOBAL) {
+            // the finished head's global keys, 32 at a time
+            if (fresh || !more) {
+                const GlobalKeys<T>& g = args.gk;
+                const int hk = kv_head(ts, h);
+                const T* gkb = g.k + b * g.kb + hk * g.kh;
+                const T* gvb = g.v + b * g.vb + hk * g.vh;
+                T* Xk = Vs + ts.slots * D;
+                T* Xv = Xk + 32 * D;
+                for (int j0 = 0; j0 < g.n; j0 += 32) {
+                    stage_global<T, D>(gkb, g.ks, gvb, g.vs, j0, g.n, Xk, Xv, wave, ts.waves, lane);
+                    wait_loads();
+                    __syncthreads();
+                    f32x4_t xb[2], s[2], dp[2];
+                    global_bias(j0, g.n, grp, xb);
+                    score_chunk<T, D>(Xk, 0, col, grp, qf, xb, s);
+                    score_chunk<T, D>(Xv, 0, col, grp, gf, nd, dp);
+#pragma unroll
+                    for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], sc2, -L2)) * dp[bb][i];
+                    accumulate_chunk<T, D>(Xk, 0, lane, pack8<T>(s), acc);
+                    __syncthreads();  // the global rows are no longer read
+                }
+            }
+        }
         if (more && !same_rows(ts, blk, h, w.h)) {
             const int p0 = slice_pos(p, blk, w.u0), hk = kv_head(ts, w.h);
             stage_pair<T, D>(p, blk, ts, sm, plane_of(kg, lk, w.b, hk, p0), lk, Ks, plane_of(vg, lv, w.b, hk, p0),
@@ -340,7 +418,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_
             if (ln.valid) store_rows<T, D>(bh_ptr(dq, ldq, b, h), vol_off(ldq, ln.pos), grp, acc, p.scale);
         }
     }
-    if (redo) redo_bwd_q<T, D, LAY, WIDE>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
+    if (redo) redo_bwd_q<T, D, LAY, WIDE, GLOBAL>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
 }
 
 // ---------------------------------------------------------------------------
@@ -999,7 +1077,10 @@ void set_h_per(TileShape& ts, int per) {
 // Workgroup box in class coordinates: up to 64 items (4 waves), power-of-two
 // extents, innermost axis first (8 wide unless the problem is 1-D); halved
 // until the staged union fits the LDS budget.
-bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts) {
+// LDS a forward / dQ workgroup adds for global keys: 32 key and 32 value rows.
+size_t global_lds(int D) { return static_cast<size_t>(2 * 32) * D * 2; }
+
+bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts, size_t extra_lds = 0) {
     int n[3];
     for (int a = 0; a < 3; ++a) n[a] = n_class_h(p.ax[a], 0);  // class 0 is the longest
     for (int items = kMaxItems; items >= 16; items /= 2) {
@@ -1022,7 +1103,7 @@ bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts) {
         const int u2 = union_extent(p.ax[2], ts.T[2], key_tile);
         ts.rowshift = std::max(3, log2_of(u2));
         ts.slots = ((u1 * (1 << ts.rowshift) + 31) / 32) * 32;
-        if (lds_bytes(kind, ts.slots, D) <= kLdsBudget) {
+        if (lds_bytes(kind, ts.slots, D) + extra_lds <= kLdsBudget) {
             const int heads = key_tile ? p.Hkv : p.Hq;
             ts.nheads = heads;
             set_h_per(ts, 1);
@@ -1165,57 +1246,80 @@ const int* geometry_table(const Prob& p, const TileShape& ts, bool key_tile, hip
     return d;
 }
 
-template <typename T, int D, int LAY, bool WIDE>
+template <typename T>
+GlobalKeys<T> to_global(const GlobalSet* g) {
+    GlobalKeys<T> r{};
+    if (g) {
+        r.k = static_cast<const T*>(g->k);
+        r.v = static_cast<const T*>(g->v);
+        r.kb = g->lk.b;
+        r.kh = g->lk.h;
+        r.vb = g->lv.b;
+        r.vh = g->lv.h;
+        r.ks = static_cast<int>(g->lk.s2);
+        r.vs = static_cast<int>(g->lv.s2);
+        r.n = g->n;
+    }
+    return r;
+}
+
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
 hipError_t run_fwd(const Prob& p, TileShape ts, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
-                   void* o, Lay lo, float* lse, Lay ll, hipStream_t s) {
-    const auto kern = k_fwd_mfma<T, D, LAY, WIDE>;
-    const size_t shm = lds_bytes(kForward, ts.slots, D);
+                   void* o, Lay lo, float* lse, Lay ll, const GlobalSet* g, hipStream_t s) {
+    const auto kern = k_fwd_mfma<T, D, LAY, WIDE, GLOBAL>;
+    const size_t shm = lds_bytes(kForward, ts.slots, D) + (GLOBAL ? global_lds(D) : 0);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
     const int* geo = geometry_table(p, ts, false, s);
-    const FwdArgs<T> a{p,       ts,       geo,      (const T*)q, (const T*)k, (const T*)v, (T*)o,
-                       lse,     to_k(lq), to_k(lk), to_k(lv),    to_k(lo),    to_k(ll)};
-    NA_LAUNCH("na_fwd_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
+    const FwdArgs<T> a{p,   ts,       geo,      (const T*)q, (const T*)k, (const T*)v, (T*)o,
+                       lse, to_k(lq), to_k(lk), to_k(lv),    to_k(lo),    to_k(ll),    to_global<T>(g)};
+    NA_LAUNCH(GLOBAL ? "na_fwd_global_mfma" : "na_fwd_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))),
+              dim3(64 * ts.waves), shm, s, a);
     return hipGetLastError();
 }
 
-template <typename T, int D, int LAY>
+template <typename T, int D, int LAY, bool GLOBAL>
 hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
-                      Lay lo, float* lse, Lay ll, hipStream_t s) {
+                      Lay lo, float* lse, Lay ll, const GlobalSet* g, hipStream_t s) {
     TileShape ts{};
-    if (!choose_tile(p, kForward, D, ts)) return hipErrorInvalidValue;
-    if (ts.rowshift > 5) return run_fwd<T, D, LAY, true>(p, ts, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
-    return run_fwd<T, D, LAY, false>(p, ts, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
+    if (!choose_tile(p, kForward, D, ts, GLOBAL ? global_lds(D) : 0)) return hipErrorInvalidValue;
+    if (ts.rowshift > 5) return run_fwd<T, D, LAY, true, GLOBAL>(p, ts, q, lq, k, lk, v, lv, o, lo, lse, ll, g, s);
+    return run_fwd<T, D, LAY, false, GLOBAL>(p, ts, q, lq, k, lk, v, lv, o, lo, lse, ll, g, s);
 }
 
 template <typename T, int D>
 hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
-                      Lay lo, float* lse, Lay ll, hipStream_t s) {
+                      Lay lo, float* lse, Lay ll, const GlobalSet* g, hipStream_t s) {
+    // global-key instances exist for the general layout group only
+    if (g) return launch_fwd<T, D, kLayGeneral, true>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, g, s);
     switch (layout_group({lq, lo}, {lk, lv}, {ll})) {
         case kLayOne:
-            return launch_fwd<T, D, kLayOne>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
+            return launch_fwd<T, D, kLayOne, false>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, nullptr, s);
         case kLayTwo:
-            return launch_fwd<T, D, kLayTwo>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
+            return launch_fwd<T, D, kLayTwo, false>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, nullptr, s);
         default:
-            return launch_fwd<T, D, kLayGeneral>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, s);
+            return launch_fwd<T, D, kLayGeneral, false>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, nullptr, s);
     }
 }
 
-template <typename T, int D, int LAY, bool WIDE>
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
 hipError_t run_bwd_q(const Prob& p, TileShape ts, const void* q, Lay lq, const void* k, Lay lk, const void* v,
                      Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
-                     const float* dlse, Lay ldl, void* dq, Lay ldq, float* delta, Lay lde, hipStream_t s) {
-    const auto kern = k_bwd_q_mfma<T, D, LAY, WIDE>;
-    const size_t shm = lds_bytes(kBackwardQ, ts.slots, D);
+                     const float* dlse, Lay ldl, void* dq, Lay ldq, float* delta, Lay lde, const GlobalSet* g,
+                     hipStream_t s) {
+    const auto kern = k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL>;
+    const size_t shm = lds_bytes(kBackwardQ, ts.slots, D) + (GLOBAL ? global_lds(D) : 0);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
     const int* geo = geometry_table(p, ts, false, s);
     const BwdQArgs<T> a{p,        ts,       geo,      (const T*)q, (const T*)k, (const T*)v, (const T*)o,
                         (const T*)dout, lse, dlse,  (T*)dq,      delta,       to_k(lq),    to_k(lk),
-                        to_k(lv), to_k(lo), to_k(ldo), to_k(ll),  to_k(ldl),   to_k(ldq),   to_k(lde)};
-    NA_LAUNCH("na_bwd_q_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
+                        to_k(lv), to_k(lo), to_k(ldo), to_k(ll),  to_k(ldl),   to_k(ldq),   to_k(lde),
+                        to_global<T>(g)};
+    NA_LAUNCH(GLOBAL ? "na_bwd_q_global_mfma" : "na_bwd_q_mfma", kern,
+              dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
     return hipGetLastError();
 }
 
@@ -1236,18 +1340,19 @@ hipError_t run_bwd_kv(const Prob& p, TileShape ts, const void* q, Lay lq, const 
     return hipGetLastError();
 }
 
-template <typename T, int D, int LAY>
+template <typename T, int D, int LAY, bool GLOBAL>
 hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
                       const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                       const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
-                      float* delta, Lay lde, hipStream_t s) {
+                      float* delta, Lay lde, const GlobalSet* g, hipStream_t s) {
     TileShape tq{}, tk{};
-    if (!choose_tile(p, kBackwardQ, D, tq) || !choose_tile(p, kBackwardKV, D, tk)) return hipErrorInvalidValue;
+    if (!choose_tile(p, kBackwardQ, D, tq, GLOBAL ? global_lds(D) : 0) || !choose_tile(p, kBackwardKV, D, tk))
+        return hipErrorInvalidValue;
     hipError_t e = tq.rowshift > 5
-                       ? run_bwd_q<T, D, LAY, true>(p, tq, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl,
-                                                    dq, ldq, delta, lde, s)
-                       : run_bwd_q<T, D, LAY, false>(p, tq, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl,
-                                                     dq, ldq, delta, lde, s);
+                       ? run_bwd_q<T, D, LAY, true, GLOBAL>(p, tq, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll,
+                                                            dlse, ldl, dq, ldq, delta, lde, g, s)
+                       : run_bwd_q<T, D, LAY, false, GLOBAL>(p, tq, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll,
+                                                             dlse, ldl, dq, ldq, delta, lde, g, s);
     if (e != hipSuccess) return e;
     if (tk.rowshift > 5)
         return run_bwd_kv<T, D, LAY, true>(p, tk, q, lq, k, lk, v, lv, dout, ldo, lse, ll, delta, lde, dk, ldk, dv,
@@ -1260,12 +1365,16 @@ template <typename T, int D>
 hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
                       const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                       const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
-                      float* delta, Lay lde, hipStream_t s) {
+                      float* delta, Lay lde, const GlobalSet* gs, hipStream_t s) {
+    // global-key instances exist for the general layout group only
+    if (gs)
+        return launch_bwd<T, D, kLayGeneral, true>(p, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl, dq,
+                                                   ldq, dk, ldk, dv, ldv, delta, lde, gs, s);
     // without dlse its layout is never read
     const int g = layout_group({lq, lo, ldo, ldq}, {lk, lv, ldk, ldv}, {ll, lde, dlse ? ldl : ll});
-#define NA_BWD_LAY(L)                                                                                          \
-    return launch_bwd<T, D, L>(p, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl, dq, ldq, dk, ldk, dv, \
-                               ldv, delta, lde, s)
+#define NA_BWD_LAY(L)                                                                                                 \
+    return launch_bwd<T, D, L, false>(p, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl, dq, ldq, dk, ldk, \
+                                      dv, ldv, delta, lde, nullptr, s)
     switch (g) {
         case kLayOne:
             NA_BWD_LAY(kLayOne);
@@ -1383,16 +1492,20 @@ bool full_query_extent(const Prob& p) {
 
 template <typename T, int D, int LAY>
 void audit_fused(LdsAudit& a) {
-    audit_one(k_fwd_mfma<T, D, LAY, false>, "k_fwd_mfma", a);
-    audit_one(k_fwd_mfma<T, D, LAY, true>, "k_fwd_mfma (wide)", a);
-    audit_one(k_bwd_q_mfma<T, D, LAY, false>, "k_bwd_q_mfma", a);
-    audit_one(k_bwd_q_mfma<T, D, LAY, true>, "k_bwd_q_mfma (wide)", a);
+    audit_one(k_fwd_mfma<T, D, LAY, false, false>, "k_fwd_mfma", a);
+    audit_one(k_fwd_mfma<T, D, LAY, true, false>, "k_fwd_mfma (wide)", a);
+    audit_one(k_bwd_q_mfma<T, D, LAY, false, false>, "k_bwd_q_mfma", a);
+    audit_one(k_bwd_q_mfma<T, D, LAY, true, false>, "k_bwd_q_mfma (wide)", a);
     audit_one(k_bwd_kv_mfma<T, D, LAY, false>, "k_bwd_kv_mfma", a);
     audit_one(k_bwd_kv_mfma<T, D, LAY, true>, "k_bwd_kv_mfma (wide)", a);
 }
 
 template <typename T, int D>
 void audit_dim(LdsAudit& a) {
+    audit_one(k_fwd_mfma<T, D, kLayGeneral, false, true>, "k_fwd_mfma (global keys)", a);
+    audit_one(k_fwd_mfma<T, D, kLayGeneral, true, true>, "k_fwd_mfma (wide, global keys)", a);
+    audit_one(k_bwd_q_mfma<T, D, kLayGeneral, false, true>, "k_bwd_q_mfma (global keys)", a);
+    audit_one(k_bwd_q_mfma<T, D, kLayGeneral, true, true>, "k_bwd_q_mfma (wide, global keys)", a);
     audit_fused<T, D, kLayGeneral>(a);
     audit_fused<T, D, kLayOne>(a);
     audit_fused<T, D, kLayTwo>(a);
@@ -1497,16 +1610,17 @@ hipError_t mfma_split_wsum(const char* name, const Prob& p, int D, const void* w
 #undef NA_WSUM
 }
 
-bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward) {
+bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward, bool global) {
     if (dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f) || !mfma_static_lds_ok()) return false;
     if (p.Dqk != p.Dv || !(D == 32 || D == 64 || D == 128)) return false;
     for (int a = 0; a < 3; ++a)
         if (p.ax[a].st != 1) return false;
     // tile indices (the launch grid) stay in 31 bits
+    const size_t extra = global ? global_lds(D) : 0;
     TileShape ts{};
-    if (!choose_tile(p, kForward, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
+    if (!choose_tile(p, kForward, D, ts, extra) || grid_blocks(p, ts) >= (1LL << 31)) return false;
     if (backward) {
-        if (!choose_tile(p, kBackwardQ, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
+        if (!choose_tile(p, kBackwardQ, D, ts, extra) || grid_blocks(p, ts) >= (1LL << 31)) return false;
         if (!choose_tile(p, kBackwardKV, D, ts) || grid_blocks(p, ts) >= (1LL << 31)) return false;
     }
     return true;
@@ -1515,8 +1629,8 @@ bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward)
 bool mfma_offsets_fit(const Prob& p, std::initializer_list<Lay> lays) { return offsets_fit(p, lays); }
 
 hipError_t mfma_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
-                        Lay lo, float* lse, Lay ll, int dtype, hipStream_t s) {
-#define NA_FWD(T, DD) return launch_fwd<T, DD>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, s)
+                        Lay lo, float* lse, Lay ll, int dtype, hipStream_t s, const GlobalSet* g) {
+#define NA_FWD(T, DD) return launch_fwd<T, DD>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, g, s)
     if (dtype == NATTEN_BF16) {
         if (p.Dqk == 32) NA_FWD(bf16, 32);
         if (p.Dqk == 64) NA_FWD(bf16, 64);
@@ -1531,10 +1645,10 @@ hipError_t mfma_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay
 hipError_t mfma_backward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
                          const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                          const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
-                         float* delta, Lay lde, int dtype, hipStream_t s) {
+                         float* delta, Lay lde, int dtype, hipStream_t s, const GlobalSet* g) {
 #define NA_BWD(T, DD)                                                                                            \
     return launch_bwd<T, DD>(p, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl, dq, ldq, dk, ldk, dv, \
-                             ldv, delta, lde, s)
+                             ldv, delta, lde, g, s)
     if (dtype == NATTEN_BF16) {
         if (p.Dqk == 32) NA_BWD(bf16, 32);
         if (p.Dqk == 64) NA_BWD(bf16, 64);

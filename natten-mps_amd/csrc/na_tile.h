@@ -519,6 +519,39 @@ __device__ __forceinline__ void load_frags(const T* __restrict__ g, long long of
         f[ks] = valid ? *reinterpret_cast<const uint4*>(g + off + ks * 32 + grp * 8) : make_uint4(0, 0, 0, 0);
 }
 
+// Global keys, 32 at a time: rows j0 .. j0+31 of the keys and values of one
+// (batch, kv head) into the 32 slots of Xk / Xv, laid out and swizzled as a
+// staged union (slot = row - j0); rows past n load as zeros.  Each wave
+// instruction moves 512 / D rows; the workgroup's waves share them.
+template <typename T, int D>
+__device__ __forceinline__ void stage_global(const T* kb, int ks, const T* vb, int vs, int j0, int n, T* Xk, T* Xv,
+                                             int wave, int waves, int lane) {
+    constexpr int P = D / 8, R = 64 / P;
+    constexpr int E = static_cast<int>(sizeof(T));
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kb), static_cast<short>(0), kPlaneBytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vb), static_cast<short>(0), kPlaneBytes, 0x00020000);
+    const int l = lane / P;
+    for (int i = wave; i < 32 / R; i += waves) {
+        const int slot = i * R + l, j = j0 + slot;
+        const int piece16 = ((lane % P) ^ swz<D>(slot)) << 4;
+        const bool ok = j < n;
+        const uint32_t ok_k = ok ? static_cast<uint32_t>(j * ks * E + piece16) : kOutOfRange;
+        const uint32_t ok_v = ok ? static_cast<uint32_t>(j * vs * E + piece16) : kOutOfRange;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)(Xk + i * R * D), 16, ok_k, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void_t*)(Xv + i * R * D), 16, ok_v, 0, 0, 0);
+    }
+}
+
+// Score-MFMA accumulator input for a block of 32 global keys starting at j0:
+// 0 for the lane's slots (8 grp + e) that hold a key, -inf past n.
+__device__ __forceinline__ void global_bias(int j0, int n, int grp, f32x4_t (&bias)[2]) {
+    const int lim = n - j0 - 8 * grp;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bias[e >> 2][e & 3] = e < lim ? 0.f : -INFINITY;
+}
+
 // Store the lane's 4 consecutive head dims per 16-dim block (scaled).
 template <typename T, int D>
 __device__ __forceinline__ void store_rows(T* __restrict__ g, long long off, int grp, const f32x4_t (&acc)[D / 16],
@@ -616,6 +649,18 @@ __device__ __forceinline__ int slice_pos(const Prob& p, const Block& k, int u0) 
 // segment), and the exact recomputation after a walk reads it again from
 // there through the segment pointer -- so the walk holds none of the
 // pointers and layouts only the recomputation needs.
+// Global keys: extra tokens every query attends besides its neighbourhood
+// (the reference's additional_keys / additional_values), rows [B, n, Hkv,
+// D] with element strides; query head h reads kv head h / rep.  n == 0:
+// none.  Offsets inside one (batch, kv head) fit in 31 bits (host check).
+template <typename T>
+struct GlobalKeys {
+    const T *k, *v;
+    long long kb, kh, vb, vh;  // batch / head strides
+    int ks, vs;                // token strides
+    int n;
+};
+
 template <typename T>
 struct FwdArgs {
     Prob p;
@@ -625,6 +670,7 @@ struct FwdArgs {
     T* out;
     float* lse;
     LayK lq, lk, lv, lo, ll;
+    GlobalKeys<T> gk;
 };
 
 template <typename T>
@@ -637,6 +683,7 @@ struct BwdQArgs {
     T* dq;
     float* delta;
     LayK lq, lk, lv, lo, ldo, ll, ldl, ldq, lde;
+    GlobalKeys<T> gk;
 };
 
 template <typename T>

@@ -28,6 +28,10 @@ ENTRY_POINTS = (
     "natten_hip_forward",
     "natten_hip_backward",
     "natten_hip_backward_noalloc",
+    "natten_hip_global_supported",
+    "natten_hip_global_workspace",
+    "natten_hip_forward_global",
+    "natten_hip_backward_global",
     "natten_hip_qk_forward",
     "natten_hip_av_forward",
     "natten_hip_qk_backward",
@@ -83,6 +87,12 @@ _SIGNATURES = {
     "natten_hip_forward": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP], ctypes.c_int),
     "natten_hip_backward": ([_P(Problem)] + [_VP, _LP] * 11 + [_VP], ctypes.c_int),
     "natten_hip_backward_noalloc": ([_P(Problem)] + [_VP, _LP] * 10 + [_VP], ctypes.c_int),
+    "natten_hip_global_supported": ([_P(Problem), ctypes.c_int32, ctypes.c_int32], ctypes.c_int),
+    "natten_hip_global_workspace": ([_P(Problem), ctypes.c_int32], ctypes.c_int64),
+    "natten_hip_forward_global": ([_P(Problem)] + [_VP, _LP] * 5 + [ctypes.c_int32] + [_VP, _LP] * 2 + [_VP],
+                                  ctypes.c_int),
+    "natten_hip_backward_global": ([_P(Problem)] + [_VP, _LP] * 5 + [ctypes.c_int32] + [_VP, _LP] * 10
+                                   + [_VP, ctypes.c_int64, _VP], ctypes.c_int),
     "natten_hip_qk_forward": ([_P(Problem)] + [_VP, _LP] * 3 + [_VP], ctypes.c_int),
     "natten_hip_av_forward": ([_P(Problem)] + [_VP, _LP] * 3 + [_VP], ctypes.c_int),
     "natten_hip_qk_backward": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP], ctypes.c_int),
@@ -178,6 +188,17 @@ def layout(t: torch.Tensor, rank: int, trailing: int) -> Layout:
     sp = list(st[1:1 + rank])
     lay.axis[:] = [0] * (3 - rank) + sp
     lay.head = st[1 + rank]
+    return lay
+
+
+def token_layout(t: torch.Tensor) -> Layout:
+    """Strides of a ``[B, N, H, D]`` tensor of tokens (global keys): the token
+    stride goes in axis[2]."""
+    lay = Layout()
+    st = t.stride()
+    lay.batch = st[0]
+    lay.axis[:] = [0, 0, st[1]]
+    lay.head = st[2]
     return lay
 
 

@@ -39,6 +39,7 @@ from . import _lib
 # Functional-layer capability flags.
 NATIVE_GQA = True
 FUSED_LSE = True
+GLOBAL_KEYS = True  # additional_keys in the fused kernels (na{r}d_*_global hooks)
 
 
 _AVAILABLE = False
@@ -553,6 +554,96 @@ def rpb_av_backward(rank: int, d_out, attn, v, kernel_size, dilation):
 
 
 # ---------------------------------------------------------------------------
+# global keys (the reference's additional_keys / additional_values): extra
+# tokens [B, N, Hkv, D] that every query attends besides its neighbourhood,
+# inside the fused kernels (natten_hip_forward_global / _backward_global)
+# ---------------------------------------------------------------------------
+
+_GLOBAL_OK: dict = {}
+
+
+def global_supported(rank: int, q, k, v, n: int, kernel_size, stride, dilation, is_causal, backward: bool) -> bool:
+    """True when the fused kernels take these global keys (the MFMA tile path:
+    bf16/fp16, head dim 32/64/128 for q, k and v, stride 1, GPU tensors)."""
+    if (q.device.type != "cuda" or q.dtype not in (torch.float16, torch.bfloat16)
+            or not (q.dtype == k.dtype == v.dtype) or q.shape[-1] != v.shape[-1] or n < 1):
+        return False
+    key = (rank, q.dtype, q.shape, k.shape[-2], n, tuple(kernel_size), tuple(stride), tuple(dilation),
+           tuple(is_causal), bool(backward))
+    ok = _GLOBAL_OK.get(key)
+    if ok is None:
+        prob = _fused_problem(rank, q, k, v, kernel_size, stride, dilation, is_causal, 1.0)
+        ok = bool(_lib.load().natten_hip_global_supported(_byref(prob), int(n), int(bool(backward))))
+        if len(_GLOBAL_OK) >= _CACHE_MAX:
+            _GLOBAL_OK.clear()
+        _GLOBAL_OK[key] = ok
+    return ok
+
+
+def _check_global(q, k, gk, gv):
+    if gk.ndim != 4 or gv.ndim != 4 or gk.shape != gv.shape:
+        raise ValueError("global keys / values must both be [B, N, heads_kv, dim] with the same shape.")
+    if gk.shape[0] != q.shape[0] or gk.shape[2] != k.shape[-2] or gk.shape[3] != q.shape[-1]:
+        raise ValueError("global keys must match the batch, kv heads and head dim of the key tensor.")
+    _on_device(q, gk, gv)
+    _same_dtype(q, gk, gv)
+
+
+def forward_with_lse_global(rank: int, q, k, v, gk, gv, kernel_size, stride, dilation, is_causal, scale):
+    """(out, lse) of neighbourhood attention plus global keys: one softmax
+    over each query's window and the N global keys (lse fp32)."""
+    q, k, v, gk, gv = _inner(q), _inner(k), _inner(v), _inner(gk), _inner(gv)
+    _check_global(q, k, gk, gv)
+    scale_value = float(q.shape[-1] ** -0.5 if scale is None else scale)
+    sig = _fwd_sig(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_value)
+    out = torch.empty(sig.out_shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty(sig.lse_shape, dtype=torch.float32, device=q.device)
+    r = sig.refs[1]
+    lgk, lgv = _lib.token_layout(gk), _lib.token_layout(gv)
+    rc = _launch(q.device, _lib.load().natten_hip_forward_global, sig.prob_ref,
+                 q.data_ptr(), r[0], k.data_ptr(), r[1], v.data_ptr(), r[2], gk.data_ptr(), _byref(lgk),
+                 gv.data_ptr(), _byref(lgv), int(gk.shape[1]), out.data_ptr(), r[3], lse.data_ptr(), r[4],
+                 _raw_stream(q.device))
+    _lib.check(rc, "forward_global")
+    return out, lse
+
+
+def fused_backward_global(rank: int, d_out, q, k, v, gk, gv, out, lse, kernel_size, dilation, stride, is_causal,
+                          scale, d_lse=None):
+    """(dq, dk, dv, dgk, dgv) of forward_with_lse_global."""
+    q, k, v, out, d_out, gk, gv = (_inner(t) for t in (q, k, v, out, d_out, gk, gv))
+    _check_global(q, k, gk, gv)
+    if lse.dtype != torch.float32 or not lse.is_contiguous():
+        lse = lse.to(torch.float32).contiguous()
+    if d_lse is not None and (d_lse.dtype != torch.float32 or not d_lse.is_contiguous()):
+        d_lse = d_lse.to(torch.float32).contiguous()
+    scale_value = float(q.shape[-1] ** -0.5 if scale is None else scale)
+    sig = _bwd_sig(rank, d_out, q, k, v, out, lse, d_lse, kernel_size, stride, dilation, is_causal, scale_value)
+    lib = _lib.load()
+    n = int(gk.shape[1])
+    work_floats = int(lib.natten_hip_global_workspace(sig.prob_ref, n))
+    if work_floats < 0:
+        raise ValueError("natten_mps_amd: invalid problem for global keys.")
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    dgk = torch.empty(gk.shape, dtype=gk.dtype, device=gk.device)
+    dgv = torch.empty(gv.shape, dtype=gv.dtype, device=gv.device)
+    delta = torch.empty(sig.lse_shape, dtype=torch.float32, device=q.device)
+    work = torch.empty(max(work_floats, 1), dtype=torch.float32, device=q.device)
+    r = sig.refs[1]
+    T = lambda t: _byref(_lib.token_layout(t))  # noqa: E731
+    rc = _launch(q.device, lib.natten_hip_backward_global, sig.prob_ref,
+                 q.data_ptr(), r[0], k.data_ptr(), r[1], v.data_ptr(), r[2], gk.data_ptr(), T(gk),
+                 gv.data_ptr(), T(gv), n, out.data_ptr(), r[3], d_out.data_ptr(), r[4], lse.data_ptr(), r[5],
+                 d_lse.data_ptr() if d_lse is not None else None, r[6], dq.data_ptr(), r[7], dk.data_ptr(), r[8],
+                 dv.data_ptr(), r[9], dgk.data_ptr(), T(dgk), dgv.data_ptr(), T(dgv), delta.data_ptr(), r[10],
+                 work.data_ptr(), work_floats, _raw_stream(q.device))
+    _lib.check(rc, "backward_global")
+    return dq, dk, dv, dgk, dgv
+
+
+# ---------------------------------------------------------------------------
 # rank-specific names (the backend-module contract)
 # ---------------------------------------------------------------------------
 
@@ -590,7 +681,19 @@ def _bind(rank: int) -> None:
     def vbwd(d_out, q, k, v, out, lse, sizes, kernel_size, dilation, scale):
         return varlen_backward(rank, d_out, q, k, v, out, lse, sizes, kernel_size, dilation, scale)
 
+    def gsup(q, k, v, n, kernel_size, stride, dilation, is_causal, backward):
+        return global_supported(rank, q, k, v, n, kernel_size, stride, dilation, is_causal, backward)
+
+    def gfwd(q, k, v, gk, gv, kernel_size, stride, dilation, is_causal, scale):
+        return forward_with_lse_global(rank, q, k, v, gk, gv, kernel_size, stride, dilation, is_causal, scale)
+
+    def gbwd(d_out, q, k, v, gk, gv, out, lse, kernel_size, dilation, stride, is_causal, scale, d_lse=None):
+        return fused_backward_global(rank, d_out, q, k, v, gk, gv, out, lse, kernel_size, dilation, stride,
+                                     is_causal, scale, d_lse)
+
     for suffix, fn in (("forward", fwd), ("forward_with_lse", fwd_lse), ("fused_backward", fbwd),
+                       ("global_supported", gsup), ("forward_with_lse_global", gfwd),
+                       ("fused_backward_global", gbwd),
                        ("qk_forward", qk), ("av_forward", av), ("qk_backward", qkb), ("av_backward", avb),
                        ("varlen_forward", vfwd), ("varlen_forward_with_lse", vfwd_lse),
                        ("varlen_backward", vbwd)):

@@ -163,6 +163,43 @@ def create_na_lse_autograd_fn(rank: int) -> type:
     return _Fn
 
 
+def create_na_global_autograd_fn(rank: int) -> type:
+    """Fused NA over each query's window plus global keys (the reference's
+    ``additional_keys`` / ``additional_values``, ``functional.py:285-299``,
+    there a split pass, dense attention and a merge): ``apply(q, k, v, gk, gv,
+    kernel_size, stride, dilation, is_causal, scale) -> (out, lse)`` with one
+    softmax over both key sets; gradients flow to all five tensors, through
+    both outputs.  Needs a backend with the ``na{r}d_forward_with_lse_global``
+    and ``na{r}d_fused_backward_global`` hooks."""
+
+    class _Fn(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, q, k, v, gk, gv, kernel_size, stride, dilation, is_causal, scale):
+            mod = ops.active_module()
+            ctx.mod = mod
+            ctx.kernel_size, ctx.stride, ctx.dilation = kernel_size, stride, dilation
+            ctx.is_causal, ctx.scale = is_causal, scale
+            out, lse = getattr(mod, f"na{rank}d_forward_with_lse_global")(q, k, v, gk, gv, kernel_size, stride,
+                                                                          dilation, is_causal, scale)
+            ctx.save_for_backward(q, k, v, gk, gv, lse, out)
+            return out, lse
+
+        @staticmethod
+        def backward(ctx, grad_output, grad_lse):
+            q, k, v, gk, gv, lse, out = ctx.saved_tensors
+            scale_value = float(q.shape[-1] ** -0.5 if ctx.scale is None else ctx.scale)
+            if grad_output is None:
+                grad_output = torch.zeros_like(out)
+            grads = getattr(ctx.mod, f"na{rank}d_fused_backward_global")(
+                grad_output, q, k, v, gk, gv, out, lse, ctx.kernel_size, ctx.dilation, ctx.stride, ctx.is_causal,
+                scale_value, grad_lse)
+            return (*grads, None, None, None, None, None)
+
+    _Fn.__name__ = _Fn.__qualname__ = f"NeighborhoodAttention{rank}DGlobalFunction"
+    _Fn.__doc__ = f"Fused {rank}D neighborhood attention plus global keys, returning (out, lse)."
+    return _Fn
+
+
 def create_na_qk_autograd_fn(rank: int) -> type:
     """``apply(q, k, kernel_size, dilation, stride, is_causal, scale) -> logits``."""
 

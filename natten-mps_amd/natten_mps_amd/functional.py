@@ -10,6 +10,9 @@ composition:
   ``F.scaled_dot_product_attention`` (``:148-206``).
 * ``return_lse`` / ``additional_keys`` (``:285-299``): NA output and LSE, plus
   dense attention over the extra tokens, merged with ``merge_attentions``.
+  Backends that declare ``GLOBAL_KEYS`` take the extra tokens as global keys
+  inside their fused kernels (one softmax over each window and the extra
+  tokens, the same result) where their ``na{r}d_global_supported`` says so.
   Backends that declare ``FUSED_LSE`` produce the NA output and LSE in one
   fused pass (differentiable through both); others use the reference's
   split QK -> logsumexp/softmax -> AV composition.
@@ -205,6 +208,20 @@ def _na(rank, query, key, value, kernel_size, stride, dilation, is_causal, scale
         k_in, v_in = _repeat_kv(key, kv_repeat), _repeat_kv(value, kv_repeat)
     has_additional = add_k is not None
     ag = _AG[rank]
+
+    if has_additional and not pure and getattr(mod, "GLOBAL_KEYS", False):
+        # the extra tokens as global keys inside the fused kernels: one
+        # softmax over each window and the extra tokens, which is what the
+        # composition below computes (split NA + dense attention + merge)
+        gk, gv = (additional_keys, additional_values) if native_gqa else (add_k, add_v)
+        grads = torch.is_grad_enabled() and any(
+            t.requires_grad for t in (query, key, value, additional_keys, additional_values))
+        if (gk.dtype == query.dtype and gv.dtype == query.dtype
+                and getattr(mod, f"na{rank}d_global_supported")(query, k_in, v_in, gk.shape[1], ks, st, dil, causal,
+                                                               grads)):
+            fn = getattr(ag, f"NeighborhoodAttention{rank}DGlobalFunction")
+            out, lse = fn.apply(query, k_in, v_in, gk, gv, ks, st, dil, causal, scale_value)
+            return (out, lse) if return_lse else out
 
     if has_additional or return_lse:
         if getattr(mod, "FUSED_LSE", False) and not pure:

@@ -19,7 +19,7 @@ HEADER = os.path.join(ROOT, "include", "natten_hip.h")
 
 def _declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(natten_hip_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char \*)\s*(natten_hip_\w+)\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
