@@ -141,7 +141,7 @@ int natten_hip_backward(const natten_problem_t *p,
  * log-sum-exp.  gk / gv are [B, n_global, heads_kv, dim] (layout: batch,
  * head, and the token stride in axis[2]; axis[0], axis[1] unused).  These
  * entry points serve the MFMA tile path only (bf16/fp16, dim_qk == dim_v in
- * {32, 64, 128}, stride 1, aligned operands) and return
+ * {32, 64, 96, 128}, stride 1, aligned operands) and return
  * NATTEN_ERR_UNSUPPORTED otherwise; natten_hip_global_supported answers that
  * from the problem alone (1 / 0; backward != 0 also checks the backward).
  * The backward also writes dgk / dgv (summed over every query of each GQA

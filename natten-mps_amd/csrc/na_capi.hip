@@ -344,7 +344,7 @@ int natten_hip_forward_global(const natten_problem_t* p, const void* q, const na
     if (!global_eligible(P, p->dtype, vec, g, false) ||
         !na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(llse)}))
         return fail(NATTEN_ERR_UNSUPPORTED,
-                    "global keys run on the MFMA tile kernels only (bf16/fp16, head dim 32/64/128, stride 1, "
+                    "global keys run on the MFMA tile kernels only (bf16/fp16, head dim 32/64/96/128, stride 1, "
                     "aligned operands)");
     return launch_status(na::mfma_forward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), lse,
                                           to_lay(llse), p->dtype, static_cast<hipStream_t>(stream), &g),
@@ -386,7 +386,7 @@ int natten_hip_backward_global(const natten_problem_t* p, const void* q, const n
                                   to_lay(ldq), to_lay(ldk), to_lay(ldv), to_lay(ldelta)}) ||
         (dlse && !na::mfma_offsets_fit(P, {to_lay(ldlse)})))
         return fail(NATTEN_ERR_UNSUPPORTED,
-                    "global keys run on the MFMA tile kernels only (bf16/fp16, head dim 32/64/128, stride 1, "
+                    "global keys run on the MFMA tile kernels only (bf16/fp16, head dim 32/64/96/128, stride 1, "
                     "aligned operands)");
     const hipStream_t s = static_cast<hipStream_t>(stream);
     rc = launch_status(na::mfma_backward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout,

@@ -49,10 +49,10 @@ __device__ __forceinline__ int row_head_pos(const GlobalKvArgs<T>& a, int r, int
 
 template <typename T, int D>
 __global__ __launch_bounds__(64) void k_global_kv(GlobalKvArgs<T> a) {
-    constexpr int P = D / 8, R = 64 / P;
+    constexpr int LD = lds_dim<D>(), P = LD / 8, R = 64 / P;
     constexpr int E = static_cast<int>(sizeof(T));
-    __shared__ __attribute__((aligned(16))) T Qs[32 * D];
-    __shared__ __attribute__((aligned(16))) T Gs[32 * D];
+    __shared__ __attribute__((aligned(16))) T Qs[32 * LD];
+    __shared__ __attribute__((aligned(16))) T Gs[32 * LD];
     __shared__ __attribute__((aligned(16))) float NL[32];
     __shared__ __attribute__((aligned(16))) float ND[32];
     const Prob& p = a.p;
@@ -93,14 +93,14 @@ __global__ __launch_bounds__(64) void k_global_kv(GlobalKvArgs<T> a) {
             const int slot = i * R + lane / P, r = r0 + slot;
             int pos[3];
             const int h = hk * p.rep + row_head_pos(a, min(r, a.rows - 1), pos);
-            const int piece16 = ((lane % P) ^ swz<D>(slot)) << 4;
-            const bool ok = r < r_end;
+            const int piece16 = ((lane % P) ^ swz<LD>(slot)) << 4;
+            const bool ok = r < r_end && (piece16 >> 4) < D / 8;
             const int oq = h * static_cast<int>(a.lq.h) + vol_off(a.lq, pos);
             const int og = h * static_cast<int>(a.ldo.h) + vol_off(a.ldo, pos);
             const uint32_t vq = ok ? static_cast<uint32_t>(oq * E + piece16) : kOutOfRange;
             const uint32_t vg = ok ? static_cast<uint32_t>(og * E + piece16) : kOutOfRange;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void_t*)(Qs + i * R * D), 16, vq, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (lds_void_t*)(Gs + i * R * D), 16, vg, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void_t*)(Qs + i * R * LD), 16, vq, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (lds_void_t*)(Gs + i * R * LD), 16, vg, 0, 0, 0);
         }
         // per row: -lse * log2 e and -delta (-inf / 0 past the slice)
         if (lane < 32) {
@@ -240,7 +240,9 @@ hipError_t run_global_kv(const Prob& p, const void* q, Lay lq, const void* dout,
 }  // namespace
 
 bool mfma_global_key_ok(const Prob& p, int dtype, const GlobalSet& g) {
-    if (dtype == NATTEN_F32 || g.n < 1 || !(p.Dqk == 32 || p.Dqk == 64 || p.Dqk == 128) || p.Dqk != p.Dv) return false;
+    if (dtype == NATTEN_F32 || g.n < 1 || !(p.Dqk == 32 || p.Dqk == 64 || p.Dqk == 96 || p.Dqk == 128) ||
+        p.Dqk != p.Dv)
+        return false;
     for (const Lay* l : {&g.lk, &g.lv})
         if (l->b < 0 || l->h < 0 || l->s2 < 0 ||
             (static_cast<long long>(g.n) * l->s2 + 256) * 2 >= kPlaneBytes)
@@ -263,10 +265,12 @@ hipError_t mfma_global_key_backward(const Prob& p, const void* q, Lay lq, const 
     if (dtype == NATTEN_BF16) {
         if (p.Dqk == 32) NA_GKV(bf16, 32);
         if (p.Dqk == 64) NA_GKV(bf16, 64);
+        if (p.Dqk == 96) NA_GKV(bf16, 96);
         NA_GKV(bf16, 128);
     }
     if (p.Dqk == 32) NA_GKV(f16, 32);
     if (p.Dqk == 64) NA_GKV(f16, 64);
+    if (p.Dqk == 96) NA_GKV(f16, 96);
     NA_GKV(f16, 128);
 #undef NA_GKV
 }

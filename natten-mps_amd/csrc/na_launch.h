@@ -81,7 +81,8 @@ struct GlobalSet {
     int n;
 };
 
-// MFMA tile path (na_mfma.hip): bf16/fp16, stride 1, equal head dims 32/64/128.
+// MFMA tile path (na_mfma.hip): bf16/fp16, stride 1, equal head dims 32/64/96/128
+// (96 stored as 128-wide LDS rows).
 // mfma_static_lds_ok: no tile kernel instance declares static LDS (checked
 // once per process); mfma_lds_audit returns 1 when so, 0 otherwise, and the
 // number of instances whose attributes were read.

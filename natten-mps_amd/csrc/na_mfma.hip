@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfm
     unsigned char* smem = lds_base();
     constexpr bool KEY_SIDE = false;
     T* Ks = reinterpret_cast<T*>(smem);
-    T* Vs = Ks + ts.slots * D;
+    T* Vs = Ks + ts.slots * lds_dim<D>();
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
     Block blk;
@@ -199,8 +199,8 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfm
                 const int hk = kv_head(ts, h);
                 const T* gkb = g.k + b * g.kb + hk * g.kh;
                 const T* gvb = g.v + b * g.vb + hk * g.vh;
-                T* Xk = Vs + ts.slots * D;
-                T* Xv = Xk + 32 * D;
+                T* Xk = Vs + ts.slots * lds_dim<D>();
+                T* Xv = Xk + 32 * lds_dim<D>();
                 for (int j0 = 0; j0 < g.n; j0 += 32) {
                     stage_global<T, D>(gkb, g.ks, gvb, g.vs, j0, g.n, Xk, Xv, wave, ts.waves, lane);
                     wait_loads();
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_
     unsigned char* smem = lds_base();
     constexpr bool KEY_SIDE = false;
     T* Ks = reinterpret_cast<T*>(smem);
-    T* Vs = Ks + ts.slots * D;
+    T* Vs = Ks + ts.slots * lds_dim<D>();
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
     Block blk;
@@ -388,8 +388,8 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_
                 const int hk = kv_head(ts, h);
                 const T* gkb = g.k + b * g.kb + hk * g.kh;
                 const T* gvb = g.v + b * g.vb + hk * g.vh;
-                T* Xk = Vs + ts.slots * D;
-                T* Xv = Xk + 32 * D;
+                T* Xk = Vs + ts.slots * lds_dim<D>();
+                T* Xv = Xk + 32 * lds_dim<D>();
                 for (int j0 = 0; j0 < g.n; j0 += 32) {
                     stage_global<T, D>(gkb, g.ks, gvb, g.vs, j0, g.n, Xk, Xv, wave, ts.waves, lane);
                     wait_loads();
@@ -510,8 +510,8 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_k
     constexpr bool KEY_SIDE = true;
     const int slots = ts.slots;
     T* Qs = reinterpret_cast<T*>(smem);
-    T* Gs = Qs + slots * D;
-    float* NL = reinterpret_cast<float*>(Gs + slots * D);  // slots + 8
+    T* Gs = Qs + slots * lds_dim<D>();
+    float* NL = reinterpret_cast<float*>(Gs + slots * lds_dim<D>());  // slots + 8
     float* ND = NL + slots + 8;                            // slots
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
@@ -1064,7 +1064,7 @@ constexpr size_t kLdsBudget = 64 * 1024;
 
 // Staged operands (split kernels: one; their row blocks come on top).
 size_t lds_bytes(Kind kind, int slots, int D) {
-    const size_t rows = static_cast<size_t>(slots) * D * 2;
+    const size_t rows = static_cast<size_t>(slots) * (D == 96 ? 128 : D) * 2;
     if (kind == kSplit || kind == kSplitKey) return kLdsPad + rows;
     return kLdsPad + (kind == kBackwardKV ? 2 * rows + (2 * static_cast<size_t>(slots) + 8) * 4 : 2 * rows);
 }
@@ -1078,7 +1078,7 @@ void set_h_per(TileShape& ts, int per) {
 // extents, innermost axis first (8 wide unless the problem is 1-D); halved
 // until the staged union fits the LDS budget.
 // LDS a forward / dQ workgroup adds for global keys: 32 key and 32 value rows.
-size_t global_lds(int D) { return static_cast<size_t>(2 * 32) * D * 2; }
+size_t global_lds(int D) { return static_cast<size_t>(2 * 32) * (D == 96 ? 128 : D) * 2; }
 
 bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts, size_t extra_lds = 0) {
     int n[3];
@@ -1517,9 +1517,24 @@ void audit_dim(LdsAudit& a) {
     audit_one(k_wsum_key_mfma<T, D, false>, "k_wsum_key_mfma", a);
 }
 
+// Head dim 96 has fused instances only (the split ops keep the vector
+// kernels there).
+template <typename T>
+void audit_dim96(LdsAudit& a) {
+    audit_one(k_fwd_mfma<T, 96, kLayGeneral, false, true>, "k_fwd_mfma (global keys)", a);
+    audit_one(k_fwd_mfma<T, 96, kLayGeneral, true, true>, "k_fwd_mfma (wide, global keys)", a);
+    audit_one(k_bwd_q_mfma<T, 96, kLayGeneral, false, true>, "k_bwd_q_mfma (global keys)", a);
+    audit_one(k_bwd_q_mfma<T, 96, kLayGeneral, true, true>, "k_bwd_q_mfma (wide, global keys)", a);
+    audit_fused<T, 96, kLayGeneral>(a);
+    audit_fused<T, 96, kLayOne>(a);
+    audit_fused<T, 96, kLayTwo>(a);
+}
+
 const LdsAudit& lds_audit() {
     static const LdsAudit result = [] {
         LdsAudit a;
+        audit_dim96<bf16>(a);
+        audit_dim96<f16>(a);
         audit_dim<bf16, 32>(a);
         audit_dim<bf16, 64>(a);
         audit_dim<bf16, 128>(a);
@@ -1612,7 +1627,7 @@ hipError_t mfma_split_wsum(const char* name, const Prob& p, int D, const void* w
 
 bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward, bool global) {
     if (dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f) || !mfma_static_lds_ok()) return false;
-    if (p.Dqk != p.Dv || !(D == 32 || D == 64 || D == 128)) return false;
+    if (p.Dqk != p.Dv || !(D == 32 || D == 64 || D == 96 || D == 128)) return false;
     for (int a = 0; a < 3; ++a)
         if (p.ax[a].st != 1) return false;
     // tile indices (the launch grid) stay in 31 bits
@@ -1634,10 +1649,12 @@ hipError_t mfma_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay
     if (dtype == NATTEN_BF16) {
         if (p.Dqk == 32) NA_FWD(bf16, 32);
         if (p.Dqk == 64) NA_FWD(bf16, 64);
+        if (p.Dqk == 96) NA_FWD(bf16, 96);
         NA_FWD(bf16, 128);
     }
     if (p.Dqk == 32) NA_FWD(f16, 32);
     if (p.Dqk == 64) NA_FWD(f16, 64);
+    if (p.Dqk == 96) NA_FWD(f16, 96);
     NA_FWD(f16, 128);
 #undef NA_FWD
 }
@@ -1652,10 +1669,12 @@ hipError_t mfma_backward(const Prob& p, const void* q, Lay lq, const void* k, La
     if (dtype == NATTEN_BF16) {
         if (p.Dqk == 32) NA_BWD(bf16, 32);
         if (p.Dqk == 64) NA_BWD(bf16, 64);
+        if (p.Dqk == 96) NA_BWD(bf16, 96);
         NA_BWD(bf16, 128);
     }
     if (p.Dqk == 32) NA_BWD(f16, 32);
     if (p.Dqk == 64) NA_BWD(f16, 64);
+    if (p.Dqk == 96) NA_BWD(f16, 96);
     NA_BWD(f16, 128);
 #undef NA_BWD
 }

@@ -138,6 +138,14 @@ __host__ __device__ constexpr int swz(int row) {
 // Staging moves R = 64 / (D/8) rows per wave instruction; the swizzle of row
 // iR + l (l < R) splits into disjoint bits of i and of l, so the lane part of
 // the LDS/global offsets is fixed for a whole tile.
+// Elements per LDS row for head dim D: 96 is stored as 128 (the last four
+// 16-byte pieces stay unread), so that rows keep a power-of-two number of
+// pieces and every lane layout and swizzle of head dim 128 applies.
+template <int D>
+__host__ __device__ constexpr int lds_dim() {
+    return D == 96 ? 128 : D;
+}
+
 template <int D>
 constexpr bool swz_splits() {
     constexpr int R = 64 / (D / 8);
@@ -424,7 +432,7 @@ struct StageMap {
 template <typename T, int D>
 __device__ __forceinline__ StageMap stage_map(const Prob& p, const TileShape& ts, const LayK& la, const LayK& lb,
                                               int lane) {
-    constexpr int P = D / 8;
+    constexpr int P = lds_dim<D>() / 8;
     StageMap m;
     const int l = lane / P;
     m.lrow = l >> ts.rowshift;
@@ -432,7 +440,7 @@ __device__ __forceinline__ StageMap stage_map(const Prob& p, const TileShape& ts
     const int d1 = p.ax[1].dil, d2 = p.ax[2].dil;
     m.lane_a = (m.lrow * d1 * la.s1 + m.lcol * d2 * la.s2) * static_cast<int>(sizeof(T));
     m.lane_b = (m.lrow * d1 * lb.s1 + m.lcol * d2 * lb.s2) * static_cast<int>(sizeof(T));
-    m.kb16 = ((lane % P) ^ swz<D>(l)) << 4;
+    m.kb16 = ((lane % P) ^ swz<lds_dim<D>()>(l)) << 4;
     return m;
 }
 
@@ -440,7 +448,7 @@ template <typename T, int D, bool PAIR = true>
 __device__ __forceinline__ void stage_pair(const Prob& p, const Block& k, const TileShape& ts, const StageMap& m,
                                            const T* plane_a, const LayK& la, T* Xa, const T* plane_b, const LayK& lb,
                                            T* Xb, int wave) {
-    constexpr int R = 64 / (D / 8);
+    constexpr int LD = lds_dim<D>(), R = 64 / (LD / 8);
     const __amdgpu_buffer_rsrc_t ra =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(plane_a), static_cast<short>(0), kPlaneBytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t rb =
@@ -456,16 +464,19 @@ __device__ __forceinline__ void stage_pair(const Prob& p, const Block& k, const 
         const int r1 = c1 + irow * d1, r2 = c2 + icol * d2;
         const int sa = __builtin_amdgcn_readfirstlane((r1 * la.s1 + r2 * la.s2) * E);
         const int sb = __builtin_amdgcn_readfirstlane((r1 * lb.s1 + r2 * lb.s2) * E);
-        const int kbh = __builtin_amdgcn_readfirstlane(swz<D>(i * R) << 4);
+        const int kbh = __builtin_amdgcn_readfirstlane(swz<LD>(i * R) << 4);
         const int lim_r = __builtin_amdgcn_readfirstlane(k.U[1] - irow);
         const int lim_c = __builtin_amdgcn_readfirstlane(k.U[2] - icol);
         const int kb = m.kb16 ^ kbh;
         // out-of-union slots: set bit 31, past the buffer range (offsets < 2^31)
-        const uint32_t bad = (m.lrow < lim_r && m.lcol < lim_c) ? 0u : kOutOfRange;
+        // (head dim 96: the pieces past the row's 12 are padding, not loaded)
+        const uint32_t bad = ((m.lrow < lim_r && m.lcol < lim_c && (LD == D || (kb >> 4) < D / 8)) ? 0u
+                                                                                                  : kOutOfRange);
         const uint32_t oa = static_cast<uint32_t>(sa + m.lane_a + kb) | bad;
         const uint32_t ob = static_cast<uint32_t>(sb + m.lane_b + kb) | bad;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(Xa + i * R * D), 16, oa, 0, 0, 0);
-        if constexpr (PAIR) __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(Xb + i * R * D), 16, ob, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(Xa + i * R * LD), 16, oa, 0, 0, 0);
+        if constexpr (PAIR)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(Xb + i * R * LD), 16, ob, 0, 0, 0);
     }
 }
 
@@ -481,8 +492,8 @@ __device__ __forceinline__ void score_chunk(const T* X, int c, int col, int grp,
         f32x4_t acc = bias[b];
 #pragma unroll
         for (int ks = 0; ks < D / 32; ++ks) {
-            const int kb = (ks * 4 + grp) ^ swz<D>(row);
-            const uint4 a = *reinterpret_cast<const uint4*>(X + row * D + kb * 8);
+            const int kb = (ks * 4 + grp) ^ swz<lds_dim<D>()>(row);
+            const uint4 a = *reinterpret_cast<const uint4*>(X + row * lds_dim<D>() + kb * 8);
             acc = Mma<T>::run(a, frag[ks], acc);
         }
         out[b] = acc;
@@ -502,8 +513,9 @@ __device__ __forceinline__ void accumulate_chunk(const T* X, int c, int lane, ui
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
         const int kb = 2 * db + ((j & 3) >> 1);
-        const T* a0 = X + r0 * D + ((kb ^ swz<D>(r0)) * 8) + sub;
-        const T* a1 = X + r1 * D + ((kb ^ swz<D>(r1)) * 8) + sub;
+        constexpr int LD = lds_dim<D>();
+        const T* a0 = X + r0 * LD + ((kb ^ swz<LD>(r0)) * 8) + sub;
+        const T* a1 = X + r1 * LD + ((kb ^ swz<LD>(r1)) * 8) + sub;
         const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)a0);
         const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)a1);
         const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
@@ -526,7 +538,7 @@ __device__ __forceinline__ void load_frags(const T* __restrict__ g, long long of
 template <typename T, int D>
 __device__ __forceinline__ void stage_global(const T* kb, int ks, const T* vb, int vs, int j0, int n, T* Xk, T* Xv,
                                              int wave, int waves, int lane) {
-    constexpr int P = D / 8, R = 64 / P;
+    constexpr int LD = lds_dim<D>(), P = LD / 8, R = 64 / P;
     constexpr int E = static_cast<int>(sizeof(T));
     const __amdgpu_buffer_rsrc_t rk =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kb), static_cast<short>(0), kPlaneBytes, 0x00020000);
@@ -535,12 +547,12 @@ __device__ __forceinline__ void stage_global(const T* kb, int ks, const T* vb, i
     const int l = lane / P;
     for (int i = wave; i < 32 / R; i += waves) {
         const int slot = i * R + l, j = j0 + slot;
-        const int piece16 = ((lane % P) ^ swz<D>(slot)) << 4;
-        const bool ok = j < n;
+        const int piece16 = ((lane % P) ^ swz<LD>(slot)) << 4;
+        const bool ok = j < n && (piece16 >> 4) < D / 8;
         const uint32_t ok_k = ok ? static_cast<uint32_t>(j * ks * E + piece16) : kOutOfRange;
         const uint32_t ok_v = ok ? static_cast<uint32_t>(j * vs * E + piece16) : kOutOfRange;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)(Xk + i * R * D), 16, ok_k, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void_t*)(Xv + i * R * D), 16, ok_v, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)(Xk + i * R * LD), 16, ok_k, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void_t*)(Xv + i * R * LD), 16, ok_v, 0, 0, 0);
     }
 }
 

@@ -564,7 +564,7 @@ _GLOBAL_OK: dict = {}
 
 def global_supported(rank: int, q, k, v, n: int, kernel_size, stride, dilation, is_causal, backward: bool) -> bool:
     """True when the fused kernels take these global keys (the MFMA tile path:
-    bf16/fp16, head dim 32/64/128 for q, k and v, stride 1, GPU tensors)."""
+    bf16/fp16, head dim 32/64/96/128 for q, k and v, stride 1, GPU tensors)."""
     if (q.device.type != "cuda" or q.dtype not in (torch.float16, torch.bfloat16)
             or not (q.dtype == k.dtype == v.dtype) or q.shape[-1] != v.shape[-1] or n < 1):
         return False

@@ -31,6 +31,7 @@ CASES = [
     (2, (16, 16), 2, 2, 128, 3, (1, 1), (False, False), 32, torch.bfloat16),
     (2, (12, 12), 2, 1, 32, 5, (1, 1), (False, False), 5, torch.float16),
     (1, (300,), 4, 4, 32, 33, (1,), (False,), 64, torch.bfloat16),
+    (2, (10, 11), 2, 2, 96, 3, (1, 1), (False, False), 7, torch.bfloat16),
 ]
 
 

@@ -120,6 +120,10 @@ FUSED = [
     (2, (24, 24), 2, 2, 32, (7, 7), (1, 1), (3, 3), (False, True), None),
     (3, (6, 9, 10), 2, 2, 32, (3, 3, 5), (1, 1, 1), (2, 1, 1), (False, True, False), None),
     (3, (5, 12, 12), 4, 2, 64, (3, 5, 5), (1, 1, 1), (1, 2, 2), (False, False, False), None),
+    # head dim 96 (MFMA tiles with rows padded to 128 in LDS for fp16/bf16)
+    (2, (12, 13), 2, 2, 96, (5, 3), (1, 1), (1, 2), (False, True), None),
+    (1, (60,), 4, 2, 96, (7,), (1,), (2,), (True,), 0.25),
+    (3, (5, 6, 7), 2, 2, 96, (3, 3, 3), (1, 1, 1), (1, 2, 1), (False, False, False), None),
 ]
 
 
