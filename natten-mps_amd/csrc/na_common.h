@@ -131,8 +131,13 @@ __host__ __device__ inline int fdiv(int n, const FastDiv& f) {
 //   non-causal:  ws(j) = 0 for j < h;  B for j + h >= n;  j - h otherwise,
 // with B = n - 1 - 2h when d == 1 or r < L % d, and B = n - K otherwise (the
 // two agree for odd K).  No divisions: kernels evaluate it per lane.
+//
+// Queries: with stride s (the tile kernels take s > 1 only with d == 1, so
+// the axis is one class) the query items t = 0 .. ceil(n/s)-1 sit at class
+// coordinates qs*t, qs = s; with s == 1 items and class coordinates agree.
 struct ClassAxis {
     int n, K, h, B, causal;
+    int qs;  // query step
 };
 
 __host__ __device__ inline ClassAxis class_axis(const Axis& a, int r) {
@@ -142,6 +147,7 @@ __host__ __device__ inline ClassAxis class_axis(const Axis& a, int r) {
     c.h = a.k / 2;
     c.causal = a.causal;
     c.B = (a.dil == 1 || r < a.len % a.dil) ? c.n - 1 - 2 * c.h : c.n - a.k;
+    c.qs = a.st;
     return c;
 }
 
@@ -171,14 +177,31 @@ __host__ __device__ inline void class_span(const ClassAxis& c, int u, int& jlo, 
         jlo = c.B >= v ? c.n - c.h : c.n;
 }
 
-// Admissible box of a query (its window) or key (its attending queries) in
-// class coordinates.
+// Window start of query item t.
+__host__ __device__ inline int query_ws(const ClassAxis& c, int t) { return class_ws(c, c.qs * t); }
+
+// Query items [tlo, thi] whose windows hold key u (empty when tlo > thi): the
+// class span's members at multiples of qs.  The span lies in [0, n], so
+// thi <= (n-1)/qs, the last item.
+__host__ __device__ inline void query_span(const ClassAxis& c, int u, int& tlo, int& thi) {
+    class_span(c, u, tlo, thi);
+    if (c.qs != 1) {
+        tlo = (tlo + c.qs - 1) / c.qs;
+        thi = thi / c.qs;
+    }
+}
+
+// Query items on an axis: ceil(n/qs), which is the axis's output extent.
+__host__ __device__ inline int query_items(const Axis& a, int n) { return a.st == 1 ? n : a.out; }
+
+// Admissible box of a query item (its window) or key (its attending query
+// items) in class coordinates.
 __host__ __device__ inline void item_box(const ClassAxis& c, int j, bool key_side, int& lo, int& hi) {
     if (!key_side) {
-        lo = class_ws(c, j);
+        lo = query_ws(c, j);
         hi = lo + c.K - 1;
     } else {
-        class_span(c, j, lo, hi);
+        query_span(c, j, lo, hi);
     }
 }
 
@@ -194,8 +217,8 @@ struct AxisGeo {
     int J, E, lo, U, n, B, glo, ghi, tile_ok, wave_ok;
 };
 
-__host__ __device__ inline AxisGeo axis_geometry(int len, int K, int dil, int causal, int lenmod, int T, int t,
-                                                 int r, int wl, int wh, bool key, const FastDiv& fd) {
+__host__ __device__ inline AxisGeo axis_geometry(int len, int K, int dil, int causal, int lenmod, int st, int out,
+                                                 int T, int t, int r, int wl, int wh, bool key, const FastDiv& fd) {
     AxisGeo o;
     ClassAxis c;
     c.n = dil == 1 ? len : fdiv(len - r + dil - 1, fd);
@@ -203,22 +226,23 @@ __host__ __device__ inline AxisGeo axis_geometry(int len, int K, int dil, int ca
     c.h = K >> 1;
     c.causal = causal;
     c.B = (dil == 1 || r < lenmod) ? c.n - 1 - 2 * c.h : c.n - K;
+    c.qs = st;
     o.n = c.n;
     o.B = c.B;
     o.J = t * T;
-    const int jend = imin(o.J + T, c.n) - 1;
+    const int jend = imin(o.J + T, key || st == 1 ? c.n : out) - 1;
     o.E = jend - o.J + 1;
     int lo, hi;
     if (!key) {
-        lo = imax(class_ws(c, o.J), 0);
-        hi = imin(class_ws(c, jend) + K - 1, c.n - 1);
+        lo = imax(query_ws(c, o.J), 0);
+        hi = imin(query_ws(c, jend) + K - 1, c.n - 1);
     } else {
         // both span ends are non-decreasing in the key; keys attended by
-        // nobody (only past the last window at an even-kernel border) sit
-        // at the end and leave hi unchanged
+        // nobody (past the last window at an even-kernel border, or at the
+        // end of a strided axis) leave hi unchanged
         int x2;
-        class_span(c, o.J, lo, x2);
-        class_span(c, jend, x2, hi);
+        query_span(c, o.J, lo, x2);
+        query_span(c, jend, x2, hi);
     }
     o.lo = lo;
     o.U = hi >= lo ? hi - lo + 1 : 0;

@@ -68,7 +68,8 @@ struct Strides3 {
 };
 
 // One axis of an item in residue-class form: residue r, class coordinate j,
-// and the class's window rule.
+// and the class's window rule.  A query item's j is its item index (the
+// output index on a strided axis, which is one class).
 struct ExactAxis {
     int r, j, dil;
     ClassAxis c;
@@ -87,7 +88,7 @@ __device__ __forceinline__ ExactAxis exact_axis(const Axis& A, int pos) {
 // (e: kernel index, row-major over the axes).
 template <class F>
 __device__ __forceinline__ void exact_window(const ExactAxis (&x)[3], F&& f) {
-    const int w0 = class_ws(x[0].c, x[0].j), w1 = class_ws(x[1].c, x[1].j), w2 = class_ws(x[2].c, x[2].j);
+    const int w0 = query_ws(x[0].c, x[0].j), w1 = query_ws(x[1].c, x[1].j), w2 = query_ws(x[2].c, x[2].j);
     const int K0 = x[0].c.K, K1 = x[1].c.K, K2 = x[2].c.K;
 #pragma unroll 1
     for (int a = 0; a < K0; ++a) {
@@ -106,24 +107,25 @@ __device__ __forceinline__ void exact_window(const ExactAxis (&x)[3], F&& f) {
     }
 }
 
-// f(i0, i1, i2, e) over the queries (stride 1: query = output position)
-// whose window holds the key whose axes are x, as their neighbour e.
+// f(i0, i1, i2, e) over the query items whose window holds the key whose
+// axes are x, as their neighbour e; i is the item's output index (its
+// position at stride 1).
 template <class F>
 __device__ __forceinline__ void exact_attending(const ExactAxis (&x)[3], F&& f) {
     int l0, h0, l1, h1, l2, h2;
-    class_span(x[0].c, x[0].j, l0, h0);
-    class_span(x[1].c, x[1].j, l1, h1);
-    class_span(x[2].c, x[2].j, l2, h2);
+    query_span(x[0].c, x[0].j, l0, h0);
+    query_span(x[1].c, x[1].j, l1, h1);
+    query_span(x[2].c, x[2].j, l2, h2);
     const int K1 = x[1].c.K, K2 = x[2].c.K;
 #pragma unroll 1
     for (int a = l0; a <= h0; ++a) {
-        const int i0 = x[0].r + a * x[0].dil, e0 = x[0].j - class_ws(x[0].c, a);
+        const int i0 = x[0].r + a * x[0].dil, e0 = x[0].j - query_ws(x[0].c, a);
 #pragma unroll 1
         for (int b = l1; b <= h1; ++b) {
-            const int i1 = x[1].r + b * x[1].dil, e1 = x[1].j - class_ws(x[1].c, b);
+            const int i1 = x[1].r + b * x[1].dil, e1 = x[1].j - query_ws(x[1].c, b);
 #pragma unroll 1
             for (int c = l2; c <= h2; ++c)
-                f(i0, i1, x[2].r + c * x[2].dil, (e0 * K1 + e1) * K2 + x[2].j - class_ws(x[2].c, c));
+                f(i0, i1, x[2].r + c * x[2].dil, (e0 * K1 + e1) * K2 + x[2].j - query_ws(x[2].c, c));
         }
     }
 }

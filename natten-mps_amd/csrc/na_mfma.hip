@@ -69,7 +69,7 @@ __device__ __forceinline__ void redo_fwd(const void* kargs, int wg, int wave, in
     const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
     const LayK &ao = LAY == kLayGeneral ? A.lo : aq, &al = A.ll;
     int b, h0, h1, pos[3];
-    if (!lane_position(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    if (!lane_position<false>(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
     ExactAxis x[3];
     for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
     f32x4_t acc[D / 16];
@@ -257,7 +257,7 @@ __device__ __forceinline__ void redo_bwd_q(const void* kargs, int wg, int wave, 
     const LayK &ao = LAY == kLayGeneral ? A.lo : aq, &ado = LAY == kLayGeneral ? A.ldo : aq;
     const LayK &adq = LAY == kLayGeneral ? A.ldq : aq, &al = A.ll, &adl = LAY == kLayGeneral ? A.ldl : al;
     int b, h0, h1, pos[3];
-    if (!lane_position(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    if (!lane_position<false>(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
     ExactAxis x[3];
     for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
     f32x4_t acc[D / 16];
@@ -458,7 +458,7 @@ __device__ __forceinline__ void redo_bwd_kv(const void* kargs, int wg, int wave,
     const LayK& adv = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.ldv;
     const LayK &ado = LAY == kLayGeneral ? A.ldo : aq, &al = A.ll, &ade = LAY == kLayGeneral ? A.lde : al;
     int b, h0, h1, pos[3];
-    if (!lane_position(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    if (!lane_position<true>(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
     ExactAxis x[3];
     for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
     f32x4_t g[D / 16];
@@ -518,6 +518,17 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_k
     Block blk;
     WaveGeo wg;
     if (!tile_geometry<KEY_SIDE>(p, ts, geo, wave, blk, wg)) return;
+    const Lane ln = lane_item(p, ts, blk, wave, col, true);
+    if (empty_union(blk)) {
+        f32x4_t z[D / 16];
+        exact_zero(z);
+        if (ln.valid)
+            for (int hk = blk.h0; hk < blk.h1; ++hk) {
+                store_rows<T, D>(bh_ptr(dk, ldk, blk.b, hk), vol_off(ldk, ln.pos), grp, z, 1.f);
+                store_rows<T, D>(bh_ptr(dv, ldv, blk.b, hk), vol_off(ldv, ln.pos), grp, z, 1.f);
+            }
+        return;
+    }
     const int rep = static_cast<int>(ts.rep.d);
     const StageMap sm = stage_map<T, D>(p, ts, lq, ldo, lane);
     // the walk runs over (batch, kv head, q head of the group, slice): its
@@ -528,7 +539,6 @@ __global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_k
     stage_pair<T, D>(p, blk, ts, sm, plane_of(q, lq, w.b, w.h * rep, slice_pos(p, blk, 0)), lq, Qs,
                      plane_of(dout, ldo, w.b, w.h * rep, slice_pos(p, blk, 0)), ldo, Gs, wave);
     if (threadIdx.x < 8) NL[slots + threadIdx.x] = -INFINITY;
-    const Lane ln = lane_item(p, ts, blk, wave, col, true);
     const float sc2 = p.scale * kLog2e;
     f32x4_t cb[2];
     if constexpr (!WIDE) column_bias(ln, ts.rowshift, 0, grp, cb);
@@ -758,7 +768,7 @@ __device__ __forceinline__ void redo_wsum(const void* kargs, int wg, int wave, i
     const WsumArgs<T>& A = *static_cast<const WsumArgs<T>*>(kargs);
     const LayK &aw = A.lw, &ax = A.lx, &ao = SAME ? ax : A.lo;
     int b, h0, h1, pos[3];
-    if (!lane_position(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    if (!lane_position<false>(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
     ExactAxis x[3];
     for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
     f32x4_t acc[D / 16];
@@ -937,7 +947,7 @@ __device__ __forceinline__ void redo_wsum_key(const void* kargs, int wg, int wav
     const WsumArgs<T>& A = *static_cast<const WsumArgs<T>*>(kargs);
     const LayK &aw = A.lw, &ax = A.lx, &ao = SAME ? ax : A.lo;
     int b, h0, h1, pos[3];
-    if (!lane_position(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    if (!lane_position<true>(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
     ExactAxis x[3];
     for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
     f32x4_t acc[D / 16];
@@ -969,10 +979,18 @@ __global__ __launch_bounds__(256) void k_wsum_key_mfma(WsumArgs<T> args) {
     Block blk;
     WaveGeo wg;
     if (!tile_geometry<true>(p, ts, geo, wave, blk, wg)) return;
+    const Lane ln = lane_item(p, ts, blk, wave, col, true);
+    if (empty_union(blk)) {
+        f32x4_t z[D / 16];
+        exact_zero(z);
+        if (ln.valid)
+            for (int h = blk.h0; h < blk.h1; ++h)
+                store_rows<T, D>(bh_ptr(out, lo, blk.b, h), vol_off(lo, ln.pos), grp, z, 1.f);
+        return;
+    }
     const StageMap sm = stage_map<T, D>(p, ts, lx, lx, lane);
     Walk w;
     walk_start(blk, w);
-    const Lane ln = lane_item(p, ts, blk, wave, col, true);
     int keylin;
     {
         const int f = wave * 16 + col, s2 = ts.tshift[2], s1 = ts.tshift[1];
@@ -1061,6 +1079,11 @@ constexpr size_t kSplitRowsBudget = 48 * 1024;
 constexpr size_t kSplitKeyLds = 128 * 1024;
 
 constexpr size_t kLdsBudget = 64 * 1024;
+// A problem whose staged union does not fit kLdsBudget even at 16 items
+// (head dim 96/128 with wide unions: strided axes, long kernels near the
+// borders) takes a tile of up to kLdsBudgetLarge: fewer workgroups per CU,
+// still the matrix cores.
+constexpr size_t kLdsBudgetLarge = 128 * 1024;
 
 // Staged operands (split kernels: one; their row blocks come on top).
 size_t lds_bytes(Kind kind, int slots, int D) {
@@ -1074,50 +1097,53 @@ void set_h_per(TileShape& ts, int per) {
     ts.hchunks = make_fastdiv(static_cast<uint32_t>((ts.nheads + per - 1) / per));
 }
 
-// Workgroup box in class coordinates: up to 64 items (4 waves), power-of-two
-// extents, innermost axis first (8 wide unless the problem is 1-D); halved
-// until the staged union fits the LDS budget.
 // LDS a forward / dQ workgroup adds for global keys: 32 key and 32 value rows.
 size_t global_lds(int D) { return static_cast<size_t>(2 * 32) * (D == 96 ? 128 : D) * 2; }
 
+// Workgroup box in class coordinates (query items on a strided axis): up to
+// 64 items (4 waves), power-of-two extents, innermost axis first (8 wide
+// unless the problem is 1-D); halved until the staged union fits the LDS
+// budget, kLdsBudget first, then kLdsBudgetLarge.
 bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts, size_t extra_lds = 0) {
-    int n[3];
-    for (int a = 0; a < 3; ++a) n[a] = n_class_h(p.ax[a], 0);  // class 0 is the longest
-    for (int items = kMaxItems; items >= 16; items /= 2) {
-        if (n[0] == 1 && n[1] == 1) {
-            ts.T[2] = std::min(pow2_at_least(n[2]), items);
-            ts.T[1] = ts.T[0] = 1;
-        } else {
-            ts.T[2] = std::min(pow2_at_least(n[2]), 8);
-            ts.T[1] = std::min(pow2_at_least(n[1]), std::max(items / ts.T[2], 1));
-            ts.T[0] = std::min(pow2_at_least(n[0]), std::max(items / (ts.T[2] * ts.T[1]), 1));
-        }
-        for (int a = 0; a < 3; ++a) {
-            ts.tshift[a] = log2_of(ts.T[a]);
-            ts.ntile[a] = (n[a] + ts.T[a] - 1) / ts.T[a];
-        }
-        const int cnt = ts.T[0] * ts.T[1] * ts.T[2];
-        ts.waves = std::max(1, (cnt + 15) / 16);
-        const bool key_tile = kind == kBackwardKV || kind == kSplitKey;
-        const int u1 = union_extent(p.ax[1], ts.T[1], key_tile);
-        const int u2 = union_extent(p.ax[2], ts.T[2], key_tile);
-        ts.rowshift = std::max(3, log2_of(u2));
-        ts.slots = ((u1 * (1 << ts.rowshift) + 31) / 32) * 32;
-        if (lds_bytes(kind, ts.slots, D) + extra_lds <= kLdsBudget) {
-            const int heads = key_tile ? p.Hkv : p.Hq;
-            ts.nheads = heads;
-            set_h_per(ts, 1);
-            ts.rep = make_fastdiv(static_cast<uint32_t>(p.rep));
-            long long spatial = 1;
-            for (int a = 0; a < 3; ++a) {
-                ts.tiles[a] = make_fastdiv(static_cast<uint32_t>(ts.ntile[a]));
-                ts.dil[a] = make_fastdiv(static_cast<uint32_t>(p.ax[a].dil));
-                ts.lenmod[a] = p.ax[a].len % p.ax[a].dil;
-                spatial *= static_cast<long long>(ts.ntile[a]) * p.ax[a].dil;
+    const bool key_tile = kind == kBackwardKV || kind == kSplitKey;
+    int n[3];  // items per axis: keys, or query items (output extent when strided); class 0 is the longest
+    for (int a = 0; a < 3; ++a) n[a] = key_tile ? n_class_h(p.ax[a], 0) : query_items(p.ax[a], n_class_h(p.ax[a], 0));
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int items = kMaxItems; items >= 16; items /= 2) {
+            if (n[0] == 1 && n[1] == 1) {
+                ts.T[2] = std::min(pow2_at_least(n[2]), items);
+                ts.T[1] = ts.T[0] = 1;
+            } else {
+                ts.T[2] = std::min(pow2_at_least(n[2]), 8);
+                ts.T[1] = std::min(pow2_at_least(n[1]), std::max(items / ts.T[2], 1));
+                ts.T[0] = std::min(pow2_at_least(n[0]), std::max(items / (ts.T[2] * ts.T[1]), 1));
             }
-            if (spatial >= (1LL << 31)) return false;
-            ts.spatial = make_fastdiv(static_cast<uint32_t>(spatial));
-            return true;
+            for (int a = 0; a < 3; ++a) {
+                ts.tshift[a] = log2_of(ts.T[a]);
+                ts.ntile[a] = (n[a] + ts.T[a] - 1) / ts.T[a];
+            }
+            const int cnt = ts.T[0] * ts.T[1] * ts.T[2];
+            ts.waves = std::max(1, (cnt + 15) / 16);
+            const int u1 = union_extent(p.ax[1], ts.T[1], key_tile);
+            const int u2 = union_extent(p.ax[2], ts.T[2], key_tile);
+            ts.rowshift = std::max(3, log2_of(u2));
+            ts.slots = ((u1 * (1 << ts.rowshift) + 31) / 32) * 32;
+            if (lds_bytes(kind, ts.slots, D) + extra_lds <= (pass == 0 ? kLdsBudget : kLdsBudgetLarge)) {
+                const int heads = key_tile ? p.Hkv : p.Hq;
+                ts.nheads = heads;
+                set_h_per(ts, 1);
+                ts.rep = make_fastdiv(static_cast<uint32_t>(p.rep));
+                long long spatial = 1;
+                for (int a = 0; a < 3; ++a) {
+                    ts.tiles[a] = make_fastdiv(static_cast<uint32_t>(ts.ntile[a]));
+                    ts.dil[a] = make_fastdiv(static_cast<uint32_t>(p.ax[a].dil));
+                    ts.lenmod[a] = p.ax[a].len % p.ax[a].dil;
+                    spatial *= static_cast<long long>(ts.ntile[a]) * p.ax[a].dil;
+                }
+                if (spatial >= (1LL << 31)) return false;
+                ts.spatial = make_fastdiv(static_cast<uint32_t>(spatial));
+                return true;
+            }
         }
     }
     return false;
@@ -1156,7 +1182,7 @@ constexpr size_t kGeoMaxBytes = size_t(64) << 20;
 
 struct GeoEntry {
     int dev, key;
-    int len[3], k[3], dil[3], causal[3], T[3], waves, rowshift;
+    int len[3], k[3], dil[3], st[3], causal[3], T[3], waves, rowshift;
     int* ptr;
 };
 
@@ -1177,6 +1203,7 @@ const int* geometry_table(const Prob& p, const TileShape& ts, bool key_tile, hip
         key.len[a] = p.ax[a].len;
         key.k[a] = p.ax[a].k;
         key.dil[a] = p.ax[a].dil;
+        key.st[a] = p.ax[a].st;
         key.causal[a] = p.ax[a].causal;
         key.T[a] = ts.T[a];
     }
@@ -1204,7 +1231,8 @@ const int* geometry_table(const Prob& p, const TileShape& ts, bool key_tile, hip
             int any = w < ts.waves ? 1 : 0, glo[3], ghi[3];
             for (int a = 0; a < 3; ++a) {
                 const AxisGeo ag = axis_geometry(p.ax[a].len, p.ax[a].k, p.ax[a].dil, p.ax[a].causal, ts.lenmod[a],
-                                                 ts.T[a], t[a], r[a], il[a], ih[a], key_tile, ts.dil[a]);
+                                                 p.ax[a].st, p.ax[a].out, ts.T[a], t[a], r[a], il[a], ih[a],
+                                                 key_tile, ts.dil[a]);
                 if (w == 0) {
                     rec[a] = r[a];
                     rec[3 + a] = ag.J;
@@ -1625,11 +1653,23 @@ hipError_t mfma_split_wsum(const char* name, const Prob& p, int D, const void* w
 #undef NA_WSUM
 }
 
+// The tile kernels index q and dq, like out, lse and dO, by query item: on
+// an axis with stride s item t is position s*t, so their spatial strides
+// scale by s.
+static Lay item_lay(const Prob& p, Lay l) {
+    l.s0 *= p.ax[0].st;
+    l.s1 *= p.ax[1].st;
+    l.s2 *= p.ax[2].st;
+    return l;
+}
+
 bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward, bool global) {
     if (dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f) || !mfma_static_lds_ok()) return false;
     if (p.Dqk != p.Dv || !(D == 32 || D == 64 || D == 96 || D == 128)) return false;
+    // a strided axis must be one residue class (its query items then sit at
+    // class coordinates stride * t); global keys come at stride 1 only
     for (int a = 0; a < 3; ++a)
-        if (p.ax[a].st != 1) return false;
+        if (p.ax[a].st != 1 && (p.ax[a].dil != 1 || global)) return false;
     // tile indices (the launch grid) stay in 31 bits
     const size_t extra = global ? global_lds(D) : 0;
     TileShape ts{};
@@ -1645,6 +1685,7 @@ bool mfma_offsets_fit(const Prob& p, std::initializer_list<Lay> lays) { return o
 
 hipError_t mfma_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
                         Lay lo, float* lse, Lay ll, int dtype, hipStream_t s, const GlobalSet* g) {
+    lq = item_lay(p, lq);
 #define NA_FWD(T, DD) return launch_fwd<T, DD>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, g, s)
     if (dtype == NATTEN_BF16) {
         if (p.Dqk == 32) NA_FWD(bf16, 32);
@@ -1663,6 +1704,8 @@ hipError_t mfma_backward(const Prob& p, const void* q, Lay lq, const void* k, La
                          const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                          const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
                          float* delta, Lay lde, int dtype, hipStream_t s, const GlobalSet* g) {
+    lq = item_lay(p, lq);
+    ldq = item_lay(p, ldq);
 #define NA_BWD(T, DD)                                                                                            \
     return launch_bwd<T, DD>(p, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dlse, ldl, dq, ldq, dk, ldk, dv, \
                              ldv, delta, lde, g, s)

@@ -273,6 +273,7 @@ __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts
             k.c[a].K = p.ax[a].k;
             k.c[a].h = p.ax[a].k >> 1;
             k.c[a].causal = p.ax[a].causal;
+            k.c[a].qs = p.ax[a].st;
         }
         const int* wr = rec + 24 + 8 * wave;
         g.any = wr[0] != 0;
@@ -299,6 +300,8 @@ __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts
 #define F_K(a) p.ax[a].k
 #define F_DIL(a) p.ax[a].dil
 #define F_CAUSAL(a) p.ax[a].causal
+#define F_ST(a) p.ax[a].st
+#define F_OUT(a) p.ax[a].out
 #define F_LENMOD(a) ts.lenmod[a]
 #define F_T(a) ts.T[a]
 #define F_DMUL(a) ts.dil[a].mul
@@ -311,12 +314,14 @@ __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts
     const FastDiv fd{static_cast<uint32_t>(NA_PICK(F_DMUL)), static_cast<uint32_t>(NA_PICK(F_DSH)),
                      static_cast<uint32_t>(dil)};
     const AxisGeo ag = axis_geometry(NA_PICK(F_LEN), NA_PICK(F_K), dil, NA_PICK(F_CAUSAL), NA_PICK(F_LENMOD),
-                                     NA_PICK(F_T), NA_PICK(F_TT), NA_PICK(F_RR), NA_PICK(F_IL), NA_PICK(F_IH), KEY,
-                                     fd);
+                                     NA_PICK(F_ST), NA_PICK(F_OUT), NA_PICK(F_T), NA_PICK(F_TT), NA_PICK(F_RR),
+                                     NA_PICK(F_IL), NA_PICK(F_IH), KEY, fd);
 #undef F_LEN
 #undef F_K
 #undef F_DIL
 #undef F_CAUSAL
+#undef F_ST
+#undef F_OUT
 #undef F_LENMOD
 #undef F_T
 #undef F_DMUL
@@ -340,6 +345,7 @@ __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts
         k.c[a].K = p.ax[a].k;
         k.c[a].h = p.ax[a].k >> 1;
         k.c[a].causal = p.ax[a].causal;
+        k.c[a].qs = p.ax[a].st;
         g.lo[a] = __builtin_amdgcn_readlane(ag.glo, a);
         g.hi[a] = __builtin_amdgcn_readlane(ag.ghi, a);
         nonempty = nonempty && __builtin_amdgcn_readlane(ag.tile_ok, a) != 0;
@@ -348,6 +354,14 @@ __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts
     g.c0 = (g.lo[1] * (1 << ts.rowshift) + g.lo[2]) >> 5;
     g.c1 = (g.hi[1] * (1 << ts.rowshift) + g.hi[2]) >> 5;
     return nonempty;
+}
+
+// A key tile whose union is empty on some axis: no query attends its keys
+// (they lie past the last window at an even-kernel border, or past the
+// last query's window on a strided axis), so every gradient it owns is
+// zero.  Query tiles always have a union (every window holds a key).
+__device__ __forceinline__ bool empty_union(const Block& k) {
+    return k.U[0] == 0 || k.U[1] == 0 || k.U[2] == 0;
 }
 
 // One lane's query (or key): validity, position and admissible box
@@ -723,7 +737,9 @@ struct WsumArgs {
 
 // The lane's item from the (XCD-remapped) workgroup index x alone (the
 // decode of tile_geometry without the unions): batch, the workgroup's run of
-// heads [h0, h1) and the position; false for lanes past the tile.
+// heads [h0, h1) and the position (a query item's output index on a strided
+// axis); false for lanes past the tile.
+template <bool KEY>
 __device__ __forceinline__ bool lane_position(const Prob& p, const TileShape& ts, int x, int wave, int col, int& b,
                                               int& h0, int& h1, int (&pos)[3]) {
     int q = fdiv(x, ts.hchunks);
@@ -740,7 +756,7 @@ __device__ __forceinline__ bool lane_position(const Prob& p, const TileShape& ts
     bool ok = true;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
-        const int n = fdiv(p.ax[a].len - r[a] + p.ax[a].dil - 1, ts.dil[a]);
+        const int n = !KEY && p.ax[a].st != 1 ? p.ax[a].out : fdiv(p.ax[a].len - r[a] + p.ax[a].dil - 1, ts.dil[a]);
         const int j = t[a] * ts.T[a] + e[a];
         ok = ok && j < n;
         pos[a] = r[a] + j * p.ax[a].dil;
@@ -806,22 +822,23 @@ int log2_of(int x) {
 }
 
 // Largest union extent on one axis over every class and tile (the same
-// spans decode_block computes on the device).
+// spans axis_geometry computes for each tile).
 int union_extent(const Axis& A, int T, bool key_tile) {
     int best = 1;
     for (int r = 0; r < A.dil; ++r) {
         const ClassAxis c = class_axis(A, r);
-        for (int J = 0; J < c.n; J += T) {
-            const int jend = (J + T < c.n ? J + T : c.n) - 1;
+        const int items = key_tile ? c.n : query_items(A, c.n);
+        for (int J = 0; J < items; J += T) {
+            const int jend = (J + T < items ? J + T : items) - 1;
             int lo, hi, x;
             if (!key_tile) {
-                lo = class_ws(c, J);
+                lo = query_ws(c, J);
                 lo = lo > 0 ? lo : 0;
-                hi = class_ws(c, jend) + c.K - 1;
+                hi = query_ws(c, jend) + c.K - 1;
                 hi = hi < c.n - 1 ? hi : c.n - 1;
             } else {
-                class_span(c, J, lo, x);
-                class_span(c, jend, x, hi);
+                query_span(c, J, lo, x);
+                query_span(c, jend, x, hi);
             }
             if (hi - lo + 1 > best) best = hi - lo + 1;
         }

@@ -103,6 +103,36 @@ long long host_class_mismatch(const natten_problem_t* p) {
     return bad;
 }
 
+// Query-item closed forms (query_ws, query_span) on axis 2 against the
+// window rule at position stride * t and brute-force membership; the axis
+// has dilation 1 when strided.  Returns the number of disagreements.
+long long host_query_item_mismatch(const natten_problem_t* p) {
+    const na::Prob P = make(p);
+    const na::Axis& A = P.ax[2];
+    long long bad = 0;
+    for (int r = 0; r < A.dil; ++r) {
+        const na::ClassAxis c = na::class_axis(A, r);
+        const int nq = na::query_items(A, c.n);
+        if (nq != (A.st == 1 ? c.n : A.out)) ++bad;
+        for (int t = 0; t < nq; ++t) {
+            const int want = (na::axis_first(A, r + t * A.st * A.dil) - r) / A.dil;
+            if (A.st > 1 && na::query_ws(c, t) != want) ++bad;
+        }
+        for (int u = 0; u < c.n; ++u) {
+            int lo, hi;
+            na::query_span(c, u, lo, hi);
+            for (int t = 0; t < nq; ++t) {
+                const int f = na::axis_first(A, r + t * A.st * A.dil);
+                const int m = r + u * A.dil;
+                const bool member = m >= f && m <= f + (A.k - 1) * A.dil && (m - f) % A.dil == 0;
+                const bool in = t >= lo && t <= hi;
+                if (member != in) ++bad;
+            }
+        }
+    }
+    return bad;
+}
+
 }  // extern "C"
 
 extern "C" {
@@ -126,20 +156,24 @@ extern "C" {
 // Tile geometry (axis_geometry, shared by the host-built tables and the
 // kernels) against brute force on one axis: for every residue class, tile
 // of T items and wave item range [wl, wh], the union box must equal the
-// min/max of the class coordinates the tile's items need (their window
-// members, or the queries attending a key) and the wave box must contain
-// what the wave's items need, equal to it when every key is attended.
+// min/max of the coordinates the tile's items need (their window members,
+// or the query items attending a key) and the wave box must contain what
+// the wave's items need, equal to it when every key is attended.  With
+// stride s > 1 (dilation 1) query item t is the query at position s*t.
 // Returns the number of mismatches.
-long long host_tile_geometry_mismatch(int L, int K, int d, int causal, int T, int key) {
-    na::Axis A{L, L, K, d, 1, causal};
+long long host_tile_geometry_mismatch(int L, int K, int d, int causal, int T, int key, int s) {
+    const int out = (L + s - 1) / s;
+    na::Axis A{L, out, K, d, s, causal};
     long long bad = 0;
     const na::FastDiv fd = na::make_fastdiv(static_cast<uint32_t>(d));
     for (int r = 0; r < d && r < L; ++r) {
         const int n = (L - r + d - 1) / d;
-        // class coordinates needed by class item j: [need_lo[j], need_hi[j]]
-        std::vector<int> need_lo(n, 1 << 30), need_hi(n, -(1 << 30));
-        for (int qj = 0; qj < n; ++qj) {
-            const int i = r + qj * d;
+        const int nq = s == 1 ? n : out;
+        const int items = key ? n : nq;
+        // coordinates needed by item j: [need_lo[j], need_hi[j]]
+        std::vector<int> need_lo(items, 1 << 30), need_hi(items, -(1 << 30));
+        for (int qj = 0; qj < nq; ++qj) {
+            const int i = r + qj * s * d;
             const int f = na::axis_first(A, i);
             for (int x = 0; x < K; ++x) {
                 const int m = f + x * d;
@@ -151,12 +185,13 @@ long long host_tile_geometry_mismatch(int L, int K, int d, int causal, int T, in
             }
         }
         bool all_attended = true;
-        for (int j = 0; j < n; ++j) all_attended = all_attended && need_lo[j] <= need_hi[j];
-        for (int t = 0; t * T < n; ++t) {
+        for (int j = 0; j < items; ++j) all_attended = all_attended && need_lo[j] <= need_hi[j];
+        for (int t = 0; t * T < items; ++t) {
             for (int wl = 0; wl < T; ++wl)
                 for (int wh = wl; wh < T; ++wh) {
-                    const na::AxisGeo g = na::axis_geometry(L, K, d, causal, L % d, T, t, r, wl, wh, key != 0, fd);
-                    const int J = t * T, E = std::min(T, n - J);
+                    const na::AxisGeo g =
+                        na::axis_geometry(L, K, d, causal, L % d, s, out, T, t, r, wl, wh, key != 0, fd);
+                    const int J = t * T, E = std::min(T, items - J);
                     if (g.J != J || g.E != E || g.n != n || !g.tile_ok) { ++bad; continue; }
                     int ulo = 1 << 30, uhi = -(1 << 30);
                     for (int j = J; j < J + E; ++j) {

@@ -146,6 +146,63 @@ def test_fused_forward_backward(case, dtype):
         _close(a, b, dtype, n)
 
 
+# Strided cases on the MFMA tile kernels: stride > 1 on axes with dilation 1
+# (query item t at position stride * t), including even kernels and stride
+# equal to the kernel, whose key tiles past the last window have no
+# attending query at all.
+STRIDED_TILE = [
+    # rank, spatial, hq, hkv, dim, ks, st, dil, causal, scale
+    (1, (70,), 4, 2, 64, (7,), (2,), (1,), (False,), None),
+    (1, (61,), 2, 2, 32, (9,), (3,), (1,), (True,), 0.3),
+    (1, (67,), 2, 1, 128, (4,), (4,), (1,), (False,), None),
+    (2, (20, 23), 2, 2, 32, (5, 7), (2, 3), (1, 1), (False, False), None),
+    (2, (17, 16), 4, 2, 64, (5, 4), (2, 1), (1, 2), (False, False), None),
+    (2, (15, 18), 2, 1, 96, (3, 5), (3, 2), (1, 1), (True, False), None),
+    (2, (12, 14), 2, 2, 128, (3, 5), (2, 4), (1, 1), (False, True), 0.2),
+    (2, (16, 16), 2, 2, 32, (8, 8), (8, 8), (1, 1), (False, False), None),
+    (3, (8, 10, 12), 2, 2, 32, (3, 5, 5), (2, 2, 3), (1, 1, 1), (False, True, False), None),
+    (3, (9, 8, 11), 4, 2, 64, (4, 3, 5), (2, 1, 2), (1, 2, 1), (False, False, True), None),
+    # stride 1 with an even kernel on the outer axis: key tiles of one
+    # unattended key
+    (3, (7, 8, 9), 2, 2, 32, (4, 3, 3), (1, 1, 1), (1, 1, 1), (False, False, False), None),
+]
+
+
+@pytest.mark.parametrize("case", STRIDED_TILE)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fused_strided_tile_path(case, dtype):
+    """Strided fused forward and backward run the MFMA tile kernels (query
+    items indexed by output position, q and dq read and written at stride *
+    t) and match the oracle in fp32 on the same inputs; dq is zero off the
+    strided positions."""
+    from natten_mps_amd import functional as F
+    from natten_mps_amd._core import _lib
+
+    rank, sp, hq, hkv, dim, ks, st, dil, causal, scale = case
+    q, k, v = _inputs(17, [(2, *sp, hq, dim), (2, *sp, hkv, dim), (2, *sp, hkv, dim)], dtype)
+    out_sp = [(n + s - 1) // s for n, s in zip(sp, st)]
+    (do,) = _inputs(18, [(2, *out_sp, hq, dim)], dtype)
+    fn = getattr(F, f"na{rank}d")
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        out, grads = _hip_fwd_bwd(fn, (q, k, v), do, kernel_size=ks, stride=st, dilation=dil, is_causal=causal,
+                                  scale=scale)
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    launched = set(_lib.profile_read(reset=True))
+    assert {"na_fwd_mfma", "na_bwd_q_mfma", "na_bwd_kv_mfma"} <= launched, launched
+    assert tuple(out.shape[1:1 + rank]) == tuple(out_sp)
+    ref, rgrads = _oracle_fwd_bwd(rank, (q, k, v), do, ks, st, dil, causal, scale)
+    _close(out, ref, dtype, "out")
+    for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
+        _close(a, b, dtype, n)
+    on = torch.zeros(sp, dtype=torch.bool)
+    on[tuple(slice(None, None, s) for s in st)] = True
+    assert torch.count_nonzero(grads[0][:, ~on]) == 0
+
+
 def test_lse_matches_logsumexp():
     from natten_mps_amd._core import hip
 
@@ -283,6 +340,7 @@ SPLIT_TILE = [
     (2, (17, 19), (7, 7), (1, 1), (False, False), None),
     (2, (20, 23), (5, 7), (2, 3), (True, False), 0.3),
     (3, (6, 9, 10), (3, 3, 5), (1, 2, 1), (False, True, False), None),
+    (3, (7, 8, 9), (4, 3, 3), (1, 1, 1), (False, False, False), None),
 ]
 
 
@@ -732,14 +790,16 @@ def test_head_dim_128_tile_path(dtype):
         _close(a, b, dtype, n)
 
 
-@pytest.mark.parametrize("rank, spatial, ks, dil, causal, heads", [
-    (2, (56, 56), (7, 7), (1, 1), (False, False), (4, 4)),
-    (2, (56, 56), (7, 7), (8, 8), (False, False), (4, 4)),
-    (1, (300,), (33,), (4,), (True,), (4, 2)),
-    (3, (6, 10, 12), (3, 5, 5), (1, 2, 2), (False, False, False), (2, 2)),
-    (2, (13, 17), (4, 6), (2, 1), (True, False), (2, 1)),
+@pytest.mark.parametrize("rank, spatial, ks, dil, causal, heads, st", [
+    (2, (56, 56), (7, 7), (1, 1), (False, False), (4, 4), (1, 1)),
+    (2, (56, 56), (7, 7), (8, 8), (False, False), (4, 4), (1, 1)),
+    (1, (300,), (33,), (4,), (True,), (4, 2), (1,)),
+    (3, (6, 10, 12), (3, 5, 5), (1, 2, 2), (False, False, False), (2, 2), (1, 1, 1)),
+    (2, (13, 17), (4, 6), (2, 1), (True, False), (2, 1), (1, 1)),
+    (2, (30, 33), (5, 7), (1, 1), (False, True), (2, 2), (2, 3)),
+    (3, (9, 10, 12), (4, 3, 5), (1, 2, 1), (False, False, False), (2, 1), (2, 1, 2)),
 ])
-def test_geometry_tables_match_in_kernel_geometry(monkeypatch, rank, spatial, ks, dil, causal, heads):
+def test_geometry_tables_match_in_kernel_geometry(monkeypatch, rank, spatial, ks, dil, causal, heads, st):
     """The tile kernels read host-built per-tile geometry records, or compute
     the same geometry in the kernel (NATTEN_HIP_GEOMETRY=device, and during
     graph capture): both must give identical bits."""
@@ -747,9 +807,10 @@ def test_geometry_tables_match_in_kernel_geometry(monkeypatch, rank, spatial, ks
 
     fn = {1: F.na1d, 2: F.na2d, 3: F.na3d}[rank]
     hq, hkv = heads
+    out_sp = [(n + s - 1) // s for n, s in zip(spatial, st)]
     q, k, v, do = _inputs(97, [(2, *spatial, hq, 32), (2, *spatial, hkv, 32), (2, *spatial, hkv, 32),
-                               (2, *spatial, hq, 32)], torch.bfloat16)
-    kw = dict(kernel_size=ks, dilation=dil, is_causal=causal)
+                               (2, *out_sp, hq, 32)], torch.bfloat16)
+    kw = dict(kernel_size=ks, dilation=dil, is_causal=causal, stride=st)
     monkeypatch.delenv("NATTEN_HIP_GEOMETRY", raising=False)
     out_t, grads_t = _hip_fwd_bwd(fn, (q, k, v), do, **kw)
     monkeypatch.setenv("NATTEN_HIP_GEOMETRY", "device")

@@ -34,9 +34,11 @@ def host_idx():
     lib.host_inverse_mismatch.restype = ctypes.c_longlong
     lib.host_class_mismatch.argtypes = [ctypes.POINTER(_lib.Problem)]
     lib.host_class_mismatch.restype = ctypes.c_longlong
+    lib.host_query_item_mismatch.argtypes = [ctypes.POINTER(_lib.Problem)]
+    lib.host_query_item_mismatch.restype = ctypes.c_longlong
     lib.host_fastdiv_errors.argtypes = [ctypes.c_uint32, ctypes.c_int, ctypes.c_int]
     lib.host_fastdiv_errors.restype = ctypes.c_longlong
-    lib.host_tile_geometry_mismatch.argtypes = [ctypes.c_int] * 6
+    lib.host_tile_geometry_mismatch.argtypes = [ctypes.c_int] * 7
     lib.host_tile_geometry_mismatch.restype = ctypes.c_longlong
     return lib
 
@@ -56,11 +58,12 @@ def test_tile_geometry_against_brute_force(host_idx):
                 for causal in (0, 1):
                     if not causal and d == 1 and K % 2 == 0 and K == L:
                         continue
-                    for T in (1, 2, 4, 8, 16):
-                        for key in (0, 1):
-                            assert host_idx.host_tile_geometry_mismatch(L, K, d, causal, T, key) == 0, \
-                                (L, K, d, causal, T, key)
-                            n += 1
+                    for s in range(1, K + 1 if d == 1 else 2):
+                        for T in (1, 2, 4, 8, 16):
+                            for key in (0, 1):
+                                assert host_idx.host_tile_geometry_mismatch(L, K, d, causal, T, key, s) == 0, \
+                                    (L, K, d, causal, T, key, s)
+                                n += 1
     assert n > 1000
 
 
@@ -90,6 +93,23 @@ def test_class_coordinate_closed_forms(host_idx):
                 (L, K, d, c)
             n += 1
     assert n > 1000
+
+
+def test_query_item_closed_forms(host_idx):
+    """Query items of the strided tile path: item t is the query at position
+    stride * t (dilation 1); its window start and the items attending each
+    key equal the window rule and brute-force membership for every (L, K,
+    stride <= K, causal) with L <= 30, and at stride 1 for every dilation."""
+    n = 0
+    for L, K, d in _sweep_starts(30):
+        if d == 1 and K % 2 == 0 and K == L:
+            continue
+        for s in range(1, K + 1 if d == 1 else 2):
+            for c in (False, True):
+                prob = _problem((L,), (K,), (d,), (s,), (c,))
+                assert host_idx.host_query_item_mismatch(ctypes.byref(prob)) == 0, (L, K, d, s, c)
+                n += 1
+    assert n > 3000
 
 
 @pytest.fixture(scope="module")
