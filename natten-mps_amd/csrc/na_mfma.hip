@@ -90,7 +90,7 @@ __device__ __forceinline__ void redo_fwd(const void* kargs, int wg, int wave, in
 }
 
 template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfma(FwdArgs<T> args) {
+__global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfma(FwdArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
     const int* __restrict__ geo = args.geo;
@@ -281,7 +281,7 @@ __device__ __forceinline__ void redo_bwd_q(const void* kargs, int wg, int wave, 
 }
 
 template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_mfma(BwdQArgs<T> args) {
+__global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_mfma(BwdQArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
     const int* __restrict__ geo = args.geo;
@@ -486,7 +486,7 @@ __device__ __forceinline__ void redo_bwd_kv(const void* kargs, int wg, int wave,
 }
 
 template <typename T, int D, int LAY, bool WIDE>
-__global__ __launch_bounds__(256) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_kv_mfma(BwdKvArgs<T> args) {
+__global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_kv_mfma(BwdKvArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
     const int* __restrict__ geo = args.geo;
@@ -1097,6 +1097,17 @@ void set_h_per(TileShape& ts, int per) {
     ts.hchunks = make_fastdiv(static_cast<uint32_t>((ts.nheads + per - 1) / per));
 }
 
+// Largest box of the fused kernels' tiles: 64 items (4 waves) unless
+// NATTEN_HIP_TILE_ITEMS asks for 16, 32 or 128 (tuning).
+int fused_items() {
+    static const int n = [] {
+        const char* e = std::getenv("NATTEN_HIP_TILE_ITEMS");
+        const int v = e ? std::atoi(e) : 0;
+        return (v == 16 || v == 32 || v == 64 || v == kMaxFusedItems) ? v : kMaxItems;
+    }();
+    return n;
+}
+
 // LDS a forward / dQ workgroup adds for global keys: 32 key and 32 value rows.
 size_t global_lds(int D) { return static_cast<size_t>(2 * 32) * (D == 96 ? 128 : D) * 2; }
 
@@ -1108,8 +1119,9 @@ bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts, size_t extra_ld
     const bool key_tile = kind == kBackwardKV || kind == kSplitKey;
     int n[3];  // items per axis: keys, or query items (output extent when strided); class 0 is the longest
     for (int a = 0; a < 3; ++a) n[a] = key_tile ? n_class_h(p.ax[a], 0) : query_items(p.ax[a], n_class_h(p.ax[a], 0));
+    const bool fused = kind == kForward || kind == kBackwardQ || kind == kBackwardKV;
     for (int pass = 0; pass < 2; ++pass) {
-        for (int items = kMaxItems; items >= 16; items /= 2) {
+        for (int items = fused ? fused_items() : kMaxItems; items >= 16; items /= 2) {
             if (n[0] == 1 && n[1] == 1) {
                 ts.T[2] = std::min(pow2_at_least(n[2]), items);
                 ts.T[1] = ts.T[0] = 1;
@@ -1224,7 +1236,7 @@ const int* geometry_table(const Prob& p, const TileShape& ts, bool key_tile, hip
         int t[3], r[3];
         spatial_coords(ts, s, t, r);
         int nonempty = 1;
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < kMaxWaves; ++w) {
             int il[3], ih[3];
             wave_items(ts, w, il, ih);
             int* wr = rec + 24 + 8 * w;

@@ -30,7 +30,11 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+// Items (queries or keys) per workgroup: 16 per wave.  The fused kernels
+// take up to kMaxFusedItems (8 waves), the split kernels up to kMaxItems.
 constexpr int kMaxItems = 64;
+constexpr int kMaxFusedItems = 128;
+constexpr int kMaxWaves = kMaxFusedItems / 16;
 // bytes of LDS before the staged operands (see lds_base)
 constexpr int kLdsPad = 16;
 // buffer range of a staged plane; out-of-union slots read at kOutOfRange
@@ -223,9 +227,10 @@ struct WaveGeo {
 
 // Host-built per-tile geometry records (kRecDwords ints per spatial tile):
 //   [0..2] r   [3..5] J   [6..8] E   [9..11] lo   [12..14] U   [15..17] n
-//   [18..20] B   [21] nonempty   then per wave w < 4 at 24 + 8w:
+//   [18..20] B   [21] nonempty   then per wave w < kMaxWaves at 24 + 8w:
 //   any, lo0, hi0, lo1, hi1, lo2, hi2, c0 | c1 << 16
-constexpr int kRecDwords = 64;
+constexpr int kRecDwords = 128;
+static_assert(24 + 8 * kMaxWaves <= kRecDwords, "geometry record too small");
 
 __host__ __device__ inline void spatial_coords(const TileShape& ts, int s, int (&t)[3], int (&r)[3]) {
     for (int a = 2; a >= 0; --a) {
