@@ -618,17 +618,20 @@ constexpr int kLayGeneral = 0, kLayOne = 1, kLayTwo = 2;
 // Waves per SIMD an instance is built for (4: at most 128 VGPRs, 5: at most
 // 96; 1: no constraint).  Saying so lets the register allocator trade VGPRs
 // for SGPRs instead of spilling SGPRs.  The choices are the measured best on
-// MI355X: at head dim 32 the forward and dQ instances without the per-chunk
-// column pattern fit 5 waves; the dK/dV kernel spills VGPRs at 5 and
-// serialises its LDS reads, and runs 7 % faster at 4; at head dim 64 the
-// dQ kernel and the wide dK/dV kernel fit 4.  WIDE instances handle unions whose rows
-// exceed 32 slots, where the column mask changes from chunk to chunk;
-// keeping them apart leaves the common instance its smaller register need.
+// MI355X: at head dim 32 the forward without the per-chunk column pattern
+// fits 5 waves; the backward kernels at 96 VGPRs serialise their
+// transposing LDS reads (the dK/dV kernel also spills), and at 4 waves they
+// run 2 % (dQ) and 7 % (dK/dV) faster; at head dim 64 the forward and the
+// wide dK/dV kernel fit 4, and the dQ kernel, whose tiles mostly leave room
+// for 2 to 4 workgroups per CU, runs 3-10 % faster with the registers of 2.
+// WIDE instances handle unions whose rows exceed 32 slots, where the column
+// mask changes from chunk to chunk; keeping them apart leaves the common
+// instance its smaller register need.
 enum KernelId { kKernFwd, kKernBwdQ, kKernBwdKV };
 
 constexpr int waves_per_simd(KernelId k, int D, bool wide) {
-    if (D == 32) return wide || k == kKernBwdKV ? 4 : 5;
-    if (D == 64) return k == kKernFwd || k == kKernBwdQ || (k == kKernBwdKV && wide) ? 4 : 1;
+    if (D == 32) return wide || k != kKernFwd ? 4 : 5;
+    if (D == 64) return k == kKernBwdQ ? 2 : k == kKernFwd || wide ? 4 : 1;
     return 1;
 }
 
