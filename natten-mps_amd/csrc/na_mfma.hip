@@ -1108,6 +1108,34 @@ int fused_items() {
     return n;
 }
 
+// NATTEN_HIP_TILE_SHAPE=t0,t1,t2 (powers of two, product 16..128) fixes the
+// first box tried for the fused kernels (tuning); null when unset.
+const int* forced_shape() {
+    static int shape[3] = {0, 0, 0};
+    static const bool set = [] {
+        const char* e = std::getenv("NATTEN_HIP_TILE_SHAPE");
+        int t[3];
+        if (!e || std::sscanf(e, "%d,%d,%d", &t[0], &t[1], &t[2]) != 3) return false;
+        const long long prod = static_cast<long long>(t[0]) * t[1] * t[2];
+        for (int a = 0; a < 3; ++a)
+            if (t[a] < 1 || (t[a] & (t[a] - 1)) != 0) return false;
+        if (prod < 16 || prod > kMaxFusedItems) return false;
+        for (int a = 0; a < 3; ++a) shape[a] = t[a];
+        return true;
+    }();
+    return set ? shape : nullptr;
+}
+
+// 3-D forward and dQ tiles first try two depth planes of 8 x 8 items (8
+// waves): a depth window of K0 then stages K0 + 1 slices for two planes
+// instead of K0 for one. On config 5 (16 x 32 x 32, K 3 x 7 x 7, head dim
+// 64) that made both kernels about 11 % faster; the dK/dV kernel, limited by
+// its registers to one such workgroup per CU, keeps 64 items.
+bool deep_query_tile(const Prob& p, Kind kind, const int (&n)[3]) {
+    return (kind == kForward || kind == kBackwardQ) && fused_items() == kMaxItems && n[0] >= 2 &&
+           p.ax[0].k > 1 && n[1] >= 8 && n[2] >= 8;
+}
+
 // LDS a forward / dQ workgroup adds for global keys: 32 key and 32 value rows.
 size_t global_lds(int D) { return static_cast<size_t>(2 * 32) * (D == 96 ? 128 : D) * 2; }
 
@@ -1117,45 +1145,58 @@ size_t global_lds(int D) { return static_cast<size_t>(2 * 32) * (D == 96 ? 128 :
 // budget, kLdsBudget first, then kLdsBudgetLarge.
 bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts, size_t extra_lds = 0) {
     const bool key_tile = kind == kBackwardKV || kind == kSplitKey;
+    const bool fused = kind == kForward || kind == kBackwardQ || kind == kBackwardKV;
     int n[3];  // items per axis: keys, or query items (output extent when strided); class 0 is the longest
     for (int a = 0; a < 3; ++a) n[a] = key_tile ? n_class_h(p.ax[a], 0) : query_items(p.ax[a], n_class_h(p.ax[a], 0));
-    const bool fused = kind == kForward || kind == kBackwardQ || kind == kBackwardKV;
+    // box T (power-of-two extents): its waves, staged union and LDS fit
+    const auto fits = [&](const int (&T)[3], size_t budget) {
+        for (int a = 0; a < 3; ++a) {
+            ts.T[a] = T[a];
+            ts.tshift[a] = log2_of(T[a]);
+            ts.ntile[a] = (n[a] + T[a] - 1) / T[a];
+        }
+        ts.waves = std::max(1, (T[0] * T[1] * T[2] + 15) / 16);
+        const int u1 = union_extent(p.ax[1], T[1], key_tile);
+        const int u2 = union_extent(p.ax[2], T[2], key_tile);
+        ts.rowshift = std::max(3, log2_of(u2));
+        ts.slots = ((u1 * (1 << ts.rowshift) + 31) / 32) * 32;
+        return lds_bytes(kind, ts.slots, D) + extra_lds <= budget;
+    };
+    const auto finish = [&]() {
+        ts.nheads = key_tile ? p.Hkv : p.Hq;
+        set_h_per(ts, 1);
+        ts.rep = make_fastdiv(static_cast<uint32_t>(p.rep));
+        long long spatial = 1;
+        for (int a = 0; a < 3; ++a) {
+            ts.tiles[a] = make_fastdiv(static_cast<uint32_t>(ts.ntile[a]));
+            ts.dil[a] = make_fastdiv(static_cast<uint32_t>(p.ax[a].dil));
+            ts.lenmod[a] = p.ax[a].len % p.ax[a].dil;
+            spatial *= static_cast<long long>(ts.ntile[a]) * p.ax[a].dil;
+        }
+        if (spatial >= (1LL << 31)) return false;
+        ts.spatial = make_fastdiv(static_cast<uint32_t>(spatial));
+        return true;
+    };
+    if (const int* forced = fused ? forced_shape() : nullptr) {
+        int T[3];
+        for (int a = 0; a < 3; ++a) T[a] = std::min(pow2_at_least(n[a]), forced[a]);
+        if (fits(T, kLdsBudget)) return finish();
+    } else if (fused && deep_query_tile(p, kind, n)) {
+        const int T[3] = {2, 8, 8};
+        if (fits(T, kLdsBudget)) return finish();
+    }
     for (int pass = 0; pass < 2; ++pass) {
         for (int items = fused ? fused_items() : kMaxItems; items >= 16; items /= 2) {
+            int T[3];
             if (n[0] == 1 && n[1] == 1) {
-                ts.T[2] = std::min(pow2_at_least(n[2]), items);
-                ts.T[1] = ts.T[0] = 1;
+                T[2] = std::min(pow2_at_least(n[2]), items);
+                T[1] = T[0] = 1;
             } else {
-                ts.T[2] = std::min(pow2_at_least(n[2]), 8);
-                ts.T[1] = std::min(pow2_at_least(n[1]), std::max(items / ts.T[2], 1));
-                ts.T[0] = std::min(pow2_at_least(n[0]), std::max(items / (ts.T[2] * ts.T[1]), 1));
+                T[2] = std::min(pow2_at_least(n[2]), 8);
+                T[1] = std::min(pow2_at_least(n[1]), std::max(items / T[2], 1));
+                T[0] = std::min(pow2_at_least(n[0]), std::max(items / (T[2] * T[1]), 1));
             }
-            for (int a = 0; a < 3; ++a) {
-                ts.tshift[a] = log2_of(ts.T[a]);
-                ts.ntile[a] = (n[a] + ts.T[a] - 1) / ts.T[a];
-            }
-            const int cnt = ts.T[0] * ts.T[1] * ts.T[2];
-            ts.waves = std::max(1, (cnt + 15) / 16);
-            const int u1 = union_extent(p.ax[1], ts.T[1], key_tile);
-            const int u2 = union_extent(p.ax[2], ts.T[2], key_tile);
-            ts.rowshift = std::max(3, log2_of(u2));
-            ts.slots = ((u1 * (1 << ts.rowshift) + 31) / 32) * 32;
-            if (lds_bytes(kind, ts.slots, D) + extra_lds <= (pass == 0 ? kLdsBudget : kLdsBudgetLarge)) {
-                const int heads = key_tile ? p.Hkv : p.Hq;
-                ts.nheads = heads;
-                set_h_per(ts, 1);
-                ts.rep = make_fastdiv(static_cast<uint32_t>(p.rep));
-                long long spatial = 1;
-                for (int a = 0; a < 3; ++a) {
-                    ts.tiles[a] = make_fastdiv(static_cast<uint32_t>(ts.ntile[a]));
-                    ts.dil[a] = make_fastdiv(static_cast<uint32_t>(p.ax[a].dil));
-                    ts.lenmod[a] = p.ax[a].len % p.ax[a].dil;
-                    spatial *= static_cast<long long>(ts.ntile[a]) * p.ax[a].dil;
-                }
-                if (spatial >= (1LL << 31)) return false;
-                ts.spatial = make_fastdiv(static_cast<uint32_t>(spatial));
-                return true;
-            }
+            if (fits(T, pass == 0 ? kLdsBudget : kLdsBudgetLarge)) return finish();
         }
     }
     return false;
