@@ -517,6 +517,12 @@ int natten_hip_varlen_forward(const natten_problem_t* p, const int32_t* lens, co
     const int D = P.Dqk > P.Dv ? P.Dqk : P.Dv;
     const int vec =
         runs_aligned(dpl_for(D), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {v, lv, P.Dv}, {out, lo, P.Dv}}) ? 1 : 0;
+    if (use_mfma() && na::mfma_varlen_eligible(P, p->dtype, D, vec != 0, false) &&
+        na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(llse)}))
+        return launch_status(na::mfma_varlen_forward(P, lens, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out,
+                                                     to_lay(lo), lse, to_lay(llse), p->dtype,
+                                                     static_cast<hipStream_t>(stream)),
+                             "varlen_forward");
     return launch_status(na::generic_forward(P, vec, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo),
                                              lse, to_lay(llse), p->dtype, static_cast<hipStream_t>(stream), lens),
                          "varlen_forward");
@@ -542,6 +548,14 @@ int natten_hip_varlen_backward(const natten_problem_t* p, const int32_t* lens, c
                                               {dout, ldo, P.Dv}, {dq, ldq, P.Dqk}, {dk, ldk, P.Dqk}, {dv, ldv, P.Dv}})
                         ? 1
                         : 0;
+    if (use_mfma() && na::mfma_varlen_eligible(P, p->dtype, D, vec != 0, true) &&
+        na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(ldo), to_lay(llse),
+                                 to_lay(ldq), to_lay(ldk), to_lay(ldv), to_lay(ldelta)}))
+        return launch_status(na::mfma_varlen_backward(P, lens, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out,
+                                                      to_lay(lo), dout, to_lay(ldo), lse, to_lay(llse), dq,
+                                                      to_lay(ldq), dk, to_lay(ldk), dv, to_lay(ldv), delta,
+                                                      to_lay(ldelta), p->dtype, static_cast<hipStream_t>(stream)),
+                             "varlen_backward");
     return launch_status(
         na::generic_backward(P, vec, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout, to_lay(ldo),
                              lse, to_lay(llse), nullptr, na::Lay{}, dq, to_lay(ldq), dk, to_lay(ldk), dv, to_lay(ldv),

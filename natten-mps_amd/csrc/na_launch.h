@@ -91,6 +91,19 @@ int mfma_lds_audit(int* checked);
 // `global`: with global keys (their LDS on top of the tiles').
 bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward, bool global = false);
 bool mfma_offsets_fit(const Prob& p, std::initializer_list<Lay> lays);
+
+// Variable-length fused forward / backward on the MFMA tile kernels: the
+// problem describes the padded extents (stride 1), lens (device, int32
+// [batch][3]) each sample's own; padding positions of every output are
+// zeroed.  Eligibility as for the tile path, with LDS sized for every
+// sample extent up to the padded one.
+bool mfma_varlen_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward);
+hipError_t mfma_varlen_forward(const Prob& p, const int* lens, const void* q, Lay lq, const void* k, Lay lk,
+                               const void* v, Lay lv, void* o, Lay lo, float* lse, Lay ll, int dtype, hipStream_t s);
+hipError_t mfma_varlen_backward(const Prob& p, const int* lens, const void* q, Lay lq, const void* k, Lay lk,
+                                const void* v, Lay lv, const void* o, Lay lo, const void* dout, Lay ldo,
+                                const float* lse, Lay ll, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
+                                float* delta, Lay lde, int dtype, hipStream_t s);
 hipError_t mfma_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
                         Lay lo, float* lse, Lay ll, int dtype, hipStream_t s, const GlobalSet* g = nullptr);
 hipError_t mfma_backward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,

@@ -63,33 +63,38 @@ __device__ __forceinline__ ExactGlobal<T> exact_global(const GlobalKeys<T>& g, i
     return ExactGlobal<T>{g.k + b * g.kb + hk * g.kh, g.v + b * g.vb + hk * g.vh, g.ks, g.vs, g.n};
 }
 
-template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN>
 __device__ __forceinline__ void redo_fwd(const void* kargs, int wg, int wave, int col, int grp) {
     const FwdArgs<T>& A = *static_cast<const FwdArgs<T>*>(kargs);
+    Prob pv;
+    TileShape tv;
+    if constexpr (VARLEN) varlen_view(A.p, A.ts, A.lens, wg, pv, tv);
+    const Prob& P = VARLEN ? pv : A.p;
+    const TileShape& TS = VARLEN ? tv : A.ts;
     const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
     const LayK &ao = LAY == kLayGeneral ? A.lo : aq, &al = A.ll;
     int b, h0, h1, pos[3];
-    if (!lane_position<false>(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    if (!lane_position<false>(P, TS, wg, wave, col, b, h0, h1, pos)) return;
     ExactAxis x[3];
-    for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
+    for (int a = 0; a < 3; ++a) x[a] = exact_axis(P.ax[a], pos[a]);
     f32x4_t acc[D / 16];
 #pragma unroll 1
     for (int h = h0; h < h1; ++h) {
-        const int hk = kv_head(A.ts, h);
+        const int hk = kv_head(TS, h);
         float lse_v;
         if constexpr (GLOBAL)
-            exact_forward_global<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), bh_ptr(A.k, ak, b, hk),
+            exact_forward_global<T, D>(P.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), bh_ptr(A.k, ak, b, hk),
                                        strides3(ak), bh_ptr(A.v, av, b, hk), strides3(av),
                                        exact_global(A.gk, b, hk), grp, acc, lse_v);
         else
-            exact_forward<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), bh_ptr(A.k, ak, b, hk),
+            exact_forward<T, D>(P.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), bh_ptr(A.k, ak, b, hk),
                                 strides3(ak), bh_ptr(A.v, av, b, hk), strides3(av), grp, acc, lse_v);
         store_rows<T, D>(bh_ptr(A.out, ao, b, h), vol_off(ao, pos), grp, acc, 1.f);
         if (grp == 0) bh_ptr(A.lse, al, b, h)[vol_off(al, pos)] = lse_v;
     }
 }
 
-template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN = false>
 __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfma(FwdArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
@@ -111,7 +116,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernFwd, D, WIDE) voi
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
     Block blk;
     WaveGeo wg;
-    if (!tile_geometry<KEY_SIDE>(p, ts, geo, wave, blk, wg)) return;
+    if (!tile_geometry<KEY_SIDE, VARLEN>(p, ts, geo, wave, blk, wg, args.lens)) return;
     const StageMap sm = stage_map<T, D>(p, ts, lk, lv, lane);
     Walk w;
     walk_start(blk, w);
@@ -242,7 +247,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernFwd, D, WIDE) voi
     }
     // items whose tile result was not finite: exact recomputation (the
     // walk's state is dead here, so this costs the loop no registers)
-    if (redo) redo_fwd<T, D, LAY, WIDE, GLOBAL>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
+    if (redo) redo_fwd<T, D, LAY, WIDE, GLOBAL, VARLEN>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
 }
 
 // ---------------------------------------------------------------------------
@@ -250,37 +255,42 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernFwd, D, WIDE) voi
 // dq = scale * sum_k P (dP - delta) k, with P = exp(scale q.k - lse) and
 // dP = dO . v.  The dP product starts from -delta.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN>
 __device__ __forceinline__ void redo_bwd_q(const void* kargs, int wg, int wave, int col, int grp) {
     const BwdQArgs<T>& A = *static_cast<const BwdQArgs<T>*>(kargs);
+    Prob pv;
+    TileShape tv;
+    if constexpr (VARLEN) varlen_view(A.p, A.ts, A.lens, wg, pv, tv);
+    const Prob& P = VARLEN ? pv : A.p;
+    const TileShape& TS = VARLEN ? tv : A.ts;
     const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
     const LayK &ao = LAY == kLayGeneral ? A.lo : aq, &ado = LAY == kLayGeneral ? A.ldo : aq;
     const LayK &adq = LAY == kLayGeneral ? A.ldq : aq, &al = A.ll, &adl = LAY == kLayGeneral ? A.ldl : al;
     int b, h0, h1, pos[3];
-    if (!lane_position<false>(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    if (!lane_position<false>(P, TS, wg, wave, col, b, h0, h1, pos)) return;
     ExactAxis x[3];
-    for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
+    for (int a = 0; a < 3; ++a) x[a] = exact_axis(P.ax[a], pos[a]);
     f32x4_t acc[D / 16];
 #pragma unroll 1
     for (int h = h0; h < h1; ++h) {
-        const int hk = kv_head(A.ts, h);
+        const int hk = kv_head(TS, h);
         const T* do_row = bh_ptr(A.dout, ado, b, h) + vol_off(ado, pos);
         float di = exact_dot<T, D>(do_row, bh_ptr(A.o, ao, b, h) + vol_off(ao, pos));
         if (A.dlse) di -= bh_ptr(A.dlse, adl, b, h)[vol_off(adl, pos)];
         if constexpr (GLOBAL)
-            exact_backward_q_global<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), do_row,
+            exact_backward_q_global<T, D>(P.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), do_row,
                                           bh_ptr(A.lse, al, b, h)[vol_off(al, pos)], di, bh_ptr(A.k, ak, b, hk),
                                           strides3(ak), bh_ptr(A.v, av, b, hk), strides3(av),
                                           exact_global(A.gk, b, hk), grp, acc);
         else
-            exact_backward_q<T, D>(A.p.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), do_row,
+            exact_backward_q<T, D>(P.scale, x, bh_ptr(A.q, aq, b, h) + vol_off(aq, pos), do_row,
                                    bh_ptr(A.lse, al, b, h)[vol_off(al, pos)], di, bh_ptr(A.k, ak, b, hk),
                                    strides3(ak), bh_ptr(A.v, av, b, hk), strides3(av), grp, acc);
-        store_rows<T, D>(bh_ptr(A.dq, adq, b, h), vol_off(adq, pos), grp, acc, A.p.scale);
+        store_rows<T, D>(bh_ptr(A.dq, adq, b, h), vol_off(adq, pos), grp, acc, P.scale);
     }
 }
 
-template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN = false>
 __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_mfma(BwdQArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
@@ -311,7 +321,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) vo
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
     Block blk;
     WaveGeo wg;
-    if (!tile_geometry<KEY_SIDE>(p, ts, geo, wave, blk, wg)) return;
+    if (!tile_geometry<KEY_SIDE, VARLEN>(p, ts, geo, wave, blk, wg, args.lens)) return;
     const StageMap sm = stage_map<T, D>(p, ts, lk, lv, lane);
     Walk w;
     walk_start(blk, w);
@@ -418,7 +428,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) vo
             if (ln.valid) store_rows<T, D>(bh_ptr(dq, ldq, b, h), vol_off(ldq, ln.pos), grp, acc, p.scale);
         }
     }
-    if (redo) redo_bwd_q<T, D, LAY, WIDE, GLOBAL>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
+    if (redo) redo_bwd_q<T, D, LAY, WIDE, GLOBAL, VARLEN>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
 }
 
 // ---------------------------------------------------------------------------
@@ -450,19 +460,24 @@ __device__ __forceinline__ void stage_scalars(const Prob& p, const Block& k, con
     }
 }
 
-template <typename T, int D, int LAY, bool WIDE>
+template <typename T, int D, int LAY, bool WIDE, bool VARLEN>
 __device__ __forceinline__ void redo_bwd_kv(const void* kargs, int wg, int wave, int col, int grp) {
     const BwdKvArgs<T>& A = *static_cast<const BwdKvArgs<T>*>(kargs);
+    Prob pv;
+    TileShape tv;
+    if constexpr (VARLEN) varlen_view(A.p, A.ts, A.lens, wg, pv, tv);
+    const Prob& P = VARLEN ? pv : A.p;
+    const TileShape& TS = VARLEN ? tv : A.ts;
     const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
     const LayK& adk = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.ldk;
     const LayK& adv = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.ldv;
     const LayK &ado = LAY == kLayGeneral ? A.ldo : aq, &al = A.ll, &ade = LAY == kLayGeneral ? A.lde : al;
     int b, h0, h1, pos[3];
-    if (!lane_position<true>(A.p, A.ts, wg, wave, col, b, h0, h1, pos)) return;
+    if (!lane_position<true>(P, TS, wg, wave, col, b, h0, h1, pos)) return;
     ExactAxis x[3];
-    for (int a = 0; a < 3; ++a) x[a] = exact_axis(A.p.ax[a], pos[a]);
+    for (int a = 0; a < 3; ++a) x[a] = exact_axis(P.ax[a], pos[a]);
     f32x4_t g[D / 16];
-    const int rep = A.p.rep;
+    const int rep = P.rep;
 #pragma unroll 1
     for (int hk = h0; hk < h1; ++hk) {
         const T* k_row = bh_ptr(A.k, ak, b, hk) + vol_off(ak, pos);
@@ -471,21 +486,21 @@ __device__ __forceinline__ void redo_bwd_kv(const void* kargs, int wg, int wave,
         exact_zero(g);
 #pragma unroll 1
         for (int h = hk * rep; h < (hk + 1) * rep; ++h)
-            exact_backward_kv<T, D, true>(A.p.scale, x, k_row, v_row, bh_ptr(A.q, aq, b, h), strides3(aq),
+            exact_backward_kv<T, D, true>(P.scale, x, k_row, v_row, bh_ptr(A.q, aq, b, h), strides3(aq),
                                           bh_ptr(A.dout, ado, b, h), strides3(ado), bh_ptr(A.lse, al, b, h),
                                           strides3(al), bh_ptr(A.delta, ade, b, h), strides3(ade), grp, g);
         store_rows<T, D>(bh_ptr(A.dv, adv, b, hk), vol_off(adv, pos), grp, g, 1.f);
         exact_zero(g);
 #pragma unroll 1
         for (int h = hk * rep; h < (hk + 1) * rep; ++h)
-            exact_backward_kv<T, D, false>(A.p.scale, x, k_row, v_row, bh_ptr(A.q, aq, b, h), strides3(aq),
+            exact_backward_kv<T, D, false>(P.scale, x, k_row, v_row, bh_ptr(A.q, aq, b, h), strides3(aq),
                                            bh_ptr(A.dout, ado, b, h), strides3(ado), bh_ptr(A.lse, al, b, h),
                                            strides3(al), bh_ptr(A.delta, ade, b, h), strides3(ade), grp, g);
-        store_rows<T, D>(bh_ptr(A.dk, adk, b, hk), vol_off(adk, pos), grp, g, A.p.scale);
+        store_rows<T, D>(bh_ptr(A.dk, adk, b, hk), vol_off(adk, pos), grp, g, P.scale);
     }
 }
 
-template <typename T, int D, int LAY, bool WIDE>
+template <typename T, int D, int LAY, bool WIDE, bool VARLEN = false>
 __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_kv_mfma(BwdKvArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
@@ -517,7 +532,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdKV, D, WIDE) v
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loops
     Block blk;
     WaveGeo wg;
-    if (!tile_geometry<KEY_SIDE>(p, ts, geo, wave, blk, wg)) return;
+    if (!tile_geometry<KEY_SIDE, VARLEN>(p, ts, geo, wave, blk, wg, args.lens)) return;
     const Lane ln = lane_item(p, ts, blk, wave, col, true);
     if (empty_union(blk)) {
         f32x4_t z[D / 16];
@@ -615,7 +630,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdKV, D, WIDE) v
             }
         }
     }
-    if (redo) redo_bwd_kv<T, D, LAY, WIDE>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
+    if (redo) redo_bwd_kv<T, D, LAY, WIDE, VARLEN>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
 }
 
 // ---------------------------------------------------------------------------
@@ -1143,7 +1158,7 @@ size_t global_lds(int D) { return static_cast<size_t>(2 * 32) * (D == 96 ? 128 :
 // 64 items (4 waves), power-of-two extents, innermost axis first (8 wide
 // unless the problem is 1-D); halved until the staged union fits the LDS
 // budget, kLdsBudget first, then kLdsBudgetLarge.
-bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts, size_t extra_lds = 0) {
+bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts, size_t extra_lds = 0, bool varlen = false) {
     const bool key_tile = kind == kBackwardKV || kind == kSplitKey;
     const bool fused = kind == kForward || kind == kBackwardQ || kind == kBackwardKV;
     int n[3];  // items per axis: keys, or query items (output extent when strided); class 0 is the longest
@@ -1156,8 +1171,9 @@ bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts, size_t extra_ld
             ts.ntile[a] = (n[a] + T[a] - 1) / T[a];
         }
         ts.waves = std::max(1, (T[0] * T[1] * T[2] + 15) / 16);
-        const int u1 = union_extent(p.ax[1], T[1], key_tile);
-        const int u2 = union_extent(p.ax[2], T[2], key_tile);
+        // variable-length samples: sized for every extent up to the padded one
+        const int u1 = varlen ? union_extent_upto(p.ax[1], T[1], key_tile) : union_extent(p.ax[1], T[1], key_tile);
+        const int u2 = varlen ? union_extent_upto(p.ax[2], T[2], key_tile) : union_extent(p.ax[2], T[2], key_tile);
         ts.rowshift = std::max(3, log2_of(u2));
         ts.slots = ((u1 * (1 << ts.rowshift) + 31) / 32) * 32;
         return lds_bytes(kind, ts.slots, D) + extra_lds <= budget;
@@ -1186,17 +1202,40 @@ bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts, size_t extra_ld
         if (fits(T, kLdsBudget)) return finish();
     }
     for (int pass = 0; pass < 2; ++pass) {
+        const size_t budget = pass == 0 ? kLdsBudget : kLdsBudgetLarge;
         for (int items = fused ? fused_items() : kMaxItems; items >= 16; items /= 2) {
-            int T[3];
-            if (n[0] == 1 && n[1] == 1) {
-                T[2] = std::min(pow2_at_least(n[2]), items);
-                T[1] = T[0] = 1;
-            } else {
-                T[2] = std::min(pow2_at_least(n[2]), 8);
-                T[1] = std::min(pow2_at_least(n[1]), std::max(items / T[2], 1));
-                T[0] = std::min(pow2_at_least(n[0]), std::max(items / (T[2] * T[1]), 1));
+            const auto shape = [&](int w2, int (&T)[3]) {
+                if (n[0] == 1 && n[1] == 1) {
+                    T[2] = std::min(pow2_at_least(n[2]), items);
+                    T[1] = T[0] = 1;
+                } else {
+                    T[2] = std::min(pow2_at_least(n[2]), w2);
+                    T[1] = std::min(pow2_at_least(n[1]), std::max(items / T[2], 1));
+                    T[0] = std::min(pow2_at_least(n[0]), std::max(items / (T[2] * T[1]), 1));
+                }
+            };
+            if (!varlen) {
+                int T[3];
+                shape(8, T);
+                if (fits(T, budget)) return finish();
+                continue;
             }
-            if (fits(T, pass == 0 ? kLdsBudget : kLdsBudgetLarge)) return finish();
+            // variable length: the union that every sample extent allows can
+            // cross a power of two at the default width (a row pitch twice as
+            // wide), so the widths 8, 4 and 16 compete on LDS
+            int best[3] = {0, 0, 0};
+            size_t best_lds = 0;
+            for (const int w2 : {8, 4, 16}) {
+                int T[3];
+                shape(w2, T);
+                if (!fits(T, budget)) continue;
+                const size_t lds = lds_bytes(kind, ts.slots, D);
+                if (best[0] == 0 || lds < best_lds) {
+                    for (int a = 0; a < 3; ++a) best[a] = T[a];
+                    best_lds = lds;
+                }
+            }
+            if (best[0] != 0 && fits(best, budget)) return finish();
         }
     }
     return false;
@@ -1344,18 +1383,18 @@ GlobalKeys<T> to_global(const GlobalSet* g) {
     return r;
 }
 
-template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN = false>
 hipError_t run_fwd(const Prob& p, TileShape ts, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
-                   void* o, Lay lo, float* lse, Lay ll, const GlobalSet* g, hipStream_t s) {
-    const auto kern = k_fwd_mfma<T, D, LAY, WIDE, GLOBAL>;
+                   void* o, Lay lo, float* lse, Lay ll, const GlobalSet* g, hipStream_t s, const int* lens = nullptr) {
+    const auto kern = k_fwd_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN>;
     const size_t shm = lds_bytes(kForward, ts.slots, D) + (GLOBAL ? global_lds(D) : 0);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
-    const int* geo = geometry_table(p, ts, false, s);
+    const int* geo = VARLEN ? nullptr : geometry_table(p, ts, false, s);
     const FwdArgs<T> a{p,   ts,       geo,      (const T*)q, (const T*)k, (const T*)v, (T*)o,
-                       lse, to_k(lq), to_k(lk), to_k(lv),    to_k(lo),    to_k(ll),    to_global<T>(g)};
-    NA_LAUNCH(GLOBAL ? "na_fwd_global_mfma" : "na_fwd_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))),
+                       lse, to_k(lq), to_k(lk), to_k(lv),    to_k(lo),    to_k(ll),    to_global<T>(g), lens};
+    NA_LAUNCH(VARLEN ? "na_varlen_fwd_mfma" : GLOBAL ? "na_fwd_global_mfma" : "na_fwd_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))),
               dim3(64 * ts.waves), shm, s, a);
     return hipGetLastError();
 }
@@ -1384,40 +1423,40 @@ hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
     }
 }
 
-template <typename T, int D, int LAY, bool WIDE, bool GLOBAL>
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN = false>
 hipError_t run_bwd_q(const Prob& p, TileShape ts, const void* q, Lay lq, const void* k, Lay lk, const void* v,
                      Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                      const float* dlse, Lay ldl, void* dq, Lay ldq, float* delta, Lay lde, const GlobalSet* g,
-                     hipStream_t s) {
-    const auto kern = k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL>;
+                     hipStream_t s, const int* lens = nullptr) {
+    const auto kern = k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN>;
     const size_t shm = lds_bytes(kBackwardQ, ts.slots, D) + (GLOBAL ? global_lds(D) : 0);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
-    const int* geo = geometry_table(p, ts, false, s);
+    const int* geo = VARLEN ? nullptr : geometry_table(p, ts, false, s);
     const BwdQArgs<T> a{p,        ts,       geo,      (const T*)q, (const T*)k, (const T*)v, (const T*)o,
                         (const T*)dout, lse, dlse,  (T*)dq,      delta,       to_k(lq),    to_k(lk),
                         to_k(lv), to_k(lo), to_k(ldo), to_k(ll),  to_k(ldl),   to_k(ldq),   to_k(lde),
-                        to_global<T>(g)};
-    NA_LAUNCH(GLOBAL ? "na_bwd_q_global_mfma" : "na_bwd_q_mfma", kern,
+                        to_global<T>(g), lens};
+    NA_LAUNCH(VARLEN ? "na_varlen_bwd_q_mfma" : GLOBAL ? "na_bwd_q_global_mfma" : "na_bwd_q_mfma", kern,
               dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
     return hipGetLastError();
 }
 
-template <typename T, int D, int LAY, bool WIDE>
+template <typename T, int D, int LAY, bool WIDE, bool VARLEN = false>
 hipError_t run_bwd_kv(const Prob& p, TileShape ts, const void* q, Lay lq, const void* k, Lay lk, const void* v,
                       Lay lv, const void* dout, Lay ldo, const float* lse, Lay ll, const float* delta, Lay lde,
-                      void* dk, Lay ldk, void* dv, Lay ldv, hipStream_t s) {
-    const auto kern = k_bwd_kv_mfma<T, D, LAY, WIDE>;
+                      void* dk, Lay ldk, void* dv, Lay ldv, hipStream_t s, const int* lens = nullptr) {
+    const auto kern = k_bwd_kv_mfma<T, D, LAY, WIDE, VARLEN>;
     const size_t shm = lds_bytes(kBackwardKV, ts.slots, D);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
-    const int* geo = geometry_table(p, ts, true, s);
+    const int* geo = VARLEN ? nullptr : geometry_table(p, ts, true, s);
     const BwdKvArgs<T> a{p,        ts,       geo,       (const T*)q, (const T*)k, (const T*)v, (const T*)dout,
                          lse,      delta,    (T*)dk,    (T*)dv,      to_k(lq),    to_k(lk),    to_k(lv),
-                         to_k(ldo), to_k(ll), to_k(lde), to_k(ldk),  to_k(ldv)};
-    NA_LAUNCH("na_bwd_kv_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
+                         to_k(ldo), to_k(ll), to_k(lde), to_k(ldk),  to_k(ldv), lens};
+    NA_LAUNCH(VARLEN ? "na_varlen_bwd_kv_mfma" : "na_bwd_kv_mfma", kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
     return hipGetLastError();
 }
 
@@ -1465,6 +1504,123 @@ hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
             NA_BWD_LAY(kLayGeneral);
     }
 #undef NA_BWD_LAY
+}
+
+// ---------------------------------------------------------------------------
+// Variable-length problems on the fused tile kernels (their VARLEN instances,
+// general layout group): tile shape and LDS sized for the padded extents and
+// every smaller one, geometry computed in the kernels per sample, and the
+// padding positions zeroed by k_varlen_pad_zero afterwards.
+// ---------------------------------------------------------------------------
+
+// Zeroing target: rows of `width` elements of `esz` bytes (16-byte aligned
+// when width > 1) at every head below `heads`, or one fp32 scalar per head.
+struct PadTarget {
+    void* base;
+    LayK lay;
+    int heads, width, esz;
+};
+
+struct PadArgs {
+    Prob p;
+    const int* lens;
+    int n;
+    PadTarget t[4];
+};
+
+// One thread per (batch, padded position, head): where the position is
+// padding for its sample (past its extent on some axis, or the whole sample
+// when its extents are out of range) every target's row of that head
+// becomes zero.
+__global__ __launch_bounds__(256) void k_varlen_pad_zero(PadArgs a) {
+    const Prob& p = a.p;
+    const int n0 = p.ax[0].len, n1 = p.ax[1].len, n2 = p.ax[2].len;
+    const int hmax = p.Hq > p.Hkv ? p.Hq : p.Hkv;
+    const long long vol = static_cast<long long>(n0) * n1 * n2;
+    long long id = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= vol * p.B * hmax) return;
+    const int h = static_cast<int>(id % hmax);
+    id /= hmax;
+    const int b = static_cast<int>(id / vol);
+    long long r = id - b * vol;
+    const int i2 = static_cast<int>(r % n2);
+    r /= n2;
+    const int i1 = static_cast<int>(r % n1), i0 = static_cast<int>(r / n1);
+    const int pos[3] = {i0, i1, i2};
+    bool keep = true;
+    for (int ax = 0; ax < 3; ++ax) {
+        const Axis& A = p.ax[ax];
+        const int L = a.lens[b * 3 + ax];
+        keep = keep && L >= A.k * A.dil && L <= A.len && !(!A.causal && A.dil == 1 && (A.k % 2) == 0 && A.k == L) &&
+               pos[ax] < L;
+    }
+    if (keep) return;
+    for (int t = 0; t < a.n; ++t) {
+        const PadTarget& g = a.t[t];
+        if (h >= g.heads) continue;
+        const long long row = b * g.lay.b + static_cast<long long>(i0) * g.lay.s0 +
+                              static_cast<long long>(i1) * g.lay.s1 + static_cast<long long>(i2) * g.lay.s2 +
+                              h * g.lay.h;
+        char* at = static_cast<char*>(g.base) + row * g.esz;
+        if (g.width == 1) {
+            *reinterpret_cast<float*>(at) = 0.f;
+        } else {
+            for (int c = 0; c < g.width * g.esz; c += 16) *reinterpret_cast<uint4*>(at + c) = make_uint4(0, 0, 0, 0);
+        }
+    }
+}
+
+hipError_t varlen_pad_zero(const Prob& p, const int* lens, std::initializer_list<PadTarget> targets, hipStream_t s) {
+    PadArgs a{};
+    a.p = p;
+    a.lens = lens;
+    for (const PadTarget& t : targets) a.t[a.n++] = t;
+    const long long n =
+        static_cast<long long>(p.B) * p.ax[0].len * p.ax[1].len * p.ax[2].len * (p.Hq > p.Hkv ? p.Hq : p.Hkv);
+    NA_LAUNCH("na_varlen_pad_zero", k_varlen_pad_zero, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+              a);
+    return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_varlen_fwd(const Prob& p, const int* lens, const void* q, Lay lq, const void* k, Lay lk,
+                             const void* v, Lay lv, void* o, Lay lo, float* lse, Lay ll, hipStream_t s) {
+    TileShape ts{};
+    if (!choose_tile(p, kForward, D, ts, 0, true)) return hipErrorInvalidValue;
+    const hipError_t e =
+        ts.rowshift > 5
+            ? run_fwd<T, D, kLayGeneral, true, false, true>(p, ts, q, lq, k, lk, v, lv, o, lo, lse, ll, nullptr, s, lens)
+            : run_fwd<T, D, kLayGeneral, false, false, true>(p, ts, q, lq, k, lk, v, lv, o, lo, lse, ll, nullptr, s,
+                                                             lens);
+    if (e != hipSuccess) return e;
+    return varlen_pad_zero(p, lens, {PadTarget{o, to_k(lo), p.Hq, p.Dv, 2}, PadTarget{lse, to_k(ll), p.Hq, 1, 4}}, s);
+}
+
+template <typename T, int D>
+hipError_t launch_varlen_bwd(const Prob& p, const int* lens, const void* q, Lay lq, const void* k, Lay lk,
+                             const void* v, Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse,
+                             Lay ll, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv, float* delta, Lay lde,
+                             hipStream_t s) {
+    TileShape tq{}, tk{};
+    if (!choose_tile(p, kBackwardQ, D, tq, 0, true) || !choose_tile(p, kBackwardKV, D, tk, 0, true))
+        return hipErrorInvalidValue;
+    hipError_t e = tq.rowshift > 5
+                       ? run_bwd_q<T, D, kLayGeneral, true, false, true>(p, tq, q, lq, k, lk, v, lv, o, lo, dout, ldo,
+                                                                         lse, ll, nullptr, Lay{}, dq, ldq, delta, lde,
+                                                                         nullptr, s, lens)
+                       : run_bwd_q<T, D, kLayGeneral, false, false, true>(p, tq, q, lq, k, lk, v, lv, o, lo, dout, ldo,
+                                                                          lse, ll, nullptr, Lay{}, dq, ldq, delta, lde,
+                                                                          nullptr, s, lens);
+    if (e != hipSuccess) return e;
+    e = tk.rowshift > 5 ? run_bwd_kv<T, D, kLayGeneral, true, true>(p, tk, q, lq, k, lk, v, lv, dout, ldo, lse, ll,
+                                                                     delta, lde, dk, ldk, dv, ldv, s, lens)
+                        : run_bwd_kv<T, D, kLayGeneral, false, true>(p, tk, q, lq, k, lk, v, lv, dout, ldo, lse, ll,
+                                                                      delta, lde, dk, ldk, dv, ldv, s, lens);
+    if (e != hipSuccess) return e;
+    return varlen_pad_zero(p, lens,
+                           {PadTarget{dq, to_k(ldq), p.Hq, p.Dqk, 2}, PadTarget{dk, to_k(ldk), p.Hkv, p.Dqk, 2},
+                            PadTarget{dv, to_k(ldv), p.Hkv, p.Dv, 2}, PadTarget{delta, to_k(lde), p.Hq, 1, 4}},
+                           s);
 }
 
 // Split kernels: one staged operand plus a row block per wave.  Heads of q
@@ -1582,7 +1738,18 @@ void audit_fused(LdsAudit& a) {
 }
 
 template <typename T, int D>
+void audit_varlen(LdsAudit& a) {
+    audit_one(k_fwd_mfma<T, D, kLayGeneral, false, false, true>, "k_fwd_mfma (varlen)", a);
+    audit_one(k_fwd_mfma<T, D, kLayGeneral, true, false, true>, "k_fwd_mfma (wide, varlen)", a);
+    audit_one(k_bwd_q_mfma<T, D, kLayGeneral, false, false, true>, "k_bwd_q_mfma (varlen)", a);
+    audit_one(k_bwd_q_mfma<T, D, kLayGeneral, true, false, true>, "k_bwd_q_mfma (wide, varlen)", a);
+    audit_one(k_bwd_kv_mfma<T, D, kLayGeneral, false, true>, "k_bwd_kv_mfma (varlen)", a);
+    audit_one(k_bwd_kv_mfma<T, D, kLayGeneral, true, true>, "k_bwd_kv_mfma (wide, varlen)", a);
+}
+
+template <typename T, int D>
 void audit_dim(LdsAudit& a) {
+    audit_varlen<T, D>(a);
     audit_one(k_fwd_mfma<T, D, kLayGeneral, false, true>, "k_fwd_mfma (global keys)", a);
     audit_one(k_fwd_mfma<T, D, kLayGeneral, true, true>, "k_fwd_mfma (wide, global keys)", a);
     audit_one(k_bwd_q_mfma<T, D, kLayGeneral, false, true>, "k_bwd_q_mfma (global keys)", a);
@@ -1609,6 +1776,7 @@ void audit_dim96(LdsAudit& a) {
     audit_fused<T, 96, kLayGeneral>(a);
     audit_fused<T, 96, kLayOne>(a);
     audit_fused<T, 96, kLayTwo>(a);
+    audit_varlen<T, 96>(a);
 }
 
 const LdsAudit& lds_audit() {
@@ -1735,6 +1903,58 @@ bool mfma_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward,
 }
 
 bool mfma_offsets_fit(const Prob& p, std::initializer_list<Lay> lays) { return offsets_fit(p, lays); }
+
+bool mfma_varlen_eligible(const Prob& p, int dtype, int D, bool aligned, bool backward) {
+    if (dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f) || !mfma_static_lds_ok()) return false;
+    if (p.Dqk != p.Dv || !(D == 32 || D == 64 || D == 96 || D == 128)) return false;
+    for (int a = 0; a < 3; ++a)
+        if (p.ax[a].st != 1) return false;
+    TileShape ts{};
+    if (!choose_tile(p, kForward, D, ts, 0, true) || grid_blocks(p, ts) >= (1LL << 31)) return false;
+    if (backward) {
+        if (!choose_tile(p, kBackwardQ, D, ts, 0, true) || grid_blocks(p, ts) >= (1LL << 31)) return false;
+        if (!choose_tile(p, kBackwardKV, D, ts, 0, true) || grid_blocks(p, ts) >= (1LL << 31)) return false;
+    }
+    // the padding kernel's grid: one thread per (batch, position, head)
+    return static_cast<long long>(p.B) * p.ax[0].len * p.ax[1].len * p.ax[2].len * (p.Hq > p.Hkv ? p.Hq : p.Hkv) <
+           (1LL << 31) * 255LL;
+}
+
+hipError_t mfma_varlen_forward(const Prob& p, const int* lens, const void* q, Lay lq, const void* k, Lay lk,
+                               const void* v, Lay lv, void* o, Lay lo, float* lse, Lay ll, int dtype, hipStream_t s) {
+#define NA_VFWD(T, DD) return launch_varlen_fwd<T, DD>(p, lens, q, lq, k, lk, v, lv, o, lo, lse, ll, s)
+    if (dtype == NATTEN_BF16) {
+        if (p.Dqk == 32) NA_VFWD(bf16, 32);
+        if (p.Dqk == 64) NA_VFWD(bf16, 64);
+        if (p.Dqk == 96) NA_VFWD(bf16, 96);
+        NA_VFWD(bf16, 128);
+    }
+    if (p.Dqk == 32) NA_VFWD(f16, 32);
+    if (p.Dqk == 64) NA_VFWD(f16, 64);
+    if (p.Dqk == 96) NA_VFWD(f16, 96);
+    NA_VFWD(f16, 128);
+#undef NA_VFWD
+}
+
+hipError_t mfma_varlen_backward(const Prob& p, const int* lens, const void* q, Lay lq, const void* k, Lay lk,
+                                const void* v, Lay lv, const void* o, Lay lo, const void* dout, Lay ldo,
+                                const float* lse, Lay ll, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
+                                float* delta, Lay lde, int dtype, hipStream_t s) {
+#define NA_VBWD(T, DD)                                                                                                 \
+    return launch_varlen_bwd<T, DD>(p, lens, q, lq, k, lk, v, lv, o, lo, dout, ldo, lse, ll, dq, ldq, dk, ldk, dv, ldv, \
+                                    delta, lde, s)
+    if (dtype == NATTEN_BF16) {
+        if (p.Dqk == 32) NA_VBWD(bf16, 32);
+        if (p.Dqk == 64) NA_VBWD(bf16, 64);
+        if (p.Dqk == 96) NA_VBWD(bf16, 96);
+        NA_VBWD(bf16, 128);
+    }
+    if (p.Dqk == 32) NA_VBWD(f16, 32);
+    if (p.Dqk == 64) NA_VBWD(f16, 64);
+    if (p.Dqk == 96) NA_VBWD(f16, 96);
+    NA_VBWD(f16, 128);
+#undef NA_VBWD
+}
 
 hipError_t mfma_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
                         Lay lo, float* lse, Lay ll, int dtype, hipStream_t s, const GlobalSet* g) {

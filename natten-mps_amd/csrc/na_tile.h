@@ -252,9 +252,16 @@ __host__ __device__ inline void spatial_coords(const TileShape& ts, int s, int (
 // tile's record is read with scalar loads; without one the per-axis work
 // runs with one axis per lane (lanes 0, 1, 2) and is read back into scalar
 // registers.  False: empty tile.
-template <bool KEY>
+//
+// Variable-length problems (VARLEN, lens = int32 [batch][3] sample extents,
+// no table): p and ts describe the padded extents; the sample's own extent
+// takes the padded one's place in the geometry (with len % dil to match), so
+// tiles past it are empty, and a sample whose extents are out of range
+// (below kernel * dilation, above the padded extent, or an even kernel equal
+// to a non-causal, undilated extent) has no tiles at all.
+template <bool KEY, bool VARLEN = false>
 __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts, const int* __restrict__ geo,
-                                              int wave, Block& k, WaveGeo& g) {
+                                              int wave, Block& k, WaveGeo& g, const int* __restrict__ lens = nullptr) {
     int x = xcd_block(blockIdx.x, gridDim.x);
     int q = fdiv(x, ts.hchunks);
     k.h0 = (x - q * static_cast<int>(ts.hchunks.d)) * ts.h_per;
@@ -263,8 +270,21 @@ __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts
     q = fdiv(x, ts.spatial);
     const int s = x - q * static_cast<int>(ts.spatial.d);
     k.b = q;
+    int vlen[3], vmod[3];
+    if constexpr (VARLEN) {
+        bool ok = true;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            const Axis& A = p.ax[a];
+            const int L = __builtin_amdgcn_readfirstlane(lens[k.b * 3 + a]);
+            ok = ok && L >= A.k * A.dil && L <= A.len && !(!A.causal && A.dil == 1 && (A.k % 2) == 0 && A.k == L);
+            vlen[a] = L;
+            vmod[a] = L - fdiv(L, ts.dil[a]) * A.dil;
+        }
+        if (!ok) return false;
+    }
 
-    if (geo) {
+    if (!VARLEN && geo) {
         const int* rec = geo + s * kRecDwords;
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
@@ -301,13 +321,13 @@ __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts
     const int lane = threadIdx.x & 63;
     const bool l0 = lane == 0, l1 = lane == 1;
 #define NA_PICK(field) (l0 ? (field(0)) : l1 ? (field(1)) : (field(2)))
-#define F_LEN(a) p.ax[a].len
+#define F_LEN(a) (VARLEN ? vlen[a] : p.ax[a].len)
 #define F_K(a) p.ax[a].k
 #define F_DIL(a) p.ax[a].dil
 #define F_CAUSAL(a) p.ax[a].causal
 #define F_ST(a) p.ax[a].st
-#define F_OUT(a) p.ax[a].out
-#define F_LENMOD(a) ts.lenmod[a]
+#define F_OUT(a) (VARLEN ? vlen[a] : p.ax[a].out)
+#define F_LENMOD(a) (VARLEN ? vmod[a] : ts.lenmod[a])
 #define F_T(a) ts.T[a]
 #define F_DMUL(a) ts.dil[a].mul
 #define F_DSH(a) ts.dil[a].shift
@@ -706,6 +726,7 @@ struct FwdArgs {
     float* lse;
     LayK lq, lk, lv, lo, ll;
     GlobalKeys<T> gk;
+    const int* lens;  // variable-length instances: int32 [batch][3] sample extents
 };
 
 template <typename T>
@@ -719,6 +740,7 @@ struct BwdQArgs {
     float* delta;
     LayK lq, lk, lv, lo, ldo, ll, ldl, ldq, lde;
     GlobalKeys<T> gk;
+    const int* lens;
 };
 
 template <typename T>
@@ -730,6 +752,7 @@ struct BwdKvArgs {
     const float *lse, *delta;
     T *dk, *dv;
     LayK lq, lk, lv, ldo, ll, lde, ldk, ldv;
+    const int* lens;
 };
 
 // Split products: weights w (rows of KV entries), staged operand x, out.
@@ -743,6 +766,29 @@ struct WsumArgs {
     LayK lw, lx, lo;
     float mul;
 };
+
+// Variable-length problems, for the exact recomputation: the problem and
+// tile shape with sample b's own extents (lens[b * 3 + a]) in place of the
+// padded ones (and len % dil to match), b from the XCD-remapped workgroup
+// index x.  False when the sample's extents are out of range (the rule of
+// tile_geometry).  The walks themselves keep the padded problem and take the
+// sample's extents in tile_geometry only.
+__device__ __forceinline__ bool varlen_view(const Prob& p0, const TileShape& ts0, const int* __restrict__ lens, int x,
+                                            Prob& p, TileShape& ts) {
+    const int b = fdiv(fdiv(x, ts0.hchunks), ts0.spatial);
+    p = p0;
+    ts = ts0;
+    bool ok = true;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const Axis& A = p0.ax[a];
+        const int L = __builtin_amdgcn_readfirstlane(lens[b * 3 + a]);
+        ok = ok && L >= A.k * A.dil && L <= A.len && !(!A.causal && A.dil == 1 && (A.k % 2) == 0 && A.k == L);
+        p.ax[a].len = p.ax[a].out = L;
+        ts.lenmod[a] = L - fdiv(L, ts0.dil[a]) * A.dil;
+    }
+    return ok;
+}
 
 // The lane's item from the (XCD-remapped) workgroup index x alone (the
 // decode of tile_geometry without the unions): batch, the workgroup's run of
@@ -852,6 +898,58 @@ int union_extent(const Axis& A, int T, bool key_tile) {
             if (hi - lo + 1 > best) best = hi - lo + 1;
         }
     }
+    return best;
+}
+
+// Largest union extent on one axis over every extent from K * dil up to
+// A.len (the samples of a variable-length problem; the same spans
+// axis_geometry computes for each tile).  A tile's union depends on the
+// extent only through the windows it meets at the axis ends, so per extent
+// the tiles within 2K + 2T of either end are evaluated, plus one interior
+// tile; the result is cached per (axis, tile extent, side).
+int union_extent_upto(const Axis& A, int T, bool key_tile) {
+    struct Entry {
+        int len, k, dil, causal, T, key, u;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    {
+        std::lock_guard<std::mutex> g(mu);
+        for (const Entry& e : cache)
+            if (e.len == A.len && e.k == A.k && e.dil == A.dil && e.causal == A.causal && e.T == T &&
+                e.key == (key_tile ? 1 : 0))
+                return e.u;
+    }
+    int best = 1;
+    const int reach = 2 * A.k + 2 * T;
+    for (int L = A.k * A.dil; L <= A.len; ++L) {
+        Axis B = A;
+        B.len = B.out = L;
+        for (int r = 0; r < B.dil && r < L; ++r) {
+            const ClassAxis c = class_axis(B, r);
+            const auto span = [&](int J) {
+                const int jend = (J + T < c.n ? J + T : c.n) - 1;
+                int lo, hi, x;
+                if (!key_tile) {
+                    lo = class_ws(c, J);
+                    lo = lo > 0 ? lo : 0;
+                    hi = class_ws(c, jend) + c.K - 1;
+                    hi = hi < c.n - 1 ? hi : c.n - 1;
+                } else {
+                    class_span(c, J, lo, x);
+                    class_span(c, jend, x, hi);
+                }
+                if (hi - lo + 1 > best) best = hi - lo + 1;
+            };
+            const int ntiles = (c.n + T - 1) / T;
+            for (int t = 0; t < ntiles; ++t) {
+                const int J = t * T;
+                if (J < reach || J + T > c.n - reach || t == ntiles / 2) span(J);
+            }
+        }
+    }
+    std::lock_guard<std::mutex> g(mu);
+    cache.push_back(Entry{A.len, A.k, A.dil, A.causal, T, key_tile ? 1 : 0, best});
     return best;
 }
 

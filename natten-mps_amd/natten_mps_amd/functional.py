@@ -372,15 +372,19 @@ def na3d_av(attn, value, kernel_size, dilation=1, *, stride=1, is_causal=False):
 # ---------------------------------------------------------------------------
 
 
-def _validate_seq_lens(seq_lens: torch.Tensor, batch_size: int, l_max: int, kernel_size: int) -> None:
-    """``functional.py:678-700``."""
+def _validate_seq_lens(seq_lens: torch.Tensor, batch_size: int, l_max: int, kernel_size: int,
+                       rows=None) -> None:
+    """``functional.py:678-700``.  ``rows``: the lengths already on the host
+    (``seq_lens.tolist()``), so that a device tensor is read back once."""
     if seq_lens.ndim != 1 or seq_lens.shape[0] != batch_size:
         raise ValueError(
             f"seq_lens must be a 1-D tensor of length B={batch_size}, got shape {tuple(seq_lens.shape)}.")
     if seq_lens.dtype not in (torch.int32, torch.int64):
         raise ValueError(f"seq_lens must be int32 or int64, got {seq_lens.dtype}.")
-    min_len = int(seq_lens.min().item())
-    max_len = int(seq_lens.max().item())
+    if rows is None:
+        rows = seq_lens.tolist()
+    min_len = int(min(rows))
+    max_len = int(max(rows))
     if min_len < kernel_size:
         raise ValueError(
             f"All seq_lens must be >= kernel_size ({kernel_size}), but min(seq_lens)={min_len}.")
@@ -389,15 +393,18 @@ def _validate_seq_lens(seq_lens: torch.Tensor, batch_size: int, l_max: int, kern
 
 
 def _validate_spatial_sizes(spatial_sizes: torch.Tensor, batch_size: int, max_spatial: tuple, kernel_size: tuple,
-                            rank: int) -> None:
-    """``functional.py:757-787``."""
+                            rank: int, rows=None) -> None:
+    """``functional.py:757-787``.  ``rows``: the sizes already on the host
+    (``spatial_sizes.tolist()``), so that a device tensor is read back once."""
     if spatial_sizes.ndim != 2 or spatial_sizes.shape[0] != batch_size or spatial_sizes.shape[1] != rank:
         raise ValueError(f"spatial_sizes must be a [B, {rank}] tensor, got shape {tuple(spatial_sizes.shape)}.")
     if spatial_sizes.dtype not in (torch.int32, torch.int64):
         raise ValueError(f"spatial_sizes must be int32 or int64, got {spatial_sizes.dtype}.")
+    if rows is None:
+        rows = spatial_sizes.tolist()
     for d in range(rank):
-        min_dim = int(spatial_sizes[:, d].min().item())
-        max_dim = int(spatial_sizes[:, d].max().item())
+        min_dim = int(min(r[d] for r in rows))
+        max_dim = int(max(r[d] for r in rows))
         if min_dim < kernel_size[d]:
             raise ValueError(
                 f"All spatial_sizes[:,{d}] must be >= kernel_size[{d}] ({kernel_size[d]}), but min={min_dim}.")
@@ -449,13 +456,17 @@ def _varlen(rank, query, key, value, sizes, kernel_size, dilation, scale):
     ks = normalize_kernel_size(kernel_size, rank)
     dil = normalize_tuple_param(dilation, rank, "dilation")
     max_sp = tuple(query.shape[1:1 + rank])
+    # the sizes are read back once (one device synchronisation when they
+    # live on the device) and every host-side check works on that copy
+    host = sizes.tolist() if sizes.ndim in (1, 2) and sizes.dtype in (torch.int32, torch.int64) else None
     if rank == 1:
-        _validate_seq_lens(sizes, B, max_sp[0], ks[0])
+        _validate_seq_lens(sizes, B, max_sp[0], ks[0], rows=host)
     else:
-        _validate_spatial_sizes(sizes, B, max_sp, ks, rank)
+        _validate_spatial_sizes(sizes, B, max_sp, ks, rank, rows=host)
     sizes2 = sizes.reshape(B, rank)
+    rows = [[int(x)] for x in host] if rank == 1 else [[int(x) for x in r] for r in host]
     # a sample's extent must hold the dilated kernel, as na*d on its slice requires
-    for ext in {tuple(int(x) for x in row) for row in sizes2.tolist()}:
+    for ext in {tuple(row) for row in rows}:
         check_dilation_kernel_vs_input(dil, ks, ext)
     scale_value = query.shape[-1] ** -0.5 if scale is None else float(scale)
 
@@ -466,7 +477,7 @@ def _varlen(rank, query, key, value, sizes, kernel_size, dilation, scale):
     out = _NAVarlenFunction.apply(rank, mod, query, key, value, sizes2, ks, dil, scale_value)
     # samples with every extent equal to its (even) kernel take the full-window
     # path of na*d, whose windows the neighbourhood rule does not describe
-    full = [b for b, row in enumerate(sizes2.tolist())
+    full = [b for b, row in enumerate(rows)
             if all(n == k for n, k in zip(row, ks)) and any(k % 2 == 0 for k in ks)]
     if full:
         out = out.clone()

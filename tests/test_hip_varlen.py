@@ -92,6 +92,59 @@ def test_varlen_backward_matches_oracle(case):
             assert (g[b][mask] == 0).all()
 
 
+# bf16 / fp16 with head dims 32-128: the MFMA tile kernels' variable-length
+# instances (sample extents read in the kernels, padding zeroed by a second
+# launch).
+TILE_CASES = [
+    # rank, padded shape [B, *sp, H, D], per-sample sizes, kernel, dilation, scale
+    (1, (3, 70, 4, 64), [[70], [41], [19]], (7,), (1,), None),
+    (1, (2, 300, 2, 32), [[300], [133]], (33,), (2,), 0.2),
+    (1, (2, 40, 2, 32), [[40], [26]], (6,), (1,), None),
+    (2, (3, 20, 24, 2, 32), [[20, 24], [13, 9], [7, 16]], (5, 7), (1, 1), None),
+    (2, (2, 16, 18, 4, 128), [[16, 18], [11, 12]], (3, 5), (1, 2), None),
+    (2, (2, 14, 14, 2, 96), [[14, 14], [9, 10]], (3, 3), (1, 1), None),
+    (3, (2, 8, 10, 12, 2, 64), [[8, 10, 12], [5, 6, 9]], (3, 3, 5), (1, 1, 1), None),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", TILE_CASES, ids=lambda c: f"{c[0]}d-D{c[1][-1]}-{c[2]}")
+def test_varlen_tile_path(case, dtype):
+    """Forward and all three gradients of the MFMA variable-length path
+    against the oracle's per-sample composition in fp32 on the same rounded
+    inputs; outputs and gradients exactly zero at padding."""
+    from natten_mps_amd._core import _lib
+
+    rank, shape, sizes, ks, dil, scale = case
+    q, k, v, do = _inputs(31, shape, dtype)
+    sz = torch.tensor(sizes, dtype=torch.int32)
+    arg = sz[:, 0] if rank == 1 else sz
+    leaves = [t.to(DEV).requires_grad_(True) for t in (q, k, v)]
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        out = _fn(rank)(*leaves, arg.to(DEV), kernel_size=ks, dilation=dil, scale=scale)
+        out.backward(do.to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    launched = set(_lib.profile_read(reset=True))
+    assert {"na_varlen_fwd_mfma", "na_varlen_bwd_q_mfma", "na_varlen_bwd_kv_mfma", "na_varlen_pad_zero"} <= launched, \
+        launched
+    ref_leaves = [t.float().requires_grad_(True) for t in (q, k, v)]
+    ref = ORACLE[rank](*ref_leaves, sz, ks, dil, scale)
+    ref.backward(do.float())
+    got = [out.detach().cpu()] + [t.grad.cpu() for t in leaves]
+    want = [ref.detach()] + [t.grad for t in ref_leaves]
+    for name, a, b in zip(("out", "dq", "dk", "dv"), got, want):
+        assert_parity(a, b, dtype, f"varlen {name}")
+    for b, ext in enumerate(sizes):  # padding exactly zero
+        mask = torch.ones(shape[1:1 + rank], dtype=torch.bool)
+        mask[tuple(slice(0, n) for n in ext)] = False
+        for g in got:
+            assert (g[b][mask] == 0).all()
+
+
 def test_varlen_uniform_sizes_equal_na_on_gpu():
     """All sizes at the maximum: na2d_varlen == na2d (the reference's
     test_uniform_sizes)."""

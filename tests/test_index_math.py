@@ -67,6 +67,40 @@ def test_tile_geometry_against_brute_force(host_idx):
     assert n > 1000
 
 
+@pytest.fixture(scope="module")
+def host_union():
+    os.makedirs(BUILD, exist_ok=True)
+    out = os.path.join(BUILD, "libunion_host.so")
+    subprocess.run(["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O1", "-std=c++17", "-fPIC", "-shared",
+                    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                    "-I" + os.path.join(ROOT, "include"), "-I" + os.path.join(ROOT, "natten-mps_amd", "csrc"),
+                    os.path.join(ROOT, "tests", "native", "union_host.hip"), "-o", out], check=True)
+    lib = ctypes.CDLL(out)
+    lib.host_union_upto_undersized.argtypes = [ctypes.c_int] * 6
+    lib.host_union_upto_undersized.restype = ctypes.c_int
+    return lib
+
+
+def test_varlen_tile_sizing_covers_every_sample_extent(host_union):
+    """The variable-length tile kernels size LDS for the largest union any
+    tile can have at any sample extent up to the padded one
+    (union_extent_upto): checked against brute force over axis_geometry at
+    every extent, for query and key tiles, all residues, causal and not."""
+    n = 0
+    for Lmax in (5, 9, 16, 23, 40, 61):
+        for K in (2, 3, 4, 5, 7, 9):
+            for d in (1, 2, 3):
+                if K * d > Lmax:
+                    continue
+                for causal in (0, 1):
+                    for T in (1, 2, 8, 16, 64):
+                        for key in (0, 1):
+                            assert host_union.host_union_upto_undersized(Lmax, K, d, causal, T, key) == 0, \
+                                (Lmax, K, d, causal, T, key)
+                            n += 1
+    assert n > 1000
+
+
 def test_fastdiv_matches_integer_division(host_idx):
     """The multiply-high division the tile kernels decode workgroup indices
     with equals n // d: every n below 2^20 for d <= 300 and every power of
