@@ -439,21 +439,52 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) vo
 // serve lanes whose row test fails.  Runs over (batch, kv head) pairs; the
 // walk's slices cover the GQA group's q heads one after the other.
 // ---------------------------------------------------------------------------
-template <typename T>
-__device__ __forceinline__ void stage_scalars(const Prob& p, const Block& k, const TileShape& ts, int b, int h,
-                                              int p0, const float* __restrict__ lse, const LayK& ll,
-                                              const float* __restrict__ delta, const LayK& lde, float* NL,
-                                              float* ND) {
-    const int d1 = p.ax[1].dil, d2 = p.ax[2].dil, mask2 = (1 << ts.rowshift) - 1;
-    const float* lb = bh_ptr(lse, ll, b, h) + p0 * ll.s0;
-    const float* db = bh_ptr(delta, lde, b, h) + p0 * lde.s0;
-    for (int s = threadIdx.x; s < ts.slots; s += blockDim.x) {
-        const int a1 = s >> ts.rowshift, a2 = s & mask2;
+// One slice's per-slot scalars in two steps, so that their loads travel with
+// the slice's staging loads instead of after them: scalar_loads issues the
+// loads of slot threadIdx.x (for slots outside the union an unconditional
+// load of a valid position, the union's first, so that both loads are in
+// flight together), scalar_store writes the values once the loads have
+// landed and handles the slots past the workgroup's threads (unions of more
+// slots than threads) with ordinary dependent loads.
+struct SlotScalars {
+    float nl, nd;
+};
+
+__device__ __forceinline__ void slot_position(const Prob& p, const Block& k, const TileShape& ts, int s, bool& in,
+                                              int& p1, int& p2) {
+    const int a1 = s >> ts.rowshift, a2 = s & ((1 << ts.rowshift) - 1);
+    in = s < ts.slots && a1 < k.U[1] && a2 < k.U[2];
+    p1 = k.r[1] + (k.lo[1] + (in ? a1 : 0)) * p.ax[1].dil;
+    p2 = k.r[2] + (k.lo[2] + (in ? a2 : 0)) * p.ax[2].dil;
+}
+
+__device__ __forceinline__ SlotScalars scalar_loads(const Prob& p, const Block& k, const TileShape& ts, int b, int h,
+                                                    int p0, const float* __restrict__ lse, const LayK& ll,
+                                                    const float* __restrict__ delta, const LayK& lde) {
+    bool in;
+    int p1, p2;
+    slot_position(p, k, ts, threadIdx.x, in, p1, p2);
+    const float l = (bh_ptr(lse, ll, b, h) + p0 * ll.s0)[p1 * ll.s1 + p2 * ll.s2];
+    const float d = (bh_ptr(delta, lde, b, h) + p0 * lde.s0)[p1 * lde.s1 + p2 * lde.s2];
+    return SlotScalars{in ? -l * kLog2e : 0.f, in ? -d : 0.f};
+}
+
+__device__ __forceinline__ void scalar_store(const Prob& p, const Block& k, const TileShape& ts, int b, int h, int p0,
+                                             const float* __restrict__ lse, const LayK& ll,
+                                             const float* __restrict__ delta, const LayK& lde, SlotScalars sc,
+                                             float* NL, float* ND) {
+    if (static_cast<int>(threadIdx.x) < ts.slots) {
+        NL[threadIdx.x] = sc.nl;
+        ND[threadIdx.x] = sc.nd;
+    }
+    for (int s = threadIdx.x + blockDim.x; s < ts.slots; s += blockDim.x) {
+        bool in;
+        int p1, p2;
+        slot_position(p, k, ts, s, in, p1, p2);
         float nl = 0.f, nd = 0.f;
-        if (a1 < k.U[1] && a2 < k.U[2]) {
-            const int p1 = k.r[1] + (k.lo[1] + a1) * d1, p2 = k.r[2] + (k.lo[2] + a2) * d2;
-            nl = -lb[p1 * ll.s1 + p2 * ll.s2] * kLog2e;
-            nd = -db[p1 * lde.s1 + p2 * lde.s2];
+        if (in) {
+            nl = -(bh_ptr(lse, ll, b, h) + p0 * ll.s0)[p1 * ll.s1 + p2 * ll.s2] * kLog2e;
+            nd = -(bh_ptr(delta, lde, b, h) + p0 * lde.s0)[p1 * lde.s1 + p2 * lde.s2];
         }
         NL[s] = nl;
         ND[s] = nd;
@@ -551,13 +582,16 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdKV, D, WIDE) v
     Walk w;
     walk_start(blk, w);
     const int nsl = rep * blk.U[0];
-    stage_pair<T, D>(p, blk, ts, sm, plane_of(q, lq, w.b, w.h * rep, slice_pos(p, blk, 0)), lq, Qs,
-                     plane_of(dout, ldo, w.b, w.h * rep, slice_pos(p, blk, 0)), ldo, Gs, wave);
+    // the staged slice's head and axis-0 position (its scalars are stored
+    // after the wait that precedes the slice's chunks)
+    int st_h = w.h * rep, st_p0 = slice_pos(p, blk, 0);
+    SlotScalars sc = scalar_loads(p, blk, ts, w.b, st_h, st_p0, lse, ll, delta, lde);
+    stage_pair<T, D>(p, blk, ts, sm, plane_of(q, lq, w.b, st_h, st_p0), lq, Qs, plane_of(dout, ldo, w.b, st_h, st_p0),
+                     ldo, Gs, wave);
     if (threadIdx.x < 8) NL[slots + threadIdx.x] = -INFINITY;
     const float sc2 = p.scale * kLog2e;
     f32x4_t cb[2];
     if constexpr (!WIDE) column_bias(ln, ts.rowshift, 0, grp, cb);
-    stage_scalars<T>(p, blk, ts, w.b, w.h * rep, slice_pos(p, blk, 0), lse, ll, delta, lde, NL, ND);
 
     uint4 kf[D / 32], vf[D / 32];
     f32x4_t gk[D / 16], gv[D / 16];
@@ -575,6 +609,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdKV, D, WIDE) v
             }
         }
         wait_loads();
+        scalar_store(p, blk, ts, b, st_h, st_p0, lse, ll, delta, lde, sc, NL, ND);
         lds_publish_barrier();  // staged rows and the slice's -lse / -delta
         if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
@@ -615,19 +650,22 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdKV, D, WIDE) v
             more = ++w.h < blk.h1;
             fresh = true;
         }
-        __syncthreads();  // the slice is no longer read
-        if (more) {
-            const int h = w.h * rep + sl / blk.U[0], p0 = slice_pos(p, blk, sl % blk.U[0]);
-            stage_pair<T, D>(p, blk, ts, sm, plane_of(q, lq, w.b, h, p0), lq, Qs, plane_of(dout, ldo, w.b, h, p0),
-                             ldo, Gs, wave);
-            stage_scalars<T>(p, blk, ts, w.b, h, p0, lse, ll, delta, lde, NL, ND);
-        }
+        // a finished pair's results go out first, so that its accumulators
+        // are dead while the next slice's loads are issued
         if (fresh) {
             redo = redo || (item_nonfinite(lane_sum(gk, lane_sum(gv, 0.f))) && ln.valid);
             if (ln.valid) {
                 store_rows<T, D>(bh_ptr(dk, ldk, b, hk), vol_off(ldk, ln.pos), grp, gk, p.scale);
                 store_rows<T, D>(bh_ptr(dv, ldv, b, hk), vol_off(ldv, ln.pos), grp, gv, 1.f);
             }
+        }
+        __syncthreads();  // the slice is no longer read
+        if (more) {
+            st_h = w.h * rep + sl / blk.U[0];
+            st_p0 = slice_pos(p, blk, sl % blk.U[0]);
+            sc = scalar_loads(p, blk, ts, w.b, st_h, st_p0, lse, ll, delta, lde);
+            stage_pair<T, D>(p, blk, ts, sm, plane_of(q, lq, w.b, st_h, st_p0), lq, Qs,
+                             plane_of(dout, ldo, w.b, st_h, st_p0), ldo, Gs, wave);
         }
     }
     if (redo) redo_bwd_kv<T, D, LAY, WIDE, VARLEN>(kernargs(), xcd_block(blockIdx.x, gridDim.x), wave, col, grp);
