@@ -106,6 +106,27 @@ def step_bytes(B, N, Hq, Hkv, D, esz, backward):
     return fwd + (bwd if backward else 0)
 
 
+def copy_bandwidth(torch, nbytes, cycles_per_ms, reps=20):
+    """Measured HBM bandwidth of a plain device copy that moves nbytes in
+    total (nbytes / 2 read, nbytes / 2 written), the practical ceiling a
+    kernel of that many bytes is compared with next to the 8 TB/s spec:
+    HIP events around reps copies queued behind a GPU spin."""
+    n = max(nbytes // 4, 1)
+    src = torch.ones(n, dtype=torch.bfloat16, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2.0 * cycles_per_ms))
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    return 2 * n * 2 / (a.elapsed_time(b) / reps * 1e-3) / 1e9
+
+
 def measured_traffic(kernel, workload):
     """HBM bytes per launch from profiles/traffic.txt ("kernel workload bytes")."""
     path = os.path.join(ROOT, "profiles", "traffic.txt")
@@ -451,9 +472,13 @@ def main():
     roof = None
     if nbytes is not None:
         gbs = nbytes / mean_s / 1e9
+        copy_gbs = copy_bandwidth(torch, nbytes, cycles_per_ms)
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_name, workload),
-                "kernel": dom_name, "mean_us": round(mean_s * 1e6, 2), "alg_bytes": nbytes}
+                "kernel": dom_name, "mean_us": round(mean_s * 1e6, 2), "alg_bytes": nbytes,
+                "copy_gbs": round(copy_gbs, 1), "frac_of_copy": round(gbs / copy_gbs, 4)}
+        _log(f"device copy moving the kernel's {nbytes / 1e6:.1f} MB: {copy_gbs:.0f} GB/s "
+             f"({copy_gbs / HBM_PEAK_GBS:.1%} of 8 TB/s); {dom_name} reaches {gbs / copy_gbs:.1%} of it")
     # MFMA utilisation of the fused tile kernels, on useful work: the MFMA
     # products each kernel needs per valid (query, key) pair and head dim --
     # forward q.k and p.v (4 flops), dQ kernel q.k, dO.v, dS.k (6), dK/dV
