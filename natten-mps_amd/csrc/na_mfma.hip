@@ -94,7 +94,10 @@ __device__ __forceinline__ void redo_fwd(const void* kargs, int wg, int wave, in
     }
 }
 
-template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN = false>
+// FLAT: every workgroup runs one (batch, head) over one slice (axis 0 of
+// extent 1, one head per workgroup): the walk has one step, and its
+// bookkeeping compiles away.
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN = false, bool FLAT = false>
 __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernFwd, D, WIDE) void k_fwd_mfma(FwdArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
@@ -194,8 +197,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernFwd, D, WIDE) voi
             };
             chunks(std::integral_constant<bool, WIDE>{});
         }
-        more = walk_next(blk, w, fresh);
-        __syncthreads();  // the slice is no longer read
+        if constexpr (FLAT) {
+            more = false;
+        } else {
+            more = walk_next(blk, w, fresh);
+            __syncthreads();  // the slice is no longer read
+        }
         if constexpr (GLOBAL) {
             // the finished head's global keys, 32 at a time, continue the
             // same online softmax (every key valid up to n)
@@ -290,7 +297,8 @@ __device__ __forceinline__ void redo_bwd_q(const void* kargs, int wg, int wave, 
     }
 }
 
-template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN = false>
+// FLAT as for k_fwd_mfma.
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN = false, bool FLAT = false>
 __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_mfma(BwdQArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
@@ -389,8 +397,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) vo
             };
             chunks(std::integral_constant<bool, WIDE>{});
         }
-        more = walk_next(blk, w, fresh);
-        __syncthreads();  // the slice is no longer read
+        if constexpr (FLAT) {
+            more = false;
+        } else {
+            more = walk_next(blk, w, fresh);
+            __syncthreads();  // the slice is no longer read
+        }
         if constexpr (GLOBAL) {
             // the finished head's global keys, 32 at a time
             if (fresh || !more) {
@@ -531,7 +543,9 @@ __device__ __forceinline__ void redo_bwd_kv(const void* kargs, int wg, int wave,
     }
 }
 
-template <typename T, int D, int LAY, bool WIDE, bool VARLEN = false>
+// FLAT: one slice and one (batch, kv head) per workgroup with one q head
+// per kv head (axis 0 of extent 1, no GQA): the walk has one step.
+template <typename T, int D, int LAY, bool WIDE, bool VARLEN = false, bool FLAT = false>
 __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdKV, D, WIDE) void k_bwd_kv_mfma(BwdKvArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
@@ -644,11 +658,15 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdKV, D, WIDE) v
             chunks(std::integral_constant<bool, WIDE>{});
         }
         // next slice: within the pair (q heads x axis-0 slices), else the next pair
-        fresh = false;
-        if (++sl >= nsl) {
-            sl = 0;
-            more = ++w.h < blk.h1;
-            fresh = true;
+        if constexpr (FLAT) {
+            more = false;
+        } else {
+            fresh = false;
+            if (++sl >= nsl) {
+                sl = 0;
+                more = ++w.h < blk.h1;
+                fresh = true;
+            }
         }
         // a finished pair's results go out first, so that its accumulators
         // are dead while the next slice's loads are issued
@@ -659,7 +677,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdKV, D, WIDE) v
                 store_rows<T, D>(bh_ptr(dv, ldv, b, hk), vol_off(ldv, ln.pos), grp, gv, 1.f);
             }
         }
-        __syncthreads();  // the slice is no longer read
+        if constexpr (!FLAT) __syncthreads();  // the slice is no longer read
         if (more) {
             st_h = w.h * rep + sl / blk.U[0];
             st_p0 = slice_pos(p, blk, sl % blk.U[0]);
@@ -1421,14 +1439,31 @@ GlobalKeys<T> to_global(const GlobalSet* g) {
     return r;
 }
 
+// A launch whose workgroups each walk a single step (FLAT instances): axis 0
+// of extent 1 (one slice per tile), one head per workgroup, and for key
+// tiles one q head per kv head.  Built for the shared layout groups with
+// rows of at most 32 slots.
+template <int LAY, bool WIDE, bool GLOBAL, bool VARLEN>
+constexpr bool kHasFlat = !WIDE && !GLOBAL && !VARLEN && LAY != kLayGeneral;
+
+bool flat_walk(const Prob& p, const TileShape& ts, bool key_tile) {
+    return p.ax[0].len == 1 && p.ax[0].k == 1 && ts.h_per == 1 && (!key_tile || p.rep == 1);
+}
+
 template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN = false>
 hipError_t run_fwd(const Prob& p, TileShape ts, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
                    void* o, Lay lo, float* lse, Lay ll, const GlobalSet* g, hipStream_t s, const int* lens = nullptr) {
-    const auto kern = k_fwd_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN>;
+    auto kern = k_fwd_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN>;
     const size_t shm = lds_bytes(kForward, ts.slots, D) + (GLOBAL ? global_lds(D) : 0);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    if constexpr (kHasFlat<LAY, WIDE, GLOBAL, VARLEN>) {
+        if (flat_walk(p, ts, false)) {
+            kern = k_fwd_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN, true>;
+            if ((e = allow_lds(kern, shm)) != hipSuccess) return e;
+        }
+    }
     const int* geo = VARLEN ? nullptr : geometry_table(p, ts, false, s);
     const FwdArgs<T> a{p,   ts,       geo,      (const T*)q, (const T*)k, (const T*)v, (T*)o,
                        lse, to_k(lq), to_k(lk), to_k(lv),    to_k(lo),    to_k(ll),    to_global<T>(g), lens};
@@ -1466,11 +1501,17 @@ hipError_t run_bwd_q(const Prob& p, TileShape ts, const void* q, Lay lq, const v
                      Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                      const float* dlse, Lay ldl, void* dq, Lay ldq, float* delta, Lay lde, const GlobalSet* g,
                      hipStream_t s, const int* lens = nullptr) {
-    const auto kern = k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN>;
+    auto kern = k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN>;
     const size_t shm = lds_bytes(kBackwardQ, ts.slots, D) + (GLOBAL ? global_lds(D) : 0);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    if constexpr (kHasFlat<LAY, WIDE, GLOBAL, VARLEN>) {
+        if (flat_walk(p, ts, false)) {
+            kern = k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN, true>;
+            if ((e = allow_lds(kern, shm)) != hipSuccess) return e;
+        }
+    }
     const int* geo = VARLEN ? nullptr : geometry_table(p, ts, false, s);
     const BwdQArgs<T> a{p,        ts,       geo,      (const T*)q, (const T*)k, (const T*)v, (const T*)o,
                         (const T*)dout, lse, dlse,  (T*)dq,      delta,       to_k(lq),    to_k(lk),
@@ -1485,11 +1526,17 @@ template <typename T, int D, int LAY, bool WIDE, bool VARLEN = false>
 hipError_t run_bwd_kv(const Prob& p, TileShape ts, const void* q, Lay lq, const void* k, Lay lk, const void* v,
                       Lay lv, const void* dout, Lay ldo, const float* lse, Lay ll, const float* delta, Lay lde,
                       void* dk, Lay ldk, void* dv, Lay ldv, hipStream_t s, const int* lens = nullptr) {
-    const auto kern = k_bwd_kv_mfma<T, D, LAY, WIDE, VARLEN>;
+    auto kern = k_bwd_kv_mfma<T, D, LAY, WIDE, VARLEN>;
     const size_t shm = lds_bytes(kBackwardKV, ts.slots, D);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    if constexpr (kHasFlat<LAY, WIDE, false, VARLEN>) {
+        if (flat_walk(p, ts, true)) {
+            kern = k_bwd_kv_mfma<T, D, LAY, WIDE, VARLEN, true>;
+            if ((e = allow_lds(kern, shm)) != hipSuccess) return e;
+        }
+    }
     const int* geo = VARLEN ? nullptr : geometry_table(p, ts, true, s);
     const BwdKvArgs<T> a{p,        ts,       geo,       (const T*)q, (const T*)k, (const T*)v, (const T*)dout,
                          lse,      delta,    (T*)dk,    (T*)dv,      to_k(lq),    to_k(lk),    to_k(lv),
@@ -1773,6 +1820,11 @@ void audit_fused(LdsAudit& a) {
     audit_one(k_bwd_q_mfma<T, D, LAY, true, false>, "k_bwd_q_mfma (wide)", a);
     audit_one(k_bwd_kv_mfma<T, D, LAY, false>, "k_bwd_kv_mfma", a);
     audit_one(k_bwd_kv_mfma<T, D, LAY, true>, "k_bwd_kv_mfma (wide)", a);
+    if constexpr (kHasFlat<LAY, false, false, false>) {
+        audit_one(k_fwd_mfma<T, D, LAY, false, false, false, true>, "k_fwd_mfma (flat)", a);
+        audit_one(k_bwd_q_mfma<T, D, LAY, false, false, false, true>, "k_bwd_q_mfma (flat)", a);
+        audit_one(k_bwd_kv_mfma<T, D, LAY, false, false, true>, "k_bwd_kv_mfma (flat)", a);
+    }
 }
 
 template <typename T, int D>
