@@ -746,7 +746,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base) {
 
 // SAME: the two [B, *sp, H, D] operands share one layout (one set of strides
 // kept in scalar registers instead of two).
-template <typename T, int D, bool SAME>
+// FLAT (here and in k_wsum_mfma, k_wsum_key_mfma) as for k_fwd_mfma.
+template <typename T, int D, bool SAME, bool FLAT = false>
 __global__ __launch_bounds__(256) void k_dot_mfma(Prob p, TileShape ts, const int* __restrict__ geo,
                                                   const T* __restrict__ a, LayK la_in, const T* __restrict__ xg,
                                                   LayK lx, T* __restrict__ out, LayK lo, float mul, float fill) {
@@ -807,8 +808,12 @@ __global__ __launch_bounds__(256) void k_dot_mfma(Prob p, TileShape ts, const in
                 }
             }
         }
-        more = walk_next(blk, w, fresh);
-        __syncthreads();  // the slice is no longer read
+        if constexpr (FLAT) {
+            more = false;
+        } else {
+            more = walk_next(blk, w, fresh);
+            __syncthreads();  // the slice is no longer read
+        }
         if (more) {
             const T* pl = plane_of(xg, lx, w.b, w.h, slice_pos(p, blk, w.u0));
             stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
@@ -850,7 +855,7 @@ __device__ __forceinline__ void redo_wsum(const void* kargs, int wg, int wave, i
     }
 }
 
-template <typename T, int D, bool SAME>
+template <typename T, int D, bool SAME, bool FLAT = false>
 __global__ __launch_bounds__(256) void k_wsum_mfma(WsumArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
@@ -930,8 +935,12 @@ __global__ __launch_bounds__(256) void k_wsum_mfma(WsumArgs<T> args) {
                 accumulate_chunk<T, D>(Xs, c, lane, make_uint4(wv[0], wv[1], wv[2], wv[3]), acc);
             }
         }
-        more = walk_next(blk, w, fresh);
-        __syncthreads();  // the slice is no longer read
+        if constexpr (FLAT) {
+            more = false;
+        } else {
+            more = walk_next(blk, w, fresh);
+            __syncthreads();  // the slice is no longer read
+        }
         if (more) {
             const T* pl = plane_of(xg, lx, w.b, w.h, slice_pos(p, blk, w.u0));
             stage_pair<T, D, false>(p, blk, ts, sm, pl, lx, Xs, pl, lx, Xs, wave);
@@ -1029,7 +1038,7 @@ __device__ __forceinline__ void redo_wsum_key(const void* kargs, int wg, int wav
     }
 }
 
-template <typename T, int D, bool SAME>
+template <typename T, int D, bool SAME, bool FLAT = false>
 __global__ __launch_bounds__(256) void k_wsum_key_mfma(WsumArgs<T> args) {
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
@@ -1120,8 +1129,12 @@ __global__ __launch_bounds__(256) void k_wsum_key_mfma(WsumArgs<T> args) {
                 accumulate_chunk<T, D>(Xs, c, lane, make_uint4(wv[0], wv[1], wv[2], wv[3]), acc);
             }
         }
-        more = walk_next(blk, w, fresh);
-        __syncthreads();  // the slice is no longer read
+        if constexpr (FLAT) {
+            more = false;
+        } else {
+            more = walk_next(blk, w, fresh);
+            __syncthreads();  // the slice is no longer read
+        }
         if (fresh || !more) {
             redo = redo || (item_nonfinite(lane_sum(acc, 0.f)) && ln.valid);
             if (ln.valid) store_rows<T, D>(bh_ptr(out, lo, b, h), vol_off(lo, ln.pos), grp, acc, mul);
@@ -1719,11 +1732,15 @@ hipError_t run_dot_as(const char* name, const Prob& p, const void* a, Lay la, co
                    float mul, float fill, hipStream_t s) {
     TileShape ts{};
     if (!choose_tile(p, kSplit, D, ts)) return hipErrorInvalidValue;
-    const auto kern = k_dot_mfma<T, D, SAME>;
+    auto kern = k_dot_mfma<T, D, SAME>;
     const size_t shm = split_lds_bytes(p, ts, D);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    if (flat_walk(p, ts, false)) {
+        kern = k_dot_mfma<T, D, SAME, true>;
+        if ((e = allow_lds(kern, shm)) != hipSuccess) return e;
+    }
     const int* geo = geometry_table(p, ts, false, s);
     NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, p, ts, geo,
               (const T*)a, to_k(la), (const T*)x, to_k(lx), (T*)o, to_k(lo), mul, fill);
@@ -1742,11 +1759,15 @@ hipError_t run_wsum_as(const char* name, const Prob& p, const void* w, Lay lw, c
                     float mul, hipStream_t s) {
     TileShape ts{};
     if (!choose_tile(p, kSplit, D, ts)) return hipErrorInvalidValue;
-    const auto kern = k_wsum_mfma<T, D, SAME>;
+    auto kern = k_wsum_mfma<T, D, SAME>;
     const size_t shm = split_lds_bytes(p, ts, D);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    if (flat_walk(p, ts, false)) {
+        kern = k_wsum_mfma<T, D, SAME, true>;
+        if ((e = allow_lds(kern, shm)) != hipSuccess) return e;
+    }
     const int* geo = geometry_table(p, ts, false, s);
     const WsumArgs<T> a{p, ts, geo, (const T*)w, (const T*)x, (T*)o, to_k(lw), to_k(lx), to_k(lo), mul};
     NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
@@ -1771,11 +1792,15 @@ hipError_t run_wsum_key_as(const char* name, const Prob& p, const void* w, Lay l
                         Lay lo, float mul, hipStream_t s) {
     TileShape ts{};
     if (!choose_tile(p, kSplitKey, D, ts)) return hipErrorInvalidValue;
-    const auto kern = k_wsum_key_mfma<T, D, SAME>;
+    auto kern = k_wsum_key_mfma<T, D, SAME>;
     const size_t shm = split_key_lds_bytes(p, ts, D);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
+    if (flat_walk(p, ts, true)) {
+        kern = k_wsum_key_mfma<T, D, SAME, true>;
+        if ((e = allow_lds(kern, shm)) != hipSuccess) return e;
+    }
     const int* geo = geometry_table(p, ts, true, s);
     const WsumArgs<T> a{p, ts, geo, (const T*)w, (const T*)x, (T*)o, to_k(lw), to_k(lx), to_k(lo), mul};
     NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, a);
@@ -1853,6 +1878,12 @@ void audit_dim(LdsAudit& a) {
     audit_one(k_wsum_mfma<T, D, false>, "k_wsum_mfma", a);
     audit_one(k_wsum_key_mfma<T, D, true>, "k_wsum_key_mfma", a);
     audit_one(k_wsum_key_mfma<T, D, false>, "k_wsum_key_mfma", a);
+    audit_one(k_dot_mfma<T, D, true, true>, "k_dot_mfma (flat)", a);
+    audit_one(k_dot_mfma<T, D, false, true>, "k_dot_mfma (flat)", a);
+    audit_one(k_wsum_mfma<T, D, true, true>, "k_wsum_mfma (flat)", a);
+    audit_one(k_wsum_mfma<T, D, false, true>, "k_wsum_mfma (flat)", a);
+    audit_one(k_wsum_key_mfma<T, D, true, true>, "k_wsum_key_mfma (flat)", a);
+    audit_one(k_wsum_key_mfma<T, D, false, true>, "k_wsum_key_mfma (flat)", a);
 }
 
 // Head dim 96 has fused instances only (the split ops keep the vector
