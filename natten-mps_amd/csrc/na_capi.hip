@@ -577,6 +577,17 @@ static int make_rpb_prob(const natten_problem_t* p, na::Prob& P) {
     return NATTEN_OK;
 }
 
+// Odd kernels on every axis: the shifted window of these ops is the main
+// operators' window (same start, end and neighbour order), so their products
+// run on the split tile kernels where those apply (the logits kernel adds
+// the bias as it stores them; na_rpb.hip reduces the bias gradient).
+static bool rpb_on_tiles(const na::Prob& P) {
+    if (!use_mfma()) return false;
+    for (int a = 0; a < 3; ++a)
+        if (P.ax[a].k % 2 == 0) return false;
+    return true;
+}
+
 int natten_hip_rpb_qk_forward(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
                               const natten_layout_t* lk, const void* rpb, void* attn, const natten_layout_t* la,
                               void* stream) {
@@ -584,8 +595,14 @@ int natten_hip_rpb_qk_forward(const natten_problem_t* p, const void* q, const na
     int rc = make_rpb_prob(p, P);
     if (rc) return rc;
     if (any_null({q, k, attn, lq, lk, la})) return fail(NATTEN_ERR_INVALID, "NULL operand");
-    return launch_status(na::rpb_qk(P, q, to_lay(lq), k, to_lay(lk), rpb, attn, to_lay(la), p->dtype,
-                                    static_cast<hipStream_t>(stream)),
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool vec = runs_aligned(dpl_for(P.Dqk), {{q, lq, P.Dqk}, {k, lk, P.Dqk}});
+    if (rpb_on_tiles(P) && na::mfma_split_eligible(P, p->dtype, P.Dqk, vec, to_lay(la), {to_lay(lq), to_lay(lk)})) {
+        return launch_status(na::mfma_split_dot("na_rpb_qk_mfma", P, P.Dqk, q, to_lay(lq), k, to_lay(lk), attn,
+                                                to_lay(la), 1.f, -INFINITY, p->dtype, s, rpb),
+                             "rpb_qk_forward");
+    }
+    return launch_status(na::rpb_qk(P, q, to_lay(lq), k, to_lay(lk), rpb, attn, to_lay(la), p->dtype, s),
                          "rpb_qk_forward");
 }
 
@@ -595,8 +612,13 @@ int natten_hip_rpb_av_forward(const natten_problem_t* p, const void* attn, const
     int rc = make_rpb_prob(p, P);
     if (rc) return rc;
     if (any_null({attn, v, out, la, lv, lo})) return fail(NATTEN_ERR_INVALID, "NULL operand");
-    return launch_status(na::rpb_av(P, attn, to_lay(la), v, to_lay(lv), out, to_lay(lo), p->dtype,
-                                    static_cast<hipStream_t>(stream)),
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool vec = runs_aligned(dpl_for(P.Dv), {{v, lv, P.Dv}, {out, lo, P.Dv}});
+    if (rpb_on_tiles(P) && na::mfma_split_eligible(P, p->dtype, P.Dv, vec, to_lay(la), {to_lay(lv), to_lay(lo)}))
+        return launch_status(na::mfma_split_wsum("na_rpb_av_mfma", P, P.Dv, attn, to_lay(la), v, to_lay(lv), out,
+                                                 to_lay(lo), 1.f, p->dtype, s),
+                             "rpb_av_forward");
+    return launch_status(na::rpb_av(P, attn, to_lay(la), v, to_lay(lv), out, to_lay(lo), p->dtype, s),
                          "rpb_av_forward");
 }
 
@@ -608,8 +630,28 @@ int natten_hip_rpb_qk_backward(const natten_problem_t* p, const void* dattn, con
     int rc = make_rpb_prob(p, P);
     if (rc) return rc;
     if (any_null({dattn, q, k, dq, dk, lda, lq, lk, ldq, ldk})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int sides = na::kQuerySide | na::kKeySide;
+    if (rpb_on_tiles(P)) {
+        const bool vec =
+            runs_aligned(dpl_for(P.Dqk), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {dq, ldq, P.Dqk}, {dk, ldk, P.Dqk}});
+        if (na::mfma_split_eligible(P, p->dtype, P.Dqk, vec, to_lay(lda), {to_lay(lk), to_lay(ldq)})) {
+            rc = launch_status(na::mfma_split_wsum("na_rpb_dq_mfma", P, P.Dqk, dattn, to_lay(lda), k, to_lay(lk), dq,
+                                                   to_lay(ldq), 1.f, p->dtype, s),
+                               "rpb_qk_backward");
+            if (rc) return rc;
+            sides &= ~na::kQuerySide;
+        }
+        if (na::mfma_split_key_eligible(P, p->dtype, P.Dqk, vec, to_lay(lda), {to_lay(lq), to_lay(ldk)})) {
+            rc = launch_status(na::mfma_split_wsum_key("na_rpb_dk_mfma", P, P.Dqk, dattn, to_lay(lda), q, to_lay(lq),
+                                                       dk, to_lay(ldk), 1.f, p->dtype, s),
+                               "rpb_qk_backward");
+            if (rc) return rc;
+            sides &= ~na::kKeySide;
+        }
+    }
     return launch_status(na::rpb_qk_backward(P, dattn, to_lay(lda), q, to_lay(lq), k, to_lay(lk), dq, to_lay(ldq), dk,
-                                             to_lay(ldk), drpb, p->dtype, static_cast<hipStream_t>(stream)),
+                                             to_lay(ldk), drpb, p->dtype, s, sides),
                          "rpb_qk_backward");
 }
 
@@ -621,9 +663,28 @@ int natten_hip_rpb_av_backward(const natten_problem_t* p, const void* dout, cons
     int rc = make_rpb_prob(p, P);
     if (rc) return rc;
     if (any_null({dout, attn, v, dattn, dv, ldo, la, lv, lda, ldv})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int sides = na::kQuerySide | na::kKeySide;
+    if (rpb_on_tiles(P)) {
+        const bool vec = runs_aligned(dpl_for(P.Dv), {{dout, ldo, P.Dv}, {v, lv, P.Dv}, {dv, ldv, P.Dv}});
+        if (na::mfma_split_eligible(P, p->dtype, P.Dv, vec, to_lay(lda), {to_lay(ldo), to_lay(lv)})) {
+            rc = launch_status(na::mfma_split_dot("na_rpb_dattn_mfma", P, P.Dv, dout, to_lay(ldo), v, to_lay(lv),
+                                                  dattn, to_lay(lda), 1.f, 0.f, p->dtype, s),
+                               "rpb_av_backward");
+            if (rc) return rc;
+            sides &= ~na::kQuerySide;
+        }
+        if (na::mfma_split_key_eligible(P, p->dtype, P.Dv, vec, to_lay(la), {to_lay(ldo), to_lay(ldv)})) {
+            rc = launch_status(na::mfma_split_wsum_key("na_rpb_dv_mfma", P, P.Dv, attn, to_lay(la), dout, to_lay(ldo),
+                                                       dv, to_lay(ldv), 1.f, p->dtype, s),
+                               "rpb_av_backward");
+            if (rc) return rc;
+            sides &= ~na::kKeySide;
+        }
+    }
+    if (!sides) return NATTEN_OK;
     return launch_status(na::rpb_av_backward(P, dout, to_lay(ldo), attn, to_lay(la), v, to_lay(lv), dattn,
-                                             to_lay(lda), dv, to_lay(ldv), p->dtype,
-                                             static_cast<hipStream_t>(stream)),
+                                             to_lay(lda), dv, to_lay(ldv), p->dtype, s, sides),
                          "rpb_av_backward");
 }
 

@@ -374,6 +374,17 @@ __device__ __forceinline__ void for_each_query_split(const Prob& p, int m0, int 
     }
 }
 
+// NATTEN 0.17's relative-position-bias start (get_pb_start) of query i on an
+// axis of length len, kernel K, dilation d (extras/allin1/reference_impl.py:30-41):
+// the bias index of the query's neighbour e along the axis is start + e.
+__host__ __device__ inline int pb_start(int i, int len, int K, int d) {
+    const int nh = K / 2;
+    if (d <= 1) return nh + (i < nh ? nh - i : 0) + (i + nh >= len ? len - i - 1 - nh : 0);
+    if (i - nh * d < 0) return K - 1 - i / d;
+    if (i + nh * d >= len) return (len - i - 1) / d;
+    return nh;
+}
+
 // ---------------------------------------------------------------------------
 // Element types.  bf16 is carried as raw bits; fp32 -> bf16 rounds to nearest
 // even with NaN kept quiet, the same rounding torch uses.

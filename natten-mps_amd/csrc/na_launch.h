@@ -39,10 +39,14 @@ hipError_t rpb_qk(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, c
                   int dtype, hipStream_t s);
 hipError_t rpb_av(const Prob& p, const void* attn, Lay la, const void* v, Lay lv, void* out, Lay lo, int dtype,
                   hipStream_t s);
+// `sides` as for the generic backward (drpb is reduced whenever non-null).
 hipError_t rpb_qk_backward(const Prob& p, const void* da, Lay lda, const void* q, Lay lq, const void* k, Lay lk,
-                           void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, int dtype, hipStream_t s);
+                           void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, int dtype, hipStream_t s,
+                           int sides = kQuerySide | kKeySide);
 hipError_t rpb_av_backward(const Prob& p, const void* dout, Lay ldo, const void* attn, Lay la, const void* v, Lay lv,
-                           void* da, Lay lda, void* dv, Lay ldv, int dtype, hipStream_t s);
+                           void* da, Lay lda, void* dv, Lay ldv, int dtype, hipStream_t s,
+                           int sides = kQuerySide | kKeySide);
+
 
 }  // namespace na
 
@@ -126,9 +130,12 @@ hipError_t mfma_global_key_backward(const Prob& p, const void* q, Lay lq, const 
 // entries per query (attn or dattn), `staged` the operands staged per tile.
 bool mfma_split_eligible(const Prob& p, int dtype, int D, bool aligned, const Lay& rows,
                          std::initializer_list<Lay> staged);
-// out[q][e] = mul * (a[q] . x[nbr(q, e)]), `fill` at invalid neighbours.
+// out[q][e] = mul * (a[q] . x[nbr(q, e)]), `fill` at invalid neighbours;
+// `bias` (relative-position bias [H, 2 K1 - 1, 2 K2 - 1], odd kernels, axis
+// 0 of kernel 1) adds bias[h, pb_start + e] per axis to every entry.
 hipError_t mfma_split_dot(const char* name, const Prob& p, int D, const void* a, Lay la, const void* x, Lay lx,
-                          void* o, Lay lo, float mul, float fill, int dtype, hipStream_t s);
+                          void* o, Lay lo, float mul, float fill, int dtype, hipStream_t s,
+                          const void* bias = nullptr);
 // Key side: out[k] = mul * sum over the queries q attending k of w[q][e(q, k)] x[q].
 bool mfma_split_key_eligible(const Prob& p, int dtype, int D, bool aligned, const Lay& rows,
                              std::initializer_list<Lay> staged);

@@ -744,13 +744,56 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), kPlaneBytes, 0x00020000);
 }
 
+// Bias-table offset of a query's first neighbour: pb1 * (2 K2 - 1) + pb2,
+// with pb = pb_start of the query's position per axis (in [0, K - 1] for odd
+// kernels, so start + e needs no clamping).
+__device__ __forceinline__ int bias_origin(const Prob& p, const Lane& ln) {
+    return pb_start(ln.pos[1], p.ax[1].len, p.ax[1].k, p.ax[1].dil) * (2 * p.ax[2].k - 1) +
+           pb_start(ln.pos[2], p.ax[2].len, p.ax[2].k, p.ax[2].dil);
+}
+
+// v[qq] += bias of entry e (kernel row e / K2 on axis 1, column e % K2) of
+// the wave's query qq: bias[h] at origin(qq) + e1 (2 K2 - 1) + e2, where
+// `origin` (bias_origin of each lane's query) was formed with every lane
+// active and is read from lane qq.  Table reads in groups of four queries:
+// the entry's part of the offset per lane, the query's in a scalar register.
+template <typename T>
+__device__ __forceinline__ void add_bias(const Prob& p, const T* __restrict__ bias, int h, int origin, int e,
+                                         uint16_t (&v)[16]) {
+    const int K1 = p.ax[1].k, K2 = p.ax[2].k, r1 = 2 * K1 - 1, r2 = 2 * K2 - 1;
+    const int e1 = e / K2, e2 = e - (e / K2) * K2;
+    const int mine = origin;
+    const __amdgpu_buffer_rsrc_t rt = rows_rsrc(bias + h * r1 * r2);
+    const int vo = (e1 * r2 + e2) * 2;
+#pragma unroll
+    for (int g = 0; g < 16; g += 4) {
+        uint16_t x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            x[i] = __builtin_amdgcn_raw_buffer_load_b16(rt, vo, __builtin_amdgcn_readlane(mine, g + i) * 2, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            T y, b;
+            __builtin_memcpy(&y, &v[g + i], 2);
+            __builtin_memcpy(&b, &x[i], 2);
+            const T z = from_f<T>(to_f(y) + to_f(b));
+            __builtin_memcpy(&v[g + i], &z, 2);
+        }
+    }
+}
+
 // SAME: the two [B, *sp, H, D] operands share one layout (one set of strides
 // kept in scalar registers instead of two).
 // FLAT (here and in k_wsum_mfma, k_wsum_key_mfma) as for k_fwd_mfma.
-template <typename T, int D, bool SAME, bool FLAT = false>
+// BIAS: `bias`, a relative-position bias [H, 2 K1 - 1, 2 K2 - 1], is added
+// to each stored entry at index (pb_start + e) per axis, for odd kernels
+// with axis 0 of kernel 1 (the DiNAT QK+RPB op); its own instances, so the
+// other products keep their registers.
+template <typename T, int D, bool SAME, bool FLAT = false, bool BIAS = false>
 __global__ __launch_bounds__(256) void k_dot_mfma(Prob p, TileShape ts, const int* __restrict__ geo,
                                                   const T* __restrict__ a, LayK la_in, const T* __restrict__ xg,
-                                                  LayK lx, T* __restrict__ out, LayK lo, float mul, float fill) {
+                                                  LayK lx, T* __restrict__ out, LayK lo, float mul, float fill,
+                                                  const T* __restrict__ bias) {
     const LayK& la = SAME ? lx : la_in;
     unsigned char* smem = lds_base();
     T* Xs = reinterpret_cast<T*>(smem);
@@ -771,6 +814,7 @@ __global__ __launch_bounds__(256) void k_dot_mfma(Prob p, TileShape ts, const in
     }
     const Lane ln = lane_item(p, ts, blk, wave, col, false);
     const int orow = ln.valid ? vol_off(lo, ln.pos) : -1;
+    const int borigin = BIAS ? bias_origin(p, ln) : 0;
     int epos[4];
     lane_entries(p, rb, lane, epos);
     const f32x4_t zero[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
@@ -828,6 +872,7 @@ __global__ __launch_bounds__(256) void k_dot_mfma(Prob p, TileShape ts, const in
                     uint16_t v[16];
 #pragma unroll
                     for (int qq = 0; qq < 16; ++qq) v[qq] = Rw[qq * rb.pitch + epos[t]];
+                    if constexpr (BIAS) add_bias<T>(p, bias, h, borigin, lane + 64 * t, v);
 #pragma unroll
                     for (int qq = 0; qq < 16; ++qq) {
                         const int off = __builtin_amdgcn_readlane(orow, qq);
@@ -1729,29 +1774,29 @@ size_t split_lds_bytes(const Prob& p, const TileShape& ts, int D) {
 
 template <typename T, int D, bool SAME>
 hipError_t run_dot_as(const char* name, const Prob& p, const void* a, Lay la, const void* x, Lay lx, void* o, Lay lo,
-                   float mul, float fill, hipStream_t s) {
+                   float mul, float fill, const void* bias, hipStream_t s) {
     TileShape ts{};
     if (!choose_tile(p, kSplit, D, ts)) return hipErrorInvalidValue;
-    auto kern = k_dot_mfma<T, D, SAME>;
+    auto kern = bias ? k_dot_mfma<T, D, SAME, false, true> : k_dot_mfma<T, D, SAME>;
     const size_t shm = split_lds_bytes(p, ts, D);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
     if (flat_walk(p, ts, false)) {
-        kern = k_dot_mfma<T, D, SAME, true>;
+        kern = bias ? k_dot_mfma<T, D, SAME, true, true> : k_dot_mfma<T, D, SAME, true>;
         if ((e = allow_lds(kern, shm)) != hipSuccess) return e;
     }
     const int* geo = geometry_table(p, ts, false, s);
     NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(grid_blocks(p, ts))), dim3(64 * ts.waves), shm, s, p, ts, geo,
-              (const T*)a, to_k(la), (const T*)x, to_k(lx), (T*)o, to_k(lo), mul, fill);
+              (const T*)a, to_k(la), (const T*)x, to_k(lx), (T*)o, to_k(lo), mul, fill, (const T*)bias);
     return hipGetLastError();
 }
 
 template <typename T, int D>
 hipError_t run_dot(const char* name, const Prob& p, const void* a, Lay la, const void* x, Lay lx, void* o, Lay lo,
-                   float mul, float fill, hipStream_t s) {
-    if (same_lay(la, lx)) return run_dot_as<T, D, true>(name, p, a, la, x, lx, o, lo, mul, fill, s);
-    return run_dot_as<T, D, false>(name, p, a, la, x, lx, o, lo, mul, fill, s);
+                   float mul, float fill, const void* bias, hipStream_t s) {
+    if (same_lay(la, lx)) return run_dot_as<T, D, true>(name, p, a, la, x, lx, o, lo, mul, fill, bias, s);
+    return run_dot_as<T, D, false>(name, p, a, la, x, lx, o, lo, mul, fill, bias, s);
 }
 
 template <typename T, int D, bool SAME>
@@ -1880,6 +1925,10 @@ void audit_dim(LdsAudit& a) {
     audit_one(k_wsum_key_mfma<T, D, false>, "k_wsum_key_mfma", a);
     audit_one(k_dot_mfma<T, D, true, true>, "k_dot_mfma (flat)", a);
     audit_one(k_dot_mfma<T, D, false, true>, "k_dot_mfma (flat)", a);
+    audit_one(k_dot_mfma<T, D, true, false, true>, "k_dot_mfma (bias)", a);
+    audit_one(k_dot_mfma<T, D, false, false, true>, "k_dot_mfma (bias)", a);
+    audit_one(k_dot_mfma<T, D, true, true, true>, "k_dot_mfma (flat, bias)", a);
+    audit_one(k_dot_mfma<T, D, false, true, true>, "k_dot_mfma (flat, bias)", a);
     audit_one(k_wsum_mfma<T, D, true, true>, "k_wsum_mfma (flat)", a);
     audit_one(k_wsum_mfma<T, D, false, true>, "k_wsum_mfma (flat)", a);
     audit_one(k_wsum_key_mfma<T, D, true, true>, "k_wsum_key_mfma (flat)", a);
@@ -1968,8 +2017,8 @@ hipError_t mfma_split_wsum_key(const char* name, const Prob& p, int D, const voi
 }
 
 hipError_t mfma_split_dot(const char* name, const Prob& p, int D, const void* a, Lay la, const void* x, Lay lx,
-                          void* o, Lay lo, float mul, float fill, int dtype, hipStream_t s) {
-#define NA_DOT(T, DD) return run_dot<T, DD>(name, p, a, la, x, lx, o, lo, mul, fill, s)
+                          void* o, Lay lo, float mul, float fill, int dtype, hipStream_t s, const void* bias) {
+#define NA_DOT(T, DD) return run_dot<T, DD>(name, p, a, la, x, lx, o, lo, mul, fill, bias, s)
     if (dtype == NATTEN_BF16) {
         if (D == 32) NA_DOT(bf16, 32);
         if (D == 64) NA_DOT(bf16, 64);

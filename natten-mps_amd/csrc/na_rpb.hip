@@ -17,6 +17,18 @@
 // bias has extent (1, 2K-1).  Vector-ALU kernels, fp32 accumulation, one
 // thread per output element; dk, dv and the bias gradient are deterministic
 // gathers (no atomics).
+//
+// For odd kernels the shifted window is the main operators' window (start,
+// end and neighbour order), so the C entry points send the products of
+// these ops to the split tile kernels where those apply (k_dot_mfma adds the
+// bias as it stores the logits), and this file reduces the bias gradient
+// (rpb_qk_backward).  An
+// odd kernel's bias start lies in [0, K-1], so the bias index of neighbour e
+// is start + e without clamping and each (query, bias index) pair has at
+// most one neighbour: the two-pass reduction below gathers per bias index
+// over LDS chunks of queries instead of scanning the tensor once per index.
+#include <algorithm>
+
 #include "na_launch.h"
 
 namespace na {
@@ -40,14 +52,8 @@ __device__ __forceinline__ int rpb_start(int i, const RAxis& a) {
 // reference_impl.py:25-27 (half-open end)
 __device__ __forceinline__ int rpb_end(int start, const RAxis& a) { return min(a.len, start + a.K * a.dil); }
 
-// reference_impl.py:30-41
-__device__ __forceinline__ int rpb_bias_start(int i, const RAxis& a) {
-    const int d = a.dil, nh = a.nh;
-    if (d <= 1) return nh + (i < nh ? nh - i : 0) + (i + nh >= a.len ? a.len - i - 1 - nh : 0);
-    if (i - nh * d < 0) return a.K - 1 - i / d;
-    if (i + nh * d >= a.len) return (a.len - i - 1) / d;
-    return nh;
-}
+// reference_impl.py:30-41 (pb_start, na_common.h)
+__device__ __forceinline__ int rpb_bias_start(int i, const RAxis& a) { return pb_start(i, a.len, a.K, a.dil); }
 
 struct RProb {
     int B, H, Dqk, Dv;
@@ -232,6 +238,113 @@ __global__ __launch_bounds__(256) void k_rpb_dbias(RProb p, const T* __restrict_
     if (threadIdx.x == 0) drpb[h * nb + rb] = from_f<T>(part[0]);
 }
 
+// Bias gradient, odd kernels, pass 1: workgroup (h, g) takes the chunks
+// g, g + G, ... of kDbChunk queries (flattened (batch, p0, p1) order).  Its
+// waves stage each chunk's dattn rows (lanes over entries) and bias starts
+// in LDS; then every thread sums the bias indices t, t + 256, ... over the
+// chunk's queries (the one neighbour with start + e == index, if any).
+// Partial sums go to part[(h * G + g) * nb + index]; the order of every sum
+// is fixed.
+constexpr int kDbChunk = 32;
+constexpr int kDbBinsPerThread = 4;
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_rpb_dbias_part(RProb p, const T* __restrict__ da, Lay lda,
+                                                        float* __restrict__ part, int G, int npos) {
+    extern __shared__ float dbs[];
+    float* vals = dbs;                                                // kDbChunk * kv
+    int* starts = reinterpret_cast<int*>(dbs + kDbChunk * p.kv);      // 2 * kDbChunk
+    long long* rowoff = reinterpret_cast<long long*>(starts + 2 * kDbChunk);  // kDbChunk, -1 past the queries
+    const int nb = p.rs[0] * p.rs[1], K0 = p.ax[0].K, K1 = p.ax[1].K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = blockIdx.x / G, g = blockIdx.x - (blockIdx.x / G) * G;
+    const int nchunk = (npos + kDbChunk - 1) / kDbChunk;
+    float acc[kDbBinsPerThread] = {0.f, 0.f, 0.f, 0.f};
+    for (int c = g; c < nchunk; c += G) {
+        __syncthreads();  // the previous chunk is no longer read
+        // one thread per query of the chunk: its row offset and bias starts
+        if (threadIdx.x < kDbChunk) {
+            const int t = c * kDbChunk + threadIdx.x;
+            int s0 = -(1 << 20), s1 = -(1 << 20);  // past the queries: no index matches
+            long long off = -1;
+            if (t < npos) {
+                const int i1 = t % p.ax[1].len, u = t / p.ax[1].len;
+                const int i0 = u % p.ax[0].len;
+                s0 = rpb_bias_start(i0, p.ax[0]);
+                s1 = rpb_bias_start(i1, p.ax[1]);
+                off = at2(lda, u / p.ax[0].len, i0, i1, h);
+            }
+            starts[2 * threadIdx.x] = s0;
+            starts[2 * threadIdx.x + 1] = s1;
+            rowoff[threadIdx.x] = off;
+        }
+        lds_publish_barrier();
+        // the wave's kDbChunk / 4 rows, lanes over entries: every load issued
+        // before the LDS stores
+        constexpr int R = kDbChunk / 4;
+        for (int e = lane; e - lane < p.kv; e += 64) {
+            float x[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const long long off = rowoff[wave + 4 * i];
+                x[i] = (off >= 0 && e < p.kv) ? to_f(da[off + e]) : 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < R; ++i)
+                if (e < p.kv) vals[(wave + 4 * i) * p.kv + e] = x[i];
+        }
+        lds_publish_barrier();
+#pragma unroll
+        for (int jb = 0; jb < kDbBinsPerThread; ++jb) {
+            const int bin = threadIdx.x + 256 * jb;
+            if (bin >= nb) break;
+            const int r0 = bin / p.rs[1], r1 = bin - (bin / p.rs[1]) * p.rs[1];
+            for (int j = 0; j < kDbChunk; ++j) {
+                const int e0 = r0 - starts[2 * j], e1 = r1 - starts[2 * j + 1];
+                if (static_cast<unsigned>(e0) < static_cast<unsigned>(K0) &&
+                    static_cast<unsigned>(e1) < static_cast<unsigned>(K1))
+                    acc[jb] += vals[j * p.kv + e0 * K1 + e1];
+            }
+        }
+    }
+#pragma unroll
+    for (int jb = 0; jb < kDbBinsPerThread; ++jb) {
+        const int bin = threadIdx.x + 256 * jb;
+        if (bin < nb) part[(static_cast<long long>(h) * G + g) * nb + bin] = acc[jb];
+    }
+}
+
+// Pass 2: one wave per (h, index): lane l sums the partials g = l, l + 64,
+// ... in order, then a fixed butterfly over the lanes.
+template <typename T>
+__global__ __launch_bounds__(256) void k_rpb_dbias_sum(RProb p, const float* __restrict__ part, int G,
+                                                       T* __restrict__ drpb) {
+    const int nb = p.rs[0] * p.rs[1];
+    const int t = static_cast<int>(blockIdx.x * 4 + (threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    if (t >= p.H * nb) return;
+    const int h = t / nb, bin = t - (t / nb) * nb;
+    float s = 0.f;
+    for (int g = lane; g < G; g += 64) s += part[(static_cast<long long>(h) * G + g) * nb + bin];
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+    if (lane == 0) drpb[t] = from_f<T>(s);
+}
+
+long long rpb_rows(const RProb& p) { return static_cast<long long>(p.B) * p.ax[0].len * p.ax[1].len * p.H; }
+
+// The two-pass bias gradient applies to odd kernels whose bias table has at
+// most 256 * kDbBinsPerThread entries (kernels up to 16).
+bool dbias_two_pass(const RProb& p) {
+    return (p.ax[0].K % 2) == 1 && (p.ax[1].K % 2) == 1 && p.rs[0] * p.rs[1] <= 256 * kDbBinsPerThread &&
+           p.kv <= 256 && rpb_rows(p) < (1LL << 31);
+}
+
+// Workgroups per head of pass 1: one per chunk, up to about 8192 in all.
+int dbias_groups(const RProb& p) {
+    const long long npos = static_cast<long long>(p.B) * p.ax[0].len * p.ax[1].len;
+    const long long nchunk = (npos + kDbChunk - 1) / kDbChunk;
+    return static_cast<int>(std::max(1LL, std::min(nchunk, static_cast<long long>(std::max(1, 8192 / p.H)))));
+}
+
 unsigned rgrid(const RProb& p, int nx) {
     const long long n = static_cast<long long>(p.B) * p.ax[0].len * p.ax[1].len * p.H * nx;
     return static_cast<unsigned>((n + 255) / 256);
@@ -254,28 +367,67 @@ hipError_t rpb_av_t(const RProb& p, const void* attn, Lay la, const void* v, Lay
 }
 
 template <typename T>
-hipError_t rpb_qk_bwd_t(const RProb& p, const void* da, Lay lda, const void* q, Lay lq, const void* k, Lay lk,
-                        void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, hipStream_t s) {
-    NA_LAUNCH("na_rpb_dq", k_rpb_dq<T>, dim3(rgrid(p, p.Dqk)), dim3(256), 0, s, p, (const T*)da, lda, (const T*)k, lk,
-              (T*)dq, ldq);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    NA_LAUNCH("na_rpb_dk", k_rpb_keyside<T>, dim3(rgrid(p, p.Dqk)), dim3(256), 0, s, p, (const T*)da, lda,
-              (const T*)q, lq, p.Dqk, (T*)dk, ldk);
-    e = hipGetLastError();
-    if (e != hipSuccess || !drpb) return e;
-    NA_LAUNCH("na_rpb_dbias", k_rpb_dbias<T>, dim3(static_cast<unsigned>(p.H * p.rs[0] * p.rs[1])), dim3(256), 0, s,
-              p, (const T*)da, lda, (T*)drpb);
+hipError_t rpb_dbias_t(const RProb& p, const void* da, Lay lda, void* drpb, hipStream_t s) {
+    const int nb = p.rs[0] * p.rs[1];
+    if (dbias_two_pass(p) && device_alloc_allowed()) {
+        // the partial sums live in stream-ordered memory of this call (no
+        // state shared between calls or streams); under graph capture, or if
+        // the allocation fails, the one-pass kernel runs instead
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        const int G = dbias_groups(p);
+        float* part = nullptr;
+        if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone &&
+            hipMallocAsync(reinterpret_cast<void**>(&part), static_cast<size_t>(p.H) * G * nb * sizeof(float), s) ==
+                hipSuccess) {
+            const size_t shm = (static_cast<size_t>(kDbChunk) * p.kv + 2 * kDbChunk) * sizeof(float) +
+                               kDbChunk * sizeof(long long);
+            const int npos = static_cast<int>(rpb_rows(p) / p.H);
+            NA_LAUNCH("na_rpb_dbias_part", k_rpb_dbias_part<T>, dim3(static_cast<unsigned>(p.H * G)), dim3(256), shm,
+                      s, p, (const T*)da, lda, part, G, npos);
+            hipError_t e = hipGetLastError();
+            if (e == hipSuccess) {
+                NA_LAUNCH("na_rpb_dbias_sum", k_rpb_dbias_sum<T>, dim3(static_cast<unsigned>((p.H * nb + 3) / 4)),
+                          dim3(256), 0, s, p, (const float*)part, G, (T*)drpb);
+                e = hipGetLastError();
+            }
+            const hipError_t f = hipFreeAsync(part, s);
+            return e != hipSuccess ? e : f;
+        }
+        (void)hipGetLastError();
+    }
+    NA_LAUNCH("na_rpb_dbias", k_rpb_dbias<T>, dim3(static_cast<unsigned>(p.H * nb)), dim3(256), 0, s, p,
+              (const T*)da, lda, (T*)drpb);
     return hipGetLastError();
 }
 
 template <typename T>
+hipError_t rpb_qk_bwd_t(const RProb& p, const void* da, Lay lda, const void* q, Lay lq, const void* k, Lay lk,
+                        void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, hipStream_t s, int sides) {
+    hipError_t e = hipSuccess;
+    if (sides & kQuerySide) {
+        NA_LAUNCH("na_rpb_dq", k_rpb_dq<T>, dim3(rgrid(p, p.Dqk)), dim3(256), 0, s, p, (const T*)da, lda, (const T*)k,
+                  lk, (T*)dq, ldq);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    if (sides & kKeySide) {
+        NA_LAUNCH("na_rpb_dk", k_rpb_keyside<T>, dim3(rgrid(p, p.Dqk)), dim3(256), 0, s, p, (const T*)da, lda,
+                  (const T*)q, lq, p.Dqk, (T*)dk, ldk);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    return drpb ? rpb_dbias_t<T>(p, da, lda, drpb, s) : hipSuccess;
+}
+
+
+template <typename T>
 hipError_t rpb_av_bwd_t(const RProb& p, const void* dout, Lay ldo, const void* attn, Lay la, const void* v, Lay lv,
-                        void* da, Lay lda, void* dv, Lay ldv, hipStream_t s) {
-    NA_LAUNCH("na_rpb_dattn", k_rpb_dattn<T>, dim3(rgrid(p, p.kv)), dim3(256), 0, s, p, (const T*)dout, ldo,
-              (const T*)v, lv, (T*)da, lda);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+                        void* da, Lay lda, void* dv, Lay ldv, hipStream_t s, int sides) {
+    if (sides & kQuerySide) {
+        NA_LAUNCH("na_rpb_dattn", k_rpb_dattn<T>, dim3(rgrid(p, p.kv)), dim3(256), 0, s, p, (const T*)dout, ldo,
+                  (const T*)v, lv, (T*)da, lda);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (!(sides & kKeySide)) return hipSuccess;
     NA_LAUNCH("na_rpb_dv", k_rpb_keyside<T>, dim3(rgrid(p, p.Dv)), dim3(256), 0, s, p, (const T*)attn, la,
               (const T*)dout, ldo, p.Dv, (T*)dv, ldv);
     return hipGetLastError();
@@ -315,19 +467,19 @@ hipError_t rpb_av(const Prob& P, const void* attn, Lay la, const void* v, Lay lv
 }
 
 hipError_t rpb_qk_backward(const Prob& P, const void* da, Lay lda, const void* q, Lay lq, const void* k, Lay lk,
-                           void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, int dtype, hipStream_t s) {
+                           void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, int dtype, hipStream_t s, int sides) {
     const RProb p = to_rprob(P);
-    if (dtype == NATTEN_F32) return rpb_qk_bwd_t<float>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, s);
-    if (dtype == NATTEN_F16) return rpb_qk_bwd_t<f16>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, s);
-    return rpb_qk_bwd_t<bf16>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, s);
+    if (dtype == NATTEN_F32) return rpb_qk_bwd_t<float>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, s, sides);
+    if (dtype == NATTEN_F16) return rpb_qk_bwd_t<f16>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, s, sides);
+    return rpb_qk_bwd_t<bf16>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, s, sides);
 }
 
 hipError_t rpb_av_backward(const Prob& P, const void* dout, Lay ldo, const void* attn, Lay la, const void* v, Lay lv,
-                           void* da, Lay lda, void* dv, Lay ldv, int dtype, hipStream_t s) {
+                           void* da, Lay lda, void* dv, Lay ldv, int dtype, hipStream_t s, int sides) {
     const RProb p = to_rprob(P);
-    if (dtype == NATTEN_F32) return rpb_av_bwd_t<float>(p, dout, ldo, attn, la, v, lv, da, lda, dv, ldv, s);
-    if (dtype == NATTEN_F16) return rpb_av_bwd_t<f16>(p, dout, ldo, attn, la, v, lv, da, lda, dv, ldv, s);
-    return rpb_av_bwd_t<bf16>(p, dout, ldo, attn, la, v, lv, da, lda, dv, ldv, s);
+    if (dtype == NATTEN_F32) return rpb_av_bwd_t<float>(p, dout, ldo, attn, la, v, lv, da, lda, dv, ldv, s, sides);
+    if (dtype == NATTEN_F16) return rpb_av_bwd_t<f16>(p, dout, ldo, attn, la, v, lv, da, lda, dv, ldv, s, sides);
+    return rpb_av_bwd_t<bf16>(p, dout, ldo, attn, la, v, lv, da, lda, dv, ldv, s, sides);
 }
 
 }  // namespace na

@@ -7,6 +7,12 @@ Tolerances: fp32 1e-5 (logits, outputs, dq, dk, dattn, dv), 1e-4 for the
 bias gradient (a sum over every query of the batch); bf16 logits/outputs
 the half-precision bound of tests/_parity.py against the oracle in fp32 on
 the same rounded inputs.
+
+Odd kernels at head dims 32/64/128 in 16-bit run the products on the split
+MFMA tile kernels (the shifted window equals the main window there, the
+logits kernel adding the bias as it stores) and the bias gradient through
+the two-pass reduction;
+test_rpb_tile_path checks the launched kernels by name.
 """
 from __future__ import annotations
 
@@ -145,3 +151,81 @@ def test_rpb_validation():
         natten2dqkrpb(q2, q2, None, (3, 5), 1)
     with pytest.raises(ValueError, match="rpb must have shape"):
         na2d_qk_rpb(q2, q2, torch.zeros(2, 5, device=DEV), 3)
+
+
+TILE_CASES = [
+    (1, (96,), 2, 32, 7, 1),
+    (1, (128,), 2, 64, 5, 3),
+    (2, (20, 18), 2, 32, 7, 1),
+    (2, (24, 24), 3, 64, 5, 2),
+    (2, (16, 16), 2, 128, 3, 1),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", TILE_CASES, ids=lambda c: "r{}sp{}H{}D{}K{}d{}".format(*c))
+def test_rpb_tile_path(case, dtype):
+    """QK+RPB, AV and all five gradients on the tile path against the oracle."""
+    import natten_mps_amd.extras.allin1 as X
+    from natten_mps_amd._core import _lib
+
+    rank, sp, H, D, K, d = case
+    qk, av = getattr(X, f"na{rank}d_qk_rpb"), getattr(X, f"na{rank}d_av_fused")
+    ref_qk, ref_av = getattr(A, f"na{rank}d_qk_rpb"), getattr(A, f"av_{rank}d")
+    kv = K ** rank
+    q, k, v = (_rand((2, *sp, H, D), s, dtype) for s in (21, 22, 23))
+    rpb = _rand((H, *([2 * K - 1] * rank)), 24, dtype)
+    ga = _rand((2, *sp, H, kv), 25, dtype)
+    go = _rand((2, *sp, H, D), 26, dtype)
+    scale = D ** -0.5
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        leaves = [t.to(DEV).requires_grad_(True) for t in (q, k, rpb)]
+        logits = qk(leaves[0], leaves[1], leaves[2], K, d, scale=scale)
+        refs = [t.float().requires_grad_(True) for t in (q, k, rpb)]
+        ref = ref_qk(refs[0], refs[1], refs[2], K, d, scale=scale)
+        assert torch.isfinite(ref).all()
+        assert_parity(logits, ref, dtype, "rpb logits")
+        logits.backward(ga.to(DEV))
+        ref.backward(ga.float())
+        for name, a, b in zip(("dq", "dk", "drpb"), leaves, refs):
+            assert_parity(a.grad, b.grad, dtype, name)
+        attn = ref.detach().softmax(-1).to(dtype)
+        a_dev, v_dev = attn.to(DEV).requires_grad_(True), v.to(DEV).requires_grad_(True)
+        out = av(a_dev, v_dev, K, d)
+        a_ref, v_ref = attn.float().requires_grad_(True), v.float().requires_grad_(True)
+        out_ref = ref_av(a_ref, v_ref, K, d)
+        assert_parity(out, out_ref, dtype, "rpb av")
+        out.backward(go.to(DEV))
+        out_ref.backward(go.float())
+        assert_parity(a_dev.grad, a_ref.grad, dtype, "dattn")
+        assert_parity(v_dev.grad, v_ref.grad, dtype, "dv")
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    ran = _lib.profile_read(reset=True)
+    for name in ("na_rpb_qk_mfma", "na_rpb_dq_mfma", "na_rpb_dk_mfma", "na_rpb_dbias_part",
+                 "na_rpb_dbias_sum", "na_rpb_av_mfma", "na_rpb_dattn_mfma", "na_rpb_dv_mfma"):
+        assert ran.get(name, (0,))[0] >= 1, (name, sorted(ran))
+    for name in ("na_rpb_qk", "na_rpb_dq", "na_rpb_dk", "na_rpb_dbias", "na_rpb_av", "na_rpb_dattn", "na_rpb_dv"):
+        assert name not in ran, (name, sorted(ran))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rpb_bias_gradient_is_deterministic(dtype):
+    """The two-pass bias gradient sums in a fixed order: repeated backward
+    calls give the same bits (2-D, odd kernel, many chunks per workgroup)."""
+    from natten_mps_amd._core import hip
+
+    q, k = (_rand((4, 40, 44, 3, 32), s, dtype).to(DEV) for s in (31, 32))
+    da = _rand((4, 40, 44, 3, 49), 33, dtype).to(DEV)
+    runs = [hip.rpb_qk_backward(2, da, q, k, True, (7, 7), (2, 2))[2] for _ in range(3)]
+    for r in runs[1:]:
+        assert torch.equal(r, runs[0])
+    r = torch.zeros(3, 13, 13, dtype=torch.float64, requires_grad=True)
+    A.na2d_qk_rpb(q.cpu().double(), k.cpu().double(), r, 7, 2).backward(da.cpu().double())
+    if dtype == torch.float32:
+        torch.testing.assert_close(runs[0].cpu().double(), r.grad, atol=1e-4, rtol=1e-4)
+    else:
+        assert_parity(runs[0], r.grad, dtype, "drpb")

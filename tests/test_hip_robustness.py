@@ -53,8 +53,8 @@ def _launched(run):
 
 def test_mfma_kernels_have_no_static_lds():
     """Every tile-kernel instance (2 dtypes x 3 head dims x 18 fused, 4
-    global-key, 6 variable-length and 12 split instances (6 of them
-    single-step), 2 dtypes x 28
+    global-key, 6 variable-length and 16 split instances (6 of them
+    single-step, 4 with the relative-position bias), 2 dtypes x 28
     fused, global-key and variable-length instances at head dim 96, and
     2 dtypes x 4 head dims x 6 single-step (FLAT) fused instances) reports 0
     bytes of static LDS, so the operands the kernels stage at a constant LDS
@@ -64,7 +64,7 @@ def test_mfma_kernels_have_no_static_lds():
 
     n = ctypes.c_int32(0)
     assert _lib.load().natten_hip_mfma_lds_check(ctypes.byref(n)) == 1
-    assert n.value == 2 * 3 * (18 + 4 + 6 + 12) + 2 * (18 + 4 + 6) + 2 * 4 * 6
+    assert n.value == 2 * 3 * (18 + 4 + 6 + 16) + 2 * (18 + 4 + 6) + 2 * 4 * 6
 
 
 # ---------------------------------------------------------------------------
