@@ -238,111 +238,108 @@ __global__ __launch_bounds__(256) void k_rpb_dbias(RProb p, const T* __restrict_
     if (threadIdx.x == 0) drpb[h * nb + rb] = from_f<T>(part[0]);
 }
 
-// Bias gradient, odd kernels, pass 1: workgroup (h, g) takes the chunks
-// g, g + G, ... of kDbChunk queries (flattened (batch, p0, p1) order).  Its
-// waves stage each chunk's dattn rows (lanes over entries) and bias starts
-// in LDS; then every thread sums the bias indices t, t + 256, ... over the
-// chunk's queries (the one neighbour with start + e == index, if any).
-// Partial sums go to part[(h * G + g) * nb + index]; the order of every sum
-// is fixed.
-constexpr int kDbChunk = 32;
-constexpr int kDbBinsPerThread = 4;
+// Bias gradient, odd kernels, pass 1: workgroup (h, g) takes kDbChunk
+// consecutive queries (flattened (batch, p0, p1) order) of head h, with one
+// thread per neighbour e (kv <= 256, ceil(kv / 64) waves).  Queries with the
+// same bias starts (pb0, pb1) -- every interior query, and runs along the
+// borders -- send entry e to the same bias index (pb0 + e0, pb1 + e1), so a
+// thread keeps a running sum over such a run and adds it to its wave's LDS
+// table when the starts change: within a run the wave's entries hit
+// distinct indices, and a wave's LDS operations keep their order, so no
+// barrier is needed until the wave tables are summed (in wave order) into
+// part[(h * nb + index) * G + g].  Every sum has a fixed order.
+constexpr int kDbChunk = 64;
+constexpr int kDbLoads = 16;  // queries whose loads are issued together
 
 template <typename T>
 __global__ __launch_bounds__(256) void k_rpb_dbias_part(RProb p, const T* __restrict__ da, Lay lda,
                                                         float* __restrict__ part, int G, int npos) {
     extern __shared__ float dbs[];
-    float* vals = dbs;                                                // kDbChunk * kv
-    int* starts = reinterpret_cast<int*>(dbs + kDbChunk * p.kv);      // 2 * kDbChunk
-    long long* rowoff = reinterpret_cast<long long*>(starts + 2 * kDbChunk);  // kDbChunk, -1 past the queries
-    const int nb = p.rs[0] * p.rs[1], K0 = p.ax[0].K, K1 = p.ax[1].K;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = p.rs[0] * p.rs[1], K1 = p.ax[1].K, nw = blockDim.x >> 6;
+    long long* rowoff = reinterpret_cast<long long*>(dbs);           // kDbChunk
+    int* st = reinterpret_cast<int*>(rowoff + kDbChunk);              // 2 * kDbChunk
+    float* bins = reinterpret_cast<float*>(st + 2 * kDbChunk);        // nw * nb
     const int h = blockIdx.x / G, g = blockIdx.x - (blockIdx.x / G) * G;
-    const int nchunk = (npos + kDbChunk - 1) / kDbChunk;
-    float acc[kDbBinsPerThread] = {0.f, 0.f, 0.f, 0.f};
-    for (int c = g; c < nchunk; c += G) {
-        __syncthreads();  // the previous chunk is no longer read
-        // one thread per query of the chunk: its row offset and bias starts
-        if (threadIdx.x < kDbChunk) {
-            const int t = c * kDbChunk + threadIdx.x;
-            int s0 = -(1 << 20), s1 = -(1 << 20);  // past the queries: no index matches
-            long long off = -1;
-            if (t < npos) {
-                const int i1 = t % p.ax[1].len, u = t / p.ax[1].len;
-                const int i0 = u % p.ax[0].len;
-                s0 = rpb_bias_start(i0, p.ax[0]);
-                s1 = rpb_bias_start(i1, p.ax[1]);
-                off = at2(lda, u / p.ax[0].len, i0, i1, h);
-            }
-            starts[2 * threadIdx.x] = s0;
-            starts[2 * threadIdx.x + 1] = s1;
-            rowoff[threadIdx.x] = off;
-        }
-        lds_publish_barrier();
-        // the wave's kDbChunk / 4 rows, lanes over entries: every load issued
-        // before the LDS stores
-        constexpr int R = kDbChunk / 4;
-        for (int e = lane; e - lane < p.kv; e += 64) {
-            float x[R];
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const long long off = rowoff[wave + 4 * i];
-                x[i] = (off >= 0 && e < p.kv) ? to_f(da[off + e]) : 0.f;
-            }
-#pragma unroll
-            for (int i = 0; i < R; ++i)
-                if (e < p.kv) vals[(wave + 4 * i) * p.kv + e] = x[i];
-        }
-        lds_publish_barrier();
-#pragma unroll
-        for (int jb = 0; jb < kDbBinsPerThread; ++jb) {
-            const int bin = threadIdx.x + 256 * jb;
-            if (bin >= nb) break;
-            const int r0 = bin / p.rs[1], r1 = bin - (bin / p.rs[1]) * p.rs[1];
-            for (int j = 0; j < kDbChunk; ++j) {
-                const int e0 = r0 - starts[2 * j], e1 = r1 - starts[2 * j + 1];
-                if (static_cast<unsigned>(e0) < static_cast<unsigned>(K0) &&
-                    static_cast<unsigned>(e1) < static_cast<unsigned>(K1))
-                    acc[jb] += vals[j * p.kv + e0 * K1 + e1];
-            }
+    const int t0 = g * kDbChunk, n = min(npos - t0, kDbChunk);
+    if (threadIdx.x < kDbChunk) {
+        // the chunk's queries, decoded once: row offset and bias starts
+        const int t = t0 + threadIdx.x;
+        if (threadIdx.x < n) {
+            const int i1 = t % p.ax[1].len, u = t / p.ax[1].len;
+            const int i0 = u % p.ax[0].len;
+            rowoff[threadIdx.x] = at2(lda, u / p.ax[0].len, i0, i1, h);
+            st[2 * threadIdx.x] = rpb_bias_start(i0, p.ax[0]);
+            st[2 * threadIdx.x + 1] = rpb_bias_start(i1, p.ax[1]);
         }
     }
+    for (int i = threadIdx.x; i < nw * nb; i += blockDim.x) bins[i] = 0.f;
+    lds_publish_barrier();
+    const int e = threadIdx.x;
+    const bool mine = e < p.kv;
+    const int e0 = e / K1, e1 = e - (e / K1) * K1;
+    float* wbins = bins + (threadIdx.x >> 6) * nb;
+    float acc = 0.f;
+    int c0 = -1, c1 = -1;  // the current run's bias starts (none yet)
+    const int ec = mine ? e : 0;  // loads at a valid address; unused past kv
+    for (int jb = 0; jb < n; jb += kDbLoads) {
+        // unconditional loads (queries past the chunk re-read its last row) so
+        // that all of them are in flight before the first is used
+        T xr[kDbLoads];
 #pragma unroll
-    for (int jb = 0; jb < kDbBinsPerThread; ++jb) {
-        const int bin = threadIdx.x + 256 * jb;
-        if (bin < nb) part[(static_cast<long long>(h) * G + g) * nb + bin] = acc[jb];
+        for (int i = 0; i < kDbLoads; ++i) xr[i] = da[rowoff[min(jb + i, n - 1)] + ec];
+        float x[kDbLoads];
+#pragma unroll
+        for (int i = 0; i < kDbLoads; ++i) x[i] = to_f(xr[i]);
+#pragma unroll
+        for (int i = 0; i < kDbLoads; ++i) {
+            if (jb + i >= n) break;
+            const int s0 = st[2 * (jb + i)], s1 = st[2 * (jb + i) + 1];
+            if (s0 != c0 || s1 != c1) {
+                if (c0 >= 0 && mine) wbins[(c0 + e0) * p.rs[1] + c1 + e1] += acc;
+                c0 = s0;
+                c1 = s1;
+                acc = 0.f;
+            }
+            acc += x[i];
+        }
+    }
+    if (c0 >= 0 && mine) wbins[(c0 + e0) * p.rs[1] + c1 + e1] += acc;
+    lds_publish_barrier();
+    for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+        float sum = 0.f;
+        for (int w = 0; w < nw; ++w) sum += bins[w * nb + i];
+        part[(static_cast<long long>(h) * nb + i) * G + g] = sum;
     }
 }
 
 // Pass 2: one wave per (h, index): lane l sums the partials g = l, l + 64,
-// ... in order, then a fixed butterfly over the lanes.
+// ... in order (consecutive in memory across the lanes), then a fixed
+// butterfly over the lanes.
 template <typename T>
 __global__ __launch_bounds__(256) void k_rpb_dbias_sum(RProb p, const float* __restrict__ part, int G,
                                                        T* __restrict__ drpb) {
     const int nb = p.rs[0] * p.rs[1];
     const int t = static_cast<int>(blockIdx.x * 4 + (threadIdx.x >> 6)), lane = threadIdx.x & 63;
     if (t >= p.H * nb) return;
-    const int h = t / nb, bin = t - (t / nb) * nb;
+    const float* row = part + static_cast<long long>(t) * G;
     float s = 0.f;
-    for (int g = lane; g < G; g += 64) s += part[(static_cast<long long>(h) * G + g) * nb + bin];
+    for (int g = lane; g < G; g += 64) s += row[g];
     for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
     if (lane == 0) drpb[t] = from_f<T>(s);
 }
 
 long long rpb_rows(const RProb& p) { return static_cast<long long>(p.B) * p.ax[0].len * p.ax[1].len * p.H; }
 
-// The two-pass bias gradient applies to odd kernels whose bias table has at
-// most 256 * kDbBinsPerThread entries (kernels up to 16).
+// The two-pass bias gradient applies to odd kernels of at most 256
+// neighbours (one thread each).
 bool dbias_two_pass(const RProb& p) {
-    return (p.ax[0].K % 2) == 1 && (p.ax[1].K % 2) == 1 && p.rs[0] * p.rs[1] <= 256 * kDbBinsPerThread &&
-           p.kv <= 256 && rpb_rows(p) < (1LL << 31);
+    return (p.ax[0].K % 2) == 1 && (p.ax[1].K % 2) == 1 && p.kv <= 256 && rpb_rows(p) < (1LL << 31);
 }
 
-// Workgroups per head of pass 1: one per chunk, up to about 8192 in all.
+// Workgroups per head of pass 1: one per chunk of kDbChunk queries.
 int dbias_groups(const RProb& p) {
     const long long npos = static_cast<long long>(p.B) * p.ax[0].len * p.ax[1].len;
-    const long long nchunk = (npos + kDbChunk - 1) / kDbChunk;
-    return static_cast<int>(std::max(1LL, std::min(nchunk, static_cast<long long>(std::max(1, 8192 / p.H)))));
+    return static_cast<int>((npos + kDbChunk - 1) / kDbChunk);
 }
 
 unsigned rgrid(const RProb& p, int nx) {
@@ -379,11 +376,12 @@ hipError_t rpb_dbias_t(const RProb& p, const void* da, Lay lda, void* drpb, hipS
         if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone &&
             hipMallocAsync(reinterpret_cast<void**>(&part), static_cast<size_t>(p.H) * G * nb * sizeof(float), s) ==
                 hipSuccess) {
-            const size_t shm = (static_cast<size_t>(kDbChunk) * p.kv + 2 * kDbChunk) * sizeof(float) +
-                               kDbChunk * sizeof(long long);
+            const int nw = (p.kv + 63) / 64;  // one thread per neighbour
+            const size_t shm = kDbChunk * (sizeof(long long) + 2 * sizeof(int)) +
+                               static_cast<size_t>(nw) * nb * sizeof(float);
             const int npos = static_cast<int>(rpb_rows(p) / p.H);
-            NA_LAUNCH("na_rpb_dbias_part", k_rpb_dbias_part<T>, dim3(static_cast<unsigned>(p.H * G)), dim3(256), shm,
-                      s, p, (const T*)da, lda, part, G, npos);
+            NA_LAUNCH("na_rpb_dbias_part", k_rpb_dbias_part<T>, dim3(static_cast<unsigned>(p.H * G)), dim3(64 * nw),
+                      shm, s, p, (const T*)da, lda, part, G, npos);
             hipError_t e = hipGetLastError();
             if (e == hipSuccess) {
                 NA_LAUNCH("na_rpb_dbias_sum", k_rpb_dbias_sum<T>, dim3(static_cast<unsigned>((p.H * nb + 3) / 4)),

@@ -229,3 +229,25 @@ def test_rpb_bias_gradient_is_deterministic(dtype):
         torch.testing.assert_close(runs[0].cpu().double(), r.grad, atol=1e-4, rtol=1e-4)
     else:
         assert_parity(runs[0], r.grad, dtype, "drpb")
+
+
+@pytest.mark.parametrize("rank", [1, 2])
+def test_rpb_without_bias_equals_split_qk(rank):
+    """Odd kernel, no bias: the QK+RPB logits are the split QK op's logits at
+    scale 1, bit for bit (the same tile kernel and window); with a bias, each
+    logit is the rounded product plus its table entry (the oracle's gather),
+    rounded once more."""
+    from natten_mps_amd import functional as F
+    from natten_mps_amd.extras.allin1.functional import natten1dqkrpb, natten2dqkrpb
+
+    sp, K, d = ((80,), 7, 2) if rank == 1 else ((18, 20), 5, 2)
+    q, k = (_rand((2, *sp, 2, 32), s, torch.bfloat16).to(DEV) for s in (41, 42))
+    qkrpb = natten1dqkrpb if rank == 1 else natten2dqkrpb
+    plain = getattr(F, f"na{rank}d_qk")(q, k, (K,) * rank, (d,) * rank, scale=1.0)
+    assert torch.equal(qkrpb(q, k, None, K, d), plain)
+    rpb = _rand((2, *([2 * K - 1] * rank)), 43, torch.bfloat16)
+    got = qkrpb(q, k, rpb.to(DEV), K, d).cpu().float()
+    z = torch.zeros((2, *sp, 2, 1), dtype=torch.float64)
+    gathered = (A.na1d_qk_rpb if rank == 1 else A.na2d_qk_rpb)(z, z, rpb.double(), K, d)  # q . k = 0
+    want = (plain.cpu().float() + gathered.float()).to(torch.bfloat16).float()
+    assert torch.equal(got, want)
