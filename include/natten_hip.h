@@ -292,7 +292,11 @@ int natten_hip_varlen_backward(const natten_problem_t *p, const int32_t *lens,
  *            over every entry at each bias index
  *   rpb_av_backward: dattn (0 for invalid neighbours), dv
  * rpb and drpb are contiguous [H, 2K1-1, 2K2-1] (1-D: [H, 2K-1]) in the
- * problem's dtype; attn is [B, *sp, H, K1*K2]. */
+ * problem's dtype; attn is [B, *sp, H, K1*K2].  Odd kernels in bf16/fp16 at
+ * head dims 32/64/128 run on the split MFMA tile kernels: there rpb_qk
+ * rounds q . k to the dtype before adding the bias (one more rounding), and
+ * drpb's partial sums take stream-ordered device memory for the call
+ * (none under graph capture, where a one-pass kernel runs instead). */
 int natten_hip_rpb_qk_forward(const natten_problem_t *p,
                               const void *q, const natten_layout_t *lq,
                               const void *k, const natten_layout_t *lk,
