@@ -27,8 +27,6 @@
 // is start + e without clamping and each (query, bias index) pair has at
 // most one neighbour: the two-pass reduction below gathers per bias index
 // over LDS chunks of queries instead of scanning the tensor once per index.
-#include <algorithm>
-
 #include "na_launch.h"
 
 namespace na {

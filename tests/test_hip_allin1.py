@@ -251,3 +251,37 @@ def test_rpb_without_bias_equals_split_qk(rank):
     gathered = (A.na1d_qk_rpb if rank == 1 else A.na2d_qk_rpb)(z, z, rpb.double(), K, d)  # q . k = 0
     want = (plain.cpu().float() + gathered.float()).to(torch.bfloat16).float()
     assert torch.equal(got, want)
+
+
+def test_rpb_tile_path_on_qkv_views():
+    """q, k, v as views into one projected qkv tensor ([B, X, Y, 3, H, D], the
+    DiNAT block's layout): the tile path reads them through their strides."""
+    import natten_mps_amd.extras.allin1 as X
+    from natten_mps_amd._core import _lib
+
+    B, Xn, Yn, H, D, K, d = 2, 16, 18, 2, 32, 5, 2
+    qkv = _rand((B, Xn, Yn, 3, H, D), 51, torch.bfloat16)
+    rpb = _rand((H, 2 * K - 1, 2 * K - 1), 52, torch.bfloat16)
+    go = _rand((B, Xn, Yn, H, D), 53, torch.bfloat16)
+    qkv_d = qkv.to(DEV).requires_grad_(True)
+    q, k, v = qkv_d.unbind(3)
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        attn = X.na2d_qk_rpb(q, k, rpb.to(DEV), K, d, scale=D ** -0.5).softmax(-1)
+        out = X.na2d_av_fused(attn, v, K, d)
+        out.backward(go.to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    ran = _lib.profile_read(reset=True)
+    for name in ("na_rpb_qk_mfma", "na_rpb_av_mfma", "na_rpb_dq_mfma", "na_rpb_dk_mfma", "na_rpb_dattn_mfma",
+                 "na_rpb_dv_mfma"):
+        assert ran.get(name, (0,))[0] >= 1, (name, sorted(ran))
+    ref_qkv = qkv.float().requires_grad_(True)
+    rq, rk, rv = ref_qkv.unbind(3)
+    ref_attn = A.na2d_qk_rpb(rq, rk, rpb.float(), K, d, scale=D ** -0.5).softmax(-1)
+    ref_out = A.av_2d(ref_attn, rv, K, d)
+    ref_out.backward(go.float())
+    assert_parity(out, ref_out, torch.bfloat16, "out")
+    assert_parity(qkv_d.grad, ref_qkv.grad, torch.bfloat16, "dqkv")
