@@ -291,6 +291,52 @@ def cpu_baseline(cfg, pairs, budget_s=30.0):
     return res
 
 
+def rpb_step(torch, steps, warmup):
+    """The DiNAT relative-position-bias ops (extras.allin1) on their own: one
+    JSON line with the eager step time and each library kernel's mean launch
+    time (per-launch events).  Not the headline metric."""
+    from natten_mps_amd._core import _lib
+    from natten_mps_amd.extras.allin1 import na2d_av_fused, na2d_qk_rpb
+
+    B, X, H, D, K = 16, 56, 4, 32, 7
+    g = torch.Generator().manual_seed(0)
+    dev = torch.device("cuda:0")
+    q, k, v = (torch.randn(B, X, X, H, D, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+    rpb = torch.randn(H, 2 * K - 1, 2 * K - 1, generator=g).to(torch.bfloat16).to(dev)
+    ga = torch.randn(B, X, X, H, K * K, generator=g).to(torch.bfloat16).to(dev)
+    go = torch.randn(B, X, X, H, D, generator=g).to(torch.bfloat16).to(dev)
+
+    def step():
+        qq, kk, rr = (t.detach().requires_grad_(True) for t in (q, k, rpb))
+        logits = na2d_qk_rpb(qq, kk, rr, K, 1, scale=D ** -0.5)
+        logits.backward(ga)
+        a = logits.detach().softmax(-1).requires_grad_(True)
+        vv = v.detach().requires_grad_(True)
+        na2d_av_fused(a, vv, K, 1).backward(go)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    kernels = {name: round(tot / n * 1e3, 1) for name, (n, tot, _, _) in _lib.profile_read(reset=True).items()}
+    print(json.dumps({"workload": "extras.allin1 na2d QK+RPB -> softmax -> AV, fwd+bwd, B=16 56x56 heads=4 dim=32 "
+                                  "K=7 bf16", "ms_per_step_eager": round(e0.elapsed_time(e1) / steps, 4),
+                      "kernel_mean_us": kernels, "kernel_sum_us": round(sum(kernels.values()), 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -304,6 +350,9 @@ def main():
     ap.add_argument("--no-split", action="store_true", help="skip the split-path comparison of config 3")
     ap.add_argument("--copy-probe", type=float, default=None, metavar="MB",
                     help="only run device-to-device copies of this many MB (calibrates rocprofv3 byte counters)")
+    ap.add_argument("--rpb", action="store_true",
+                    help="only time the extras.allin1 QK+RPB -> softmax -> AV step at DiNAT scale "
+                         "(B=16, 56x56, 4 heads, dim 32, K=7, bf16), forward + backward")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -324,6 +373,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": 2 * n, "copies": args.steps}), flush=True)
+        return
+
+    if args.rpb:
+        rpb_step(torch, args.steps, args.warmup)
         return
 
     import natten_mps_amd
