@@ -91,9 +91,9 @@ def kernel_bytes(name, B, N, Hq, Hkv, D, esz):
     bwd_q_mfma = bwd_q + tq                       # ... the tile kernel also reads o
     bwd_kv = tq + 2 * tkv + tq + 2 * lse + 2 * tkv  # q, k, v, dout, lse, delta -> dk, dv
     return {
-        "na_forward": fwd, "na_fwd_mfma": fwd,
-        "na_bwd_dq": bwd_q, "na_bwd_q_mfma": bwd_q_mfma,
-        "na_bwd_dkdv": bwd_kv, "na_bwd_kv_mfma": bwd_kv,
+        "na_forward": fwd, "na_fwd_mfma": fwd, "na_fwd_lean": fwd,
+        "na_bwd_dq": bwd_q, "na_bwd_q_mfma": bwd_q_mfma, "na_bwd_q_lean": bwd_q_mfma,
+        "na_bwd_dkdv": bwd_kv, "na_bwd_kv_mfma": bwd_kv, "na_bwd_kv_lean": bwd_kv,
     }.get(name)
 
 
@@ -540,7 +540,8 @@ def main():
     # pairs of their unions; those executed flops are in the counter
     # profiles, not here.)
     mfma = None
-    per_pair = {"na_fwd_mfma": 4.0, "na_bwd_q_mfma": 6.0, "na_bwd_kv_mfma": 8.0}
+    per_pair = {"na_fwd_mfma": 4.0, "na_bwd_q_mfma": 6.0, "na_bwd_kv_mfma": 8.0,
+                "na_fwd_lean": 4.0, "na_bwd_q_lean": 6.0, "na_bwd_kv_lean": 8.0}
     if dtype != torch.float32:
         kern = {}
         for name, (n, tot, _, _) in stats.items():

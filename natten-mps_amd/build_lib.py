@@ -21,7 +21,7 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "natten_mps_amd", "libnatten_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["na_generic.hip", "na_mfma.hip", "na_global.hip", "na_rpb.hip", "na_profile.hip", "na_capi.hip"]
+SOURCES = ["na_generic.hip", "na_mfma.hip", "na_lean.hip", "na_global.hip", "na_rpb.hip", "na_profile.hip", "na_capi.hip"]
 
 FLAGS = [
     "--offload-arch=gfx950",

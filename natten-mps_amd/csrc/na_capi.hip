@@ -162,10 +162,16 @@ int natten_hip_forward(const natten_problem_t* p, const void* q, const natten_la
         runs_aligned(dpl_for(D), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {v, lv, P.Dv}, {out, lo, P.Dv}}) ? 1 : 0;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (use_mfma() && na::mfma_eligible(P, p->dtype, D, vec != 0, false) &&
-        na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(llse)}))
+        na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(llse)})) {
+        if (na::lean_eligible(P, p->dtype, vec != 0, {to_lay(lq), to_lay(lo)}, {to_lay(lk), to_lay(lv)})) {
+            const hipError_t e = na::lean_forward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo),
+                                                  lse, to_lay(llse), p->dtype, s);
+            if (e != hipErrorNotSupported) return launch_status(e, "forward");
+        }
         return launch_status(na::mfma_forward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), lse,
                                               to_lay(llse), p->dtype, s),
                              "forward");
+    }
     return launch_status(na::generic_forward(P, vec, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo),
                                              lse, to_lay(llse), p->dtype, s),
                          "forward");
@@ -191,13 +197,22 @@ int backward_impl(const natten_problem_t* p, const na::Prob& P, const void* q, c
     if (use_mfma() && na::mfma_eligible(P, p->dtype, D, vec != 0, true) &&
         na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(ldo), to_lay(llse),
                                  to_lay(ldq), to_lay(ldk), to_lay(ldv), to_lay(ldelta)}) &&
-        (!dlse || na::mfma_offsets_fit(P, {to_lay(ldlse)})))
+        (!dlse || na::mfma_offsets_fit(P, {to_lay(ldlse)}))) {
+        if (na::lean_eligible(P, p->dtype, vec != 0, {to_lay(lq), to_lay(lo), to_lay(ldo), to_lay(ldq)},
+                              {to_lay(lk), to_lay(lv), to_lay(ldk), to_lay(ldv)})) {
+            const hipError_t e = na::lean_backward(
+                P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout, to_lay(ldo), lse, to_lay(llse),
+                dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv, to_lay(ldv), delta, to_lay(ldelta),
+                p->dtype, static_cast<hipStream_t>(stream));
+            if (e != hipErrorNotSupported) return launch_status(e, "backward");
+        }
         return launch_status(na::mfma_backward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout,
                                                to_lay(ldo), lse,
                                                to_lay(llse), dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv,
                                                to_lay(ldv), delta, to_lay(ldelta), p->dtype,
                                                static_cast<hipStream_t>(stream)),
                              "backward");
+    }
     return launch_status(
         na::generic_backward(P, vec, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout, to_lay(ldo),
                              lse, to_lay(llse), dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv,

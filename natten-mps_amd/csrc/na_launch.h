@@ -115,6 +115,20 @@ hipError_t mfma_backward(const Prob& p, const void* q, Lay lq, const void* k, La
                          const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
                          float* delta, Lay lde, int dtype, hipStream_t s, const GlobalSet* g = nullptr);
 
+// Lean 2-D tile kernels (na_lean.hip): 2-D problems at stride 1, bf16/fp16,
+// head dim 32 or 64, kernel sizes up to 9, q-side and k-side operands each
+// in one layout.  The launchers return hipErrorNotSupported when they have
+// no launch for the problem (no tile table can be built: stream capture or a
+// no-allocation scope), and the caller then takes the general tile kernels.
+bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list<Lay> qside,
+                   std::initializer_list<Lay> kvside);
+hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
+                        Lay lo, float* lse, Lay ll, int dtype, hipStream_t s);
+hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
+                         const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
+                         const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
+                         float* delta, Lay lde, int dtype, hipStream_t s);
+
 // Key side of the global keys' backward (na_global.hip): dk and dv of the
 // global keys (summed over every query of each q head of the group), from the
 // forward's lse and the backward's delta.  Partial sums over slices of the

@@ -1,0 +1,1010 @@
+// Lean tile kernels for 2-D neighbourhood attention (gfx950, bf16 / fp16,
+// head dim 32 or 64, stride 1): forward, backward dQ and backward dK/dV.
+//
+// They serve the common case of the MFMA tile path with a fixed tile and
+// fixed lane layouts, so that a wave spends its instructions on the products
+// and the softmax instead of on general tile geometry:
+//
+// * A workgroup owns an 8 x 8 box of queries (keys) of one class pair (r1,
+//   r2) and one (batch, head); wave w owns box rows 2w and 2w+1, lane column
+//   n = lane % 16 the item (2w + n/8, n%8).  In class coordinates a window is
+//   an undilated K1 x K2 run; window starts are non-decreasing along an axis
+//   and grow by at most one per item, so the union of the box's windows (of
+//   the queries attending the box's keys) spans at most 7 + K rows and a
+//   wave's own two rows at most K1 + 1 of them.
+// * LDS holds the union row-major with 16 slots per union row (K2 <= 9 keeps
+//   a row's windows inside 16 columns), two union rows per 32-slot chunk;
+//   rows and columns past the union are staged from outside the buffer's
+//   range and read as zeros.  16-byte pieces are XOR-swizzled by slot as in
+//   the general tile kernels (swz, na_tile.h).
+// * Everything a tile needs beyond the problem is one host-built record of
+//   16 dwords (positions of the box and the union, extents, and every item's
+//   window start per axis relative to the union), read with one scalar load.
+// * The forward computes all of a wave's score blocks first (K1 + 1 union
+//   rows at most), takes one maximum per query and exponentiates once: no
+//   online rescaling.
+//
+// MFMA layouts are those of na_mfma.hip (16x16x32): in a chunk the lane
+// (n, g = lane / 16) holds the 8 consecutive slots 8g .. 8g+7 of item n
+// (union row 2c + g/2, columns 8(g%2) ..), the B operand of the product that
+// contracts over slots; that product reads its A operand transposed out of
+// LDS with ds_read_b64_tr_b16.
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "na_tile.h"
+
+namespace na {
+
+namespace {
+
+constexpr int kLeanRec = 16;                 // dwords per tile record
+constexpr uint32_t kLeanOOR = 0x40000000u;   // offset past every staged plane's range (planes < 2^30 bytes)
+constexpr int kLeanWaves = 4;
+
+typedef unsigned int v2u32_t __attribute__((ext_vector_type(2)));
+
+// Layout of one operand group: batch and head strides, and the element
+// strides of the two spatial axes (axis 0 of the padded problem has extent 1).
+struct LeanLay {
+    long long b, h;
+    int s1, s2;
+};
+
+template <typename T>
+struct LeanFwdArgs {
+    const int* rec;
+    const T *q, *k, *v;
+    T* out;
+    float* lse;
+    LeanLay lq, lk, ll;           // q and out; k and v; lse
+    FastDiv heads, tiles, rep;    // workgroup decode; kv head = h / rep
+    int d1, d2, K1, K2;
+    uint32_t qbytes, kbytes;      // byte range of one (batch, head) plane of q / k
+    float sc2;                    // scale * log2(e)
+    Prob p;                       // for the exact recomputation
+};
+
+// Signed byte i (0..7) of the pair (lo, hi).
+__device__ __forceinline__ int sbyte(int lo, int hi, int i) {
+    const int w = i < 4 ? lo : hi;
+    return (w << (24 - 8 * (i & 3))) >> 24;
+}
+
+// Logical 16-byte piece that lands at physical piece `pp` of slot `slot`.
+template <int D>
+__device__ __forceinline__ int lean_piece(int pp, int slot) {
+    return pp ^ swz<D>(slot);
+}
+
+// Staging of union rows [0, nst) of two operands sharing one layout into
+// Xa / Xb (16 slots per row): rows at or past U1 and columns at or past U2
+// load from outside the range (zeros).  Rows are dealt to the waves in turn.
+template <typename T, int D>
+__device__ __forceinline__ void lean_stage(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, T* Xa, T* Xb,
+                                           int base, int step1, int step2, int U1, int U2, int nst, int wave,
+                                           int lane) {
+    constexpr int P = D / 8, SPI = 64 / P, HALVES = 16 / SPI;
+    static_assert(kLeanWaves % 2 == 0, "a wave's rows must keep one parity");
+    // lane part of the offset per half row; a wave's rows i = wave + 4j all
+    // have the parity of `wave`, which fixes the swizzle's row bit
+    uint32_t off[HALVES];
+    const int pp = lane % P;
+#pragma unroll
+    for (int hf = 0; hf < HALVES; ++hf) {
+        const int c = hf * SPI + lane / P;
+        const int slot = (wave & 1) * 16 + c;
+        off[hf] = c < U2 ? static_cast<uint32_t>(c * step2 + lean_piece<D>(pp, slot) * 16) : kLeanOOR;
+    }
+#pragma unroll 1
+    for (int i = wave; i < nst; i += kLeanWaves) {
+        const uint32_t ro = i < U1 ? static_cast<uint32_t>(base + i * step1) : kLeanOOR;
+#pragma unroll
+        for (int hf = 0; hf < HALVES; ++hf) {
+            const uint32_t o = off[hf] + ro;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(Xa + (i * 16 + hf * SPI) * D), 16, o, 0, 0,
+                                                     0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(Xb + (i * 16 + hf * SPI) * D), 16, o, 0, 0,
+                                                     0);
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t lean_rsrc(const T* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(p), static_cast<short>(0), static_cast<int>(bytes),
+                                             0x00020000);
+}
+
+// LDS byte offsets (from the operand's base) of the lane's score A operand
+// for blocks b = 0, 1 of chunk 0 of a wave whose rows start at union row
+// `first`, k-step ks: slot 8(n/4) + 4b + n%4, logical piece 4ks + g.
+template <int D>
+__device__ __forceinline__ int lean_score_off(int first, int col, int grp, int b, int ks) {
+    const int slot = first * 16 + 8 * (col >> 2) + 4 * b + (col & 3);
+    return slot * D * 2 + ((ks * 4 + grp) ^ swz<D>(slot)) * 16;
+}
+
+// LDS byte offset of the lane's transposing read (rows r0 or r1 = r0 + 4 of
+// chunk 0, 16-dim block db): see accumulate_chunk in na_tile.h.
+template <int D>
+__device__ __forceinline__ int lean_tr_off(int first, int lane, int hi, int db) {
+    const int g = lane >> 4, j = lane & 15;
+    const int r = first * 16 + 8 * g + (j >> 2) + 4 * hi;
+    const int kb = 2 * db + ((j & 3) >> 1);
+    return r * D * 2 + (kb ^ swz<D>(r)) * 16 + (j & 1) * 8;
+}
+
+template <typename T, int D>
+__device__ __forceinline__ f32x4_t lean_score(const unsigned char* X, const int (&aoff)[2][D / 32], int c, int b,
+                                              const uint4 (&frag)[D / 32], f32x4_t acc) {
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+        const uint4 a = *reinterpret_cast<const uint4*>(X + aoff[b][ks] + c * 32 * D * 2);
+        acc = Mma<T>::run(a, frag[ks], acc);
+    }
+    return acc;
+}
+
+// acc[db] += X^T[db block][chunk c slots] * packed (B operand: 8 slots of the lane's item).
+template <typename T, int D>
+__device__ __forceinline__ void lean_accumulate(const unsigned char* X, const int (&toff)[2][D / 16], int c,
+                                                uint4 packed, f32x4_t (&acc)[D / 16]) {
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(X + toff[0][db] + c * 32 * D * 2));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(X + toff[1][db] + c * 32 * D * 2));
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+        acc[db] = Mma<T>::run(make_uint4(l2.x, l2.y, h2.x, h2.y), packed, acc[db]);
+    }
+}
+
+// Column mask of the lane as the score MFMA's accumulator input: slot
+// columns 8(g%2) + 4b + i inside [clo, clo + K2) -> 0, else -inf.
+__device__ __forceinline__ void lean_colbias(int clo, int K2, int grp, f32x4_t (&bias)[2]) {
+    const int c0 = 8 * (grp & 1) - clo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const unsigned cc = static_cast<unsigned>(c0 + e);
+        bias[e >> 2][e & 3] = cc < static_cast<unsigned>(K2) ? 0.f : -INFINITY;
+    }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void lean_redo_fwd(const void* kargs, int pos1, int pos2, int b, int h, int hk, int grp) {
+    const LeanFwdArgs<T>& A = *static_cast<const LeanFwdArgs<T>*>(kargs);
+    ExactAxis x[3];
+    x[0] = exact_axis(A.p.ax[0], 0);
+    x[1] = exact_axis(A.p.ax[1], pos1);
+    x[2] = exact_axis(A.p.ax[2], pos2);
+    const T* qp = A.q + b * A.lq.b + h * A.lq.h;
+    const T* kp = A.k + b * A.lk.b + hk * A.lk.h;
+    const T* vp = A.v + b * A.lk.b + hk * A.lk.h;
+    const Strides3 ks{0, A.lk.s1, A.lk.s2};
+    const int qo = pos1 * A.lq.s1 + pos2 * A.lq.s2;
+    f32x4_t acc[D / 16];
+    float lse_v;
+    exact_forward<T, D>(A.p.scale, x, qp + qo, kp, ks, vp, ks, grp, acc, lse_v);
+    store_rows<T, D>(A.out + b * A.lq.b + h * A.lq.h, qo, grp, acc, 1.f);
+    if (grp == 0) A.lse[b * A.ll.b + h * A.ll.h + pos1 * A.ll.s1 + pos2 * A.ll.s2] = lse_v;
+}
+
+// ---------------------------------------------------------------------------
+// Forward.  NCH chunks (2 NCH >= K1 + 1 union rows) per wave.
+// ---------------------------------------------------------------------------
+template <typename T, int D, int NCH>
+__global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) {
+    constexpr int NR = 2 * NCH + 6;
+    unsigned char* smem = lds_base();
+    T* Ks = reinterpret_cast<T*>(smem);
+    T* Vs = Ks + NR * 16 * D;
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int x = xcd_block(blockIdx.x, gridDim.x);
+    const int bt = fdiv(x, a.heads);
+    const int h = x - bt * static_cast<int>(a.heads.d);
+    const int b = fdiv(bt, a.tiles);
+    const int t = bt - b * static_cast<int>(a.tiles.d);
+    const int hk = a.rep.d == 1 ? h : fdiv(h, a.rep);
+    const int* r = a.rec + t * kLeanRec;
+    const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
+    const int U1 = ext & 0xFF, U2 = (ext >> 8) & 0xFF, E1 = (ext >> 16) & 0xFF, E2 = (ext >> 24) & 0xFF;
+
+    // stage the union's K and V rows
+    {
+        const long long kvo = b * a.lk.b + hk * a.lk.h;
+        const int s1 = a.lk.s1 * a.d1 * 2, s2 = a.lk.s2 * a.d2 * 2;
+        lean_stage<T, D>(lean_rsrc(a.k + kvo, a.kbytes), lean_rsrc(a.v + kvo, a.kbytes), Ks, Vs,
+                         (ur0 * a.lk.s1 + uc0 * a.lk.s2) * 2, s1, s2, U1, U2, nst, wave, lane);
+    }
+
+    // the lane's query and its fragments
+    const int qr = 2 * wave + (col >> 3), qc = col & 7;
+    const bool valid = qr < E1 && qc < E2;
+    const int pos1 = pr0 + qr * a.d1, pos2 = pc0 + qc * a.d2;
+    const int qoff = pos1 * a.lq.s1 + pos2 * a.lq.s2;
+    const long long qbo = b * a.lq.b + h * a.lq.h;
+    uint4 qf[D / 32];
+    {
+        const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + qbo, a.qbytes);
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            const uint32_t o = valid ? static_cast<uint32_t>(qoff * 2 + ks * 64 + grp * 16) : kLeanOOR;
+            qf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 0));
+        }
+    }
+    // window of the lane's query, relative to the wave's first union row / the union's first column
+    const int w0 = sbyte(r[6], r[7], 2 * wave), w1 = sbyte(r[6], r[7], 2 * wave + 1);
+    const int first = __builtin_amdgcn_readfirstlane(w0 > 0 ? w0 : 0);
+    const int rlo = valid ? ((col >> 3) ? w1 : w0) - first : 1 << 20;
+    const int clo = sbyte(r[8], r[9], qc);
+    f32x4_t cb[2];
+    lean_colbias(clo, a.K2, grp, cb);
+    int aoff[2][D / 32], toff[2][D / 16];
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) aoff[bb][ks] = lean_score_off<D>(first, col, grp, bb, ks);
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<D>(first, lane, hi, db);
+
+    wait_loads();
+    __syncthreads();
+
+    const unsigned char* Kb = reinterpret_cast<const unsigned char*>(Ks);
+    const unsigned char* Vb = reinterpret_cast<const unsigned char*>(Vs);
+    f32x4_t s[NCH][2];
+    bool rv[NCH];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        s[c][0] = lean_score<T, D>(Kb, aoff, c, 0, qf, cb[0]);
+        s[c][1] = lean_score<T, D>(Kb, aoff, c, 1, qf, cb[1]);
+        const int row = 2 * c + (grp >> 1) - rlo;
+        rv[c] = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1);
+        mx = fmaxp(mx, rv[c] ? max8(s[c]) : -INFINITY);
+    }
+    const float m = max_rows(mx) * a.sc2;
+    const float mref = m == -INFINITY ? 0.f : m;
+    const uint4 ones = make_uint4(Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes);
+    f32x4_t acc[D / 16], lacc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const float off = rv[c] ? -mref : -INFINITY;
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[c][bb][i] = __builtin_amdgcn_exp2f(fmaf(s[c][bb][i], a.sc2, off));
+        const uint4 pk = pack8<T>(s[c]);
+        lean_accumulate<T, D>(Vb, toff, c, pk, acc);
+        lacc = Mma<T>::run(ones, pk, lacc);
+    }
+    const float lsum = lacc[0];
+    const bool redo = valid && item_nonfinite(lane_sum(acc, lsum));
+    if (valid) {
+        const float inv = 1.f / lsum;
+        const __amdgpu_buffer_rsrc_t ro = lean_rsrc(a.out + qbo, a.qbytes);
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) {
+            const uint2 w = make_uint2(Mma<T>::pack(acc[db][0] * inv, acc[db][1] * inv),
+                                       Mma<T>::pack(acc[db][2] * inv, acc[db][3] * inv));
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, w), ro, qoff * 2 + db * 32 + grp * 8,
+                                                  0, 0);
+        }
+        if (grp == 0)
+            a.lse[b * a.ll.b + h * a.ll.h + pos1 * a.ll.s1 + pos2 * a.ll.s2] = (m + __log2f(lsum)) * kLn2;
+    }
+    if (redo) lean_redo_fwd<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, h, hk, grp);
+}
+
+
+template <typename T>
+struct LeanBwdArgs {
+    const int* rec;
+    const T *q, *k, *v, *o, *dout;
+    const float *lse, *dlse;
+    T *dq, *dk, *dv;
+    float* delta;
+    LeanLay lq, lk, ll;           // q, out, dout, dq; k, v, dk, dv; lse, dlse, delta
+    FastDiv heads, tiles, rep;
+    int d1, d2, K1, K2;
+    uint32_t qbytes, kbytes;
+    float sc2, scale;
+    Prob p;
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void lean_redo_bwd_q(const void* kargs, int pos1, int pos2, int b, int h, int hk, int grp) {
+    const LeanBwdArgs<T>& A = *static_cast<const LeanBwdArgs<T>*>(kargs);
+    ExactAxis x[3];
+    x[0] = exact_axis(A.p.ax[0], 0);
+    x[1] = exact_axis(A.p.ax[1], pos1);
+    x[2] = exact_axis(A.p.ax[2], pos2);
+    const long long qb = b * A.lq.b + h * A.lq.h, kb = b * A.lk.b + hk * A.lk.h;
+    const long long lb = b * A.ll.b + h * A.ll.h + pos1 * A.ll.s1 + pos2 * A.ll.s2;
+    const Strides3 ks{0, A.lk.s1, A.lk.s2};
+    const int qo = pos1 * A.lq.s1 + pos2 * A.lq.s2;
+    const T* do_row = A.dout + qb + qo;
+    float di = exact_dot<T, D>(do_row, A.o + qb + qo);
+    if (A.dlse) di -= A.dlse[lb];
+    f32x4_t acc[D / 16];
+    exact_backward_q<T, D>(A.p.scale, x, A.q + qb + qo, do_row, A.lse[lb], di, A.k + kb, ks, A.v + kb, ks, grp, acc);
+    store_rows<T, D>(A.dq + qb, qo, grp, acc, A.p.scale);
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void lean_redo_bwd_kv(const void* kargs, int pos1, int pos2, int b, int hk, int grp) {
+    const LeanBwdArgs<T>& A = *static_cast<const LeanBwdArgs<T>*>(kargs);
+    ExactAxis x[3];
+    x[0] = exact_axis(A.p.ax[0], 0);
+    x[1] = exact_axis(A.p.ax[1], pos1);
+    x[2] = exact_axis(A.p.ax[2], pos2);
+    const long long kb = b * A.lk.b + hk * A.lk.h;
+    const int ko = pos1 * A.lk.s1 + pos2 * A.lk.s2;
+    const Strides3 qs{0, A.lq.s1, A.lq.s2}, ls{0, A.ll.s1, A.ll.s2};
+    f32x4_t g[D / 16];
+    const int rep = A.p.rep;
+    exact_zero(g);
+#pragma unroll 1
+    for (int h = hk * rep; h < (hk + 1) * rep; ++h) {
+        const long long qb = b * A.lq.b + h * A.lq.h, lb = b * A.ll.b + h * A.ll.h;
+        exact_backward_kv<T, D, true>(A.p.scale, x, A.k + kb + ko, A.v + kb + ko, A.q + qb, qs, A.dout + qb, qs,
+                                      A.lse + lb, ls, A.delta + lb, ls, grp, g);
+    }
+    store_rows<T, D>(A.dv + kb, ko, grp, g, 1.f);
+    exact_zero(g);
+#pragma unroll 1
+    for (int h = hk * rep; h < (hk + 1) * rep; ++h) {
+        const long long qb = b * A.lq.b + h * A.lq.h, lb = b * A.ll.b + h * A.ll.h;
+        exact_backward_kv<T, D, false>(A.p.scale, x, A.k + kb + ko, A.v + kb + ko, A.q + qb, qs, A.dout + qb, qs,
+                                       A.lse + lb, ls, A.delta + lb, ls, grp, g);
+    }
+    store_rows<T, D>(A.dk + kb, ko, grp, g, A.p.scale);
+}
+
+// ---------------------------------------------------------------------------
+// Backward, query side: delta = dO . O - dlse (written for the key side),
+// dq = scale * sum P (dP - delta) k with P = exp(scale q.k - lse).  The dP
+// product starts from -delta.
+// ---------------------------------------------------------------------------
+template <typename T, int D, int NCH>
+__global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_q(LeanBwdArgs<T> a) {
+    constexpr int NR = 2 * NCH + 6;
+    unsigned char* smem = lds_base();
+    T* Ks = reinterpret_cast<T*>(smem);
+    T* Vs = Ks + NR * 16 * D;
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int x = xcd_block(blockIdx.x, gridDim.x);
+    const int bt = fdiv(x, a.heads);
+    const int h = x - bt * static_cast<int>(a.heads.d);
+    const int b = fdiv(bt, a.tiles);
+    const int t = bt - b * static_cast<int>(a.tiles.d);
+    const int hk = a.rep.d == 1 ? h : fdiv(h, a.rep);
+    const int* r = a.rec + t * kLeanRec;
+    const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
+    const int U1 = ext & 0xFF, U2 = (ext >> 8) & 0xFF, E1 = (ext >> 16) & 0xFF, E2 = (ext >> 24) & 0xFF;
+    {
+        const long long kvo = b * a.lk.b + hk * a.lk.h;
+        lean_stage<T, D>(lean_rsrc(a.k + kvo, a.kbytes), lean_rsrc(a.v + kvo, a.kbytes), Ks, Vs,
+                         (ur0 * a.lk.s1 + uc0 * a.lk.s2) * 2, a.lk.s1 * a.d1 * 2, a.lk.s2 * a.d2 * 2, U1, U2, nst,
+                         wave, lane);
+    }
+    const int qr = 2 * wave + (col >> 3), qc = col & 7;
+    const bool valid = qr < E1 && qc < E2;
+    const int pos1 = pr0 + qr * a.d1, pos2 = pc0 + qc * a.d2;
+    const int qoff = pos1 * a.lq.s1 + pos2 * a.lq.s2;
+    const long long qbo = b * a.lq.b + h * a.lq.h;
+    const long long lo = b * a.ll.b + h * a.ll.h + pos1 * a.ll.s1 + pos2 * a.ll.s2;
+    uint4 qf[D / 32], gf[D / 32], of[D / 32];
+    {
+        const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + qbo, a.qbytes);
+        const __amdgpu_buffer_rsrc_t rg = lean_rsrc(a.dout + qbo, a.qbytes);
+        const __amdgpu_buffer_rsrc_t ro = lean_rsrc(a.o + qbo, a.qbytes);
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            const uint32_t o = valid ? static_cast<uint32_t>(qoff * 2 + ks * 64 + grp * 16) : kLeanOOR;
+            qf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 0));
+            gf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rg, o, 0, 0));
+            of[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ro, o, 0, 0));
+        }
+    }
+    const float L2 = valid ? a.lse[lo] * kLog2e : 0.f;
+    const float dl = (valid && a.dlse) ? a.dlse[lo] : 0.f;
+    const int w0 = sbyte(r[6], r[7], 2 * wave), w1 = sbyte(r[6], r[7], 2 * wave + 1);
+    const int first = __builtin_amdgcn_readfirstlane(w0 > 0 ? w0 : 0);
+    const int rlo = valid ? ((col >> 3) ? w1 : w0) - first : 1 << 20;
+    f32x4_t cb[2];
+    lean_colbias(sbyte(r[8], r[9], qc), a.K2, grp, cb);
+    int aoff[2][D / 32], toff[2][D / 16];
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) aoff[bb][ks] = lean_score_off<D>(first, col, grp, bb, ks);
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<D>(first, lane, hi, db);
+
+    // delta from this lane's 8 head dims per 32, summed over the 4 lane rows
+    float di = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+        const T* g8 = reinterpret_cast<const T*>(&gf[ks]);
+        const T* o8 = reinterpret_cast<const T*>(&of[ks]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) di = fmaf(to_f(g8[e]), to_f(o8[e]), di);
+    }
+    di = sum_rows(di) - dl;
+    if (valid && grp == 0) a.delta[lo] = di;
+    const f32x4_t nd = f32x4_t{-di, -di, -di, -di};
+
+    wait_loads();
+    __syncthreads();
+
+    const unsigned char* Kb = reinterpret_cast<const unsigned char*>(Ks);
+    const unsigned char* Vb = reinterpret_cast<const unsigned char*>(Vs);
+    f32x4_t acc[D / 16];
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        f32x4_t s[2], dp[2];
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+            s[bb] = lean_score<T, D>(Kb, aoff, c, bb, qf, cb[bb]);
+            dp[bb] = lean_score<T, D>(Vb, aoff, c, bb, gf, nd);
+        }
+        const int row = 2 * c + (grp >> 1) - rlo;
+        const float off = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1) ? -L2 : -INFINITY;
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], a.sc2, off)) * dp[bb][i];
+        lean_accumulate<T, D>(Kb, toff, c, pack8<T>(s), acc);
+    }
+    const bool redo = valid && item_nonfinite(lane_sum(acc, 0.f));
+    if (valid) {
+        const __amdgpu_buffer_rsrc_t rd = lean_rsrc(a.dq + qbo, a.qbytes);
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) {
+            const uint2 w = make_uint2(Mma<T>::pack(acc[db][0] * a.scale, acc[db][1] * a.scale),
+                                       Mma<T>::pack(acc[db][2] * a.scale, acc[db][3] * a.scale));
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, w), rd, qoff * 2 + db * 32 + grp * 8,
+                                                  0, 0);
+        }
+    }
+    if (redo) lean_redo_bwd_q<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, h, hk, grp);
+}
+
+// ---------------------------------------------------------------------------
+// Backward, key side (one q head per kv head): over the queries attending
+// each key, dv = sum P dO and dk = scale * sum P (dP - delta) q.  The union
+// of the attending queries is staged (q and dO rows, and per slot
+// -lse log2 e and -delta); a wave walks its own union rows, at most
+// MAXCH chunks.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> a, int nr) {
+    unsigned char* smem = lds_base();
+    T* Qs = reinterpret_cast<T*>(smem);
+    T* Gs = Qs + nr * 16 * D;
+    float* NL = reinterpret_cast<float*>(Gs + nr * 16 * D);
+    float* ND = NL + nr * 16;
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int x = xcd_block(blockIdx.x, gridDim.x);
+    const int bt = fdiv(x, a.heads);
+    const int hk = x - bt * static_cast<int>(a.heads.d);  // kv head (one q head each)
+    const int b = fdiv(bt, a.tiles);
+    const int t = bt - b * static_cast<int>(a.tiles.d);
+    const int h = hk;
+    const int* r = a.rec + t * kLeanRec;
+    const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
+    const int U1 = ext & 0xFF, U2 = (ext >> 8) & 0xFF, E1 = (ext >> 16) & 0xFF, E2 = (ext >> 24) & 0xFF;
+    const int kr = 2 * wave + (col >> 3), kc = col & 7;
+    const bool valid = kr < E1 && kc < E2;
+    const int pos1 = pr0 + kr * a.d1, pos2 = pc0 + kc * a.d2;
+    const int koff = pos1 * a.lk.s1 + pos2 * a.lk.s2;
+    const long long kbo = b * a.lk.b + hk * a.lk.h;
+    if (r[14]) {  // no query attends these keys
+        if (valid) {
+            const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.dk + kbo, a.kbytes);
+            const __amdgpu_buffer_rsrc_t rv = lean_rsrc(a.dv + kbo, a.kbytes);
+#pragma unroll
+            for (int db = 0; db < D / 16; ++db) {
+                __builtin_amdgcn_raw_buffer_store_b64(v2u32_t{0u, 0u}, rk, koff * 2 + db * 32 + grp * 8, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b64(v2u32_t{0u, 0u}, rv, koff * 2 + db * 32 + grp * 8, 0, 0);
+            }
+        }
+        return;
+    }
+    // per-slot -lse log2 e and -delta: slot threadIdx.x (and up, past 256 slots)
+    const long long lbase = b * a.ll.b + h * a.ll.h;
+    const auto slot_pos = [&](int sidx, bool& in) {
+        const int u = sidx >> 4, cc = sidx & 15;
+        in = u < U1 && cc < U2;
+        return (ur0 + (in ? u : 0) * a.d1) * a.ll.s1 + (uc0 + (in ? cc : 0) * a.d2) * a.ll.s2;
+    };
+    bool sin;
+    const int sp = slot_pos(threadIdx.x, sin);
+    const float sl = a.lse[lbase + sp], sd = a.delta[lbase + sp];
+    {
+        const long long qo = b * a.lq.b + h * a.lq.h;
+        lean_stage<T, D>(lean_rsrc(a.q + qo, a.qbytes), lean_rsrc(a.dout + qo, a.qbytes), Qs, Gs,
+                         (ur0 * a.lq.s1 + uc0 * a.lq.s2) * 2, a.lq.s1 * a.d1 * 2, a.lq.s2 * a.d2 * 2, U1, U2, nst,
+                         wave, lane);
+    }
+    uint4 kf[D / 32], vf[D / 32];
+    {
+        const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.k + kbo, a.kbytes);
+        const __amdgpu_buffer_rsrc_t rv = lean_rsrc(a.v + kbo, a.kbytes);
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            const uint32_t o = valid ? static_cast<uint32_t>(koff * 2 + ks * 64 + grp * 16) : kLeanOOR;
+            kf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, o, 0, 0));
+            vf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, 0));
+        }
+    }
+    // the wave's union rows [first, last]; the lane's attending rows and columns
+    const int first = __builtin_amdgcn_readfirstlane(sbyte(r[6], r[7], 2 * wave));
+    const int last = __builtin_amdgcn_readfirstlane(sbyte(r[10], r[11], 2 * wave + 1));
+    const int nch = (last - first + 2) >> 1;
+    // attending rows [rlo, rlo + rn) of the wave's rows, columns [clo, chi];
+    // an unattended key has an empty range (rn <= 0, chi < clo)
+    const int rlo = sbyte(r[6], r[7], kr) - first;
+    const int rn = valid ? sbyte(r[10], r[11], kr) - first - rlo + 1 : 0;
+    const int clo = sbyte(r[8], r[9], kc), chi = sbyte(r[12], r[13], kc);
+    f32x4_t cb[2];
+    lean_colbias(clo, chi >= clo ? chi - clo + 1 : 0, grp, cb);
+    int aoff[2][D / 32], toff[2][D / 16];
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) aoff[bb][ks] = lean_score_off<D>(first, col, grp, bb, ks);
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<D>(first, lane, hi, db);
+
+    wait_loads();
+    if (static_cast<int>(threadIdx.x) < nr * 16) {
+        NL[threadIdx.x] = sin ? -sl * kLog2e : 0.f;
+        ND[threadIdx.x] = sin ? -sd : 0.f;
+    }
+    for (int s = threadIdx.x + 64 * kLeanWaves; s < nr * 16; s += 64 * kLeanWaves) {
+        bool in;
+        const int o = slot_pos(s, in);
+        NL[s] = in ? -a.lse[lbase + o] * kLog2e : 0.f;
+        ND[s] = in ? -a.delta[lbase + o] : 0.f;
+    }
+    lds_publish_barrier();
+
+    const unsigned char* Qb = reinterpret_cast<const unsigned char*>(Qs);
+    const unsigned char* Gb = reinterpret_cast<const unsigned char*>(Gs);
+    f32x4_t gk[D / 16], gv[D / 16];
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) gk[db] = gv[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const float* nlp = NL + first * 16 + 8 * grp;
+    const float* ndp = ND + first * 16 + 8 * grp;
+#pragma unroll 1
+    for (int c = 0; c < nch; ++c) {
+        const f32x4_t nd[2] = {*reinterpret_cast<const f32x4_t*>(ndp + 32 * c),
+                               *reinterpret_cast<const f32x4_t*>(ndp + 32 * c + 4)};
+        const f32x4_t nl[2] = {*reinterpret_cast<const f32x4_t*>(nlp + 32 * c),
+                               *reinterpret_cast<const f32x4_t*>(nlp + 32 * c + 4)};
+        f32x4_t s[2], dp[2];
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+            s[bb] = lean_score<T, D>(Qb, aoff, c, bb, kf, cb[bb]);
+            dp[bb] = lean_score<T, D>(Gb, aoff, c, bb, vf, nd[bb]);
+        }
+        const int row = 2 * c + (grp >> 1) - rlo;
+        const bool rv = row >= 0 && row < rn;
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], a.sc2, rv ? nl[bb][i] : -INFINITY));
+                dp[bb][i] *= s[bb][i];
+            }
+        lean_accumulate<T, D>(Gb, toff, c, pack8<T>(s), gv);
+        lean_accumulate<T, D>(Qb, toff, c, pack8<T>(dp), gk);
+    }
+    const bool redo = valid && item_nonfinite(lane_sum(gk, lane_sum(gv, 0.f)));
+    if (valid) {
+        const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.dk + kbo, a.kbytes);
+        const __amdgpu_buffer_rsrc_t rv = lean_rsrc(a.dv + kbo, a.kbytes);
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) {
+            const uint2 wk = make_uint2(Mma<T>::pack(gk[db][0] * a.scale, gk[db][1] * a.scale),
+                                        Mma<T>::pack(gk[db][2] * a.scale, gk[db][3] * a.scale));
+            const uint2 wv = make_uint2(Mma<T>::pack(gv[db][0], gv[db][1]), Mma<T>::pack(gv[db][2], gv[db][3]));
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, wk), rk, koff * 2 + db * 32 + grp * 8,
+                                                  0, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, wv), rv, koff * 2 + db * 32 + grp * 8,
+                                                  0, 0);
+        }
+    }
+    if (redo) lean_redo_bwd_kv<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, hk, grp);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+namespace {
+
+// Tile records of one problem geometry (axes 1 and 2), query tiles (key
+// false) or key tiles (key true), cached per device for the process.
+struct LeanGeo {
+    int dev, key;
+    int len[2], k[2], dil[2], causal[2];
+    int* ptr;
+    int ntiles, nst_max, rows_max;
+    std::vector<int> host;  // source of the asynchronous upload, kept with the table
+};
+
+struct LeanAxisTile {
+    int pos0, upos0, E, U;
+    int ws[8];   // per item: window start (key tiles: first attending query), union-relative
+    int we[8];   // key tiles: last attending query, union-relative
+};
+
+// Tile t of class r on one axis: items J = 8t .. 8t+7 (class coordinates).
+bool lean_axis_tile(const Axis& A, int r, int t, bool key, LeanAxisTile& o) {
+    const ClassAxis c = class_axis(A, r);
+    const int J = 8 * t;
+    const int jend = std::min(J + 8, c.n) - 1;
+    o.E = jend - J + 1;
+    int lo, hi;
+    if (!key) {
+        lo = std::max(class_ws(c, J), 0);
+        hi = std::min(class_ws(c, jend) + c.K - 1, c.n - 1);
+    } else {
+        int x;
+        class_span(c, J, lo, x);
+        class_span(c, jend, x, hi);
+        if (hi < lo) return false;
+    }
+    o.U = hi - lo + 1;
+    o.pos0 = r + J * A.dil;
+    o.upos0 = r + lo * A.dil;
+    for (int e = 0; e < 8; ++e) {
+        const int j = std::min(J + e, jend);
+        if (!key) {
+            o.ws[e] = class_ws(c, j) - lo;
+            o.we[e] = o.ws[e] + c.K - 1;
+        } else {
+            int a0, a1;
+            class_span(c, j, a0, a1);
+            o.ws[e] = a0 - lo;
+            o.we[e] = a1 - lo;
+        }
+    }
+    return true;
+}
+
+int pack_bytes(const int* v, int i0) {
+    uint32_t w = 0;
+    for (int e = 0; e < 4; ++e) w |= (static_cast<uint32_t>(v[i0 + e]) & 0xFFu) << (8 * e);
+    return static_cast<int>(w);
+}
+
+// Builds (or finds) the records.  Query tiles: rows of a wave start at
+// max(ws[2w], 0) and span at most K1 + 1 rows; nst = rows to stage.
+const LeanGeo* lean_geometry(const Prob& p, bool key, int nch, hipStream_t s) {
+    static std::mutex mu;
+    static std::vector<LeanGeo*> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    LeanGeo k{};
+    k.dev = dev;
+    k.key = key ? 1 : 0;
+    for (int a = 0; a < 2; ++a) {
+        k.len[a] = p.ax[a + 1].len;
+        k.k[a] = p.ax[a + 1].k;
+        k.dil[a] = p.ax[a + 1].dil;
+        k.causal[a] = p.ax[a + 1].causal;
+    }
+    std::lock_guard<std::mutex> g(mu);
+    for (LeanGeo* e : cache)
+        if (std::memcmp(e, &k, offsetof(LeanGeo, ptr)) == 0) return e;
+    if (!device_alloc_allowed()) return nullptr;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
+    const Axis &A1 = p.ax[1], &A2 = p.ax[2];
+    std::vector<int> h;
+    int nst_max = 0, rows_max = 0;
+    for (int r1 = 0; r1 < A1.dil; ++r1) {
+        const int n1 = (A1.len - r1 + A1.dil - 1) / A1.dil;
+        for (int r2 = 0; r2 < A2.dil; ++r2) {
+            const int n2 = (A2.len - r2 + A2.dil - 1) / A2.dil;
+            for (int t1 = 0; t1 < (n1 + 7) / 8; ++t1) {
+                LeanAxisTile a1;
+                const bool ok1 = lean_axis_tile(A1, r1, t1, key, a1);
+                for (int t2 = 0; t2 < (n2 + 7) / 8; ++t2) {
+                    LeanAxisTile a2;
+                    const bool ok2 = lean_axis_tile(A2, r2, t2, key, a2);
+                    int rec[kLeanRec] = {};
+                    if (ok1 && ok2) {
+                        if (a2.U > 16) return nullptr;  // eligibility should have excluded it
+                        // rows a wave reads: query tiles NCH chunks from max(ws, 0);
+                        // key tiles its own attending rows, in whole chunks
+                        int nst = 0;
+                        for (int w = 0; w < 4; ++w) {
+                            const int f = key ? a1.ws[2 * w] : std::max(a1.ws[2 * w], 0);
+                            const int rows = a1.we[2 * w + 1] - f + 1;
+                            rows_max = std::max(rows_max, rows);
+                            nst = std::max(nst, f + (key ? 2 * ((std::max(rows, 0) + 1) / 2) : 2 * nch));
+                        }
+                        nst = std::max(nst, a1.U);
+                        nst_max = std::max(nst_max, nst);
+                        rec[0] = a1.pos0;
+                        rec[1] = a2.pos0;
+                        rec[2] = a1.upos0;
+                        rec[3] = a2.upos0;
+                        rec[4] = a1.U | (a2.U << 8) | (a1.E << 16) | (a2.E << 24);
+                        rec[5] = nst;
+                        rec[6] = pack_bytes(a1.ws, 0);
+                        rec[7] = pack_bytes(a1.ws, 4);
+                        rec[8] = pack_bytes(a2.ws, 0);
+                        rec[9] = pack_bytes(a2.ws, 4);
+                        rec[10] = pack_bytes(a1.we, 0);
+                        rec[11] = pack_bytes(a1.we, 4);
+                        rec[12] = pack_bytes(a2.we, 0);
+                        rec[13] = pack_bytes(a2.we, 4);
+                    } else {
+                        // a key tile that no query attends: extents only (zero gradients)
+                        rec[0] = ok1 ? a1.pos0 : r1 + 8 * t1 * A1.dil;
+                        rec[1] = ok2 ? a2.pos0 : r2 + 8 * t2 * A2.dil;
+                        rec[4] = (std::min(8, n1 - 8 * t1) << 16) | (std::min(8, n2 - 8 * t2) << 24);
+                        rec[14] = 1;
+                    }
+                    h.insert(h.end(), rec, rec + kLeanRec);
+                }
+            }
+        }
+    }
+    if (!key && nst_max > 2 * nch + 6) return nullptr;
+    if (key && nst_max > 32) return nullptr;
+    int* d = nullptr;
+    const size_t bytes = h.size() * sizeof(int);
+    if (hipMalloc(reinterpret_cast<void**>(&d), bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    LeanGeo* e = new LeanGeo(k);
+    e->host = std::move(h);
+    // stream-ordered upload; the host copy lives as long as the table
+    if (hipMemcpyAsync(d, e->host.data(), bytes, hipMemcpyHostToDevice, s) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(d);
+        delete e;
+        return nullptr;
+    }
+    e->ptr = d;
+    e->ntiles = static_cast<int>(e->host.size() / kLeanRec);
+    e->nst_max = nst_max;
+    e->rows_max = rows_max;
+    cache.push_back(e);
+    return e;
+}
+
+LeanLay lean_lay(const Lay& l) {
+    return LeanLay{l.b, l.h, static_cast<int>(l.s1), static_cast<int>(l.s2)};
+}
+
+// Byte range of one (batch, head) plane of an operand of head dim D.
+uint32_t plane_bytes(const Prob& p, const Lay& l, int D) {
+    const long long v = ((static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
+                         (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + D) * 2;
+    return static_cast<uint32_t>(v);
+}
+
+bool lean_switch() {
+    static const bool on = [] {
+        const char* e = std::getenv("NATTEN_HIP_LEAN");
+        return !(e && std::strcmp(e, "0") == 0);
+    }();
+    return on;
+}
+
+// Chunks per wave for kernel K1 (query side): K1 + 1 rows.
+int lean_nch(int K1) { return (K1 + 2) / 2; }
+
+}  // namespace
+
+// Lean path eligibility: a 2-D (or 2-D-padded) problem at stride 1, head dim
+// 32 or 64 for q, k and v, 16-bit, K2 <= 9, K1 <= 9, per-axis extents below
+// 2^15, planes below 2^30 bytes, q/out and k/v sharing one layout each.
+bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list<Lay> qside,
+                   std::initializer_list<Lay> kvside) {
+    if (!lean_switch() || dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f)) return false;
+    if (p.Dqk != p.Dv || (p.Dqk != 32 && p.Dqk != 64)) return false;
+    if (p.ax[0].len != 1 || p.ax[0].k != 1) return false;
+    for (int a = 1; a < 3; ++a) {
+        const Axis& A = p.ax[a];
+        if (A.st != 1 || A.k > 9 || A.len >= (1 << 15)) return false;
+    }
+    if (!all_same(qside) || !all_same(kvside)) return false;
+    for (const Lay& l : {*qside.begin(), *kvside.begin()}) {
+        if (l.s1 < 0 || l.s2 < 0 || l.b < 0 || l.h < 0) return false;
+        const long long v = ((static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
+                             (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + p.Dqk) * 2;
+        if (v >= (1LL << 30)) return false;
+    }
+    return true;
+}
+
+template <typename T, int D, int NCH>
+hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, const void* k, Lay lk,
+                        const void* v, void* o, float* lse, Lay ll, hipStream_t s) {
+    LeanFwdArgs<T> a{};
+    a.rec = g->ptr;
+    a.q = static_cast<const T*>(q);
+    a.k = static_cast<const T*>(k);
+    a.v = static_cast<const T*>(v);
+    a.out = static_cast<T*>(o);
+    a.lse = lse;
+    a.lq = lean_lay(lq);
+    a.lk = lean_lay(lk);
+    a.ll = lean_lay(ll);
+    a.heads = make_fastdiv(p.Hq);
+    a.tiles = make_fastdiv(g->ntiles);
+    a.rep = make_fastdiv(p.rep);
+    a.d1 = p.ax[1].dil;
+    a.d2 = p.ax[2].dil;
+    a.K1 = p.ax[1].k;
+    a.K2 = p.ax[2].k;
+    a.qbytes = plane_bytes(p, lq, D);
+    a.kbytes = plane_bytes(p, lk, D);
+    a.sc2 = p.scale * kLog2e;
+    a.p = p;
+    const long long blocks = static_cast<long long>(p.B) * p.Hq * g->ntiles;
+    const size_t shm = kLdsPad + static_cast<size_t>(2) * (2 * NCH + 6) * 16 * D * sizeof(T);
+    NA_LAUNCH("na_fwd_lean", (k_lean_fwd<T, D, NCH>), dim3(static_cast<unsigned>(blocks)), dim3(64 * kLeanWaves), shm,
+              s, a);
+    return hipGetLastError();
+}
+
+// Forward on the lean kernels; hipErrorNotSupported when this problem has no
+// lean launch (the caller then takes the general tile kernels).
+hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
+                        Lay lo, float* lse, Lay ll, int dtype, hipStream_t s) {
+    (void)lv;
+    (void)lo;
+    const int nch = lean_nch(p.ax[1].k);
+    if (static_cast<long long>(p.B) * p.Hq * 4096 >= (1LL << 31)) return hipErrorNotSupported;
+    const LeanGeo* g = lean_geometry(p, false, nch, s);
+    if (!g) return hipErrorNotSupported;
+#define NA_LF(T, DD, N) return lean_fwd_run<T, DD, N>(p, g, q, lq, k, lk, v, o, lse, ll, s)
+#define NA_LF_N(T, DD)          \
+    switch (nch) {              \
+        case 1: NA_LF(T, DD, 1); \
+        case 2: NA_LF(T, DD, 2); \
+        case 3: NA_LF(T, DD, 3); \
+        case 4: NA_LF(T, DD, 4); \
+        default: NA_LF(T, DD, 5); \
+    }
+    if (dtype == NATTEN_BF16) {
+        if (p.Dqk == 32) NA_LF_N(bf16, 32);
+        NA_LF_N(bf16, 64);
+    }
+    if (p.Dqk == 32) NA_LF_N(f16, 32);
+    NA_LF_N(f16, 64);
+#undef NA_LF_N
+#undef NA_LF
+}
+
+template <typename T, int D>
+LeanBwdArgs<T> lean_bwd_args(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v,
+                             const void* o, const void* dout, const float* lse, Lay ll, const float* dlse, void* dq,
+                             void* dk, void* dv, float* delta) {
+    LeanBwdArgs<T> a{};
+    a.q = static_cast<const T*>(q);
+    a.k = static_cast<const T*>(k);
+    a.v = static_cast<const T*>(v);
+    a.o = static_cast<const T*>(o);
+    a.dout = static_cast<const T*>(dout);
+    a.lse = lse;
+    a.dlse = dlse;
+    a.dq = static_cast<T*>(dq);
+    a.dk = static_cast<T*>(dk);
+    a.dv = static_cast<T*>(dv);
+    a.delta = delta;
+    a.lq = lean_lay(lq);
+    a.lk = lean_lay(lk);
+    a.ll = lean_lay(ll);
+    a.rep = make_fastdiv(p.rep);
+    a.d1 = p.ax[1].dil;
+    a.d2 = p.ax[2].dil;
+    a.K1 = p.ax[1].k;
+    a.K2 = p.ax[2].k;
+    a.qbytes = plane_bytes(p, lq, D);
+    a.kbytes = plane_bytes(p, lk, D);
+    a.sc2 = p.scale * kLog2e;
+    a.scale = p.scale;
+    a.p = p;
+    return a;
+}
+
+template <typename T, int D, int NCH>
+hipError_t lean_bwd_run(const Prob& p, const LeanGeo* gq, const LeanGeo* gk, const LeanBwdArgs<T>& base,
+                        hipStream_t s) {
+    LeanBwdArgs<T> a = base;
+    a.rec = gq->ptr;
+    a.heads = make_fastdiv(p.Hq);
+    a.tiles = make_fastdiv(gq->ntiles);
+    {
+        const long long blocks = static_cast<long long>(p.B) * p.Hq * gq->ntiles;
+        const size_t shm = kLdsPad + static_cast<size_t>(2) * (2 * NCH + 6) * 16 * D * sizeof(T);
+        NA_LAUNCH("na_bwd_q_lean", (k_lean_bwd_q<T, D, NCH>), dim3(static_cast<unsigned>(blocks)),
+                  dim3(64 * kLeanWaves), shm, s, a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    a.rec = gk->ptr;
+    a.heads = make_fastdiv(p.Hkv);
+    a.tiles = make_fastdiv(gk->ntiles);
+    const int nr = std::max(gk->nst_max, 1);
+    const long long blocks = static_cast<long long>(p.B) * p.Hkv * gk->ntiles;
+    const size_t shm = kLdsPad + static_cast<size_t>(nr) * 16 * (2 * D * sizeof(T) + 2 * sizeof(float));
+    auto kern = k_lean_bwd_kv<T, D>;
+    hipError_t e = allow_lds(kern, shm);
+    if (e != hipSuccess) return e;
+    NA_LAUNCH("na_bwd_kv_lean", kern, dim3(static_cast<unsigned>(blocks)), dim3(64 * kLeanWaves), shm, s, a, nr);
+    return hipGetLastError();
+}
+
+// Backward on the lean kernels (one q head per kv head); hipErrorNotSupported
+// when this problem has no lean launch.
+hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
+                         const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
+                         const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
+                         float* delta, Lay lde, int dtype, hipStream_t s) {
+    (void)lv;
+    (void)lo;
+    (void)ldo;
+    (void)ldq;
+    (void)ldk;
+    (void)ldv;
+    if (p.rep != 1) return hipErrorNotSupported;
+    if (!same_lay(ll, lde) || (dlse && !same_lay(ll, ldl))) return hipErrorNotSupported;
+    if (static_cast<long long>(p.B) * p.Hq * 4096 >= (1LL << 31)) return hipErrorNotSupported;
+    const int nch = lean_nch(p.ax[1].k);
+    const LeanGeo* gq = lean_geometry(p, false, nch, s);
+    const LeanGeo* gk = gq ? lean_geometry(p, true, nch, s) : nullptr;
+    if (!gq || !gk) return hipErrorNotSupported;
+#define NA_LB(T, DD, N)                                                                                           \
+    return lean_bwd_run<T, DD, N>(p, gq, gk,                                                                      \
+                                  lean_bwd_args<T, DD>(p, q, lq, k, lk, v, o, dout, lse, ll, dlse, dq, dk, dv, delta), \
+                                  s)
+#define NA_LB_N(T, DD)          \
+    switch (nch) {              \
+        case 1: NA_LB(T, DD, 1); \
+        case 2: NA_LB(T, DD, 2); \
+        case 3: NA_LB(T, DD, 3); \
+        case 4: NA_LB(T, DD, 4); \
+        default: NA_LB(T, DD, 5); \
+    }
+    if (dtype == NATTEN_BF16) {
+        if (p.Dqk == 32) NA_LB_N(bf16, 32);
+        NA_LB_N(bf16, 64);
+    }
+    if (p.Dqk == 32) NA_LB_N(f16, 32);
+    NA_LB_N(f16, 64);
+#undef NA_LB_N
+#undef NA_LB
+}
+
+}  // namespace na
