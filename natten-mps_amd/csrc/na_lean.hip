@@ -308,13 +308,14 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
 
 template <typename T>
 struct LeanBwdArgs {
-    const int* rec;
+    const int *rec, *rec_k;       // query-tile and key-tile records
     const T *q, *k, *v, *o, *dout;
     const float *lse, *dlse;
     T *dq, *dk, *dv;
     float* delta;
     LeanLay lq, lk, ll;           // q, out, dout, dq; k, v, dk, dv; lse, dlse, delta
-    FastDiv heads, tiles, rep;
+    FastDiv heads, tiles, rep;    // task decode (q heads, spatial tiles)
+    int nr;                       // LDS rows of a key tile
     int d1, d2, K1, K2;
     uint32_t qbytes, kbytes;
     float sc2, scale;
@@ -375,15 +376,15 @@ __device__ __forceinline__ void lean_redo_bwd_kv(const void* kargs, int pos1, in
 // dq = scale * sum P (dP - delta) k with P = exp(scale q.k - lse).  The dP
 // product starts from -delta.
 // ---------------------------------------------------------------------------
+// Query tile of task x = (batch, tile, head), head fastest.
 template <typename T, int D, int NCH>
-__global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_q(LeanBwdArgs<T> a) {
+__device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) {
     constexpr int NR = 2 * NCH + 6;
     unsigned char* smem = lds_base();
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + NR * 16 * D;
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int x = xcd_block(blockIdx.x, gridDim.x);
     const int bt = fdiv(x, a.heads);
     const int h = x - bt * static_cast<int>(a.heads.d);
     const int b = fdiv(bt, a.tiles);
@@ -434,15 +435,10 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_q(LeanBwdArgs<T> a
 #pragma unroll
         for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<D>(first, lane, hi, db);
 
-    // delta from this lane's 8 head dims per 32, summed over the 4 lane rows
+    // delta = dO . O: this lane's 8 head dims per 32, then the 4 lane rows
     float di = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) {
-        const T* g8 = reinterpret_cast<const T*>(&gf[ks]);
-        const T* o8 = reinterpret_cast<const T*>(&of[ks]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) di = fmaf(to_f(g8[e]), to_f(o8[e]), di);
-    }
+    for (int ks = 0; ks < D / 32; ++ks) di = dot8<T>(gf[ks], of[ks], di);
     di = sum_rows(di) - dl;
     if (valid && grp == 0) a.delta[lo] = di;
     const f32x4_t nd = f32x4_t{-di, -di, -di, -di};
@@ -492,8 +488,11 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_q(LeanBwdArgs<T> a
 // -lse log2 e and -delta); a wave walks its own union rows, at most
 // MAXCH chunks.
 // ---------------------------------------------------------------------------
+// Key tile of task x = (batch, tile, kv head): reads the delta rows the
+// query tiles wrote.
 template <typename T, int D>
-__global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> a, int nr) {
+__device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x) {
+    const int nr = a.nr;
     unsigned char* smem = lds_base();
     T* Qs = reinterpret_cast<T*>(smem);
     T* Gs = Qs + nr * 16 * D;
@@ -501,13 +500,12 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> 
     float* ND = NL + nr * 16;
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int x = xcd_block(blockIdx.x, gridDim.x);
     const int bt = fdiv(x, a.heads);
     const int hk = x - bt * static_cast<int>(a.heads.d);  // kv head (one q head each)
     const int b = fdiv(bt, a.tiles);
     const int t = bt - b * static_cast<int>(a.tiles.d);
     const int h = hk;
-    const int* r = a.rec + t * kLeanRec;
+    const int* r = a.rec_k + t * kLeanRec;
     const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
     const int U1 = ext & 0xFF, U2 = (ext >> 8) & 0xFF, E1 = (ext >> 16) & 0xFF, E2 = (ext >> 24) & 0xFF;
     const int kr = 2 * wave + (col >> 3), kc = col & 7;
@@ -536,9 +534,9 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> 
     };
     bool sin;
     const int sp = slot_pos(threadIdx.x, sin);
+    const long long qo = b * a.lq.b + h * a.lq.h;
     const float sl = a.lse[lbase + sp], sd = a.delta[lbase + sp];
     {
-        const long long qo = b * a.lq.b + h * a.lq.h;
         lean_stage<T, D>(lean_rsrc(a.q + qo, a.qbytes), lean_rsrc(a.dout + qo, a.qbytes), Qs, Gs,
                          (ur0 * a.lq.s1 + uc0 * a.lq.s2) * 2, a.lq.s1 * a.d1 * 2, a.lq.s2 * a.d2 * 2, U1, U2, nst,
                          wave, lane);
@@ -635,6 +633,16 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> 
         }
     }
     if (redo) lean_redo_bwd_kv<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, hk, grp);
+}
+
+template <typename T, int D, int NCH>
+__global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_q(LeanBwdArgs<T> a) {
+    lean_bwd_q_tile<T, D, NCH>(a, xcd_block(blockIdx.x, gridDim.x));
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> a) {
+    lean_bwd_kv_tile<T, D>(a, xcd_block(blockIdx.x, gridDim.x));
 }
 
 }  // namespace
@@ -943,26 +951,20 @@ hipError_t lean_bwd_run(const Prob& p, const LeanGeo* gq, const LeanGeo* gk, con
                         hipStream_t s) {
     LeanBwdArgs<T> a = base;
     a.rec = gq->ptr;
+    a.rec_k = gk->ptr;
     a.heads = make_fastdiv(p.Hq);
     a.tiles = make_fastdiv(gq->ntiles);
-    {
-        const long long blocks = static_cast<long long>(p.B) * p.Hq * gq->ntiles;
-        const size_t shm = kLdsPad + static_cast<size_t>(2) * (2 * NCH + 6) * 16 * D * sizeof(T);
-        NA_LAUNCH("na_bwd_q_lean", (k_lean_bwd_q<T, D, NCH>), dim3(static_cast<unsigned>(blocks)),
-                  dim3(64 * kLeanWaves), shm, s, a);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-    }
-    a.rec = gk->ptr;
-    a.heads = make_fastdiv(p.Hkv);
-    a.tiles = make_fastdiv(gk->ntiles);
-    const int nr = std::max(gk->nst_max, 1);
-    const long long blocks = static_cast<long long>(p.B) * p.Hkv * gk->ntiles;
-    const size_t shm = kLdsPad + static_cast<size_t>(nr) * 16 * (2 * D * sizeof(T) + 2 * sizeof(float));
-    auto kern = k_lean_bwd_kv<T, D>;
-    hipError_t e = allow_lds(kern, shm);
+    a.nr = std::max(gk->nst_max, 1);
+    const size_t shm_q = kLdsPad + static_cast<size_t>(2) * (2 * NCH + 6) * 16 * D * sizeof(T);
+    const size_t shm_k = kLdsPad + static_cast<size_t>(a.nr) * 16 * (2 * D * sizeof(T) + 2 * sizeof(float));
+    const long long tasks = static_cast<long long>(p.B) * p.Hq * gq->ntiles;
+    NA_LAUNCH("na_bwd_q_lean", (k_lean_bwd_q<T, D, NCH>), dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves),
+              shm_q, s, a);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    NA_LAUNCH("na_bwd_kv_lean", kern, dim3(static_cast<unsigned>(blocks)), dim3(64 * kLeanWaves), shm, s, a, nr);
+    auto kern = k_lean_bwd_kv<T, D>;
+    if ((e = allow_lds(kern, shm_k)) != hipSuccess) return e;
+    NA_LAUNCH("na_bwd_kv_lean", kern, dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves), shm_k, s, a);
     return hipGetLastError();
 }
 
@@ -980,11 +982,11 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
     (void)ldv;
     if (p.rep != 1) return hipErrorNotSupported;
     if (!same_lay(ll, lde) || (dlse && !same_lay(ll, ldl))) return hipErrorNotSupported;
-    if (static_cast<long long>(p.B) * p.Hq * 4096 >= (1LL << 31)) return hipErrorNotSupported;
+    if (static_cast<long long>(p.B) * p.Hq * 8192 >= (1LL << 31)) return hipErrorNotSupported;
     const int nch = lean_nch(p.ax[1].k);
     const LeanGeo* gq = lean_geometry(p, false, nch, s);
     const LeanGeo* gk = gq ? lean_geometry(p, true, nch, s) : nullptr;
-    if (!gq || !gk) return hipErrorNotSupported;
+    if (!gq || !gk || gq->ntiles != gk->ntiles) return hipErrorNotSupported;
 #define NA_LB(T, DD, N)                                                                                           \
     return lean_bwd_run<T, DD, N>(p, gq, gk,                                                                      \
                                   lean_bwd_args<T, DD>(p, q, lq, k, lk, v, o, dout, lse, ll, dlse, dq, dk, dv, delta), \

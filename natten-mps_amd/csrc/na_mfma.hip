@@ -358,12 +358,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) vo
             // delta from this lane's 8 head dims per 32, summed over the 4 lane rows
             float di = 0.f;
 #pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) {
-                const T* g8 = reinterpret_cast<const T*>(&gf[ks]);
-                const T* o8 = reinterpret_cast<const T*>(&of[ks]);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) di = fmaf(to_f(g8[e]), to_f(o8[e]), di);
-            }
+            for (int ks = 0; ks < D / 32; ++ks) di = dot8<T>(gf[ks], of[ks], di);
             di = sum_rows(di);
             if (dlse && ln.valid) di -= bh_ptr(dlse, ldl, b, h)[vol_off(ldl, ln.pos)];
             if (ln.valid && grp == 0) bh_ptr(delta, lde, b, h)[vol_off(lde, ln.pos)] = di;

@@ -129,6 +129,26 @@ __device__ __forceinline__ float max8(const f32x4_t (&s)[2]) {
     return fmaxp(b, c);
 }
 
+// acc + the 8 products of two runs of 8 16-bit elements, in pairs
+// (v_dot2_f32_bf16 / v_dot2_f32_f16, fp32 accumulation).  Every tile kernel
+// forms delta = dO . O with it in one order (per 8-dim piece, pieces of a
+// lane in k-step order, then the four lanes of an item pairwise), so that
+// the kernels that compute delta agree bit for bit.
+template <typename T>
+__device__ __forceinline__ float dot8(uint4 x, uint4 y, float acc) {
+    const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ys[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (std::is_same<T, bf16>::value)
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, xs[i]), __builtin_bit_cast(bf16x2_t, ys[i]),
+                                                  acc, false);
+        else
+            acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, xs[i]), __builtin_bit_cast(f16x2_t, ys[i]), acc,
+                                         false);
+    }
+    return acc;
+}
+
 // XOR swizzle of the 16-byte pieces of LDS row `row` (D / 8 pieces per row):
 // the 16 rows one score-operand read touches (rows 8x + y + 4b, x, y < 4)
 // land on distinct banks for every head dim.
