@@ -490,14 +490,15 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
 // ---------------------------------------------------------------------------
 // Key tile of task x = (batch, tile, kv head): reads the delta rows the
 // query tiles wrote.
-template <typename T, int D>
+// A wave walks at most MAXC chunks (the host checks its rows fit).
+template <typename T, int D, int MAXC>
 __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x) {
     const int nr = a.nr;
     unsigned char* smem = lds_base();
     T* Qs = reinterpret_cast<T*>(smem);
     T* Gs = Qs + nr * 16 * D;
-    float* NL = reinterpret_cast<float*>(Gs + nr * 16 * D);
-    float* ND = NL + nr * 16;
+    float* NL = reinterpret_cast<float*>(Gs + nr * 16 * D);  // nr * 16 slots, then 8 x -inf
+    float* ND = NL + nr * 16 + 8;
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int bt = fdiv(x, a.heads);
@@ -578,6 +579,8 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
         NL[threadIdx.x] = sin ? -sl * kLog2e : 0.f;
         ND[threadIdx.x] = sin ? -sd : 0.f;
     }
+    // the exponent offsets of lanes whose row test fails: P = 0
+    if (threadIdx.x < 8) NL[nr * 16 + threadIdx.x] = -INFINITY;
     for (int s = threadIdx.x + 64 * kLeanWaves; s < nr * 16; s += 64 * kLeanWaves) {
         bool in;
         const int o = slot_pos(s, in);
@@ -593,25 +596,27 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     for (int db = 0; db < D / 16; ++db) gk[db] = gv[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const float* nlp = NL + first * 16 + 8 * grp;
     const float* ndp = ND + first * 16 + 8 * grp;
-#pragma unroll 1
-    for (int c = 0; c < nch; ++c) {
+    const float* ninf = NL + nr * 16;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        if (c >= nch) break;  // wave-uniform
+        const int row = 2 * c + (grp >> 1) - rlo;
+        // a failed row test reads the -inf entries (one select per chunk)
+        const float* nlc = (row >= 0 && row < rn) ? nlp + 32 * c : ninf;
         const f32x4_t nd[2] = {*reinterpret_cast<const f32x4_t*>(ndp + 32 * c),
                                *reinterpret_cast<const f32x4_t*>(ndp + 32 * c + 4)};
-        const f32x4_t nl[2] = {*reinterpret_cast<const f32x4_t*>(nlp + 32 * c),
-                               *reinterpret_cast<const f32x4_t*>(nlp + 32 * c + 4)};
+        const f32x4_t nl[2] = {*reinterpret_cast<const f32x4_t*>(nlc), *reinterpret_cast<const f32x4_t*>(nlc + 4)};
         f32x4_t s[2], dp[2];
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb) {
             s[bb] = lean_score<T, D>(Qb, aoff, c, bb, kf, cb[bb]);
             dp[bb] = lean_score<T, D>(Gb, aoff, c, bb, vf, nd[bb]);
         }
-        const int row = 2 * c + (grp >> 1) - rlo;
-        const bool rv = row >= 0 && row < rn;
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], a.sc2, rv ? nl[bb][i] : -INFINITY));
+                s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], a.sc2, nl[bb][i]));
                 dp[bb][i] *= s[bb][i];
             }
         lean_accumulate<T, D>(Gb, toff, c, pack8<T>(s), gv);
@@ -640,9 +645,9 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_q(LeanBwdArgs<T> a
     lean_bwd_q_tile<T, D, NCH>(a, xcd_block(blockIdx.x, gridDim.x));
 }
 
-template <typename T, int D>
+template <typename T, int D, int MAXC>
 __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> a) {
-    lean_bwd_kv_tile<T, D>(a, xcd_block(blockIdx.x, gridDim.x));
+    lean_bwd_kv_tile<T, D, MAXC>(a, xcd_block(blockIdx.x, gridDim.x));
 }
 
 }  // namespace
@@ -956,13 +961,14 @@ hipError_t lean_bwd_run(const Prob& p, const LeanGeo* gq, const LeanGeo* gk, con
     a.tiles = make_fastdiv(gq->ntiles);
     a.nr = std::max(gk->nst_max, 1);
     const size_t shm_q = kLdsPad + static_cast<size_t>(2) * (2 * NCH + 6) * 16 * D * sizeof(T);
-    const size_t shm_k = kLdsPad + static_cast<size_t>(a.nr) * 16 * (2 * D * sizeof(T) + 2 * sizeof(float));
+    const size_t shm_k =
+        kLdsPad + static_cast<size_t>(a.nr) * 16 * (2 * D * sizeof(T) + 2 * sizeof(float)) + 8 * sizeof(float);
     const long long tasks = static_cast<long long>(p.B) * p.Hq * gq->ntiles;
     NA_LAUNCH("na_bwd_q_lean", (k_lean_bwd_q<T, D, NCH>), dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves),
               shm_q, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    auto kern = k_lean_bwd_kv<T, D>;
+    auto kern = k_lean_bwd_kv<T, D, NCH + 2>;
     if ((e = allow_lds(kern, shm_k)) != hipSuccess) return e;
     NA_LAUNCH("na_bwd_kv_lean", kern, dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves), shm_k, s, a);
     return hipGetLastError();
@@ -986,7 +992,7 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
     const int nch = lean_nch(p.ax[1].k);
     const LeanGeo* gq = lean_geometry(p, false, nch, s);
     const LeanGeo* gk = gq ? lean_geometry(p, true, nch, s) : nullptr;
-    if (!gq || !gk || gq->ntiles != gk->ntiles) return hipErrorNotSupported;
+    if (!gq || !gk || gq->ntiles != gk->ntiles || gk->rows_max > 2 * (nch + 2)) return hipErrorNotSupported;
 #define NA_LB(T, DD, N)                                                                                           \
     return lean_bwd_run<T, DD, N>(p, gq, gk,                                                                      \
                                   lean_bwd_args<T, DD>(p, q, lq, k, lk, v, o, dout, lse, ll, dlse, dq, dk, dv, delta), \
