@@ -1,13 +1,17 @@
 """Benchmark of the hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--dilation 1] [--no-cpu] [--no-graph]
-                    [--no-split] [--config 3] [--causal FF]
+                    [--no-split] [--no-all] [--config N] [--causal FF]
 
 Default workload: na2d forward+backward at DiNAT scale (B=16, 56x56, 4 heads,
-head dim 32, kernel 7, bf16), BASELINE config 3.  ``--config N`` runs another
-of the five BASELINE configs instead (``--dilation`` for configs 3 and 4,
-``--causal TF`` for config 2); every config carries the CPU baseline of its
-own workload.
+head dim 32, kernel 7, bf16), BASELINE config 3, the headline; the same JSON
+line then carries ``all_configs``: one row per other BASELINE config and
+variant (config 1; config 2 non-causal and causal on axis 0; config 3 at
+dilation 8; config 4 at dilation 1 and 4; config 5), each with its step time,
+TFLOP/s, step HBM-floor fraction, per-kernel launch times, its dominant
+kernel's fraction of 8 TB/s and its own CPU baseline (``--no-all`` skips
+them).  ``--config N`` runs that config alone (``--dilation`` for configs 3
+and 4, ``--causal TF`` for config 2).
 
 A step is one pass through the public API (``natten_mps_amd.na{1,2,3}d``, then
 ``torch.autograd.grad`` for the configs with a backward) on synthetic seeded
@@ -34,7 +38,10 @@ engine kept on the calling thread in
   backward as their difference;
 * split_path (config 3): the split composition na2d_qk -> softmax -> na2d_av
   (forward + backward) timed eagerly, and its largest absolute difference
-  from the fused path's outputs and gradients.
+  from the fused path's outputs and gradients;
+* config.host_us_per_step (config 3): the library's own host time per eager
+  step -- the backend's forward and backward calls, timed on the CPU while
+  the GPU is held behind a spin (torch's autograd engine excluded).
 """
 from __future__ import annotations
 
@@ -337,58 +344,47 @@ def rpb_step(torch, steps, warmup):
                       "kernel_mean_us": kernels, "kernel_sum_us": round(sum(kernels.values()), 1)}), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
-    ap.add_argument("--dilation", type=int, default=None, help="dilation of configs 3 and 4 (default 1)")
-    ap.add_argument("--causal", default=None, help="config 2 causal flags, e.g. TF")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-graph", action="store_true", help="time eager steps only")
-    ap.add_argument("--no-split", action="store_true", help="skip the split-path comparison of config 3")
-    ap.add_argument("--copy-probe", type=float, default=None, metavar="MB",
-                    help="only run device-to-device copies of this many MB (calibrates rocprofv3 byte counters)")
-    ap.add_argument("--rpb", action="store_true",
-                    help="only time the extras.allin1 QK+RPB -> softmax -> AV step at DiNAT scale "
-                         "(B=16, 56x56, 4 heads, dim 32, K=7, bf16), forward + backward")
-    args = ap.parse_args()
+def host_time_per_step(torch, rank, leaves, do, cfg, steps, cycles_per_ms):
+    """Host (CPU) time of the library's own work per eager step: the 'hip'
+    backend's forward and backward hooks (argument checks, cached problem
+    and layouts, output allocation, the C call), timed on the host over
+    ``steps`` calls while the GPU is held behind a spin, so that no call
+    waits for the device.  torch's autograd engine is not included."""
+    from natten_mps_amd._core import hip
 
-    if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
-              "neighbourhood attention shards over batch x heads with no communication, "
-              "so the N-GPU figure is N x the 1-GPU value.", file=sys.stderr)
-        sys.exit(2)
+    q, k, v = (t.detach() for t in leaves)
+    ks, dil, causal = cfg["kernel"], cfg["dilation"], cfg["causal"]
+    stride = (1,) * rank
+    out, lse = hip.forward_with_lse(rank, q, k, v, ks, stride, dil, causal, None)
+    hip.fused_backward(rank, do, q, k, v, out, lse, ks, dil, stride, causal, None)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int((steps * 0.5 + 20.0) * cycles_per_ms))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        hip.forward_with_lse(rank, q, k, v, ks, stride, dil, causal, None)
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        hip.fused_backward(rank, do, q, k, v, out, lse, ks, dil, stride, causal, None)
+    t2 = time.perf_counter()
+    torch.cuda.synchronize()
+    return {"forward_us": round((t1 - t0) / steps * 1e6, 2), "backward_us": round((t2 - t1) / steps * 1e6, 2),
+            "step_us": round((t2 - t0) / steps * 1e6, 2)}
 
-    import torch
 
-    if args.copy_probe is not None:
-        # a plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch
-        # give the factors that turn those counters into HBM bytes
-        n = int(args.copy_probe * 1e6) // 2
-        src = torch.randn(n, device="cuda:0").to(torch.bfloat16)
-        dst = torch.empty_like(src)
-        for _ in range(args.steps):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes": 2 * n, "copies": args.steps}), flush=True)
-        return
-
-    if args.rpb:
-        rpb_step(torch, args.steps, args.warmup)
-        return
-
+def measure(torch, cid, steps, warmup, dilation=None, causal=None, graph=True, split=False, cpu=True,
+            cpu_budget=30.0, host=False):
+    """One config: eager and graph-replayed step times, per-kernel launch
+    times, roofline and MFMA figures, the CPU baseline; the JSON record."""
     import natten_mps_amd
     from natten_mps_amd import functional as F
     from natten_mps_amd._core import _lib
 
-    cfg = dict(CONFIGS[args.config])
+    cfg = dict(CONFIGS[cid])
     rank = len(cfg["spatial"])
-    if args.dilation is not None and args.config in (3, 4):
-        cfg["dilation"] = (args.dilation,) * rank
-    if args.causal is not None and args.config == 2:
-        cfg["causal"] = tuple(c.upper() == "T" for c in args.causal)
+    if dilation is not None and cid in (3, 4):
+        cfg["dilation"] = (dilation,) * rank
+    if causal is not None and cid == 2:
+        cfg["causal"] = tuple(c.upper() == "T" for c in causal)
     natten_mps_amd.set_backend("hip")
     dev = torch.device("cuda:0")
     dtype = getattr(torch, cfg["dtype"])
@@ -414,7 +410,7 @@ def main():
             return (out,)
         return torch.autograd.grad(out, leaves, do)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     _lib.profile_read(reset=True)
@@ -429,6 +425,8 @@ def main():
         torch.cuda.synchronize()
         return 2_000_000 / max(a.elapsed_time(b), 1e-3)
 
+    cycles_per_ms = spin_cycles_per_ms()
+
     def timed(run, profile=False, head_start_ms=0.0):
         """Mean GPU time per call of run() over K calls.  With head_start_ms
         the stream first spins that long, so that the host queues the K calls
@@ -440,12 +438,12 @@ def main():
         if head_start_ms > 0:
             torch.cuda._sleep(int(head_start_ms * cycles_per_ms))
         start.record()
-        for _ in range(args.steps):
+        for _ in range(steps):
             run()
         stop.record()
         torch.cuda.synchronize()
         _lib.profile_enable(False)
-        return start.elapsed_time(stop) / args.steps
+        return start.elapsed_time(stop) / steps
 
     # eager step time with the per-launch event timing off; the same K steps
     # are then repeated with every library launch bracketed by HIP events on
@@ -464,19 +462,18 @@ def main():
             ms_eager_one_thread = timed(step)
         finally:
             torch.autograd.set_multithreading_enabled(True)
-    cycles_per_ms = spin_cycles_per_ms()
-    ms_profiled = timed(step, profile=True, head_start_ms=2.0 * args.steps * ms_eager + 5.0)
+    ms_profiled = timed(step, profile=True, head_start_ms=2.0 * steps * ms_eager + 5.0)
     stats = _lib.profile_read(reset=True)
-    _log(f"eager step {ms_eager:.4f} ms (queued ahead, with per-launch events: {ms_profiled:.4f} ms)")
+    _log(f"[config {cid}] eager step {ms_eager:.4f} ms (queued ahead, with per-launch events: {ms_profiled:.4f} ms)")
     if ms_eager_one_thread is not None:
-        _log(f"eager step with autograd on the calling thread {ms_eager_one_thread:.4f} ms")
+        _log(f"[config {cid}] eager step with autograd on the calling thread {ms_eager_one_thread:.4f} ms")
 
     # the same step captured once in a HIP graph (forward + autograd backward)
     # and replayed: identical kernels and buffers without the per-step host
     # work.  Every replay is checked bit for bit against an eager step, with
     # eager work and synchronisation between the replays.
     ms_graph = None
-    if not args.no_graph:
+    if graph:
         try:
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
@@ -484,13 +481,13 @@ def main():
                 for _ in range(3):
                     step()
             torch.cuda.current_stream().wait_stream(side)
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
+            cg = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(cg):
                 g_out = step()
             ref = [t.clone() for t in step()]
             graph_ok = True
             for _ in range(3):
-                graph.replay()
+                cg.replay()
                 torch.cuda.synchronize()
                 graph_ok &= all(torch.equal(a, b) for a, b in zip(g_out, ref))
                 ref = [t.clone() for t in step()]
@@ -498,12 +495,12 @@ def main():
             if graph_ok:
                 # replays queued behind a spin, so that the host's graph
                 # launch cost (tens of µs) stays out of a short step's time
-                ms_graph = timed(graph.replay, head_start_ms=2.0 * args.steps * max(ms_eager, 0.05) + 5.0)
-                _log(f"graph step {ms_graph:.4f} ms")
+                ms_graph = timed(cg.replay, head_start_ms=2.0 * steps * max(ms_eager, 0.05) + 5.0)
+                _log(f"[config {cid}] graph step {ms_graph:.4f} ms")
             else:
-                _log("graph replay differs from the eager step; reporting the eager time")
+                _log(f"[config {cid}] graph replay differs from the eager step; reporting the eager time")
         except Exception as e:  # capture is an optimisation of the timing, never required
-            _log("graph capture failed:", repr(e))
+            _log(f"[config {cid}] graph capture failed:", repr(e))
     ms = ms_graph if ms_graph is not None else ms_eager
 
     pairs = B * Hq * _valid_pairs(cfg["spatial"], cfg["kernel"], cfg["dilation"], cfg["causal"], dev)
@@ -512,13 +509,14 @@ def main():
     esz = torch.tensor([], dtype=dtype).element_size()
     sbytes = step_bytes(B, N, Hq, Hkv, D, esz, cfg["backward"])
 
-    gpu_total = sum(s[1] for s in stats.values())
+    gpu_total = sum(st[1] for st in stats.values())
     for name, (n, tot, mn, mx) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
         _log(f"  {name:14s} launches={n:4d} mean={tot / n * 1e3:8.1f} us  min={mn * 1e3:8.1f}  max={mx * 1e3:8.1f}"
              f"  share={tot / gpu_total:5.1%}")
+    kernel_mean_us = {name: round(tot / n * 1e3, 2) for name, (n, tot, _, _) in stats.items()}
     dils = [str(d) for d in cfg["dilation"]]
     dil_tag = dils[0] if len(set(dils)) == 1 else "x".join(dils)
-    workload = f"config{args.config}_d{dil_tag}"
+    workload = f"config{cid}_d{dil_tag}"
     dom_name, (dn, dtot, _, _) = max(stats.items(), key=lambda kv: kv[1][1])
     nbytes = kernel_bytes(dom_name, B, N, Hq, Hkv, D, esz)
     mean_s = dtot / dn * 1e-3
@@ -530,7 +528,7 @@ def main():
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_name, workload),
                 "kernel": dom_name, "mean_us": round(mean_s * 1e6, 2), "alg_bytes": nbytes,
                 "copy_gbs": round(copy_gbs, 1), "frac_of_copy": round(gbs / copy_gbs, 4)}
-        _log(f"device copy moving the kernel's {nbytes / 1e6:.1f} MB: {copy_gbs:.0f} GB/s "
+        _log(f"[config {cid}] device copy moving the kernel's {nbytes / 1e6:.1f} MB: {copy_gbs:.0f} GB/s "
              f"({copy_gbs / HBM_PEAK_GBS:.1%} of 8 TB/s); {dom_name} reaches {gbs / copy_gbs:.1%} of it")
     # MFMA utilisation of the fused tile kernels, on useful work: the MFMA
     # products each kernel needs per valid (query, key) pair and head dim --
@@ -552,7 +550,7 @@ def main():
                               "mean_us": round(t * 1e6, 2)}
         mfma = {"peak_tflops": MFMA_PEAK_TFLOPS, "useful_tflops_step": round(tflops, 2),
                 "useful_frac_step": round(tflops / MFMA_PEAK_TFLOPS, 4), "kernels": kern}
-    _log(f"step {ms:.4f} ms  {tflops:.2f} TFLOP/s  {sbytes / (ms * 1e-3) / 1e9:.0f} GB/s  "
+    _log(f"[config {cid}] step {ms:.4f} ms  {tflops:.2f} TFLOP/s  {sbytes / (ms * 1e-3) / 1e9:.0f} GB/s  "
          f"HBM floor {sbytes / 8e12 * 1e6:.1f} us -> {sbytes / 8e12 / (ms * 1e-3):.1%} of roofline (step)")
 
     # config 3 asks for the fused path against the split composition
@@ -560,20 +558,29 @@ def main():
     # its step time (eager, queued ahead like the fused eager step) and the
     # largest difference between the two paths' outputs and gradients
     split_path = None
-    if args.config == 3 and not args.no_split:
+    if split and cid == 3:
         try:
-            split_path = compare_split(leaves, do, cfg, timed, args)
+            ns = argparse.Namespace(steps=steps, warmup=warmup, no_graph=not graph)
+            split_path = compare_split(leaves, do, cfg, timed, ns)
             _log(f"split path step {split_path['ms_per_step']:.4f} ms eager, {split_path['graph_ms_per_step']} ms "
                  f"graph, max |fused - split| {split_path['max_abs_diff']:.3g}")
         except Exception as e:  # a comparison, never required
             _log("split comparison failed:", repr(e))
 
-    cpu = None
-    if not args.no_cpu:
+    host_us = None
+    if host and cfg["backward"]:
         try:
-            cpu = cpu_baseline(cfg, pairs)
-            _log(f"cpu baseline: forward {cpu['fwd_ms']} ms, step {cpu['step_ms']} ms, {cpu['value']} TFLOP/s "
-                 f"({cpu['cores']} threads)")
+            host_us = host_time_per_step(torch, rank, leaves, do, cfg, steps, cycles_per_ms)
+            _log(f"[config {cid}] library host time per step: {host_us}")
+        except Exception as e:  # reported, never required
+            _log("host timing failed:", repr(e))
+
+    cpu_rec = None
+    if cpu:
+        try:
+            cpu_rec = cpu_baseline(cfg, pairs, budget_s=cpu_budget)
+            _log(f"[config {cid}] cpu baseline: forward {cpu_rec['fwd_ms']} ms, step {cpu_rec['step_ms']} ms, "
+                 f"{cpu_rec['value']} TFLOP/s ({cpu_rec['cores']} threads)")
         except Exception as e:  # the baseline is reported, never required
             _log("cpu baseline failed:", repr(e))
 
@@ -581,14 +588,14 @@ def main():
     causal_tag = "".join("T" if c else "F" for c in cfg["causal"])
     desc = (f"na{rank}d {'fwd+bwd' if cfg['backward'] else 'fwd'} B={B} {shape} heads={Hq}/{Hkv} dim={D} "
             f"K={cfg['kernel']} dilation={cfg['dilation']} causal={causal_tag} {DTYPE_TAG[cfg['dtype']]} "
-            f"(BASELINE config {args.config})")
-    print(json.dumps({
-        "metric": METRIC if args.config == 3 else f"na{rank}d step ms & effective TFLOP/s (config {args.config})",
+            f"(BASELINE config {cid})")
+    return {
+        "metric": METRIC if cid == 3 else f"na{rank}d step ms & effective TFLOP/s (config {cid})",
         "value": round(tflops, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -600,13 +607,93 @@ def main():
                    else "eager", "eager_ms_per_step": round(ms_eager, 4),
                    "eager_ms_per_step_autograd_one_thread": None if ms_eager_one_thread is None
                    else round(ms_eager_one_thread, 4),
+                   "host_us_per_step": host_us,
                    "step_hbm_bytes": sbytes, "step_gbs": round(sbytes / (ms * 1e-3) / 1e9, 1),
-                   "hbm_floor_frac_step": round(sbytes / 8e12 / (ms * 1e-3), 4)},
+                   "hbm_floor_frac_step": round(sbytes / 8e12 / (ms * 1e-3), 4),
+                   "kernel_mean_us": kernel_mean_us},
         "roofline": roof,
         "mfma": mfma,
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu_rec,
         "split_path": split_path,
-    }), flush=True)
+    }
+
+
+# The rows beside the headline (config 3, dilation 1) in the default run:
+# every BASELINE config and variant, each with its own CPU baseline.
+OTHER_ROWS = [(1, {}), (2, {"causal": "FF"}), (2, {"causal": "TF"}), (3, {"dilation": 8}), (4, {"dilation": 1}),
+              (4, {"dilation": 4}), (5, {})]
+
+
+def summary(rec):
+    """The per-config fields of an all_configs row."""
+    roof = rec["roofline"] or {}
+    return {"workload": rec["config"]["workload"], "ms_per_step": rec["ms_per_step"],
+            "timing": rec["config"]["timing"], "eager_ms_per_step": rec["config"]["eager_ms_per_step"],
+            "tflops": rec["value"], "hbm_floor_frac_step": rec["config"]["hbm_floor_frac_step"],
+            "kernel_mean_us": rec["config"]["kernel_mean_us"],
+            "dominant_kernel": roof.get("kernel"), "dominant_frac": roof.get("frac"),
+            "dominant_frac_of_copy": roof.get("frac_of_copy"),
+            "mfma_useful_frac_step": (rec["mfma"] or {}).get("useful_frac_step"),
+            "cpu_baseline": rec["cpu_baseline"]}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=None, choices=sorted(CONFIGS),
+                    help="only this config (default: the headline, config 3, plus a row per config)")
+    ap.add_argument("--dilation", type=int, default=None, help="dilation of configs 3 and 4 (default 1)")
+    ap.add_argument("--causal", default=None, help="config 2 causal flags, e.g. TF")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-graph", action="store_true", help="time eager steps only")
+    ap.add_argument("--no-split", action="store_true", help="skip the split-path comparison of config 3")
+    ap.add_argument("--no-all", action="store_true", help="the headline config only, no per-config rows")
+    ap.add_argument("--copy-probe", type=float, default=None, metavar="MB",
+                    help="only run device-to-device copies of this many MB (calibrates rocprofv3 byte counters)")
+    ap.add_argument("--rpb", action="store_true",
+                    help="only time the extras.allin1 QK+RPB -> softmax -> AV step at DiNAT scale "
+                         "(B=16, 56x56, 4 heads, dim 32, K=7, bf16), forward + backward")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); every GPU box of this "
+              "pool has one GPU, and no multi-GPU figure is measured.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if args.copy_probe is not None:
+        # a plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch
+        # give the factors that turn those counters into HBM bytes
+        n = int(args.copy_probe * 1e6) // 2
+        src = torch.randn(n, device="cuda:0").to(torch.bfloat16)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": 2 * n, "copies": args.steps}), flush=True)
+        return
+
+    if args.rpb:
+        rpb_step(torch, args.steps, args.warmup)
+        return
+
+    cid = 3 if args.config is None else args.config
+    rec = measure(torch, cid, args.steps, args.warmup, dilation=args.dilation, causal=args.causal,
+                  graph=not args.no_graph, split=not args.no_split, cpu=not args.no_cpu, host=cid == 3)
+    if args.config is None and not args.no_all:
+        rows = []
+        for other, kw in OTHER_ROWS:
+            try:
+                r = measure(torch, other, min(args.steps, 10), min(args.warmup, 3), graph=not args.no_graph,
+                            cpu=not args.no_cpu, cpu_budget=6.0, **kw)
+                rows.append(summary(r))
+            except Exception as e:  # a row that fails is reported as such, never fatal
+                rows.append({"config": other, **kw, "error": repr(e)})
+        rec["all_configs"] = rows
+    print(json.dumps(rec), flush=True)
 
 
 if __name__ == "__main__":

@@ -4,11 +4,17 @@
  *
  * Plain pointers, sizes and element strides; no torch types.  The caller owns
  * every buffer (inputs, outputs, workspaces) and the stream.  The only device
- * memory the library allocates itself is a small table of tile geometry per
- * problem shape (a few hundred bytes per tile), built on the first call with
- * that shape outside stream capture and kept until the process ends; during
- * capture, or when the tables would pass 64 MiB, the kernels compute the same
- * geometry themselves.  Every entry point returns 0 on success and a
+ * memory the library allocates itself is the tile geometry of each problem
+ * shape (a few hundred bytes per tile of the general tile kernels, 64 bytes
+ * per 8x8 tile of the 2-D ones), built on the first call with that shape
+ * outside stream capture, uploaded by an asynchronous copy on that call's
+ * stream (no host synchronisation) and kept until the process ends; a later
+ * call on another stream waits for that copy on its own stream.  During
+ * capture, in natten_hip_backward_noalloc, or when the general tables would
+ * pass 64 MiB, the general kernels compute the same geometry themselves and
+ * the 2-D ones leave the problem to them.  Workspaces (global keys, the
+ * relative-position-bias gradient) are the caller's, sized by the
+ * natten_hip_*_workspace queries.  Every entry point returns 0 on success and a
  * non-zero natten_status_t otherwise, with a message available from
  * natten_hip_last_error().  Launches are asynchronous on `stream` (a
  * hipStream_t; NULL = the default stream).
@@ -42,7 +48,9 @@
  *   natten_hip_rpb_qk_forward  extras/allin1/functional.py:47-100, 153-250 and
  *                              extras/allin1/metal.py (natten{1,2}dqkrpb)
  *   natten_hip_rpb_av_forward  extras/allin1/functional.py:103-150, 253-325 (natten{1,2}dav)
- *   natten_hip_rpb_qk_backward extras/allin1/functional.py:333-365, 413-448 (QK+RPB backward)
+ *   natten_hip_rpb_qk_backward extras/allin1/functional.py:333-365, 413-448 (QK+RPB backward;
+ *   natten_hip_rpb_qk_backward_ws  the same op with the caller's workspace for
+ *   natten_hip_rpb_dbias_workspace the bias gradient's partial sums)
  *   natten_hip_rpb_av_backward extras/allin1/functional.py:368-400, 451-485 (AV backward)
  */
 #ifndef NATTEN_HIP_H
@@ -294,9 +302,14 @@ int natten_hip_varlen_backward(const natten_problem_t *p, const int32_t *lens,
  * rpb and drpb are contiguous [H, 2K1-1, 2K2-1] (1-D: [H, 2K-1]) in the
  * problem's dtype; attn is [B, *sp, H, K1*K2].  Odd kernels in bf16/fp16 at
  * head dims 32/64/128 run on the split MFMA tile kernels: there rpb_qk
- * rounds q . k to the dtype before adding the bias (one more rounding), and
- * drpb's partial sums take stream-ordered device memory for the call
- * (none under graph capture, where a one-pass kernel runs instead). */
+ * rounds q . k to the dtype before adding the bias (one more rounding).
+ * drpb is reduced in one pass by natten_hip_rpb_qk_backward; where
+ * natten_hip_rpb_dbias_workspace(p) is positive, natten_hip_rpb_qk_backward_ws
+ * given an fp32 workspace of that many floats reduces it in two passes
+ * (partial sums per slice of the queries, then one fixed-order sum: the same
+ * value, several times faster on large images).  A workspace that is NULL or
+ * smaller takes the one-pass kernel.  0 from the query: the one pass serves
+ * the problem; -1: invalid problem. */
 int natten_hip_rpb_qk_forward(const natten_problem_t *p,
                               const void *q, const natten_layout_t *lq,
                               const void *k, const natten_layout_t *lk,
@@ -318,6 +331,17 @@ int natten_hip_rpb_qk_backward(const natten_problem_t *p,
                                void *dk, const natten_layout_t *ldk,
                                void *drpb,
                                void *stream);
+
+int64_t natten_hip_rpb_dbias_workspace(const natten_problem_t *p);
+int natten_hip_rpb_qk_backward_ws(const natten_problem_t *p,
+                                  const void *dattn, const natten_layout_t *lda,
+                                  const void *q, const natten_layout_t *lq,
+                                  const void *k, const natten_layout_t *lk,
+                                  void *dq, const natten_layout_t *ldq,
+                                  void *dk, const natten_layout_t *ldk,
+                                  void *drpb,
+                                  float *work, int64_t work_floats,
+                                  void *stream);
 
 int natten_hip_rpb_av_backward(const natten_problem_t *p,
                                const void *dout, const natten_layout_t *ldo,

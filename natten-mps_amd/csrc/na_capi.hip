@@ -144,10 +144,11 @@ int natten_hip_abi_version(void) { return NATTEN_HIP_ABI_VERSION; }
 const char* natten_hip_last_error(void) { return g_err; }
 
 int natten_hip_mfma_lds_check(int32_t* checked) {
-    int n = 0;
+    int n = 0, n_lean = 0;
     const int ok = na::mfma_lds_audit(&n);
-    if (checked) *checked = n;
-    return ok;
+    const int ok_lean = na::lean_lds_audit(&n_lean);
+    if (checked) *checked = n + n_lean;
+    return ok && ok_lean ? 1 : 0;
 }
 
 int natten_hip_forward(const natten_problem_t* p, const void* q, const natten_layout_t* lq, const void* k,
@@ -161,13 +162,15 @@ int natten_hip_forward(const natten_problem_t* p, const void* q, const natten_la
     const int vec =
         runs_aligned(dpl_for(D), {{q, lq, P.Dqk}, {k, lk, P.Dqk}, {v, lv, P.Dv}, {out, lo, P.Dv}}) ? 1 : 0;
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    // the lean 2-D tiles first (their checks are cheap), then the general tiles
+    if (use_mfma() && na::lean_eligible(P, p->dtype, vec != 0, {to_lay(lq), to_lay(lo)}, {to_lay(lk), to_lay(lv)},
+                                        {to_lay(llse)})) {
+        const hipError_t e = na::lean_forward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), lse,
+                                              to_lay(llse), p->dtype, s);
+        if (e != hipErrorNotSupported) return launch_status(e, "forward");
+    }
     if (use_mfma() && na::mfma_eligible(P, p->dtype, D, vec != 0, false) &&
         na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(llse)})) {
-        if (na::lean_eligible(P, p->dtype, vec != 0, {to_lay(lq), to_lay(lo)}, {to_lay(lk), to_lay(lv)})) {
-            const hipError_t e = na::lean_forward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo),
-                                                  lse, to_lay(llse), p->dtype, s);
-            if (e != hipErrorNotSupported) return launch_status(e, "forward");
-        }
         return launch_status(na::mfma_forward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), lse,
                                               to_lay(llse), p->dtype, s),
                              "forward");
@@ -194,18 +197,22 @@ int backward_impl(const natten_problem_t* p, const na::Prob& P, const void* q, c
                                               {dout, ldo, P.Dv}, {dq, ldq, P.Dqk}, {dk, ldk, P.Dqk}, {dv, ldv, P.Dv}})
                         ? 1
                         : 0;
+    // the lean 2-D tiles first (their checks are cheap), then the general tiles
+    if (use_mfma() &&
+        na::lean_eligible(P, p->dtype, vec != 0, {to_lay(lq), to_lay(lo), to_lay(ldo), to_lay(ldq)},
+                          {to_lay(lk), to_lay(lv), to_lay(ldk), to_lay(ldv)},
+                          dlse ? std::initializer_list<na::Lay>{to_lay(llse), to_lay(ldelta), to_lay(ldlse)}
+                               : std::initializer_list<na::Lay>{to_lay(llse), to_lay(ldelta)})) {
+        const hipError_t e = na::lean_backward(
+            P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout, to_lay(ldo), lse, to_lay(llse),
+            dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv, to_lay(ldv), delta, to_lay(ldelta), p->dtype,
+            static_cast<hipStream_t>(stream));
+        if (e != hipErrorNotSupported) return launch_status(e, "backward");
+    }
     if (use_mfma() && na::mfma_eligible(P, p->dtype, D, vec != 0, true) &&
         na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(ldo), to_lay(llse),
                                  to_lay(ldq), to_lay(ldk), to_lay(ldv), to_lay(ldelta)}) &&
         (!dlse || na::mfma_offsets_fit(P, {to_lay(ldlse)}))) {
-        if (na::lean_eligible(P, p->dtype, vec != 0, {to_lay(lq), to_lay(lo), to_lay(ldo), to_lay(ldq)},
-                              {to_lay(lk), to_lay(lv), to_lay(ldk), to_lay(ldv)})) {
-            const hipError_t e = na::lean_backward(
-                P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout, to_lay(ldo), lse, to_lay(llse),
-                dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv, to_lay(ldv), delta, to_lay(ldelta),
-                p->dtype, static_cast<hipStream_t>(stream));
-            if (e != hipErrorNotSupported) return launch_status(e, "backward");
-        }
         return launch_status(na::mfma_backward(P, q, to_lay(lq), k, to_lay(lk), v, to_lay(lv), out, to_lay(lo), dout,
                                                to_lay(ldo), lse,
                                                to_lay(llse), dlse, to_lay(ldlse), dq, to_lay(ldq), dk, to_lay(ldk), dv,
@@ -332,7 +339,7 @@ int natten_hip_global_supported(const natten_problem_t* p, int32_t n_global, int
     g.n = n_global;
     g.lk.s2 = g.lv.s2 = static_cast<long long>(p->heads_kv) * p->dim_qk;
     g.lk.h = g.lv.h = p->dim_qk;
-    return n_global >= 1 && global_eligible(P, p->dtype, 1, g, backward != 0) ? 1 : 0;
+    return n_global >= 1 && P.scale > 0.f && global_eligible(P, p->dtype, 1, g, backward != 0) ? 1 : 0;
 }
 
 int64_t natten_hip_global_workspace(const natten_problem_t* p, int32_t n_global) {
@@ -396,10 +403,12 @@ int natten_hip_backward_global(const natten_problem_t* p, const void* q, const n
                                               {dout, ldo, P.Dv}, {dq, ldq, P.Dqk}, {dk, ldk, P.Dqk}, {dv, ldv, P.Dv}})
                         ? 1
                         : 0;
+    // every check of both launches before the first: an unsupported problem
+    // is rejected with no output written
     if (!global_eligible(P, p->dtype, vec, g, true) ||
         !na::mfma_offsets_fit(P, {to_lay(lq), to_lay(lk), to_lay(lv), to_lay(lo), to_lay(ldo), to_lay(llse),
                                   to_lay(ldq), to_lay(ldk), to_lay(ldv), to_lay(ldelta)}) ||
-        (dlse && !na::mfma_offsets_fit(P, {to_lay(ldlse)})))
+        (dlse && !na::mfma_offsets_fit(P, {to_lay(ldlse)})) || !na::mfma_global_batch_fit(P, to_lay(lq), to_lay(ldo)))
         return fail(NATTEN_ERR_UNSUPPORTED,
                     "global keys run on the MFMA tile kernels only (bf16/fp16, head dim 32/64/96/128, stride 1, "
                     "aligned operands)");
@@ -637,14 +646,17 @@ int natten_hip_rpb_av_forward(const natten_problem_t* p, const void* attn, const
                          "rpb_av_forward");
 }
 
-int natten_hip_rpb_qk_backward(const natten_problem_t* p, const void* dattn, const natten_layout_t* lda,
-                               const void* q, const natten_layout_t* lq, const void* k, const natten_layout_t* lk,
-                               void* dq, const natten_layout_t* ldq, void* dk, const natten_layout_t* ldk, void* drpb,
-                               void* stream) {
+namespace {
+
+int rpb_qk_backward_impl(const natten_problem_t* p, const void* dattn, const natten_layout_t* lda, const void* q,
+                         const natten_layout_t* lq, const void* k, const natten_layout_t* lk, void* dq,
+                         const natten_layout_t* ldq, void* dk, const natten_layout_t* ldk, void* drpb, float* work,
+                         int64_t work_floats, void* stream) {
     na::Prob P;
     int rc = make_rpb_prob(p, P);
     if (rc) return rc;
     if (any_null({dattn, q, k, dq, dk, lda, lq, lk, ldq, ldk})) return fail(NATTEN_ERR_INVALID, "NULL operand");
+    if (work_floats < 0) return fail(NATTEN_ERR_INVALID, "rpb_qk_backward: negative workspace size");
     const hipStream_t s = static_cast<hipStream_t>(stream);
     int sides = na::kQuerySide | na::kKeySide;
     if (rpb_on_tiles(P)) {
@@ -666,8 +678,31 @@ int natten_hip_rpb_qk_backward(const natten_problem_t* p, const void* dattn, con
         }
     }
     return launch_status(na::rpb_qk_backward(P, dattn, to_lay(lda), q, to_lay(lq), k, to_lay(lk), dq, to_lay(ldq), dk,
-                                             to_lay(ldk), drpb, p->dtype, s, sides),
+                                             to_lay(ldk), drpb, p->dtype, s, sides, work,
+                                             static_cast<size_t>(work_floats)),
                          "rpb_qk_backward");
+}
+
+}  // namespace
+
+int natten_hip_rpb_qk_backward(const natten_problem_t* p, const void* dattn, const natten_layout_t* lda,
+                               const void* q, const natten_layout_t* lq, const void* k, const natten_layout_t* lk,
+                               void* dq, const natten_layout_t* ldq, void* dk, const natten_layout_t* ldk, void* drpb,
+                               void* stream) {
+    return rpb_qk_backward_impl(p, dattn, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, nullptr, 0, stream);
+}
+
+int64_t natten_hip_rpb_dbias_workspace(const natten_problem_t* p) {
+    na::Prob P;
+    if (make_rpb_prob(p, P)) return -1;
+    return static_cast<int64_t>(na::rpb_dbias_workspace(P));
+}
+
+int natten_hip_rpb_qk_backward_ws(const natten_problem_t* p, const void* dattn, const natten_layout_t* lda,
+                                  const void* q, const natten_layout_t* lq, const void* k, const natten_layout_t* lk,
+                                  void* dq, const natten_layout_t* ldq, void* dk, const natten_layout_t* ldk,
+                                  void* drpb, float* work, int64_t work_floats, void* stream) {
+    return rpb_qk_backward_impl(p, dattn, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, work, work_floats, stream);
 }
 
 int natten_hip_rpb_av_backward(const natten_problem_t* p, const void* dout, const natten_layout_t* ldo,

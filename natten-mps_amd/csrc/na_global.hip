@@ -252,6 +252,10 @@ bool mfma_global_key_ok(const Prob& p, int dtype, const GlobalSet& g) {
     return grid < (1LL << 31) && static_cast<long long>(p.rep) * p.nout < (1LL << 31);
 }
 
+bool mfma_global_batch_fit(const Prob& p, const Lay& lq, const Lay& ldo) {
+    return batch_offsets_fit(p, lq, 2) && batch_offsets_fit(p, ldo, 2);
+}
+
 size_t global_workspace_floats(const Prob& p, int n) {
     const GlobalSplit sp = global_split(p, n);
     return static_cast<size_t>(sp.splits) * p.B * p.Hkv * sp.blocks * 16 * 2 * std::max(p.Dqk, p.Dv);

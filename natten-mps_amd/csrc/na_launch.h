@@ -39,10 +39,13 @@ hipError_t rpb_qk(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, c
                   int dtype, hipStream_t s);
 hipError_t rpb_av(const Prob& p, const void* attn, Lay la, const void* v, Lay lv, void* out, Lay lo, int dtype,
                   hipStream_t s);
-// `sides` as for the generic backward (drpb is reduced whenever non-null).
+// `sides` as for the generic backward (drpb is reduced whenever non-null,
+// in two passes through `work` when it holds rpb_dbias_workspace floats,
+// else in one pass).
 hipError_t rpb_qk_backward(const Prob& p, const void* da, Lay lda, const void* q, Lay lq, const void* k, Lay lk,
                            void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, int dtype, hipStream_t s,
-                           int sides = kQuerySide | kKeySide);
+                           int sides = kQuerySide | kKeySide, float* work = nullptr, size_t work_floats = 0);
+size_t rpb_dbias_workspace(const Prob& p);
 hipError_t rpb_av_backward(const Prob& p, const void* dout, Lay ldo, const void* attn, Lay la, const void* v, Lay lv,
                            void* da, Lay lda, void* dv, Lay ldv, int dtype, hipStream_t s,
                            int sides = kQuerySide | kKeySide);
@@ -75,6 +78,21 @@ private:
     bool prev_;
 };
 bool device_alloc_allowed();
+
+// A device table (tile geometry) filled by an asynchronous copy on the stream
+// that first needed it.  table_upload enqueues the copy of `bytes` from `h`
+// (which the caller keeps alive as long as the table) and records an event;
+// table_ready says whether a launch on `s` may read the table now, after
+// making `s` wait for the copy when it was enqueued on another stream and is
+// not known to be complete (false under stream capture in that case: the
+// caller then does without the table).  Callers hold their cache's lock.
+struct TableUpload {
+    hipStream_t stream = nullptr;
+    hipEvent_t ev = nullptr;
+    bool done = false;
+};
+hipError_t table_upload(TableUpload& u, void* d, const void* h, size_t bytes, hipStream_t s);
+bool table_ready(TableUpload& u, hipStream_t s);
 
 // Global keys of a fused call (the reference's additional_keys): rows of
 // keys and values [B, n, Hkv, D] with their batch / head strides and the
@@ -121,7 +139,9 @@ hipError_t mfma_backward(const Prob& p, const void* q, Lay lq, const void* k, La
 // no launch for the problem (no tile table can be built: stream capture or a
 // no-allocation scope), and the caller then takes the general tile kernels.
 bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list<Lay> qside,
-                   std::initializer_list<Lay> kvside);
+                   std::initializer_list<Lay> kvside, std::initializer_list<Lay> rows);
+// Static-LDS audit of the lean instances (as mfma_lds_audit).
+int lean_lds_audit(int* checked);
 hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
                         Lay lo, float* lse, Lay ll, int dtype, hipStream_t s);
 hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
@@ -135,6 +155,8 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
 // queries go to `work` (global_workspace_floats of them), then one pass adds
 // them in a fixed order.  mfma_global_key_ok: the problem fits the kernel.
 bool mfma_global_key_ok(const Prob& p, int dtype, const GlobalSet& g);
+// The key side's q / dO operands: every offset within one batch in 31 bits.
+bool mfma_global_batch_fit(const Prob& p, const Lay& lq, const Lay& ldo);
 size_t global_workspace_floats(const Prob& p, int n);
 hipError_t mfma_global_key_backward(const Prob& p, const void* q, Lay lq, const void* dout, Lay ldo, const float* lse,
                                     Lay ll, const float* delta, Lay lde, const GlobalSet& g, void* dk, Lay ldk,

@@ -665,6 +665,7 @@ struct LeanGeo {
     int* ptr;
     int ntiles, nst_max, rows_max;
     std::vector<int> host;  // source of the asynchronous upload, kept with the table
+    TableUpload up;
 };
 
 struct LeanAxisTile {
@@ -731,7 +732,7 @@ const LeanGeo* lean_geometry(const Prob& p, bool key, int nch, hipStream_t s) {
     }
     std::lock_guard<std::mutex> g(mu);
     for (LeanGeo* e : cache)
-        if (std::memcmp(e, &k, offsetof(LeanGeo, ptr)) == 0) return e;
+        if (std::memcmp(e, &k, offsetof(LeanGeo, ptr)) == 0) return table_ready(e->up, s) ? e : nullptr;
     if (!device_alloc_allowed()) return nullptr;
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
@@ -799,7 +800,7 @@ const LeanGeo* lean_geometry(const Prob& p, bool key, int nch, hipStream_t s) {
     LeanGeo* e = new LeanGeo(k);
     e->host = std::move(h);
     // stream-ordered upload; the host copy lives as long as the table
-    if (hipMemcpyAsync(d, e->host.data(), bytes, hipMemcpyHostToDevice, s) != hipSuccess) {
+    if (table_upload(e->up, d, e->host.data(), bytes, s) != hipSuccess) {
         (void)hipGetLastError();
         (void)hipFree(d);
         delete e;
@@ -832,6 +833,40 @@ bool lean_switch() {
     return on;
 }
 
+// The lean kernels address LDS from the constant offset of lds_base(), as
+// the general tile kernels do: every instance is checked once per process
+// for static LDS (which would overlap it); one with static LDS turns the
+// lean path off with a message.
+template <typename T, int D, int NCH>
+void lean_audit_one(LdsAudit& a) {
+    audit_one(k_lean_fwd<T, D, NCH>, "k_lean_fwd", a);
+    audit_one(k_lean_bwd_q<T, D, NCH>, "k_lean_bwd_q", a);
+    audit_one(k_lean_bwd_kv<T, D, NCH + 2>, "k_lean_bwd_kv", a);
+}
+
+template <typename T, int D>
+void lean_audit_dim(LdsAudit& a) {
+    lean_audit_one<T, D, 1>(a);
+    lean_audit_one<T, D, 2>(a);
+    lean_audit_one<T, D, 3>(a);
+    lean_audit_one<T, D, 4>(a);
+    lean_audit_one<T, D, 5>(a);
+}
+
+const LdsAudit& lean_audit() {
+    static const LdsAudit result = [] {
+        LdsAudit a;
+        lean_audit_dim<bf16, 32>(a);
+        lean_audit_dim<bf16, 64>(a);
+        lean_audit_dim<f16, 32>(a);
+        lean_audit_dim<f16, 64>(a);
+        return a;
+    }();
+    return result;
+}
+
+bool lean_static_lds_ok() { return lean_audit().bad == 0; }
+
 // Chunks per wave for kernel K1 (query side): K1 + 1 rows.
 int lean_nch(int K1) { return (K1 + 2) / 2; }
 
@@ -841,22 +876,37 @@ int lean_nch(int K1) { return (K1 + 2) / 2; }
 // 32 or 64 for q, k and v, 16-bit, K2 <= 9, K1 <= 9, per-axis extents below
 // 2^15, planes below 2^30 bytes, q/out and k/v sharing one layout each.
 bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list<Lay> qside,
-                   std::initializer_list<Lay> kvside) {
-    if (!lean_switch() || dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f)) return false;
+                   std::initializer_list<Lay> kvside, std::initializer_list<Lay> rows) {
+    if (!lean_switch() || dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f) || !lean_static_lds_ok())
+        return false;
     if (p.Dqk != p.Dv || (p.Dqk != 32 && p.Dqk != 64)) return false;
-    if (p.ax[0].len != 1 || p.ax[0].k != 1) return false;
+    // 2-D: axis 0 padded; a short first axis (1-D problems) stays on the
+    // general tiles, which lay a 1-D axis out along whole tiles
+    if (p.ax[0].len != 1 || p.ax[0].k != 1 || p.ax[1].len < 8) return false;
     for (int a = 1; a < 3; ++a) {
         const Axis& A = p.ax[a];
         if (A.st != 1 || A.k > 9 || A.len >= (1 << 15)) return false;
     }
-    if (!all_same(qside) || !all_same(kvside)) return false;
+    if (!all_same(qside) || !all_same(kvside) || !all_same(rows)) return false;
     for (const Lay& l : {*qside.begin(), *kvside.begin()}) {
         if (l.s1 < 0 || l.s2 < 0 || l.b < 0 || l.h < 0) return false;
         const long long v = ((static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
                              (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + p.Dqk) * 2;
         if (v >= (1LL << 30)) return false;
     }
+    // fp32 rows (lse, delta, dlse): in-plane element offsets in 31 bits
+    const Lay& r = *rows.begin();
+    if (r.s1 < 0 || r.s2 < 0 || r.b < 0 || r.h < 0) return false;
+    if ((static_cast<long long>(p.ax[1].len) - 1) * r.s1 + (static_cast<long long>(p.ax[2].len) - 1) * r.s2 >=
+        (1LL << 31))
+        return false;
     return true;
+}
+
+int lean_lds_audit(int* checked) {
+    const LdsAudit& a = lean_audit();
+    if (checked) *checked = a.checked;
+    return a.bad == 0 ? 1 : 0;
 }
 
 template <typename T, int D, int NCH>

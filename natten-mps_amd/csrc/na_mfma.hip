@@ -1385,9 +1385,45 @@ struct GeoEntry {
     int dev, key;
     int len[3], k[3], dil[3], st[3], causal[3], T[3], waves, rowshift;
     int* ptr;
+    std::vector<int>* host;  // source of the asynchronous upload, kept with the table
+    TableUpload* up;
 };
 
 thread_local bool t_no_device_alloc = false;
+
+}  // namespace
+
+hipError_t table_upload(TableUpload& u, void* d, const void* h, size_t bytes, hipStream_t s) {
+    hipError_t e = hipEventCreateWithFlags(&u.ev, hipEventDisableTiming);
+    if (e != hipSuccess) return e;
+    e = hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipEventRecord(u.ev, s);
+    if (e != hipSuccess) {
+        (void)hipEventDestroy(u.ev);
+        u.ev = nullptr;
+        return e;
+    }
+    u.stream = s;
+    return hipSuccess;
+}
+
+bool table_ready(TableUpload& u, hipStream_t s) {
+    if (u.done || s == u.stream) return true;
+    const hipError_t q = hipEventQuery(u.ev);
+    if (q == hipSuccess) {
+        u.done = true;
+        return true;
+    }
+    if (q != hipErrorNotReady) {
+        (void)hipGetLastError();
+        return false;
+    }
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return false;
+    return hipStreamWaitEvent(s, u.ev, 0) == hipSuccess;
+}
+
+namespace {
 
 const int* geometry_table(const Prob& p, const TileShape& ts, bool key_tile, hipStream_t stream) {
     const char* env = std::getenv("NATTEN_HIP_GEOMETRY");
@@ -1412,14 +1448,15 @@ const int* geometry_table(const Prob& p, const TileShape& ts, bool key_tile, hip
     key.rowshift = ts.rowshift;
     std::lock_guard<std::mutex> g(mu);
     for (const GeoEntry& e : cache)
-        if (std::memcmp(&e, &key, offsetof(GeoEntry, ptr)) == 0) return e.ptr;
+        if (std::memcmp(&e, &key, offsetof(GeoEntry, ptr)) == 0) return table_ready(*e.up, stream) ? e.ptr : nullptr;
     if (!device_alloc_allowed()) return nullptr;
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
     const long long S = ts.spatial.d;
     const size_t bytes = static_cast<size_t>(S) * kRecDwords * sizeof(int);
     if (total + bytes > kGeoMaxBytes) return nullptr;
-    std::vector<int> h(static_cast<size_t>(S) * kRecDwords, 0);
+    auto* hv = new std::vector<int>(static_cast<size_t>(S) * kRecDwords, 0);
+    std::vector<int>& h = *hv;
     for (int s = 0; s < S; ++s) {
         int* rec = h.data() + static_cast<size_t>(s) * kRecDwords;
         int t[3], r[3];
@@ -1462,14 +1499,20 @@ const int* geometry_table(const Prob& p, const TileShape& ts, bool key_tile, hip
     int* d = nullptr;
     if (hipMalloc(reinterpret_cast<void**>(&d), bytes) != hipSuccess) {
         (void)hipGetLastError();
+        delete hv;
         return nullptr;
     }
-    if (hipMemcpy(d, h.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) {
+    auto* up = new TableUpload;
+    if (table_upload(*up, d, h.data(), bytes, stream) != hipSuccess) {
         (void)hipGetLastError();
         (void)hipFree(d);
+        delete up;
+        delete hv;
         return nullptr;
     }
     key.ptr = d;
+    key.host = hv;
+    key.up = up;
     cache.push_back(key);
     total += bytes;
     return d;

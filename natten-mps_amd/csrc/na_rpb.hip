@@ -292,7 +292,13 @@ __global__ __launch_bounds__(256) void k_rpb_dbias_part(RProb p, const T* __rest
         for (int i = 0; i < kDbLoads; ++i) {
             if (jb + i >= n) break;
             const int s0 = st[2 * (jb + i)], s1 = st[2 * (jb + i) + 1];
-            if (s0 != c0 || s1 != c1) {
+            if (s0 != c0 || s1 != c1) {  // s0, s1 are the same in every lane
+                // a lane's flush may update an entry that another lane of
+                // this wave flushed earlier: order the wave's LDS accesses
+                // explicitly instead of relying on the compiler keeping them
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 if (c0 >= 0 && mine) wbins[(c0 + e0) * p.rs[1] + c1 + e1] += acc;
                 c0 = s0;
                 c1 = s1;
@@ -301,6 +307,9 @@ __global__ __launch_bounds__(256) void k_rpb_dbias_part(RProb p, const T* __rest
             acc += x[i];
         }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (c0 >= 0 && mine) wbins[(c0 + e0) * p.rs[1] + c1 + e1] += acc;
     lds_publish_barrier();
     for (int i = threadIdx.x; i < nb; i += blockDim.x) {
@@ -361,35 +370,33 @@ hipError_t rpb_av_t(const RProb& p, const void* attn, Lay la, const void* v, Lay
     return hipGetLastError();
 }
 
+// Floats of the two-pass bias gradient's partial sums (0: the one-pass
+// kernel serves the problem).
+size_t dbias_work_floats(const RProb& p) {
+    if (!dbias_two_pass(p)) return 0;
+    return static_cast<size_t>(p.H) * dbias_groups(p) * p.rs[0] * p.rs[1];
+}
+
+// The bias gradient: two passes through the caller's workspace when it holds
+// dbias_work_floats floats, else the one-pass kernel (no workspace).
 template <typename T>
-hipError_t rpb_dbias_t(const RProb& p, const void* da, Lay lda, void* drpb, hipStream_t s) {
+hipError_t rpb_dbias_t(const RProb& p, const void* da, Lay lda, void* drpb, float* work, size_t work_floats,
+                       hipStream_t s) {
     const int nb = p.rs[0] * p.rs[1];
-    if (dbias_two_pass(p) && device_alloc_allowed()) {
-        // the partial sums live in stream-ordered memory of this call (no
-        // state shared between calls or streams); under graph capture, or if
-        // the allocation fails, the one-pass kernel runs instead
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const size_t need = dbias_work_floats(p);
+    if (need > 0 && work && work_floats >= need) {
         const int G = dbias_groups(p);
-        float* part = nullptr;
-        if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone &&
-            hipMallocAsync(reinterpret_cast<void**>(&part), static_cast<size_t>(p.H) * G * nb * sizeof(float), s) ==
-                hipSuccess) {
-            const int nw = (p.kv + 63) / 64;  // one thread per neighbour
-            const size_t shm = kDbChunk * (sizeof(long long) + 2 * sizeof(int)) +
-                               static_cast<size_t>(nw) * nb * sizeof(float);
-            const int npos = static_cast<int>(rpb_rows(p) / p.H);
-            NA_LAUNCH("na_rpb_dbias_part", k_rpb_dbias_part<T>, dim3(static_cast<unsigned>(p.H * G)), dim3(64 * nw),
-                      shm, s, p, (const T*)da, lda, part, G, npos);
-            hipError_t e = hipGetLastError();
-            if (e == hipSuccess) {
-                NA_LAUNCH("na_rpb_dbias_sum", k_rpb_dbias_sum<T>, dim3(static_cast<unsigned>((p.H * nb + 3) / 4)),
-                          dim3(256), 0, s, p, (const float*)part, G, (T*)drpb);
-                e = hipGetLastError();
-            }
-            const hipError_t f = hipFreeAsync(part, s);
-            return e != hipSuccess ? e : f;
-        }
-        (void)hipGetLastError();
+        const int nw = (p.kv + 63) / 64;  // one thread per neighbour
+        const size_t shm =
+            kDbChunk * (sizeof(long long) + 2 * sizeof(int)) + static_cast<size_t>(nw) * nb * sizeof(float);
+        const int npos = static_cast<int>(rpb_rows(p) / p.H);
+        NA_LAUNCH("na_rpb_dbias_part", k_rpb_dbias_part<T>, dim3(static_cast<unsigned>(p.H * G)), dim3(64 * nw), shm,
+                  s, p, (const T*)da, lda, work, G, npos);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        NA_LAUNCH("na_rpb_dbias_sum", k_rpb_dbias_sum<T>, dim3(static_cast<unsigned>((p.H * nb + 3) / 4)), dim3(256),
+                  0, s, p, (const float*)work, G, (T*)drpb);
+        return hipGetLastError();
     }
     NA_LAUNCH("na_rpb_dbias", k_rpb_dbias<T>, dim3(static_cast<unsigned>(p.H * nb)), dim3(256), 0, s, p,
               (const T*)da, lda, (T*)drpb);
@@ -398,7 +405,8 @@ hipError_t rpb_dbias_t(const RProb& p, const void* da, Lay lda, void* drpb, hipS
 
 template <typename T>
 hipError_t rpb_qk_bwd_t(const RProb& p, const void* da, Lay lda, const void* q, Lay lq, const void* k, Lay lk,
-                        void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, hipStream_t s, int sides) {
+                        void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, float* work, size_t work_floats,
+                        hipStream_t s, int sides) {
     hipError_t e = hipSuccess;
     if (sides & kQuerySide) {
         NA_LAUNCH("na_rpb_dq", k_rpb_dq<T>, dim3(rgrid(p, p.Dqk)), dim3(256), 0, s, p, (const T*)da, lda, (const T*)k,
@@ -410,7 +418,7 @@ hipError_t rpb_qk_bwd_t(const RProb& p, const void* da, Lay lda, const void* q, 
                   (const T*)q, lq, p.Dqk, (T*)dk, ldk);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    return drpb ? rpb_dbias_t<T>(p, da, lda, drpb, s) : hipSuccess;
+    return drpb ? rpb_dbias_t<T>(p, da, lda, drpb, work, work_floats, s) : hipSuccess;
 }
 
 
@@ -463,12 +471,17 @@ hipError_t rpb_av(const Prob& P, const void* attn, Lay la, const void* v, Lay lv
 }
 
 hipError_t rpb_qk_backward(const Prob& P, const void* da, Lay lda, const void* q, Lay lq, const void* k, Lay lk,
-                           void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, int dtype, hipStream_t s, int sides) {
+                           void* dq, Lay ldq, void* dk, Lay ldk, void* drpb, int dtype, hipStream_t s, int sides,
+                           float* work, size_t work_floats) {
     const RProb p = to_rprob(P);
-    if (dtype == NATTEN_F32) return rpb_qk_bwd_t<float>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, s, sides);
-    if (dtype == NATTEN_F16) return rpb_qk_bwd_t<f16>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, s, sides);
-    return rpb_qk_bwd_t<bf16>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, s, sides);
+    if (dtype == NATTEN_F32)
+        return rpb_qk_bwd_t<float>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, work, work_floats, s, sides);
+    if (dtype == NATTEN_F16)
+        return rpb_qk_bwd_t<f16>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, work, work_floats, s, sides);
+    return rpb_qk_bwd_t<bf16>(p, da, lda, q, lq, k, lk, dq, ldq, dk, ldk, drpb, work, work_floats, s, sides);
 }
+
+size_t rpb_dbias_workspace(const Prob& P) { return dbias_work_floats(to_rprob(P)); }
 
 hipError_t rpb_av_backward(const Prob& P, const void* dout, Lay ldo, const void* attn, Lay la, const void* v, Lay lv,
                            void* da, Lay lda, void* dv, Lay ldv, int dtype, hipStream_t s, int sides) {

@@ -42,6 +42,8 @@ ENTRY_POINTS = (
     "natten_hip_rpb_qk_forward",
     "natten_hip_rpb_av_forward",
     "natten_hip_rpb_qk_backward",
+    "natten_hip_rpb_dbias_workspace",
+    "natten_hip_rpb_qk_backward_ws",
     "natten_hip_rpb_av_backward",
     "natten_hip_profile_enable",
     "natten_hip_profile_read",
@@ -103,6 +105,9 @@ _SIGNATURES = {
     "natten_hip_rpb_qk_forward": ([_P(Problem)] + [_VP, _LP] * 2 + [_VP] + [_VP, _LP] + [_VP], ctypes.c_int),
     "natten_hip_rpb_av_forward": ([_P(Problem)] + [_VP, _LP] * 3 + [_VP], ctypes.c_int),
     "natten_hip_rpb_qk_backward": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP, _VP], ctypes.c_int),
+    "natten_hip_rpb_dbias_workspace": ([_P(Problem)], ctypes.c_int64),
+    "natten_hip_rpb_qk_backward_ws": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP, _VP, ctypes.c_int64, _VP],
+                                      ctypes.c_int),
     "natten_hip_rpb_av_backward": ([_P(Problem)] + [_VP, _LP] * 5 + [_VP], ctypes.c_int),
     "natten_hip_profile_enable": ([ctypes.c_int], ctypes.c_int),
     "natten_hip_profile_read": ([_P(KernelStat), ctypes.c_int, ctypes.c_int], ctypes.c_int),

@@ -530,9 +530,14 @@ def rpb_qk_backward(rank: int, d_attn, q, k, with_rpb: bool, kernel_size, dilati
     drpb = (torch.empty((H, *[2 * x - 1 for x in kernel_size]), dtype=q.dtype, device=q.device)
             if with_rpb else None)
     L = lambda t: _byref(_lib.layout(t, rank, 1))  # noqa: E731
-    rc = _launch(q.device, _lib.load().natten_hip_rpb_qk_backward, _byref(prob), _lib.ptr(d_attn), L(d_attn),
+    lib = _lib.load()
+    # The bias gradient's partial sums go to a workspace owned here (the
+    # library allocates nothing for them); none when the one pass serves.
+    work_floats = int(lib.natten_hip_rpb_dbias_workspace(_byref(prob))) if with_rpb else 0
+    work = torch.empty(max(work_floats, 0), dtype=torch.float32, device=q.device) if work_floats > 0 else None
+    rc = _launch(q.device, lib.natten_hip_rpb_qk_backward_ws, _byref(prob), _lib.ptr(d_attn), L(d_attn),
                  _lib.ptr(q), L(q), _lib.ptr(k), L(k), _lib.ptr(dq), L(dq), _lib.ptr(dk), L(dk), _lib.ptr(drpb),
-                 _raw_stream(q.device))
+                 _lib.ptr(work), max(work_floats, 0), _raw_stream(q.device))
     _lib.check(rc, "rpb_qk_backward")
     return dq, dk, drpb
 
@@ -562,11 +567,27 @@ def rpb_av_backward(rank: int, d_out, attn, v, kernel_size, dilation):
 _GLOBAL_OK: dict = {}
 
 
-def global_supported(rank: int, q, k, v, n: int, kernel_size, stride, dilation, is_causal, backward: bool) -> bool:
+def _aligned_runs(*ts) -> bool:
+    """Every tensor 16-byte aligned with its outer strides multiples of 8
+    elements and a unit innermost stride (what the tile kernels read)."""
+    for t in ts:
+        if t.data_ptr() % 16 or t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]):
+            return False
+    return True
+
+
+def global_supported(rank: int, q, k, v, n: int, kernel_size, stride, dilation, is_causal, backward: bool,
+                     gk=None, gv=None, scale=None) -> bool:
     """True when the fused kernels take these global keys (the MFMA tile path:
-    bf16/fp16, head dim 32/64/96/128 for q, k and v, stride 1, GPU tensors)."""
+    bf16/fp16, head dim 32/64/96/128 for q, k and v, stride 1, GPU tensors,
+    aligned operands, a positive scale).  The problem part is asked of the
+    library (natten_hip_global_supported, cached per shape); the operands'
+    own alignment and the scale are checked here on every call."""
     if (q.device.type != "cuda" or q.dtype not in (torch.float16, torch.bfloat16)
             or not (q.dtype == k.dtype == v.dtype) or q.shape[-1] != v.shape[-1] or n < 1):
+        return False
+    scale_value = float(q.shape[-1] ** -0.5 if scale is None else scale)
+    if not scale_value > 0.0 or not _aligned_runs(*(t for t in (q, k, v, gk, gv) if t is not None)):
         return False
     key = (rank, q.dtype, q.shape, k.shape[-2], n, tuple(kernel_size), tuple(stride), tuple(dilation),
            tuple(is_causal), bool(backward))
@@ -681,8 +702,9 @@ def _bind(rank: int) -> None:
     def vbwd(d_out, q, k, v, out, lse, sizes, kernel_size, dilation, scale):
         return varlen_backward(rank, d_out, q, k, v, out, lse, sizes, kernel_size, dilation, scale)
 
-    def gsup(q, k, v, n, kernel_size, stride, dilation, is_causal, backward):
-        return global_supported(rank, q, k, v, n, kernel_size, stride, dilation, is_causal, backward)
+    def gsup(q, k, v, n, kernel_size, stride, dilation, is_causal, backward, gk=None, gv=None, scale=None):
+        return global_supported(rank, q, k, v, n, kernel_size, stride, dilation, is_causal, backward, gk, gv,
+                                scale)
 
     def gfwd(q, k, v, gk, gv, kernel_size, stride, dilation, is_causal, scale):
         return forward_with_lse_global(rank, q, k, v, gk, gv, kernel_size, stride, dilation, is_causal, scale)

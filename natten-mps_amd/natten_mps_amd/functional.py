@@ -218,10 +218,15 @@ def _na(rank, query, key, value, kernel_size, stride, dilation, is_causal, scale
             t.requires_grad for t in (query, key, value, additional_keys, additional_values))
         if (gk.dtype == query.dtype and gv.dtype == query.dtype
                 and getattr(mod, f"na{rank}d_global_supported")(query, k_in, v_in, gk.shape[1], ks, st, dil, causal,
-                                                               grads)):
+                                                               grads, gk, gv, scale_value)):
             fn = getattr(ag, f"NeighborhoodAttention{rank}DGlobalFunction")
-            out, lse = fn.apply(query, k_in, v_in, gk, gv, ks, st, dil, causal, scale_value)
-            return (out, lse) if return_lse else out
+            try:
+                out, lse = fn.apply(query, k_in, v_in, gk, gv, ks, st, dil, causal, scale_value)
+                return (out, lse) if return_lse else out
+            except NotImplementedError:
+                # the backend declined these operands after all (a limit its
+                # probe does not see): the composition below computes the same
+                pass
 
     if has_additional or return_lse:
         if getattr(mod, "FUSED_LSE", False) and not pure:

@@ -19,11 +19,19 @@ used by every GPU test that compares values.
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 FP32_TOL = 1e-5
 HALF_NORM_REL = 2e-2
 HALF_GUARD = 5e-2
+
+# (test, tensor, dtype, norm-wise relative error, largest elementwise
+# |a - b| / (1 + |b|)) of every half-precision comparison of the session;
+# conftest prints the largest at the end, so a drift towards the guard stays
+# visible.
+RECORD: list = []
 
 
 def assert_parity(got: torch.Tensor, ref: torch.Tensor, dtype: torch.dtype, name: str = "") -> None:
@@ -42,6 +50,11 @@ def assert_parity(got: torch.Tensor, ref: torch.Tensor, dtype: torch.dtype, name
         return
     err = float((a.double() - b.double()).norm())
     scale = float(b.double().norm())
+    elem = float(((a.double() - b.double()).abs() / (1.0 + b.double().abs())).max())
+    test = os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0]
+    RECORD.append((test, name, str(dtype).replace("torch.", ""), err / max(scale, 1e-30), elem))
     assert err <= HALF_NORM_REL * scale + 1e-12, (
-        f"{name}: relative error {err / max(scale, 1e-30):.3g} exceeds {HALF_NORM_REL} (norm-wise)")
-    torch.testing.assert_close(a, b, atol=HALF_GUARD, rtol=HALF_GUARD, msg=lambda m: f"{name} (guard): {m}")
+        f"{name}: relative error {err / max(scale, 1e-30):.3g} exceeds {HALF_NORM_REL} (norm-wise); "
+        f"largest elementwise |a-b|/(1+|b|) {elem:.3g}")
+    torch.testing.assert_close(a, b, atol=HALF_GUARD, rtol=HALF_GUARD,
+                               msg=lambda m: f"{name} (guard; norm-wise {err / max(scale, 1e-30):.3g}): {m}")

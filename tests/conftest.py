@@ -39,6 +39,26 @@ def pytest_collection_modifyitems(config, items):
             item.add_marker(skip)
 
 
+def pytest_terminal_summary(terminalreporter):
+    """The largest half-precision errors of the session against the oracle
+    (tests/_parity.py records every comparison), elementwise and norm-wise,
+    so that a drift between the 2e-2 norm-wise bound and the 5e-2 guard shows
+    in the output of every run."""
+    try:
+        from _parity import RECORD
+    except ImportError:
+        return
+    if not RECORD:
+        return
+    tr = terminalreporter
+    tr.section("half-precision parity: largest errors against the oracle")
+    tr.write_line(f"{len(RECORD)} comparisons; bounds: norm-wise 2e-2, elementwise guard 5e-2 (+5e-2 |ref|)")
+    for label, key in (("elementwise |a-b|/(1+|b|)", 4), ("norm-wise relative", 3)):
+        tr.write_line(f"largest {label}:")
+        for rec in sorted(RECORD, key=lambda r: -r[key])[:8]:
+            tr.write_line(f"  {rec[key]:.4g}  {rec[1]:5s} {rec[2]:8s} {rec[0]}")
+
+
 @pytest.fixture
 def pure_backend():
     import natten_mps_amd

@@ -285,3 +285,54 @@ def test_rpb_tile_path_on_qkv_views():
     ref_out.backward(go.float())
     assert_parity(out, ref_out, torch.bfloat16, "out")
     assert_parity(qkv_d.grad, ref_qkv.grad, torch.bfloat16, "dqkv")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rpb_bias_gradient_workspace_entry_points(dtype):
+    """natten_hip_rpb_qk_backward (no workspace: the one-pass bias gradient)
+    and natten_hip_rpb_qk_backward_ws (the caller's workspace of
+    natten_hip_rpb_dbias_workspace floats: two passes) give the same dq and
+    dk bits and bias gradients within the bound of the dtype, both against
+    the oracle in float64; a workspace one float short takes the one pass."""
+    import ctypes
+
+    from natten_mps_amd._core import _lib, hip
+
+    q, k = (_rand((2, 24, 20, 2, 32), s, dtype).to(DEV) for s in (41, 42))
+    da = _rand((2, 24, 20, 2, 25), 43, dtype).to(DEV)
+    prob = hip._rpb_problem(2, q, 2, 32, 32, (5, 5), (2, 2))
+    lib = _lib.load()
+    need = int(lib.natten_hip_rpb_dbias_workspace(ctypes.byref(prob)))
+    assert need > 0, need
+    L = lambda t: ctypes.byref(_lib.layout(t, 2, 1))  # noqa: E731
+
+    def run(work, nfloat):
+        dq, dk = torch.empty_like(q), torch.empty_like(k)
+        drpb = torch.empty((2, 9, 9), dtype=dtype, device=DEV)
+        _lib.profile_enable(True)
+        try:
+            rc = lib.natten_hip_rpb_qk_backward_ws(
+                ctypes.byref(prob), _lib.ptr(da), L(da), _lib.ptr(q), L(q), _lib.ptr(k), L(k), _lib.ptr(dq), L(dq),
+                _lib.ptr(dk), L(dk), _lib.ptr(drpb), _lib.ptr(work), nfloat, _lib.stream_of(q))
+            _lib.check(rc, "rpb_qk_backward_ws")
+            torch.cuda.synchronize()
+        finally:
+            _lib.profile_enable(False)
+        return dq, dk, drpb, _lib.profile_read(reset=True)
+
+    work = torch.empty(need, dtype=torch.float32, device=DEV)
+    two = run(work, need)
+    short = run(work, need - 1)
+    none = run(None, 0)
+    assert "na_rpb_dbias_part" in two[3] and "na_rpb_dbias" not in two[3], sorted(two[3])
+    for r in (short, none):
+        assert "na_rpb_dbias" in r[3] and "na_rpb_dbias_part" not in r[3], sorted(r[3])
+        assert torch.equal(r[0], two[0]) and torch.equal(r[1], two[1])
+        assert torch.equal(r[2], none[2])
+    rg = torch.zeros(2, 9, 9, dtype=torch.float64, requires_grad=True)
+    A.na2d_qk_rpb(q.cpu().double(), k.cpu().double(), rg, 5, 2).backward(da.cpu().double())
+    for r in (two, none):
+        if dtype == torch.float32:
+            torch.testing.assert_close(r[2].cpu().double(), rg.grad, atol=1e-4, rtol=1e-4)
+        else:
+            assert_parity(r[2], rg.grad, dtype, "drpb")

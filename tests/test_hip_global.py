@@ -128,3 +128,50 @@ def test_global_keys_fall_back_to_the_composition_where_unsupported(pure_backend
     got = _run(2, (q, k, v, gk, gv), do, dl, DEV, kernel_size=3)
     for name, a, b in zip(("out", "lse", "dq", "dk", "dv", "dgk", "dgv"), got, ref):
         assert_parity(a, b, torch.float32, name)
+
+
+def _misaligned(t):
+    """The same values at a storage offset of one element: 2-byte aligned,
+    so the tile kernels' 16-byte loads cannot read it."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    view = buf[1:].view(t.shape)
+    view.copy_(t)
+    return view
+
+
+@pytest.mark.parametrize("what", ["misaligned_q", "negative_scale"])
+def test_global_keys_fall_back_where_operands_decline(what, pure_backend):
+    """A problem the library's global-key probe accepts by shape but whose
+    operands the tile kernels refuse -- a query view that is not 16-byte
+    aligned, or a scale <= 0 -- takes the composition (split NA, dense
+    attention, merge) instead of raising, and matches the oracle composition."""
+    import natten_mps_amd
+    from natten_mps_amd import functional as F
+    from natten_mps_amd._core import _lib
+
+    q, k, v, gk, gv, do = _inputs(21, [(2, 10, 12, 2, 32), (2, 10, 12, 2, 32), (2, 10, 12, 2, 32), (2, 3, 2, 32),
+                                       (2, 3, 2, 32), (2, 10, 12, 2, 32)], torch.bfloat16)
+    (dl,) = _inputs(22, [(2, 10, 12, 2)], torch.float32)
+    kw = dict(kernel_size=5)
+    if what == "negative_scale":
+        kw["scale"] = -0.25
+    ref = _run(2, (q, k, v, gk, gv), do, dl, "cpu", ref_dtype=torch.float32, **kw)
+    natten_mps_amd.set_backend("hip")
+    leaves = [t.to(DEV) for t in (q, k, v, gk, gv)]
+    if what == "misaligned_q":
+        leaves[0] = _misaligned(leaves[0])
+        assert leaves[0].data_ptr() % 16 != 0
+    leaves = [t.detach().requires_grad_(True) for t in leaves]
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        out, lse = F.na2d(*leaves[:3], return_lse=True, additional_keys=leaves[3], additional_values=leaves[4], **kw)
+        torch.autograd.backward([out, lse], [do.to(DEV), dl.to(DEV)])
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    launched = set(_lib.profile_read(reset=True))
+    assert not any("global" in n for n in launched), launched
+    got = [out.detach().cpu(), lse.detach().cpu()] + [t.grad.cpu() for t in leaves]
+    for name, a, b in zip(("out", "lse", "dq", "dk", "dv", "dgk", "dgv"), got, ref):
+        assert_parity(a, b, torch.bfloat16, name)
