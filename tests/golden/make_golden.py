@@ -17,6 +17,14 @@ records inputs and outputs for small seeded cases:
 
 Outputs: ``golden.npz`` (arrays; bf16 kept as raw uint16 bits, int64 maps as int32) and
 ``golden.json`` (the case list: op, rank, parameters, dtype, array keys).
+
+With ``--allin1`` it writes ``allin1.npz`` / ``allin1.json`` instead: the
+reference's ``extras/allin1`` ops through its public functions
+(``na{1,2}d_qk_rpb``, ``na{1,2}d_av_fused``; on the CPU these take the pure
+torch path of ``extras/allin1/functional.py:47-325`` and its autograd
+fallback), fp32, odd and even kernels, dilation 1 and > 1, 1-D and 2-D,
+with a random bias and with none: logits, dq, dk, drpb for the QK+RPB op,
+out, dattn, dv for the AV op.
 """
 from __future__ import annotations
 
@@ -245,5 +253,74 @@ def main(ref_src: str) -> None:
     print(f"wrote {len(cases)} cases, {len(arrays)} arrays")
 
 
+# rank, spatial, heads, dim, kernel, dilation, with a bias, scale
+ALLIN1_CASES = [
+    (1, (24,), 2, 8, 5, 1, True, 0.5),
+    (1, (24,), 2, 8, 4, 2, True, None),
+    (1, (23,), 3, 8, 7, 3, True, 0.3),
+    (1, (16,), 2, 8, 2, 1, True, None),
+    (1, (18,), 2, 8, 6, 3, False, 0.4),
+    (2, (10, 12), 2, 8, 3, 2, True, 0.5),
+    (2, (9, 11), 2, 8, 4, 1, True, None),
+    (2, (12, 10), 2, 8, 4, 2, True, 0.3),
+    (2, (11, 13), 2, 8, 5, 2, False, None),
+    (2, (7, 8), 2, 8, 6, 1, True, 0.25),
+]
+
+
+def main_allin1(ref_src: str) -> None:
+    sys.path.insert(0, ref_src)
+    import natten_mps
+    from natten_mps.extras import allin1 as RA
+
+    arrays: dict[str, np.ndarray] = {}
+    cases: list[dict] = []
+    for ci, (rank, sp, heads, dim, K, dil, with_rpb, scale) in enumerate(ALLIN1_CASES):
+        g = _gen(7000 + ci)
+        q = _randn(g, (2, *sp, heads, dim), torch.float32)
+        k = _randn(g, (2, *sp, heads, dim), torch.float32)
+        v = _randn(g, (2, *sp, heads, dim), torch.float32)
+        rpb = _randn(g, (heads, *([2 * K - 1] * rank)), torch.float32) if with_rpb else None
+        kv = K ** rank
+        dlog = _randn(g, (2, *sp, heads, kv), torch.float32)
+        dout = _randn(g, (2, *sp, heads, dim), torch.float32)
+        ql, kl = q.clone().requires_grad_(True), k.clone().requires_grad_(True)
+        rl = rpb.clone().requires_grad_(True) if with_rpb else None
+        qk = RA.na1d_qk_rpb if rank == 1 else RA.na2d_qk_rpb
+        av = RA.na1d_av_fused if rank == 1 else RA.na2d_av_fused
+        logits = qk(ql, kl, rl, K, dil, scale=scale)
+        wrt = [ql, kl] + ([rl] if with_rpb else [])
+        g_qk = torch.autograd.grad(logits, wrt, dlog)
+        # the AV op on softmax-normalised weights of the same logits (masked
+        # entries are -inf, so their weights are 0)
+        attn = torch.softmax(logits.detach(), -1)
+        al, vl = attn.clone().requires_grad_(True), v.clone().requires_grad_(True)
+        out = av(al, vl, K, dil)
+        g_av = torch.autograd.grad(out, [al, vl], dout)
+        p = f"allin1_{ci}/"
+        named = [("q", q), ("k", k), ("v", v), ("dlogits", dlog), ("dout", dout), ("logits", logits),
+                 ("dq", g_qk[0]), ("dk", g_qk[1]), ("attn", attn), ("out", out), ("dattn", g_av[0]),
+                 ("dv", g_av[1])]
+        if with_rpb:
+            named += [("rpb", rpb), ("drpb", g_qk[2])]
+        cases.append(dict(kind="allin1", key=p, rank=rank, spatial=list(sp), heads=heads, dim=dim,
+                          kernel_size=K, dilation=dil, with_rpb=with_rpb, scale=scale, dtype="float32",
+                          arrays=[p + n for n, _ in named]))
+        for n, t in named:
+            arrays[p + n] = t.detach().to(torch.float32).numpy()
+
+    np.savez_compressed(os.path.join(HERE, "allin1.npz"), **arrays)
+    with open(os.path.join(HERE, "allin1.json"), "w") as f:
+        json.dump(dict(torch_version=torch.__version__, reference="natten_mps " + natten_mps.__version__,
+                       source="natten_mps.extras.allin1 na{1,2}d_qk_rpb / na{1,2}d_av_fused on the CPU",
+                       cases=cases), f, indent=1)
+    print(f"wrote {len(cases)} allin1 cases, {len(arrays)} arrays")
+
+
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference/src")
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    src = args[0] if args else "/root/reference/src"
+    if "--allin1" in sys.argv:
+        main_allin1(src)
+    else:
+        main(src)

@@ -111,3 +111,47 @@ def test_shapes_scale_and_none_rpb():
     torch.testing.assert_close(a, b, atol=0, rtol=0)
     q2 = _rand((2, 6, 7, 3, 4), 22)
     assert A.na2d_qk_rpb(q2, q2, None, 3).shape == (2, 6, 7, 3, 9)
+
+
+def _allin1_golden():
+    import json
+    import os
+
+    import numpy as np
+
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    with open(os.path.join(here, "allin1.json")) as f:
+        meta = json.load(f)
+    arrays = np.load(os.path.join(here, "allin1.npz"))
+    return meta["cases"], arrays
+
+
+_ALLIN1_CASES, _ALLIN1_ARRAYS = _allin1_golden()
+
+
+@pytest.mark.parametrize("case", _ALLIN1_CASES, ids=lambda c: c["key"].rstrip("/"))
+def test_oracle_matches_reference_allin1_fixtures(case):
+    """The reference's own extras/allin1 ops (pure torch path on the CPU,
+    tests/golden/make_golden.py --allin1): odd and even kernels, dilation
+    1 and > 1, 1-D and 2-D, with and without a bias.  The oracle in fp32 on
+    the same inputs gives the logits, dq, dk, drpb, out, dattn and dv within
+    1e-5 (fp32 summation order aside, the same arithmetic)."""
+    a = {n.split("/")[-1]: torch.from_numpy(_ALLIN1_ARRAYS[n]) for n in case["arrays"]}
+    rank, K, d, scale = case["rank"], case["kernel_size"], case["dilation"], case["scale"]
+    qk = A.na1d_qk_rpb if rank == 1 else A.na2d_qk_rpb
+    av = A.av_1d if rank == 1 else A.av_2d
+    q, k = a["q"].clone().requires_grad_(True), a["k"].clone().requires_grad_(True)
+    r = a["rpb"].clone().requires_grad_(True) if case["with_rpb"] else None
+    logits = qk(q, k, r, K, d, scale)
+    torch.testing.assert_close(logits, a["logits"], atol=1e-5, rtol=1e-5)
+    grads = torch.autograd.grad(logits, [q, k] + ([r] if r is not None else []), a["dlogits"])
+    torch.testing.assert_close(grads[0], a["dq"], atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(grads[1], a["dk"], atol=1e-5, rtol=1e-5)
+    if r is not None:
+        torch.testing.assert_close(grads[2], a["drpb"], atol=1e-4, rtol=1e-5)
+    at, v = a["attn"].clone().requires_grad_(True), a["v"].clone().requires_grad_(True)
+    out = av(at, v, K, d)
+    torch.testing.assert_close(out, a["out"], atol=1e-5, rtol=1e-5)
+    da, dv = torch.autograd.grad(out, [at, v], a["dout"])
+    torch.testing.assert_close(da, a["dattn"], atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(dv, a["dv"], atol=1e-5, rtol=1e-5)

@@ -131,11 +131,14 @@ def test_config5_na3d_bf16():
     q, k, v, do = _seeded(5, [(2, 16, 32, 32, 8, 64)] * 4, torch.bfloat16)
     ks, dil = (3, 7, 7), (1, 2, 2)
     out, grads = _run(F.na3d, q, k, v, do, kernel_size=ks, dilation=dil)
-    sl = (slice(0, 1), Ellipsis, slice(0, 1), slice(None))
-    ref, rgrads = _oracle(3, q[sl], k[sl], v[sl], do[sl], ks, (1, 1, 1), dil, (False, False, False))
-    _close(out[sl], ref, 2e-2, "out")
-    for n_, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
-        _close(a[sl], b, 2e-2, n_)
+    # (batch 0, head 0) and (batch 1, head 5): the oracle on one head of one
+    # sample at a time
+    for b, h in ((0, 0), (1, 5)):
+        sl = (slice(b, b + 1), Ellipsis, slice(h, h + 1), slice(None))
+        ref, rgrads = _oracle(3, q[sl], k[sl], v[sl], do[sl], ks, (1, 1, 1), dil, (False, False, False))
+        _close(out[sl], ref, 2e-2, f"out[b{b},h{h}]")
+        for n_, a, r in zip(("dq", "dk", "dv"), grads, rgrads):
+            _close(a[sl], r, 2e-2, f"{n_}[b{b},h{h}]")
 
 
 @pytest.mark.parametrize("cfg", [4, 5])

@@ -224,11 +224,11 @@ def test_split_av_nonfinite_stays_local():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("rank", [1, 2])
+@pytest.mark.parametrize("rank", [1, 2, 3])
 def test_dim_v_differs_forward_and_gradients(rank, dtype):
     from natten_mps_amd import functional as F
 
-    sp, ks, dil = ((40,), 7, 2) if rank == 1 else ((12, 14), (5, 3), (1, 2))
+    sp, ks, dil = {1: ((40,), 7, 2), 2: ((12, 14), (5, 3), (1, 2)), 3: ((6, 7, 9), (3, 3, 5), (1, 2, 1))}[rank]
     q, k, v, do = _inputs(341, [(2, *sp, 2, 64), (2, *sp, 2, 64), (2, *sp, 2, 256), (2, *sp, 2, 256)], dtype)
     leaves = [x.to(DEV).requires_grad_(True) for x in (q, k, v)]
     out = getattr(F, f"na{rank}d")(*leaves, kernel_size=ks, dilation=dil)
