@@ -367,8 +367,11 @@ def host_time_per_step(torch, rank, leaves, do, cfg, steps, cycles_per_ms):
         hip.fused_backward(rank, do, q, k, v, out, lse, ks, dil, stride, causal, None)
     t2 = time.perf_counter()
     torch.cuda.synchronize()
+    from natten_mps_amd._core import _lib
+
     return {"forward_us": round((t1 - t0) / steps * 1e6, 2), "backward_us": round((t2 - t1) / steps * 1e6, 2),
-            "step_us": round((t2 - t0) / steps * 1e6, 2)}
+            "step_us": round((t2 - t0) / steps * 1e6, 2),
+            "binding": "c++ (_natten_torch.so)" if _lib.binding() is not None else "ctypes"}
 
 
 def measure(torch, cid, steps, warmup, dilation=None, causal=None, graph=True, split=False, cpu=True,

@@ -6,6 +6,10 @@
 Objects go to natten-mps_amd/_build/, the library to
 natten-mps_amd/natten_mps_amd/libnatten_hip.so (git-ignored; it travels to
 the GPU box with the working tree).
+
+It also builds natten-mps_amd/natten_mps_amd/_natten_torch.so, the C++ host
+binding of the fused forward / backward (csrc/na_torch.cpp, g++ against the
+installed torch headers), linked to libnatten_hip.so beside it.
 """
 from __future__ import annotations
 
@@ -19,6 +23,9 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "natten_mps_amd", "libnatten_hip.so")
+BIND_NAME = "_natten_torch"
+BIND = os.path.join(HERE, "natten_mps_amd", BIND_NAME + ".so")
+CXX = os.environ.get("CXX", "g++")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["na_generic.hip", "na_mfma.hip", "na_lean.hip", "na_global.hip", "na_rpb.hip", "na_profile.hip", "na_capi.hip"]
@@ -54,13 +61,35 @@ def commands():
         obj = os.path.join(OBJ, src.replace(".hip", ".o"))
         objs.append(obj)
         cmds.append([HIPCC, *FLAGS, "-c", path, "-o", obj])
-    link = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", LIB]
+    link = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-soname,libnatten_hip.so", *objs, "-o", LIB]
     return cmds, link
+
+
+def binding_commands():
+    """Compile and link commands of the torch host binding (g++, no HIP)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension as E
+
+    src = os.path.join(CSRC, "na_torch.cpp")
+    obj = os.path.join(OBJ, "na_torch.o")
+    abi = int(getattr(torch._C, "_GLIBCXX_USE_CXX11_ABI", True))
+    inc = [f"-I{os.path.join(ROOT, 'include')}"] + [f"-isystem{p}" for p in E.include_paths()]
+    inc.append(f"-isystem{sysconfig.get_paths()['include']}")
+    comp = [CXX, "-O2", "-std=c++17", "-fPIC", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+            f"-DTORCH_EXTENSION_NAME={BIND_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H", *inc, "-c", src, "-o", obj]
+    tlib = E.library_paths()[0]
+    link = [CXX, "-shared", obj, "-o", BIND, f"-L{os.path.dirname(LIB)}", "-lnatten_hip", "-Wl,-rpath,$ORIGIN",
+            f"-L{tlib}", "-lc10", "-ltorch_cpu", "-ltorch", "-ltorch_python"]
+    return comp, link
 
 
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     cmds, link = commands()
+    bcomp, blink = binding_commands()
+    cmds = cmds + [bcomp]
     with cf.ThreadPoolExecutor(max_workers=min(len(cmds), 8)) as ex:
         for cmd, _ in zip(cmds, ex.map(_run, cmds)):
             if verbose:
@@ -71,13 +100,18 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(" ".join(link[:-1] + [LIB]))
+    btmp = BIND + ".tmp"
+    _run([btmp if x == BIND else x for x in blink])
+    os.replace(btmp, BIND)
+    if verbose:
+        print(" ".join(blink))
     return LIB
 
 
 if __name__ == "__main__":
     if "--check" in sys.argv:
         c, l = commands()
-        for x in c + [l]:
+        for x in c + [l, *binding_commands()]:
             print(" ".join(x))
     else:
         print(build(verbose=True))

@@ -17,6 +17,9 @@ LIB_NAME = "libnatten_hip.so"
 LIB_PATH = os.environ.get("NATTEN_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.dirname(os.path.abspath(__file__))), LIB_NAME)
 ABI_VERSION = 1
+# C++ host binding of the fused forward / backward (csrc/na_torch.cpp), built
+# beside the library; NATTEN_HIP_BINDING=0 keeps those calls on ctypes.
+BIND_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "_natten_torch.so")
 
 F32, F16, BF16 = 0, 1, 2
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
@@ -119,6 +122,31 @@ _lock = threading.Lock()
 
 def is_built() -> bool:
     return os.path.exists(LIB_PATH)
+
+
+_bind = None
+_bind_checked = False
+
+
+def binding():
+    """The C++ host binding module, or None when it is not built or switched
+    off.  It links to libnatten_hip.so by its soname, so the library loaded
+    here first is the one it calls."""
+    global _bind, _bind_checked
+    if _bind_checked:
+        return _bind
+    load()
+    mod = None
+    if os.environ.get("NATTEN_HIP_BINDING", "1") != "0" and os.path.exists(BIND_PATH):
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("_natten_torch", BIND_PATH)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        if mod.abi_version != ABI_VERSION:
+            raise RuntimeError("natten_mps_amd: _natten_torch.so ABI version mismatch; rebuild it.")
+    _bind, _bind_checked = mod, True
+    return _bind
 
 
 def load() -> ctypes.CDLL:

@@ -136,7 +136,17 @@ _CACHE_MAX = 512
 
 
 class _Sig:
-    __slots__ = ("prob", "prob_ref", "refs", "out_shape", "lse_shape", "strided", "device")
+    __slots__ = ("prob", "prob_ref", "refs", "out_shape", "lse_shape", "strided", "device", "fast")
+
+
+def _fast_call(sig, lays, out_shape, lse_shape, strided):
+    """The signature's call object in the C++ host binding (None without it):
+    the problem and layouts as raw bytes of their C structs."""
+    b = _lib.binding()
+    if b is None:
+        return None
+    blob = b"".join(bytes(x) if x is not None else bytes(_lib.Layout()) for x in lays)
+    return b.FusedCall(bytes(sig.prob), blob, list(out_shape), list(lse_shape), bool(strided))
 
 
 _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
@@ -173,6 +183,7 @@ def _fwd_sig(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_valu
     lse = torch.empty(sig.lse_shape, dtype=torch.float32, device="meta")
     lays = [_lib.layout(t, rank, 1) for t in (q, k, v, out)] + [_lib.layout(lse, rank, 0)]
     sig.refs = [lays, [ctypes.byref(x) for x in lays]]
+    sig.fast = _fast_call(sig, lays, sig.out_shape, sig.lse_shape, False)
     return sig
 
 
@@ -188,6 +199,8 @@ def forward_with_lse(rank: int, q, k, v, kernel_size, stride, dilation, is_causa
         if len(_FWD_CACHE) >= _CACHE_MAX:
             _FWD_CACHE.clear()
         _FWD_CACHE[key] = sig
+    if sig.fast is not None:
+        return sig.fast.forward(q, k, v, _raw_stream(q.device))
     out = torch.empty(sig.out_shape, dtype=q.dtype, device=q.device)
     lse = torch.empty(sig.lse_shape, dtype=torch.float32, device=q.device)
     r = sig.refs[1]
@@ -217,6 +230,7 @@ def _bwd_sig(rank, d_out, q, k, v, out, lse, d_lse, kernel_size, stride, dilatio
     lays += [_lib.layout(meta(t), rank, 1) for t in (q, k, v)]
     lays += [_lib.layout(torch.empty(sig.lse_shape, device="meta"), rank, 0)]
     sig.refs = [lays, [ctypes.byref(x) if x is not None else None for x in lays]]
+    sig.fast = _fast_call(sig, lays, (), sig.lse_shape, sig.strided)
     return sig
 
 
@@ -240,6 +254,8 @@ def fused_backward(rank: int, d_out, q, k, v, out, lse, kernel_size, dilation, s
         if len(_BWD_CACHE) >= _CACHE_MAX:
             _BWD_CACHE.clear()
         _BWD_CACHE[key] = sig
+    if sig.fast is not None:
+        return sig.fast.backward(q, k, v, out, d_out, lse, d_lse, _raw_stream(q.device))
     dq = (torch.zeros if sig.strided else torch.empty)(q.shape, dtype=q.dtype, device=q.device)
     dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
     dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)

@@ -115,3 +115,25 @@ def test_ctypes_arity_matches_header():
         assert m, name
         params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
         assert len(params) == len(args), (name, len(params), len(args))
+
+
+def test_torch_binding_loads_against_the_same_library(lib):
+    """The C++ host binding (_natten_torch.so) is built beside the library,
+    needs it by soname and resolves to the copy already loaded: one
+    libnatten_hip.so mapping in the process.  Its call object rejects
+    malformed descriptors before any device work."""
+    import torch
+
+    b = _lib.binding()
+    assert b is not None, "the host binding _natten_torch.so is not built"
+    assert b.abi_version == _lib.ABI_VERSION
+    maps = {line.split()[-1] for line in open("/proc/self/maps") if line.rstrip().endswith("libnatten_hip.so")}
+    assert len(maps) == 1, maps
+    needed = subprocess.run(["readelf", "-d", _lib.BIND_PATH], capture_output=True, text=True, check=True).stdout
+    assert "[libnatten_hip.so]" in needed
+    with pytest.raises(ValueError, match="problem size"):
+        b.FusedCall(b"\0" * 4, bytes(_lib.Layout()) * 5, [1], [1], False)
+    call = b.FusedCall(bytes(_prob()), bytes(_lib.Layout()) * 5, [1], [1], False)
+    with pytest.raises(ValueError, match="not a backward signature"):
+        z = torch.zeros(1)
+        call.backward(z, z, z, z, z, z, None, 0)

@@ -296,3 +296,53 @@ def test_split_key_side_multi_slice_is_bitwise_deterministic():
     for _ in range(4):
         for name, a, b in zip(("dq", "dk", "dv"), step(), ref):
             assert torch.equal(a, b), f"{name}: {int((a != b).sum())} elements differ between runs"
+
+
+# ---------------------------------------------------------------------------
+# the C++ host binding of the fused calls against the ctypes path
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("case", ["lean2d", "strided3d_lse"])
+def test_host_binding_matches_ctypes_path(case, monkeypatch):
+    """The fused forward / backward through the C++ host binding
+    (_natten_torch.so) and through ctypes give the same bits: same kernels,
+    same buffers' layouts; the binding allocates dq zeroed where stride > 1
+    leaves non-query positions, as the ctypes path does.  An unsupported
+    problem raises NotImplementedError through the binding."""
+    from natten_mps_amd._core import _lib, hip
+
+    assert _lib.binding() is not None, "the host binding _natten_torch.so is not built"
+    if case == "lean2d":
+        rank, shape, ks, st, dil, causal, dtype = 2, (2, 16, 24, 2, 32), (7, 7), (1, 1), (1, 1), (False, False), \
+            torch.bfloat16
+        dl = None
+    else:
+        rank, shape, ks, st, dil, causal, dtype = 3, (1, 6, 8, 9, 2, 16), (3, 3, 3), (1, 2, 1), (1, 1, 2), \
+            (True, False, False), torch.float32
+        dl = True
+    q, k, v = (x.to(DEV) for x in _inputs(901, [shape] * 3, dtype))
+
+    def run():
+        hip._FWD_CACHE.clear()
+        hip._BWD_CACHE.clear()
+        out, lse = hip.forward_with_lse(rank, q, k, v, ks, st, dil, causal, None)
+        g = torch.Generator().manual_seed(3)
+        dout = torch.randn(out.shape, generator=g).to(dtype).to(DEV)
+        dlse = torch.randn(lse.shape, generator=g).to(DEV) if dl else None
+        grads = hip.fused_backward(rank, dout, q, k, v, out, lse, ks, dil, st, causal, None, dlse)
+        torch.cuda.synchronize()
+        return [out, lse, *grads]
+
+    fast = run()
+    assert all(s.fast is not None for s in hip._FWD_CACHE.values())
+    monkeypatch.setattr(_lib, "_bind", None)
+    slow = run()
+    assert all(s.fast is None for s in hip._FWD_CACHE.values())
+    for name, a, b in zip(("out", "lse", "dq", "dk", "dv"), fast, slow):
+        assert torch.equal(a, b), name
+    monkeypatch.undo()
+    hip._FWD_CACHE.clear()
+    x = torch.zeros((1, 6, 1, 32), device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        hip.forward_with_lse(1, x, x, x, (6,), (1,), (1,), (False,), None)
