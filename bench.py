@@ -183,7 +183,7 @@ def compare_split(leaves, do, cfg, timed, args):
     kv = ks[0] * ks[1]
     split_bytes = q.numel() * q.element_size() * (2 + kv / q.shape[-1])
     kernel_frac = {name: round(split_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)
-                   for name, us in kernels.items() if name.endswith("_mfma") and us > 0}
+                   for name, us in kernels.items() if name.endswith(("_mfma", "_lean")) and us > 0}
     # the same split step replayed from a HIP graph (checked equal to eager
     # steps, as for the fused step): GPU time without the host's per-op work
     ms_graph = None

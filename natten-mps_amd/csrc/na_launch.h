@@ -142,6 +142,13 @@ bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list
                    std::initializer_list<Lay> kvside, std::initializer_list<Lay> rows);
 // Static-LDS audit of the lean instances (as mfma_lds_audit).
 int lean_lds_audit(int* checked);
+// Split ops' key side (out[k] = mul * sum over attending q of w[q][e] x[q])
+// on the 8x8 key tiles; hipErrorNotSupported when there is no launch (the
+// caller then takes the general split kernel).
+bool lean_wsum_key_eligible(const Prob& p, int dtype, int D, bool aligned, const Lay& lw, const Lay& lx,
+                            const Lay& lo);
+hipError_t lean_wsum_key(const char* name, const Prob& p, int D, const void* w, Lay lw, const void* x, Lay lx,
+                         void* o, Lay lo, float mul, int dtype, hipStream_t s);
 hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
                         Lay lo, float* lse, Lay ll, int dtype, hipStream_t s);
 hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,

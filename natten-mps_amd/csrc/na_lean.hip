@@ -650,6 +650,204 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> 
     lean_bwd_kv_tile<T, D, MAXC>(a, xcd_block(blockIdx.x, gridDim.x));
 }
 
+// ---------------------------------------------------------------------------
+// Split ops, key side: out[k] = mul * sum over the queries q attending key k
+// of w[q][e(q, k)] x[q] (the dk of QK's backward with w = dattn, x = q; the
+// dv of AV's backward with w = attn, x = dO).  Key tiles as in k_lean_bwd_kv:
+// the union of the attending queries is staged, x rows by the 16-byte DMA
+// and each union query's row of w (KV entries) by 4-byte DMA into a slot
+// row of P words (the words that hold the row's entries), rows after rows.  In class coordinates
+// e(q, k) = (J1(k) - ws1(q)) K2 + (J2(k) - ws2(q)); the host tables d1[u] =
+// J1(first key) - ws1(union row u) and d2[u] (per union column) make it
+// (d1[u1] + kr) K2 + (d2[u2] + kc) for the lane's key (kr, kc), and the pair
+// is attended exactly when both terms lie in [0, K).  The weights of a chunk
+// are then one LDS entry each, gathered into the B operand of the product
+// that contracts over the chunk's 32 slots (as the key side's P in
+// k_lean_bwd_kv).  The w rows share one 2-byte phase (lead) per (batch, head):
+// the host checks that the row strides are even.
+// ---------------------------------------------------------------------------
+template <typename T>
+struct LeanWsumKeyArgs {
+    const int* rec;               // two records per key tile: the key record, then d1 / d2
+    const T *w, *x;
+    T* out;
+    LeanLay lw, lx, lo;
+    FastDiv heads, tiles;
+    FastDiv P;                    // words per staged w row
+    int nr;                       // LDS rows
+    int d1, d2, K1, K2;
+    uint32_t xbytes, wbytes;      // byte ranges of one (batch, head) plane of x and of w
+    float mul;
+    Prob p;
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void lean_redo_wsum_key(const void* kargs, int pos1, int pos2, int b, int h, int grp) {
+    const LeanWsumKeyArgs<T>& A = *static_cast<const LeanWsumKeyArgs<T>*>(kargs);
+    ExactAxis x[3];
+    x[0] = exact_axis(A.p.ax[0], 0);
+    x[1] = exact_axis(A.p.ax[1], pos1);
+    x[2] = exact_axis(A.p.ax[2], pos2);
+    f32x4_t acc[D / 16];
+    exact_wsum_key<T, D>(x, A.w + b * A.lw.b + h * A.lw.h, Strides3{0, A.lw.s1, A.lw.s2},
+                         A.x + b * A.lx.b + h * A.lx.h, Strides3{0, A.lx.s1, A.lx.s2}, grp, acc);
+    store_rows<T, D>(A.out + b * A.lo.b + h * A.lo.h, pos1 * A.lo.s1 + pos2 * A.lo.s2, grp, acc, A.mul);
+}
+
+// Staging of one operand's union rows [0, nst) (as lean_stage, one operand).
+template <typename T, int D>
+__device__ __forceinline__ void lean_stage1(__amdgpu_buffer_rsrc_t ra, T* Xa, int base, int step1, int step2, int U1,
+                                            int U2, int nst, int wave, int lane) {
+    constexpr int P = D / 8, SPI = 64 / P, HALVES = 16 / SPI;
+    uint32_t off[HALVES];
+    const int pp = lane % P;
+#pragma unroll
+    for (int hf = 0; hf < HALVES; ++hf) {
+        const int c = hf * SPI + lane / P;
+        const int slot = (wave & 1) * 16 + c;
+        off[hf] = c < U2 ? static_cast<uint32_t>(c * step2 + lean_piece<D>(pp, slot) * 16) : kLeanOOR;
+    }
+#pragma unroll 1
+    for (int i = wave; i < nst; i += kLeanWaves) {
+        const uint32_t ro = i < U1 ? static_cast<uint32_t>(base + i * step1) : kLeanOOR;
+#pragma unroll
+        for (int hf = 0; hf < HALVES; ++hf) {
+            const uint32_t o = off[hf] + ro;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(Xa + (i * 16 + hf * SPI) * D), 16, o, 0, 0,
+                                                     0);
+        }
+    }
+}
+
+template <typename T, int D, int MAXC>
+__global__ __launch_bounds__(64 * kLeanWaves) void k_lean_wsum_key(LeanWsumKeyArgs<T> a) {
+    const int nr = a.nr, P = static_cast<int>(a.P.d);
+    unsigned char* smem = lds_base();
+    T* Xs = reinterpret_cast<T*>(smem);
+    uint32_t* Ws32 = reinterpret_cast<uint32_t*>(Xs + nr * 16 * D);
+    const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int x = xcd_block(blockIdx.x, gridDim.x);
+    const int bt = fdiv(x, a.heads);
+    const int h = x - bt * static_cast<int>(a.heads.d);
+    const int b = fdiv(bt, a.tiles);
+    const int t = bt - b * static_cast<int>(a.tiles.d);
+    const int* r = a.rec + t * (2 * kLeanRec);
+    const int* r2 = r + kLeanRec;
+    const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
+    const int U1 = ext & 0xFF, U2 = (ext >> 8) & 0xFF, E1 = (ext >> 16) & 0xFF, E2 = (ext >> 24) & 0xFF;
+    const int kr = 2 * wave + (col >> 3), kc = col & 7;
+    const bool valid = kr < E1 && kc < E2;
+    const int pos1 = pr0 + kr * a.d1, pos2 = pc0 + kc * a.d2;
+    const int ooff = pos1 * a.lo.s1 + pos2 * a.lo.s2;
+    const long long obo = b * a.lo.b + h * a.lo.h;
+    if (r[14]) {  // no query attends these keys
+        if (valid) {
+            const __amdgpu_buffer_rsrc_t ro = lean_rsrc(a.out + obo, kLeanOOR);
+#pragma unroll
+            for (int db = 0; db < D / 16; ++db)
+                __builtin_amdgcn_raw_buffer_store_b64(v2u32_t{0u, 0u}, ro, ooff * 2 + db * 32 + grp * 8, 0, 0);
+        }
+        return;
+    }
+    // x rows of the union
+    const long long xo = b * a.lx.b + h * a.lx.h;
+    lean_stage1<T, D>(lean_rsrc(a.x + xo, a.xbytes), Xs, (ur0 * a.lx.s1 + uc0 * a.lx.s2) * 2, a.lx.s1 * a.d1 * 2,
+                      a.lx.s2 * a.d2 * 2, U1, U2, nst, wave, lane);
+    // w rows of the union: slot s = 16 u + cc at word s P, the words one
+    // after another; word t of the block goes to lane t % 64 of the DMA
+    // instruction t / 64 (rows and columns past the union load nothing
+    // useful: the tables mask them)
+    const T* wplane = a.w + b * a.lw.b + h * a.lw.h;
+    const int lead = static_cast<int>((reinterpret_cast<uintptr_t>(wplane) >> 1) & 1);
+    {
+        const __amdgpu_buffer_rsrc_t rw = lean_rsrc(wplane - lead, a.wbytes);
+        const int rs = a.lw.s1 * a.d1 * 2, cs = a.lw.s2 * a.d2 * 2;  // bytes between union rows / columns
+        const int rbase = (ur0 * a.lw.s1 + uc0 * a.lw.s2) * 2;
+        const int total = U1 * 16 * P;
+#pragma unroll 1
+        for (int t0 = wave * 64; t0 < total; t0 += 64 * kLeanWaves) {
+            const int t = t0 + lane;
+            const int slot = fdiv(t, a.P);
+            const int k = t - slot * P, u = slot >> 4, cc = slot & 15;
+            const uint32_t o = (t < total && cc < U2) ? static_cast<uint32_t>(rbase + u * rs + cc * cs + k * 4)
+                                                      : kLeanOOR;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t*)(Ws32 + t0), 4, o, 0, 0, 0);
+        }
+    }
+    // the wave's union rows [first, last] (of the key record)
+    const int first = __builtin_amdgcn_readfirstlane(sbyte(r[6], r[7], 2 * wave));
+    const int last = __builtin_amdgcn_readfirstlane(sbyte(r[10], r[11], 2 * wave + 1));
+    const int nch = (last - first + 2) >> 1;
+    // the lane's 8 slots of a chunk: union columns 8 (g % 2) + j; entry
+    // offsets (in 16-bit entries from the slot row 16 u1 + 8 (g % 2)) and
+    // the column masks, two entries per word
+    const int pe = 2 * P;  // entries per slot row
+    int cp[8];
+    uint32_t cm[4];
+    {
+        const int t0 = (grp & 1) ? r2[6] : r2[4], t1 = (grp & 1) ? r2[7] : r2[5];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int e2 = sbyte(t0, t1, j) + kc;
+            cp[j] = j * pe + lead + e2;
+            const uint32_t ok = static_cast<unsigned>(e2) < static_cast<unsigned>(a.K2) ? 0xFFFFu : 0u;
+            if (j & 1)
+                cm[j >> 1] |= ok << 16;
+            else
+                cm[j >> 1] = ok;
+        }
+    }
+    int toff[2][D / 16];
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi)
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<D>(first, lane, hi, db);
+
+    const int d10 = r2[0], d11 = r2[1], d12 = r2[2], d13 = r2[3];  // d1 bytes of union rows 0-15
+
+    wait_loads();
+    __syncthreads();
+
+    const unsigned char* Xb = reinterpret_cast<const unsigned char*>(Xs);
+    const uint16_t* Ws = reinterpret_cast<const uint16_t*>(Ws32);
+    f32x4_t acc[D / 16];
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        if (c >= nch) break;  // wave-uniform
+        // union row of the lane's slots, its d1 entry (rows past the table: none attend)
+        const int ua = first + 2 * c, ub = ua + 1;
+        const int da = ua < 8 ? sbyte(d10, d11, ua) : (ua < 16 ? sbyte(d12, d13, ua - 8) : -100);
+        const int dbb = ub < 8 ? sbyte(d10, d11, ub) : (ub < 16 ? sbyte(d12, d13, ub - 8) : -100);
+        const int u1 = (grp >> 1) ? ub : ua;
+        const int e1 = ((grp >> 1) ? dbb : da) + kr;
+        const bool rok = valid && static_cast<unsigned>(e1) < static_cast<unsigned>(a.K1);
+        const int rowpart = (u1 * 16 + 8 * (grp & 1)) * pe + e1 * a.K2;
+        uint32_t wv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo16 = Ws[rowpart + cp[2 * i]];
+            const uint32_t hi16 = Ws[rowpart + cp[2 * i + 1]];
+            wv[i] = rok ? ((lo16 | (hi16 << 16)) & cm[i]) : 0u;
+        }
+        lean_accumulate<T, D>(Xb, toff, c, make_uint4(wv[0], wv[1], wv[2], wv[3]), acc);
+    }
+    const bool redo = valid && item_nonfinite(lane_sum(acc, 0.f));
+    if (valid) {
+        const __amdgpu_buffer_rsrc_t ro = lean_rsrc(a.out + obo, kLeanOOR);
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) {
+            const uint2 wo = make_uint2(Mma<T>::pack(acc[db][0] * a.mul, acc[db][1] * a.mul),
+                                        Mma<T>::pack(acc[db][2] * a.mul, acc[db][3] * a.mul));
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, wo), ro, ooff * 2 + db * 32 + grp * 8,
+                                                  0, 0);
+        }
+    }
+    if (redo) lean_redo_wsum_key<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, h, grp);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -670,6 +868,7 @@ struct LeanGeo {
 
 struct LeanAxisTile {
     int pos0, upos0, E, U;
+    int J, lo;   // class coordinates of the first item and of the union's first member
     int ws[8];   // per item: window start (key tiles: first attending query), union-relative
     int we[8];   // key tiles: last attending query, union-relative
 };
@@ -691,6 +890,8 @@ bool lean_axis_tile(const Axis& A, int r, int t, bool key, LeanAxisTile& o) {
         if (hi < lo) return false;
     }
     o.U = hi - lo + 1;
+    o.J = J;
+    o.lo = lo;
     o.pos0 = r + J * A.dil;
     o.upos0 = r + lo * A.dil;
     for (int e = 0; e < 8; ++e) {
@@ -714,16 +915,30 @@ int pack_bytes(const int* v, int i0) {
     return static_cast<int>(w);
 }
 
+// d[u] = J - ws(lo + u) over the union members u < U of a key tile's axis
+// (the entry offset of the tile's first key in member u's window), -100
+// past the union; packed as 16 signed bytes.
+void split_table(const Axis& A, int r, const LeanAxisTile& a, int* out4) {
+    const ClassAxis c = class_axis(A, r);
+    int d[16];
+    for (int u = 0; u < 16; ++u) d[u] = u < a.U ? a.J - class_ws(c, a.lo + u) : -100;
+    for (int i = 0; i < 4; ++i) out4[i] = pack_bytes(d, 4 * i);
+}
+
 // Builds (or finds) the records.  Query tiles: rows of a wave start at
-// max(ws[2w], 0) and span at most K1 + 1 rows; nst = rows to stage.
-const LeanGeo* lean_geometry(const Prob& p, bool key, int nch, hipStream_t s) {
+// max(ws[2w], 0) and span at most K1 + 1 rows; nst = rows to stage.  Mode:
+// 0 query tiles, 1 key tiles, 2 key tiles of the split key side (each key
+// record followed by a second one holding the d1 / d2 tables).
+const LeanGeo* lean_geometry(const Prob& p, int mode, int nch, hipStream_t s) {
     static std::mutex mu;
     static std::vector<LeanGeo*> cache;
+    const bool key = mode != 0;
+    const int per_tile = mode == 2 ? 2 * kLeanRec : kLeanRec;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     LeanGeo k{};
     k.dev = dev;
-    k.key = key ? 1 : 0;
+    k.key = mode;
     for (int a = 0; a < 2; ++a) {
         k.len[a] = p.ax[a + 1].len;
         k.k[a] = p.ax[a + 1].k;
@@ -785,6 +1000,15 @@ const LeanGeo* lean_geometry(const Prob& p, bool key, int nch, hipStream_t s) {
                         rec[14] = 1;
                     }
                     h.insert(h.end(), rec, rec + kLeanRec);
+                    if (mode == 2) {
+                        int tab[kLeanRec] = {};
+                        if (ok1 && ok2) {
+                            if (a1.U > 16) return nullptr;
+                            split_table(A1, r1, a1, tab);
+                            split_table(A2, r2, a2, tab + 4);
+                        }
+                        h.insert(h.end(), tab, tab + kLeanRec);
+                    }
                 }
             }
         }
@@ -807,7 +1031,7 @@ const LeanGeo* lean_geometry(const Prob& p, bool key, int nch, hipStream_t s) {
         return nullptr;
     }
     e->ptr = d;
-    e->ntiles = static_cast<int>(e->host.size() / kLeanRec);
+    e->ntiles = static_cast<int>(e->host.size() / per_tile);
     e->nst_max = nst_max;
     e->rows_max = rows_max;
     cache.push_back(e);
@@ -842,6 +1066,7 @@ void lean_audit_one(LdsAudit& a) {
     audit_one(k_lean_fwd<T, D, NCH>, "k_lean_fwd", a);
     audit_one(k_lean_bwd_q<T, D, NCH>, "k_lean_bwd_q", a);
     audit_one(k_lean_bwd_kv<T, D, NCH + 2>, "k_lean_bwd_kv", a);
+    audit_one(k_lean_wsum_key<T, D, NCH + 2>, "k_lean_wsum_key", a);
 }
 
 template <typename T, int D>
@@ -948,7 +1173,7 @@ hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay
     (void)lo;
     const int nch = lean_nch(p.ax[1].k);
     if (static_cast<long long>(p.B) * p.Hq * 4096 >= (1LL << 31)) return hipErrorNotSupported;
-    const LeanGeo* g = lean_geometry(p, false, nch, s);
+    const LeanGeo* g = lean_geometry(p, 0, nch, s);
     if (!g) return hipErrorNotSupported;
 #define NA_LF(T, DD, N) return lean_fwd_run<T, DD, N>(p, g, q, lq, k, lk, v, o, lse, ll, s)
 #define NA_LF_N(T, DD)          \
@@ -1040,8 +1265,8 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
     if (!same_lay(ll, lde) || (dlse && !same_lay(ll, ldl))) return hipErrorNotSupported;
     if (static_cast<long long>(p.B) * p.Hq * 8192 >= (1LL << 31)) return hipErrorNotSupported;
     const int nch = lean_nch(p.ax[1].k);
-    const LeanGeo* gq = lean_geometry(p, false, nch, s);
-    const LeanGeo* gk = gq ? lean_geometry(p, true, nch, s) : nullptr;
+    const LeanGeo* gq = lean_geometry(p, 0, nch, s);
+    const LeanGeo* gk = gq ? lean_geometry(p, 1, nch, s) : nullptr;
     if (!gq || !gk || gq->ntiles != gk->ntiles || gk->rows_max > 2 * (nch + 2)) return hipErrorNotSupported;
 #define NA_LB(T, DD, N)                                                                                           \
     return lean_bwd_run<T, DD, N>(p, gq, gk,                                                                      \
@@ -1063,6 +1288,106 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
     NA_LB_N(f16, 64);
 #undef NA_LB_N
 #undef NA_LB
+}
+
+// Split ops, key side, on the 8x8 key tiles: eligibility beyond the general
+// lean checks -- one head count, w's row strides even (one 2-byte phase of
+// the w rows per (batch, head)), w's plane below 2^30 bytes.
+bool lean_wsum_key_eligible(const Prob& p, int dtype, int D, bool aligned, const Lay& lw, const Lay& lx,
+                            const Lay& lo) {
+    if (!lean_switch() || dtype == NATTEN_F32 || !aligned || !lean_static_lds_ok()) return false;
+    if (p.Hq != p.Hkv || (D != 32 && D != 64)) return false;
+    if (p.ax[0].len != 1 || p.ax[0].k != 1 || p.ax[1].len < 8) return false;
+    for (int a = 1; a < 3; ++a) {
+        const Axis& A = p.ax[a];
+        if (A.st != 1 || A.k > 9 || A.len >= (1 << 15)) return false;
+    }
+    for (const Lay& l : {lx, lo, lw}) {
+        if (l.s1 < 0 || l.s2 < 0 || l.b < 0 || l.h < 0) return false;
+        const long long v = ((static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
+                             (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + std::max(D, p.kv + 2)) * 2;
+        if (v >= (1LL << 30)) return false;
+    }
+    return (lw.s1 & 1) == 0 && (lw.s2 & 1) == 0;
+}
+
+namespace {
+
+template <typename T, int D, int MAXC>
+hipError_t lean_wsum_key_run(const char* name, const Prob& p, const LeanGeo* g, const void* w, Lay lw, const void* x,
+                             Lay lx, void* o, Lay lo, float mul, hipStream_t s) {
+    LeanWsumKeyArgs<T> a{};
+    a.rec = g->ptr;
+    a.w = static_cast<const T*>(w);
+    a.x = static_cast<const T*>(x);
+    a.out = static_cast<T*>(o);
+    a.lw = lean_lay(lw);
+    a.lx = lean_lay(lx);
+    a.lo = lean_lay(lo);
+    a.heads = make_fastdiv(p.Hq);
+    a.tiles = make_fastdiv(g->ntiles);
+    a.nr = std::max(g->nst_max, 1);
+    const int P = (p.kv + 2) / 2;  // words of a row with its 2-byte phase
+    a.P = make_fastdiv(P);
+    a.d1 = p.ax[1].dil;
+    a.d2 = p.ax[2].dil;
+    a.K1 = p.ax[1].k;
+    a.K2 = p.ax[2].k;
+    a.xbytes = plane_bytes(p, lx, D);
+    const long long wb = ((static_cast<long long>(p.ax[1].len) - 1) * lw.s1 +
+                          (static_cast<long long>(p.ax[2].len) - 1) * lw.s2 + p.kv + 1) * 2;
+    a.wbytes = static_cast<uint32_t>((wb + 3) & ~3LL);
+    a.mul = mul;
+    a.p = p;
+    // x rows, w slot rows (the DMA's last instruction may write up to 63
+    // words past them), and room for the gather's masked reads past the last
+    // slot row: at most (K1 + 6) K2 + K2 + 7 entries from a slot's start
+    const size_t over = std::max<size_t>(63 * 4, (static_cast<size_t>(p.ax[1].k + 7) * p.ax[2].k + 8) * 2);
+    const size_t shm = kLdsPad + static_cast<size_t>(a.nr) * 16 * (D * sizeof(T) + P * 4) + over;
+    if (shm > 160 * 1024) return hipErrorNotSupported;
+    auto kern = k_lean_wsum_key<T, D, MAXC>;
+    hipError_t e = allow_lds(kern, shm);
+    if (e != hipSuccess) return e;
+    const long long tasks = static_cast<long long>(p.B) * p.Hq * g->ntiles;
+    NA_LAUNCH(name, kern, dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves), shm, s, a);
+    return hipGetLastError();
+}
+
+// Launch names of the key-side split ops on these kernels.
+const char* lean_key_name(const char* name) {
+    if (std::strcmp(name, "na_qk_bwd_k_mfma") == 0) return "na_qk_bwd_k_lean";
+    if (std::strcmp(name, "na_av_bwd_v_mfma") == 0) return "na_av_bwd_v_lean";
+    if (std::strcmp(name, "na_rpb_dk_mfma") == 0) return "na_rpb_dk_lean";
+    if (std::strcmp(name, "na_rpb_dv_mfma") == 0) return "na_rpb_dv_lean";
+    return name;
+}
+
+}  // namespace
+
+hipError_t lean_wsum_key(const char* name, const Prob& p, int D, const void* w, Lay lw, const void* x, Lay lx,
+                         void* o, Lay lo, float mul, int dtype, hipStream_t s) {
+    const int nch = lean_nch(p.ax[1].k);
+    if (static_cast<long long>(p.B) * p.Hq * 8192 >= (1LL << 31)) return hipErrorNotSupported;
+    const LeanGeo* g = lean_geometry(p, 2, nch, s);
+    if (!g || g->rows_max > 2 * (nch + 2)) return hipErrorNotSupported;
+    name = lean_key_name(name);
+#define NA_LW(T, DD, N) return lean_wsum_key_run<T, DD, N + 2>(name, p, g, w, lw, x, lx, o, lo, mul, s)
+#define NA_LW_N(T, DD)          \
+    switch (nch) {              \
+        case 1: NA_LW(T, DD, 1); \
+        case 2: NA_LW(T, DD, 2); \
+        case 3: NA_LW(T, DD, 3); \
+        case 4: NA_LW(T, DD, 4); \
+        default: NA_LW(T, DD, 5); \
+    }
+    if (dtype == NATTEN_BF16) {
+        if (D == 32) NA_LW_N(bf16, 32);
+        NA_LW_N(bf16, 64);
+    }
+    if (D == 32) NA_LW_N(f16, 32);
+    NA_LW_N(f16, 64);
+#undef NA_LW_N
+#undef NA_LW
 }
 
 }  // namespace na

@@ -2042,6 +2042,12 @@ bool mfma_split_key_eligible(const Prob& p, int dtype, int D, bool aligned, cons
 
 hipError_t mfma_split_wsum_key(const char* name, const Prob& p, int D, const void* w, Lay lw, const void* x, Lay lx,
                                void* o, Lay lo, float mul, int dtype, hipStream_t s) {
+    // the 8x8 key tiles first (2-D, head dim 32 / 64, K <= 9); their
+    // operands' alignment is the one mfma_split_key_eligible checked
+    if (lean_wsum_key_eligible(p, dtype, D, true, lw, lx, lo)) {
+        const hipError_t e = lean_wsum_key(name, p, D, w, lw, x, lx, o, lo, mul, dtype, s);
+        if (e != hipErrorNotSupported) return e;
+    }
 #define NA_WSUMK(T, DD) return run_wsum_key<T, DD>(name, p, w, lw, x, lx, o, lo, mul, s)
     if (dtype == NATTEN_BF16) {
         if (D == 32) NA_WSUMK(bf16, 32);

@@ -390,7 +390,9 @@ def test_split_ops_tile_path(case, dim, dtype):
     ran = _lib.profile_read(reset=True)
     for name in ("na_qk_mfma", "na_av_mfma", "na_qk_bwd_q_mfma", "na_av_bwd_a_mfma", "na_qk_bwd_k_mfma",
                  "na_av_bwd_v_mfma"):
-        assert ran.get(name, (0,))[0] >= 1, (name, sorted(ran))
+        # the key-side launches run on the 8x8 key tiles where those apply (2-D, head dim 32 / 64)
+        alt = name.replace("_mfma", "_lean")
+        assert ran.get(name, (0,))[0] + ran.get(alt, (0,))[0] >= 1, (name, sorted(ran))
 
 
 def _random_split_cases(n, seed=2024):
@@ -599,7 +601,9 @@ def test_split_ops_tile_path_strided_views():
     ran = _lib.profile_read(reset=True)
     for name in ("na_qk_mfma", "na_av_mfma", "na_qk_bwd_q_mfma", "na_av_bwd_a_mfma", "na_qk_bwd_k_mfma",
                  "na_av_bwd_v_mfma"):
-        assert ran.get(name, (0,))[0] >= 1, (name, sorted(ran))
+        # the key-side launches run on the 8x8 key tiles where those apply (2-D, head dim 32 / 64)
+        alt = name.replace("_mfma", "_lean")
+        assert ran.get(name, (0,))[0] + ran.get(alt, (0,))[0] >= 1, (name, sorted(ran))
 
     xr = x.float().requires_grad_(True)
     qr, kr, vr = xr.permute(3, 0, 1, 2, 4, 5).unbind(0)
