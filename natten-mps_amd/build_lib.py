@@ -85,6 +85,51 @@ def binding_commands():
     return comp, link
 
 
+LLVM = "/opt/rocm/llvm/bin"
+
+
+def outlined_device_functions(obj: str) -> list:
+    """Device functions of a built object that are not kernels.
+
+    The kernels' non-finite recomputation paths read the kernel-argument
+    segment pointer (kernargs() in na_tile.h), which is only meaningful in
+    the kernel's own code: a copy of such a path compiled out of line would
+    read another address.  So every device function must be inlined into a
+    kernel: each FUNC symbol of the gfx950 code object needs a kernel
+    descriptor (<name>.kd).  Returns the names that have none."""
+    import tempfile
+
+    if ".hip_fatbin" not in _run([os.path.join(LLVM, "llvm-readelf"), "-S", "-W", obj]).stdout:
+        return []  # host code only
+    with tempfile.TemporaryDirectory() as tmp:
+        fat, co = os.path.join(tmp, "fat.bin"), os.path.join(tmp, "dev.co")
+        _run([os.path.join(LLVM, "llvm-objcopy"), f"--dump-section=.hip_fatbin={fat}", obj,
+              os.path.join(tmp, "rest.o")])
+        _run([os.path.join(LLVM, "clang-offload-bundler"), "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950",
+              f"--input={fat}", f"--output={co}", "--unbundle"])
+        syms = _run([os.path.join(LLVM, "llvm-readelf"), "-s", "-W", co]).stdout.split("\n")
+    funcs, kds = set(), set()
+    for line in syms:
+        parts = line.split()
+        if len(parts) >= 8 and parts[3] == "FUNC":
+            funcs.add(parts[7])
+        elif len(parts) >= 8 and parts[7].endswith(".kd"):
+            kds.add(parts[7][:-3])
+    return sorted(funcs - kds)
+
+
+def check_inlined(verbose: bool = False) -> None:
+    cmds, _ = commands()
+    for cmd in cmds:
+        obj = cmd[-1]
+        bad = outlined_device_functions(obj)
+        if bad:
+            raise RuntimeError(f"{obj}: device functions compiled out of line (must be inlined into kernels): "
+                               f"{bad[:5]}")
+    if verbose:
+        print(f"checked {len(cmds)} objects: every device function is inlined into a kernel")
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     cmds, link = commands()
@@ -100,6 +145,7 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(" ".join(link[:-1] + [LIB]))
+    check_inlined(verbose)
     btmp = BIND + ".tmp"
     _run([btmp if x == BIND else x for x in blink])
     os.replace(btmp, BIND)

@@ -137,3 +137,20 @@ def test_torch_binding_loads_against_the_same_library(lib):
     with pytest.raises(ValueError, match="not a backward signature"):
         z = torch.zeros(1)
         call.backward(z, z, z, z, z, z, None, 0)
+
+
+def test_every_device_function_is_inlined_into_a_kernel():
+    """The non-finite recomputation paths read the kernel-argument pointer,
+    which only the kernel's own code may do: the built gfx950 code objects
+    hold no device function outside a kernel (each FUNC symbol has its
+    kernel descriptor).  build_lib.build() runs the same check."""
+    import sys
+
+    sys.path.insert(0, os.path.join(ROOT, "natten-mps_amd"))
+    import build_lib
+
+    objs = [cmd[-1] for cmd in build_lib.commands()[0]]
+    if not all(os.path.exists(o) for o in objs):
+        pytest.skip("objects not built here (natten-mps_amd/_build)")
+    for o in objs:
+        assert build_lib.outlined_device_functions(o) == [], o
