@@ -27,18 +27,31 @@ namespace na {
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-// a . b over D elements (16-byte aligned rows, D % 8 == 0), fp32 accumulation.
+// a . b over D elements (16-byte aligned rows, D % 8 == 0), fp32 accumulation
+// in element order.
 template <typename T, int D>
 __device__ __forceinline__ float exact_dot(const T* __restrict__ a, const T* __restrict__ b) {
     float s = 0.f;
+    if constexpr (sizeof(T) == 4) {
 #pragma unroll 1
-    for (int c = 0; c < D; c += 8) {
-        const uint4 x = *reinterpret_cast<const uint4*>(a + c);
-        const uint4 y = *reinterpret_cast<const uint4*>(b + c);
-        const T* xe = reinterpret_cast<const T*>(&x);
-        const T* ye = reinterpret_cast<const T*>(&y);
+        for (int c = 0; c < D; c += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(a + c);
+            const float4 y = *reinterpret_cast<const float4*>(b + c);
+            s = fmaf(x.x, y.x, s);
+            s = fmaf(x.y, y.y, s);
+            s = fmaf(x.z, y.z, s);
+            s = fmaf(x.w, y.w, s);
+        }
+    } else {
+#pragma unroll 1
+        for (int c = 0; c < D; c += 8) {
+            const uint4 x = *reinterpret_cast<const uint4*>(a + c);
+            const uint4 y = *reinterpret_cast<const uint4*>(b + c);
+            const T* xe = reinterpret_cast<const T*>(&x);
+            const T* ye = reinterpret_cast<const T*>(&y);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s = fmaf(to_f(xe[e]), to_f(ye[e]), s);
+            for (int e = 0; e < 8; ++e) s = fmaf(to_f(xe[e]), to_f(ye[e]), s);
+        }
     }
     return s;
 }
@@ -48,10 +61,18 @@ template <typename T, int D>
 __device__ __forceinline__ void exact_axpy(float w, const T* __restrict__ x, int grp, f32x4_t (&acc)[D / 16]) {
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
-        const uint2 r = *reinterpret_cast<const uint2*>(x + db * 16 + grp * 4);
-        const T* e = reinterpret_cast<const T*>(&r);
+        if constexpr (sizeof(T) == 4) {
+            const float4 r = *reinterpret_cast<const float4*>(x + db * 16 + grp * 4);
+            acc[db][0] = fmaf(w, r.x, acc[db][0]);
+            acc[db][1] = fmaf(w, r.y, acc[db][1]);
+            acc[db][2] = fmaf(w, r.z, acc[db][2]);
+            acc[db][3] = fmaf(w, r.w, acc[db][3]);
+        } else {
+            const uint2 r = *reinterpret_cast<const uint2*>(x + db * 16 + grp * 4);
+            const T* e = reinterpret_cast<const T*>(&r);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[db][i] = fmaf(w, to_f(e[i]), acc[db][i]);
+            for (int i = 0; i < 4; ++i) acc[db][i] = fmaf(w, to_f(e[i]), acc[db][i]);
+        }
     }
 }
 

@@ -46,7 +46,34 @@ constexpr int kLeanRec = 16;                 // dwords per tile record
 constexpr uint32_t kLeanOOR = 0x40000000u;   // offset past every staged plane's range (planes < 2^30 bytes)
 constexpr int kLeanWaves = 4;
 
+// Element types: bf16 / fp16 (v_mfma_f32_16x16x32, the products' operands
+// 8 elements per lane) and fp32 (v_mfma_f32_16x16x4_f32, one element per
+// lane and k-step).  A staged row of D elements is as wide as kRowD 16-bit
+// elements: staging and the XOR swizzle act on its 16-byte pieces as for a
+// 16-bit row of that width.  A lane's fragment of a row (the B operand of
+// the products over head dims) is kNF 16-byte pieces: 16-bit, dims 32 j +
+// 8 g .. + 7 of piece j for lane group g; fp32, dims (D / 4) g + 4 j .. + 3,
+// so that k-step ks of the fp32 product takes dim (D / 4) g + ks.
+template <typename T>
+constexpr bool kF32 = sizeof(T) == 4;
+template <typename T, int D>
+constexpr int kRowD = D * static_cast<int>(sizeof(T)) / 2;
+template <typename T, int D>
+constexpr int kNF = D * static_cast<int>(sizeof(T)) / 64;
+// Offset variants of the transposed reads (fp32: per low slot bits that the
+// swizzle takes, see lean_tr_off).
+template <typename T, int D>
+constexpr int kTV = !kF32<T> ? 2 : (D == 32 ? 2 : 4);
+constexpr int kLeanEsz2 = 2;
+
+// Byte offset of fragment piece j of lane group g inside a row.
+template <typename T, int D>
+__device__ __forceinline__ int lean_frag_off(int j, int g) {
+    return kF32<T> ? g * D + j * 16 : j * 64 + g * 16;
+}
+
 typedef unsigned int v2u32_t __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u32_t __attribute__((ext_vector_type(4)));
 
 // Layout of one operand group: batch and head strides, and the element
 // strides of the two spatial axes (axis 0 of the padded problem has extent 1).
@@ -88,7 +115,8 @@ template <typename T, int D>
 __device__ __forceinline__ void lean_stage(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, T* Xa, T* Xb,
                                            int base, int step1, int step2, int U1, int U2, int nst, int wave,
                                            int lane) {
-    constexpr int P = D / 8, SPI = 64 / P, HALVES = 16 / SPI;
+    constexpr int R = kRowD<T, D>;
+    constexpr int P = R / 8, SPI = 64 / P, HALVES = 16 / SPI;
     static_assert(kLeanWaves % 2 == 0, "a wave's rows must keep one parity");
     // lane part of the offset per half row; a wave's rows i = wave + 4j all
     // have the parity of `wave`, which fixes the swizzle's row bit
@@ -98,7 +126,7 @@ __device__ __forceinline__ void lean_stage(__amdgpu_buffer_rsrc_t ra, __amdgpu_b
     for (int hf = 0; hf < HALVES; ++hf) {
         const int c = hf * SPI + lane / P;
         const int slot = (wave & 1) * 16 + c;
-        off[hf] = c < U2 ? static_cast<uint32_t>(c * step2 + lean_piece<D>(pp, slot) * 16) : kLeanOOR;
+        off[hf] = c < U2 ? static_cast<uint32_t>(c * step2 + lean_piece<R>(pp, slot) * 16) : kLeanOOR;
     }
 #pragma unroll 1
     for (int i = wave; i < nst; i += kLeanWaves) {
@@ -123,31 +151,58 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t lean_rsrc(const T* p, uint32_t
 // LDS byte offsets (from the operand's base) of the lane's score A operand
 // for blocks b = 0, 1 of chunk 0 of a wave whose rows start at union row
 // `first`, k-step ks: slot 8(n/4) + 4b + n%4, logical piece 4ks + g.
-template <int D>
+template <typename T, int D>
 __device__ __forceinline__ int lean_score_off(int first, int col, int grp, int b, int ks) {
+    constexpr int R = kRowD<T, D>;
     const int slot = first * 16 + 8 * (col >> 2) + 4 * b + (col & 3);
-    return slot * D * 2 + ((ks * 4 + grp) ^ swz<D>(slot)) * 16;
+    const int piece = kF32<T> ? (D / 16) * grp + ks : ks * 4 + grp;
+    return slot * R * 2 + (piece ^ swz<R>(slot)) * 16;
 }
 
 // LDS byte offset of the lane's transposing read (rows r0 or r1 = r0 + 4 of
 // chunk 0, 16-dim block db): see accumulate_chunk in na_tile.h.
-template <int D>
+// fp32: the A operand of k-step kk (0..7) for lane (m, g) is element
+// d = 16 db + m of slot 8 g + kk of the chunk; variant v carries the slot
+// bits below 8 that the swizzle reads ((kk >> 1) & 1 at D = 32, kk & 3 at
+// D = 64), and the read adds kk rows.
+template <typename T, int D>
 __device__ __forceinline__ int lean_tr_off(int first, int lane, int hi, int db) {
     const int g = lane >> 4, j = lane & 15;
+    if constexpr (kF32<T>) {
+        constexpr int R = kRowD<T, D>;
+        const int s0 = first * 16 + 8 * g;
+        const int rep = s0 + (D == 32 ? 2 * hi : hi);
+        return s0 * R * 2 + (((4 * db + (j >> 2)) ^ swz<R>(rep)) * 16) + (j & 3) * 4;
+    }
     const int r = first * 16 + 8 * g + (j >> 2) + 4 * hi;
     const int kb = 2 * db + ((j & 3) >> 1);
     return r * D * 2 + (kb ^ swz<D>(r)) * 16 + (j & 1) * 8;
 }
 
 template <typename T, int D>
-__device__ __forceinline__ f32x4_t lean_score(const unsigned char* X, const int (&aoff)[2][D / 32], int c, int b,
-                                              const uint4 (&frag)[D / 32], f32x4_t acc) {
+__device__ __forceinline__ f32x4_t lean_score(const unsigned char* X, const int (&aoff)[2][kNF<T, D>], int c, int b,
+                                              const uint4 (&frag)[kNF<T, D>], f32x4_t acc) {
+    if constexpr (kF32<T>) {
+        constexpr int R = kRowD<T, D>;
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) {
-        const uint4 a = *reinterpret_cast<const uint4*>(X + aoff[b][ks] + c * 32 * D * 2);
-        acc = Mma<T>::run(a, frag[ks], acc);
+        for (int j = 0; j < kNF<T, D>; ++j) {
+            const uint4 a = *reinterpret_cast<const uint4*>(X + aoff[b][j] + c * 32 * R * 2);
+            const uint32_t av[4] = {a.x, a.y, a.z, a.w};
+            const uint32_t bv[4] = {frag[j].x, frag[j].y, frag[j].z, frag[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(av[e]), __uint_as_float(bv[e]), acc, 0, 0,
+                                                            0);
+        }
+        return acc;
+    } else {
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            const uint4 a = *reinterpret_cast<const uint4*>(X + aoff[b][ks] + c * 32 * D * 2);
+            acc = Mma<T>::run(a, frag[ks], acc);
+        }
+        return acc;
     }
-    return acc;
 }
 
 // acc[db] += X^T[db block][chunk c slots] * packed (B operand: 8 slots of the lane's item).
@@ -160,6 +215,55 @@ __device__ __forceinline__ void lean_accumulate(const unsigned char* X, const in
         const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(X + toff[1][db] + c * 32 * D * 2));
         const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
         acc[db] = Mma<T>::run(make_uint4(l2.x, l2.y, h2.x, h2.y), packed, acc[db]);
+    }
+}
+
+// acc[db] += X^T[db block][chunk c slots] * p, p the lane's 8 slot values
+// (16-bit: rounded to T and packed as the B operand; fp32: k-step kk takes
+// slot 8 g + kk, value p[kk / 4][kk % 4]).
+template <typename T, int D>
+__device__ __forceinline__ void lean_acc(const unsigned char* X, const int (&toff)[kTV<T, D>][D / 16], int c,
+                                         const f32x4_t (&p)[2], f32x4_t (&acc)[D / 16]) {
+    if constexpr (kF32<T>) {
+        constexpr int R = kRowD<T, D>;
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const int v = D == 32 ? ((kk >> 1) & 1) : (kk & 3);
+                const float a = *reinterpret_cast<const float*>(X + toff[v][db] + (c * 32 + kk) * R * 2);
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, p[kk >> 2][kk & 3], acc[db], 0, 0, 0);
+            }
+    } else {
+        lean_accumulate<T, D>(X, toff, c, pack8<T>(p), acc);
+    }
+}
+
+// acc + the products of two fragment pieces (16-bit: dot8, 8 elements in
+// pairs; fp32: 4 elements in order).
+template <typename T>
+__device__ __forceinline__ float lean_dot(uint4 x, uint4 y, float acc) {
+    if constexpr (kF32<T>) {
+        acc = fmaf(__uint_as_float(x.x), __uint_as_float(y.x), acc);
+        acc = fmaf(__uint_as_float(x.y), __uint_as_float(y.y), acc);
+        acc = fmaf(__uint_as_float(x.z), __uint_as_float(y.z), acc);
+        return fmaf(__uint_as_float(x.w), __uint_as_float(y.w), acc);
+    } else {
+        return dot8<T>(x, y, acc);
+    }
+}
+
+// Store of the lane's 4 consecutive dims of 16-dim block db (times mul) into
+// the row at byte offset `row`.
+template <typename T>
+__device__ __forceinline__ void lean_store4(__amdgpu_buffer_rsrc_t rs, int row, int db, int grp, f32x4_t v, float mul) {
+    if constexpr (kF32<T>) {
+        const uint4 w = make_uint4(__float_as_uint(v[0] * mul), __float_as_uint(v[1] * mul), __float_as_uint(v[2] * mul),
+                                   __float_as_uint(v[3] * mul));
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32_t, w), rs, row + db * 64 + grp * 16, 0, 0);
+    } else {
+        const uint2 w = make_uint2(Mma<T>::pack(v[0] * mul, v[1] * mul), Mma<T>::pack(v[2] * mul, v[3] * mul));
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, w), rs, row + db * 32 + grp * 8, 0, 0);
     }
 }
 
@@ -198,7 +302,7 @@ __device__ __forceinline__ void lean_redo_fwd(const void* kargs, int pos1, int p
 // ---------------------------------------------------------------------------
 template <typename T, int D, int NCH>
 __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) {
-    constexpr int NR = 2 * NCH + 6;
+    constexpr int NR = 2 * NCH + 6, NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
     unsigned char* smem = lds_base();
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + NR * 16 * D;
@@ -217,9 +321,9 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
     // stage the union's K and V rows
     {
         const long long kvo = b * a.lk.b + hk * a.lk.h;
-        const int s1 = a.lk.s1 * a.d1 * 2, s2 = a.lk.s2 * a.d2 * 2;
+        const int s1 = a.lk.s1 * a.d1 * ES, s2 = a.lk.s2 * a.d2 * ES;
         lean_stage<T, D>(lean_rsrc(a.k + kvo, a.kbytes), lean_rsrc(a.v + kvo, a.kbytes), Ks, Vs,
-                         (ur0 * a.lk.s1 + uc0 * a.lk.s2) * 2, s1, s2, U1, U2, nst, wave, lane);
+                         (ur0 * a.lk.s1 + uc0 * a.lk.s2) * ES, s1, s2, U1, U2, nst, wave, lane);
     }
 
     // the lane's query and its fragments
@@ -228,12 +332,12 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
     const int pos1 = pr0 + qr * a.d1, pos2 = pc0 + qc * a.d2;
     const int qoff = pos1 * a.lq.s1 + pos2 * a.lq.s2;
     const long long qbo = b * a.lq.b + h * a.lq.h;
-    uint4 qf[D / 32];
+    uint4 qf[NF];
     {
         const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + qbo, a.qbytes);
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) {
-            const uint32_t o = valid ? static_cast<uint32_t>(qoff * 2 + ks * 64 + grp * 16) : kLeanOOR;
+        for (int ks = 0; ks < NF; ++ks) {
+            const uint32_t o = valid ? static_cast<uint32_t>(qoff * ES + lean_frag_off<T, D>(ks, grp)) : kLeanOOR;
             qf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 0));
         }
     }
@@ -244,15 +348,15 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
     const int clo = sbyte(r[8], r[9], qc);
     f32x4_t cb[2];
     lean_colbias(clo, a.K2, grp, cb);
-    int aoff[2][D / 32], toff[2][D / 16];
+    int aoff[2][NF], toff[TV][D / 16];
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) aoff[bb][ks] = lean_score_off<D>(first, col, grp, bb, ks);
+        for (int ks = 0; ks < NF; ++ks) aoff[bb][ks] = lean_score_off<T, D>(first, col, grp, bb, ks);
 #pragma unroll
-    for (int hi = 0; hi < 2; ++hi)
+    for (int hi = 0; hi < TV; ++hi)
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<D>(first, lane, hi, db);
+        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<T, D>(first, lane, hi, db);
 
     wait_loads();
     __syncthreads();
@@ -272,8 +376,8 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
     }
     const float m = max_rows(mx) * a.sc2;
     const float mref = m == -INFINITY ? 0.f : m;
-    const uint4 ones = make_uint4(Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes);
     f32x4_t acc[D / 16], lacc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float lpart = 0.f;
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -283,22 +387,28 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) s[c][bb][i] = __builtin_amdgcn_exp2f(fmaf(s[c][bb][i], a.sc2, off));
-        const uint4 pk = pack8<T>(s[c]);
-        lean_accumulate<T, D>(Vb, toff, c, pk, acc);
-        lacc = Mma<T>::run(ones, pk, lacc);
+        if constexpr (kF32<T>) {
+            // row sums of the probabilities themselves, in slot order
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) lpart += s[c][bb][i];
+            lean_acc<T, D>(Vb, toff, c, s[c], acc);
+        } else {
+            // row sums from one more MFMA against ones: the same rounded P as the product
+            const uint4 pk = pack8<T>(s[c]);
+            lean_accumulate<T, D>(Vb, toff, c, pk, acc);
+            const uint4 ones = make_uint4(Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes);
+            lacc = Mma<T>::run(ones, pk, lacc);
+        }
     }
-    const float lsum = lacc[0];
+    const float lsum = kF32<T> ? sum_rows(lpart) : lacc[0];
     const bool redo = valid && item_nonfinite(lane_sum(acc, lsum));
     if (valid) {
         const float inv = 1.f / lsum;
         const __amdgpu_buffer_rsrc_t ro = lean_rsrc(a.out + qbo, a.qbytes);
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db) {
-            const uint2 w = make_uint2(Mma<T>::pack(acc[db][0] * inv, acc[db][1] * inv),
-                                       Mma<T>::pack(acc[db][2] * inv, acc[db][3] * inv));
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, w), ro, qoff * 2 + db * 32 + grp * 8,
-                                                  0, 0);
-        }
+        for (int db = 0; db < D / 16; ++db) lean_store4<T>(ro, qoff * ES, db, grp, acc[db], inv);
         if (grp == 0)
             a.lse[b * a.ll.b + h * a.ll.h + pos1 * a.ll.s1 + pos2 * a.ll.s2] = (m + __log2f(lsum)) * kLn2;
     }
@@ -379,7 +489,7 @@ __device__ __forceinline__ void lean_redo_bwd_kv(const void* kargs, int pos1, in
 // Query tile of task x = (batch, tile, head), head fastest.
 template <typename T, int D, int NCH>
 __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) {
-    constexpr int NR = 2 * NCH + 6;
+    constexpr int NR = 2 * NCH + 6, NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
     unsigned char* smem = lds_base();
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + NR * 16 * D;
@@ -396,7 +506,7 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
     {
         const long long kvo = b * a.lk.b + hk * a.lk.h;
         lean_stage<T, D>(lean_rsrc(a.k + kvo, a.kbytes), lean_rsrc(a.v + kvo, a.kbytes), Ks, Vs,
-                         (ur0 * a.lk.s1 + uc0 * a.lk.s2) * 2, a.lk.s1 * a.d1 * 2, a.lk.s2 * a.d2 * 2, U1, U2, nst,
+                         (ur0 * a.lk.s1 + uc0 * a.lk.s2) * ES, a.lk.s1 * a.d1 * ES, a.lk.s2 * a.d2 * ES, U1, U2, nst,
                          wave, lane);
     }
     const int qr = 2 * wave + (col >> 3), qc = col & 7;
@@ -405,14 +515,14 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
     const int qoff = pos1 * a.lq.s1 + pos2 * a.lq.s2;
     const long long qbo = b * a.lq.b + h * a.lq.h;
     const long long lo = b * a.ll.b + h * a.ll.h + pos1 * a.ll.s1 + pos2 * a.ll.s2;
-    uint4 qf[D / 32], gf[D / 32], of[D / 32];
+    uint4 qf[NF], gf[NF], of[NF];
     {
         const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + qbo, a.qbytes);
         const __amdgpu_buffer_rsrc_t rg = lean_rsrc(a.dout + qbo, a.qbytes);
         const __amdgpu_buffer_rsrc_t ro = lean_rsrc(a.o + qbo, a.qbytes);
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) {
-            const uint32_t o = valid ? static_cast<uint32_t>(qoff * 2 + ks * 64 + grp * 16) : kLeanOOR;
+        for (int ks = 0; ks < NF; ++ks) {
+            const uint32_t o = valid ? static_cast<uint32_t>(qoff * ES + lean_frag_off<T, D>(ks, grp)) : kLeanOOR;
             qf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 0));
             gf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rg, o, 0, 0));
             of[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ro, o, 0, 0));
@@ -425,20 +535,20 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
     const int rlo = valid ? ((col >> 3) ? w1 : w0) - first : 1 << 20;
     f32x4_t cb[2];
     lean_colbias(sbyte(r[8], r[9], qc), a.K2, grp, cb);
-    int aoff[2][D / 32], toff[2][D / 16];
+    int aoff[2][NF], toff[TV][D / 16];
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) aoff[bb][ks] = lean_score_off<D>(first, col, grp, bb, ks);
+        for (int ks = 0; ks < NF; ++ks) aoff[bb][ks] = lean_score_off<T, D>(first, col, grp, bb, ks);
 #pragma unroll
-    for (int hi = 0; hi < 2; ++hi)
+    for (int hi = 0; hi < TV; ++hi)
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<D>(first, lane, hi, db);
+        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<T, D>(first, lane, hi, db);
 
-    // delta = dO . O: this lane's 8 head dims per 32, then the 4 lane rows
+    // delta = dO . O: this lane's head dims, then the 4 lane rows
     float di = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) di = dot8<T>(gf[ks], of[ks], di);
+    for (int ks = 0; ks < NF; ++ks) di = lean_dot<T>(gf[ks], of[ks], di);
     di = sum_rows(di) - dl;
     if (valid && grp == 0) a.delta[lo] = di;
     const f32x4_t nd = f32x4_t{-di, -di, -di, -di};
@@ -465,18 +575,13 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], a.sc2, off)) * dp[bb][i];
-        lean_accumulate<T, D>(Kb, toff, c, pack8<T>(s), acc);
+        lean_acc<T, D>(Kb, toff, c, s, acc);
     }
     const bool redo = valid && item_nonfinite(lane_sum(acc, 0.f));
     if (valid) {
         const __amdgpu_buffer_rsrc_t rd = lean_rsrc(a.dq + qbo, a.qbytes);
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db) {
-            const uint2 w = make_uint2(Mma<T>::pack(acc[db][0] * a.scale, acc[db][1] * a.scale),
-                                       Mma<T>::pack(acc[db][2] * a.scale, acc[db][3] * a.scale));
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, w), rd, qoff * 2 + db * 32 + grp * 8,
-                                                  0, 0);
-        }
+        for (int db = 0; db < D / 16; ++db) lean_store4<T>(rd, qoff * ES, db, grp, acc[db], a.scale);
     }
     if (redo) lean_redo_bwd_q<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, h, hk, grp);
 }
@@ -493,6 +598,7 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
 // A wave walks at most MAXC chunks (the host checks its rows fit).
 template <typename T, int D, int MAXC>
 __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x) {
+    constexpr int NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
     const int nr = a.nr;
     unsigned char* smem = lds_base();
     T* Qs = reinterpret_cast<T*>(smem);
@@ -518,10 +624,11 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
         if (valid) {
             const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.dk + kbo, a.kbytes);
             const __amdgpu_buffer_rsrc_t rv = lean_rsrc(a.dv + kbo, a.kbytes);
+            const f32x4_t z = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int db = 0; db < D / 16; ++db) {
-                __builtin_amdgcn_raw_buffer_store_b64(v2u32_t{0u, 0u}, rk, koff * 2 + db * 32 + grp * 8, 0, 0);
-                __builtin_amdgcn_raw_buffer_store_b64(v2u32_t{0u, 0u}, rv, koff * 2 + db * 32 + grp * 8, 0, 0);
+                lean_store4<T>(rk, koff * ES, db, grp, z, 1.f);
+                lean_store4<T>(rv, koff * ES, db, grp, z, 1.f);
             }
         }
         return;
@@ -539,16 +646,16 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     const float sl = a.lse[lbase + sp], sd = a.delta[lbase + sp];
     {
         lean_stage<T, D>(lean_rsrc(a.q + qo, a.qbytes), lean_rsrc(a.dout + qo, a.qbytes), Qs, Gs,
-                         (ur0 * a.lq.s1 + uc0 * a.lq.s2) * 2, a.lq.s1 * a.d1 * 2, a.lq.s2 * a.d2 * 2, U1, U2, nst,
+                         (ur0 * a.lq.s1 + uc0 * a.lq.s2) * ES, a.lq.s1 * a.d1 * ES, a.lq.s2 * a.d2 * ES, U1, U2, nst,
                          wave, lane);
     }
-    uint4 kf[D / 32], vf[D / 32];
+    uint4 kf[NF], vf[NF];
     {
         const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.k + kbo, a.kbytes);
         const __amdgpu_buffer_rsrc_t rv = lean_rsrc(a.v + kbo, a.kbytes);
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) {
-            const uint32_t o = valid ? static_cast<uint32_t>(koff * 2 + ks * 64 + grp * 16) : kLeanOOR;
+        for (int ks = 0; ks < NF; ++ks) {
+            const uint32_t o = valid ? static_cast<uint32_t>(koff * ES + lean_frag_off<T, D>(ks, grp)) : kLeanOOR;
             kf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, o, 0, 0));
             vf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, 0));
         }
@@ -564,15 +671,15 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     const int clo = sbyte(r[8], r[9], kc), chi = sbyte(r[12], r[13], kc);
     f32x4_t cb[2];
     lean_colbias(clo, chi >= clo ? chi - clo + 1 : 0, grp, cb);
-    int aoff[2][D / 32], toff[2][D / 16];
+    int aoff[2][NF], toff[TV][D / 16];
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) aoff[bb][ks] = lean_score_off<D>(first, col, grp, bb, ks);
+        for (int ks = 0; ks < NF; ++ks) aoff[bb][ks] = lean_score_off<T, D>(first, col, grp, bb, ks);
 #pragma unroll
-    for (int hi = 0; hi < 2; ++hi)
+    for (int hi = 0; hi < TV; ++hi)
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<D>(first, lane, hi, db);
+        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<T, D>(first, lane, hi, db);
 
     wait_loads();
     if (static_cast<int>(threadIdx.x) < nr * 16) {
@@ -619,8 +726,8 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
                 s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], a.sc2, nl[bb][i]));
                 dp[bb][i] *= s[bb][i];
             }
-        lean_accumulate<T, D>(Gb, toff, c, pack8<T>(s), gv);
-        lean_accumulate<T, D>(Qb, toff, c, pack8<T>(dp), gk);
+        lean_acc<T, D>(Gb, toff, c, s, gv);
+        lean_acc<T, D>(Qb, toff, c, dp, gk);
     }
     const bool redo = valid && item_nonfinite(lane_sum(gk, lane_sum(gv, 0.f)));
     if (valid) {
@@ -628,13 +735,8 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
         const __amdgpu_buffer_rsrc_t rv = lean_rsrc(a.dv + kbo, a.kbytes);
 #pragma unroll
         for (int db = 0; db < D / 16; ++db) {
-            const uint2 wk = make_uint2(Mma<T>::pack(gk[db][0] * a.scale, gk[db][1] * a.scale),
-                                        Mma<T>::pack(gk[db][2] * a.scale, gk[db][3] * a.scale));
-            const uint2 wv = make_uint2(Mma<T>::pack(gv[db][0], gv[db][1]), Mma<T>::pack(gv[db][2], gv[db][3]));
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, wk), rk, koff * 2 + db * 32 + grp * 8,
-                                                  0, 0);
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32_t, wv), rv, koff * 2 + db * 32 + grp * 8,
-                                                  0, 0);
+            lean_store4<T>(rk, koff * ES, db, grp, gk[db], a.scale);
+            lean_store4<T>(rv, koff * ES, db, grp, gv[db], 1.f);
         }
     }
     if (redo) lean_redo_bwd_kv<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, hk, grp);
@@ -802,7 +904,7 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_wsum_key(LeanWsumKeyAr
 #pragma unroll
     for (int hi = 0; hi < 2; ++hi)
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<D>(first, lane, hi, db);
+        for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<T, D>(first, lane, hi, db);
 
     const int d10 = r2[0], d11 = r2[1], d12 = r2[2], d13 = r2[3];  // d1 bytes of union rows 0-15
 
@@ -1042,10 +1144,11 @@ LeanLay lean_lay(const Lay& l) {
     return LeanLay{l.b, l.h, static_cast<int>(l.s1), static_cast<int>(l.s2)};
 }
 
-// Byte range of one (batch, head) plane of an operand of head dim D.
-uint32_t plane_bytes(const Prob& p, const Lay& l, int D) {
+// Byte range of one (batch, head) plane of an operand of head dim D
+// (elements of esz bytes).
+uint32_t plane_bytes(const Prob& p, const Lay& l, int D, int esz = 2) {
     const long long v = ((static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
-                         (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + D) * 2;
+                         (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + D) * esz;
     return static_cast<uint32_t>(v);
 }
 
@@ -1066,7 +1169,7 @@ void lean_audit_one(LdsAudit& a) {
     audit_one(k_lean_fwd<T, D, NCH>, "k_lean_fwd", a);
     audit_one(k_lean_bwd_q<T, D, NCH>, "k_lean_bwd_q", a);
     audit_one(k_lean_bwd_kv<T, D, NCH + 2>, "k_lean_bwd_kv", a);
-    audit_one(k_lean_wsum_key<T, D, NCH + 2>, "k_lean_wsum_key", a);
+    if constexpr (!kF32<T>) audit_one(k_lean_wsum_key<T, D, NCH + 2>, "k_lean_wsum_key", a);
 }
 
 template <typename T, int D>
@@ -1085,6 +1188,8 @@ const LdsAudit& lean_audit() {
         lean_audit_dim<bf16, 64>(a);
         lean_audit_dim<f16, 32>(a);
         lean_audit_dim<f16, 64>(a);
+        lean_audit_dim<float, 32>(a);
+        lean_audit_dim<float, 64>(a);
         return a;
     }();
     return result;
@@ -1102,8 +1207,7 @@ int lean_nch(int K1) { return (K1 + 2) / 2; }
 // 2^15, planes below 2^30 bytes, q/out and k/v sharing one layout each.
 bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list<Lay> qside,
                    std::initializer_list<Lay> kvside, std::initializer_list<Lay> rows) {
-    if (!lean_switch() || dtype == NATTEN_F32 || !aligned || !(p.scale > 0.f) || !lean_static_lds_ok())
-        return false;
+    if (!lean_switch() || !aligned || !(p.scale > 0.f) || !lean_static_lds_ok()) return false;
     if (p.Dqk != p.Dv || (p.Dqk != 32 && p.Dqk != 64)) return false;
     // 2-D: axis 0 padded; a short first axis (1-D problems) stays on the
     // general tiles, which lay a 1-D axis out along whole tiles
@@ -1116,7 +1220,8 @@ bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list
     for (const Lay& l : {*qside.begin(), *kvside.begin()}) {
         if (l.s1 < 0 || l.s2 < 0 || l.b < 0 || l.h < 0) return false;
         const long long v = ((static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
-                             (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + p.Dqk) * 2;
+                             (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + p.Dqk) *
+                            (dtype == NATTEN_F32 ? 4 : 2);
         if (v >= (1LL << 30)) return false;
     }
     // fp32 rows (lse, delta, dlse): in-plane element offsets in 31 bits
@@ -1154,14 +1259,17 @@ hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, 
     a.d2 = p.ax[2].dil;
     a.K1 = p.ax[1].k;
     a.K2 = p.ax[2].k;
-    a.qbytes = plane_bytes(p, lq, D);
-    a.kbytes = plane_bytes(p, lk, D);
+    a.qbytes = plane_bytes(p, lq, D, sizeof(T));
+    a.kbytes = plane_bytes(p, lk, D, sizeof(T));
     a.sc2 = p.scale * kLog2e;
     a.p = p;
     const long long blocks = static_cast<long long>(p.B) * p.Hq * g->ntiles;
     const size_t shm = kLdsPad + static_cast<size_t>(2) * (2 * NCH + 6) * 16 * D * sizeof(T);
-    NA_LAUNCH("na_fwd_lean", (k_lean_fwd<T, D, NCH>), dim3(static_cast<unsigned>(blocks)), dim3(64 * kLeanWaves), shm,
-              s, a);
+    if (shm > 160 * 1024) return hipErrorNotSupported;
+    auto kern = k_lean_fwd<T, D, NCH>;
+    const hipError_t e = allow_lds(kern, shm);
+    if (e != hipSuccess) return e;
+    NA_LAUNCH("na_fwd_lean", kern, dim3(static_cast<unsigned>(blocks)), dim3(64 * kLeanWaves), shm, s, a);
     return hipGetLastError();
 }
 
@@ -1187,6 +1295,10 @@ hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay
     if (dtype == NATTEN_BF16) {
         if (p.Dqk == 32) NA_LF_N(bf16, 32);
         NA_LF_N(bf16, 64);
+    }
+    if (dtype == NATTEN_F32) {
+        if (p.Dqk == 32) NA_LF_N(float, 32);
+        NA_LF_N(float, 64);
     }
     if (p.Dqk == 32) NA_LF_N(f16, 32);
     NA_LF_N(f16, 64);
@@ -1218,8 +1330,8 @@ LeanBwdArgs<T> lean_bwd_args(const Prob& p, const void* q, Lay lq, const void* k
     a.d2 = p.ax[2].dil;
     a.K1 = p.ax[1].k;
     a.K2 = p.ax[2].k;
-    a.qbytes = plane_bytes(p, lq, D);
-    a.kbytes = plane_bytes(p, lk, D);
+    a.qbytes = plane_bytes(p, lq, D, sizeof(T));
+    a.kbytes = plane_bytes(p, lk, D, sizeof(T));
     a.sc2 = p.scale * kLog2e;
     a.scale = p.scale;
     a.p = p;
@@ -1239,9 +1351,12 @@ hipError_t lean_bwd_run(const Prob& p, const LeanGeo* gq, const LeanGeo* gk, con
     const size_t shm_k =
         kLdsPad + static_cast<size_t>(a.nr) * 16 * (2 * D * sizeof(T) + 2 * sizeof(float)) + 8 * sizeof(float);
     const long long tasks = static_cast<long long>(p.B) * p.Hq * gq->ntiles;
-    NA_LAUNCH("na_bwd_q_lean", (k_lean_bwd_q<T, D, NCH>), dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves),
-              shm_q, s, a);
-    hipError_t e = hipGetLastError();
+    if (shm_q > 160 * 1024 || shm_k > 160 * 1024) return hipErrorNotSupported;
+    auto kq = k_lean_bwd_q<T, D, NCH>;
+    hipError_t e = allow_lds(kq, shm_q);
+    if (e != hipSuccess) return e;
+    NA_LAUNCH("na_bwd_q_lean", kq, dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves), shm_q, s, a);
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     auto kern = k_lean_bwd_kv<T, D, NCH + 2>;
     if ((e = allow_lds(kern, shm_k)) != hipSuccess) return e;
@@ -1283,6 +1398,10 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
     if (dtype == NATTEN_BF16) {
         if (p.Dqk == 32) NA_LB_N(bf16, 32);
         NA_LB_N(bf16, 64);
+    }
+    if (dtype == NATTEN_F32) {
+        if (p.Dqk == 32) NA_LB_N(float, 32);
+        NA_LB_N(float, 64);
     }
     if (p.Dqk == 32) NA_LB_N(f16, 32);
     NA_LB_N(f16, 64);

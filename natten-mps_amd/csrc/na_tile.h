@@ -629,9 +629,14 @@ __device__ __forceinline__ void store_rows(T* __restrict__ g, long long off, int
                                            float mul) {
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
-        const uint2 w = make_uint2(Mma<T>::pack(acc[db][0] * mul, acc[db][1] * mul),
-                                   Mma<T>::pack(acc[db][2] * mul, acc[db][3] * mul));
-        *reinterpret_cast<uint2*>(g + off + db * 16 + grp * 4) = w;
+        if constexpr (sizeof(T) == 4) {
+            *reinterpret_cast<float4*>(g + off + db * 16 + grp * 4) =
+                make_float4(acc[db][0] * mul, acc[db][1] * mul, acc[db][2] * mul, acc[db][3] * mul);
+        } else {
+            const uint2 w = make_uint2(Mma<T>::pack(acc[db][0] * mul, acc[db][1] * mul),
+                                       Mma<T>::pack(acc[db][2] * mul, acc[db][3] * mul));
+            *reinterpret_cast<uint2*>(g + off + db * 16 + grp * 4) = w;
+        }
     }
 }
 

@@ -41,7 +41,8 @@ def assert_parity(got: torch.Tensor, ref: torch.Tensor, dtype: torch.dtype, name
     b = ref.detach().float().cpu()
     assert a.shape == b.shape, f"{name}: shape {tuple(a.shape)} != {tuple(b.shape)}"
     if dtype == torch.float32:
-        torch.testing.assert_close(a, b, atol=FP32_TOL, rtol=FP32_TOL, msg=lambda m: f"{name}: {m}")
+        # NaN where the oracle has NaN (and Inf exactly where it has Inf)
+        torch.testing.assert_close(a, b, atol=FP32_TOL, rtol=FP32_TOL, equal_nan=True, msg=lambda m: f"{name}: {m}")
         return
     fa, fb = torch.isfinite(a), torch.isfinite(b)
     assert torch.equal(fa, fb), f"{name}: {int((fa != fb).sum())} elements differ in finiteness"

@@ -58,14 +58,15 @@ def test_mfma_kernels_have_no_static_lds():
     fused, global-key and variable-length instances at head dim 96, and
     2 dtypes x 4 head dims x 6 single-step (FLAT) fused instances, and the
     lean 2-D kernels: 2 dtypes x 2 head dims x 5 chunk counts x forward, dQ,
-    dK/dV and the split key side) reports 0 bytes of static LDS, so the operands the kernels
+    dK/dV and the split key side, and fp32 x 2 head dims x 5 chunk counts x
+    forward, dQ and dK/dV) reports 0 bytes of static LDS, so the operands the kernels
     stage at a constant LDS offset cannot overlap a __shared__ array; with
     one that did, the library would refuse the tile path."""
     from natten_mps_amd._core import _lib
 
     n = ctypes.c_int32(0)
     assert _lib.load().natten_hip_mfma_lds_check(ctypes.byref(n)) == 1
-    assert n.value == 2 * 3 * (18 + 4 + 6 + 16) + 2 * (18 + 4 + 6) + 2 * 4 * 6 + 2 * 2 * 5 * 4
+    assert n.value == 2 * 3 * (18 + 4 + 6 + 16) + 2 * (18 + 4 + 6) + 2 * 4 * 6 + 2 * 2 * 5 * 4 + 2 * 5 * 3
 
 
 # ---------------------------------------------------------------------------
@@ -136,6 +137,9 @@ NONFINITE_FUSED = [
     (2, (24, 24), 4, 2, 64, (5, 5), (2, 2), (11, 12), torch.float16),
     (3, (6, 12, 12), 2, 2, 32, (3, 5, 5), (1, 1, 2), (3, 6, 5), torch.bfloat16),
     (1, (200,), 4, 1, 64, (9,), (2,), (100,), torch.bfloat16),
+    # fp32 on the 2-D tile kernels
+    (2, (20, 22), 2, 2, 32, (7, 7), (1, 1), (9, 10), torch.float32),
+    (2, (18, 20), 2, 2, 64, (5, 3), (1, 2), (8, 9), torch.float32),
 ]
 
 
@@ -346,3 +350,44 @@ def test_host_binding_matches_ctypes_path(case, monkeypatch):
     x = torch.zeros((1, 6, 1, 32), device=DEV, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError):
         hip.forward_with_lse(1, x, x, x, (6,), (1,), (1,), (False,), None)
+
+
+# ---------------------------------------------------------------------------
+# fp32 on the 2-D tile kernels (v_mfma_f32_16x16x4_f32)
+# ---------------------------------------------------------------------------
+
+FP32_TILE = [
+    # spatial, heads, dim, kernel, dilation, causal, scale
+    ((32, 32), 4, 32, (7, 7), (1, 1), (False, False), None),
+    ((17, 23), 2, 32, (5, 7), (2, 3), (True, False), 0.3),
+    ((20, 16), 2, 64, (3, 5), (1, 2), (False, True), None),
+    ((40, 36), 1, 64, (7, 7), (2, 1), (False, True), 0.125),
+    ((9, 12), 3, 32, (4, 6), (1, 1), (False, False), None),
+]
+
+
+@pytest.mark.parametrize("case", FP32_TILE, ids=lambda c: f"{c[0]}-D{c[2]}-K{c[3]}-d{c[4]}-c{c[5]}")
+def test_fp32_on_2d_tile_kernels(case):
+    """fp32 2-D problems at head dim 32 / 64 run the 2-D tile kernels with
+    fp32 MFMA (forward, dQ, dK/dV launches named na_*_lean) and match the
+    oracle in fp32 within 1e-5 elementwise, odd and even kernels, dilation,
+    causal axes."""
+    from natten_mps_amd import functional as F
+
+    sp, heads, dim, ks, dil, causal, scale = case
+    q, k, v, do = _inputs(951, [(2, *sp, heads, dim)] * 4, torch.float32)
+    leaves = [x.to(DEV).requires_grad_(True) for x in (q, k, v)]
+
+    def run():
+        out = F.na2d(*leaves, kernel_size=ks, dilation=dil, is_causal=causal, scale=scale)
+        out.backward(do.to(DEV))
+        return out
+
+    out, ran = _launched(run)
+    assert {"na_fwd_lean", "na_bwd_q_lean", "na_bwd_kv_lean"} <= ran, ran
+    rl = [x.clone().requires_grad_(True) for x in (q, k, v)]
+    ref = P.forward(2, *rl, ks, (1, 1), dil, causal, scale)
+    ref.backward(do)
+    assert_parity(out, ref, torch.float32, "out")
+    for name, a, b in zip(("dq", "dk", "dv"), leaves, rl):
+        assert_parity(a.grad, b.grad, torch.float32, name)
