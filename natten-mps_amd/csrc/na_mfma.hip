@@ -1216,9 +1216,29 @@ size_t lds_bytes(Kind kind, int slots, int D) {
     return kLdsPad + (kind == kBackwardKV ? 2 * rows + (2 * static_cast<size_t>(slots) + 8) * 4 : 2 * rows);
 }
 
-void set_h_per(TileShape& ts, int per) {
+// Head chunks per group of the workgroup order (decode_block).  A 3-D
+// window (K0 > 1) takes groups of 2: with every head of a tile in a row the
+// K/V planes that neighbouring depth tiles share (all heads of a region)
+// outgrow an XCD's L2 before the next depth tile reads them, and the
+// kernels fetched 1.3-1.8x their compulsory bytes at config 5; in pairs
+// they fetch 1.03-1.04x, and the lse / delta rows are still written two
+// heads at a time.  Otherwise all chunks form one group (heads fastest).
+// NATTEN_HIP_HEAD_GROUP=g (a divisor of the chunk count) overrides (tuning).
+void set_h_per(const Prob& p, TileShape& ts, int per) {
+    static const int forced = [] {
+        const char* e = std::getenv("NATTEN_HIP_HEAD_GROUP");
+        return e ? std::atoi(e) : 0;
+    }();
     ts.h_per = per;
-    ts.hchunks = make_fastdiv(static_cast<uint32_t>((ts.nheads + per - 1) / per));
+    const int chunks = (ts.nheads + per - 1) / per;
+    ts.hchunks = make_fastdiv(static_cast<uint32_t>(chunks));
+    int g = chunks;
+    if (forced > 0 && chunks % forced == 0)
+        g = forced;
+    else if (forced <= 0 && p.ax[0].k > 1 && chunks >= 4 && chunks % 2 == 0)
+        g = 2;
+    ts.hg = make_fastdiv(static_cast<uint32_t>(g));
+    ts.hgroups = make_fastdiv(static_cast<uint32_t>(chunks / g));
 }
 
 // Largest box of the fused kernels' tiles: 64 items (4 waves) unless
@@ -1289,7 +1309,7 @@ bool choose_tile(const Prob& p, Kind kind, int D, TileShape& ts, size_t extra_ld
     };
     const auto finish = [&]() {
         ts.nheads = key_tile ? p.Hkv : p.Hq;
-        set_h_per(ts, 1);
+        set_h_per(p, ts, 1);
         ts.rep = make_fastdiv(static_cast<uint32_t>(p.rep));
         long long spatial = 1;
         for (int a = 0; a < 3; ++a) {
@@ -1370,7 +1390,7 @@ void fit_h_per(const Prob& p, TileShape& ts, long long resident) {
     const long long cells = spatial_tiles(p, ts) * p.B;
     long long per = forced > 0 ? forced : (cells * ts.nheads) / (4 * resident);
     per = std::max(1LL, std::min<long long>(per, ts.nheads));
-    set_h_per(ts, static_cast<int>(per));
+    set_h_per(p, ts, static_cast<int>(per));
 }
 
 // Per-tile geometry records, built on the host once per (device, tile kind,

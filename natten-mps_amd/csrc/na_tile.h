@@ -195,7 +195,21 @@ struct TileShape {
     int lenmod[3];
     int nheads, h_per;  // heads, and how many of them one workgroup runs
     FastDiv rep, hchunks, spatial, tiles[3], dil[3];
+    FastDiv hg, hgroups;  // head chunks per group (fastest), groups (slowest within a batch)
 };
+
+// Workgroup x (after the XCD remap) -> batch b, head chunk hc and spatial
+// tile s: head chunks vary fastest in groups of hg, then the spatial tile,
+// then the group, then the batch.  With hg = hchunks (one group) this is
+// heads fastest, then tiles, then batches.
+__device__ __forceinline__ void decode_block(const TileShape& ts, int x, int& b, int& hc, int& s) {
+    const int q1 = fdiv(x, ts.hg);
+    const int hl = x - q1 * static_cast<int>(ts.hg.d);
+    const int q2 = fdiv(q1, ts.spatial);
+    s = q1 - q2 * static_cast<int>(ts.spatial.d);
+    b = fdiv(q2, ts.hgroups);
+    hc = (q2 - b * static_cast<int>(ts.hgroups.d)) * static_cast<int>(ts.hg.d) + hl;
+}
 
 // Operand layout as the kernels take it: 64-bit batch and head strides, and
 // 32-bit strides inside one (batch, head) (the host checks the offsets fit).
@@ -282,14 +296,10 @@ __host__ __device__ inline void spatial_coords(const TileShape& ts, int s, int (
 template <bool KEY, bool VARLEN = false>
 __device__ __forceinline__ bool tile_geometry(const Prob& p, const TileShape& ts, const int* __restrict__ geo,
                                               int wave, Block& k, WaveGeo& g, const int* __restrict__ lens = nullptr) {
-    int x = xcd_block(blockIdx.x, gridDim.x);
-    int q = fdiv(x, ts.hchunks);
-    k.h0 = (x - q * static_cast<int>(ts.hchunks.d)) * ts.h_per;
+    int hc, s;
+    decode_block(ts, xcd_block(blockIdx.x, gridDim.x), k.b, hc, s);
+    k.h0 = hc * ts.h_per;
     k.h1 = min(k.h0 + ts.h_per, ts.nheads);
-    x = q;
-    q = fdiv(x, ts.spatial);
-    const int s = x - q * static_cast<int>(ts.spatial.d);
-    k.b = q;
     int vlen[3], vmod[3];
     if constexpr (VARLEN) {
         bool ok = true;
@@ -800,7 +810,8 @@ struct WsumArgs {
 // sample's extents in tile_geometry only.
 __device__ __forceinline__ bool varlen_view(const Prob& p0, const TileShape& ts0, const int* __restrict__ lens, int x,
                                             Prob& p, TileShape& ts) {
-    const int b = fdiv(fdiv(x, ts0.hchunks), ts0.spatial);
+    int b, hc, s;
+    decode_block(ts0, x, b, hc, s);
     p = p0;
     ts = ts0;
     bool ok = true;
@@ -822,13 +833,10 @@ __device__ __forceinline__ bool varlen_view(const Prob& p0, const TileShape& ts0
 template <bool KEY>
 __device__ __forceinline__ bool lane_position(const Prob& p, const TileShape& ts, int x, int wave, int col, int& b,
                                               int& h0, int& h1, int (&pos)[3]) {
-    int q = fdiv(x, ts.hchunks);
-    h0 = (x - q * static_cast<int>(ts.hchunks.d)) * ts.h_per;
+    int hc, s;
+    decode_block(ts, x, b, hc, s);
+    h0 = hc * ts.h_per;
     h1 = min(h0 + ts.h_per, ts.nheads);
-    x = q;
-    q = fdiv(x, ts.spatial);
-    const int s = x - q * static_cast<int>(ts.spatial.d);
-    b = q;
     int t[3], r[3];
     spatial_coords(ts, s, t, r);
     const int f = wave * 16 + col, s2 = ts.tshift[2], s1 = ts.tshift[1];
