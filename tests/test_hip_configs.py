@@ -9,7 +9,10 @@ affordable on the host:
 * cfg 4: batch item 0, the prefix of 2048 positions (a causal 1-D window never
   reaches forward, so a prefix is self-contained; dK/dV are compared where
   every contributing query lies in the prefix);
-* cfg 5: batch item 0, head 0 (heads are independent, Hq == Hkv).
+* cfg 5: batch item 0, head 0, and batch item 1, head 5 (heads are
+  independent, Hq == Hkv);
+* cfgs 3, 4, 5 at full size against the split composition (QK -> softmax ->
+  AV, other kernels), every batch item, head and position.
 
 Bounds: ``tests/_parity.py`` (bf16 within 2e-2 norm-wise relative with an
 elementwise guard, the oracle run in fp32 on the same bf16 inputs; fp32
@@ -167,3 +170,45 @@ def test_backward_is_bitwise_deterministic(cfg):
     for _ in range(4):
         for name, a, b in zip(("out", "dq", "dk", "dv"), step(), ref):
             assert torch.equal(a, b), f"{name}: {int((a != b).sum())} elements differ between runs"
+
+
+# Full-size check: the fused path against the split composition on the whole
+# problem.  The two share no kernel (fused forward/backward tile kernels
+# against the split QK / AV tile kernels, torch's softmax in fp32 between
+# them), so agreement over every batch item, head and position checks what
+# the sliced oracle comparisons above leave out.  The split path rounds its
+# logits and probabilities to bf16, so the bound is the half-precision one
+# with the fused result as reference.
+FULL = {
+    3: dict(shape=(16, 56, 56), hq=4, hkv=4, dim=32, ks=(7, 7), dil=(1, 1), causal=(False, False)),
+    4: dict(shape=(4, 16384), hq=8, hkv=2, dim=64, ks=(33,), dil=(1,), causal=(True,)),
+    5: dict(shape=(2, 16, 32, 32), hq=8, hkv=8, dim=64, ks=(3, 7, 7), dil=(1, 2, 2), causal=(False, False, False)),
+}
+
+
+@pytest.mark.parametrize("cfg", sorted(FULL))
+def test_full_size_fused_matches_split_composition(cfg):
+    from natten_mps_amd import functional as F
+
+    c = FULL[cfg]
+    rank = len(c["ks"])
+    B, sp = c["shape"][0], c["shape"][1:]
+    q, k, v, do = _seeded(cfg, [(B, *sp, c["hq"], c["dim"]), (B, *sp, c["hkv"], c["dim"]),
+                                (B, *sp, c["hkv"], c["dim"]), (B, *sp, c["hq"], c["dim"])], torch.bfloat16)
+    kw = dict(kernel_size=c["ks"], dilation=c["dil"], is_causal=c["causal"])
+    fn = {1: F.na1d, 2: F.na2d, 3: F.na3d}[rank]
+    out, grads = _run(fn, q, k, v, do, **kw)
+
+    rep = c["hq"] // c["hkv"]
+    leaves = [t.to(DEV).requires_grad_(True) for t in (q, k, v)]
+    kx, vx = (t.repeat_interleave(rep, dim=-2) if rep > 1 else t for t in leaves[1:])
+    qk = {1: F.na1d_qk, 2: F.na2d_qk, 3: F.na3d_qk}[rank]
+    av = {1: F.na1d_av, 2: F.na2d_av, 3: F.na3d_av}[rank]
+    logits = qk(leaves[0], kx, c["ks"], c["dil"], is_causal=c["causal"], scale=c["dim"] ** -0.5)
+    attn = torch.softmax(logits.float(), -1).to(torch.bfloat16)
+    ref = av(attn, vx, c["ks"], c["dil"], is_causal=c["causal"])
+    ref.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    assert_parity(ref.detach(), out, torch.bfloat16, f"cfg{cfg} split out")
+    for name, a, g in zip(("dq", "dk", "dv"), leaves, grads):
+        assert_parity(a.grad, g, torch.bfloat16, f"cfg{cfg} split {name}")
