@@ -344,33 +344,39 @@ def rpb_step(torch, steps, warmup):
                       "kernel_mean_us": kernels, "kernel_sum_us": round(sum(kernels.values()), 1)}), flush=True)
 
 
-def host_time_per_step(torch, rank, leaves, do, cfg, steps, cycles_per_ms):
+def host_time_per_step(torch, rank, leaves, do, cfg, steps, cycles_per_ms, blocks=5):
     """Host (CPU) time of the library's own work per eager step: the 'hip'
     backend's forward and backward hooks (argument checks, cached problem
-    and layouts, output allocation, the C call), timed on the host over
-    ``steps`` calls while the GPU is held behind a spin, so that no call
-    waits for the device.  torch's autograd engine is not included."""
-    from natten_mps_amd._core import hip
+    and layouts, output allocation, the C call), timed on the host in
+    ``blocks`` blocks of ``max(steps, 200)`` forward calls then as many
+    backward calls, each block while the GPU is held behind a spin so that no
+    call waits for the device; the median block of each.  torch's autograd
+    engine is not included."""
+    from natten_mps_amd._core import _lib, hip
 
+    steps = max(steps, 200)
     q, k, v = (t.detach() for t in leaves)
     ks, dil, causal = cfg["kernel"], cfg["dilation"], cfg["causal"]
     stride = (1,) * rank
     out, lse = hip.forward_with_lse(rank, q, k, v, ks, stride, dil, causal, None)
     hip.fused_backward(rank, do, q, k, v, out, lse, ks, dil, stride, causal, None)
+    fwd, bwd = [], []
+    for _ in range(blocks):
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int((steps * 0.05 + 20.0) * cycles_per_ms))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            hip.forward_with_lse(rank, q, k, v, ks, stride, dil, causal, None)
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            hip.fused_backward(rank, do, q, k, v, out, lse, ks, dil, stride, causal, None)
+        t2 = time.perf_counter()
+        fwd.append((t1 - t0) / steps * 1e6)
+        bwd.append((t2 - t1) / steps * 1e6)
     torch.cuda.synchronize()
-    torch.cuda._sleep(int((steps * 0.5 + 20.0) * cycles_per_ms))
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        hip.forward_with_lse(rank, q, k, v, ks, stride, dil, causal, None)
-    t1 = time.perf_counter()
-    for _ in range(steps):
-        hip.fused_backward(rank, do, q, k, v, out, lse, ks, dil, stride, causal, None)
-    t2 = time.perf_counter()
-    torch.cuda.synchronize()
-    from natten_mps_amd._core import _lib
-
-    return {"forward_us": round((t1 - t0) / steps * 1e6, 2), "backward_us": round((t2 - t1) / steps * 1e6, 2),
-            "step_us": round((t2 - t0) / steps * 1e6, 2),
+    f, b = sorted(fwd)[blocks // 2], sorted(bwd)[blocks // 2]
+    return {"forward_us": round(f, 2), "backward_us": round(b, 2), "step_us": round(f + b, 2),
+            "blocks": blocks, "calls_per_block": steps,
             "binding": "c++ (_natten_torch.so)" if _lib.binding() is not None else "ctypes"}
 
 

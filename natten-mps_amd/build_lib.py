@@ -66,7 +66,8 @@ def commands():
 
 
 def binding_commands():
-    """Compile and link commands of the torch host binding (g++, no HIP)."""
+    """Compile and link commands of the torch host binding (g++, host code
+    only: the HIP runtime headers, no device code)."""
     import sysconfig
 
     import torch
@@ -77,11 +78,14 @@ def binding_commands():
     abi = int(getattr(torch._C, "_GLIBCXX_USE_CXX11_ABI", True))
     inc = [f"-I{os.path.join(ROOT, 'include')}"] + [f"-isystem{p}" for p in E.include_paths()]
     inc.append(f"-isystem{sysconfig.get_paths()['include']}")
+    # torch's HIP headers (the caching allocator's empty tensor, the current
+    # stream) include the HIP runtime's
+    inc += ["-D__HIP_PLATFORM_AMD__", "-isystem/opt/rocm/include"]
     comp = [CXX, "-O2", "-std=c++17", "-fPIC", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
             f"-DTORCH_EXTENSION_NAME={BIND_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H", *inc, "-c", src, "-o", obj]
     tlib = E.library_paths()[0]
     link = [CXX, "-shared", obj, "-o", BIND, f"-L{os.path.dirname(LIB)}", "-lnatten_hip", "-Wl,-rpath,$ORIGIN",
-            f"-L{tlib}", "-lc10", "-ltorch_cpu", "-ltorch", "-ltorch_python"]
+            f"-L{tlib}", "-lc10", "-ltorch_cpu", "-ltorch", "-ltorch_python", "-ltorch_hip", "-lc10_hip"]
     return comp, link
 
 

@@ -7,18 +7,30 @@
 // A FusedCall holds what is fixed per call signature (shapes, strides,
 // dtype, parameters): the problem descriptor and the element-stride layouts
 // that hip.py computed once, and the output shapes.  forward / backward
-// allocate the outputs with ATen on the inputs' device and call
-// natten_hip_forward / natten_hip_backward on the stream given (the raw
-// hipStream_t of torch's current stream, passed by the caller).  Errors map
-// as in the ctypes path: invalid input -> ValueError, unsupported ->
+// allocate the outputs from torch's device caching allocator on the inputs'
+// device and call natten_hip_forward / natten_hip_backward on the stream
+// given (the raw hipStream_t of torch's current stream).  Errors map as in
+// the ctypes path: invalid input -> ValueError, unsupported ->
 // NotImplementedError, launch failure -> RuntimeError.
+//
+// fwd / bwd are the per-call entry of hip.py: they take the backend hook's
+// own arguments, build the signature key from the tensors' metadata and the
+// parameter sequences, and run the FusedCall registered for that key on
+// torch's current stream of the inputs' device; None when no call is
+// registered (hip.py then checks the arguments, builds the signature and
+// registers it) or when an argument needs hip.py's handling (a non-unit
+// innermost stride, lse / dlse that are not contiguous fp32, parameters that
+// are not sequences of ints).
 //
 // Reference: the backend hooks this serves are those the autograd factory
 // calls (autograd/_factory.py:37-38,66-67 of /root/reference/src/natten_mps).
 #include <torch/extension.h>
 
+#include <ATen/hip/EmptyTensor.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/core/impl/DeviceGuardImplInterface.h>
+#include <c10/hip/HIPCachingAllocator.h>
+#include <c10/hip/HIPStream.h>
 
 #include <cstring>
 #include <optional>
@@ -42,6 +54,26 @@ namespace {
 // Layout slots: forward q k v out lse; backward q k v out dO lse dlse dq dk dv delta.
 constexpr int kFwdLays = 5, kBwdLays = 11;
 
+// A device tensor from torch's caching allocator (no dispatcher round trip).
+at::Tensor alloc(at::IntArrayRef shape, at::ScalarType dt, const at::Device& d) {
+    return at::detail::empty_cuda(shape, dt, d, std::nullopt);
+}
+
+// Workspace from the caching allocator on the current device for one call:
+// given back when the call returns (or throws).  The block belongs to the
+// stream it was taken for, so the allocator hands it out again only to work
+// ordered after this call's kernels on that stream.
+struct Workspace {
+    void* ptr = nullptr;
+    Workspace(size_t bytes, hipStream_t s)
+        : ptr(bytes ? c10::hip::HIPCachingAllocator::raw_alloc_with_stream(bytes, s) : nullptr) {}
+    ~Workspace() {
+        if (ptr) c10::hip::HIPCachingAllocator::raw_delete(ptr);
+    }
+    Workspace(const Workspace&) = delete;
+    Workspace& operator=(const Workspace&) = delete;
+};
+
 struct FusedCall {
     natten_problem_t prob;
     std::vector<natten_layout_t> lay;
@@ -64,8 +96,8 @@ struct FusedCall {
         if (lay.size() != kFwdLays) throw pybind11::value_error("FusedCall.forward: not a forward signature");
         c10::OptionalDeviceGuard guard;
         if (current_index() != q.get_device()) guard.reset_device(q.device());
-        at::Tensor out = at::empty(out_shape, q.options());
-        at::Tensor lse = at::empty(lse_shape, q.options().dtype(at::kFloat));
+        at::Tensor out = alloc(out_shape, q.scalar_type(), q.device());
+        at::Tensor lse = alloc(lse_shape, at::kFloat, q.device());
         const int rc = natten_hip_forward(&prob, q.data_ptr(), &lay[0], k.data_ptr(), &lay[1], v.data_ptr(), &lay[2],
                                           out.data_ptr(), &lay[3], lse.data_ptr<float>(), &lay[4],
                                           reinterpret_cast<void*>(stream));
@@ -82,15 +114,18 @@ struct FusedCall {
         c10::OptionalDeviceGuard guard;
         if (current_index() != q.get_device()) guard.reset_device(q.device());
         // dq is zeroed where stride > 1 leaves positions that are not queries
-        at::Tensor dq = strided ? at::zeros(q.sizes(), q.options()) : at::empty(q.sizes(), q.options());
-        at::Tensor dk = at::empty(k.sizes(), k.options());
-        at::Tensor dv = at::empty(v.sizes(), v.options());
-        at::Tensor delta = at::empty(lse_shape, q.options().dtype(at::kFloat));
+        at::Tensor dq = alloc(q.sizes(), q.scalar_type(), q.device());
+        if (strided) dq.zero_();
+        at::Tensor dk = alloc(k.sizes(), k.scalar_type(), k.device());
+        at::Tensor dv = alloc(v.sizes(), v.scalar_type(), v.device());
+        int64_t rows = 1;
+        for (int64_t x : lse_shape) rows *= x;
+        const Workspace delta(static_cast<size_t>(rows) * sizeof(float), reinterpret_cast<hipStream_t>(stream));
         const float* dl = d_lse.has_value() ? d_lse->data_ptr<float>() : nullptr;
         const int rc = natten_hip_backward(
             &prob, q.data_ptr(), &lay[0], k.data_ptr(), &lay[1], v.data_ptr(), &lay[2], out.data_ptr(), &lay[3],
             d_out.data_ptr(), &lay[4], lse.data_ptr<float>(), &lay[5], dl, dl ? &lay[6] : nullptr, dq.data_ptr(),
-            &lay[7], dk.data_ptr(), &lay[8], dv.data_ptr(), &lay[9], delta.data_ptr<float>(), &lay[10],
+            &lay[7], dk.data_ptr(), &lay[8], dv.data_ptr(), &lay[9], static_cast<float*>(delta.ptr), &lay[10],
             reinterpret_cast<void*>(stream));
         if (rc != NATTEN_OK) raise_status(rc, "backward");
         return {dq, dk, dv};
@@ -100,6 +135,175 @@ struct FusedCall {
         return c10::impl::getDeviceGuardImpl(c10::DeviceType::CUDA)->getDevice().index();
     }
 };
+
+// ---------------------------------------------------------------------------
+// signature cache of the per-call entry
+// ---------------------------------------------------------------------------
+
+// The key: rank, each tensor's dtype, device, sizes and strides, the
+// parameter sequences and the scale argument, as 64-bit words.
+struct Key {
+    static constexpr int kMax = 160;
+    int64_t w[kMax];
+    int n = 0;
+    bool ok = true;
+
+    void put(int64_t x) {
+        if (n < kMax) w[n++] = x;
+        else ok = false;
+    }
+    // inner: the innermost stride must be 1; fp32c: fp32 and contiguous
+    void tensor(const at::Tensor& t, bool inner, bool fp32c = false) {
+        if (!t.defined() || !t.is_cuda()) {
+            ok = false;
+            return;
+        }
+        const int64_t d = t.dim();
+        put(static_cast<int64_t>(t.scalar_type()));
+        put(t.get_device());
+        put(d);
+        const auto sz = t.sizes(), st = t.strides();
+        for (int64_t i = 0; i < d; ++i) {
+            put(sz[i]);
+            put(st[i]);
+        }
+        if (inner && (d == 0 || st[d - 1] != 1)) ok = false;
+        if (fp32c && (t.scalar_type() != at::kFloat || !t.is_contiguous())) ok = false;
+    }
+    void ints(pybind11::handle h) {
+        PyObject* o = h.ptr();
+        if (!PyTuple_Check(o) && !PyList_Check(o)) {
+            ok = false;
+            return;
+        }
+        const Py_ssize_t len = PySequence_Fast_GET_SIZE(o);
+        put(len);
+        for (Py_ssize_t i = 0; i < len; ++i) {
+            PyObject* it = PySequence_Fast_GET_ITEM(o, i);
+            if (!PyLong_Check(it)) {
+                ok = false;
+                return;
+            }
+            const long long x = PyLong_AsLongLong(it);
+            if (x == -1 && PyErr_Occurred()) {
+                PyErr_Clear();
+                ok = false;
+                return;
+            }
+            put(x);
+        }
+    }
+    void scale(pybind11::handle h) {
+        PyObject* o = h.ptr();
+        if (o == Py_None) {
+            put(0);
+            put(0);
+        } else if (PyFloat_CheckExact(o)) {
+            const double x = PyFloat_AS_DOUBLE(o);
+            int64_t bits;
+            std::memcpy(&bits, &x, sizeof(bits));
+            put(1);
+            put(bits);
+        } else {
+            ok = false;
+        }
+    }
+    bool operator==(const Key& o) const { return n == o.n && std::memcmp(w, o.w, n * sizeof(int64_t)) == 0; }
+};
+
+struct Entry {
+    Key key;
+    FusedCall* call;
+    pybind11::object owner;
+};
+
+constexpr size_t kCacheMax = 64;
+std::vector<Entry> g_fwd, g_bwd;
+
+const FusedCall* find(const std::vector<Entry>& cache, const Key& k) {
+    if (!k.ok) return nullptr;
+    for (const Entry& e : cache)
+        if (e.key == k) return e.call;
+    return nullptr;
+}
+
+bool remember(std::vector<Entry>& cache, const Key& k, pybind11::object call) {
+    if (!k.ok) return false;
+    if (cache.size() >= kCacheMax) cache.clear();
+    cache.push_back(Entry{k, call.cast<FusedCall*>(), std::move(call)});
+    return true;
+}
+
+Key fwd_key(int64_t rank, const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, pybind11::handle ks,
+            pybind11::handle st, pybind11::handle dil, pybind11::handle causal, pybind11::handle scale) {
+    Key key;
+    key.put(rank);
+    key.tensor(q, true);
+    key.tensor(k, true);
+    key.tensor(v, true);
+    key.ints(ks);
+    key.ints(st);
+    key.ints(dil);
+    key.ints(causal);
+    key.scale(scale);
+    return key;
+}
+
+Key bwd_key(int64_t rank, const at::Tensor& dout, const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+            const at::Tensor& out, const at::Tensor& lse, pybind11::handle ks, pybind11::handle dil,
+            pybind11::handle st, pybind11::handle causal, pybind11::handle scale,
+            const std::optional<at::Tensor>& dlse) {
+    Key key;
+    key.put(rank);
+    key.tensor(q, true);
+    key.tensor(k, true);
+    key.tensor(v, true);
+    key.tensor(out, true);
+    key.tensor(dout, true);
+    key.tensor(lse, false, true);
+    if (dlse.has_value()) key.tensor(*dlse, false, true);
+    else key.put(-1);
+    key.ints(ks);
+    key.ints(dil);
+    key.ints(st);
+    key.ints(causal);
+    key.scale(scale);
+    return key;
+}
+
+int64_t current_stream(const at::Tensor& t) {
+    return reinterpret_cast<int64_t>(c10::hip::getCurrentHIPStream(t.get_device()).stream());
+}
+
+pybind11::object fwd(int64_t rank, const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, pybind11::handle ks,
+                     pybind11::handle st, pybind11::handle dil, pybind11::handle causal, pybind11::handle scale) {
+    const FusedCall* c = find(g_fwd, fwd_key(rank, q, k, v, ks, st, dil, causal, scale));
+    if (!c) return pybind11::none();
+    return pybind11::cast(c->forward(q, k, v, current_stream(q)));
+}
+
+bool fwd_register(int64_t rank, const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, pybind11::handle ks,
+                  pybind11::handle st, pybind11::handle dil, pybind11::handle causal, pybind11::handle scale,
+                  pybind11::object call) {
+    return remember(g_fwd, fwd_key(rank, q, k, v, ks, st, dil, causal, scale), std::move(call));
+}
+
+pybind11::object bwd(int64_t rank, const at::Tensor& dout, const at::Tensor& q, const at::Tensor& k,
+                     const at::Tensor& v, const at::Tensor& out, const at::Tensor& lse, pybind11::handle ks,
+                     pybind11::handle dil, pybind11::handle st, pybind11::handle causal, pybind11::handle scale,
+                     const std::optional<at::Tensor>& dlse) {
+    const FusedCall* c = find(g_bwd, bwd_key(rank, dout, q, k, v, out, lse, ks, dil, st, causal, scale, dlse));
+    if (!c) return pybind11::none();
+    return pybind11::cast(c->backward(q, k, v, out, dout, lse, dlse, current_stream(q)));
+}
+
+bool bwd_register(int64_t rank, const at::Tensor& dout, const at::Tensor& q, const at::Tensor& k,
+                  const at::Tensor& v, const at::Tensor& out, const at::Tensor& lse, pybind11::handle ks,
+                  pybind11::handle dil, pybind11::handle st, pybind11::handle causal, pybind11::handle scale,
+                  const std::optional<at::Tensor>& dlse, pybind11::object call) {
+    return remember(g_bwd, bwd_key(rank, dout, q, k, v, out, lse, ks, dil, st, causal, scale, dlse),
+                    std::move(call));
+}
 
 }  // namespace
 
@@ -111,4 +315,19 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
                             std::vector<int64_t>, bool>())
         .def("forward", &FusedCall::forward)
         .def("backward", &FusedCall::backward);
+    m.def("fwd", &fwd, "cached fused forward: (out, lse), or None when the signature is not registered");
+    m.def("fwd_register", &fwd_register, "register the FusedCall of a forward signature");
+    m.def("bwd", &bwd, "cached fused backward: (dq, dk, dv), or None when the signature is not registered");
+    m.def("bwd_register", &bwd_register, "register the FusedCall of a backward signature");
+    m.def("clear", [] {
+        g_fwd.clear();
+        g_bwd.clear();
+    }, "drop every registered signature");
+    // the cached objects hold Python references: release them before the
+    // interpreter's own teardown
+    auto atexit = pybind11::module_::import("atexit");
+    atexit.attr("register")(pybind11::cpp_function([] {
+        g_fwd.clear();
+        g_bwd.clear();
+    }));
 }

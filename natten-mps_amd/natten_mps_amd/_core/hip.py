@@ -188,6 +188,15 @@ def _fwd_sig(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale_valu
 
 
 def forward_with_lse(rank: int, q, k, v, kernel_size, stride, dilation, is_causal, scale):
+    b = _lib.binding()
+    if b is not None:
+        # the binding's own signature cache: the whole call in C++ when this
+        # signature was seen before (None otherwise, or when an argument
+        # needs the handling below)
+        r = b.fwd(rank, q, k, v, kernel_size, stride, dilation, is_causal, scale)
+        if r is not None:
+            return r
+        q0, k0, v0 = q, k, v
     q, k, v = _inner(q), _inner(k), _inner(v)
     scale_value = float(q.shape[-1] ** -0.5 if scale is None else scale)
     key = (rank, q.dtype, k.dtype, v.dtype, q.device, k.device, v.device, q.shape, q.stride(), k.shape,
@@ -200,6 +209,8 @@ def forward_with_lse(rank: int, q, k, v, kernel_size, stride, dilation, is_causa
             _FWD_CACHE.clear()
         _FWD_CACHE[key] = sig
     if sig.fast is not None:
+        if b is not None:
+            b.fwd_register(rank, q0, k0, v0, kernel_size, stride, dilation, is_causal, scale, sig.fast)
         return sig.fast.forward(q, k, v, _raw_stream(q.device))
     out = torch.empty(sig.out_shape, dtype=q.dtype, device=q.device)
     lse = torch.empty(sig.lse_shape, dtype=torch.float32, device=q.device)
@@ -236,6 +247,12 @@ def _bwd_sig(rank, d_out, q, k, v, out, lse, d_lse, kernel_size, stride, dilatio
 
 def fused_backward(rank: int, d_out, q, k, v, out, lse, kernel_size, dilation, stride, is_causal, scale,
                    d_lse=None):
+    b = _lib.binding()
+    if b is not None:
+        r = b.bwd(rank, d_out, q, k, v, out, lse, kernel_size, dilation, stride, is_causal, scale, d_lse)
+        if r is not None:
+            return r
+        given = (d_out, q, k, v, out, lse, d_lse)
     q, k, v, out, d_out = _inner(q), _inner(k), _inner(v), _inner(out), _inner(d_out)
     if lse.dtype != torch.float32 or not lse.is_contiguous():
         lse = lse.to(torch.float32).contiguous()
@@ -255,6 +272,10 @@ def fused_backward(rank: int, d_out, q, k, v, out, lse, kernel_size, dilation, s
             _BWD_CACHE.clear()
         _BWD_CACHE[key] = sig
     if sig.fast is not None:
+        if b is not None:
+            g_out, g_q, g_k, g_v, g_o, g_lse, g_dlse = given
+            b.bwd_register(rank, g_out, g_q, g_k, g_v, g_o, g_lse, kernel_size, dilation, stride, is_causal, scale,
+                           g_dlse, sig.fast)
         return sig.fast.backward(q, k, v, out, d_out, lse, d_lse, _raw_stream(q.device))
     dq = (torch.zeros if sig.strided else torch.empty)(q.shape, dtype=q.dtype, device=q.device)
     dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)

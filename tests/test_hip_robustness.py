@@ -352,6 +352,53 @@ def test_host_binding_matches_ctypes_path(case, monkeypatch):
         hip.forward_with_lse(1, x, x, x, (6,), (1,), (1,), (False,), None)
 
 
+def test_binding_signature_cache():
+    """The binding's own signature cache: a signature seen once runs wholly in
+    C++ afterwards (hip.py's caches stay empty) with the same bits; arguments
+    it does not take (a non-unit innermost stride, non-fp32 lse, a scale given
+    as an int) go through hip.py and still give the same results."""
+    from natten_mps_amd._core import _lib, hip
+
+    b = _lib.binding()
+    assert b is not None, "the host binding _natten_torch.so is not built"
+    rank, ks, st, dil, causal = 2, (5, 5), (1, 1), (1, 1), (False, False)
+    q, k, v, do = (x.to(DEV) for x in _inputs(907, [(2, 12, 20, 2, 32)] * 4, torch.bfloat16))
+    b.clear()
+    hip._FWD_CACHE.clear()
+    hip._BWD_CACHE.clear()
+    out, lse = hip.forward_with_lse(rank, q, k, v, ks, st, dil, causal, None)
+    grads = hip.fused_backward(rank, do, q, k, v, out, lse, ks, dil, st, causal, None)
+    assert len(hip._FWD_CACHE) == 1 and len(hip._BWD_CACHE) == 1
+    hip._FWD_CACHE.clear()
+    hip._BWD_CACHE.clear()
+    out2, lse2 = hip.forward_with_lse(rank, q, k, v, ks, st, dil, causal, None)
+    grads2 = hip.fused_backward(rank, do, q, k, v, out2, lse2, ks, dil, st, causal, None)
+    assert not hip._FWD_CACHE and not hip._BWD_CACHE, "the second call did not stay in the binding"
+    for name, a, c in zip(("out", "lse", "dq", "dk", "dv"), (out, lse, *grads), (out2, lse2, *grads2)):
+        assert torch.equal(a, c), name
+    # arguments the binding leaves to hip.py
+    wide = torch.empty((*q.shape[:-1], 64), dtype=q.dtype, device=DEV)
+    wide[..., ::2] = q
+    qs = wide[..., ::2]
+    assert qs.stride(-1) == 2
+    out3, lse3 = hip.forward_with_lse(rank, qs, k, v, ks, st, dil, causal, None)
+    assert torch.equal(out3, out) and torch.equal(lse3, lse)
+    grads3 = hip.fused_backward(rank, do, q, k, v, out, lse.double(), ks, dil, st, causal, None)
+    for name, a, c in zip(("dq", "dk", "dv"), grads, grads3):
+        assert torch.equal(a, c), name
+    out4, _ = hip.forward_with_lse(rank, q, k, v, ks, st, dil, causal, 1)
+    out5, _ = hip.forward_with_lse(rank, q, k, v, ks, st, dil, causal, 1.0)
+    assert torch.equal(out4, out5)
+    # a registered signature on another stream runs on that stream
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        out6, lse6 = hip.forward_with_lse(rank, q, k, v, ks, st, dil, causal, None)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(out6, out) and torch.equal(lse6, lse)
+
+
 # ---------------------------------------------------------------------------
 # fp32 on the 2-D tile kernels (v_mfma_f32_16x16x4_f32)
 # ---------------------------------------------------------------------------
