@@ -757,8 +757,13 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> 
 // of w[q][e(q, k)] x[q] (the dk of QK's backward with w = dattn, x = q; the
 // dv of AV's backward with w = attn, x = dO).  Key tiles as in k_lean_bwd_kv:
 // the union of the attending queries is staged, x rows by the 16-byte DMA
-// and each union query's row of w (KV entries) by 4-byte DMA into a slot
-// row of P words (the words that hold the row's entries), rows after rows.  In class coordinates
+// (16 slots per union row) and each union query's row of w (KV entries) by
+// 16-byte DMA into a slot row of N16 16-byte chunks (UW slots per union
+// row, UW the widest union of the problem): the row's window of P words (the words that
+// hold its entries, 4P >= 16 bytes) in chunks 0 .. N16-2 at 16-byte steps
+// and the last chunk ending where the window ends, so no read leaves the
+// window (the last chunk overlaps the one before it by `sh` entries, which
+// the gather skips for entries past chunk N16-2).  In class coordinates
 // e(q, k) = (J1(k) - ws1(q)) K2 + (J2(k) - ws2(q)); the host tables d1[u] =
 // J1(first key) - ws1(union row u) and d2[u] (per union column) make it
 // (d1[u1] + kr) K2 + (d2[u2] + kc) for the lane's key (kr, kc), and the pair
@@ -775,7 +780,9 @@ struct LeanWsumKeyArgs {
     T* out;
     LeanLay lw, lx, lo;
     FastDiv heads, tiles;
-    FastDiv P;                    // words per staged w row
+    FastDiv N16;                  // 16-byte chunks per staged w row
+    FastDiv UW;                   // w slot rows per union row (the widest union)
+    int wwin;                     // bytes of a w row's window (4P)
     int nr;                       // LDS rows
     int d1, d2, K1, K2;
     uint32_t xbytes, wbytes;      // byte ranges of one (batch, head) plane of x and of w
@@ -823,7 +830,7 @@ __device__ __forceinline__ void lean_stage1(__amdgpu_buffer_rsrc_t ra, T* Xa, in
 
 template <typename T, int D, int MAXC>
 __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_wsum_key(LeanWsumKeyArgs<T> a) {
-    const int nr = a.nr, P = static_cast<int>(a.P.d);
+    const int nr = a.nr, N16 = static_cast<int>(a.N16.d);
     unsigned char* smem = lds_base();
     T* Xs = reinterpret_cast<T*>(smem);
     uint32_t* Ws32 = reinterpret_cast<uint32_t*>(Xs + nr * 16 * D);
@@ -856,35 +863,39 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_wsum_key(LeanWsumKeyAr
     const long long xo = b * a.lx.b + h * a.lx.h;
     lean_stage1<T, D>(lean_rsrc(a.x + xo, a.xbytes), Xs, (ur0 * a.lx.s1 + uc0 * a.lx.s2) * 2, a.lx.s1 * a.d1 * 2,
                       a.lx.s2 * a.d2 * 2, U1, U2, nst, wave, lane);
-    // w rows of the union: slot s = 16 u + cc at word s P, the words one
-    // after another; word t of the block goes to lane t % 64 of the DMA
-    // instruction t / 64 (rows and columns past the union load nothing
-    // useful: the tables mask them)
+    // w rows of the union: slot s = UW u + cc at byte 16 N16 s, chunk k of
+    // the slot's window at byte 16 k (the last at wwin - 16); chunk t of the
+    // block goes to lane t % 64 of the DMA instruction t / 64 (rows and
+    // columns past the union load nothing useful: the tables mask them)
     const T* wplane = a.w + b * a.lw.b + h * a.lw.h;
     const int lead = static_cast<int>((reinterpret_cast<uintptr_t>(wplane) >> 1) & 1);
     {
         const __amdgpu_buffer_rsrc_t rw = lean_rsrc(wplane - lead, a.wbytes);
         const int rs = a.lw.s1 * a.d1 * 2, cs = a.lw.s2 * a.d2 * 2;  // bytes between union rows / columns
         const int rbase = (ur0 * a.lw.s1 + uc0 * a.lw.s2) * 2;
-        const int total = U1 * 16 * P;
+        const int uw = static_cast<int>(a.UW.d);
+        const int total = U1 * uw * N16;
 #pragma unroll 1
         for (int t0 = wave * 64; t0 < total; t0 += 64 * kLeanWaves) {
             const int t = t0 + lane;
-            const int slot = fdiv(t, a.P);
-            const int k = t - slot * P, u = slot >> 4, cc = slot & 15;
-            const uint32_t o = (t < total && cc < U2) ? static_cast<uint32_t>(rbase + u * rs + cc * cs + k * 4)
+            const int slot = fdiv(t, a.N16);
+            const int k = t - slot * N16, u = fdiv(slot, a.UW), cc = slot - u * uw;
+            const int cb = k == N16 - 1 ? a.wwin - 16 : k * 16;
+            const uint32_t o = (t < total && cc < U2) ? static_cast<uint32_t>(rbase + u * rs + cc * cs + cb)
                                                       : kLeanOOR;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t*)(Ws32 + t0), 4, o, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t*)(Ws32 + 4 * t0), 16, o, 0, 0, 0);
         }
     }
     // the wave's union rows [first, last] (of the key record)
     const int first = __builtin_amdgcn_readfirstlane(sbyte(r[6], r[7], 2 * wave));
     const int last = __builtin_amdgcn_readfirstlane(sbyte(r[10], r[11], 2 * wave + 1));
     const int nch = (last - first + 2) >> 1;
-    // the lane's 8 slots of a chunk: union columns 8 (g % 2) + j; entry
-    // offsets (in 16-bit entries from the slot row 16 u1 + 8 (g % 2)) and
-    // the column masks, two entries per word
-    const int pe = 2 * P;  // entries per slot row
+    // the lane's 8 slots of a chunk: union columns 8 (g % 2) + j; window
+    // entry offsets lead + e2 of the lane's key column and the column masks,
+    // two entries per word.  A window entry ew sits at entry ew of the slot
+    // row, or ew + sh from entry thr on (the last chunk's shift).
+    const int pe = 8 * N16;                       // entries per slot row
+    const int thr = 8 * (N16 - 1), sh = (16 * N16 - a.wwin) >> 1;
     int cp[8];
     uint32_t cm[4];
     {
@@ -892,7 +903,7 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_wsum_key(LeanWsumKeyAr
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int e2 = sbyte(t0, t1, j) + kc;
-            cp[j] = j * pe + lead + e2;
+            cp[j] = lead + e2;
             const uint32_t ok = static_cast<unsigned>(e2) < static_cast<unsigned>(a.K2) ? 0xFFFFu : 0u;
             if (j & 1)
                 cm[j >> 1] |= ok << 16;
@@ -926,12 +937,13 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_wsum_key(LeanWsumKeyAr
         const int u1 = (grp >> 1) ? ub : ua;
         const int e1 = ((grp >> 1) ? dbb : da) + kr;
         const bool rok = valid && static_cast<unsigned>(e1) < static_cast<unsigned>(a.K1);
-        const int rowpart = (u1 * 16 + 8 * (grp & 1)) * pe + e1 * a.K2;
+        const int rowpart = (u1 * static_cast<int>(a.UW.d) + 8 * (grp & 1)) * pe, eo = e1 * a.K2;
         uint32_t wv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t lo16 = Ws[rowpart + cp[2 * i]];
-            const uint32_t hi16 = Ws[rowpart + cp[2 * i + 1]];
+            const int ea = eo + cp[2 * i], eb = eo + cp[2 * i + 1];
+            const uint32_t lo16 = Ws[rowpart + 2 * i * pe + ea + (ea >= thr ? sh : 0)];
+            const uint32_t hi16 = Ws[rowpart + (2 * i + 1) * pe + eb + (eb >= thr ? sh : 0)];
             wv[i] = rok ? ((lo16 | (hi16 << 16)) & cm[i]) : 0u;
         }
         lean_accumulate<T, D>(Xb, toff, c, make_uint4(wv[0], wv[1], wv[2], wv[3]), acc);
@@ -963,7 +975,7 @@ struct LeanGeo {
     int dev, key;
     int len[2], k[2], dil[2], causal[2];
     int* ptr;
-    int ntiles, nst_max, rows_max;
+    int ntiles, nst_max, rows_max, u2_max;
     std::vector<int> host;  // source of the asynchronous upload, kept with the table
     TableUpload up;
 };
@@ -1055,7 +1067,7 @@ const LeanGeo* lean_geometry(const Prob& p, int mode, int nch, hipStream_t s) {
     if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
     const Axis &A1 = p.ax[1], &A2 = p.ax[2];
     std::vector<int> h;
-    int nst_max = 0, rows_max = 0;
+    int nst_max = 0, rows_max = 0, u2_max = 1;
     for (int r1 = 0; r1 < A1.dil; ++r1) {
         const int n1 = (A1.len - r1 + A1.dil - 1) / A1.dil;
         for (int r2 = 0; r2 < A2.dil; ++r2) {
@@ -1080,6 +1092,7 @@ const LeanGeo* lean_geometry(const Prob& p, int mode, int nch, hipStream_t s) {
                         }
                         nst = std::max(nst, a1.U);
                         nst_max = std::max(nst_max, nst);
+                        u2_max = std::max(u2_max, a2.U);
                         rec[0] = a1.pos0;
                         rec[1] = a2.pos0;
                         rec[2] = a1.upos0;
@@ -1136,6 +1149,7 @@ const LeanGeo* lean_geometry(const Prob& p, int mode, int nch, hipStream_t s) {
     e->ntiles = static_cast<int>(e->host.size() / per_tile);
     e->nst_max = nst_max;
     e->rows_max = rows_max;
+    e->u2_max = u2_max;
     cache.push_back(e);
     return e;
 }
@@ -1411,12 +1425,14 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
 
 // Split ops, key side, on the 8x8 key tiles: eligibility beyond the general
 // lean checks -- one head count, w's row strides even (one 2-byte phase of
-// the w rows per (batch, head)), w's plane below 2^30 bytes.
+// the w rows per (batch, head)), w's plane below 2^30 bytes, at least 6
+// window entries (one 16-byte chunk per w row).
 bool lean_wsum_key_eligible(const Prob& p, int dtype, int D, bool aligned, const Lay& lw, const Lay& lx,
                             const Lay& lo) {
     if (!lean_switch() || dtype == NATTEN_F32 || !aligned || !lean_static_lds_ok()) return false;
     if (p.Hq != p.Hkv || (D != 32 && D != 64)) return false;
     if (p.ax[0].len != 1 || p.ax[0].k != 1 || p.ax[1].len < 8) return false;
+    if (p.kv < 6) return false;  // a w row's window is staged in 16-byte chunks
     for (int a = 1; a < 3; ++a) {
         const Axis& A = p.ax[a];
         if (A.st != 1 || A.k > 9 || A.len >= (1 << 15)) return false;
@@ -1447,7 +1463,11 @@ hipError_t lean_wsum_key_run(const char* name, const Prob& p, const LeanGeo* g, 
     a.tiles = make_fastdiv(g->ntiles);
     a.nr = std::max(g->nst_max, 1);
     const int P = (p.kv + 2) / 2;  // words of a row with its 2-byte phase
-    a.P = make_fastdiv(P);
+    const int n16 = (4 * P + 15) / 16;
+    if (4 * P < 16) return hipErrorNotSupported;  // a window shorter than one chunk
+    a.N16 = make_fastdiv(n16);
+    a.UW = make_fastdiv(g->u2_max);
+    a.wwin = 4 * P;
     a.d1 = p.ax[1].dil;
     a.d2 = p.ax[2].dil;
     a.K1 = p.ax[1].k;
@@ -1458,11 +1478,15 @@ hipError_t lean_wsum_key_run(const char* name, const Prob& p, const LeanGeo* g, 
     a.wbytes = static_cast<uint32_t>((wb + 3) & ~3LL);
     a.mul = mul;
     a.p = p;
-    // x rows, w slot rows (the DMA's last instruction may write up to 63
-    // words past them), and room for the gather's masked reads past the last
-    // slot row: at most (K1 + 6) K2 + K2 + 7 entries from a slot's start
-    const size_t over = std::max<size_t>(63 * 4, (static_cast<size_t>(p.ax[1].k + 7) * p.ax[2].k + 8) * 2);
-    const size_t shm = kLdsPad + static_cast<size_t>(a.nr) * 16 * (D * sizeof(T) + P * 4) + over;
+    // x rows (16 slots per union row), w slot rows (UW per union row; the
+    // DMA's last instruction may write up to 63 chunks past them), and room
+    // for the gather's masked reads past the last slot row: up to 16 - UW
+    // slots of the last union row, at most (K1 + 6) K2 + K2 + 7 entries from
+    // a slot's start plus the last chunk's shift (under 8 entries)
+    const size_t over = std::max<size_t>(
+        63 * 16, static_cast<size_t>(16 - g->u2_max) * n16 * 16 +
+                     (static_cast<size_t>(p.ax[1].k + 7) * p.ax[2].k + 16) * 2);
+    const size_t shm = kLdsPad + static_cast<size_t>(a.nr) * (16 * D * sizeof(T) + g->u2_max * n16 * 16) + over;
     if (shm > 160 * 1024) return hipErrorNotSupported;
     auto kern = k_lean_wsum_key<T, D, MAXC>;
     hipError_t e = allow_lds(kern, shm);
