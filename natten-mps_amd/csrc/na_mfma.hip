@@ -1428,7 +1428,17 @@ hipError_t table_upload(TableUpload& u, void* d, const void* h, size_t bytes, hi
 }
 
 bool table_ready(TableUpload& u, hipStream_t s) {
-    if (u.done || s == u.stream) return true;
+    if (u.done) return true;
+    // Under capture the upload's event is neither queried nor waited on (a
+    // graph may be replayed on any stream, after any amount of other work):
+    // until an ordinary call has seen the upload complete, a captured launch
+    // declines the table and its kernels compute the geometry themselves.
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    if (st != hipStreamCaptureStatusNone) return false;
     const hipError_t q = hipEventQuery(u.ev);
     if (q == hipSuccess) {
         u.done = true;
@@ -1438,8 +1448,7 @@ bool table_ready(TableUpload& u, hipStream_t s) {
         (void)hipGetLastError();
         return false;
     }
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return false;
+    if (s == u.stream) return true;  // stream order covers the copy
     return hipStreamWaitEvent(s, u.ev, 0) == hipSuccess;
 }
 
