@@ -1,7 +1,8 @@
-// Host binding of the fused forward / backward for the 'hip' backend: the
-// per-call work of natten_mps_amd/_core/hip.py (output allocation, the C
-// call, the status check) in C++ on top of the C ABI, so an eager step pays
-// a few microseconds of host time instead of the ctypes marshalling of ten to
+// Host binding of the fused forward / backward and of the split QK / AV ops
+// (and their backward) for the 'hip' backend: the per-call work of
+// natten_mps_amd/_core/hip.py (output allocation, the C call, the status
+// check) in C++ on top of the C ABI, so an eager call pays a few
+// microseconds of host time instead of the ctypes marshalling of ten to
 // twenty arguments and one torch allocation per output from Python.
 //
 // A FusedCall holds what is fixed per call signature (shapes, strides,
@@ -13,17 +14,21 @@
 // the ctypes path: invalid input -> ValueError, unsupported ->
 // NotImplementedError, launch failure -> RuntimeError.
 //
-// fwd / bwd are the per-call entry of hip.py: they take the backend hook's
-// own arguments, build the signature key from the tensors' metadata and the
-// parameter sequences, and run the FusedCall registered for that key on
-// torch's current stream of the inputs' device; None when no call is
+// SplitCall does the same for the four split ops (qk, av, qk_bwd, av_bwd).
+//
+// fwd / bwd (and qk / av / qk_bwd / av_bwd) are the per-call entry of
+// hip.py: they take the backend hook's own arguments, build the signature
+// key from the tensors' metadata and the parameter sequences, and run the
+// call object registered for that key on torch's current stream of the
+// inputs' device; None when no call is
 // registered (hip.py then checks the arguments, builds the signature and
 // registers it) or when an argument needs hip.py's handling (a non-unit
 // innermost stride, lse / dlse that are not contiguous fp32, parameters that
 // are not sequences of ints).
 //
 // Reference: the backend hooks this serves are those the autograd factory
-// calls (autograd/_factory.py:37-38,66-67 of /root/reference/src/natten_mps).
+// calls (autograd/_factory.py:37-38,66-67 of /root/reference/src/natten_mps)
+// and the split ops' forward and backward hooks (_core/ops.py:98-152).
 #include <torch/extension.h>
 
 #include <ATen/hip/EmptyTensor.h>
@@ -136,6 +141,88 @@ struct FusedCall {
     }
 };
 
+// The split ops (QK, AV and their backward), as FusedCall: the problem and
+// layouts of one call signature, fixed.  Layout slots: QK q k attn; AV attn v
+// out; QK backward dattn q k dq dk; AV backward dout attn v dattn dv.
+enum SplitOp { kQk = 0, kAv = 1, kQkBwd = 2, kAvBwd = 3 };
+constexpr size_t kSplitLays[4] = {3, 3, 5, 5};
+
+struct SplitCall {
+    int op;
+    natten_problem_t prob;
+    std::vector<natten_layout_t> lay;
+    std::vector<int64_t> out_shape;  // QK: attn; AV: out
+    bool zero_dq;                    // QK backward: dq zeroed where strides leave non-query positions
+
+    SplitCall(int op_, const pybind11::bytes& prob_bytes, const pybind11::bytes& lay_bytes,
+              std::vector<int64_t> out_shape_, bool zero_dq_)
+        : op(op_), out_shape(std::move(out_shape_)), zero_dq(zero_dq_) {
+        const std::string p = prob_bytes, l = lay_bytes;
+        if (op < kQk || op > kAvBwd) throw pybind11::value_error("SplitCall: unknown op");
+        if (p.size() != sizeof(natten_problem_t)) throw pybind11::value_error("SplitCall: problem size mismatch");
+        if (l.size() != kSplitLays[op] * sizeof(natten_layout_t))
+            throw pybind11::value_error("SplitCall: layout size mismatch");
+        std::memcpy(&prob, p.data(), sizeof(prob));
+        lay.resize(kSplitLays[op]);
+        std::memcpy(lay.data(), l.data(), l.size());
+    }
+
+    void want(int o) const {
+        if (op != o) throw pybind11::value_error("SplitCall: called as another op");
+    }
+
+    at::Tensor qk(const at::Tensor& q, const at::Tensor& k, int64_t stream) const {
+        want(kQk);
+        c10::OptionalDeviceGuard guard;
+        if (FusedCall::current_index() != q.get_device()) guard.reset_device(q.device());
+        at::Tensor attn = alloc(out_shape, q.scalar_type(), q.device());
+        const int rc = natten_hip_qk_forward(&prob, q.data_ptr(), &lay[0], k.data_ptr(), &lay[1], attn.data_ptr(),
+                                             &lay[2], reinterpret_cast<void*>(stream));
+        if (rc != NATTEN_OK) raise_status(rc, "qk_forward");
+        return attn;
+    }
+
+    at::Tensor av(const at::Tensor& attn, const at::Tensor& v, int64_t stream) const {
+        want(kAv);
+        c10::OptionalDeviceGuard guard;
+        if (FusedCall::current_index() != v.get_device()) guard.reset_device(v.device());
+        at::Tensor out = alloc(out_shape, v.scalar_type(), v.device());
+        const int rc = natten_hip_av_forward(&prob, attn.data_ptr(), &lay[0], v.data_ptr(), &lay[1], out.data_ptr(),
+                                             &lay[2], reinterpret_cast<void*>(stream));
+        if (rc != NATTEN_OK) raise_status(rc, "av_forward");
+        return out;
+    }
+
+    std::tuple<at::Tensor, at::Tensor> qk_backward(const at::Tensor& da, const at::Tensor& q, const at::Tensor& k,
+                                                   int64_t stream) const {
+        want(kQkBwd);
+        c10::OptionalDeviceGuard guard;
+        if (FusedCall::current_index() != q.get_device()) guard.reset_device(q.device());
+        at::Tensor dq = alloc(q.sizes(), q.scalar_type(), q.device());
+        if (zero_dq) dq.zero_();
+        at::Tensor dk = alloc(k.sizes(), k.scalar_type(), k.device());
+        const int rc = natten_hip_qk_backward(&prob, da.data_ptr(), &lay[0], q.data_ptr(), &lay[1], k.data_ptr(),
+                                              &lay[2], dq.data_ptr(), &lay[3], dk.data_ptr(), &lay[4],
+                                              reinterpret_cast<void*>(stream));
+        if (rc != NATTEN_OK) raise_status(rc, "qk_backward");
+        return {dq, dk};
+    }
+
+    std::tuple<at::Tensor, at::Tensor> av_backward(const at::Tensor& dout, const at::Tensor& attn,
+                                                   const at::Tensor& v, int64_t stream) const {
+        want(kAvBwd);
+        c10::OptionalDeviceGuard guard;
+        if (FusedCall::current_index() != v.get_device()) guard.reset_device(v.device());
+        at::Tensor da = alloc(attn.sizes(), attn.scalar_type(), attn.device());
+        at::Tensor dv = alloc(v.sizes(), v.scalar_type(), v.device());
+        const int rc = natten_hip_av_backward(&prob, dout.data_ptr(), &lay[0], attn.data_ptr(), &lay[1],
+                                              v.data_ptr(), &lay[2], da.data_ptr(), &lay[3], dv.data_ptr(), &lay[4],
+                                              reinterpret_cast<void*>(stream));
+        if (rc != NATTEN_OK) raise_status(rc, "av_backward");
+        return {da, dv};
+    }
+};
+
 // ---------------------------------------------------------------------------
 // signature cache of the per-call entry
 // ---------------------------------------------------------------------------
@@ -211,27 +298,37 @@ struct Key {
     bool operator==(const Key& o) const { return n == o.n && std::memcmp(w, o.w, n * sizeof(int64_t)) == 0; }
 };
 
+template <typename C>
 struct Entry {
     Key key;
-    FusedCall* call;
+    C* call;
     pybind11::object owner;
 };
 
 constexpr size_t kCacheMax = 64;
-std::vector<Entry> g_fwd, g_bwd;
+std::vector<Entry<FusedCall>> g_fwd, g_bwd;
+std::vector<Entry<SplitCall>> g_split[4];
 
-const FusedCall* find(const std::vector<Entry>& cache, const Key& k) {
+template <typename C>
+const C* find(const std::vector<Entry<C>>& cache, const Key& k) {
     if (!k.ok) return nullptr;
-    for (const Entry& e : cache)
+    for (const Entry<C>& e : cache)
         if (e.key == k) return e.call;
     return nullptr;
 }
 
-bool remember(std::vector<Entry>& cache, const Key& k, pybind11::object call) {
+template <typename C>
+bool remember(std::vector<Entry<C>>& cache, const Key& k, pybind11::object call) {
     if (!k.ok) return false;
     if (cache.size() >= kCacheMax) cache.clear();
-    cache.push_back(Entry{k, call.cast<FusedCall*>(), std::move(call)});
+    cache.push_back(Entry<C>{k, call.cast<C*>(), std::move(call)});
     return true;
+}
+
+void clear_all() {
+    g_fwd.clear();
+    g_bwd.clear();
+    for (auto& c : g_split) c.clear();
 }
 
 Key fwd_key(int64_t rank, const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, pybind11::handle ks,
@@ -305,10 +402,69 @@ bool bwd_register(int64_t rank, const at::Tensor& dout, const at::Tensor& q, con
                     std::move(call));
 }
 
+// Split ops: the key of op `op` over its input tensors (every one with a
+// unit innermost stride), the parameter sequences and the scale argument
+// (None for AV and its backward).
+Key split_key(int op, int64_t rank, std::initializer_list<const at::Tensor*> ts, pybind11::handle ks,
+              pybind11::handle dil, pybind11::handle st, pybind11::handle causal, pybind11::handle scale) {
+    Key key;
+    key.put(op);
+    key.put(rank);
+    for (const at::Tensor* t : ts) key.tensor(*t, true);
+    key.ints(ks);
+    key.ints(dil);
+    key.ints(st);
+    key.ints(causal);
+    key.scale(scale);
+    return key;
+}
+
+pybind11::object qk(int64_t rank, const at::Tensor& q, const at::Tensor& k, pybind11::handle ks, pybind11::handle dil,
+                    pybind11::handle st, pybind11::handle causal, pybind11::handle scale) {
+    const SplitCall* c = find(g_split[kQk], split_key(kQk, rank, {&q, &k}, ks, dil, st, causal, scale));
+    if (!c) return pybind11::none();
+    return pybind11::cast(c->qk(q, k, current_stream(q)));
+}
+
+pybind11::object av(int64_t rank, const at::Tensor& attn, const at::Tensor& v, pybind11::handle ks,
+                    pybind11::handle dil, pybind11::handle st, pybind11::handle causal) {
+    const SplitCall* c =
+        find(g_split[kAv], split_key(kAv, rank, {&attn, &v}, ks, dil, st, causal, pybind11::none()));
+    if (!c) return pybind11::none();
+    return pybind11::cast(c->av(attn, v, current_stream(v)));
+}
+
+pybind11::object qk_bwd(int64_t rank, const at::Tensor& da, const at::Tensor& q, const at::Tensor& k,
+                        pybind11::handle ks, pybind11::handle dil, pybind11::handle st, pybind11::handle causal,
+                        pybind11::handle scale) {
+    const SplitCall* c =
+        find(g_split[kQkBwd], split_key(kQkBwd, rank, {&da, &q, &k}, ks, dil, st, causal, scale));
+    if (!c) return pybind11::none();
+    return pybind11::cast(c->qk_backward(da, q, k, current_stream(q)));
+}
+
+pybind11::object av_bwd(int64_t rank, const at::Tensor& dout, const at::Tensor& attn, const at::Tensor& v,
+                        pybind11::handle ks, pybind11::handle dil, pybind11::handle st, pybind11::handle causal) {
+    const SplitCall* c = find(g_split[kAvBwd],
+                              split_key(kAvBwd, rank, {&dout, &attn, &v}, ks, dil, st, causal, pybind11::none()));
+    if (!c) return pybind11::none();
+    return pybind11::cast(c->av_backward(dout, attn, v, current_stream(v)));
+}
+
+bool split_register(int64_t rank, const std::vector<at::Tensor>& ts, pybind11::handle ks, pybind11::handle dil,
+                    pybind11::handle st, pybind11::handle causal, pybind11::handle scale, pybind11::object call) {
+    const int op = call.cast<SplitCall&>().op;
+    const size_t n = op == kQk || op == kAv ? 2 : 3;
+    if (ts.size() != n) throw pybind11::value_error("split_register: wrong number of tensors");
+    const Key key = n == 2 ? split_key(op, rank, {&ts[0], &ts[1]}, ks, dil, st, causal, scale)
+                           : split_key(op, rank, {&ts[0], &ts[1], &ts[2]}, ks, dil, st, causal, scale);
+    return remember(g_split[op], key, std::move(call));
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
-    m.doc() = "Host binding of natten_hip_forward / natten_hip_backward for the 'hip' backend";
+    m.doc() = "Host binding of the fused and split entry points for the 'hip' backend";
     m.attr("abi_version") = natten_hip_abi_version();
     pybind11::class_<FusedCall>(m, "FusedCall")
         .def(pybind11::init<const pybind11::bytes&, const pybind11::bytes&, std::vector<int64_t>,
@@ -319,15 +475,22 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("fwd_register", &fwd_register, "register the FusedCall of a forward signature");
     m.def("bwd", &bwd, "cached fused backward: (dq, dk, dv), or None when the signature is not registered");
     m.def("bwd_register", &bwd_register, "register the FusedCall of a backward signature");
-    m.def("clear", [] {
-        g_fwd.clear();
-        g_bwd.clear();
-    }, "drop every registered signature");
+    pybind11::class_<SplitCall>(m, "SplitCall")
+        .def(pybind11::init<int, const pybind11::bytes&, const pybind11::bytes&, std::vector<int64_t>, bool>())
+        .def_readonly("op", &SplitCall::op)
+        .def("qk", &SplitCall::qk)
+        .def("av", &SplitCall::av)
+        .def("qk_backward", &SplitCall::qk_backward)
+        .def("av_backward", &SplitCall::av_backward);
+    m.def("qk", &qk, "cached split QK: attn, or None when the signature is not registered");
+    m.def("av", &av, "cached split AV: out, or None when the signature is not registered");
+    m.def("qk_bwd", &qk_bwd, "cached split QK backward: (dq, dk), or None");
+    m.def("av_bwd", &av_bwd, "cached split AV backward: (dattn, dv), or None");
+    m.def("split_register", &split_register,
+          "register the SplitCall of a split-op signature (its input tensors in the op's argument order)");
+    m.def("clear", &clear_all, "drop every registered signature");
     // the cached objects hold Python references: release them before the
     // interpreter's own teardown
     auto atexit = pybind11::module_::import("atexit");
-    atexit.attr("register")(pybind11::cpp_function([] {
-        g_fwd.clear();
-        g_bwd.clear();
-    }));
+    atexit.attr("register")(pybind11::cpp_function(&clear_all));
 }

@@ -149,6 +149,21 @@ def _fast_call(sig, lays, out_shape, lse_shape, strided):
     return b.FusedCall(bytes(sig.prob), blob, list(out_shape), list(lse_shape), bool(strided))
 
 
+def _register_split(b, op, rank, given, used, outs, prob, kernel_size, dilation, stride, is_causal, scale,
+                    zero_dq=False):
+    """Register a split-op signature with the binding: ``given`` are the
+    hook's input tensors, ``used`` what the C call received (registered only
+    when they are the same tensors, i.e. nothing was converted), ``outs`` the
+    outputs it allocated (contiguous, as the binding allocates them)."""
+    if any(a is not u for a, u in zip(given, used)):
+        return
+    lays = [_lib.layout(t, rank, 1) for t in (*used, *outs)]
+    blob = b"".join(bytes(x) for x in lays)
+    out_shape = list(outs[0].shape) if op in (0, 1) else []
+    call = b.SplitCall(op, bytes(prob), blob, out_shape, bool(zero_dq))
+    b.split_register(rank, list(given), kernel_size, dilation, stride, is_causal, scale, call)
+
+
 _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
@@ -321,6 +336,12 @@ def _attn_extent(rank, attn, sp, stride):
 
 
 def qk_forward(rank: int, q, k, kernel_size, dilation, stride, is_causal, scale):
+    b = _lib.binding()
+    if b is not None:
+        r = b.qk(rank, q, k, kernel_size, dilation, stride, is_causal, scale)
+        if r is not None:
+            return r
+    given = (q, k)
     if q.ndim != rank + 3 or q.shape != k.shape:
         raise ValueError(f"na{rank}d_qk expects query/key of identical shape [B, *spatial, heads, dim].")
     _on_device(q, k)
@@ -341,10 +362,18 @@ def qk_forward(rank: int, q, k, kernel_size, dilation, stride, is_causal, scale)
             _byref(_lib.layout(k, rank, 1)), _lib.ptr(attn), _byref(_lib.layout(attn, rank, 1)),
             _lib.stream_of(q))
     _lib.check(rc, "qk_forward")
+    if b is not None:
+        _register_split(b, 0, rank, given, (q, k), (attn,), prob, kernel_size, dilation, stride, is_causal, scale)
     return attn
 
 
 def av_forward(rank: int, attn, v, kernel_size, dilation, stride, is_causal):
+    b = _lib.binding()
+    if b is not None:
+        r = b.av(rank, attn, v, kernel_size, dilation, stride, is_causal)
+        if r is not None:
+            return r
+    given = (attn, v)
     if attn.ndim != rank + 3 or v.ndim != rank + 3:
         raise ValueError(f"na{rank}d_av expects attn [B, *spatial, heads, KV] and value [B, *spatial, heads, dim].")
     if attn.shape[0] != v.shape[0] or attn.shape[-2] != v.shape[-2]:
@@ -366,10 +395,18 @@ def av_forward(rank: int, attn, v, kernel_size, dilation, stride, is_causal):
             _byref(_lib.layout(v, rank, 1)), _lib.ptr(out), _byref(_lib.layout(out, rank, 1)),
             _lib.stream_of(v))
     _lib.check(rc, "av_forward")
+    if b is not None:
+        _register_split(b, 1, rank, given, (attn, v), (out,), prob, kernel_size, dilation, stride, is_causal, None)
     return out
 
 
 def qk_backward(rank: int, d_attn, q, k, kernel_size, dilation, stride, is_causal, scale=None):
+    b = _lib.binding()
+    if b is not None:
+        r = b.qk_bwd(rank, d_attn, q, k, kernel_size, dilation, stride, is_causal, scale)
+        if r is not None:
+            return r
+    given = (d_attn, q, k)
     _on_device(d_attn, q, k)
     d_attn = d_attn.to(q.dtype)
     d_attn, q, k = _inner(d_attn), _inner(q), _inner(k)
@@ -387,10 +424,19 @@ def qk_backward(rank: int, d_attn, q, k, kernel_size, dilation, stride, is_causa
             _byref(prob), _lib.ptr(d_attn), L(d_attn), _lib.ptr(q), L(q), _lib.ptr(k), L(k),
             _lib.ptr(dq), L(dq), _lib.ptr(dk), L(dk), _lib.stream_of(q))
     _lib.check(rc, "qk_backward")
+    if b is not None:
+        _register_split(b, 2, rank, given, (d_attn, q, k), (dq, dk), prob, kernel_size, dilation, stride,
+                        is_causal, scale, zero_dq=strided)
     return dq, dk
 
 
 def av_backward(rank: int, d_out, attn, v, kernel_size, dilation, stride, is_causal):
+    b = _lib.binding()
+    if b is not None:
+        r = b.av_bwd(rank, d_out, attn, v, kernel_size, dilation, stride, is_causal)
+        if r is not None:
+            return r
+    given = (d_out, attn, v)
     _on_device(d_out, attn, v)
     d_out = d_out.to(v.dtype)
     attn = attn.to(v.dtype)
@@ -408,6 +454,9 @@ def av_backward(rank: int, d_out, attn, v, kernel_size, dilation, stride, is_cau
             _byref(prob), _lib.ptr(d_out), L(d_out), _lib.ptr(attn), L(attn), _lib.ptr(v), L(v),
             _lib.ptr(d_attn), L(d_attn), _lib.ptr(dv), L(dv), _lib.stream_of(v))
     _lib.check(rc, "av_backward")
+    if b is not None:
+        _register_split(b, 3, rank, given, (d_out, attn, v), (d_attn, dv), prob, kernel_size, dilation, stride,
+                        is_causal, None)
     return d_attn, dv
 
 

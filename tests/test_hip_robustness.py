@@ -399,6 +399,53 @@ def test_binding_signature_cache():
     assert torch.equal(out6, out) and torch.equal(lse6, lse)
 
 
+@pytest.mark.parametrize("stride", [(1, 1), (2, 1)])
+def test_split_ops_through_the_binding_cache(stride, monkeypatch):
+    """The four split ops (QK, AV, their backward) run wholly in the binding
+    once their signature is registered: the repeated calls below succeed with
+    hip.py's layout builder switched off, and give the bits of the first
+    calls and of the ctypes path.  dq of the strided QK backward is zero off
+    the query positions in both.  A d_attn of another dtype is converted by
+    hip.py (never registered) and matches too."""
+    from natten_mps_amd._core import _lib, hip
+
+    b = _lib.binding()
+    assert b is not None, "the host binding _natten_torch.so is not built"
+    rank, ks, dil, causal = 2, (5, 5), (1, 2), (False, False)
+    q, k, v = (x.to(DEV) for x in _inputs(911, [(2, 14, 18, 2, 32)] * 3, torch.bfloat16))
+    out_sp = tuple((n + s_ - 1) // s_ for n, s_ in zip(q.shape[1:3], stride))
+    (da, do) = (x.to(DEV) for x in _inputs(912, [(2, *out_sp, 2, 25), (2, *out_sp, 2, 32)], torch.bfloat16))
+
+    def calls():
+        attn = hip.qk_forward(rank, q, k, ks, dil, stride, causal, 0.25)
+        out = hip.av_forward(rank, attn, v, ks, dil, stride, causal)
+        dq, dk = hip.qk_backward(rank, da, q, k, ks, dil, stride, causal, 0.25)
+        dattn, dv = hip.av_backward(rank, do, attn, v, ks, dil, stride, causal)
+        torch.cuda.synchronize()
+        return [attn, out, dq, dk, dattn, dv]
+
+    names = ("attn", "out", "dq", "dk", "dattn", "dv")
+    b.clear()
+    first = calls()
+
+    def no_python_path(*a, **kw):
+        raise AssertionError("a registered split-op signature went through hip.py")
+
+    monkeypatch.setattr(_lib, "layout", no_python_path)
+    second = calls()
+    monkeypatch.undo()
+    monkeypatch.setattr(_lib, "_bind", None)
+    third = calls()
+    monkeypatch.undo()
+    for name, a, c, d in zip(names, first, second, third):
+        assert torch.equal(a, c), f"{name}: binding cache differs from the first call"
+        assert torch.equal(a, d), f"{name}: binding differs from the ctypes path"
+    if stride != (1, 1):
+        assert not first[2][:, 1::2].any(), "dq must be zero off the strided query positions"
+    dq32, dk32 = hip.qk_backward(rank, da.float(), q, k, ks, dil, stride, causal, 0.25)
+    assert torch.equal(dq32, first[2]) and torch.equal(dk32, first[3])
+
+
 # ---------------------------------------------------------------------------
 # fp32 on the 2-D tile kernels (v_mfma_f32_16x16x4_f32)
 # ---------------------------------------------------------------------------
