@@ -89,17 +89,19 @@ def _valid_pairs(spatial, kernel, dilation, causal, device):
     return int(valid.sum().item())
 
 
-def kernel_bytes(name, B, N, Hq, Hkv, D, esz):
+def kernel_bytes(name, B, N, Hq, Hkv, D, esz, rank=2):
     """Algorithmic HBM bytes of one launch (compulsory traffic: every operand
-    read once, every result written once; K/V at Hkv heads; fp32 LSE/delta)."""
+    read once, every result written once; K/V at Hkv heads; fp32 LSE/delta).
+    The dQ tile kernels of 1-D and 2-D problems take delta from their own
+    P dP and do not read o; those of 3-D problems read o for delta = dO . o."""
     tq, tkv, lse = B * N * Hq * D * esz, B * N * Hkv * D * esz, B * N * Hq * 4
     fwd = tq + 2 * tkv + tq + lse                 # q, k, v -> out, lse
-    bwd_q = tq + 2 * tkv + tq + lse + tq + lse    # q, k, v, dout, o, lse -> dq, delta
-    bwd_q_mfma = bwd_q + tq                       # ... the tile kernel also reads o
+    bwd_q = tq + 2 * tkv + tq + lse + tq + lse    # q, k, v, dout, lse -> dq, delta
+    bwd_q_mfma = bwd_q + (tq if rank == 3 else 0)  # ... 3-D: the tile kernel also reads o
     bwd_kv = tq + 2 * tkv + tq + 2 * lse + 2 * tkv  # q, k, v, dout, lse, delta -> dk, dv
     return {
         "na_forward": fwd, "na_fwd_mfma": fwd, "na_fwd_lean": fwd,
-        "na_bwd_dq": bwd_q, "na_bwd_q_mfma": bwd_q_mfma, "na_bwd_q_lean": bwd_q_mfma,
+        "na_bwd_dq": bwd_q, "na_bwd_q_mfma": bwd_q_mfma, "na_bwd_q_lean": bwd_q,
         "na_bwd_dkdv": bwd_kv, "na_bwd_kv_mfma": bwd_kv, "na_bwd_kv_lean": bwd_kv,
     }.get(name)
 
@@ -527,7 +529,7 @@ def measure(torch, cid, steps, warmup, dilation=None, causal=None, graph=True, s
     dil_tag = dils[0] if len(set(dils)) == 1 else "x".join(dils)
     workload = f"config{cid}_d{dil_tag}"
     dom_name, (dn, dtot, _, _) = max(stats.items(), key=lambda kv: kv[1][1])
-    nbytes = kernel_bytes(dom_name, B, N, Hq, Hkv, D, esz)
+    nbytes = kernel_bytes(dom_name, B, N, Hq, Hkv, D, esz, rank)
     mean_s = dtot / dn * 1e-3
     roof = None
     if nbytes is not None:

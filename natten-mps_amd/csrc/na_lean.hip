@@ -483,8 +483,10 @@ __device__ __forceinline__ void lean_redo_bwd_kv(const void* kargs, int pos1, in
 
 // ---------------------------------------------------------------------------
 // Backward, query side: delta = dO . O - dlse (written for the key side),
-// dq = scale * sum P (dP - delta) k with P = exp(scale q.k - lse).  The dP
-// product starts from -delta.
+// dq = scale * sum P (dP - delta) k with P = exp(scale q.k - lse).  delta
+// comes from the kernel's own products, sum over the window of P dP (equal
+// to dO . O), in a first pass that keeps every chunk's P and dP; O is read
+// only where that sum is not finite.
 // ---------------------------------------------------------------------------
 // Query tile of task x = (batch, tile, head), head fastest.
 template <typename T, int D, int NCH>
@@ -515,17 +517,15 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
     const int qoff = pos1 * a.lq.s1 + pos2 * a.lq.s2;
     const long long qbo = b * a.lq.b + h * a.lq.h;
     const long long lo = b * a.ll.b + h * a.ll.h + pos1 * a.ll.s1 + pos2 * a.ll.s2;
-    uint4 qf[NF], gf[NF], of[NF];
+    uint4 qf[NF], gf[NF];
     {
         const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + qbo, a.qbytes);
         const __amdgpu_buffer_rsrc_t rg = lean_rsrc(a.dout + qbo, a.qbytes);
-        const __amdgpu_buffer_rsrc_t ro = lean_rsrc(a.o + qbo, a.qbytes);
 #pragma unroll
         for (int ks = 0; ks < NF; ++ks) {
             const uint32_t o = valid ? static_cast<uint32_t>(qoff * ES + lean_frag_off<T, D>(ks, grp)) : kLeanOOR;
             qf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 0));
             gf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rg, o, 0, 0));
-            of[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ro, o, 0, 0));
         }
     }
     const float L2 = valid ? a.lse[lo] * kLog2e : 0.f;
@@ -545,37 +545,51 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
 #pragma unroll
         for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<T, D>(first, lane, hi, db);
 
-    // delta = dO . O: this lane's head dims, then the 4 lane rows
-    float di = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < NF; ++ks) di = lean_dot<T>(gf[ks], of[ks], di);
-    di = sum_rows(di) - dl;
-    if (valid && grp == 0) a.delta[lo] = di;
-    const f32x4_t nd = f32x4_t{-di, -di, -di, -di};
-
     wait_loads();
     __syncthreads();
 
     const unsigned char* Kb = reinterpret_cast<const unsigned char*>(Ks);
     const unsigned char* Vb = reinterpret_cast<const unsigned char*>(Vs);
+    // P and dP (= dO . v) of every chunk first, and delta = sum over the
+    // window of P dP (= dO . O) from them; where that is not finite (a
+    // non-finite operand outside the window reaching the sum through a
+    // masked slot), dO . O from the rows
+    f32x4_t pr[NCH][2], dpr[NCH][2];
+    float di;
+    {
+        const f32x4_t zero = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        float part = 0.f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int row = 2 * c + (grp >> 1) - rlo;
+            const float off = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1) ? -L2 : -INFINITY;
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+                const f32x4_t sc = lean_score<T, D>(Kb, aoff, c, bb, qf, cb[bb]);
+                dpr[c][bb] = lean_score<T, D>(Vb, aoff, c, bb, gf, zero);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pr[c][bb][i] = __builtin_amdgcn_exp2f(fmaf(sc[i], a.sc2, off));
+                    part = fmaf(pr[c][bb][i], dpr[c][bb][i], part);
+                }
+            }
+        }
+        di = sum_rows(part) - dl;
+        if (valid && !(__builtin_fabsf(di) <= __FLT_MAX__))
+            di = exact_dot<T, D>(a.dout + qbo + qoff, a.o + qbo + qoff) - dl;
+    }
+    if (valid && grp == 0) a.delta[lo] = di;
     f32x4_t acc[D / 16];
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        f32x4_t s[2], dp[2];
-#pragma unroll
-        for (int bb = 0; bb < 2; ++bb) {
-            s[bb] = lean_score<T, D>(Kb, aoff, c, bb, qf, cb[bb]);
-            dp[bb] = lean_score<T, D>(Vb, aoff, c, bb, gf, nd);
-        }
-        const int row = 2 * c + (grp >> 1) - rlo;
-        const float off = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1) ? -L2 : -INFINITY;
+        f32x4_t ds[2];
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], a.sc2, off)) * dp[bb][i];
-        lean_acc<T, D>(Kb, toff, c, s, acc);
+            for (int i = 0; i < 4; ++i) ds[bb][i] = pr[c][bb][i] * (dpr[c][bb][i] - di);
+        lean_acc<T, D>(Kb, toff, c, ds, acc);
     }
     const bool redo = valid && item_nonfinite(lane_sum(acc, 0.f));
     if (valid) {

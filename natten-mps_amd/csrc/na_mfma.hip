@@ -297,9 +297,15 @@ __device__ __forceinline__ void redo_bwd_q(const void* kargs, int wg, int wave, 
     }
 }
 
-// FLAT as for k_fwd_mfma.
-template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN = false, bool FLAT = false>
+// FLAT as for k_fwd_mfma.  PDP: one slice per head (axis 0 of extent 1:
+// 1-D and 2-D problems) and no global keys; delta from the kernel's own
+// products (the sum over the window of P dP, which equals dO . O) in a first
+// pass over the chunks, so O is not read, and dS = P (dP - delta) with dP
+// from a zero accumulator (the 2-D tile kernel's arithmetic, bit for bit).
+// Otherwise delta = dO . O from the rows and dP is accumulated from -delta.
+template <typename T, int D, int LAY, bool WIDE, bool GLOBAL, bool VARLEN = false, bool FLAT = false, bool PDP = false>
 __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) void k_bwd_q_mfma(BwdQArgs<T> args) {
+    static_assert(!PDP || (!GLOBAL && !VARLEN), "delta from P dP: one slice per head, no global keys");
     const Prob& p = args.p;
     const TileShape& ts = args.ts;
     const int* __restrict__ geo = args.geo;
@@ -345,29 +351,62 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) vo
 
     uint4 qf[D / 32], gf[D / 32];
     f32x4_t acc[D / 16], nd[2];
-    float L2;
+    float L2, dsub = 0.f;
     bool more = true, fresh = true, redo = false;
     while (more) {
         const int b = w.b, h = w.h, u0 = w.u0;
         if (fresh) {
-            uint4 of[D / 32];
             load_frags<T, D>(bh_ptr(q, lq, b, h), vol_off(lq, ln.pos), ln.valid, grp, qf);
             load_frags<T, D>(bh_ptr(dout, ldo, b, h), vol_off(ldo, ln.pos), ln.valid, grp, gf);
-            load_frags<T, D>(bh_ptr(o, lo, b, h), vol_off(lo, ln.pos), ln.valid, grp, of);
             L2 = ln.valid ? bh_ptr(lse, ll, b, h)[vol_off(ll, ln.pos)] * kLog2e : 0.f;
-            // delta from this lane's 8 head dims per 32, summed over the 4 lane rows
-            float di = 0.f;
+            if constexpr (!PDP) {
+                uint4 of[D / 32];
+                load_frags<T, D>(bh_ptr(o, lo, b, h), vol_off(lo, ln.pos), ln.valid, grp, of);
+                // delta from this lane's 8 head dims per 32, summed over the 4 lane rows
+                float di = 0.f;
 #pragma unroll
-            for (int ks = 0; ks < D / 32; ++ks) di = dot8<T>(gf[ks], of[ks], di);
-            di = sum_rows(di);
-            if (dlse && ln.valid) di -= bh_ptr(dlse, ldl, b, h)[vol_off(ldl, ln.pos)];
-            if (ln.valid && grp == 0) bh_ptr(delta, lde, b, h)[vol_off(lde, ln.pos)] = di;
-            nd[0] = nd[1] = f32x4_t{-di, -di, -di, -di};
+                for (int ks = 0; ks < D / 32; ++ks) di = dot8<T>(gf[ks], of[ks], di);
+                di = sum_rows(di);
+                if (dlse && ln.valid) di -= bh_ptr(dlse, ldl, b, h)[vol_off(ldl, ln.pos)];
+                if (ln.valid && grp == 0) bh_ptr(delta, lde, b, h)[vol_off(lde, ln.pos)] = di;
+                nd[0] = nd[1] = f32x4_t{-di, -di, -di, -di};
+            }
 #pragma unroll
             for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         }
         wait_loads();
         __syncthreads();
+        if (PDP && fresh) {
+            float part = 0.f;
+            if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
+                const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
+                const f32x4_t zero[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+                for (int c = wg.c0; c <= wg.c1; ++c) {
+                    f32x4_t s[2], dp[2];
+                    if constexpr (!WIDE) {
+                        score_chunk<T, D>(Ks, c, col, grp, qf, cb, s);
+                    } else {
+                        f32x4_t bias[2];
+                        column_bias(ln, ts.rowshift, c, grp, bias);
+                        score_chunk<T, D>(Ks, c, col, grp, qf, bias, s);
+                    }
+                    score_chunk<T, D>(Vs, c, col, grp, gf, zero, dp);
+                    part = delta_part(s, dp, sc2, row_ok(ln, ts.rowshift, in0, c, grp) ? -L2 : -INFINITY, part);
+                }
+            }
+            float di = sum_rows(part);
+            if (dlse && ln.valid) di -= bh_ptr(dlse, ldl, b, h)[vol_off(ldl, ln.pos)];
+            // a non-finite operand outside the window can reach the sum
+            // through a masked slot: dO . O from the rows there
+            if (ln.valid && !(__builtin_fabsf(di) <= __FLT_MAX__)) {
+                di = exact_dot<T, D>(bh_ptr(dout, ldo, b, h) + vol_off(ldo, ln.pos),
+                                     bh_ptr(o, lo, b, h) + vol_off(lo, ln.pos));
+                if (dlse) di -= bh_ptr(dlse, ldl, b, h)[vol_off(ldl, ln.pos)];
+            }
+            if (ln.valid && grp == 0) bh_ptr(delta, lde, b, h)[vol_off(lde, ln.pos)] = di;
+            nd[0] = nd[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            dsub = di;
+        }
         if (wg.any && u0 >= wg.lo[0] && u0 <= wg.hi[0]) {
             const bool in0 = u0 >= ln.lo[0] && u0 <= ln.hi[0];
             const auto chunks = [&](auto) {
@@ -385,8 +424,11 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) vo
 #pragma unroll
                     for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], sc2, off)) * dp[bb][i];
+                        for (int i = 0; i < 4; ++i) {
+                            const float e = __builtin_amdgcn_exp2f(fmaf(s[bb][i], sc2, off));
+                            if constexpr (PDP) s[bb][i] = e * (dp[bb][i] - dsub);
+                            else s[bb][i] = e * dp[bb][i];
+                        }
                     accumulate_chunk<T, D>(Ks, c, lane, pack8<T>(s), acc);
                 }
             };
@@ -1626,14 +1668,19 @@ hipError_t run_bwd_q(const Prob& p, TileShape ts, const void* q, Lay lq, const v
                      Lay lv, const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
                      const float* dlse, Lay ldl, void* dq, Lay ldq, float* delta, Lay lde, const GlobalSet* g,
                      hipStream_t s, const int* lens = nullptr) {
-    auto kern = k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN>;
+    // delta from P dP where the walk has one slice per head
+    constexpr bool kPdpOk = !GLOBAL && !VARLEN;
+    const bool pdp = kPdpOk && p.ax[0].len == 1;
+    auto kern = pdp ? k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN, false, kPdpOk>
+                    : k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN>;
     const size_t shm = lds_bytes(kBackwardQ, ts.slots, D) + (GLOBAL ? global_lds(D) : 0);
     hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     fit_h_per(p, ts, resident_blocks(kern, 64 * ts.waves, shm));
     if constexpr (kHasFlat<LAY, WIDE, GLOBAL, VARLEN>) {
         if (flat_walk(p, ts, false)) {
-            kern = k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN, true>;
+            kern = pdp ? k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN, true, kPdpOk>
+                       : k_bwd_q_mfma<T, D, LAY, WIDE, GLOBAL, VARLEN, true>;
             if ((e = allow_lds(kern, shm)) != hipSuccess) return e;
         }
     }
@@ -1955,11 +2002,14 @@ void audit_fused(LdsAudit& a) {
     audit_one(k_fwd_mfma<T, D, LAY, true, false>, "k_fwd_mfma (wide)", a);
     audit_one(k_bwd_q_mfma<T, D, LAY, false, false>, "k_bwd_q_mfma", a);
     audit_one(k_bwd_q_mfma<T, D, LAY, true, false>, "k_bwd_q_mfma (wide)", a);
+    audit_one(k_bwd_q_mfma<T, D, LAY, false, false, false, false, true>, "k_bwd_q_mfma (P dP)", a);
+    audit_one(k_bwd_q_mfma<T, D, LAY, true, false, false, false, true>, "k_bwd_q_mfma (wide, P dP)", a);
     audit_one(k_bwd_kv_mfma<T, D, LAY, false>, "k_bwd_kv_mfma", a);
     audit_one(k_bwd_kv_mfma<T, D, LAY, true>, "k_bwd_kv_mfma (wide)", a);
     if constexpr (kHasFlat<LAY, false, false, false>) {
         audit_one(k_fwd_mfma<T, D, LAY, false, false, false, true>, "k_fwd_mfma (flat)", a);
         audit_one(k_bwd_q_mfma<T, D, LAY, false, false, false, true>, "k_bwd_q_mfma (flat)", a);
+        audit_one(k_bwd_q_mfma<T, D, LAY, false, false, false, true, true>, "k_bwd_q_mfma (flat, P dP)", a);
         audit_one(k_bwd_kv_mfma<T, D, LAY, false, false, true>, "k_bwd_kv_mfma (flat)", a);
     }
 }

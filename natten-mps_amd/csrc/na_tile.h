@@ -94,6 +94,20 @@ __device__ __forceinline__ float sum_rows(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// delta = dO . O of a query from the dQ kernel's own products: the sum over
+// its window of P dP (dP = dO . v), equal to dO . O in exact arithmetic (O is
+// the P-weighted sum of v), so the dQ kernels need not read O.  The lane's
+// part over one chunk, its 2 x 4 slots in order (the order k_lean_bwd_q
+// sums them in); a masked slot has P = 0.
+__device__ __forceinline__ float delta_part(const f32x4_t (&s)[2], const f32x4_t (&dp)[2], float sc2, float off,
+                                            float part) {
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part = fmaf(__builtin_amdgcn_exp2f(fmaf(s[bb][i], sc2, off)), dp[bb][i], part);
+    return part;
+}
+
 // Sum of a lane's accumulators (plus `extra`): not finite exactly when one
 // of them is not finite (a sum of finite accumulators of this size cannot
 // overflow).
