@@ -14,7 +14,9 @@
 // the ctypes path: invalid input -> ValueError, unsupported ->
 // NotImplementedError, launch failure -> RuntimeError.
 //
-// SplitCall does the same for the four split ops (qk, av, qk_bwd, av_bwd).
+// SplitCall does the same for the four split ops (qk, av, qk_bwd, av_bwd)
+// and the four relative-position-bias ops (rpb_qk, rpb_av, rpb_qk_bwd,
+// rpb_av_bwd).
 //
 // fwd / bwd (and qk / av / qk_bwd / av_bwd) are the per-call entry of
 // hip.py: they take the backend hook's own arguments, build the signature
@@ -28,7 +30,8 @@
 //
 // Reference: the backend hooks this serves are those the autograd factory
 // calls (autograd/_factory.py:37-38,66-67 of /root/reference/src/natten_mps)
-// and the split ops' forward and backward hooks (_core/ops.py:98-152).
+// the split ops' forward and backward hooks (_core/ops.py:98-152), and the
+// relative-position-bias ops of extras/allin1 (extras/allin1/functional.py).
 #include <torch/extension.h>
 
 #include <ATen/hip/EmptyTensor.h>
@@ -144,21 +147,28 @@ struct FusedCall {
 // The split ops (QK, AV and their backward), as FusedCall: the problem and
 // layouts of one call signature, fixed.  Layout slots: QK q k attn; AV attn v
 // out; QK backward dattn q k dq dk; AV backward dout attn v dattn dv.
-enum SplitOp { kQk = 0, kAv = 1, kQkBwd = 2, kAvBwd = 3 };
-constexpr size_t kSplitLays[4] = {3, 3, 5, 5};
+// The relative-position-bias ops (natten_hip_rpb_*) use the same slots: QK
+// q k attn (plus the bias table, no layout); AV attn v out; QK backward dattn
+// q k dq dk (plus the bias gradient and its workspace); AV backward dout attn
+// v dattn dv.
+enum SplitOp { kQk = 0, kAv = 1, kQkBwd = 2, kAvBwd = 3, kRpbQk = 4, kRpbAv = 5, kRpbQkBwd = 6, kRpbAvBwd = 7 };
+constexpr int kSplitOps = 8;
+constexpr size_t kSplitLays[kSplitOps] = {3, 3, 5, 5, 3, 3, 5, 5};
 
 struct SplitCall {
     int op;
     natten_problem_t prob;
     std::vector<natten_layout_t> lay;
-    std::vector<int64_t> out_shape;  // QK: attn; AV: out
+    std::vector<int64_t> out_shape;  // QK: attn; AV: out; RPB QK backward: the bias gradient
     bool zero_dq;                    // QK backward: dq zeroed where strides leave non-query positions
+    int64_t work_floats = 0;         // RPB QK backward: the bias gradient's workspace
 
     SplitCall(int op_, const pybind11::bytes& prob_bytes, const pybind11::bytes& lay_bytes,
-              std::vector<int64_t> out_shape_, bool zero_dq_)
-        : op(op_), out_shape(std::move(out_shape_)), zero_dq(zero_dq_) {
+              std::vector<int64_t> out_shape_, bool zero_dq_, int64_t work_floats_)
+        : op(op_), out_shape(std::move(out_shape_)), zero_dq(zero_dq_), work_floats(work_floats_) {
         const std::string p = prob_bytes, l = lay_bytes;
-        if (op < kQk || op > kAvBwd) throw pybind11::value_error("SplitCall: unknown op");
+        if (op < 0 || op >= kSplitOps) throw pybind11::value_error("SplitCall: unknown op");
+        if (work_floats < 0) throw pybind11::value_error("SplitCall: negative workspace");
         if (p.size() != sizeof(natten_problem_t)) throw pybind11::value_error("SplitCall: problem size mismatch");
         if (l.size() != kSplitLays[op] * sizeof(natten_layout_t))
             throw pybind11::value_error("SplitCall: layout size mismatch");
@@ -219,6 +229,64 @@ struct SplitCall {
                                               v.data_ptr(), &lay[2], da.data_ptr(), &lay[3], dv.data_ptr(), &lay[4],
                                               reinterpret_cast<void*>(stream));
         if (rc != NATTEN_OK) raise_status(rc, "av_backward");
+        return {da, dv};
+    }
+
+    at::Tensor rpb_qk(const at::Tensor& q, const at::Tensor& k, const std::optional<at::Tensor>& rpb,
+                      int64_t stream) const {
+        want(kRpbQk);
+        c10::OptionalDeviceGuard guard;
+        if (FusedCall::current_index() != q.get_device()) guard.reset_device(q.device());
+        at::Tensor attn = alloc(out_shape, q.scalar_type(), q.device());
+        const int rc = natten_hip_rpb_qk_forward(&prob, q.data_ptr(), &lay[0], k.data_ptr(), &lay[1],
+                                                 rpb.has_value() ? rpb->data_ptr() : nullptr, attn.data_ptr(),
+                                                 &lay[2], reinterpret_cast<void*>(stream));
+        if (rc != NATTEN_OK) raise_status(rc, "rpb_qk_forward");
+        return attn;
+    }
+
+    at::Tensor rpb_av(const at::Tensor& attn, const at::Tensor& v, int64_t stream) const {
+        want(kRpbAv);
+        c10::OptionalDeviceGuard guard;
+        if (FusedCall::current_index() != v.get_device()) guard.reset_device(v.device());
+        at::Tensor out = alloc(v.sizes(), v.scalar_type(), v.device());
+        const int rc = natten_hip_rpb_av_forward(&prob, attn.data_ptr(), &lay[0], v.data_ptr(), &lay[1],
+                                                 out.data_ptr(), &lay[2], reinterpret_cast<void*>(stream));
+        if (rc != NATTEN_OK) raise_status(rc, "rpb_av_forward");
+        return out;
+    }
+
+    // (dq, dk, drpb); drpb None without a bias (an empty out_shape)
+    pybind11::tuple rpb_qk_backward(const at::Tensor& da, const at::Tensor& q, const at::Tensor& k,
+                                    int64_t stream) const {
+        want(kRpbQkBwd);
+        c10::OptionalDeviceGuard guard;
+        if (FusedCall::current_index() != q.get_device()) guard.reset_device(q.device());
+        at::Tensor dq = alloc(q.sizes(), q.scalar_type(), q.device());
+        at::Tensor dk = alloc(k.sizes(), k.scalar_type(), k.device());
+        std::optional<at::Tensor> drpb;
+        if (!out_shape.empty()) drpb = alloc(out_shape, q.scalar_type(), q.device());
+        const Workspace work(static_cast<size_t>(drpb ? work_floats : 0) * sizeof(float),
+                             reinterpret_cast<hipStream_t>(stream));
+        const int rc = natten_hip_rpb_qk_backward_ws(
+            &prob, da.data_ptr(), &lay[0], q.data_ptr(), &lay[1], k.data_ptr(), &lay[2], dq.data_ptr(), &lay[3],
+            dk.data_ptr(), &lay[4], drpb ? drpb->data_ptr() : nullptr, static_cast<float*>(work.ptr),
+            work.ptr ? work_floats : 0, reinterpret_cast<void*>(stream));
+        if (rc != NATTEN_OK) raise_status(rc, "rpb_qk_backward");
+        return pybind11::make_tuple(dq, dk, drpb ? pybind11::cast(*drpb) : pybind11::none());
+    }
+
+    std::tuple<at::Tensor, at::Tensor> rpb_av_backward(const at::Tensor& dout, const at::Tensor& attn,
+                                                       const at::Tensor& v, int64_t stream) const {
+        want(kRpbAvBwd);
+        c10::OptionalDeviceGuard guard;
+        if (FusedCall::current_index() != v.get_device()) guard.reset_device(v.device());
+        at::Tensor da = alloc(attn.sizes(), attn.scalar_type(), attn.device());
+        at::Tensor dv = alloc(v.sizes(), v.scalar_type(), v.device());
+        const int rc = natten_hip_rpb_av_backward(&prob, dout.data_ptr(), &lay[0], attn.data_ptr(), &lay[1],
+                                                  v.data_ptr(), &lay[2], da.data_ptr(), &lay[3], dv.data_ptr(),
+                                                  &lay[4], reinterpret_cast<void*>(stream));
+        if (rc != NATTEN_OK) raise_status(rc, "rpb_av_backward");
         return {da, dv};
     }
 };
@@ -307,7 +375,7 @@ struct Entry {
 
 constexpr size_t kCacheMax = 64;
 std::vector<Entry<FusedCall>> g_fwd, g_bwd;
-std::vector<Entry<SplitCall>> g_split[4];
+std::vector<Entry<SplitCall>> g_split[kSplitOps];
 
 template <typename C>
 const C* find(const std::vector<Entry<C>>& cache, const Key& k) {
@@ -451,9 +519,76 @@ pybind11::object av_bwd(int64_t rank, const at::Tensor& dout, const at::Tensor& 
     return pybind11::cast(c->av_backward(dout, attn, v, current_stream(v)));
 }
 
+// Relative-position-bias ops: the key of op `op` over its input tensors, a
+// flag (the bias table's presence or, for QK backward, whether a bias
+// gradient is asked for) and the kernel and dilation sequences.
+Key rpb_key(int op, int64_t rank, std::initializer_list<const at::Tensor*> ts, const at::Tensor* table, int flag,
+            pybind11::handle ks, pybind11::handle dil) {
+    Key key;
+    key.put(op);
+    key.put(rank);
+    for (const at::Tensor* t : ts) key.tensor(*t, true);
+    if (table) key.tensor(*table, true);
+    key.put(flag);
+    key.ints(ks);
+    key.ints(dil);
+    return key;
+}
+
+pybind11::object rpb_qk(int64_t rank, const at::Tensor& q, const at::Tensor& k, const std::optional<at::Tensor>& rpb,
+                        pybind11::handle ks, pybind11::handle dil) {
+    const SplitCall* c = find(g_split[kRpbQk], rpb_key(kRpbQk, rank, {&q, &k}, rpb ? &*rpb : nullptr,
+                                                       rpb.has_value(), ks, dil));
+    if (!c) return pybind11::none();
+    return pybind11::cast(c->rpb_qk(q, k, rpb, current_stream(q)));
+}
+
+pybind11::object rpb_av(int64_t rank, const at::Tensor& attn, const at::Tensor& v, pybind11::handle ks,
+                        pybind11::handle dil) {
+    const SplitCall* c = find(g_split[kRpbAv], rpb_key(kRpbAv, rank, {&attn, &v}, nullptr, 0, ks, dil));
+    if (!c) return pybind11::none();
+    return pybind11::cast(c->rpb_av(attn, v, current_stream(v)));
+}
+
+pybind11::object rpb_qk_bwd(int64_t rank, const at::Tensor& da, const at::Tensor& q, const at::Tensor& k,
+                            bool with_rpb, pybind11::handle ks, pybind11::handle dil) {
+    const SplitCall* c =
+        find(g_split[kRpbQkBwd], rpb_key(kRpbQkBwd, rank, {&da, &q, &k}, nullptr, with_rpb, ks, dil));
+    if (!c) return pybind11::none();
+    return c->rpb_qk_backward(da, q, k, current_stream(q));
+}
+
+pybind11::object rpb_av_bwd(int64_t rank, const at::Tensor& dout, const at::Tensor& attn, const at::Tensor& v,
+                            pybind11::handle ks, pybind11::handle dil) {
+    const SplitCall* c = find(g_split[kRpbAvBwd], rpb_key(kRpbAvBwd, rank, {&dout, &attn, &v}, nullptr, 0, ks, dil));
+    if (!c) return pybind11::none();
+    return pybind11::cast(c->rpb_av_backward(dout, attn, v, current_stream(v)));
+}
+
+// ts: the op's input tensors in argument order (RPB QK: q, k and the bias
+// table when there is one); flag as in rpb_key.
+bool rpb_register(int64_t rank, const std::vector<at::Tensor>& ts, int flag, pybind11::handle ks,
+                  pybind11::handle dil, pybind11::object call) {
+    const int op = call.cast<SplitCall&>().op;
+    if (op < kRpbQk) throw pybind11::value_error("rpb_register: not a relative-position-bias op");
+    Key key;
+    if (op == kRpbQk) {
+        if (ts.size() != 2 + (flag ? 1 : 0)) throw pybind11::value_error("rpb_register: wrong number of tensors");
+        key = rpb_key(op, rank, {&ts[0], &ts[1]}, flag ? &ts[2] : nullptr, flag, ks, dil);
+    } else if (op == kRpbAv) {
+        if (ts.size() != 2) throw pybind11::value_error("rpb_register: wrong number of tensors");
+        key = rpb_key(op, rank, {&ts[0], &ts[1]}, nullptr, flag, ks, dil);
+    } else {
+        if (ts.size() != 3) throw pybind11::value_error("rpb_register: wrong number of tensors");
+        key = rpb_key(op, rank, {&ts[0], &ts[1], &ts[2]}, nullptr, flag, ks, dil);
+    }
+    return remember(g_split[op], key, std::move(call));
+}
+
 bool split_register(int64_t rank, const std::vector<at::Tensor>& ts, pybind11::handle ks, pybind11::handle dil,
                     pybind11::handle st, pybind11::handle causal, pybind11::handle scale, pybind11::object call) {
     const int op = call.cast<SplitCall&>().op;
+    if (op > kAvBwd) throw pybind11::value_error("split_register: a relative-position-bias op (rpb_register)");
     const size_t n = op == kQk || op == kAv ? 2 : 3;
     if (ts.size() != n) throw pybind11::value_error("split_register: wrong number of tensors");
     const Key key = n == 2 ? split_key(op, rank, {&ts[0], &ts[1]}, ks, dil, st, causal, scale)
@@ -476,12 +611,24 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("bwd", &bwd, "cached fused backward: (dq, dk, dv), or None when the signature is not registered");
     m.def("bwd_register", &bwd_register, "register the FusedCall of a backward signature");
     pybind11::class_<SplitCall>(m, "SplitCall")
-        .def(pybind11::init<int, const pybind11::bytes&, const pybind11::bytes&, std::vector<int64_t>, bool>())
+        .def(pybind11::init<int, const pybind11::bytes&, const pybind11::bytes&, std::vector<int64_t>, bool,
+                            int64_t>(),
+             pybind11::arg("op"), pybind11::arg("prob"), pybind11::arg("layouts"), pybind11::arg("out_shape"),
+             pybind11::arg("zero_dq"), pybind11::arg("work_floats") = 0)
         .def_readonly("op", &SplitCall::op)
         .def("qk", &SplitCall::qk)
         .def("av", &SplitCall::av)
         .def("qk_backward", &SplitCall::qk_backward)
-        .def("av_backward", &SplitCall::av_backward);
+        .def("av_backward", &SplitCall::av_backward)
+        .def("rpb_qk", &SplitCall::rpb_qk)
+        .def("rpb_av", &SplitCall::rpb_av)
+        .def("rpb_qk_backward", &SplitCall::rpb_qk_backward)
+        .def("rpb_av_backward", &SplitCall::rpb_av_backward);
+    m.def("rpb_qk", &rpb_qk, "cached relative-position-bias QK: attn, or None");
+    m.def("rpb_av", &rpb_av, "cached relative-position-bias AV: out, or None");
+    m.def("rpb_qk_bwd", &rpb_qk_bwd, "cached relative-position-bias QK backward: (dq, dk, drpb), or None");
+    m.def("rpb_av_bwd", &rpb_av_bwd, "cached relative-position-bias AV backward: (dattn, dv), or None");
+    m.def("rpb_register", &rpb_register, "register the SplitCall of a relative-position-bias op signature");
     m.def("qk", &qk, "cached split QK: attn, or None when the signature is not registered");
     m.def("av", &av, "cached split AV: out, or None when the signature is not registered");
     m.def("qk_bwd", &qk_bwd, "cached split QK backward: (dq, dk), or None");

@@ -571,9 +571,26 @@ def _rpb_table(rank, rpb, heads, kernel_size, dtype):
     return rpb.to(dtype).contiguous()
 
 
+def _register_rpb(b, op, rank, given, used, flag, outs, prob, kernel_size, dilation, out_shape=(), work_floats=0):
+    """Register a relative-position-bias op signature with the binding, as
+    _register_split (``used``: the tensors with layouts, the bias table aside)."""
+    if any(a is not u for a, u in zip(given, used)):
+        return
+    lays = [_lib.layout(t, rank, 1) for t in (*used[:5 if op != 4 else 2], *outs)]
+    blob = b"".join(bytes(x) for x in lays)
+    call = b.SplitCall(op, bytes(prob), blob, list(out_shape), False, int(work_floats))
+    b.rpb_register(rank, [t for t in given if t is not None], int(flag), kernel_size, dilation, call)
+
+
 def rpb_qk_forward(rank: int, q, k, rpb, kernel_size, dilation):
     """Logits ``[B, *sp, H, prod(kernel)]`` = q . k + rpb (unscaled), -inf at
     invalid neighbours."""
+    b = _lib.binding()
+    if b is not None:
+        r = b.rpb_qk(rank, q, k, rpb, kernel_size, dilation)
+        if r is not None:
+            return r
+    given = (q, k, rpb)
     _on_device(q, k, rpb)
     _same_dtype(q, k)
     q, k = _inner(q), _inner(k)
@@ -588,10 +605,19 @@ def rpb_qk_forward(rank: int, q, k, rpb, kernel_size, dilation):
     rc = _launch(q.device, _lib.load().natten_hip_rpb_qk_forward, _byref(prob), _lib.ptr(q), L(q), _lib.ptr(k),
                  L(k), _lib.ptr(table), _lib.ptr(attn), L(attn), _raw_stream(q.device))
     _lib.check(rc, "rpb_qk_forward")
+    if b is not None:
+        _register_rpb(b, 4, rank, given, (q, k, table), rpb is not None, (attn,), prob, kernel_size, dilation,
+                      out_shape=attn.shape)
     return attn
 
 
 def rpb_av_forward(rank: int, attn, v, kernel_size, dilation):
+    b = _lib.binding()
+    if b is not None:
+        r = b.rpb_av(rank, attn, v, kernel_size, dilation)
+        if r is not None:
+            return r
+    given = (attn, v)
     _on_device(attn, v)
     attn = _inner(attn.to(v.dtype))
     v = _inner(v)
@@ -601,11 +627,19 @@ def rpb_av_forward(rank: int, attn, v, kernel_size, dilation):
     rc = _launch(v.device, _lib.load().natten_hip_rpb_av_forward, _byref(prob), _lib.ptr(attn), L(attn),
                  _lib.ptr(v), L(v), _lib.ptr(out), L(out), _raw_stream(v.device))
     _lib.check(rc, "rpb_av_forward")
+    if b is not None:
+        _register_rpb(b, 5, rank, given, (attn, v), 0, (out,), prob, kernel_size, dilation)
     return out
 
 
 def rpb_qk_backward(rank: int, d_attn, q, k, with_rpb: bool, kernel_size, dilation):
     """``(dq, dk, drpb)``; drpb is None when the op had no bias."""
+    b = _lib.binding()
+    if b is not None:
+        r = b.rpb_qk_bwd(rank, d_attn, q, k, bool(with_rpb), kernel_size, dilation)
+        if r is not None:
+            return r
+    given = (d_attn, q, k)
     _on_device(d_attn, q, k)
     d_attn = _inner(d_attn.to(q.dtype))
     q, k = _inner(q), _inner(k)
@@ -625,10 +659,19 @@ def rpb_qk_backward(rank: int, d_attn, q, k, with_rpb: bool, kernel_size, dilati
                  _lib.ptr(q), L(q), _lib.ptr(k), L(k), _lib.ptr(dq), L(dq), _lib.ptr(dk), L(dk), _lib.ptr(drpb),
                  _lib.ptr(work), max(work_floats, 0), _raw_stream(q.device))
     _lib.check(rc, "rpb_qk_backward")
+    if b is not None:
+        _register_rpb(b, 6, rank, given, (d_attn, q, k), bool(with_rpb), (dq, dk), prob, kernel_size, dilation,
+                      out_shape=drpb.shape if drpb is not None else (), work_floats=max(work_floats, 0))
     return dq, dk, drpb
 
 
 def rpb_av_backward(rank: int, d_out, attn, v, kernel_size, dilation):
+    b = _lib.binding()
+    if b is not None:
+        r = b.rpb_av_bwd(rank, d_out, attn, v, kernel_size, dilation)
+        if r is not None:
+            return r
+    given = (d_out, attn, v)
     _on_device(d_out, attn, v)
     d_out = _inner(d_out.to(v.dtype))
     attn = _inner(attn.to(v.dtype))
@@ -641,6 +684,8 @@ def rpb_av_backward(rank: int, d_out, attn, v, kernel_size, dilation):
                  _lib.ptr(attn), L(attn), _lib.ptr(v), L(v), _lib.ptr(d_attn), L(d_attn), _lib.ptr(dv), L(dv),
                  _raw_stream(v.device))
     _lib.check(rc, "rpb_av_backward")
+    if b is not None:
+        _register_rpb(b, 7, rank, given, (d_out, attn, v), 0, (d_attn, dv), prob, kernel_size, dilation)
     return d_attn, dv
 
 

@@ -385,3 +385,49 @@ def test_rpb_matches_reference_fixtures(case):
     da, dv = torch.autograd.grad(out, [at, v], a["dout"].to(DEV))
     torch.testing.assert_close(da.cpu(), a["dattn"], atol=1e-5, rtol=1e-5, msg=lambda m: f"dattn: {m}")
     torch.testing.assert_close(dv.cpu(), a["dv"], atol=1e-5, rtol=1e-5, msg=lambda m: f"dv: {m}")
+
+
+@pytest.mark.parametrize("with_rpb", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rpb_ops_through_the_binding_cache(with_rpb, dtype, monkeypatch):
+    """The four relative-position-bias ops run wholly in the host binding
+    once their signature is registered: repeated calls succeed with the
+    Python layout builder switched off and give the bits of the first calls
+    and of the ctypes path (bias gradient and its workspace included)."""
+    from natten_mps_amd._core import _lib, hip
+
+    b = _lib.binding()
+    assert b is not None, "the host binding _natten_torch.so is not built"
+    rank, ks, dil = 2, (5, 5), (2, 1)
+    q, k, v = (_rand((2, 14, 12, 2, 32), 930 + i, dtype).to(DEV) for i in range(3))
+    rpb = _rand((2, 9, 9), 933, dtype).to(DEV) if with_rpb else None
+    da = _rand((2, 14, 12, 2, 25), 934, dtype).to(DEV)
+    do = _rand((2, 14, 12, 2, 32), 935, dtype).to(DEV)
+
+    def calls():
+        attn = hip.rpb_qk_forward(rank, q, k, rpb, ks, dil)
+        out = hip.rpb_av_forward(rank, attn.softmax(-1), v, ks, dil)
+        dq, dk, drpb = hip.rpb_qk_backward(rank, da, q, k, with_rpb, ks, dil)
+        dattn, dv = hip.rpb_av_backward(rank, do, attn.softmax(-1), v, ks, dil)
+        torch.cuda.synchronize()
+        return [attn, out, dq, dk, drpb, dattn, dv]
+
+    names = ("attn", "out", "dq", "dk", "drpb", "dattn", "dv")
+    b.clear()
+    first = calls()
+
+    def no_python_path(*a, **kw):
+        raise AssertionError("a registered relative-position-bias signature went through hip.py")
+
+    monkeypatch.setattr(_lib, "layout", no_python_path)
+    second = calls()
+    monkeypatch.undo()
+    monkeypatch.setattr(_lib, "_bind", None)
+    third = calls()
+    monkeypatch.undo()
+    for name, x, y, z in zip(names, first, second, third):
+        if x is None:
+            assert y is None and z is None, name
+            continue
+        assert torch.equal(x, y), f"{name}: binding cache differs from the first call"
+        assert torch.equal(x, z), f"{name}: binding differs from the ctypes path"
