@@ -88,10 +88,10 @@ struct LeanFwdArgs {
     const T *q, *k, *v;
     T* out;
     float* lse;
-    LeanLay lq, lk, ll;           // q and out; k and v; lse
+    LeanLay lq, lk, ll, lo;       // q; k and v; lse; out
     FastDiv heads, tiles, rep;    // workgroup decode; kv head = h / rep
     int d1, d2, K1, K2;
-    uint32_t qbytes, kbytes;      // byte range of one (batch, head) plane of q / k
+    uint32_t qbytes, kbytes, obytes;  // byte range of one (batch, head) plane of q / k / out
     float sc2;                    // scale * log2(e)
     Prob p;                       // for the exact recomputation
 };
@@ -137,6 +137,32 @@ __device__ __forceinline__ void lean_stage(__amdgpu_buffer_rsrc_t ra, __amdgpu_b
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(Xa + (i * 16 + hf * SPI) * D), 16, o, 0, 0,
                                                      0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(Xb + (i * 16 + hf * SPI) * D), 16, o, 0, 0,
+                                                     0);
+        }
+    }
+}
+
+// Staging of one operand's union rows [0, nst) (as lean_stage, one operand).
+template <typename T, int D>
+__device__ __forceinline__ void lean_stage1(__amdgpu_buffer_rsrc_t ra, T* Xa, int base, int step1, int step2, int U1,
+                                            int U2, int nst, int wave, int lane) {
+    constexpr int R = kRowD<T, D>;
+    constexpr int P = R / 8, SPI = 64 / P, HALVES = 16 / SPI;
+    uint32_t off[HALVES];
+    const int pp = lane % P;
+#pragma unroll
+    for (int hf = 0; hf < HALVES; ++hf) {
+        const int c = hf * SPI + lane / P;
+        const int slot = (wave & 1) * 16 + c;
+        off[hf] = c < U2 ? static_cast<uint32_t>(c * step2 + lean_piece<R>(pp, slot) * 16) : kLeanOOR;
+    }
+#pragma unroll 1
+    for (int i = wave; i < nst; i += kLeanWaves) {
+        const uint32_t ro = i < U1 ? static_cast<uint32_t>(base + i * step1) : kLeanOOR;
+#pragma unroll
+        for (int hf = 0; hf < HALVES; ++hf) {
+            const uint32_t o = off[hf] + ro;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(Xa + (i * 16 + hf * SPI) * D), 16, o, 0, 0,
                                                      0);
         }
     }
@@ -293,7 +319,7 @@ __device__ __forceinline__ void lean_redo_fwd(const void* kargs, int pos1, int p
     f32x4_t acc[D / 16];
     float lse_v;
     exact_forward<T, D>(A.p.scale, x, qp + qo, kp, ks, vp, ks, grp, acc, lse_v);
-    store_rows<T, D>(A.out + b * A.lq.b + h * A.lq.h, qo, grp, acc, 1.f);
+    store_rows<T, D>(A.out + b * A.lo.b + h * A.lo.h, pos1 * A.lo.s1 + pos2 * A.lo.s2, grp, acc, 1.f);
     if (grp == 0) A.lse[b * A.ll.b + h * A.ll.h + pos1 * A.ll.s1 + pos2 * A.ll.s2] = lse_v;
 }
 
@@ -406,9 +432,10 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
     const bool redo = valid && item_nonfinite(lane_sum(acc, lsum));
     if (valid) {
         const float inv = 1.f / lsum;
-        const __amdgpu_buffer_rsrc_t ro = lean_rsrc(a.out + qbo, a.qbytes);
+        const __amdgpu_buffer_rsrc_t ro = lean_rsrc(a.out + (b * a.lo.b + h * a.lo.h), a.obytes);
+        const int ooff = pos1 * a.lo.s1 + pos2 * a.lo.s2;
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db) lean_store4<T>(ro, qoff * ES, db, grp, acc[db], inv);
+        for (int db = 0; db < D / 16; ++db) lean_store4<T>(ro, ooff * ES, db, grp, acc[db], inv);
         if (grp == 0)
             a.lse[b * a.ll.b + h * a.ll.h + pos1 * a.ll.s1 + pos2 * a.ll.s2] = (m + __log2f(lsum)) * kLn2;
     }
@@ -423,11 +450,12 @@ struct LeanBwdArgs {
     const float *lse, *dlse;
     T *dq, *dk, *dv;
     float* delta;
-    LeanLay lq, lk, ll;           // q, out, dout, dq; k, v, dk, dv; lse, dlse, delta
+    LeanLay lq, lk, ll;           // q; k and v; lse, dlse and delta
+    LeanLay lo, ldo, ldq, ldk;    // out; dout; dq; dk and dv
     FastDiv heads, tiles, rep;    // task decode (q heads, spatial tiles)
     int nr;                       // LDS rows of a key tile
     int d1, d2, K1, K2;
-    uint32_t qbytes, kbytes;
+    uint32_t qbytes, kbytes, dobytes, dqbytes, dkbytes;  // plane byte ranges
     float sc2, scale;
     Prob p;
 };
@@ -443,12 +471,12 @@ __device__ __forceinline__ void lean_redo_bwd_q(const void* kargs, int pos1, int
     const long long lb = b * A.ll.b + h * A.ll.h + pos1 * A.ll.s1 + pos2 * A.ll.s2;
     const Strides3 ks{0, A.lk.s1, A.lk.s2};
     const int qo = pos1 * A.lq.s1 + pos2 * A.lq.s2;
-    const T* do_row = A.dout + qb + qo;
-    float di = exact_dot<T, D>(do_row, A.o + qb + qo);
+    const T* do_row = A.dout + (b * A.ldo.b + h * A.ldo.h + pos1 * A.ldo.s1 + pos2 * A.ldo.s2);
+    float di = exact_dot<T, D>(do_row, A.o + (b * A.lo.b + h * A.lo.h + pos1 * A.lo.s1 + pos2 * A.lo.s2));
     if (A.dlse) di -= A.dlse[lb];
     f32x4_t acc[D / 16];
     exact_backward_q<T, D>(A.p.scale, x, A.q + qb + qo, do_row, A.lse[lb], di, A.k + kb, ks, A.v + kb, ks, grp, acc);
-    store_rows<T, D>(A.dq + qb, qo, grp, acc, A.p.scale);
+    store_rows<T, D>(A.dq + (b * A.ldq.b + h * A.ldq.h), pos1 * A.ldq.s1 + pos2 * A.ldq.s2, grp, acc, A.p.scale);
 }
 
 template <typename T, int D>
@@ -458,27 +486,29 @@ __device__ __forceinline__ void lean_redo_bwd_kv(const void* kargs, int pos1, in
     x[0] = exact_axis(A.p.ax[0], 0);
     x[1] = exact_axis(A.p.ax[1], pos1);
     x[2] = exact_axis(A.p.ax[2], pos2);
-    const long long kb = b * A.lk.b + hk * A.lk.h;
-    const int ko = pos1 * A.lk.s1 + pos2 * A.lk.s2;
-    const Strides3 qs{0, A.lq.s1, A.lq.s2}, ls{0, A.ll.s1, A.ll.s2};
+    const long long kb = b * A.lk.b + hk * A.lk.h, gb = b * A.ldk.b + hk * A.ldk.h;
+    const int ko = pos1 * A.lk.s1 + pos2 * A.lk.s2, go = pos1 * A.ldk.s1 + pos2 * A.ldk.s2;
+    const Strides3 qs{0, A.lq.s1, A.lq.s2}, gs{0, A.ldo.s1, A.ldo.s2}, ls{0, A.ll.s1, A.ll.s2};
     f32x4_t g[D / 16];
     const int rep = A.p.rep;
     exact_zero(g);
 #pragma unroll 1
     for (int h = hk * rep; h < (hk + 1) * rep; ++h) {
         const long long qb = b * A.lq.b + h * A.lq.h, lb = b * A.ll.b + h * A.ll.h;
-        exact_backward_kv<T, D, true>(A.p.scale, x, A.k + kb + ko, A.v + kb + ko, A.q + qb, qs, A.dout + qb, qs,
+        const long long db = b * A.ldo.b + h * A.ldo.h;
+        exact_backward_kv<T, D, true>(A.p.scale, x, A.k + kb + ko, A.v + kb + ko, A.q + qb, qs, A.dout + db, gs,
                                       A.lse + lb, ls, A.delta + lb, ls, grp, g);
     }
-    store_rows<T, D>(A.dv + kb, ko, grp, g, 1.f);
+    store_rows<T, D>(A.dv + gb, go, grp, g, 1.f);
     exact_zero(g);
 #pragma unroll 1
     for (int h = hk * rep; h < (hk + 1) * rep; ++h) {
         const long long qb = b * A.lq.b + h * A.lq.h, lb = b * A.ll.b + h * A.ll.h;
-        exact_backward_kv<T, D, false>(A.p.scale, x, A.k + kb + ko, A.v + kb + ko, A.q + qb, qs, A.dout + qb, qs,
+        const long long db = b * A.ldo.b + h * A.ldo.h;
+        exact_backward_kv<T, D, false>(A.p.scale, x, A.k + kb + ko, A.v + kb + ko, A.q + qb, qs, A.dout + db, gs,
                                        A.lse + lb, ls, A.delta + lb, ls, grp, g);
     }
-    store_rows<T, D>(A.dk + kb, ko, grp, g, A.p.scale);
+    store_rows<T, D>(A.dk + gb, go, grp, g, A.p.scale);
 }
 
 // ---------------------------------------------------------------------------
@@ -517,15 +547,18 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
     const int qoff = pos1 * a.lq.s1 + pos2 * a.lq.s2;
     const long long qbo = b * a.lq.b + h * a.lq.h;
     const long long lo = b * a.ll.b + h * a.ll.h + pos1 * a.ll.s1 + pos2 * a.ll.s2;
+    const int goff = pos1 * a.ldo.s1 + pos2 * a.ldo.s2;
+    const long long gbo = b * a.ldo.b + h * a.ldo.h;
     uint4 qf[NF], gf[NF];
     {
         const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + qbo, a.qbytes);
-        const __amdgpu_buffer_rsrc_t rg = lean_rsrc(a.dout + qbo, a.qbytes);
+        const __amdgpu_buffer_rsrc_t rg = lean_rsrc(a.dout + gbo, a.dobytes);
 #pragma unroll
         for (int ks = 0; ks < NF; ++ks) {
             const uint32_t o = valid ? static_cast<uint32_t>(qoff * ES + lean_frag_off<T, D>(ks, grp)) : kLeanOOR;
+            const uint32_t og = valid ? static_cast<uint32_t>(goff * ES + lean_frag_off<T, D>(ks, grp)) : kLeanOOR;
             qf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 0));
-            gf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rg, o, 0, 0));
+            gf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rg, og, 0, 0));
         }
     }
     const float L2 = valid ? a.lse[lo] * kLog2e : 0.f;
@@ -576,7 +609,8 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
         }
         di = sum_rows(part) - dl;
         if (valid && !(__builtin_fabsf(di) <= __FLT_MAX__))
-            di = exact_dot<T, D>(a.dout + qbo + qoff, a.o + qbo + qoff) - dl;
+            di = exact_dot<T, D>(a.dout + gbo + goff,
+                                 a.o + (b * a.lo.b + h * a.lo.h + pos1 * a.lo.s1 + pos2 * a.lo.s2)) - dl;
     }
     if (valid && grp == 0) a.delta[lo] = di;
     f32x4_t acc[D / 16];
@@ -593,9 +627,10 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
     }
     const bool redo = valid && item_nonfinite(lane_sum(acc, 0.f));
     if (valid) {
-        const __amdgpu_buffer_rsrc_t rd = lean_rsrc(a.dq + qbo, a.qbytes);
+        const __amdgpu_buffer_rsrc_t rd = lean_rsrc(a.dq + (b * a.ldq.b + h * a.ldq.h), a.dqbytes);
+        const int dqoff = pos1 * a.ldq.s1 + pos2 * a.ldq.s2;
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db) lean_store4<T>(rd, qoff * ES, db, grp, acc[db], a.scale);
+        for (int db = 0; db < D / 16; ++db) lean_store4<T>(rd, dqoff * ES, db, grp, acc[db], a.scale);
     }
     if (redo) lean_redo_bwd_q<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, h, hk, grp);
 }
@@ -634,15 +669,17 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     const int pos1 = pr0 + kr * a.d1, pos2 = pc0 + kc * a.d2;
     const int koff = pos1 * a.lk.s1 + pos2 * a.lk.s2;
     const long long kbo = b * a.lk.b + hk * a.lk.h;
+    const int dkoff = pos1 * a.ldk.s1 + pos2 * a.ldk.s2;
+    const long long dkbo = b * a.ldk.b + hk * a.ldk.h;
     if (r[14]) {  // no query attends these keys
         if (valid) {
-            const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.dk + kbo, a.kbytes);
-            const __amdgpu_buffer_rsrc_t rv = lean_rsrc(a.dv + kbo, a.kbytes);
+            const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.dk + dkbo, a.dkbytes);
+            const __amdgpu_buffer_rsrc_t rv = lean_rsrc(a.dv + dkbo, a.dkbytes);
             const f32x4_t z = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int db = 0; db < D / 16; ++db) {
-                lean_store4<T>(rk, koff * ES, db, grp, z, 1.f);
-                lean_store4<T>(rv, koff * ES, db, grp, z, 1.f);
+                lean_store4<T>(rk, dkoff * ES, db, grp, z, 1.f);
+                lean_store4<T>(rv, dkoff * ES, db, grp, z, 1.f);
             }
         }
         return;
@@ -656,12 +693,20 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     };
     bool sin;
     const int sp = slot_pos(threadIdx.x, sin);
-    const long long qo = b * a.lq.b + h * a.lq.h;
+    const long long qo = b * a.lq.b + h * a.lq.h, go = b * a.ldo.b + h * a.ldo.h;
     const float sl = a.lse[lbase + sp], sd = a.delta[lbase + sp];
     {
-        lean_stage<T, D>(lean_rsrc(a.q + qo, a.qbytes), lean_rsrc(a.dout + qo, a.qbytes), Qs, Gs,
-                         (ur0 * a.lq.s1 + uc0 * a.lq.s2) * ES, a.lq.s1 * a.d1 * ES, a.lq.s2 * a.d2 * ES, U1, U2, nst,
-                         wave, lane);
+        const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + qo, a.qbytes), rg = lean_rsrc(a.dout + go, a.dobytes);
+        if (a.lq.s1 == a.ldo.s1 && a.lq.s2 == a.ldo.s2) {
+            lean_stage<T, D>(rq, rg, Qs, Gs, (ur0 * a.lq.s1 + uc0 * a.lq.s2) * ES, a.lq.s1 * a.d1 * ES,
+                             a.lq.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
+        } else {
+            // q and dO rows at different strides (a packed qkv tensor's views)
+            lean_stage1<T, D>(rq, Qs, (ur0 * a.lq.s1 + uc0 * a.lq.s2) * ES, a.lq.s1 * a.d1 * ES,
+                              a.lq.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
+            lean_stage1<T, D>(rg, Gs, (ur0 * a.ldo.s1 + uc0 * a.ldo.s2) * ES, a.ldo.s1 * a.d1 * ES,
+                              a.ldo.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
+        }
     }
     uint4 kf[NF], vf[NF];
     {
@@ -745,12 +790,12 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     }
     const bool redo = valid && item_nonfinite(lane_sum(gk, lane_sum(gv, 0.f)));
     if (valid) {
-        const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.dk + kbo, a.kbytes);
-        const __amdgpu_buffer_rsrc_t rv = lean_rsrc(a.dv + kbo, a.kbytes);
+        const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.dk + dkbo, a.dkbytes);
+        const __amdgpu_buffer_rsrc_t rv = lean_rsrc(a.dv + dkbo, a.dkbytes);
 #pragma unroll
         for (int db = 0; db < D / 16; ++db) {
-            lean_store4<T>(rk, koff * ES, db, grp, gk[db], a.scale);
-            lean_store4<T>(rv, koff * ES, db, grp, gv[db], 1.f);
+            lean_store4<T>(rk, dkoff * ES, db, grp, gk[db], a.scale);
+            lean_store4<T>(rv, dkoff * ES, db, grp, gv[db], 1.f);
         }
     }
     if (redo) lean_redo_bwd_kv<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, hk, grp);
@@ -815,31 +860,6 @@ __device__ __forceinline__ void lean_redo_wsum_key(const void* kargs, int pos1, 
     exact_wsum_key<T, D>(x, A.w + b * A.lw.b + h * A.lw.h, Strides3{0, A.lw.s1, A.lw.s2},
                          A.x + b * A.lx.b + h * A.lx.h, Strides3{0, A.lx.s1, A.lx.s2}, grp, acc);
     store_rows<T, D>(A.out + b * A.lo.b + h * A.lo.h, pos1 * A.lo.s1 + pos2 * A.lo.s2, grp, acc, A.mul);
-}
-
-// Staging of one operand's union rows [0, nst) (as lean_stage, one operand).
-template <typename T, int D>
-__device__ __forceinline__ void lean_stage1(__amdgpu_buffer_rsrc_t ra, T* Xa, int base, int step1, int step2, int U1,
-                                            int U2, int nst, int wave, int lane) {
-    constexpr int P = D / 8, SPI = 64 / P, HALVES = 16 / SPI;
-    uint32_t off[HALVES];
-    const int pp = lane % P;
-#pragma unroll
-    for (int hf = 0; hf < HALVES; ++hf) {
-        const int c = hf * SPI + lane / P;
-        const int slot = (wave & 1) * 16 + c;
-        off[hf] = c < U2 ? static_cast<uint32_t>(c * step2 + lean_piece<D>(pp, slot) * 16) : kLeanOOR;
-    }
-#pragma unroll 1
-    for (int i = wave; i < nst; i += kLeanWaves) {
-        const uint32_t ro = i < U1 ? static_cast<uint32_t>(base + i * step1) : kLeanOOR;
-#pragma unroll
-        for (int hf = 0; hf < HALVES; ++hf) {
-            const uint32_t o = off[hf] + ro;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)(Xa + (i * 16 + hf * SPI) * D), 16, o, 0, 0,
-                                                     0);
-        }
-    }
 }
 
 template <typename T, int D, int MAXC>
@@ -1231,8 +1251,10 @@ int lean_nch(int K1) { return (K1 + 2) / 2; }
 }  // namespace
 
 // Lean path eligibility: a 2-D (or 2-D-padded) problem at stride 1, head dim
-// 32 or 64 for q, k and v, 16-bit, K2 <= 9, K1 <= 9, per-axis extents below
-// 2^15, planes below 2^30 bytes, q/out and k/v sharing one layout each.
+// 32 or 64 for q, k and v, K2 <= 9, K1 <= 9, per-axis extents below 2^15,
+// planes below 2^30 bytes.  Every operand has its own layout, except that
+// the operands staged or stored together share one: kvside lists pairs
+// (k, v) and (dk, dv), and the fp32 rows (lse, delta, dlse) share one.
 bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list<Lay> qside,
                    std::initializer_list<Lay> kvside, std::initializer_list<Lay> rows) {
     if (!lean_switch() || !aligned || !(p.scale > 0.f) || !lean_static_lds_ok()) return false;
@@ -1244,13 +1266,17 @@ bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list
         const Axis& A = p.ax[a];
         if (A.st != 1 || A.k > 9 || A.len >= (1 << 15)) return false;
     }
-    if (!all_same(qside) || !all_same(kvside) || !all_same(rows)) return false;
-    for (const Lay& l : {*qside.begin(), *kvside.begin()}) {
-        if (l.s1 < 0 || l.s2 < 0 || l.b < 0 || l.h < 0) return false;
-        const long long v = ((static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
-                             (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + p.Dqk) *
-                            (dtype == NATTEN_F32 ? 4 : 2);
-        if (v >= (1LL << 30)) return false;
+    if (kvside.size() % 2 != 0 || !all_same(rows)) return false;
+    for (const Lay* l = kvside.begin(); l != kvside.end(); l += 2)
+        if (!same_lay(l[0], l[1])) return false;
+    for (const auto& side : {qside, kvside}) {
+        for (const Lay& l : side) {
+            if (l.s1 < 0 || l.s2 < 0 || l.b < 0 || l.h < 0) return false;
+            const long long v = ((static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
+                                 (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + p.Dqk) *
+                                (dtype == NATTEN_F32 ? 4 : 2);
+            if (v >= (1LL << 30)) return false;
+        }
     }
     // fp32 rows (lse, delta, dlse): in-plane element offsets in 31 bits
     const Lay& r = *rows.begin();
@@ -1269,7 +1295,7 @@ int lean_lds_audit(int* checked) {
 
 template <typename T, int D, int NCH>
 hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, const void* k, Lay lk,
-                        const void* v, void* o, float* lse, Lay ll, hipStream_t s) {
+                        const void* v, void* o, Lay lo, float* lse, Lay ll, hipStream_t s) {
     LeanFwdArgs<T> a{};
     a.rec = g->ptr;
     a.q = static_cast<const T*>(q);
@@ -1280,6 +1306,7 @@ hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, 
     a.lq = lean_lay(lq);
     a.lk = lean_lay(lk);
     a.ll = lean_lay(ll);
+    a.lo = lean_lay(lo);
     a.heads = make_fastdiv(p.Hq);
     a.tiles = make_fastdiv(g->ntiles);
     a.rep = make_fastdiv(p.rep);
@@ -1289,6 +1316,7 @@ hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, 
     a.K2 = p.ax[2].k;
     a.qbytes = plane_bytes(p, lq, D, sizeof(T));
     a.kbytes = plane_bytes(p, lk, D, sizeof(T));
+    a.obytes = plane_bytes(p, lo, D, sizeof(T));
     a.sc2 = p.scale * kLog2e;
     a.p = p;
     const long long blocks = static_cast<long long>(p.B) * p.Hq * g->ntiles;
@@ -1306,12 +1334,11 @@ hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, 
 hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
                         Lay lo, float* lse, Lay ll, int dtype, hipStream_t s) {
     (void)lv;
-    (void)lo;
     const int nch = lean_nch(p.ax[1].k);
     if (static_cast<long long>(p.B) * p.Hq * 4096 >= (1LL << 31)) return hipErrorNotSupported;
     const LeanGeo* g = lean_geometry(p, 0, nch, s);
     if (!g) return hipErrorNotSupported;
-#define NA_LF(T, DD, N) return lean_fwd_run<T, DD, N>(p, g, q, lq, k, lk, v, o, lse, ll, s)
+#define NA_LF(T, DD, N) return lean_fwd_run<T, DD, N>(p, g, q, lq, k, lk, v, o, lo, lse, ll, s)
 #define NA_LF_N(T, DD)          \
     switch (nch) {              \
         case 1: NA_LF(T, DD, 1); \
@@ -1336,8 +1363,8 @@ hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay
 
 template <typename T, int D>
 LeanBwdArgs<T> lean_bwd_args(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v,
-                             const void* o, const void* dout, const float* lse, Lay ll, const float* dlse, void* dq,
-                             void* dk, void* dv, float* delta) {
+                             const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
+                             const float* dlse, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, float* delta) {
     LeanBwdArgs<T> a{};
     a.q = static_cast<const T*>(q);
     a.k = static_cast<const T*>(k);
@@ -1353,6 +1380,10 @@ LeanBwdArgs<T> lean_bwd_args(const Prob& p, const void* q, Lay lq, const void* k
     a.lq = lean_lay(lq);
     a.lk = lean_lay(lk);
     a.ll = lean_lay(ll);
+    a.lo = lean_lay(lo);
+    a.ldo = lean_lay(ldo);
+    a.ldq = lean_lay(ldq);
+    a.ldk = lean_lay(ldk);
     a.rep = make_fastdiv(p.rep);
     a.d1 = p.ax[1].dil;
     a.d2 = p.ax[2].dil;
@@ -1360,6 +1391,9 @@ LeanBwdArgs<T> lean_bwd_args(const Prob& p, const void* q, Lay lq, const void* k
     a.K2 = p.ax[2].k;
     a.qbytes = plane_bytes(p, lq, D, sizeof(T));
     a.kbytes = plane_bytes(p, lk, D, sizeof(T));
+    a.dobytes = plane_bytes(p, ldo, D, sizeof(T));
+    a.dqbytes = plane_bytes(p, ldq, D, sizeof(T));
+    a.dkbytes = plane_bytes(p, ldk, D, sizeof(T));
     a.sc2 = p.scale * kLog2e;
     a.scale = p.scale;
     a.p = p;
@@ -1399,10 +1433,6 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
                          const float* dlse, Lay ldl, void* dq, Lay ldq, void* dk, Lay ldk, void* dv, Lay ldv,
                          float* delta, Lay lde, int dtype, hipStream_t s) {
     (void)lv;
-    (void)lo;
-    (void)ldo;
-    (void)ldq;
-    (void)ldk;
     (void)ldv;
     if (p.rep != 1) return hipErrorNotSupported;
     if (!same_lay(ll, lde) || (dlse && !same_lay(ll, ldl))) return hipErrorNotSupported;
@@ -1413,7 +1443,8 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
     if (!gq || !gk || gq->ntiles != gk->ntiles || gk->rows_max > 2 * (nch + 2)) return hipErrorNotSupported;
 #define NA_LB(T, DD, N)                                                                                           \
     return lean_bwd_run<T, DD, N>(p, gq, gk,                                                                      \
-                                  lean_bwd_args<T, DD>(p, q, lq, k, lk, v, o, dout, lse, ll, dlse, dq, dk, dv, delta), \
+                                  lean_bwd_args<T, DD>(p, q, lq, k, lk, v, o, lo, dout, ldo, lse, ll, dlse, dq, ldq, \
+                                                       dk, ldk, dv, delta),                                          \
                                   s)
 #define NA_LB_N(T, DD)          \
     switch (nch) {              \

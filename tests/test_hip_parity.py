@@ -203,6 +203,49 @@ def test_fused_strided_tile_path(case, dtype):
     assert torch.count_nonzero(grads[0][:, ~on]) == 0
 
 
+PACKED_LEAN = [
+    # spatial, heads, dim, kernel, dilation, causal, dtype
+    ((24, 32), 2, 32, (7, 7), (1, 1), (False, False), torch.bfloat16),
+    ((32, 24), 4, 64, (5, 3), (2, 1), (True, False), torch.float16),
+    ((24, 24), 2, 32, (5, 5), (1, 2), (False, True), torch.float32),
+]
+
+
+@pytest.mark.parametrize("do_layout", ["contiguous", "packed"])
+@pytest.mark.parametrize("case", PACKED_LEAN)
+def test_lean_tiles_on_packed_qkv_views(case, do_layout):
+    """q, k and v as views of one packed [B, H, W, 3, heads, D] tensor (the
+    layout the NeighborhoodAttention modules produce), with out, dq, dk and
+    dv contiguous and dO contiguous or a view of another packed tensor (then
+    at q's strides): the 2-D tile kernels take every operand at its own
+    strides (launches na_*_lean) and match the oracle."""
+    from natten_mps_amd import functional as F
+    from natten_mps_amd._core import _lib
+
+    sp, h, dim, ks, dil, causal, dtype = case
+    qkv, dbig = _inputs(19, [(2, *sp, 3, h, dim), (2, *sp, 3, h, dim)], dtype)
+    do = dbig[..., 1, :, :] if do_layout == "packed" else dbig[..., 1, :, :].contiguous()
+    leaf = qkv.to(DEV).requires_grad_(True)
+    q, k, v = leaf.permute(3, 0, 1, 2, 4, 5).unbind(0)
+    do_dev = dbig.to(DEV)[..., 1, :, :] if do_layout == "packed" else do.to(DEV)
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        out = F.na2d(q, k, v, kernel_size=ks, dilation=dil, is_causal=causal)
+        out.backward(do_dev)
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    launched = set(_lib.profile_read(reset=True))
+    assert {"na_fwd_lean", "na_bwd_q_lean", "na_bwd_kv_lean"} <= launched, launched
+    rq, rk, rv = (t.contiguous() for t in qkv.permute(3, 0, 1, 2, 4, 5).unbind(0))
+    ref, rgrads = _oracle_fwd_bwd(2, (rq, rk, rv), do, ks, (1, 1), dil, causal)
+    _close(out.detach().cpu(), ref, dtype, "out")
+    grad = leaf.grad.cpu()
+    for i, (n, b) in enumerate(zip(("dq", "dk", "dv"), rgrads)):
+        _close(grad[..., i, :, :], b, dtype, n)
+
+
 def test_lse_matches_logsumexp():
     from natten_mps_amd._core import hip
 
