@@ -71,8 +71,8 @@ __device__ __forceinline__ void redo_fwd(const void* kargs, int wg, int wave, in
     if constexpr (VARLEN) varlen_view(A.p, A.ts, A.lens, wg, pv, tv);
     const Prob& P = VARLEN ? pv : A.p;
     const TileShape& TS = VARLEN ? tv : A.ts;
-    const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
-    const LayK &ao = LAY == kLayGeneral ? A.lo : aq, &al = A.ll;
+    const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : kVAtK<LAY> ? A.lk : A.lv;
+    const LayK &ao = kOwnOut<LAY> ? A.lo : aq, &al = A.ll;
     int b, h0, h1, pos[3];
     if (!lane_position<false>(P, TS, wg, wave, col, b, h0, h1, pos)) return;
     ExactAxis x[3];
@@ -109,8 +109,8 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernFwd, D, WIDE) voi
     float* __restrict__ lse = args.lse;
     const LayK &lq = args.lq, &lk_in = args.lk, &lv_in = args.lv, &lo_in = args.lo, &ll = args.ll;
     const LayK& lk = LAY == kLayOne ? lq : lk_in;
-    const LayK& lv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : lv_in;
-    const LayK& lo = LAY == kLayGeneral ? lo_in : lq;
+    const LayK& lv = LAY == kLayOne ? lq : kVAtK<LAY> ? lk_in : lv_in;
+    const LayK& lo = kOwnOut<LAY> ? lo_in : lq;
     unsigned char* smem = lds_base();
     constexpr bool KEY_SIDE = false;
     T* Ks = reinterpret_cast<T*>(smem);
@@ -270,9 +270,9 @@ __device__ __forceinline__ void redo_bwd_q(const void* kargs, int wg, int wave, 
     if constexpr (VARLEN) varlen_view(A.p, A.ts, A.lens, wg, pv, tv);
     const Prob& P = VARLEN ? pv : A.p;
     const TileShape& TS = VARLEN ? tv : A.ts;
-    const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
-    const LayK &ao = LAY == kLayGeneral ? A.lo : aq, &ado = LAY == kLayGeneral ? A.ldo : aq;
-    const LayK &adq = LAY == kLayGeneral ? A.ldq : aq, &al = A.ll, &adl = LAY == kLayGeneral ? A.ldl : al;
+    const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : kVAtK<LAY> ? A.lk : A.lv;
+    const LayK &ao = kOwnOut<LAY> ? A.lo : aq, &ado = LAY == kLayGeneral ? A.ldo : ao;
+    const LayK &adq = LAY == kLayGeneral ? A.ldq : ao, &al = A.ll, &adl = LAY == kLayGeneral ? A.ldl : al;
     int b, h0, h1, pos[3];
     if (!lane_position<false>(P, TS, wg, wave, col, b, h0, h1, pos)) return;
     ExactAxis x[3];
@@ -321,10 +321,10 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdQ, D, WIDE) vo
     const LayK &lq = args.lq, &lk_in = args.lk, &lv_in = args.lv, &lo_in = args.lo, &ldo_in = args.ldo;
     const LayK &ll = args.ll, &ldl_in = args.ldl, &ldq_in = args.ldq, &lde_in = args.lde;
     const LayK& lk = LAY == kLayOne ? lq : lk_in;
-    const LayK& lv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : lv_in;
-    const LayK& lo = LAY == kLayGeneral ? lo_in : lq;
-    const LayK& ldo = LAY == kLayGeneral ? ldo_in : lq;
-    const LayK& ldq = LAY == kLayGeneral ? ldq_in : lq;
+    const LayK& lv = LAY == kLayOne ? lq : kVAtK<LAY> ? lk_in : lv_in;
+    const LayK& lo = kOwnOut<LAY> ? lo_in : lq;
+    const LayK& ldo = LAY == kLayGeneral ? ldo_in : lo;
+    const LayK& ldq = LAY == kLayGeneral ? ldq_in : lo;
     const LayK& ldl = LAY == kLayGeneral ? ldl_in : ll;
     const LayK& lde = LAY == kLayGeneral ? lde_in : ll;
     unsigned char* smem = lds_base();
@@ -548,10 +548,10 @@ __device__ __forceinline__ void redo_bwd_kv(const void* kargs, int wg, int wave,
     if constexpr (VARLEN) varlen_view(A.p, A.ts, A.lens, wg, pv, tv);
     const Prob& P = VARLEN ? pv : A.p;
     const TileShape& TS = VARLEN ? tv : A.ts;
-    const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.lv;
+    const LayK &aq = A.lq, &ak = LAY == kLayOne ? aq : A.lk, &av = LAY == kLayOne ? aq : kVAtK<LAY> ? A.lk : A.lv;
     const LayK& adk = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.ldk;
-    const LayK& adv = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : A.ldv;
-    const LayK &ado = LAY == kLayGeneral ? A.ldo : aq, &al = A.ll, &ade = LAY == kLayGeneral ? A.lde : al;
+    const LayK& adv = LAY == kLayOne ? aq : LAY == kLayTwo ? A.lk : LAY == kLayFour ? A.ldk : A.ldv;
+    const LayK &ado = kOwnOut<LAY> ? A.ldo : aq, &al = A.ll, &ade = LAY == kLayGeneral ? A.lde : al;
     int b, h0, h1, pos[3];
     if (!lane_position<true>(P, TS, wg, wave, col, b, h0, h1, pos)) return;
     ExactAxis x[3];
@@ -598,10 +598,10 @@ __global__ __launch_bounds__(64 * kMaxWaves) NA_OCCUPANCY(kKernBwdKV, D, WIDE) v
     const LayK &lq = args.lq, &lk_in = args.lk, &lv_in = args.lv, &ldo_in = args.ldo, &ll = args.ll;
     const LayK &lde_in = args.lde, &ldk_in = args.ldk, &ldv_in = args.ldv;
     const LayK& lk = LAY == kLayOne ? lq : lk_in;
-    const LayK& lv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : lv_in;
+    const LayK& lv = LAY == kLayOne ? lq : kVAtK<LAY> ? lk_in : lv_in;
     const LayK& ldk = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : ldk_in;
-    const LayK& ldv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : ldv_in;
-    const LayK& ldo = LAY == kLayGeneral ? ldo_in : lq;
+    const LayK& ldv = LAY == kLayOne ? lq : LAY == kLayTwo ? lk_in : LAY == kLayFour ? ldk_in : ldv_in;
+    const LayK& ldo = kOwnOut<LAY> ? ldo_in : lq;
     const LayK& lde = LAY == kLayGeneral ? lde_in : ll;
     unsigned char* smem = lds_base();
     constexpr bool KEY_SIDE = true;
@@ -1658,6 +1658,8 @@ hipError_t launch_fwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
             return launch_fwd<T, D, kLayOne, false>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, nullptr, s);
         case kLayTwo:
             return launch_fwd<T, D, kLayTwo, false>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, nullptr, s);
+        case kLayFour:
+            return launch_fwd<T, D, kLayFour, false>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, nullptr, s);
         default:
             return launch_fwd<T, D, kLayGeneral, false>(p, q, lq, k, lk, v, lv, o, lo, lse, ll, nullptr, s);
     }
@@ -1757,6 +1759,8 @@ hipError_t launch_bwd(const Prob& p, const void* q, Lay lq, const void* k, Lay l
             NA_BWD_LAY(kLayOne);
         case kLayTwo:
             NA_BWD_LAY(kLayTwo);
+        case kLayFour:
+            NA_BWD_LAY(kLayFour);
         default:
             NA_BWD_LAY(kLayGeneral);
     }
@@ -2034,6 +2038,7 @@ void audit_dim(LdsAudit& a) {
     audit_fused<T, D, kLayGeneral>(a);
     audit_fused<T, D, kLayOne>(a);
     audit_fused<T, D, kLayTwo>(a);
+    audit_fused<T, D, kLayFour>(a);
     audit_one(k_dot_mfma<T, D, true>, "k_dot_mfma", a);
     audit_one(k_dot_mfma<T, D, false>, "k_dot_mfma", a);
     audit_one(k_wsum_mfma<T, D, true>, "k_wsum_mfma", a);
@@ -2063,6 +2068,7 @@ void audit_dim96(LdsAudit& a) {
     audit_fused<T, 96, kLayGeneral>(a);
     audit_fused<T, 96, kLayOne>(a);
     audit_fused<T, 96, kLayTwo>(a);
+    audit_fused<T, 96, kLayFour>(a);
     audit_varlen<T, 96>(a);
 }
 

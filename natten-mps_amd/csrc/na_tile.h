@@ -680,9 +680,17 @@ __device__ __forceinline__ int kv_head(const TileShape& ts, int h) { return ts.r
 // kLayOne: every 16-bit operand has q's layout and every fp32 row operand
 // lse's.  kLayTwo: the query-side 16-bit operands (q, out, dO, dq) share q's
 // layout, the key-side ones (k, v, dk, dv) k's, the fp32 rows lse's (GQA).
-// kLayGeneral: each operand its own.  Fewer distinct layouts keep fewer
-// scalar registers live, which at head dim 32 removes the SGPR spills.
-constexpr int kLayGeneral = 0, kLayOne = 1, kLayTwo = 2;
+// kLayFour: q its own; k and v one; out, dO and dq one; dk and dv one (q,
+// k and v as views of one packed tensor, the gradients and out contiguous,
+// as the nn modules call).  kLayGeneral: each operand its own.  Fewer
+// distinct layouts keep fewer registers live, which at head dim 32 removes
+// the SGPR spills and at head dim 64 the VGPR spills of the dQ kernel.
+constexpr int kLayGeneral = 0, kLayOne = 1, kLayTwo = 2, kLayFour = 3;
+// v read at k's layout; out (and what shares it) at its own layout.
+template <int LAY>
+constexpr bool kVAtK = LAY == kLayTwo || LAY == kLayFour;
+template <int LAY>
+constexpr bool kOwnOut = LAY == kLayGeneral || LAY == kLayFour;
 
 // Waves per SIMD an instance is built for (4: at most 128 VGPRs, 5: at most
 // 96; 1: no constraint).  Saying so lets the register allocator trade VGPRs
@@ -1064,8 +1072,16 @@ bool all_same(std::initializer_list<Lay> g) {
 // and its fp32 row operands (first of each list is the one the kernel reads).
 int layout_group(std::initializer_list<Lay> qside, std::initializer_list<Lay> kvside,
                  std::initializer_list<Lay> rows) {
-    if (!all_same(qside) || !all_same(kvside) || !all_same(rows)) return kLayGeneral;
-    return same_lay(*qside.begin(), *kvside.begin()) ? kLayOne : kLayTwo;
+    if (!all_same(rows)) return kLayGeneral;
+    if (all_same(qside) && all_same(kvside)) return same_lay(*qside.begin(), *kvside.begin()) ? kLayOne : kLayTwo;
+    // kLayFour: qside = q, then out, dO, dq sharing one layout; kvside = k, v,
+    // then dk, dv, each pair sharing one
+    if (kvside.size() % 2 != 0) return kLayGeneral;
+    for (const Lay* l = kvside.begin(); l != kvside.end(); l += 2)
+        if (!same_lay(l[0], l[1])) return kLayGeneral;
+    for (const Lay* l = qside.begin() + 1; l != qside.end(); ++l)
+        if (!same_lay(*l, qside.begin()[1])) return kLayGeneral;
+    return kLayFour;
 }
 
 }  // namespace

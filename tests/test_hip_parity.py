@@ -246,6 +246,62 @@ def test_lean_tiles_on_packed_qkv_views(case, do_layout):
         _close(grad[..., i, :, :], b, dtype, n)
 
 
+PACKED_TILES = [
+    # rank, spatial, heads q / kv, dim, kernel, dilation, causal, dtype
+    (3, (6, 10, 12), 4, 4, 64, (3, 5, 5), (1, 2, 1), (False, False, False), torch.bfloat16),
+    (3, (5, 8, 9), 2, 2, 32, (3, 3, 5), (1, 1, 1), (True, False, False), torch.float16),
+    (1, (300,), 4, 2, 64, (9,), (2,), (True,), torch.bfloat16),
+    (1, (257,), 6, 3, 32, (13,), (1,), (False,), torch.float16),
+]
+
+
+@pytest.mark.parametrize("case", PACKED_TILES)
+def test_tile_kernels_on_packed_views(case):
+    """The nn modules' layouts on the general tile kernels: q, k and v as
+    views of one packed [B, *sp, 3, heads, D] tensor, or (GQA) q contiguous
+    and k, v views of a packed [B, *sp, 2, kv heads, D] tensor; out and the
+    gradients contiguous.  These run in the layout group that keeps q; k and
+    v; out, dO and dq; dk and dv at one layout each, and match the oracle."""
+    from natten_mps_amd import functional as F
+    from natten_mps_amd._core import _lib
+
+    rank, sp, hq, hkv, dim, ks, dil, causal, dtype = case
+    perm = (rank + 1, 0, *range(1, rank + 1), rank + 2, rank + 3)
+    if hq == hkv:
+        (packed, do) = _inputs(23, [(2, *sp, 3, hq, dim), (2, *sp, hq, dim)], dtype)
+        leaves = [packed.to(DEV).requires_grad_(True)]
+        q, k, v = leaves[0].permute(*perm).unbind(0)
+        rq, rk, rv = (t.contiguous() for t in packed.permute(*perm).unbind(0))
+    else:
+        (qc, packed, do) = _inputs(23, [(2, *sp, hq, dim), (2, *sp, 2, hkv, dim), (2, *sp, hq, dim)], dtype)
+        leaves = [qc.to(DEV).requires_grad_(True), packed.to(DEV).requires_grad_(True)]
+        q = leaves[0]
+        k, v = leaves[1].permute(*perm).unbind(0)
+        rq = qc
+        rk, rv = (t.contiguous() for t in packed.permute(*perm).unbind(0))
+    fn = getattr(F, f"na{rank}d")
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        out = fn(q, k, v, kernel_size=ks, dilation=dil, is_causal=causal)
+        out.backward(do.to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    launched = set(_lib.profile_read(reset=True))
+    assert {"na_fwd_mfma", "na_bwd_q_mfma", "na_bwd_kv_mfma"} <= launched, launched
+    ref, (gq, gk, gv) = _oracle_fwd_bwd(rank, (rq, rk, rv), do, ks, (1,) * rank, dil, causal)
+    _close(out.detach().cpu(), ref, dtype, "out")
+    if hq == hkv:
+        grad = leaves[0].grad.cpu()
+        got = [grad[..., i, :, :] for i in range(3)]
+    else:
+        grad = leaves[1].grad.cpu()
+        got = [leaves[0].grad.cpu(), grad[..., 0, :, :], grad[..., 1, :, :]]
+    for n, a, b in zip(("dq", "dk", "dv"), got, (gq, gk, gv)):
+        _close(a, b, dtype, n)
+
+
 def test_lse_matches_logsumexp():
     from natten_mps_amd._core import hip
 

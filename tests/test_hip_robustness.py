@@ -52,14 +52,14 @@ def _launched(run):
 
 
 def test_mfma_kernels_have_no_static_lds():
-    """Every tile-kernel instance (2 dtypes x 3 head dims x 18 fused, 4
-    global-key, 6 variable-length and 16 split instances (6 of them
-    single-step, 4 with the relative-position bias), 2 dtypes x 28
-    fused, global-key and variable-length instances at head dim 96, and
-    2 dtypes x 4 head dims x 6 single-step (FLAT) fused instances, the lean
+    """Every tile-kernel instance (2 dtypes x 3 head dims x 24 fused (4
+    layout groups), 4 global-key, 6 variable-length and 16 split instances
+    (6 of them single-step, 4 with the relative-position bias), 2 dtypes x
+    34 fused, global-key and variable-length instances at head dim 96, and
+    2 dtypes x 4 head dims x 9 single-step (FLAT) fused instances, the lean
     2-D kernels: 2 dtypes x 2 head dims x 5 chunk counts x forward, dQ,
     dK/dV and the split key side, and fp32 x 2 head dims x 5 chunk counts x
-    forward, dQ and dK/dV, and 2 dtypes x 4 head dims x 8 dQ instances that
+    forward, dQ and dK/dV, and 2 dtypes x 4 head dims x 11 dQ instances that
     take delta from P dP) reports 0 bytes of static LDS, so the operands the kernels
     stage at a constant LDS offset cannot overlap a __shared__ array; with
     one that did, the library would refuse the tile path."""
@@ -67,7 +67,7 @@ def test_mfma_kernels_have_no_static_lds():
 
     n = ctypes.c_int32(0)
     assert _lib.load().natten_hip_mfma_lds_check(ctypes.byref(n)) == 1
-    assert n.value == 2 * 3 * (18 + 4 + 6 + 16) + 2 * (18 + 4 + 6) + 2 * 4 * 6 + 2 * 2 * 5 * 4 + 2 * 5 * 3 + 2 * 4 * 8
+    assert n.value == 2 * 3 * (24 + 4 + 6 + 16) + 2 * (24 + 4 + 6) + 2 * 4 * 9 + 2 * 2 * 5 * 4 + 2 * 5 * 3 + 2 * 4 * 11
 
 
 # ---------------------------------------------------------------------------
