@@ -76,11 +76,66 @@ typedef unsigned int v2u32_t __attribute__((ext_vector_type(2)));
 typedef unsigned int v4u32_t __attribute__((ext_vector_type(4)));
 
 // Layout of one operand group: batch and head strides, and the element
-// strides of the two spatial axes (axis 0 of the padded problem has extent 1).
+// strides of the spatial axes (axis 0 of a 2-D problem has extent 1).
 struct LeanLay {
     long long b, h;
-    int s1, s2;
+    int s1, s2, s0;
 };
+
+// Workgroup decode of the tile kernels.  2-D: heads fastest, then the tile,
+// then the batch.  3-D: the heads of a group of hg fastest, then the
+// in-plane tile, then the depth position, then the head group, then the
+// batch -- the tiles of neighbouring depths, which stage the same planes,
+// run close together on one XCD while the planes of only hg heads are live.
+struct LeanTask {
+    int b, h, t, z;
+};
+
+struct LeanDecode {
+    FastDiv heads, tiles;       // 2-D
+    FastDiv hg, zlen, hgroups;  // 3-D: heads per group, depth extent, groups
+};
+
+template <bool D3>
+__device__ __forceinline__ LeanTask lean_task(const LeanDecode& d, int x) {
+    LeanTask k;
+    if constexpr (!D3) {
+        const int bt = fdiv(x, d.heads);
+        k.h = x - bt * static_cast<int>(d.heads.d);
+        k.b = fdiv(bt, d.tiles);
+        k.t = bt - k.b * static_cast<int>(d.tiles.d);
+        k.z = 0;
+    } else {
+        const int x1 = fdiv(x, d.hg);
+        const int hl = x - x1 * static_cast<int>(d.hg.d);
+        const int x2 = fdiv(x1, d.tiles);
+        k.t = x1 - x2 * static_cast<int>(d.tiles.d);
+        const int x3 = fdiv(x2, d.zlen);
+        k.z = x2 - x3 * static_cast<int>(d.zlen.d);
+        k.b = fdiv(x3, d.hgroups);
+        k.h = (x3 - k.b * static_cast<int>(d.hgroups.d)) * static_cast<int>(d.hg.d) + hl;
+    }
+    return k;
+}
+
+// Depth planes of a 3-D tile: planes z0 + j d for j in [j0, n).  Query
+// tiles: the key planes of the window of depth z (a causal window's planes
+// below 0 skipped); key tiles: the query planes whose windows hold z.
+struct LeanDepth {
+    int z0, d, j0, n;
+};
+
+__device__ __forceinline__ LeanDepth lean_depth_q(const Axis& A, int z) {
+    LeanDepth w{axis_first(A, z), A.dil, 0, A.k};
+    while (w.z0 + w.j0 * w.d < 0) ++w.j0;
+    return w;
+}
+
+__device__ __forceinline__ LeanDepth lean_depth_k(const Axis& A, int z) {
+    int lo, hi;
+    if (!axis_query_range(A, z, lo, hi)) return LeanDepth{z, A.dil, 0, 0};
+    return LeanDepth{z, A.dil, lo, hi + 1};
+}
 
 template <typename T>
 struct LeanFwdArgs {
@@ -89,7 +144,8 @@ struct LeanFwdArgs {
     T* out;
     float* lse;
     LeanLay lq, lk, ll, lo;       // q; k and v; lse; out
-    FastDiv heads, tiles, rep;    // workgroup decode; kv head = h / rep
+    LeanDecode dec;               // workgroup decode
+    FastDiv rep;                  // kv head = h / rep
     int d1, d2, K1, K2;
     uint32_t qbytes, kbytes, obytes;  // byte range of one (batch, head) plane of q / k / out
     float sc2;                    // scale * log2(e)
@@ -305,28 +361,32 @@ __device__ __forceinline__ void lean_colbias(int clo, int K2, int grp, f32x4_t (
 }
 
 template <typename T, int D>
-__device__ __forceinline__ void lean_redo_fwd(const void* kargs, int pos1, int pos2, int b, int h, int hk, int grp) {
+__device__ __forceinline__ void lean_redo_fwd(const void* kargs, int z, int pos1, int pos2, int b, int h, int hk,
+                                              int grp) {
     const LeanFwdArgs<T>& A = *static_cast<const LeanFwdArgs<T>*>(kargs);
     ExactAxis x[3];
-    x[0] = exact_axis(A.p.ax[0], 0);
+    x[0] = exact_axis(A.p.ax[0], z);
     x[1] = exact_axis(A.p.ax[1], pos1);
     x[2] = exact_axis(A.p.ax[2], pos2);
     const T* qp = A.q + b * A.lq.b + h * A.lq.h;
     const T* kp = A.k + b * A.lk.b + hk * A.lk.h;
     const T* vp = A.v + b * A.lk.b + hk * A.lk.h;
-    const Strides3 ks{0, A.lk.s1, A.lk.s2};
-    const int qo = pos1 * A.lq.s1 + pos2 * A.lq.s2;
+    const Strides3 ks{A.lk.s0, A.lk.s1, A.lk.s2};
+    const int qo = z * A.lq.s0 + pos1 * A.lq.s1 + pos2 * A.lq.s2;
     f32x4_t acc[D / 16];
     float lse_v;
     exact_forward<T, D>(A.p.scale, x, qp + qo, kp, ks, vp, ks, grp, acc, lse_v);
-    store_rows<T, D>(A.out + b * A.lo.b + h * A.lo.h, pos1 * A.lo.s1 + pos2 * A.lo.s2, grp, acc, 1.f);
-    if (grp == 0) A.lse[b * A.ll.b + h * A.ll.h + pos1 * A.ll.s1 + pos2 * A.ll.s2] = lse_v;
+    store_rows<T, D>(A.out + b * A.lo.b + h * A.lo.h, z * A.lo.s0 + pos1 * A.lo.s1 + pos2 * A.lo.s2, grp, acc, 1.f);
+    if (grp == 0) A.lse[b * A.ll.b + h * A.ll.h + z * A.ll.s0 + pos1 * A.ll.s1 + pos2 * A.ll.s2] = lse_v;
 }
 
 // ---------------------------------------------------------------------------
-// Forward.  NCH chunks (2 NCH >= K1 + 1 union rows) per wave.
+// Forward.  NCH chunks (2 NCH >= K1 + 1 union rows) per wave.  3-D (D3):
+// the tile walks its window's key planes, staging each plane's union in
+// turn, with one online-softmax rescale per plane; 2-D: one plane, one
+// maximum, no rescale.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int NCH>
+template <typename T, int D, int NCH, bool D3 = false>
 __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) {
     constexpr int NR = 2 * NCH + 6, NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
     unsigned char* smem = lds_base();
@@ -334,30 +394,31 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
     T* Vs = Ks + NR * 16 * D;
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int x = xcd_block(blockIdx.x, gridDim.x);
-    const int bt = fdiv(x, a.heads);
-    const int h = x - bt * static_cast<int>(a.heads.d);
-    const int b = fdiv(bt, a.tiles);
-    const int t = bt - b * static_cast<int>(a.tiles.d);
+    const LeanTask tk = lean_task<D3>(a.dec, xcd_block(blockIdx.x, gridDim.x));
+    const int b = tk.b, h = tk.h, t = tk.t, z = tk.z;
     const int hk = a.rep.d == 1 ? h : fdiv(h, a.rep);
     const int* r = a.rec + t * kLeanRec;
     const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
     const int U1 = ext & 0xFF, U2 = (ext >> 8) & 0xFF, E1 = (ext >> 16) & 0xFF, E2 = (ext >> 24) & 0xFF;
+    LeanDepth dw{0, 0, 0, 1};
+    if constexpr (D3) dw = lean_depth_q(a.p.ax[0], z);
 
-    // stage the union's K and V rows
-    {
-        const long long kvo = b * a.lk.b + hk * a.lk.h;
-        const int s1 = a.lk.s1 * a.d1 * ES, s2 = a.lk.s2 * a.d2 * ES;
-        lean_stage<T, D>(lean_rsrc(a.k + kvo, a.kbytes), lean_rsrc(a.v + kvo, a.kbytes), Ks, Vs,
-                         (ur0 * a.lk.s1 + uc0 * a.lk.s2) * ES, s1, s2, U1, U2, nst, wave, lane);
-    }
+    // stage the union's K and V rows (of the first key plane)
+    const long long kvo = b * a.lk.b + hk * a.lk.h;
+    const int kst = (ur0 * a.lk.s1 + uc0 * a.lk.s2) * ES, ks1 = a.lk.s1 * a.d1 * ES, ks2 = a.lk.s2 * a.d2 * ES;
+    const auto stage = [&](int j) {
+        const long long o = kvo + static_cast<long long>(dw.z0 + j * dw.d) * a.lk.s0;
+        lean_stage<T, D>(lean_rsrc(a.k + o, a.kbytes), lean_rsrc(a.v + o, a.kbytes), Ks, Vs, kst, ks1, ks2, U1, U2,
+                         nst, wave, lane);
+    };
+    stage(dw.j0);
 
     // the lane's query and its fragments
     const int qr = 2 * wave + (col >> 3), qc = col & 7;
     const bool valid = qr < E1 && qc < E2;
     const int pos1 = pr0 + qr * a.d1, pos2 = pc0 + qc * a.d2;
     const int qoff = pos1 * a.lq.s1 + pos2 * a.lq.s2;
-    const long long qbo = b * a.lq.b + h * a.lq.h;
+    const long long qbo = b * a.lq.b + h * a.lq.h + static_cast<long long>(z) * a.lq.s0;
     uint4 qf[NF];
     {
         const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + qbo, a.qbytes);
@@ -384,62 +445,85 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
 #pragma unroll
         for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<T, D>(first, lane, hi, db);
 
-    wait_loads();
-    __syncthreads();
-
     const unsigned char* Kb = reinterpret_cast<const unsigned char*>(Ks);
     const unsigned char* Vb = reinterpret_cast<const unsigned char*>(Vs);
-    f32x4_t s[NCH][2];
-    bool rv[NCH];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        s[c][0] = lean_score<T, D>(Kb, aoff, c, 0, qf, cb[0]);
-        s[c][1] = lean_score<T, D>(Kb, aoff, c, 1, qf, cb[1]);
-        const int row = 2 * c + (grp >> 1) - rlo;
-        rv[c] = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1);
-        mx = fmaxp(mx, rv[c] ? max8(s[c]) : -INFINITY);
-    }
-    const float m = max_rows(mx) * a.sc2;
-    const float mref = m == -INFINITY ? 0.f : m;
     f32x4_t acc[D / 16], lacc = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float lpart = 0.f;
+    float lpart = 0.f, m = -INFINITY;
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int j = dw.j0; j < dw.n; ++j) {
+        wait_loads();
+        __syncthreads();
+        f32x4_t s[NCH][2];
+        bool rv[NCH];
+        float mx = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const float off = rv[c] ? -mref : -INFINITY;
+        for (int c = 0; c < NCH; ++c) {
+            s[c][0] = lean_score<T, D>(Kb, aoff, c, 0, qf, cb[0]);
+            s[c][1] = lean_score<T, D>(Kb, aoff, c, 1, qf, cb[1]);
+            const int row = 2 * c + (grp >> 1) - rlo;
+            rv[c] = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1);
+            mx = fmaxp(mx, rv[c] ? max8(s[c]) : -INFINITY);
+        }
+        float mref;
+        if constexpr (D3) {
+            // online softmax over the planes: one rescale per plane
+            const float mnew = fmaxp(m, max_rows(mx) * a.sc2);
+            mref = mnew == -INFINITY ? 0.f : mnew;
+            const float corr = __builtin_amdgcn_exp2f(m - mref);
+            m = mnew;
+            lacc *= corr;
+            lpart *= corr;
 #pragma unroll
-        for (int bb = 0; bb < 2; ++bb)
+            for (int db = 0; db < D / 16; ++db) acc[db] *= corr;
+        } else {
+            m = max_rows(mx) * a.sc2;
+            mref = m == -INFINITY ? 0.f : m;
+        }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s[c][bb][i] = __builtin_amdgcn_exp2f(fmaf(s[c][bb][i], a.sc2, off));
-        if constexpr (kF32<T>) {
-            // row sums of the probabilities themselves, in slot order
+        for (int c = 0; c < NCH; ++c) {
+            const float off = rv[c] ? -mref : -INFINITY;
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) lpart += s[c][bb][i];
-            lean_acc<T, D>(Vb, toff, c, s[c], acc);
-        } else {
-            // row sums from one more MFMA against ones: the same rounded P as the product
-            const uint4 pk = pack8<T>(s[c]);
-            lean_accumulate<T, D>(Vb, toff, c, pk, acc);
-            const uint4 ones = make_uint4(Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes);
-            lacc = Mma<T>::run(ones, pk, lacc);
+                for (int i = 0; i < 4; ++i) s[c][bb][i] = __builtin_amdgcn_exp2f(fmaf(s[c][bb][i], a.sc2, off));
+            if constexpr (kF32<T>) {
+                // row sums of the probabilities themselves, in slot order
+#pragma unroll
+                for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) lpart += s[c][bb][i];
+                lean_acc<T, D>(Vb, toff, c, s[c], acc);
+            } else {
+                // row sums from one more MFMA against ones: the same rounded P as the product
+                const uint4 pk = pack8<T>(s[c]);
+                lean_accumulate<T, D>(Vb, toff, c, pk, acc);
+                const uint4 ones = make_uint4(Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes, Mma<T>::kOnes);
+                lacc = Mma<T>::run(ones, pk, lacc);
+            }
+        }
+        if constexpr (D3) {
+            if (j + 1 < dw.n) {
+                __syncthreads();  // the plane is no longer read
+                stage(j + 1);
+            }
         }
     }
     const float lsum = kF32<T> ? sum_rows(lpart) : lacc[0];
     const bool redo = valid && item_nonfinite(lane_sum(acc, lsum));
     if (valid) {
         const float inv = 1.f / lsum;
-        const __amdgpu_buffer_rsrc_t ro = lean_rsrc(a.out + (b * a.lo.b + h * a.lo.h), a.obytes);
+        const __amdgpu_buffer_rsrc_t ro =
+            lean_rsrc(a.out + (b * a.lo.b + h * a.lo.h + static_cast<long long>(z) * a.lo.s0), a.obytes);
         const int ooff = pos1 * a.lo.s1 + pos2 * a.lo.s2;
 #pragma unroll
         for (int db = 0; db < D / 16; ++db) lean_store4<T>(ro, ooff * ES, db, grp, acc[db], inv);
         if (grp == 0)
-            a.lse[b * a.ll.b + h * a.ll.h + pos1 * a.ll.s1 + pos2 * a.ll.s2] = (m + __log2f(lsum)) * kLn2;
+            a.lse[b * a.ll.b + h * a.ll.h + static_cast<long long>(z) * a.ll.s0 + pos1 * a.ll.s1 + pos2 * a.ll.s2] =
+                (m + __log2f(lsum)) * kLn2;
     }
-    if (redo) lean_redo_fwd<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, h, hk, grp);
+    if (redo) lean_redo_fwd<T, D>(kernargs(), opaque(z), opaque(pos1), opaque(pos2), b, h, hk, grp);
 }
 
 
@@ -452,43 +536,48 @@ struct LeanBwdArgs {
     float* delta;
     LeanLay lq, lk, ll;           // q; k and v; lse, dlse and delta
     LeanLay lo, ldo, ldq, ldk;    // out; dout; dq; dk and dv
-    FastDiv heads, tiles, rep;    // task decode (q heads, spatial tiles)
+    LeanDecode dec;               // task decode
+    FastDiv rep;
     int nr;                       // LDS rows of a key tile
     int d1, d2, K1, K2;
-    uint32_t qbytes, kbytes, dobytes, dqbytes, dkbytes;  // plane byte ranges
+    uint32_t qbytes, kbytes, obytes, dobytes, dqbytes, dkbytes;  // plane byte ranges
     float sc2, scale;
     Prob p;
 };
 
 template <typename T, int D>
-__device__ __forceinline__ void lean_redo_bwd_q(const void* kargs, int pos1, int pos2, int b, int h, int hk, int grp) {
+__device__ __forceinline__ void lean_redo_bwd_q(const void* kargs, int z, int pos1, int pos2, int b, int h, int hk,
+                                                int grp) {
     const LeanBwdArgs<T>& A = *static_cast<const LeanBwdArgs<T>*>(kargs);
     ExactAxis x[3];
-    x[0] = exact_axis(A.p.ax[0], 0);
+    x[0] = exact_axis(A.p.ax[0], z);
     x[1] = exact_axis(A.p.ax[1], pos1);
     x[2] = exact_axis(A.p.ax[2], pos2);
     const long long qb = b * A.lq.b + h * A.lq.h, kb = b * A.lk.b + hk * A.lk.h;
-    const long long lb = b * A.ll.b + h * A.ll.h + pos1 * A.ll.s1 + pos2 * A.ll.s2;
-    const Strides3 ks{0, A.lk.s1, A.lk.s2};
-    const int qo = pos1 * A.lq.s1 + pos2 * A.lq.s2;
-    const T* do_row = A.dout + (b * A.ldo.b + h * A.ldo.h + pos1 * A.ldo.s1 + pos2 * A.ldo.s2);
-    float di = exact_dot<T, D>(do_row, A.o + (b * A.lo.b + h * A.lo.h + pos1 * A.lo.s1 + pos2 * A.lo.s2));
+    const long long lb = b * A.ll.b + h * A.ll.h + z * A.ll.s0 + pos1 * A.ll.s1 + pos2 * A.ll.s2;
+    const Strides3 ks{A.lk.s0, A.lk.s1, A.lk.s2};
+    const int qo = z * A.lq.s0 + pos1 * A.lq.s1 + pos2 * A.lq.s2;
+    const T* do_row = A.dout + (b * A.ldo.b + h * A.ldo.h + z * A.ldo.s0 + pos1 * A.ldo.s1 + pos2 * A.ldo.s2);
+    float di = exact_dot<T, D>(do_row,
+                               A.o + (b * A.lo.b + h * A.lo.h + z * A.lo.s0 + pos1 * A.lo.s1 + pos2 * A.lo.s2));
     if (A.dlse) di -= A.dlse[lb];
     f32x4_t acc[D / 16];
     exact_backward_q<T, D>(A.p.scale, x, A.q + qb + qo, do_row, A.lse[lb], di, A.k + kb, ks, A.v + kb, ks, grp, acc);
-    store_rows<T, D>(A.dq + (b * A.ldq.b + h * A.ldq.h), pos1 * A.ldq.s1 + pos2 * A.ldq.s2, grp, acc, A.p.scale);
+    store_rows<T, D>(A.dq + (b * A.ldq.b + h * A.ldq.h), z * A.ldq.s0 + pos1 * A.ldq.s1 + pos2 * A.ldq.s2, grp, acc,
+                     A.p.scale);
 }
 
 template <typename T, int D>
-__device__ __forceinline__ void lean_redo_bwd_kv(const void* kargs, int pos1, int pos2, int b, int hk, int grp) {
+__device__ __forceinline__ void lean_redo_bwd_kv(const void* kargs, int z, int pos1, int pos2, int b, int hk,
+                                                 int grp) {
     const LeanBwdArgs<T>& A = *static_cast<const LeanBwdArgs<T>*>(kargs);
     ExactAxis x[3];
-    x[0] = exact_axis(A.p.ax[0], 0);
+    x[0] = exact_axis(A.p.ax[0], z);
     x[1] = exact_axis(A.p.ax[1], pos1);
     x[2] = exact_axis(A.p.ax[2], pos2);
     const long long kb = b * A.lk.b + hk * A.lk.h, gb = b * A.ldk.b + hk * A.ldk.h;
-    const int ko = pos1 * A.lk.s1 + pos2 * A.lk.s2, go = pos1 * A.ldk.s1 + pos2 * A.ldk.s2;
-    const Strides3 qs{0, A.lq.s1, A.lq.s2}, gs{0, A.ldo.s1, A.ldo.s2}, ls{0, A.ll.s1, A.ll.s2};
+    const int ko = z * A.lk.s0 + pos1 * A.lk.s1 + pos2 * A.lk.s2, go = z * A.ldk.s0 + pos1 * A.ldk.s1 + pos2 * A.ldk.s2;
+    const Strides3 qs{A.lq.s0, A.lq.s1, A.lq.s2}, gs{A.ldo.s0, A.ldo.s1, A.ldo.s2}, ls{A.ll.s0, A.ll.s1, A.ll.s2};
     f32x4_t g[D / 16];
     const int rep = A.p.rep;
     exact_zero(g);
@@ -518,8 +607,10 @@ __device__ __forceinline__ void lean_redo_bwd_kv(const void* kargs, int pos1, in
 // to dO . O), in a first pass that keeps every chunk's P and dP; O is read
 // only where that sum is not finite.
 // ---------------------------------------------------------------------------
-// Query tile of task x = (batch, tile, head), head fastest.
-template <typename T, int D, int NCH>
+// Query tile of task x (lean_task).  3-D (D3): delta = dO . O from the rows
+// (the products of one plane do not hold the window's sum), the dP products
+// start from -delta, and the tile walks its window's key planes.
+template <typename T, int D, int NCH, bool D3 = false>
 __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) {
     constexpr int NR = 2 * NCH + 6, NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
     unsigned char* smem = lds_base();
@@ -527,29 +618,34 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
     T* Vs = Ks + NR * 16 * D;
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int bt = fdiv(x, a.heads);
-    const int h = x - bt * static_cast<int>(a.heads.d);
-    const int b = fdiv(bt, a.tiles);
-    const int t = bt - b * static_cast<int>(a.tiles.d);
+    const LeanTask tk = lean_task<D3>(a.dec, x);
+    const int b = tk.b, h = tk.h, t = tk.t, z = tk.z;
     const int hk = a.rep.d == 1 ? h : fdiv(h, a.rep);
     const int* r = a.rec + t * kLeanRec;
     const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
     const int U1 = ext & 0xFF, U2 = (ext >> 8) & 0xFF, E1 = (ext >> 16) & 0xFF, E2 = (ext >> 24) & 0xFF;
-    {
-        const long long kvo = b * a.lk.b + hk * a.lk.h;
-        lean_stage<T, D>(lean_rsrc(a.k + kvo, a.kbytes), lean_rsrc(a.v + kvo, a.kbytes), Ks, Vs,
-                         (ur0 * a.lk.s1 + uc0 * a.lk.s2) * ES, a.lk.s1 * a.d1 * ES, a.lk.s2 * a.d2 * ES, U1, U2, nst,
-                         wave, lane);
-    }
+    LeanDepth dw{0, 0, 0, 1};
+    if constexpr (D3) dw = lean_depth_q(a.p.ax[0], z);
+    const long long kvo = b * a.lk.b + hk * a.lk.h;
+    const int kst = (ur0 * a.lk.s1 + uc0 * a.lk.s2) * ES, ks1 = a.lk.s1 * a.d1 * ES, ks2 = a.lk.s2 * a.d2 * ES;
+    const auto stage = [&](int j) {
+        const long long o = kvo + static_cast<long long>(dw.z0 + j * dw.d) * a.lk.s0;
+        lean_stage<T, D>(lean_rsrc(a.k + o, a.kbytes), lean_rsrc(a.v + o, a.kbytes), Ks, Vs, kst, ks1, ks2, U1, U2,
+                         nst, wave, lane);
+    };
+    stage(dw.j0);
     const int qr = 2 * wave + (col >> 3), qc = col & 7;
     const bool valid = qr < E1 && qc < E2;
     const int pos1 = pr0 + qr * a.d1, pos2 = pc0 + qc * a.d2;
+    const long long zl = z;
     const int qoff = pos1 * a.lq.s1 + pos2 * a.lq.s2;
-    const long long qbo = b * a.lq.b + h * a.lq.h;
-    const long long lo = b * a.ll.b + h * a.ll.h + pos1 * a.ll.s1 + pos2 * a.ll.s2;
+    const long long qbo = b * a.lq.b + h * a.lq.h + zl * a.lq.s0;
+    const long long lo = b * a.ll.b + h * a.ll.h + zl * a.ll.s0 + pos1 * a.ll.s1 + pos2 * a.ll.s2;
     const int goff = pos1 * a.ldo.s1 + pos2 * a.ldo.s2;
-    const long long gbo = b * a.ldo.b + h * a.ldo.h;
-    uint4 qf[NF], gf[NF];
+    const long long gbo = b * a.ldo.b + h * a.ldo.h + zl * a.ldo.s0;
+    const int ooff = pos1 * a.lo.s1 + pos2 * a.lo.s2;
+    const long long obo = b * a.lo.b + h * a.lo.h + zl * a.lo.s0;
+    uint4 qf[NF], gf[NF], of[NF];
     {
         const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + qbo, a.qbytes);
         const __amdgpu_buffer_rsrc_t rg = lean_rsrc(a.dout + gbo, a.dobytes);
@@ -559,6 +655,14 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
             const uint32_t og = valid ? static_cast<uint32_t>(goff * ES + lean_frag_off<T, D>(ks, grp)) : kLeanOOR;
             qf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 0));
             gf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rg, og, 0, 0));
+        }
+        if constexpr (D3) {
+            const __amdgpu_buffer_rsrc_t ro = lean_rsrc(a.o + obo, a.obytes);
+#pragma unroll
+            for (int ks = 0; ks < NF; ++ks) {
+                const uint32_t o = valid ? static_cast<uint32_t>(ooff * ES + lean_frag_off<T, D>(ks, grp)) : kLeanOOR;
+                of[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ro, o, 0, 0));
+            }
         }
     }
     const float L2 = valid ? a.lse[lo] * kLog2e : 0.f;
@@ -578,61 +682,92 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
 #pragma unroll
         for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<T, D>(first, lane, hi, db);
 
-    wait_loads();
-    __syncthreads();
-
     const unsigned char* Kb = reinterpret_cast<const unsigned char*>(Ks);
     const unsigned char* Vb = reinterpret_cast<const unsigned char*>(Vs);
-    // P and dP (= dO . v) of every chunk first, and delta = sum over the
-    // window of P dP (= dO . O) from them; where that is not finite (a
-    // non-finite operand outside the window reaching the sum through a
-    // masked slot), dO . O from the rows
-    f32x4_t pr[NCH][2], dpr[NCH][2];
-    float di;
-    {
-        const f32x4_t zero = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        float part = 0.f;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const int row = 2 * c + (grp >> 1) - rlo;
-            const float off = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1) ? -L2 : -INFINITY;
-#pragma unroll
-            for (int bb = 0; bb < 2; ++bb) {
-                const f32x4_t sc = lean_score<T, D>(Kb, aoff, c, bb, qf, cb[bb]);
-                dpr[c][bb] = lean_score<T, D>(Vb, aoff, c, bb, gf, zero);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    pr[c][bb][i] = __builtin_amdgcn_exp2f(fmaf(sc[i], a.sc2, off));
-                    part = fmaf(pr[c][bb][i], dpr[c][bb][i], part);
-                }
-            }
-        }
-        di = sum_rows(part) - dl;
-        if (valid && !(__builtin_fabsf(di) <= __FLT_MAX__))
-            di = exact_dot<T, D>(a.dout + gbo + goff,
-                                 a.o + (b * a.lo.b + h * a.lo.h + pos1 * a.lo.s1 + pos2 * a.lo.s2)) - dl;
-    }
-    if (valid && grp == 0) a.delta[lo] = di;
     f32x4_t acc[D / 16];
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) acc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (D3) {
+        // delta from this lane's head dims, summed over the 4 lane rows
+        float di = 0.f;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        f32x4_t ds[2];
+        for (int ks = 0; ks < NF; ++ks) di = lean_dot<T>(gf[ks], of[ks], di);
+        di = sum_rows(di) - dl;
+        if (valid && grp == 0) a.delta[lo] = di;
+        const f32x4_t nd[2] = {f32x4_t{-di, -di, -di, -di}, f32x4_t{-di, -di, -di, -di}};
+#pragma unroll 1
+        for (int j = dw.j0; j < dw.n; ++j) {
+            wait_loads();
+            __syncthreads();
 #pragma unroll
-        for (int bb = 0; bb < 2; ++bb)
+            for (int c = 0; c < NCH; ++c) {
+                const int row = 2 * c + (grp >> 1) - rlo;
+                const float off = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1) ? -L2 : -INFINITY;
+                f32x4_t ds[2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) ds[bb][i] = pr[c][bb][i] * (dpr[c][bb][i] - di);
-        lean_acc<T, D>(Kb, toff, c, ds, acc);
+                for (int bb = 0; bb < 2; ++bb) {
+                    const f32x4_t sc = lean_score<T, D>(Kb, aoff, c, bb, qf, cb[bb]);
+                    const f32x4_t dp = lean_score<T, D>(Vb, aoff, c, bb, gf, nd[bb]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) ds[bb][i] = __builtin_amdgcn_exp2f(fmaf(sc[i], a.sc2, off)) * dp[i];
+                }
+                lean_acc<T, D>(Kb, toff, c, ds, acc);
+            }
+            if (j + 1 < dw.n) {
+                __syncthreads();  // the plane is no longer read
+                stage(j + 1);
+            }
+        }
+    } else {
+        wait_loads();
+        __syncthreads();
+        // P and dP (= dO . v) of every chunk first, and delta = sum over the
+        // window of P dP (= dO . O) from them; where that is not finite (a
+        // non-finite operand outside the window reaching the sum through a
+        // masked slot), dO . O from the rows
+        f32x4_t pr[NCH][2], dpr[NCH][2];
+        float di;
+        {
+            const f32x4_t zero = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            float part = 0.f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int row = 2 * c + (grp >> 1) - rlo;
+                const float off = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1) ? -L2 : -INFINITY;
+#pragma unroll
+                for (int bb = 0; bb < 2; ++bb) {
+                    const f32x4_t sc = lean_score<T, D>(Kb, aoff, c, bb, qf, cb[bb]);
+                    dpr[c][bb] = lean_score<T, D>(Vb, aoff, c, bb, gf, zero);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        pr[c][bb][i] = __builtin_amdgcn_exp2f(fmaf(sc[i], a.sc2, off));
+                        part = fmaf(pr[c][bb][i], dpr[c][bb][i], part);
+                    }
+                }
+            }
+            di = sum_rows(part) - dl;
+            if (valid && !(__builtin_fabsf(di) <= __FLT_MAX__))
+                di = exact_dot<T, D>(a.dout + gbo + goff, a.o + obo + ooff) - dl;
+        }
+        if (valid && grp == 0) a.delta[lo] = di;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            f32x4_t ds[2];
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ds[bb][i] = pr[c][bb][i] * (dpr[c][bb][i] - di);
+            lean_acc<T, D>(Kb, toff, c, ds, acc);
+        }
     }
     const bool redo = valid && item_nonfinite(lane_sum(acc, 0.f));
     if (valid) {
-        const __amdgpu_buffer_rsrc_t rd = lean_rsrc(a.dq + (b * a.ldq.b + h * a.ldq.h), a.dqbytes);
+        const __amdgpu_buffer_rsrc_t rd = lean_rsrc(a.dq + (b * a.ldq.b + h * a.ldq.h + zl * a.ldq.s0), a.dqbytes);
         const int dqoff = pos1 * a.ldq.s1 + pos2 * a.ldq.s2;
 #pragma unroll
         for (int db = 0; db < D / 16; ++db) lean_store4<T>(rd, dqoff * ES, db, grp, acc[db], a.scale);
     }
-    if (redo) lean_redo_bwd_q<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, h, hk, grp);
+    if (redo) lean_redo_bwd_q<T, D>(kernargs(), opaque(z), opaque(pos1), opaque(pos2), b, h, hk, grp);
 }
 
 // ---------------------------------------------------------------------------
@@ -642,10 +777,11 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
 // -lse log2 e and -delta); a wave walks its own union rows, at most
 // MAXCH chunks.
 // ---------------------------------------------------------------------------
-// Key tile of task x = (batch, tile, kv head): reads the delta rows the
-// query tiles wrote.
+// Key tile of task x (lean_task; heads are kv heads): reads the delta rows
+// the query tiles wrote.  3-D (D3): the tile walks the query planes whose
+// windows hold its key plane, staging each plane's union in turn.
 // A wave walks at most MAXC chunks (the host checks its rows fit).
-template <typename T, int D, int MAXC>
+template <typename T, int D, int MAXC, bool D3 = false>
 __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x) {
     constexpr int NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
     const int nr = a.nr;
@@ -656,10 +792,8 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     float* ND = NL + nr * 16 + 8;
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int bt = fdiv(x, a.heads);
-    const int hk = x - bt * static_cast<int>(a.heads.d);  // kv head (one q head each)
-    const int b = fdiv(bt, a.tiles);
-    const int t = bt - b * static_cast<int>(a.tiles.d);
+    const LeanTask tk = lean_task<D3>(a.dec, x);
+    const int b = tk.b, hk = tk.h, t = tk.t, z = tk.z;  // kv head (one q head each)
     const int h = hk;
     const int* r = a.rec_k + t * kLeanRec;
     const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
@@ -667,25 +801,27 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     const int kr = 2 * wave + (col >> 3), kc = col & 7;
     const bool valid = kr < E1 && kc < E2;
     const int pos1 = pr0 + kr * a.d1, pos2 = pc0 + kc * a.d2;
+    const long long zl = z;
     const int koff = pos1 * a.lk.s1 + pos2 * a.lk.s2;
-    const long long kbo = b * a.lk.b + hk * a.lk.h;
+    const long long kbo = b * a.lk.b + hk * a.lk.h + zl * a.lk.s0;
     const int dkoff = pos1 * a.ldk.s1 + pos2 * a.ldk.s2;
-    const long long dkbo = b * a.ldk.b + hk * a.ldk.h;
-    if (r[14]) {  // no query attends these keys
+    const long long dkbo = b * a.ldk.b + hk * a.ldk.h + zl * a.ldk.s0;
+    LeanDepth dw{0, 0, 0, 1};
+    if constexpr (D3) dw = lean_depth_k(a.p.ax[0], z);
+    if (r[14] || dw.n <= dw.j0) {  // no query attends these keys
         if (valid) {
             const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.dk + dkbo, a.dkbytes);
             const __amdgpu_buffer_rsrc_t rv = lean_rsrc(a.dv + dkbo, a.dkbytes);
-            const f32x4_t z = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            const f32x4_t zr = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int db = 0; db < D / 16; ++db) {
-                lean_store4<T>(rk, dkoff * ES, db, grp, z, 1.f);
-                lean_store4<T>(rv, dkoff * ES, db, grp, z, 1.f);
+                lean_store4<T>(rk, dkoff * ES, db, grp, zr, 1.f);
+                lean_store4<T>(rv, dkoff * ES, db, grp, zr, 1.f);
             }
         }
         return;
     }
     // per-slot -lse log2 e and -delta: slot threadIdx.x (and up, past 256 slots)
-    const long long lbase = b * a.ll.b + h * a.ll.h;
     const auto slot_pos = [&](int sidx, bool& in) {
         const int u = sidx >> 4, cc = sidx & 15;
         in = u < U1 && cc < U2;
@@ -693,11 +829,17 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     };
     bool sin;
     const int sp = slot_pos(threadIdx.x, sin);
-    const long long qo = b * a.lq.b + h * a.lq.h, go = b * a.ldo.b + h * a.ldo.h;
-    const float sl = a.lse[lbase + sp], sd = a.delta[lbase + sp];
-    {
-        const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + qo, a.qbytes), rg = lean_rsrc(a.dout + go, a.dobytes);
-        if (a.lq.s1 == a.ldo.s1 && a.lq.s2 == a.ldo.s2) {
+    // query plane j: q and dO rows, and the lse / delta rows
+    const long long qo0 = b * a.lq.b + h * a.lq.h, go0 = b * a.ldo.b + h * a.ldo.h, lb0 = b * a.ll.b + h * a.ll.h;
+    const auto plane = [&](int j) { return static_cast<long long>(dw.z0 + j * dw.d); };
+    const bool same_qg = a.lq.s1 == a.ldo.s1 && a.lq.s2 == a.ldo.s2;
+    const auto stage = [&](int j, float& sl, float& sd) {
+        const long long lbase = lb0 + plane(j) * a.ll.s0;
+        sl = a.lse[lbase + sp];
+        sd = a.delta[lbase + sp];
+        const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + (qo0 + plane(j) * a.lq.s0), a.qbytes);
+        const __amdgpu_buffer_rsrc_t rg = lean_rsrc(a.dout + (go0 + plane(j) * a.ldo.s0), a.dobytes);
+        if (same_qg) {
             lean_stage<T, D>(rq, rg, Qs, Gs, (ur0 * a.lq.s1 + uc0 * a.lq.s2) * ES, a.lq.s1 * a.d1 * ES,
                              a.lq.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
         } else {
@@ -707,7 +849,9 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
             lean_stage1<T, D>(rg, Gs, (ur0 * a.ldo.s1 + uc0 * a.ldo.s2) * ES, a.ldo.s1 * a.d1 * ES,
                               a.ldo.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
         }
-    }
+    };
+    float sl, sd;
+    stage(dw.j0, sl, sd);
     uint4 kf[NF], vf[NF];
     {
         const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.k + kbo, a.kbytes);
@@ -740,21 +884,6 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
 #pragma unroll
         for (int db = 0; db < D / 16; ++db) toff[hi][db] = lean_tr_off<T, D>(first, lane, hi, db);
 
-    wait_loads();
-    if (static_cast<int>(threadIdx.x) < nr * 16) {
-        NL[threadIdx.x] = sin ? -sl * kLog2e : 0.f;
-        ND[threadIdx.x] = sin ? -sd : 0.f;
-    }
-    // the exponent offsets of lanes whose row test fails: P = 0
-    if (threadIdx.x < 8) NL[nr * 16 + threadIdx.x] = -INFINITY;
-    for (int s = threadIdx.x + 64 * kLeanWaves; s < nr * 16; s += 64 * kLeanWaves) {
-        bool in;
-        const int o = slot_pos(s, in);
-        NL[s] = in ? -a.lse[lbase + o] * kLog2e : 0.f;
-        ND[s] = in ? -a.delta[lbase + o] : 0.f;
-    }
-    lds_publish_barrier();
-
     const unsigned char* Qb = reinterpret_cast<const unsigned char*>(Qs);
     const unsigned char* Gb = reinterpret_cast<const unsigned char*>(Gs);
     f32x4_t gk[D / 16], gv[D / 16];
@@ -763,30 +892,56 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     const float* nlp = NL + first * 16 + 8 * grp;
     const float* ndp = ND + first * 16 + 8 * grp;
     const float* ninf = NL + nr * 16;
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-        if (c >= nch) break;  // wave-uniform
-        const int row = 2 * c + (grp >> 1) - rlo;
-        // a failed row test reads the -inf entries (one select per chunk)
-        const float* nlc = (row >= 0 && row < rn) ? nlp + 32 * c : ninf;
-        const f32x4_t nd[2] = {*reinterpret_cast<const f32x4_t*>(ndp + 32 * c),
-                               *reinterpret_cast<const f32x4_t*>(ndp + 32 * c + 4)};
-        const f32x4_t nl[2] = {*reinterpret_cast<const f32x4_t*>(nlc), *reinterpret_cast<const f32x4_t*>(nlc + 4)};
-        f32x4_t s[2], dp[2];
-#pragma unroll
-        for (int bb = 0; bb < 2; ++bb) {
-            s[bb] = lean_score<T, D>(Qb, aoff, c, bb, kf, cb[bb]);
-            dp[bb] = lean_score<T, D>(Gb, aoff, c, bb, vf, nd[bb]);
+#pragma unroll 1
+    for (int j = dw.j0; j < dw.n; ++j) {
+        wait_loads();
+        if (static_cast<int>(threadIdx.x) < nr * 16) {
+            NL[threadIdx.x] = sin ? -sl * kLog2e : 0.f;
+            ND[threadIdx.x] = sin ? -sd : 0.f;
         }
-#pragma unroll
-        for (int bb = 0; bb < 2; ++bb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], a.sc2, nl[bb][i]));
-                dp[bb][i] *= s[bb][i];
+        // the exponent offsets of lanes whose row test fails: P = 0
+        if (threadIdx.x < 8) NL[nr * 16 + threadIdx.x] = -INFINITY;
+        {
+            const long long lbase = lb0 + plane(j) * a.ll.s0;
+            for (int s = threadIdx.x + 64 * kLeanWaves; s < nr * 16; s += 64 * kLeanWaves) {
+                bool in;
+                const int o = slot_pos(s, in);
+                NL[s] = in ? -a.lse[lbase + o] * kLog2e : 0.f;
+                ND[s] = in ? -a.delta[lbase + o] : 0.f;
             }
-        lean_acc<T, D>(Gb, toff, c, s, gv);
-        lean_acc<T, D>(Qb, toff, c, dp, gk);
+        }
+        lds_publish_barrier();
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+            if (c >= nch) break;  // wave-uniform
+            const int row = 2 * c + (grp >> 1) - rlo;
+            // a failed row test reads the -inf entries (one select per chunk)
+            const float* nlc = (row >= 0 && row < rn) ? nlp + 32 * c : ninf;
+            const f32x4_t nd[2] = {*reinterpret_cast<const f32x4_t*>(ndp + 32 * c),
+                                   *reinterpret_cast<const f32x4_t*>(ndp + 32 * c + 4)};
+            const f32x4_t nl[2] = {*reinterpret_cast<const f32x4_t*>(nlc), *reinterpret_cast<const f32x4_t*>(nlc + 4)};
+            f32x4_t s[2], dp[2];
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+                s[bb] = lean_score<T, D>(Qb, aoff, c, bb, kf, cb[bb]);
+                dp[bb] = lean_score<T, D>(Gb, aoff, c, bb, vf, nd[bb]);
+            }
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    s[bb][i] = __builtin_amdgcn_exp2f(fmaf(s[bb][i], a.sc2, nl[bb][i]));
+                    dp[bb][i] *= s[bb][i];
+                }
+            lean_acc<T, D>(Gb, toff, c, s, gv);
+            lean_acc<T, D>(Qb, toff, c, dp, gk);
+        }
+        if constexpr (D3) {
+            if (j + 1 < dw.n) {
+                __syncthreads();  // the plane and its scalars are no longer read
+                stage(j + 1, sl, sd);
+            }
+        }
     }
     const bool redo = valid && item_nonfinite(lane_sum(gk, lane_sum(gv, 0.f)));
     if (valid) {
@@ -798,17 +953,17 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
             lean_store4<T>(rv, dkoff * ES, db, grp, gv[db], 1.f);
         }
     }
-    if (redo) lean_redo_bwd_kv<T, D>(kernargs(), opaque(pos1), opaque(pos2), b, hk, grp);
+    if (redo) lean_redo_bwd_kv<T, D>(kernargs(), opaque(z), opaque(pos1), opaque(pos2), b, hk, grp);
 }
 
-template <typename T, int D, int NCH>
+template <typename T, int D, int NCH, bool D3 = false>
 __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_q(LeanBwdArgs<T> a) {
-    lean_bwd_q_tile<T, D, NCH>(a, xcd_block(blockIdx.x, gridDim.x));
+    lean_bwd_q_tile<T, D, NCH, D3>(a, xcd_block(blockIdx.x, gridDim.x));
 }
 
-template <typename T, int D, int MAXC>
+template <typename T, int D, int MAXC, bool D3 = false>
 __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> a) {
-    lean_bwd_kv_tile<T, D, MAXC>(a, xcd_block(blockIdx.x, gridDim.x));
+    lean_bwd_kv_tile<T, D, MAXC, D3>(a, xcd_block(blockIdx.x, gridDim.x));
 }
 
 // ---------------------------------------------------------------------------
@@ -1189,7 +1344,22 @@ const LeanGeo* lean_geometry(const Prob& p, int mode, int nch, hipStream_t s) {
 }
 
 LeanLay lean_lay(const Lay& l) {
-    return LeanLay{l.b, l.h, static_cast<int>(l.s1), static_cast<int>(l.s2)};
+    return LeanLay{l.b, l.h, static_cast<int>(l.s1), static_cast<int>(l.s2), static_cast<int>(l.s0)};
+}
+
+// A 3-D problem: the tiles walk depth planes (axis 0 of a 2-D problem has
+// extent 1).
+bool lean_3d(const Prob& p) { return p.ax[0].len > 1; }
+
+LeanDecode lean_decode(const Prob& p, int heads, int ntiles) {
+    LeanDecode d;
+    d.heads = make_fastdiv(heads);
+    d.tiles = make_fastdiv(ntiles);
+    const int hg = heads % 2 == 0 ? 2 : 1;
+    d.hg = make_fastdiv(hg);
+    d.zlen = make_fastdiv(p.ax[0].len);
+    d.hgroups = make_fastdiv(heads / hg);
+    return d;
 }
 
 // Byte range of one (batch, head) plane of an operand of head dim D
@@ -1217,7 +1387,13 @@ void lean_audit_one(LdsAudit& a) {
     audit_one(k_lean_fwd<T, D, NCH>, "k_lean_fwd", a);
     audit_one(k_lean_bwd_q<T, D, NCH>, "k_lean_bwd_q", a);
     audit_one(k_lean_bwd_kv<T, D, NCH + 2>, "k_lean_bwd_kv", a);
-    if constexpr (!kF32<T>) audit_one(k_lean_wsum_key<T, D, NCH + 2>, "k_lean_wsum_key", a);
+    if constexpr (!kF32<T>) {
+        audit_one(k_lean_wsum_key<T, D, NCH + 2>, "k_lean_wsum_key", a);
+    } else {
+        audit_one(k_lean_fwd<T, D, NCH, true>, "k_lean_fwd (3-D)", a);
+        audit_one(k_lean_bwd_q<T, D, NCH, true>, "k_lean_bwd_q (3-D)", a);
+        audit_one(k_lean_bwd_kv<T, D, NCH + 2, true>, "k_lean_bwd_kv (3-D)", a);
+    }
 }
 
 template <typename T, int D>
@@ -1250,18 +1426,25 @@ int lean_nch(int K1) { return (K1 + 2) / 2; }
 
 }  // namespace
 
-// Lean path eligibility: a 2-D (or 2-D-padded) problem at stride 1, head dim
-// 32 or 64 for q, k and v, K2 <= 9, K1 <= 9, per-axis extents below 2^15,
-// planes below 2^30 bytes.  Every operand has its own layout, except that
-// the operands staged or stored together share one: kvside lists pairs
-// (k, v) and (dk, dv), and the fp32 rows (lse, delta, dlse) share one.
+// Lean path eligibility: a 2-D (or 2-D-padded) problem at stride 1, or an
+// fp32 3-D one at stride 1 (the 16-bit ones run faster on the general tile
+// kernels, whose 3-D tiles share each staged plane between two depths; in
+// fp32 those have no instances), head dim 32 or 64 for q, k and v, K2 <= 9,
+// K1 <= 9, in-plane extents below 2^15, planes below 2^30 bytes (and a
+// (batch, head) volume's element offsets in 31 bits for 3-D).  Every
+// operand has its own layout, except that the operands staged or stored
+// together share one: kvside lists pairs (k, v) and (dk, dv), and the fp32
+// rows (lse, delta, dlse) share one.
 bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list<Lay> qside,
                    std::initializer_list<Lay> kvside, std::initializer_list<Lay> rows) {
     if (!lean_switch() || !aligned || !(p.scale > 0.f) || !lean_static_lds_ok()) return false;
     if (p.Dqk != p.Dv || (p.Dqk != 32 && p.Dqk != 64)) return false;
-    // 2-D: axis 0 padded; a short first axis (1-D problems) stays on the
-    // general tiles, which lay a 1-D axis out along whole tiles
-    if (p.ax[0].len != 1 || p.ax[0].k != 1 || p.ax[1].len < 8) return false;
+    // a short first in-plane axis (1-D problems) stays on the general tiles,
+    // which lay a 1-D axis out along whole tiles
+    if (p.ax[1].len < 8) return false;
+    const bool d3 = lean_3d(p);
+    if (!d3 && p.ax[0].k != 1) return false;
+    if (d3 && (dtype != NATTEN_F32 || p.ax[0].st != 1 || p.ax[0].len >= (1 << 15))) return false;
     for (int a = 1; a < 3; ++a) {
         const Axis& A = p.ax[a];
         if (A.st != 1 || A.k > 9 || A.len >= (1 << 15)) return false;
@@ -1269,19 +1452,22 @@ bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list
     if (kvside.size() % 2 != 0 || !all_same(rows)) return false;
     for (const Lay* l = kvside.begin(); l != kvside.end(); l += 2)
         if (!same_lay(l[0], l[1])) return false;
+    const long long z1 = static_cast<long long>(p.ax[0].len) - 1;
+    const int esz = dtype == NATTEN_F32 ? 4 : 2;
     for (const auto& side : {qside, kvside}) {
         for (const Lay& l : side) {
-            if (l.s1 < 0 || l.s2 < 0 || l.b < 0 || l.h < 0) return false;
-            const long long v = ((static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
-                                 (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + p.Dqk) *
-                                (dtype == NATTEN_F32 ? 4 : 2);
-            if (v >= (1LL << 30)) return false;
+            if (l.s1 < 0 || l.s2 < 0 || l.b < 0 || l.h < 0 || l.s0 < 0) return false;
+            const long long v = (static_cast<long long>(p.ax[1].len) - 1) * l.s1 +
+                                (static_cast<long long>(p.ax[2].len) - 1) * l.s2 + p.Dqk;
+            if (v * esz >= (1LL << 30)) return false;
+            if (d3 && z1 * l.s0 + v >= (1LL << 31)) return false;
         }
     }
-    // fp32 rows (lse, delta, dlse): in-plane element offsets in 31 bits
+    // fp32 rows (lse, delta, dlse): element offsets in 31 bits
     const Lay& r = *rows.begin();
-    if (r.s1 < 0 || r.s2 < 0 || r.b < 0 || r.h < 0) return false;
-    if ((static_cast<long long>(p.ax[1].len) - 1) * r.s1 + (static_cast<long long>(p.ax[2].len) - 1) * r.s2 >=
+    if (r.s1 < 0 || r.s2 < 0 || r.b < 0 || r.h < 0 || r.s0 < 0) return false;
+    if (z1 * r.s0 + (static_cast<long long>(p.ax[1].len) - 1) * r.s1 +
+            (static_cast<long long>(p.ax[2].len) - 1) * r.s2 >=
         (1LL << 31))
         return false;
     return true;
@@ -1293,7 +1479,7 @@ int lean_lds_audit(int* checked) {
     return a.bad == 0 ? 1 : 0;
 }
 
-template <typename T, int D, int NCH>
+template <typename T, int D, int NCH, bool D3>
 hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, const void* k, Lay lk,
                         const void* v, void* o, Lay lo, float* lse, Lay ll, hipStream_t s) {
     LeanFwdArgs<T> a{};
@@ -1307,8 +1493,7 @@ hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, 
     a.lk = lean_lay(lk);
     a.ll = lean_lay(ll);
     a.lo = lean_lay(lo);
-    a.heads = make_fastdiv(p.Hq);
-    a.tiles = make_fastdiv(g->ntiles);
+    a.dec = lean_decode(p, p.Hq, g->ntiles);
     a.rep = make_fastdiv(p.rep);
     a.d1 = p.ax[1].dil;
     a.d2 = p.ax[2].dil;
@@ -1319,10 +1504,10 @@ hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, 
     a.obytes = plane_bytes(p, lo, D, sizeof(T));
     a.sc2 = p.scale * kLog2e;
     a.p = p;
-    const long long blocks = static_cast<long long>(p.B) * p.Hq * g->ntiles;
+    const long long blocks = static_cast<long long>(p.B) * p.Hq * g->ntiles * p.ax[0].len;
     const size_t shm = kLdsPad + static_cast<size_t>(2) * (2 * NCH + 6) * 16 * D * sizeof(T);
     if (shm > 160 * 1024) return hipErrorNotSupported;
-    auto kern = k_lean_fwd<T, D, NCH>;
+    auto kern = k_lean_fwd<T, D, NCH, D3>;
     const hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     NA_LAUNCH("na_fwd_lean", kern, dim3(static_cast<unsigned>(blocks)), dim3(64 * kLeanWaves), shm, s, a);
@@ -1335,29 +1520,36 @@ hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay
                         Lay lo, float* lse, Lay ll, int dtype, hipStream_t s) {
     (void)lv;
     const int nch = lean_nch(p.ax[1].k);
-    if (static_cast<long long>(p.B) * p.Hq * 4096 >= (1LL << 31)) return hipErrorNotSupported;
+    if (static_cast<long long>(p.B) * p.Hq * p.ax[0].len * 4096 >= (1LL << 31)) return hipErrorNotSupported;
     const LeanGeo* g = lean_geometry(p, 0, nch, s);
     if (!g) return hipErrorNotSupported;
-#define NA_LF(T, DD, N) return lean_fwd_run<T, DD, N>(p, g, q, lq, k, lk, v, o, lo, lse, ll, s)
-#define NA_LF_N(T, DD)          \
-    switch (nch) {              \
-        case 1: NA_LF(T, DD, 1); \
-        case 2: NA_LF(T, DD, 2); \
-        case 3: NA_LF(T, DD, 3); \
-        case 4: NA_LF(T, DD, 4); \
-        default: NA_LF(T, DD, 5); \
+    const bool d3 = lean_3d(p);
+    // 3-D instances exist for fp32 only (the eligibility keeps 16-bit 3-D away)
+#define NA_LF(T, DD, N) return lean_fwd_run<T, DD, N, false>(p, g, q, lq, k, lk, v, o, lo, lse, ll, s)
+#define NA_LF3(T, DD, N)                                                              \
+    return d3 ? lean_fwd_run<T, DD, N, true>(p, g, q, lq, k, lk, v, o, lo, lse, ll, s) \
+              : lean_fwd_run<T, DD, N, false>(p, g, q, lq, k, lk, v, o, lo, lse, ll, s)
+#define NA_LF_N(T, DD, F)    \
+    switch (nch) {           \
+        case 1: F(T, DD, 1); \
+        case 2: F(T, DD, 2); \
+        case 3: F(T, DD, 3); \
+        case 4: F(T, DD, 4); \
+        default: F(T, DD, 5); \
     }
+    if (d3 && dtype != NATTEN_F32) return hipErrorNotSupported;
     if (dtype == NATTEN_BF16) {
-        if (p.Dqk == 32) NA_LF_N(bf16, 32);
-        NA_LF_N(bf16, 64);
+        if (p.Dqk == 32) NA_LF_N(bf16, 32, NA_LF);
+        NA_LF_N(bf16, 64, NA_LF);
     }
     if (dtype == NATTEN_F32) {
-        if (p.Dqk == 32) NA_LF_N(float, 32);
-        NA_LF_N(float, 64);
+        if (p.Dqk == 32) NA_LF_N(float, 32, NA_LF3);
+        NA_LF_N(float, 64, NA_LF3);
     }
-    if (p.Dqk == 32) NA_LF_N(f16, 32);
-    NA_LF_N(f16, 64);
+    if (p.Dqk == 32) NA_LF_N(f16, 32, NA_LF);
+    NA_LF_N(f16, 64, NA_LF);
 #undef NA_LF_N
+#undef NA_LF3
 #undef NA_LF
 }
 
@@ -1391,6 +1583,7 @@ LeanBwdArgs<T> lean_bwd_args(const Prob& p, const void* q, Lay lq, const void* k
     a.K2 = p.ax[2].k;
     a.qbytes = plane_bytes(p, lq, D, sizeof(T));
     a.kbytes = plane_bytes(p, lk, D, sizeof(T));
+    a.obytes = plane_bytes(p, lo, D, sizeof(T));
     a.dobytes = plane_bytes(p, ldo, D, sizeof(T));
     a.dqbytes = plane_bytes(p, ldq, D, sizeof(T));
     a.dkbytes = plane_bytes(p, ldk, D, sizeof(T));
@@ -1400,27 +1593,26 @@ LeanBwdArgs<T> lean_bwd_args(const Prob& p, const void* q, Lay lq, const void* k
     return a;
 }
 
-template <typename T, int D, int NCH>
+template <typename T, int D, int NCH, bool D3>
 hipError_t lean_bwd_run(const Prob& p, const LeanGeo* gq, const LeanGeo* gk, const LeanBwdArgs<T>& base,
                         hipStream_t s) {
     LeanBwdArgs<T> a = base;
     a.rec = gq->ptr;
     a.rec_k = gk->ptr;
-    a.heads = make_fastdiv(p.Hq);
-    a.tiles = make_fastdiv(gq->ntiles);
+    a.dec = lean_decode(p, p.Hq, gq->ntiles);
     a.nr = std::max(gk->nst_max, 1);
     const size_t shm_q = kLdsPad + static_cast<size_t>(2) * (2 * NCH + 6) * 16 * D * sizeof(T);
     const size_t shm_k =
         kLdsPad + static_cast<size_t>(a.nr) * 16 * (2 * D * sizeof(T) + 2 * sizeof(float)) + 8 * sizeof(float);
-    const long long tasks = static_cast<long long>(p.B) * p.Hq * gq->ntiles;
+    const long long tasks = static_cast<long long>(p.B) * p.Hq * gq->ntiles * p.ax[0].len;
     if (shm_q > 160 * 1024 || shm_k > 160 * 1024) return hipErrorNotSupported;
-    auto kq = k_lean_bwd_q<T, D, NCH>;
+    auto kq = k_lean_bwd_q<T, D, NCH, D3>;
     hipError_t e = allow_lds(kq, shm_q);
     if (e != hipSuccess) return e;
     NA_LAUNCH("na_bwd_q_lean", kq, dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves), shm_q, s, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    auto kern = k_lean_bwd_kv<T, D, NCH + 2>;
+    auto kern = k_lean_bwd_kv<T, D, NCH + 2, D3>;
     if ((e = allow_lds(kern, shm_k)) != hipSuccess) return e;
     NA_LAUNCH("na_bwd_kv_lean", kern, dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves), shm_k, s, a);
     return hipGetLastError();
@@ -1436,36 +1628,41 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
     (void)ldv;
     if (p.rep != 1) return hipErrorNotSupported;
     if (!same_lay(ll, lde) || (dlse && !same_lay(ll, ldl))) return hipErrorNotSupported;
-    if (static_cast<long long>(p.B) * p.Hq * 8192 >= (1LL << 31)) return hipErrorNotSupported;
+    if (static_cast<long long>(p.B) * p.Hq * p.ax[0].len * 8192 >= (1LL << 31)) return hipErrorNotSupported;
+    const bool d3 = lean_3d(p);
+    if (d3 && dtype != NATTEN_F32) return hipErrorNotSupported;  // 3-D instances exist for fp32 only
     const int nch = lean_nch(p.ax[1].k);
     const LeanGeo* gq = lean_geometry(p, 0, nch, s);
     const LeanGeo* gk = gq ? lean_geometry(p, 1, nch, s) : nullptr;
     if (!gq || !gk || gq->ntiles != gk->ntiles || gk->rows_max > 2 * (nch + 2)) return hipErrorNotSupported;
-#define NA_LB(T, DD, N)                                                                                           \
-    return lean_bwd_run<T, DD, N>(p, gq, gk,                                                                      \
-                                  lean_bwd_args<T, DD>(p, q, lq, k, lk, v, o, lo, dout, ldo, lse, ll, dlse, dq, ldq, \
-                                                       dk, ldk, dv, delta),                                          \
-                                  s)
-#define NA_LB_N(T, DD)          \
-    switch (nch) {              \
-        case 1: NA_LB(T, DD, 1); \
-        case 2: NA_LB(T, DD, 2); \
-        case 3: NA_LB(T, DD, 3); \
-        case 4: NA_LB(T, DD, 4); \
-        default: NA_LB(T, DD, 5); \
+#define NA_LB_A(T, DD) \
+    lean_bwd_args<T, DD>(p, q, lq, k, lk, v, o, lo, dout, ldo, lse, ll, dlse, dq, ldq, dk, ldk, dv, delta)
+#define NA_LB(T, DD, N) return lean_bwd_run<T, DD, N, false>(p, gq, gk, NA_LB_A(T, DD), s)
+#define NA_LB3(T, DD, N)                                                         \
+    return d3 ? lean_bwd_run<T, DD, N, true>(p, gq, gk, NA_LB_A(T, DD), s) \
+              : lean_bwd_run<T, DD, N, false>(p, gq, gk, NA_LB_A(T, DD), s)
+#define NA_LB_N(T, DD, F)    \
+    switch (nch) {           \
+        case 1: F(T, DD, 1); \
+        case 2: F(T, DD, 2); \
+        case 3: F(T, DD, 3); \
+        case 4: F(T, DD, 4); \
+        default: F(T, DD, 5); \
     }
     if (dtype == NATTEN_BF16) {
-        if (p.Dqk == 32) NA_LB_N(bf16, 32);
-        NA_LB_N(bf16, 64);
+        if (p.Dqk == 32) NA_LB_N(bf16, 32, NA_LB);
+        NA_LB_N(bf16, 64, NA_LB);
     }
     if (dtype == NATTEN_F32) {
-        if (p.Dqk == 32) NA_LB_N(float, 32);
-        NA_LB_N(float, 64);
+        if (p.Dqk == 32) NA_LB_N(float, 32, NA_LB3);
+        NA_LB_N(float, 64, NA_LB3);
     }
-    if (p.Dqk == 32) NA_LB_N(f16, 32);
-    NA_LB_N(f16, 64);
+    if (p.Dqk == 32) NA_LB_N(f16, 32, NA_LB);
+    NA_LB_N(f16, 64, NA_LB);
 #undef NA_LB_N
+#undef NA_LB3
 #undef NA_LB
+#undef NA_LB_A
 }
 
 // Split ops, key side, on the 8x8 key tiles: eligibility beyond the general

@@ -246,6 +246,55 @@ def test_lean_tiles_on_packed_qkv_views(case, do_layout):
         _close(grad[..., i, :, :], b, dtype, n)
 
 
+LEAN3D_FP32 = [
+    # spatial, heads, dim, kernel, dilation, causal, q/k/v as views of one packed tensor
+    ((5, 10, 12), 2, 32, (3, 3, 3), (1, 1, 1), (False, False, False), False),
+    ((6, 9, 16), 2, 64, (3, 5, 3), (2, 1, 2), (True, False, False), False),
+    ((7, 12, 10), 4, 32, (4, 3, 5), (1, 2, 1), (False, True, False), True),
+    ((4, 16, 16), 2, 64, (3, 7, 7), (1, 2, 2), (False, False, False), False),
+]
+
+
+@pytest.mark.parametrize("case", LEAN3D_FP32)
+def test_fp32_3d_on_depth_walking_tiles(case):
+    """fp32 3-D problems at head dim 32 / 64 run on the 8x8 tile kernels
+    walking the window's depth planes (launches na_*_lean; the general tile
+    kernels have no fp32 instances), forward and gradients against the
+    oracle evaluated in float64 (windows of up to 147 products per element,
+    tests/_parity.py)."""
+    from natten_mps_amd import functional as F
+    from natten_mps_amd._core import _lib
+
+    sp, h, dim, ks, dil, causal, packed = case
+    if packed:
+        qkv, do = _inputs(29, [(2, *sp, 3, h, dim), (2, *sp, h, dim)], torch.float32)
+        leaf = qkv.to(DEV).requires_grad_(True)
+        q, k, v = leaf.permute(4, 0, 1, 2, 3, 5, 6).unbind(0)
+        ref_in = tuple(t.contiguous() for t in qkv.permute(4, 0, 1, 2, 3, 5, 6).unbind(0))
+    else:
+        q0, k0, v0, do = _inputs(29, [(2, *sp, h, dim)] * 4, torch.float32)
+        leaves = [t.to(DEV).requires_grad_(True) for t in (q0, k0, v0)]
+        q, k, v = leaves
+        ref_in = (q0, k0, v0)
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        out = F.na3d(q, k, v, kernel_size=ks, dilation=dil, is_causal=causal)
+        out.backward(do.to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    launched = set(_lib.profile_read(reset=True))
+    assert {"na_fwd_lean", "na_bwd_q_lean", "na_bwd_kv_lean"} <= launched, launched
+    ref, rgrads = _oracle_fwd_bwd(3, ref_in, do, ks, (1, 1, 1), dil, causal, dtype=torch.float64)
+    _close(out.detach().cpu(), ref, torch.float32, "out")
+    if packed:
+        got = [leaf.grad.cpu()[..., i, :, :] for i in range(3)]
+    else:
+        got = [t.grad.cpu() for t in leaves]
+    for n, a, b in zip(("dq", "dk", "dv"), got, rgrads):
+        _close(a, b, torch.float32, n)
+
 PACKED_TILES = [
     # rank, spatial, heads q / kv, dim, kernel, dilation, causal, dtype
     (3, (6, 10, 12), 4, 4, 64, (3, 5, 5), (1, 2, 1), (False, False, False), torch.bfloat16),
