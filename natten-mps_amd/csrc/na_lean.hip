@@ -771,15 +771,17 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
 }
 
 // ---------------------------------------------------------------------------
-// Backward, key side (one q head per kv head): over the queries attending
-// each key, dv = sum P dO and dk = scale * sum P (dP - delta) q.  The union
+// Backward, key side: over the queries attending each key (of every q head
+// of its kv head's group), dv = sum P dO and dk = scale * sum P (dP - delta)
+// q.  The union
 // of the attending queries is staged (q and dO rows, and per slot
 // -lse log2 e and -delta); a wave walks its own union rows, at most
 // MAXCH chunks.
 // ---------------------------------------------------------------------------
 // Key tile of task x (lean_task; heads are kv heads): reads the delta rows
-// the query tiles wrote.  3-D (D3): the tile walks the query planes whose
-// windows hold its key plane, staging each plane's union in turn.
+// the query tiles wrote.  The tile walks the q heads of its kv head's group
+// (GQA: rep of them) and, 3-D (D3), the query planes whose windows hold its
+// key plane, staging each (plane, q head)'s union in turn.
 // A wave walks at most MAXC chunks (the host checks its rows fit).
 template <typename T, int D, int MAXC, bool D3 = false>
 __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x) {
@@ -793,8 +795,8 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const LeanTask tk = lean_task<D3>(a.dec, x);
-    const int b = tk.b, hk = tk.h, t = tk.t, z = tk.z;  // kv head (one q head each)
-    const int h = hk;
+    const int b = tk.b, hk = tk.h, t = tk.t, z = tk.z;  // kv head
+    const int rep = static_cast<int>(a.rep.d), h0 = hk * rep;
     const int* r = a.rec_k + t * kLeanRec;
     const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
     const int U1 = ext & 0xFF, U2 = (ext >> 8) & 0xFF, E1 = (ext >> 16) & 0xFF, E2 = (ext >> 24) & 0xFF;
@@ -829,16 +831,17 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     };
     bool sin;
     const int sp = slot_pos(threadIdx.x, sin);
-    // query plane j: q and dO rows, and the lse / delta rows
-    const long long qo0 = b * a.lq.b + h * a.lq.h, go0 = b * a.ldo.b + h * a.ldo.h, lb0 = b * a.ll.b + h * a.ll.h;
+    // query plane j of q head h: q and dO rows, and the lse / delta rows
     const auto plane = [&](int j) { return static_cast<long long>(dw.z0 + j * dw.d); };
+    const auto lbase = [&](int j, int h) { return b * a.ll.b + h * a.ll.h + plane(j) * a.ll.s0; };
     const bool same_qg = a.lq.s1 == a.ldo.s1 && a.lq.s2 == a.ldo.s2;
-    const auto stage = [&](int j, float& sl, float& sd) {
-        const long long lbase = lb0 + plane(j) * a.ll.s0;
-        sl = a.lse[lbase + sp];
-        sd = a.delta[lbase + sp];
-        const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + (qo0 + plane(j) * a.lq.s0), a.qbytes);
-        const __amdgpu_buffer_rsrc_t rg = lean_rsrc(a.dout + (go0 + plane(j) * a.ldo.s0), a.dobytes);
+    const auto stage = [&](int j, int h, float& sl, float& sd) {
+        const long long lb = lbase(j, h);
+        sl = a.lse[lb + sp];
+        sd = a.delta[lb + sp];
+        const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + (b * a.lq.b + h * a.lq.h + plane(j) * a.lq.s0), a.qbytes);
+        const __amdgpu_buffer_rsrc_t rg =
+            lean_rsrc(a.dout + (b * a.ldo.b + h * a.ldo.h + plane(j) * a.ldo.s0), a.dobytes);
         if (same_qg) {
             lean_stage<T, D>(rq, rg, Qs, Gs, (ur0 * a.lq.s1 + uc0 * a.lq.s2) * ES, a.lq.s1 * a.d1 * ES,
                              a.lq.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
@@ -851,7 +854,7 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
         }
     };
     float sl, sd;
-    stage(dw.j0, sl, sd);
+    stage(dw.j0, h0, sl, sd);
     uint4 kf[NF], vf[NF];
     {
         const __amdgpu_buffer_rsrc_t rk = lean_rsrc(a.k + kbo, a.kbytes);
@@ -892,8 +895,10 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     const float* nlp = NL + first * 16 + 8 * grp;
     const float* ndp = ND + first * 16 + 8 * grp;
     const float* ninf = NL + nr * 16;
+    // the (plane, q head) steps: heads fastest
+    int j = dw.j0, h = h0;
 #pragma unroll 1
-    for (int j = dw.j0; j < dw.n; ++j) {
+    while (true) {
         wait_loads();
         if (static_cast<int>(threadIdx.x) < nr * 16) {
             NL[threadIdx.x] = sin ? -sl * kLog2e : 0.f;
@@ -902,12 +907,12 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
         // the exponent offsets of lanes whose row test fails: P = 0
         if (threadIdx.x < 8) NL[nr * 16 + threadIdx.x] = -INFINITY;
         {
-            const long long lbase = lb0 + plane(j) * a.ll.s0;
+            const long long lb = lbase(j, h);
             for (int s = threadIdx.x + 64 * kLeanWaves; s < nr * 16; s += 64 * kLeanWaves) {
                 bool in;
                 const int o = slot_pos(s, in);
-                NL[s] = in ? -a.lse[lbase + o] * kLog2e : 0.f;
-                ND[s] = in ? -a.delta[lbase + o] : 0.f;
+                NL[s] = in ? -a.lse[lb + o] * kLog2e : 0.f;
+                ND[s] = in ? -a.delta[lb + o] : 0.f;
             }
         }
         lds_publish_barrier();
@@ -936,12 +941,12 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
             lean_acc<T, D>(Gb, toff, c, s, gv);
             lean_acc<T, D>(Qb, toff, c, dp, gk);
         }
-        if constexpr (D3) {
-            if (j + 1 < dw.n) {
-                __syncthreads();  // the plane and its scalars are no longer read
-                stage(j + 1, sl, sd);
-            }
+        if (++h == h0 + rep) {
+            h = h0;
+            if (++j >= dw.n) break;
         }
+        __syncthreads();  // the staged rows and their scalars are no longer read
+        stage(j, h, sl, sd);
     }
     const bool redo = valid && item_nonfinite(lane_sum(gk, lane_sum(gv, 0.f)));
     if (valid) {
@@ -1614,11 +1619,15 @@ hipError_t lean_bwd_run(const Prob& p, const LeanGeo* gq, const LeanGeo* gk, con
     if (e != hipSuccess) return e;
     auto kern = k_lean_bwd_kv<T, D, NCH + 2, D3>;
     if ((e = allow_lds(kern, shm_k)) != hipSuccess) return e;
-    NA_LAUNCH("na_bwd_kv_lean", kern, dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves), shm_k, s, a);
+    // key tiles over the kv heads, each walking the q heads of its group
+    LeanBwdArgs<T> ak = a;
+    ak.dec = lean_decode(p, p.Hkv, gq->ntiles);
+    const long long ktasks = static_cast<long long>(p.B) * p.Hkv * gq->ntiles * p.ax[0].len;
+    NA_LAUNCH("na_bwd_kv_lean", kern, dim3(static_cast<unsigned>(ktasks)), dim3(64 * kLeanWaves), shm_k, s, ak);
     return hipGetLastError();
 }
 
-// Backward on the lean kernels (one q head per kv head); hipErrorNotSupported
+// Backward on the lean kernels; hipErrorNotSupported
 // when this problem has no lean launch.
 hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv,
                          const void* o, Lay lo, const void* dout, Lay ldo, const float* lse, Lay ll,
@@ -1626,7 +1635,6 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
                          float* delta, Lay lde, int dtype, hipStream_t s) {
     (void)lv;
     (void)ldv;
-    if (p.rep != 1) return hipErrorNotSupported;
     if (!same_lay(ll, lde) || (dlse && !same_lay(ll, ldl))) return hipErrorNotSupported;
     if (static_cast<long long>(p.B) * p.Hq * p.ax[0].len * 8192 >= (1LL << 31)) return hipErrorNotSupported;
     const bool d3 = lean_3d(p);

@@ -295,6 +295,43 @@ def test_fp32_3d_on_depth_walking_tiles(case):
     for n, a, b in zip(("dq", "dk", "dv"), got, rgrads):
         _close(a, b, torch.float32, n)
 
+GQA_LEAN = [
+    # rank, spatial, heads q / kv, dim, kernel, dilation, causal, dtype
+    (2, (24, 32), 4, 2, 32, (7, 7), (1, 1), (False, False), torch.bfloat16),
+    (2, (16, 24), 6, 2, 64, (5, 5), (1, 2), (True, False), torch.float16),
+    (2, (24, 16), 4, 1, 32, (3, 5), (2, 1), (False, False), torch.float32),
+    (3, (4, 8, 16), 4, 2, 32, (3, 3, 5), (1, 1, 1), (False, False, True), torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", GQA_LEAN)
+def test_gqa_backward_on_lean_tiles(case):
+    """GQA (fewer kv heads than q heads) on the 8x8 tile kernels: the query
+    side reads kv head h / rep, and each key tile walks the q heads of its kv
+    head's group, summing their contributions to dk and dv (launches
+    na_*_lean), against the oracle with K/V expanded per q head."""
+    from natten_mps_amd import functional as F
+    from natten_mps_amd._core import _lib
+
+    rank, sp, hq, hkv, dim, ks, dil, causal, dtype = case
+    q, k, v, do = _inputs(31, [(2, *sp, hq, dim), (2, *sp, hkv, dim), (2, *sp, hkv, dim), (2, *sp, hq, dim)],
+                          dtype)
+    fn = getattr(F, f"na{rank}d")
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        out, grads = _hip_fwd_bwd(fn, (q, k, v), do, kernel_size=ks, dilation=dil, is_causal=causal)
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    launched = set(_lib.profile_read(reset=True))
+    assert {"na_fwd_lean", "na_bwd_q_lean", "na_bwd_kv_lean"} <= launched, launched
+    ref_dtype = torch.float64 if rank == 3 else torch.float32
+    ref, rgrads = _oracle_fwd_bwd(rank, (q, k, v), do, ks, (1,) * rank, dil, causal, dtype=ref_dtype)
+    _close(out, ref, dtype, "out")
+    for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
+        _close(a, b, dtype, n)
+
 PACKED_TILES = [
     # rank, spatial, heads q / kv, dim, kernel, dilation, causal, dtype
     (3, (6, 10, 12), 4, 4, 64, (3, 5, 5), (1, 2, 1), (False, False, False), torch.bfloat16),
