@@ -67,6 +67,36 @@ at::Tensor alloc(at::IntArrayRef shape, at::ScalarType dt, const at::Device& d) 
     return at::detail::empty_cuda(shape, dt, d, std::nullopt);
 }
 
+int64_t numel(at::IntArrayRef shape) {
+    int64_t n = 1;
+    for (int64_t x : shape) n *= x;
+    return n;
+}
+
+// Several results of one call carved from one caching-allocator block (one
+// allocator call instead of one per result): each part starts on a 256-byte
+// boundary, and the block is given back when the last part is freed.
+struct Block {
+    std::vector<int64_t> off;
+    int64_t bytes = 0;
+    c10::Storage st;
+
+    int add(int64_t nbytes) {
+        bytes = (bytes + 255) & ~int64_t(255);
+        off.push_back(bytes);
+        bytes += nbytes;
+        return static_cast<int>(off.size()) - 1;
+    }
+    void allocate(const at::Device& d) { st = alloc({std::max<int64_t>(bytes, 1)}, at::kByte, d).storage(); }
+    at::Tensor part(int i, at::IntArrayRef shape, at::ScalarType dt) const {
+        at::Tensor t = at::detail::make_tensor<c10::TensorImpl>(
+            c10::Storage(st), c10::DispatchKeySet(c10::DispatchKey::CUDA), c10::scalarTypeToTypeMeta(dt));
+        t.unsafeGetTensorImpl()->set_sizes_contiguous(shape);
+        t.unsafeGetTensorImpl()->set_storage_offset(off[i] / static_cast<int64_t>(c10::elementSize(dt)));
+        return t;
+    }
+};
+
 // Workspace from the caching allocator on the current device for one call:
 // given back when the call returns (or throws).  The block belongs to the
 // stream it was taken for, so the allocator hands it out again only to work
@@ -104,8 +134,13 @@ struct FusedCall {
         if (lay.size() != kFwdLays) throw pybind11::value_error("FusedCall.forward: not a forward signature");
         c10::OptionalDeviceGuard guard;
         if (current_index() != q.get_device()) guard.reset_device(q.device());
-        at::Tensor out = alloc(out_shape, q.scalar_type(), q.device());
-        at::Tensor lse = alloc(lse_shape, at::kFloat, q.device());
+        // out and lse share one block (the autograd Function keeps both)
+        Block blk;
+        blk.add(numel(out_shape) * static_cast<int64_t>(c10::elementSize(q.scalar_type())));
+        blk.add(numel(lse_shape) * static_cast<int64_t>(sizeof(float)));
+        blk.allocate(q.device());
+        at::Tensor out = blk.part(0, out_shape, q.scalar_type());
+        at::Tensor lse = blk.part(1, lse_shape, at::kFloat);
         const int rc = natten_hip_forward(&prob, q.data_ptr(), &lay[0], k.data_ptr(), &lay[1], v.data_ptr(), &lay[2],
                                           out.data_ptr(), &lay[3], lse.data_ptr<float>(), &lay[4],
                                           reinterpret_cast<void*>(stream));
@@ -121,19 +156,28 @@ struct FusedCall {
         if (lay.size() != kBwdLays) throw pybind11::value_error("FusedCall.backward: not a backward signature");
         c10::OptionalDeviceGuard guard;
         if (current_index() != q.get_device()) guard.reset_device(q.device());
+        // dq, dk, dv and the delta rows from one block; delta's part lives as
+        // long as the gradients (lse-sized, one float per query and head)
+        Block blk;
+        const auto bytes = [](const at::Tensor& t) {
+            return t.numel() * static_cast<int64_t>(c10::elementSize(t.scalar_type()));
+        };
+        blk.add(bytes(q));
+        blk.add(bytes(k));
+        blk.add(bytes(v));
+        blk.add(numel(lse_shape) * static_cast<int64_t>(sizeof(float)));
+        blk.allocate(q.device());
+        at::Tensor dq = blk.part(0, q.sizes(), q.scalar_type());
         // dq is zeroed where stride > 1 leaves positions that are not queries
-        at::Tensor dq = alloc(q.sizes(), q.scalar_type(), q.device());
         if (strided) dq.zero_();
-        at::Tensor dk = alloc(k.sizes(), k.scalar_type(), k.device());
-        at::Tensor dv = alloc(v.sizes(), v.scalar_type(), v.device());
-        int64_t rows = 1;
-        for (int64_t x : lse_shape) rows *= x;
-        const Workspace delta(static_cast<size_t>(rows) * sizeof(float), reinterpret_cast<hipStream_t>(stream));
+        at::Tensor dk = blk.part(1, k.sizes(), k.scalar_type());
+        at::Tensor dv = blk.part(2, v.sizes(), v.scalar_type());
+        float* const delta = static_cast<float*>(blk.st.mutable_data()) + blk.off[3] / sizeof(float);
         const float* dl = d_lse.has_value() ? d_lse->data_ptr<float>() : nullptr;
         const int rc = natten_hip_backward(
             &prob, q.data_ptr(), &lay[0], k.data_ptr(), &lay[1], v.data_ptr(), &lay[2], out.data_ptr(), &lay[3],
             d_out.data_ptr(), &lay[4], lse.data_ptr<float>(), &lay[5], dl, dl ? &lay[6] : nullptr, dq.data_ptr(),
-            &lay[7], dk.data_ptr(), &lay[8], dv.data_ptr(), &lay[9], static_cast<float*>(delta.ptr), &lay[10],
+            &lay[7], dk.data_ptr(), &lay[8], dv.data_ptr(), &lay[9], delta, &lay[10],
             reinterpret_cast<void*>(stream));
         if (rc != NATTEN_OK) raise_status(rc, "backward");
         return {dq, dk, dv};
