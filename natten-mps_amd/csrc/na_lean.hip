@@ -46,6 +46,14 @@ constexpr int kLeanRec = 16;                 // dwords per tile record
 constexpr uint32_t kLeanOOR = 0x40000000u;   // offset past every staged plane's range (planes < 2^30 bytes)
 constexpr int kLeanWaves = 4;
 
+// Staged rows of a query tile reading NCH chunks per wave: a wave's first
+// row is at most 6 (2-D: union rows of its window) or 3 (1-D: 16 items per
+// wave, windows start at most one slot apart per item).
+template <bool ONE_D>
+__host__ __device__ constexpr int lean_rows(int nch) {
+    return 2 * nch + (ONE_D ? 4 : 6);
+}
+
 // Element types: bf16 / fp16 (v_mfma_f32_16x16x32, the products' operands
 // 8 elements per lane) and fp32 (v_mfma_f32_16x16x4_f32, one element per
 // lane and k-step).  A staged row of D elements is as wide as kRowD 16-bit
@@ -360,6 +368,30 @@ __device__ __forceinline__ void lean_colbias(int clo, int K2, int grp, f32x4_t (
     }
 }
 
+// 1-D tiles (64 consecutive class items per tile, 16 per wave, the union's
+// slots 16 to a staged row): the class rule of the tile's residue class from
+// its record (class size r[6], border start r[7]) and the axis.
+__device__ __forceinline__ ClassAxis lean_class1d(const int* r, const Axis& A) {
+    ClassAxis c;
+    c.n = r[6];
+    c.K = A.k;
+    c.h = A.k / 2;
+    c.B = r[7];
+    c.causal = A.causal;
+    c.qs = 1;
+    return c;
+}
+
+// Mask of chunk c for a lane whose valid slots (counted from the wave's
+// first staged row) are [lo, lo + w), as the score MFMA's accumulator input:
+// the lane's slots 32c + 8g + 4b + i -> 0 inside, -inf outside.
+__device__ __forceinline__ void lean_chunkbias(int c, int lo, int w, int grp, f32x4_t (&bias)[2]) {
+    const int t0 = 32 * c + 8 * grp - lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        bias[e >> 2][e & 3] = static_cast<unsigned>(t0 + e) < static_cast<unsigned>(w) ? 0.f : -INFINITY;
+}
+
 template <typename T, int D>
 __device__ __forceinline__ void lean_redo_fwd(const void* kargs, int z, int pos1, int pos2, int b, int h, int hk,
                                               int grp) {
@@ -386,9 +418,9 @@ __device__ __forceinline__ void lean_redo_fwd(const void* kargs, int z, int pos1
 // turn, with one online-softmax rescale per plane; 2-D: one plane, one
 // maximum, no rescale.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int NCH, bool D3 = false>
+template <typename T, int D, int NCH, bool D3 = false, bool ONE_D = false>
 __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) {
-    constexpr int NR = 2 * NCH + 6, NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
+    constexpr int NR = lean_rows<ONE_D>(NCH), NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
     unsigned char* smem = lds_base();
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + NR * 16 * D;
@@ -403,9 +435,12 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
     LeanDepth dw{0, 0, 0, 1};
     if constexpr (D3) dw = lean_depth_q(a.p.ax[0], z);
 
-    // stage the union's K and V rows (of the first key plane)
+    // stage the union's K and V rows (of the first key plane; 1-D: union
+    // slots 16 to a row)
     const long long kvo = b * a.lk.b + hk * a.lk.h;
-    const int kst = (ur0 * a.lk.s1 + uc0 * a.lk.s2) * ES, ks1 = a.lk.s1 * a.d1 * ES, ks2 = a.lk.s2 * a.d2 * ES;
+    const int ks2 = a.lk.s2 * a.d2 * ES;
+    const int kst = ONE_D ? ur0 * a.lk.s2 * ES : (ur0 * a.lk.s1 + uc0 * a.lk.s2) * ES;
+    const int ks1 = ONE_D ? 16 * ks2 : a.lk.s1 * a.d1 * ES;
     const auto stage = [&](int j) {
         const long long o = kvo + static_cast<long long>(dw.z0 + j * dw.d) * a.lk.s0;
         lean_stage<T, D>(lean_rsrc(a.k + o, a.kbytes), lean_rsrc(a.v + o, a.kbytes), Ks, Vs, kst, ks1, ks2, U1, U2,
@@ -413,10 +448,30 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
     };
     stage(dw.j0);
 
-    // the lane's query and its fragments
-    const int qr = 2 * wave + (col >> 3), qc = col & 7;
-    const bool valid = qr < E1 && qc < E2;
-    const int pos1 = pr0 + qr * a.d1, pos2 = pc0 + qc * a.d2;
+    // the lane's query and its window, relative to the wave's first staged
+    // union row (2-D: window rows [rlo, rlo + K1) and columns [clo, clo +
+    // K2); 1-D: window slots [rlo, rlo + K))
+    bool valid;
+    int pos1, pos2, first, rlo, clo = 0;
+    if constexpr (ONE_D) {
+        const ClassAxis c = lean_class1d(r, a.p.ax[2]);
+        const int item = 16 * wave + col, E = (ext >> 16) & 0xFF;
+        valid = item < E;
+        pos1 = 0;
+        pos2 = pr0 + item * a.d2;
+        const int ow = class_ws(c, pc0 + 16 * wave) - uc0;
+        first = __builtin_amdgcn_readfirstlane(ow > 0 ? ow >> 4 : 0);
+        rlo = valid ? class_ws(c, pc0 + item) - uc0 - 16 * first : 1 << 20;
+    } else {
+        const int qr = 2 * wave + (col >> 3), qc = col & 7;
+        valid = qr < E1 && qc < E2;
+        pos1 = pr0 + qr * a.d1;
+        pos2 = pc0 + qc * a.d2;
+        const int w0 = sbyte(r[6], r[7], 2 * wave), w1 = sbyte(r[6], r[7], 2 * wave + 1);
+        first = __builtin_amdgcn_readfirstlane(w0 > 0 ? w0 : 0);
+        rlo = valid ? ((col >> 3) ? w1 : w0) - first : 1 << 20;
+        clo = sbyte(r[8], r[9], qc);
+    }
     const int qoff = pos1 * a.lq.s1 + pos2 * a.lq.s2;
     const long long qbo = b * a.lq.b + h * a.lq.h + static_cast<long long>(z) * a.lq.s0;
     uint4 qf[NF];
@@ -428,13 +483,8 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
             qf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, 0));
         }
     }
-    // window of the lane's query, relative to the wave's first union row / the union's first column
-    const int w0 = sbyte(r[6], r[7], 2 * wave), w1 = sbyte(r[6], r[7], 2 * wave + 1);
-    const int first = __builtin_amdgcn_readfirstlane(w0 > 0 ? w0 : 0);
-    const int rlo = valid ? ((col >> 3) ? w1 : w0) - first : 1 << 20;
-    const int clo = sbyte(r[8], r[9], qc);
     f32x4_t cb[2];
-    lean_colbias(clo, a.K2, grp, cb);
+    if constexpr (!ONE_D) lean_colbias(clo, a.K2, grp, cb);
     int aoff[2][NF], toff[TV][D / 16];
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb)
@@ -460,10 +510,15 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
         float mx = -INFINITY;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
+            if constexpr (ONE_D) {
+                lean_chunkbias(c, rlo, a.K2, grp, cb);
+                rv[c] = true;
+            } else {
+                const int row = 2 * c + (grp >> 1) - rlo;
+                rv[c] = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1);
+            }
             s[c][0] = lean_score<T, D>(Kb, aoff, c, 0, qf, cb[0]);
             s[c][1] = lean_score<T, D>(Kb, aoff, c, 1, qf, cb[1]);
-            const int row = 2 * c + (grp >> 1) - rlo;
-            rv[c] = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1);
             mx = fmaxp(mx, rv[c] ? max8(s[c]) : -INFINITY);
         }
         float mref;
@@ -610,9 +665,9 @@ __device__ __forceinline__ void lean_redo_bwd_kv(const void* kargs, int z, int p
 // Query tile of task x (lean_task).  3-D (D3): delta = dO . O from the rows
 // (the products of one plane do not hold the window's sum), the dP products
 // start from -delta, and the tile walks its window's key planes.
-template <typename T, int D, int NCH, bool D3 = false>
+template <typename T, int D, int NCH, bool D3 = false, bool ONE_D = false>
 __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) {
-    constexpr int NR = 2 * NCH + 6, NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
+    constexpr int NR = lean_rows<ONE_D>(NCH), NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
     unsigned char* smem = lds_base();
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + NR * 16 * D;
@@ -627,16 +682,37 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
     LeanDepth dw{0, 0, 0, 1};
     if constexpr (D3) dw = lean_depth_q(a.p.ax[0], z);
     const long long kvo = b * a.lk.b + hk * a.lk.h;
-    const int kst = (ur0 * a.lk.s1 + uc0 * a.lk.s2) * ES, ks1 = a.lk.s1 * a.d1 * ES, ks2 = a.lk.s2 * a.d2 * ES;
+    const int ks2 = a.lk.s2 * a.d2 * ES;
+    const int kst = ONE_D ? ur0 * a.lk.s2 * ES : (ur0 * a.lk.s1 + uc0 * a.lk.s2) * ES;
+    const int ks1 = ONE_D ? 16 * ks2 : a.lk.s1 * a.d1 * ES;
     const auto stage = [&](int j) {
         const long long o = kvo + static_cast<long long>(dw.z0 + j * dw.d) * a.lk.s0;
         lean_stage<T, D>(lean_rsrc(a.k + o, a.kbytes), lean_rsrc(a.v + o, a.kbytes), Ks, Vs, kst, ks1, ks2, U1, U2,
                          nst, wave, lane);
     };
     stage(dw.j0);
-    const int qr = 2 * wave + (col >> 3), qc = col & 7;
-    const bool valid = qr < E1 && qc < E2;
-    const int pos1 = pr0 + qr * a.d1, pos2 = pc0 + qc * a.d2;
+    // the lane's query and its window (as in k_lean_fwd)
+    bool valid;
+    int pos1, pos2, first, rlo, clo = 0;
+    if constexpr (ONE_D) {
+        const ClassAxis c = lean_class1d(r, a.p.ax[2]);
+        const int item = 16 * wave + col, E = (ext >> 16) & 0xFF;
+        valid = item < E;
+        pos1 = 0;
+        pos2 = pr0 + item * a.d2;
+        const int ow = class_ws(c, pc0 + 16 * wave) - uc0;
+        first = __builtin_amdgcn_readfirstlane(ow > 0 ? ow >> 4 : 0);
+        rlo = valid ? class_ws(c, pc0 + item) - uc0 - 16 * first : 1 << 20;
+    } else {
+        const int qr = 2 * wave + (col >> 3), qc = col & 7;
+        valid = qr < E1 && qc < E2;
+        pos1 = pr0 + qr * a.d1;
+        pos2 = pc0 + qc * a.d2;
+        const int w0 = sbyte(r[6], r[7], 2 * wave), w1 = sbyte(r[6], r[7], 2 * wave + 1);
+        first = __builtin_amdgcn_readfirstlane(w0 > 0 ? w0 : 0);
+        rlo = valid ? ((col >> 3) ? w1 : w0) - first : 1 << 20;
+        clo = sbyte(r[8], r[9], qc);
+    }
     const long long zl = z;
     const int qoff = pos1 * a.lq.s1 + pos2 * a.lq.s2;
     const long long qbo = b * a.lq.b + h * a.lq.h + zl * a.lq.s0;
@@ -667,11 +743,19 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
     }
     const float L2 = valid ? a.lse[lo] * kLog2e : 0.f;
     const float dl = (valid && a.dlse) ? a.dlse[lo] : 0.f;
-    const int w0 = sbyte(r[6], r[7], 2 * wave), w1 = sbyte(r[6], r[7], 2 * wave + 1);
-    const int first = __builtin_amdgcn_readfirstlane(w0 > 0 ? w0 : 0);
-    const int rlo = valid ? ((col >> 3) ? w1 : w0) - first : 1 << 20;
     f32x4_t cb[2];
-    lean_colbias(sbyte(r[8], r[9], qc), a.K2, grp, cb);
+    if constexpr (!ONE_D) lean_colbias(clo, a.K2, grp, cb);
+    // chunk c's mask (1-D) and row offset of the exponent (2-D: -inf where
+    // the row test fails)
+    const auto chunk_mask = [&](int c, float& off) {
+        if constexpr (ONE_D) {
+            lean_chunkbias(c, rlo, a.K2, grp, cb);
+            off = -L2;
+        } else {
+            const int row = 2 * c + (grp >> 1) - rlo;
+            off = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1) ? -L2 : -INFINITY;
+        }
+    };
     int aoff[2][NF], toff[TV][D / 16];
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb)
@@ -701,8 +785,8 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
             __syncthreads();
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
-                const int row = 2 * c + (grp >> 1) - rlo;
-                const float off = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1) ? -L2 : -INFINITY;
+                float off;
+                chunk_mask(c, off);
                 f32x4_t ds[2];
 #pragma unroll
                 for (int bb = 0; bb < 2; ++bb) {
@@ -732,8 +816,8 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
             float part = 0.f;
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
-                const int row = 2 * c + (grp >> 1) - rlo;
-                const float off = static_cast<unsigned>(row) < static_cast<unsigned>(a.K1) ? -L2 : -INFINITY;
+                float off;
+                chunk_mask(c, off);
 #pragma unroll
                 for (int bb = 0; bb < 2; ++bb) {
                     const f32x4_t sc = lean_score<T, D>(Kb, aoff, c, bb, qf, cb[bb]);
@@ -783,7 +867,7 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
 // (GQA: rep of them) and, 3-D (D3), the query planes whose windows hold its
 // key plane, staging each (plane, q head)'s union in turn.
 // A wave walks at most MAXC chunks (the host checks its rows fit).
-template <typename T, int D, int MAXC, bool D3 = false>
+template <typename T, int D, int MAXC, bool D3 = false, bool ONE_D = false>
 __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x) {
     constexpr int NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
     const int nr = a.nr;
@@ -800,9 +884,10 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     const int* r = a.rec_k + t * kLeanRec;
     const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
     const int U1 = ext & 0xFF, U2 = (ext >> 8) & 0xFF, E1 = (ext >> 16) & 0xFF, E2 = (ext >> 24) & 0xFF;
-    const int kr = 2 * wave + (col >> 3), kc = col & 7;
-    const bool valid = kr < E1 && kc < E2;
-    const int pos1 = pr0 + kr * a.d1, pos2 = pc0 + kc * a.d2;
+    // the lane's key (1-D: item 16 w + n of the tile's 64)
+    const int kr = 2 * wave + (col >> 3), kc = col & 7, item = 16 * wave + col;
+    const bool valid = ONE_D ? item < E1 : (kr < E1 && kc < E2);
+    const int pos1 = ONE_D ? 0 : pr0 + kr * a.d1, pos2 = ONE_D ? pr0 + item * a.d2 : pc0 + kc * a.d2;
     const long long zl = z;
     const int koff = pos1 * a.lk.s1 + pos2 * a.lk.s2;
     const long long kbo = b * a.lk.b + hk * a.lk.h + zl * a.lk.s0;
@@ -825,6 +910,10 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     }
     // per-slot -lse log2 e and -delta: slot threadIdx.x (and up, past 256 slots)
     const auto slot_pos = [&](int sidx, bool& in) {
+        if constexpr (ONE_D) {
+            in = sidx < r[8];  // the union's members
+            return (ur0 + (in ? sidx : 0) * a.d2) * a.ll.s2;
+        }
         const int u = sidx >> 4, cc = sidx & 15;
         in = u < U1 && cc < U2;
         return (ur0 + (in ? u : 0) * a.d1) * a.ll.s1 + (uc0 + (in ? cc : 0) * a.d2) * a.ll.s2;
@@ -842,15 +931,15 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
         const __amdgpu_buffer_rsrc_t rq = lean_rsrc(a.q + (b * a.lq.b + h * a.lq.h + plane(j) * a.lq.s0), a.qbytes);
         const __amdgpu_buffer_rsrc_t rg =
             lean_rsrc(a.dout + (b * a.ldo.b + h * a.ldo.h + plane(j) * a.ldo.s0), a.dobytes);
+        // union rows: 2-D one row per union row; 1-D 16 union slots per row
+        const auto base = [&](const LeanLay& l) { return (ONE_D ? ur0 * l.s2 : ur0 * l.s1 + uc0 * l.s2) * ES; };
+        const auto step1 = [&](const LeanLay& l) { return ONE_D ? 16 * l.s2 * a.d2 * ES : l.s1 * a.d1 * ES; };
         if (same_qg) {
-            lean_stage<T, D>(rq, rg, Qs, Gs, (ur0 * a.lq.s1 + uc0 * a.lq.s2) * ES, a.lq.s1 * a.d1 * ES,
-                             a.lq.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
+            lean_stage<T, D>(rq, rg, Qs, Gs, base(a.lq), step1(a.lq), a.lq.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
         } else {
             // q and dO rows at different strides (a packed qkv tensor's views)
-            lean_stage1<T, D>(rq, Qs, (ur0 * a.lq.s1 + uc0 * a.lq.s2) * ES, a.lq.s1 * a.d1 * ES,
-                              a.lq.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
-            lean_stage1<T, D>(rg, Gs, (ur0 * a.ldo.s1 + uc0 * a.ldo.s2) * ES, a.ldo.s1 * a.d1 * ES,
-                              a.ldo.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
+            lean_stage1<T, D>(rq, Qs, base(a.lq), step1(a.lq), a.lq.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
+            lean_stage1<T, D>(rg, Gs, base(a.ldo), step1(a.ldo), a.ldo.s2 * a.d2 * ES, U1, U2, nst, wave, lane);
         }
     };
     float sl, sd;
@@ -866,17 +955,27 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
             vf[ks] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, 0));
         }
     }
-    // the wave's union rows [first, last]; the lane's attending rows and columns
-    const int first = __builtin_amdgcn_readfirstlane(sbyte(r[6], r[7], 2 * wave));
-    const int last = __builtin_amdgcn_readfirstlane(sbyte(r[10], r[11], 2 * wave + 1));
-    const int nch = (last - first + 2) >> 1;
-    // attending rows [rlo, rlo + rn) of the wave's rows, columns [clo, chi];
-    // an unattended key has an empty range (rn <= 0, chi < clo)
-    const int rlo = sbyte(r[6], r[7], kr) - first;
-    const int rn = valid ? sbyte(r[10], r[11], kr) - first - rlo + 1 : 0;
-    const int clo = sbyte(r[8], r[9], kc), chi = sbyte(r[12], r[13], kc);
+    // the wave's first staged row and chunk count; the lane's attending
+    // queries (2-D: rows [rlo, rlo + rn) and columns [clo, chi]; 1-D: slots
+    // [rlo, rlo + rn) from the first row); an unattended key has an empty range
+    int first, nch, rlo, rn;
     f32x4_t cb[2];
-    lean_colbias(clo, chi >= clo ? chi - clo + 1 : 0, grp, cb);
+    if constexpr (ONE_D) {
+        first = __builtin_amdgcn_readfirstlane(sbyte(r[9], r[9], wave));
+        nch = __builtin_amdgcn_readfirstlane(sbyte(r[10], r[10], wave));
+        int alo, ahi;
+        class_span(lean_class1d(r, a.p.ax[2]), pc0 + (valid ? item : 0), alo, ahi);
+        rlo = alo - uc0 - 16 * first;
+        rn = valid ? ahi - alo + 1 : 0;
+    } else {
+        first = __builtin_amdgcn_readfirstlane(sbyte(r[6], r[7], 2 * wave));
+        const int last = __builtin_amdgcn_readfirstlane(sbyte(r[10], r[11], 2 * wave + 1));
+        nch = (last - first + 2) >> 1;
+        rlo = sbyte(r[6], r[7], kr) - first;
+        rn = valid ? sbyte(r[10], r[11], kr) - first - rlo + 1 : 0;
+        const int clo = sbyte(r[8], r[9], kc), chi = sbyte(r[12], r[13], kc);
+        lean_colbias(clo, chi >= clo ? chi - clo + 1 : 0, grp, cb);
+    }
     int aoff[2][NF], toff[TV][D / 16];
 #pragma unroll
     for (int bb = 0; bb < 2; ++bb)
@@ -919,9 +1018,15 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
 #pragma unroll
         for (int c = 0; c < MAXC; ++c) {
             if (c >= nch) break;  // wave-uniform
-            const int row = 2 * c + (grp >> 1) - rlo;
-            // a failed row test reads the -inf entries (one select per chunk)
-            const float* nlc = (row >= 0 && row < rn) ? nlp + 32 * c : ninf;
+            const float* nlc;
+            if constexpr (ONE_D) {
+                lean_chunkbias(c, rlo, rn > 0 ? rn : 0, grp, cb);
+                nlc = nlp + 32 * c;
+            } else {
+                const int row = 2 * c + (grp >> 1) - rlo;
+                // a failed row test reads the -inf entries (one select per chunk)
+                nlc = (row >= 0 && row < rn) ? nlp + 32 * c : ninf;
+            }
             const f32x4_t nd[2] = {*reinterpret_cast<const f32x4_t*>(ndp + 32 * c),
                                    *reinterpret_cast<const f32x4_t*>(ndp + 32 * c + 4)};
             const f32x4_t nl[2] = {*reinterpret_cast<const f32x4_t*>(nlc), *reinterpret_cast<const f32x4_t*>(nlc + 4)};
@@ -961,14 +1066,14 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     if (redo) lean_redo_bwd_kv<T, D>(kernargs(), opaque(z), opaque(pos1), opaque(pos2), b, hk, grp);
 }
 
-template <typename T, int D, int NCH, bool D3 = false>
+template <typename T, int D, int NCH, bool D3 = false, bool ONE_D = false>
 __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_q(LeanBwdArgs<T> a) {
-    lean_bwd_q_tile<T, D, NCH, D3>(a, xcd_block(blockIdx.x, gridDim.x));
+    lean_bwd_q_tile<T, D, NCH, D3, ONE_D>(a, xcd_block(blockIdx.x, gridDim.x));
 }
 
-template <typename T, int D, int MAXC, bool D3 = false>
+template <typename T, int D, int MAXC, bool D3 = false, bool ONE_D = false>
 __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> a) {
-    lean_bwd_kv_tile<T, D, MAXC, D3>(a, xcd_block(blockIdx.x, gridDim.x));
+    lean_bwd_kv_tile<T, D, MAXC, D3, ONE_D>(a, xcd_block(blockIdx.x, gridDim.x));
 }
 
 // ---------------------------------------------------------------------------
@@ -1233,6 +1338,97 @@ void split_table(const Axis& A, int r, const LeanAxisTile& a, int* out4) {
     for (int i = 0; i < 4; ++i) out4[i] = pack_bytes(d, 4 * i);
 }
 
+// A 1-D problem (axes 0 and 1 of extent 1): tiles of 64 consecutive class
+// items along axis 2.
+bool lean_1d(const Prob& p) { return p.ax[0].len == 1 && p.ax[1].len == 1 && p.ax[1].k == 1; }
+
+// Chunks of 32 slots a wave of a 1-D query tile reads: its 16 windows from
+// the staged row holding the first of them (up to 15 slots in).
+int lean_nch_1d(int K) { return std::max(1, (K + 30 + 31) / 32); }
+
+// Records of the 1-D tiles (one per 64 class items of each residue class):
+// query tiles (key false) pos0, J, the union's first position and class
+// coordinate, ext (staged rows | 16 << 8 | items << 16), rows to stage, the
+// class size and border start, the union's size; key tiles also each
+// wave's first staged row (bytes of [9]) and chunk count (bytes of [10]),
+// and [14] = 1 where no query attends the tile.  False when a wave's
+// windows (attending spans) do not fit nch (key tiles: nch + 2) chunks.
+bool lean_records_1d(const Prob& p, bool key, int nch, std::vector<int>& h, int& nst_max, int& rows_max) {
+    const Axis& A = p.ax[2];
+    for (int r = 0; r < A.dil; ++r) {
+        const ClassAxis c = class_axis(A, r);
+        for (int J = 0; J < c.n; J += 64) {
+            const int E = std::min(64, c.n - J), jend = J + E - 1;
+            int rec[kLeanRec] = {};
+            rec[0] = r + J * A.dil;
+            rec[1] = J;
+            rec[6] = c.n;
+            rec[7] = c.B;
+            int U0, Uend;
+            if (!key) {
+                U0 = std::max(class_ws(c, J), 0);
+                Uend = std::min(class_ws(c, jend) + c.K - 1, c.n - 1);
+            } else {
+                U0 = c.n;
+                Uend = -1;
+                for (int u = J; u <= jend; ++u) {
+                    int lo, hi;
+                    class_span(c, u, lo, hi);
+                    if (lo <= hi) {
+                        U0 = std::min(U0, lo);
+                        Uend = std::max(Uend, hi);
+                    }
+                }
+            }
+            if (Uend < U0) {  // key tile that no query attends: extents only (zero gradients)
+                rec[4] = E << 16;
+                rec[14] = 1;
+                h.insert(h.end(), rec, rec + kLeanRec);
+                continue;
+            }
+            const int NU = Uend - U0 + 1, rows = (NU + 15) / 16;
+            int nst = rows, fb[4] = {}, nb[4] = {};
+            for (int w = 0; w < 4 && 16 * w < E; ++w) {
+                const int u0 = J + 16 * w, u1 = std::min(u0 + 15, jend);
+                int first, end = 0;  // end: one past the wave's last slot, from its first row
+                if (!key) {
+                    first = std::max(class_ws(c, u0) - U0, 0) >> 4;
+                    for (int j = u0; j <= u1; ++j) end = std::max(end, class_ws(c, j) - U0 - 16 * first + c.K);
+                } else {
+                    int wlo = c.n, whi = -1;
+                    for (int u = u0; u <= u1; ++u) {
+                        int lo, hi;
+                        class_span(c, u, lo, hi);
+                        if (lo <= hi) {
+                            wlo = std::min(wlo, lo);
+                            whi = std::max(whi, hi);
+                        }
+                    }
+                    if (whi < wlo) continue;  // no key of the wave is attended
+                    first = (wlo - U0) >> 4;
+                    end = whi - U0 - 16 * first + 1;
+                }
+                const int need = (end + 31) / 32;
+                if (need > (key ? nch + 2 : nch)) return false;
+                fb[w] = first;
+                nb[w] = need;
+                nst = std::max(nst, first + 2 * (key ? need : nch));
+                rows_max = std::max(rows_max, 2 * need);
+            }
+            rec[2] = r + U0 * A.dil;
+            rec[3] = U0;
+            rec[4] = rows | (16 << 8) | (E << 16);
+            rec[5] = nst;
+            rec[8] = NU;
+            rec[9] = pack_bytes(fb, 0);
+            rec[10] = pack_bytes(nb, 0);
+            nst_max = std::max(nst_max, nst);
+            h.insert(h.end(), rec, rec + kLeanRec);
+        }
+    }
+    return true;
+}
+
 // Builds (or finds) the records.  Query tiles: rows of a wave start at
 // max(ws[2w], 0) and span at most K1 + 1 rows; nst = rows to stage.  Mode:
 // 0 query tiles, 1 key tiles, 2 key tiles of the split key side (each key
@@ -1262,6 +1458,9 @@ const LeanGeo* lean_geometry(const Prob& p, int mode, int nch, hipStream_t s) {
     const Axis &A1 = p.ax[1], &A2 = p.ax[2];
     std::vector<int> h;
     int nst_max = 0, rows_max = 0, u2_max = 1;
+    if (lean_1d(p)) {
+        if (mode == 2 || !lean_records_1d(p, key, nch, h, nst_max, rows_max)) return nullptr;
+    } else {
     for (int r1 = 0; r1 < A1.dil; ++r1) {
         const int n1 = (A1.len - r1 + A1.dil - 1) / A1.dil;
         for (int r2 = 0; r2 < A2.dil; ++r2) {
@@ -1322,7 +1521,8 @@ const LeanGeo* lean_geometry(const Prob& p, int mode, int nch, hipStream_t s) {
             }
         }
     }
-    if (!key && nst_max > 2 * nch + 6) return nullptr;
+    }
+    if (!key && nst_max > (lean_1d(p) ? lean_rows<true>(nch) : lean_rows<false>(nch))) return nullptr;
     if (key && nst_max > 32) return nullptr;
     int* d = nullptr;
     const size_t bytes = h.size() * sizeof(int);
@@ -1392,6 +1592,9 @@ void lean_audit_one(LdsAudit& a) {
     audit_one(k_lean_fwd<T, D, NCH>, "k_lean_fwd", a);
     audit_one(k_lean_bwd_q<T, D, NCH>, "k_lean_bwd_q", a);
     audit_one(k_lean_bwd_kv<T, D, NCH + 2>, "k_lean_bwd_kv", a);
+    audit_one(k_lean_fwd<T, D, NCH, false, true>, "k_lean_fwd (1-D)", a);
+    audit_one(k_lean_bwd_q<T, D, NCH, false, true>, "k_lean_bwd_q (1-D)", a);
+    audit_one(k_lean_bwd_kv<T, D, NCH + 2, false, true>, "k_lean_bwd_kv (1-D)", a);
     if constexpr (!kF32<T>) {
         audit_one(k_lean_wsum_key<T, D, NCH + 2>, "k_lean_wsum_key", a);
     } else {
@@ -1444,15 +1647,21 @@ bool lean_eligible(const Prob& p, int dtype, bool aligned, std::initializer_list
                    std::initializer_list<Lay> kvside, std::initializer_list<Lay> rows) {
     if (!lean_switch() || !aligned || !(p.scale > 0.f) || !lean_static_lds_ok()) return false;
     if (p.Dqk != p.Dv || (p.Dqk != 32 && p.Dqk != 64)) return false;
-    // a short first in-plane axis (1-D problems) stays on the general tiles,
-    // which lay a 1-D axis out along whole tiles
-    if (p.ax[1].len < 8) return false;
-    const bool d3 = lean_3d(p);
-    if (!d3 && p.ax[0].k != 1) return false;
-    if (d3 && (dtype != NATTEN_F32 || p.ax[0].st != 1 || p.ax[0].len >= (1 << 15))) return false;
-    for (int a = 1; a < 3; ++a) {
-        const Axis& A = p.ax[a];
-        if (A.st != 1 || A.k > 9 || A.len >= (1 << 15)) return false;
+    // 1-D problems run as 64-item tiles along axis 2 (K <= 129: at most 5
+    // chunks per wave); a short first in-plane axis otherwise stays on the
+    // general tiles
+    const bool d1 = lean_1d(p), d3 = lean_3d(p);
+    if (d1) {
+        const Axis& A = p.ax[2];
+        if (A.st != 1 || A.k > 129 || lean_nch_1d(A.k) > 5 || A.len >= (1 << 30)) return false;
+    } else {
+        if (p.ax[1].len < 8) return false;
+        if (!d3 && p.ax[0].k != 1) return false;
+        if (d3 && (dtype != NATTEN_F32 || p.ax[0].st != 1 || p.ax[0].len >= (1 << 15))) return false;
+        for (int a = 1; a < 3; ++a) {
+            const Axis& A = p.ax[a];
+            if (A.st != 1 || A.k > 9 || A.len >= (1 << 15)) return false;
+        }
     }
     if (kvside.size() % 2 != 0 || !all_same(rows)) return false;
     for (const Lay* l = kvside.begin(); l != kvside.end(); l += 2)
@@ -1484,7 +1693,7 @@ int lean_lds_audit(int* checked) {
     return a.bad == 0 ? 1 : 0;
 }
 
-template <typename T, int D, int NCH, bool D3>
+template <typename T, int D, int NCH, bool D3, bool ONE_D = false>
 hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, const void* k, Lay lk,
                         const void* v, void* o, Lay lo, float* lse, Lay ll, hipStream_t s) {
     LeanFwdArgs<T> a{};
@@ -1510,9 +1719,10 @@ hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, 
     a.sc2 = p.scale * kLog2e;
     a.p = p;
     const long long blocks = static_cast<long long>(p.B) * p.Hq * g->ntiles * p.ax[0].len;
-    const size_t shm = kLdsPad + static_cast<size_t>(2) * (2 * NCH + 6) * 16 * D * sizeof(T);
+    if (blocks >= (1LL << 31)) return hipErrorNotSupported;
+    const size_t shm = kLdsPad + static_cast<size_t>(2) * lean_rows<ONE_D>(NCH) * 16 * D * sizeof(T);
     if (shm > 160 * 1024) return hipErrorNotSupported;
-    auto kern = k_lean_fwd<T, D, NCH, D3>;
+    auto kern = k_lean_fwd<T, D, NCH, D3, ONE_D>;
     const hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
     NA_LAUNCH("na_fwd_lean", kern, dim3(static_cast<unsigned>(blocks)), dim3(64 * kLeanWaves), shm, s, a);
@@ -1524,16 +1734,19 @@ hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, 
 hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay lk, const void* v, Lay lv, void* o,
                         Lay lo, float* lse, Lay ll, int dtype, hipStream_t s) {
     (void)lv;
-    const int nch = lean_nch(p.ax[1].k);
+    const bool d1 = lean_1d(p), d3 = lean_3d(p);
+    const int nch = d1 ? lean_nch_1d(p.ax[2].k) : lean_nch(p.ax[1].k);
     if (static_cast<long long>(p.B) * p.Hq * p.ax[0].len * 4096 >= (1LL << 31)) return hipErrorNotSupported;
     const LeanGeo* g = lean_geometry(p, 0, nch, s);
     if (!g) return hipErrorNotSupported;
-    const bool d3 = lean_3d(p);
     // 3-D instances exist for fp32 only (the eligibility keeps 16-bit 3-D away)
-#define NA_LF(T, DD, N) return lean_fwd_run<T, DD, N, false>(p, g, q, lq, k, lk, v, o, lo, lse, ll, s)
-#define NA_LF3(T, DD, N)                                                              \
-    return d3 ? lean_fwd_run<T, DD, N, true>(p, g, q, lq, k, lk, v, o, lo, lse, ll, s) \
-              : lean_fwd_run<T, DD, N, false>(p, g, q, lq, k, lk, v, o, lo, lse, ll, s)
+#define NA_LF_ARGS p, g, q, lq, k, lk, v, o, lo, lse, ll, s
+#define NA_LF(T, DD, N)                                                      \
+    return d1 ? lean_fwd_run<T, DD, N, false, true>(NA_LF_ARGS) \
+              : lean_fwd_run<T, DD, N, false>(NA_LF_ARGS)
+#define NA_LF3(T, DD, N)                                                                         \
+    return d1 ? lean_fwd_run<T, DD, N, false, true>(NA_LF_ARGS)                                  \
+              : (d3 ? lean_fwd_run<T, DD, N, true>(NA_LF_ARGS) : lean_fwd_run<T, DD, N, false>(NA_LF_ARGS))
 #define NA_LF_N(T, DD, F)    \
     switch (nch) {           \
         case 1: F(T, DD, 1); \
@@ -1556,6 +1769,7 @@ hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay
 #undef NA_LF_N
 #undef NA_LF3
 #undef NA_LF
+#undef NA_LF_ARGS
 }
 
 template <typename T, int D>
@@ -1598,7 +1812,7 @@ LeanBwdArgs<T> lean_bwd_args(const Prob& p, const void* q, Lay lq, const void* k
     return a;
 }
 
-template <typename T, int D, int NCH, bool D3>
+template <typename T, int D, int NCH, bool D3, bool ONE_D = false>
 hipError_t lean_bwd_run(const Prob& p, const LeanGeo* gq, const LeanGeo* gk, const LeanBwdArgs<T>& base,
                         hipStream_t s) {
     LeanBwdArgs<T> a = base;
@@ -1606,18 +1820,18 @@ hipError_t lean_bwd_run(const Prob& p, const LeanGeo* gq, const LeanGeo* gk, con
     a.rec_k = gk->ptr;
     a.dec = lean_decode(p, p.Hq, gq->ntiles);
     a.nr = std::max(gk->nst_max, 1);
-    const size_t shm_q = kLdsPad + static_cast<size_t>(2) * (2 * NCH + 6) * 16 * D * sizeof(T);
+    const size_t shm_q = kLdsPad + static_cast<size_t>(2) * lean_rows<ONE_D>(NCH) * 16 * D * sizeof(T);
     const size_t shm_k =
         kLdsPad + static_cast<size_t>(a.nr) * 16 * (2 * D * sizeof(T) + 2 * sizeof(float)) + 8 * sizeof(float);
     const long long tasks = static_cast<long long>(p.B) * p.Hq * gq->ntiles * p.ax[0].len;
-    if (shm_q > 160 * 1024 || shm_k > 160 * 1024) return hipErrorNotSupported;
-    auto kq = k_lean_bwd_q<T, D, NCH, D3>;
+    if (tasks >= (1LL << 31) || shm_q > 160 * 1024 || shm_k > 160 * 1024) return hipErrorNotSupported;
+    auto kq = k_lean_bwd_q<T, D, NCH, D3, ONE_D>;
     hipError_t e = allow_lds(kq, shm_q);
     if (e != hipSuccess) return e;
     NA_LAUNCH("na_bwd_q_lean", kq, dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves), shm_q, s, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    auto kern = k_lean_bwd_kv<T, D, NCH + 2, D3>;
+    auto kern = k_lean_bwd_kv<T, D, NCH + 2, D3, ONE_D>;
     if ((e = allow_lds(kern, shm_k)) != hipSuccess) return e;
     // key tiles over the kv heads, each walking the q heads of its group
     LeanBwdArgs<T> ak = a;
@@ -1637,18 +1851,21 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
     (void)ldv;
     if (!same_lay(ll, lde) || (dlse && !same_lay(ll, ldl))) return hipErrorNotSupported;
     if (static_cast<long long>(p.B) * p.Hq * p.ax[0].len * 8192 >= (1LL << 31)) return hipErrorNotSupported;
-    const bool d3 = lean_3d(p);
+    const bool d1 = lean_1d(p), d3 = lean_3d(p);
     if (d3 && dtype != NATTEN_F32) return hipErrorNotSupported;  // 3-D instances exist for fp32 only
-    const int nch = lean_nch(p.ax[1].k);
+    const int nch = d1 ? lean_nch_1d(p.ax[2].k) : lean_nch(p.ax[1].k);
     const LeanGeo* gq = lean_geometry(p, 0, nch, s);
     const LeanGeo* gk = gq ? lean_geometry(p, 1, nch, s) : nullptr;
     if (!gq || !gk || gq->ntiles != gk->ntiles || gk->rows_max > 2 * (nch + 2)) return hipErrorNotSupported;
 #define NA_LB_A(T, DD) \
     lean_bwd_args<T, DD>(p, q, lq, k, lk, v, o, lo, dout, ldo, lse, ll, dlse, dq, ldq, dk, ldk, dv, delta)
-#define NA_LB(T, DD, N) return lean_bwd_run<T, DD, N, false>(p, gq, gk, NA_LB_A(T, DD), s)
-#define NA_LB3(T, DD, N)                                                         \
-    return d3 ? lean_bwd_run<T, DD, N, true>(p, gq, gk, NA_LB_A(T, DD), s) \
+#define NA_LB(T, DD, N)                                                         \
+    return d1 ? lean_bwd_run<T, DD, N, false, true>(p, gq, gk, NA_LB_A(T, DD), s) \
               : lean_bwd_run<T, DD, N, false>(p, gq, gk, NA_LB_A(T, DD), s)
+#define NA_LB3(T, DD, N)                                                              \
+    return d1 ? lean_bwd_run<T, DD, N, false, true>(p, gq, gk, NA_LB_A(T, DD), s)     \
+              : (d3 ? lean_bwd_run<T, DD, N, true>(p, gq, gk, NA_LB_A(T, DD), s)      \
+                    : lean_bwd_run<T, DD, N, false>(p, gq, gk, NA_LB_A(T, DD), s))
 #define NA_LB_N(T, DD, F)    \
     switch (nch) {           \
         case 1: F(T, DD, 1); \

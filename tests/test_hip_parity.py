@@ -332,12 +332,67 @@ def test_gqa_backward_on_lean_tiles(case):
     for n, a, b in zip(("dq", "dk", "dv"), grads, rgrads):
         _close(a, b, dtype, n)
 
+LEAN1D = [
+    # length, heads q / kv, dim, kernel, dilation, causal, dtype, q/k/v as views of one packed tensor
+    (300, 4, 2, 64, 33, 1, True, torch.bfloat16, False),
+    (517, 2, 2, 32, 7, 3, False, torch.float16, False),
+    (70, 2, 1, 64, 9, 4, False, torch.bfloat16, False),
+    (1000, 4, 4, 32, 65, 2, True, torch.bfloat16, True),
+    (200, 2, 2, 32, 33, 1, False, torch.float32, False),
+    (333, 4, 2, 64, 15, 2, True, torch.float32, False),
+    (1000, 2, 2, 32, 129, 1, False, torch.float32, False),
+    (40, 2, 2, 64, 4, 1, False, torch.float32, True),
+]
+
+
+@pytest.mark.parametrize("case", LEAN1D)
+def test_1d_on_lean_tiles(case):
+    """1-D problems on the tile kernels' 1-D mode (64 consecutive class items
+    per tile, the union staged 16 slots to a row, each wave's windows masked
+    per 32-slot chunk; launches na_*_lean), forward and gradients against the
+    oracle (fp32 against the oracle in float64 where a window sums more than
+    64 products)."""
+    from natten_mps_amd import functional as F
+    from natten_mps_amd._core import _lib
+
+    L, hq, hkv, dim, ks, dil, causal, dtype, packed = case
+    if packed:
+        qkv, do = _inputs(37, [(2, L, 3, hq, dim), (2, L, hq, dim)], dtype)
+        leaves = [qkv.to(DEV).requires_grad_(True)]
+        q, k, v = leaves[0].permute(2, 0, 1, 3, 4).unbind(0)
+        ref_in = tuple(t.contiguous() for t in qkv.permute(2, 0, 1, 3, 4).unbind(0))
+    else:
+        q0, k0, v0, do = _inputs(37, [(2, L, hq, dim), (2, L, hkv, dim), (2, L, hkv, dim), (2, L, hq, dim)], dtype)
+        leaves = [t.to(DEV).requires_grad_(True) for t in (q0, k0, v0)]
+        q, k, v = leaves
+        ref_in = (q0, k0, v0)
+    _lib.profile_read(reset=True)
+    _lib.profile_enable(True)
+    try:
+        out = F.na1d(q, k, v, kernel_size=ks, dilation=dil, is_causal=causal)
+        out.backward(do.to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        _lib.profile_enable(False)
+    launched = set(_lib.profile_read(reset=True))
+    assert {"na_fwd_lean", "na_bwd_q_lean", "na_bwd_kv_lean"} <= launched, launched
+    ref_dtype = torch.float64 if (dtype == torch.float32 and ks > 64) else torch.float32
+    ref, rgrads = _oracle_fwd_bwd(1, ref_in, do, (ks,), (1,), (dil,), (causal,), dtype=ref_dtype)
+    _close(out.detach().cpu(), ref, dtype, "out")
+    if packed:
+        got = [leaves[0].grad.cpu()[:, :, i] for i in range(3)]
+    else:
+        got = [t.grad.cpu() for t in leaves]
+    for n, a, b in zip(("dq", "dk", "dv"), got, rgrads):
+        _close(a, b, dtype, n)
+
 PACKED_TILES = [
     # rank, spatial, heads q / kv, dim, kernel, dilation, causal, dtype
     (3, (6, 10, 12), 4, 4, 64, (3, 5, 5), (1, 2, 1), (False, False, False), torch.bfloat16),
     (3, (5, 8, 9), 2, 2, 32, (3, 3, 5), (1, 1, 1), (True, False, False), torch.float16),
     (1, (300,), 4, 2, 64, (9,), (2,), (True,), torch.bfloat16),
     (1, (257,), 6, 3, 32, (13,), (1,), (False,), torch.float16),
+    (1, (190,), 4, 2, 128, (11,), (1,), (False,), torch.bfloat16),
 ]
 
 
@@ -346,8 +401,10 @@ def test_tile_kernels_on_packed_views(case):
     """The nn modules' layouts on the general tile kernels: q, k and v as
     views of one packed [B, *sp, 3, heads, D] tensor, or (GQA) q contiguous
     and k, v views of a packed [B, *sp, 2, kv heads, D] tensor; out and the
-    gradients contiguous.  These run in the layout group that keeps q; k and
-    v; out, dO and dq; dk and dv at one layout each, and match the oracle."""
+    gradients contiguous.  The general tile kernels run these in the layout
+    group that keeps q; k and v; out, dO and dq; dk and dv at one layout each
+    (1-D problems at head dim 32 / 64 run the 8x8 tile kernels' 1-D mode,
+    which takes every operand at its own strides), and match the oracle."""
     from natten_mps_amd import functional as F
     from natten_mps_amd._core import _lib
 
@@ -375,7 +432,8 @@ def test_tile_kernels_on_packed_views(case):
     finally:
         _lib.profile_enable(False)
     launched = set(_lib.profile_read(reset=True))
-    assert {"na_fwd_mfma", "na_bwd_q_mfma", "na_bwd_kv_mfma"} <= launched, launched
+    kind = "lean" if rank == 1 and dim in (32, 64) else "mfma"
+    assert {f"na_fwd_{kind}", f"na_bwd_q_{kind}", f"na_bwd_kv_{kind}"} <= launched, launched
     ref, (gq, gk, gv) = _oracle_fwd_bwd(rank, (rq, rk, rv), do, ks, (1,) * rank, dil, causal)
     _close(out.detach().cpu(), ref, dtype, "out")
     if hq == hkv:
