@@ -1066,13 +1066,20 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
     if (redo) lean_redo_bwd_kv<T, D>(kernargs(), opaque(z), opaque(pos1), opaque(pos2), b, hk, grp);
 }
 
+// Waves per SIMD the key-side kernel is built for: 5 (at most 96 VGPRs) for
+// the 16-bit 2-D kernel at head dim 32, whose LDS holds 5 workgroups per CU
+// (the dQ kernel at 96 VGPRs spills and runs slower at 5 waves than at 4);
+// no constraint otherwise.
+constexpr int lean_kv_waves(int D, bool f32, bool d3, bool one_d) { return D == 32 && !f32 && !d3 && !one_d ? 5 : 1; }
+
 template <typename T, int D, int NCH, bool D3 = false, bool ONE_D = false>
 __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_q(LeanBwdArgs<T> a) {
     lean_bwd_q_tile<T, D, NCH, D3, ONE_D>(a, xcd_block(blockIdx.x, gridDim.x));
 }
 
 template <typename T, int D, int MAXC, bool D3 = false, bool ONE_D = false>
-__global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_kv(LeanBwdArgs<T> a) {
+__global__ __launch_bounds__(64 * kLeanWaves) __attribute__((amdgpu_waves_per_eu(
+    lean_kv_waves(D, kF32<T>, D3, ONE_D)))) void k_lean_bwd_kv(LeanBwdArgs<T> a) {
     lean_bwd_kv_tile<T, D, MAXC, D3, ONE_D>(a, xcd_block(blockIdx.x, gridDim.x));
 }
 
