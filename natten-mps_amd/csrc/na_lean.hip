@@ -1,5 +1,11 @@
-// Lean tile kernels for 2-D neighbourhood attention (gfx950, bf16 / fp16,
-// head dim 32 or 64, stride 1): forward, backward dQ and backward dK/dV.
+// Lean tile kernels (gfx950, bf16 / fp16 / fp32, head dim 32 or 64, stride
+// 1): forward, backward dQ and backward dK/dV for 2-D problems, for 1-D
+// problems (ONE_D: a tile is 64 consecutive items of a residue class, 16 per
+// wave, its window union staged 16 slots to a row and masked per 32-slot
+// chunk), and for fp32 3-D problems (D3: the 2-D tile at one depth walks
+// its window's depth planes).  Every operand is read or written at its own
+// strides (k and v, and dk and dv, share one), and the key side walks the
+// q heads of its kv head's group (GQA).
 //
 // They serve the common case of the MFMA tile path with a fixed tile and
 // fixed lane layouts, so that a wave spends its instructions on the products
