@@ -181,13 +181,13 @@ __device__ __forceinline__ int lean_piece(int pp, int slot) {
 // Staging of union rows [0, nst) of two operands sharing one layout into
 // Xa / Xb (16 slots per row): rows at or past U1 and columns at or past U2
 // load from outside the range (zeros).  Rows are dealt to the waves in turn.
-template <typename T, int D>
+template <typename T, int D, int NW = kLeanWaves>
 __device__ __forceinline__ void lean_stage(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, T* Xa, T* Xb,
                                            int base, int step1, int step2, int U1, int U2, int nst, int wave,
                                            int lane) {
     constexpr int R = kRowD<T, D>;
     constexpr int P = R / 8, SPI = 64 / P, HALVES = 16 / SPI;
-    static_assert(kLeanWaves % 2 == 0, "a wave's rows must keep one parity");
+    static_assert(NW % 2 == 0, "a wave's rows must keep one parity");
     // lane part of the offset per half row; a wave's rows i = wave + 4j all
     // have the parity of `wave`, which fixes the swizzle's row bit
     uint32_t off[HALVES];
@@ -199,7 +199,7 @@ __device__ __forceinline__ void lean_stage(__amdgpu_buffer_rsrc_t ra, __amdgpu_b
         off[hf] = c < U2 ? static_cast<uint32_t>(c * step2 + lean_piece<R>(pp, slot) * 16) : kLeanOOR;
     }
 #pragma unroll 1
-    for (int i = wave; i < nst; i += kLeanWaves) {
+    for (int i = wave; i < nst; i += NW) {
         const uint32_t ro = i < U1 ? static_cast<uint32_t>(base + i * step1) : kLeanOOR;
 #pragma unroll
         for (int hf = 0; hf < HALVES; ++hf) {
@@ -424,16 +424,20 @@ __device__ __forceinline__ void lean_redo_fwd(const void* kargs, int z, int pos1
 // turn, with one online-softmax rescale per plane; 2-D: one plane, one
 // maximum, no rescale.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int NCH, bool D3 = false, bool ONE_D = false>
-__global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) {
+// HP q heads per workgroup (HP = 2: two q heads of one kv head's group,
+// waves 0-3 and 4-7, share the staged K/V rows).
+template <typename T, int D, int NCH, bool D3 = false, bool ONE_D = false, int HP = 1>
+__global__ __launch_bounds__(64 * kLeanWaves * HP) void k_lean_fwd(LeanFwdArgs<T> a) {
     constexpr int NR = lean_rows<ONE_D>(NCH), NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
+    static_assert(!(D3 && HP > 1), "one head per workgroup for depth walks");
     unsigned char* smem = lds_base();
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + NR * 16 * D;
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave_wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = wave_wg & (kLeanWaves - 1);  // the wave's place in its head's tile
     const LeanTask tk = lean_task<D3>(a.dec, xcd_block(blockIdx.x, gridDim.x));
-    const int b = tk.b, h = tk.h, t = tk.t, z = tk.z;
+    const int b = tk.b, h = tk.h * HP + (wave_wg / kLeanWaves), t = tk.t, z = tk.z;
     const int hk = a.rep.d == 1 ? h : fdiv(h, a.rep);
     const int* r = a.rec + t * kLeanRec;
     const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
@@ -449,8 +453,8 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_fwd(LeanFwdArgs<T> a) 
     const int ks1 = ONE_D ? 16 * ks2 : a.lk.s1 * a.d1 * ES;
     const auto stage = [&](int j) {
         const long long o = kvo + static_cast<long long>(dw.z0 + j * dw.d) * a.lk.s0;
-        lean_stage<T, D>(lean_rsrc(a.k + o, a.kbytes), lean_rsrc(a.v + o, a.kbytes), Ks, Vs, kst, ks1, ks2, U1, U2,
-                         nst, wave, lane);
+        lean_stage<T, D, kLeanWaves * HP>(lean_rsrc(a.k + o, a.kbytes), lean_rsrc(a.v + o, a.kbytes), Ks, Vs, kst,
+                                          ks1, ks2, U1, U2, nst, wave_wg, lane);
     };
     stage(dw.j0);
 
@@ -1588,6 +1592,15 @@ uint32_t plane_bytes(const Prob& p, const Lay& l, int D, int esz = 2) {
     return static_cast<uint32_t>(v);
 }
 
+// Two q heads per workgroup for GQA (NATTEN_HIP_LEAN_PAIRS=0 turns it off).
+bool lean_head_pairs() {
+    static const bool on = [] {
+        const char* e = std::getenv("NATTEN_HIP_LEAN_PAIRS");
+        return !(e && std::strcmp(e, "0") == 0);
+    }();
+    return on;
+}
+
 bool lean_switch() {
     static const bool on = [] {
         const char* e = std::getenv("NATTEN_HIP_LEAN");
@@ -1606,6 +1619,10 @@ void lean_audit_one(LdsAudit& a) {
     audit_one(k_lean_bwd_q<T, D, NCH>, "k_lean_bwd_q", a);
     audit_one(k_lean_bwd_kv<T, D, NCH + 2>, "k_lean_bwd_kv", a);
     audit_one(k_lean_fwd<T, D, NCH, false, true>, "k_lean_fwd (1-D)", a);
+    if constexpr (!kF32<T>) {
+        audit_one(k_lean_fwd<T, D, NCH, false, false, 2>, "k_lean_fwd (head pairs)", a);
+        audit_one(k_lean_fwd<T, D, NCH, false, true, 2>, "k_lean_fwd (1-D, head pairs)", a);
+    }
     audit_one(k_lean_bwd_q<T, D, NCH, false, true>, "k_lean_bwd_q (1-D)", a);
     audit_one(k_lean_bwd_kv<T, D, NCH + 2, false, true>, "k_lean_bwd_kv (1-D)", a);
     if constexpr (!kF32<T>) {
@@ -1706,7 +1723,7 @@ int lean_lds_audit(int* checked) {
     return a.bad == 0 ? 1 : 0;
 }
 
-template <typename T, int D, int NCH, bool D3, bool ONE_D = false>
+template <typename T, int D, int NCH, bool D3, bool ONE_D = false, int HP = 1>
 hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, const void* k, Lay lk,
                         const void* v, void* o, Lay lo, float* lse, Lay ll, hipStream_t s) {
     LeanFwdArgs<T> a{};
@@ -1720,7 +1737,7 @@ hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, 
     a.lk = lean_lay(lk);
     a.ll = lean_lay(ll);
     a.lo = lean_lay(lo);
-    a.dec = lean_decode(p, p.Hq, g->ntiles);
+    a.dec = lean_decode(p, p.Hq / HP, g->ntiles);
     a.rep = make_fastdiv(p.rep);
     a.d1 = p.ax[1].dil;
     a.d2 = p.ax[2].dil;
@@ -1731,14 +1748,14 @@ hipError_t lean_fwd_run(const Prob& p, const LeanGeo* g, const void* q, Lay lq, 
     a.obytes = plane_bytes(p, lo, D, sizeof(T));
     a.sc2 = p.scale * kLog2e;
     a.p = p;
-    const long long blocks = static_cast<long long>(p.B) * p.Hq * g->ntiles * p.ax[0].len;
+    const long long blocks = static_cast<long long>(p.B) * (p.Hq / HP) * g->ntiles * p.ax[0].len;
     if (blocks >= (1LL << 31)) return hipErrorNotSupported;
     const size_t shm = kLdsPad + static_cast<size_t>(2) * lean_rows<ONE_D>(NCH) * 16 * D * sizeof(T);
     if (shm > 160 * 1024) return hipErrorNotSupported;
-    auto kern = k_lean_fwd<T, D, NCH, D3, ONE_D>;
+    auto kern = k_lean_fwd<T, D, NCH, D3, ONE_D, HP>;
     const hipError_t e = allow_lds(kern, shm);
     if (e != hipSuccess) return e;
-    NA_LAUNCH("na_fwd_lean", kern, dim3(static_cast<unsigned>(blocks)), dim3(64 * kLeanWaves), shm, s, a);
+    NA_LAUNCH("na_fwd_lean", kern, dim3(static_cast<unsigned>(blocks)), dim3(64 * kLeanWaves * HP), shm, s, a);
     return hipGetLastError();
 }
 
@@ -1754,9 +1771,12 @@ hipError_t lean_forward(const Prob& p, const void* q, Lay lq, const void* k, Lay
     if (!g) return hipErrorNotSupported;
     // 3-D instances exist for fp32 only (the eligibility keeps 16-bit 3-D away)
 #define NA_LF_ARGS p, g, q, lq, k, lk, v, o, lo, lse, ll, s
-#define NA_LF(T, DD, N)                                                      \
-    return d1 ? lean_fwd_run<T, DD, N, false, true>(NA_LF_ARGS) \
-              : lean_fwd_run<T, DD, N, false>(NA_LF_ARGS)
+    // GQA with an even group: two q heads per workgroup share the staged K/V
+    const bool pairs = p.rep % 2 == 0 && lean_head_pairs();
+#define NA_LF(T, DD, N)                                                                                 \
+    return d1 ? (pairs ? lean_fwd_run<T, DD, N, false, true, 2>(NA_LF_ARGS)                             \
+                       : lean_fwd_run<T, DD, N, false, true>(NA_LF_ARGS))                               \
+              : (pairs ? lean_fwd_run<T, DD, N, false, false, 2>(NA_LF_ARGS) : lean_fwd_run<T, DD, N, false>(NA_LF_ARGS))
 #define NA_LF3(T, DD, N)                                                                         \
     return d1 ? lean_fwd_run<T, DD, N, false, true>(NA_LF_ARGS)                                  \
               : (d3 ? lean_fwd_run<T, DD, N, true>(NA_LF_ARGS) : lean_fwd_run<T, DD, N, false>(NA_LF_ARGS))
