@@ -675,16 +675,18 @@ __device__ __forceinline__ void lean_redo_bwd_kv(const void* kargs, int z, int p
 // Query tile of task x (lean_task).  3-D (D3): delta = dO . O from the rows
 // (the products of one plane do not hold the window's sum), the dP products
 // start from -delta, and the tile walks its window's key planes.
-template <typename T, int D, int NCH, bool D3 = false, bool ONE_D = false>
+template <typename T, int D, int NCH, bool D3 = false, bool ONE_D = false, int HP = 1>
 __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) {
     constexpr int NR = lean_rows<ONE_D>(NCH), NF = kNF<T, D>, TV = kTV<T, D>, ES = sizeof(T);
+    static_assert(!(D3 && HP > 1), "one head per workgroup for depth walks");
     unsigned char* smem = lds_base();
     T* Ks = reinterpret_cast<T*>(smem);
     T* Vs = Ks + NR * 16 * D;
     const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave_wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = wave_wg & (kLeanWaves - 1);  // the wave's place in its head's tile
     const LeanTask tk = lean_task<D3>(a.dec, x);
-    const int b = tk.b, h = tk.h, t = tk.t, z = tk.z;
+    const int b = tk.b, h = tk.h * HP + (wave_wg / kLeanWaves), t = tk.t, z = tk.z;
     const int hk = a.rep.d == 1 ? h : fdiv(h, a.rep);
     const int* r = a.rec + t * kLeanRec;
     const int pr0 = r[0], pc0 = r[1], ur0 = r[2], uc0 = r[3], ext = r[4], nst = r[5];
@@ -697,8 +699,8 @@ __device__ __forceinline__ void lean_bwd_q_tile(const LeanBwdArgs<T>& a, int x) 
     const int ks1 = ONE_D ? 16 * ks2 : a.lk.s1 * a.d1 * ES;
     const auto stage = [&](int j) {
         const long long o = kvo + static_cast<long long>(dw.z0 + j * dw.d) * a.lk.s0;
-        lean_stage<T, D>(lean_rsrc(a.k + o, a.kbytes), lean_rsrc(a.v + o, a.kbytes), Ks, Vs, kst, ks1, ks2, U1, U2,
-                         nst, wave, lane);
+        lean_stage<T, D, kLeanWaves * HP>(lean_rsrc(a.k + o, a.kbytes), lean_rsrc(a.v + o, a.kbytes), Ks, Vs, kst,
+                                          ks1, ks2, U1, U2, nst, wave_wg, lane);
     };
     stage(dw.j0);
     // the lane's query and its window (as in k_lean_fwd)
@@ -1082,9 +1084,9 @@ __device__ __forceinline__ void lean_bwd_kv_tile(const LeanBwdArgs<T>& a, int x)
 // no constraint otherwise.
 constexpr int lean_kv_waves(int D, bool f32, bool d3, bool one_d) { return D == 32 && !f32 && !d3 && !one_d ? 5 : 1; }
 
-template <typename T, int D, int NCH, bool D3 = false, bool ONE_D = false>
-__global__ __launch_bounds__(64 * kLeanWaves) void k_lean_bwd_q(LeanBwdArgs<T> a) {
-    lean_bwd_q_tile<T, D, NCH, D3, ONE_D>(a, xcd_block(blockIdx.x, gridDim.x));
+template <typename T, int D, int NCH, bool D3 = false, bool ONE_D = false, int HP = 1>
+__global__ __launch_bounds__(64 * kLeanWaves * HP) void k_lean_bwd_q(LeanBwdArgs<T> a) {
+    lean_bwd_q_tile<T, D, NCH, D3, ONE_D, HP>(a, xcd_block(blockIdx.x, gridDim.x));
 }
 
 template <typename T, int D, int MAXC, bool D3 = false, bool ONE_D = false>
@@ -1622,6 +1624,8 @@ void lean_audit_one(LdsAudit& a) {
     if constexpr (!kF32<T>) {
         audit_one(k_lean_fwd<T, D, NCH, false, false, 2>, "k_lean_fwd (head pairs)", a);
         audit_one(k_lean_fwd<T, D, NCH, false, true, 2>, "k_lean_fwd (1-D, head pairs)", a);
+        audit_one(k_lean_bwd_q<T, D, NCH, false, false, 2>, "k_lean_bwd_q (head pairs)", a);
+        audit_one(k_lean_bwd_q<T, D, NCH, false, true, 2>, "k_lean_bwd_q (1-D, head pairs)", a);
     }
     audit_one(k_lean_bwd_q<T, D, NCH, false, true>, "k_lean_bwd_q (1-D)", a);
     audit_one(k_lean_bwd_kv<T, D, NCH + 2, false, true>, "k_lean_bwd_kv (1-D)", a);
@@ -1845,23 +1849,23 @@ LeanBwdArgs<T> lean_bwd_args(const Prob& p, const void* q, Lay lq, const void* k
     return a;
 }
 
-template <typename T, int D, int NCH, bool D3, bool ONE_D = false>
+template <typename T, int D, int NCH, bool D3, bool ONE_D = false, int HP = 1>
 hipError_t lean_bwd_run(const Prob& p, const LeanGeo* gq, const LeanGeo* gk, const LeanBwdArgs<T>& base,
                         hipStream_t s) {
     LeanBwdArgs<T> a = base;
     a.rec = gq->ptr;
     a.rec_k = gk->ptr;
-    a.dec = lean_decode(p, p.Hq, gq->ntiles);
+    a.dec = lean_decode(p, p.Hq / HP, gq->ntiles);
     a.nr = std::max(gk->nst_max, 1);
     const size_t shm_q = kLdsPad + static_cast<size_t>(2) * lean_rows<ONE_D>(NCH) * 16 * D * sizeof(T);
     const size_t shm_k =
         kLdsPad + static_cast<size_t>(a.nr) * 16 * (2 * D * sizeof(T) + 2 * sizeof(float)) + 8 * sizeof(float);
-    const long long tasks = static_cast<long long>(p.B) * p.Hq * gq->ntiles * p.ax[0].len;
+    const long long tasks = static_cast<long long>(p.B) * (p.Hq / HP) * gq->ntiles * p.ax[0].len;
     if (tasks >= (1LL << 31) || shm_q > 160 * 1024 || shm_k > 160 * 1024) return hipErrorNotSupported;
-    auto kq = k_lean_bwd_q<T, D, NCH, D3, ONE_D>;
+    auto kq = k_lean_bwd_q<T, D, NCH, D3, ONE_D, HP>;
     hipError_t e = allow_lds(kq, shm_q);
     if (e != hipSuccess) return e;
-    NA_LAUNCH("na_bwd_q_lean", kq, dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves), shm_q, s, a);
+    NA_LAUNCH("na_bwd_q_lean", kq, dim3(static_cast<unsigned>(tasks)), dim3(64 * kLeanWaves * HP), shm_q, s, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     auto kern = k_lean_bwd_kv<T, D, NCH + 2, D3, ONE_D>;
@@ -1892,9 +1896,13 @@ hipError_t lean_backward(const Prob& p, const void* q, Lay lq, const void* k, La
     if (!gq || !gk || gq->ntiles != gk->ntiles || gk->rows_max > 2 * (nch + 2)) return hipErrorNotSupported;
 #define NA_LB_A(T, DD) \
     lean_bwd_args<T, DD>(p, q, lq, k, lk, v, o, lo, dout, ldo, lse, ll, dlse, dq, ldq, dk, ldk, dv, delta)
-#define NA_LB(T, DD, N)                                                         \
-    return d1 ? lean_bwd_run<T, DD, N, false, true>(p, gq, gk, NA_LB_A(T, DD), s) \
-              : lean_bwd_run<T, DD, N, false>(p, gq, gk, NA_LB_A(T, DD), s)
+    // GQA with an even group: two q heads per dQ workgroup share the staged K/V
+    const bool pairs = p.rep % 2 == 0 && lean_head_pairs();
+#define NA_LB(T, DD, N)                                                                          \
+    return d1 ? (pairs ? lean_bwd_run<T, DD, N, false, true, 2>(p, gq, gk, NA_LB_A(T, DD), s)     \
+                       : lean_bwd_run<T, DD, N, false, true>(p, gq, gk, NA_LB_A(T, DD), s))       \
+              : (pairs ? lean_bwd_run<T, DD, N, false, false, 2>(p, gq, gk, NA_LB_A(T, DD), s)    \
+                       : lean_bwd_run<T, DD, N, false>(p, gq, gk, NA_LB_A(T, DD), s))
 #define NA_LB3(T, DD, N)                                                              \
     return d1 ? lean_bwd_run<T, DD, N, false, true>(p, gq, gk, NA_LB_A(T, DD), s)     \
               : (d3 ? lean_bwd_run<T, DD, N, true>(p, gq, gk, NA_LB_A(T, DD), s)      \

@@ -59,7 +59,7 @@ def test_mfma_kernels_have_no_static_lds():
     2 dtypes x 4 head dims x 9 single-step (FLAT) fused instances, the lean
     2-D kernels: 2 dtypes x 2 head dims x 5 chunk counts x forward, dQ,
     dK/dV and the split key side, their 1-D forward, dQ and dK/dV, and the
-    forward with two q heads per workgroup (2-D and 1-D), and
+    forward and dQ with two q heads per workgroup (2-D and 1-D), and
     fp32 x 2 head dims x 5 chunk counts x forward, dQ and dK/dV for 2-D, 1-D
     and 3-D (depth-walking) problems, and
     2 dtypes x 4 head dims x 11 dQ instances that
@@ -70,7 +70,7 @@ def test_mfma_kernels_have_no_static_lds():
 
     n = ctypes.c_int32(0)
     assert _lib.load().natten_hip_mfma_lds_check(ctypes.byref(n)) == 1
-    assert n.value == 2 * 3 * (24 + 4 + 6 + 16) + 2 * (24 + 4 + 6) + 2 * 4 * 9 + 2 * 2 * 5 * 9 + 2 * 5 * 9 + 2 * 4 * 11
+    assert n.value == 2 * 3 * (24 + 4 + 6 + 16) + 2 * (24 + 4 + 6) + 2 * 4 * 9 + 2 * 2 * 5 * 11 + 2 * 5 * 9 + 2 * 4 * 11
 
 
 # ---------------------------------------------------------------------------
