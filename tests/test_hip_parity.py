@@ -342,6 +342,9 @@ LEAN1D = [
     (333, 4, 2, 64, 15, 2, True, torch.float32, False),
     (1000, 2, 2, 32, 129, 1, False, torch.float32, False),
     (40, 2, 2, 64, 4, 1, False, torch.float32, True),
+    # shorter than a wave's 16 items, and than a tile per residue class
+    (10, 2, 2, 32, 3, 1, False, torch.bfloat16, False),
+    (21, 4, 2, 64, 9, 2, True, torch.float32, False),
 ]
 
 
