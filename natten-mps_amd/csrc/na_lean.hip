@@ -1100,13 +1100,10 @@ __global__ __launch_bounds__(64 * kLeanWaves) __attribute__((amdgpu_waves_per_eu
 // of w[q][e(q, k)] x[q] (the dk of QK's backward with w = dattn, x = q; the
 // dv of AV's backward with w = attn, x = dO).  Key tiles as in k_lean_bwd_kv:
 // the union of the attending queries is staged, x rows by the 16-byte DMA
-// (16 slots per union row) and each union query's row of w (KV entries) by
-// 16-byte DMA into a slot row of N16 16-byte chunks (UW slots per union
-// row, UW the widest union of the problem): the row's window of P words (the words that
-// hold its entries, 4P >= 16 bytes) in chunks 0 .. N16-2 at 16-byte steps
-// and the last chunk ending where the window ends, so no read leaves the
-// window (the last chunk overlaps the one before it by `sh` entries, which
-// the gather skips for entries past chunk N16-2).  In class coordinates
+// (16 slots per union row) and, of each union query's row of w (KV
+// entries), only the band of window rows that meet the key tile, by 16-byte
+// DMA into one slot per union column (about a third of the row at K = 7;
+// the band's layout is given where the kernel stages it).  In class coordinates
 // e(q, k) = (J1(k) - ws1(q)) K2 + (J2(k) - ws2(q)); the host tables d1[u] =
 // J1(first key) - ws1(union row u) and d2[u] (per union column) make it
 // (d1[u1] + kr) K2 + (d2[u2] + kc) for the lane's key (kr, kc), and the pair
@@ -1123,9 +1120,6 @@ struct LeanWsumKeyArgs {
     T* out;
     LeanLay lw, lx, lo;
     FastDiv heads, tiles;
-    FastDiv N16;                  // 16-byte chunks per staged w row
-    FastDiv UW;                   // w slot rows per union row (the widest union)
-    int wwin;                     // bytes of a w row's window (4P)
     int nr;                       // LDS rows
     int d1, d2, K1, K2;
     uint32_t xbytes, wbytes;      // byte ranges of one (batch, head) plane of x and of w
@@ -1148,7 +1142,7 @@ __device__ __forceinline__ void lean_redo_wsum_key(const void* kargs, int pos1, 
 
 template <typename T, int D, int MAXC>
 __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_wsum_key(LeanWsumKeyArgs<T> a) {
-    const int nr = a.nr, N16 = static_cast<int>(a.N16.d);
+    const int nr = a.nr;
     unsigned char* smem = lds_base();
     T* Xs = reinterpret_cast<T*>(smem);
     uint32_t* Ws32 = reinterpret_cast<uint32_t*>(Xs + nr * 16 * D);
@@ -1181,39 +1175,69 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_wsum_key(LeanWsumKeyAr
     const long long xo = b * a.lx.b + h * a.lx.h;
     lean_stage1<T, D>(lean_rsrc(a.x + xo, a.xbytes), Xs, (ur0 * a.lx.s1 + uc0 * a.lx.s2) * 2, a.lx.s1 * a.d1 * 2,
                       a.lx.s2 * a.d2 * 2, U1, U2, nst, wave, lane);
-    // w rows of the union: slot s = UW u + cc at byte 16 N16 s, chunk k of
-    // the slot's window at byte 16 k (the last at wwin - 16); chunk t of the
-    // block goes to lane t % 64 of the DMA instruction t / 64 (rows and
-    // columns past the union load nothing useful: the tables mask them)
+    // w rows of the union, each over its band only: union row u's queries
+    // meet the tile's key rows kr < E1 at window rows e1 = d1[u] + kr, so
+    // the band is [lo, hi] = [d1[u], d1[u] + E1 - 1] clipped to [0, K1), n
+    // rows, entries [lo K2, (hi + 1) K2).  It is staged from the word that
+    // holds its first entry (entry sb = (lead + lo K2) rounded down to even,
+    // counted from the plane's word-aligned base) in n16 = (n K2 + 8) / 8
+    // chunks of 16 bytes, enough for either phase.  Row u's slots (union
+    // columns cc < U2) start at chunk W_u + cc n16_u, W_u = U2 (n16_0 + ... +
+    // n16_{u-1}); chunk t of a row goes to lane t % 64 of the row's DMA
+    // instruction t / 64.  Lane u of each 16 holds row u's W, n16 and sb.
     const T* wplane = a.w + b * a.lw.b + h * a.lw.h;
     const int lead = static_cast<int>((reinterpret_cast<uintptr_t>(wplane) >> 1) & 1);
+    int bw = 0, bn, bs;
+    {
+        const int u = lane & 15;
+        const int d1u = u < 8 ? sbyte(r2[0], r2[1], u) : sbyte(r2[2], r2[3], u - 8);
+        const int lo = max(d1u, 0), hi = min(d1u + E1 - 1, a.K1 - 1);
+        bn = u < U1 && hi >= lo ? ((hi - lo + 1) * a.K2 + 8) >> 3 : 0;
+        bs = (lead + lo * a.K2) & ~1;
+        int run = 0;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            bw = u == v ? run : bw;
+            run += __builtin_amdgcn_readlane(bn, v);
+        }
+        bw *= U2;
+    }
     {
         const __amdgpu_buffer_rsrc_t rw = lean_rsrc(wplane - lead, a.wbytes);
         const int rs = a.lw.s1 * a.d1 * 2, cs = a.lw.s2 * a.d2 * 2;  // bytes between union rows / columns
         const int rbase = (ur0 * a.lw.s1 + uc0 * a.lw.s2) * 2;
-        const int uw = static_cast<int>(a.UW.d);
-        const int total = U1 * uw * N16;
+        // union rows round-robin over the waves; lanes past a row's chunks
+        // stay inactive (no LDS write), so rows never overlap
 #pragma unroll 1
-        for (int t0 = wave * 64; t0 < total; t0 += 64 * kLeanWaves) {
-            const int t = t0 + lane;
-            const int slot = fdiv(t, a.N16);
-            const int k = t - slot * N16, u = fdiv(slot, a.UW), cc = slot - u * uw;
-            const int cb = k == N16 - 1 ? a.wwin - 16 : k * 16;
-            const uint32_t o = (t < total && cc < U2) ? static_cast<uint32_t>(rbase + u * rs + cc * cs + cb)
-                                                      : kLeanOOR;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t*)(Ws32 + 4 * t0), 16, o, 0, 0, 0);
+        for (int u = wave; u < U1; u += kLeanWaves) {
+            const int n = __builtin_amdgcn_readlane(bn, u);
+            if (n == 0) continue;
+            const int w0 = __builtin_amdgcn_readlane(bw, u), sb = __builtin_amdgcn_readlane(bs, u);
+            const int cnt = U2 * n, ro = rbase + u * rs + 2 * sb;
+            const float rn = __builtin_amdgcn_rcpf(static_cast<float>(n));
+#pragma unroll 1
+            for (int t0 = 0; t0 < cnt; t0 += 64) {
+                // slot cc and chunk k (t < 16 * 11: the float quotient is
+                // exact to far below the 1 / (2 n) margin)
+                const int t = t0 + lane;
+                const int cc = static_cast<int>((static_cast<float>(t) + 0.5f) * rn);
+                const int k = t - cc * n;
+                if (t < cnt)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void_t*)(Ws32 + 4 * (w0 + t0)), 16,
+                                                             static_cast<uint32_t>(ro + cc * cs + 16 * k), 0, 0, 0);
+            }
         }
     }
     // the wave's union rows [first, last] (of the key record)
     const int first = __builtin_amdgcn_readfirstlane(sbyte(r[6], r[7], 2 * wave));
     const int last = __builtin_amdgcn_readfirstlane(sbyte(r[10], r[11], 2 * wave + 1));
     const int nch = (last - first + 2) >> 1;
-    // the lane's 8 slots of a chunk: union columns 8 (g % 2) + j; window
-    // entry offsets lead + e2 of the lane's key column and the column masks,
-    // two entries per word.  A window entry ew sits at entry ew of the slot
-    // row, or ew + sh from entry thr on (the last chunk's shift).
-    const int pe = 8 * N16;                       // entries per slot row
-    const int thr = 8 * (N16 - 1), sh = (16 * N16 - a.wwin) >> 1;
+    // the lane's 8 slots of a chunk: union columns 8 (g % 2) + j (past the
+    // union: the last column, whose entries the masks drop); window entry
+    // offsets lead + e2 of the lane's key column and the column masks, two
+    // entries per word.  Window entry ew of union row u sits at entry ew -
+    // sb_u of its slot.
+    const int c0 = 8 * (grp & 1), clast = U2 - 1;
     int cp[8];
     uint32_t cm[4];
     {
@@ -1252,16 +1276,21 @@ __global__ __launch_bounds__(64 * kLeanWaves) void k_lean_wsum_key(LeanWsumKeyAr
         const int ua = first + 2 * c, ub = ua + 1;
         const int da = ua < 8 ? sbyte(d10, d11, ua) : (ua < 16 ? sbyte(d12, d13, ua - 8) : -100);
         const int dbb = ub < 8 ? sbyte(d10, d11, ub) : (ub < 16 ? sbyte(d12, d13, ub - 8) : -100);
-        const int u1 = (grp >> 1) ? ub : ua;
-        const int e1 = ((grp >> 1) ? dbb : da) + kr;
+        const bool second = grp >> 1;
+        const int e1 = (second ? dbb : da) + kr;
         const bool rok = valid && static_cast<unsigned>(e1) < static_cast<unsigned>(a.K1);
-        const int rowpart = (u1 * static_cast<int>(a.UW.d) + 8 * (grp & 1)) * pe, eo = e1 * a.K2;
+        // the band of the lane's union row (a valid e1 lies in it)
+        const int ra = min(ua, 15), rb = min(ub, 15);
+        const int wa = __builtin_amdgcn_readlane(bw, ra), na = __builtin_amdgcn_readlane(bn, ra);
+        const int sa = __builtin_amdgcn_readlane(bs, ra), wb2 = __builtin_amdgcn_readlane(bw, rb);
+        const int nb = __builtin_amdgcn_readlane(bn, rb), sb2 = __builtin_amdgcn_readlane(bs, rb);
+        const int pe = 8 * (second ? nb : na);  // entries per slot of the row
+        const int base = rok ? 8 * (second ? wb2 : wa) - (second ? sb2 : sa) + e1 * a.K2 : 0;
         uint32_t wv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int ea = eo + cp[2 * i], eb = eo + cp[2 * i + 1];
-            const uint32_t lo16 = Ws[rowpart + 2 * i * pe + ea + (ea >= thr ? sh : 0)];
-            const uint32_t hi16 = Ws[rowpart + (2 * i + 1) * pe + eb + (eb >= thr ? sh : 0)];
+            const uint32_t lo16 = Ws[base + min(c0 + 2 * i, clast) * pe + cp[2 * i]];
+            const uint32_t hi16 = Ws[base + min(c0 + 2 * i + 1, clast) * pe + cp[2 * i + 1]];
             wv[i] = rok ? ((lo16 | (hi16 << 16)) & cm[i]) : 0u;
         }
         lean_accumulate<T, D>(Xb, toff, c, make_uint4(wv[0], wv[1], wv[2], wv[3]), acc);
@@ -1294,6 +1323,7 @@ struct LeanGeo {
     int len[2], k[2], dil[2], causal[2];
     int* ptr;
     int ntiles, nst_max, rows_max, u2_max;
+    int wchunks_max;        // split key tiles: the most 16-byte chunks of staged w bands
     std::vector<int> host;  // source of the asynchronous upload, kept with the table
     TableUpload up;
 };
@@ -1355,6 +1385,20 @@ void split_table(const Axis& A, int r, const LeanAxisTile& a, int* out4) {
     int d[16];
     for (int u = 0; u < 16; ++u) d[u] = u < a.U ? a.J - class_ws(c, a.lo + u) : -100;
     for (int i = 0; i < 4; ++i) out4[i] = pack_bytes(d, 4 * i);
+}
+
+// 16-byte chunks per union column that a split key tile stages of its w
+// rows: union row u only its band of window rows that meet the tile's key
+// rows, n of them, in (n K2 + 8) / 8 chunks.
+int split_chunks(const Axis& A, int r, const LeanAxisTile& a, int K2) {
+    const ClassAxis c = class_axis(A, r);
+    int sum = 0;
+    for (int u = 0; u < a.U; ++u) {
+        const int d = a.J - class_ws(c, a.lo + u);
+        const int lo = std::max(d, 0), hi = std::min(d + a.E - 1, A.k - 1);
+        if (hi >= lo) sum += ((hi - lo + 1) * K2 + 8) >> 3;
+    }
+    return sum;
 }
 
 // A 1-D problem (axes 0 and 1 of extent 1): tiles of 64 consecutive class
@@ -1476,7 +1520,7 @@ const LeanGeo* lean_geometry(const Prob& p, int mode, int nch, hipStream_t s) {
     if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) return nullptr;
     const Axis &A1 = p.ax[1], &A2 = p.ax[2];
     std::vector<int> h;
-    int nst_max = 0, rows_max = 0, u2_max = 1;
+    int nst_max = 0, rows_max = 0, u2_max = 1, wch_max = 0;
     if (lean_1d(p)) {
         if (mode == 2 || !lean_records_1d(p, key, nch, h, nst_max, rows_max)) return nullptr;
     } else {
@@ -1533,6 +1577,7 @@ const LeanGeo* lean_geometry(const Prob& p, int mode, int nch, hipStream_t s) {
                             if (a1.U > 16) return nullptr;
                             split_table(A1, r1, a1, tab);
                             split_table(A2, r2, a2, tab + 4);
+                            wch_max = std::max(wch_max, split_chunks(A1, r1, a1, A2.k) * a2.U);
                         }
                         h.insert(h.end(), tab, tab + kLeanRec);
                     }
@@ -1563,6 +1608,7 @@ const LeanGeo* lean_geometry(const Prob& p, int mode, int nch, hipStream_t s) {
     e->nst_max = nst_max;
     e->rows_max = rows_max;
     e->u2_max = u2_max;
+    e->wchunks_max = wch_max;
     cache.push_back(e);
     return e;
 }
@@ -1970,12 +2016,6 @@ hipError_t lean_wsum_key_run(const char* name, const Prob& p, const LeanGeo* g, 
     a.heads = make_fastdiv(p.Hq);
     a.tiles = make_fastdiv(g->ntiles);
     a.nr = std::max(g->nst_max, 1);
-    const int P = (p.kv + 2) / 2;  // words of a row with its 2-byte phase
-    const int n16 = (4 * P + 15) / 16;
-    if (4 * P < 16) return hipErrorNotSupported;  // a window shorter than one chunk
-    a.N16 = make_fastdiv(n16);
-    a.UW = make_fastdiv(g->u2_max);
-    a.wwin = 4 * P;
     a.d1 = p.ax[1].dil;
     a.d2 = p.ax[2].dil;
     a.K1 = p.ax[1].k;
@@ -1986,15 +2026,11 @@ hipError_t lean_wsum_key_run(const char* name, const Prob& p, const LeanGeo* g, 
     a.wbytes = static_cast<uint32_t>((wb + 3) & ~3LL);
     a.mul = mul;
     a.p = p;
-    // x rows (16 slots per union row), w slot rows (UW per union row; the
-    // DMA's last instruction may write up to 63 chunks past them), and room
-    // for the gather's masked reads past the last slot row: up to 16 - UW
-    // slots of the last union row, at most (K1 + 6) K2 + K2 + 7 entries from
-    // a slot's start plus the last chunk's shift (under 8 entries)
-    const size_t over = std::max<size_t>(
-        63 * 16, static_cast<size_t>(16 - g->u2_max) * n16 * 16 +
-                     (static_cast<size_t>(p.ax[1].k + 7) * p.ax[2].k + 16) * 2);
-    const size_t shm = kLdsPad + static_cast<size_t>(a.nr) * (16 * D * sizeof(T) + g->u2_max * n16 * 16) + over;
+    // x rows (16 slots per union row), the w bands (the most chunks of any
+    // tile), and room for the gather's masked reads, which end less than 16
+    // entries past the last slot
+    const size_t shm = kLdsPad + static_cast<size_t>(a.nr) * 16 * D * sizeof(T) +
+                       (static_cast<size_t>(g->wchunks_max) + 2) * 16;
     if (shm > 160 * 1024) return hipErrorNotSupported;
     auto kern = k_lean_wsum_key<T, D, MAXC>;
     hipError_t e = allow_lds(kern, shm);
