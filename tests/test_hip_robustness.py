@@ -489,3 +489,54 @@ def test_fp32_on_2d_tile_kernels(case):
     assert_parity(out, ref, torch.float32, "out")
     for name, a, b in zip(("dq", "dk", "dv"), leaves, rl):
         assert_parity(a.grad, b.grad, torch.float32, name)
+
+
+# ---------------------------------------------------------------------------
+# the split key side's weight bands: K up to 9 (bands of up to 10 chunks),
+# dilation, causal windows, non-square images, and weight planes at both
+# 2-byte phases (2 heads of an odd number of weights each)
+# ---------------------------------------------------------------------------
+
+SPLIT_BANDS = [
+    ((9, 11), (5, 5), (1, 1), (False, False)),
+    ((10, 13), (9, 9), (1, 1), (False, False)),
+    ((16, 12), (7, 3), (2, 1), (True, False)),
+    ((12, 11), (5, 5), (1, 2), (False, True)),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_BANDS)
+def test_split_key_side_weight_bands(case):
+    """dk of QK's backward and dv of AV's backward on the key-side tile
+    kernel, whose staging keeps only the band of each weight row that meets
+    the key tile, against the oracle (with dq and dattn)."""
+    from natten_mps_amd import functional as F
+
+    sp, ks, dil, causal = case
+    kv = ks[0] * ks[1]
+    q, k, v, do = _inputs(351, [(2, *sp, 2, 32)] * 4, torch.bfloat16)
+    (dl, lg) = _inputs(352, [(2, *sp, 2, kv)] * 2, torch.float32)
+    rq, rk = q.float().requires_grad_(True), k.float().requires_grad_(True)
+    ref_l = P.na2d_qk_forward(rq, rk, ks, dil, (1, 1), causal, None)
+    finite = torch.isfinite(ref_l)
+    dl = torch.where(finite, dl, torch.zeros_like(dl)).to(torch.bfloat16)
+    attn = torch.softmax(torch.where(finite, lg, torch.full_like(lg, -1e30)), -1).to(torch.bfloat16)
+    qd, kd = q.to(DEV).requires_grad_(True), k.to(DEV).requires_grad_(True)
+    ad, vd = attn.to(DEV).requires_grad_(True), v.to(DEV).requires_grad_(True)
+
+    def run():
+        logits = F.na2d_qk(qd, kd, ks, dil, is_causal=causal)
+        logits.backward(dl.to(DEV))
+        out = F.na2d_av(ad, vd, ks, dil, is_causal=causal)
+        out.backward(do.to(DEV))
+        return out
+
+    out, ran = _launched(run)
+    assert {"na_qk_bwd_k_lean", "na_av_bwd_v_lean"} <= ran, ran
+    ref_l.backward(dl.float())
+    ra, rv = attn.float().requires_grad_(True), v.float().requires_grad_(True)
+    ref_o = P.na2d_av_forward(ra, rv, ks, dil, (1, 1), causal)
+    ref_o.backward(do.float())
+    assert_parity(out, ref_o, torch.bfloat16, "out")
+    for name, a, b in (("dq", qd, rq), ("dk", kd, rk), ("dattn", ad, ra), ("dv", vd, rv)):
+        assert_parity(a.grad, b.grad, torch.bfloat16, name)
